@@ -1,0 +1,228 @@
+#!/usr/bin/env python3
+"""Benchmark of the temporal random walk hot path on one MI355X.
+
+Workload (the headline config): directed power-law
+graph, 1,000,000 node ids, 20,000,000 edges, src/dst Zipf(s=1.8) mapped through
+one shared random permutation, self-loops redrawn, timestamps uniform in
+[0, 1e8) quantised to 100,000 values (numpy PCG64, seed 44).  One step =
+ingest the whole batch (index build) + sample 10,000,000 walks with
+max_walk_len=80, walk_bias=ExponentialIndex, initial_edge_bias=Uniform,
+forward in time.  Inputs are resident in HBM before the timed region; the
+walks stay in HBM (device-resident boundary).
+
+Prints ONE JSON line.  `value` = walk steps/s (sum of walk lengths, the
+reference's definition, test_run/walk_sampling_speed_test.cpp:39-50) over the
+wall time of the sampling calls; index-build edges/s is reported beside it.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "temporal-random-walk_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "sampled walk steps/s + index-build edges/s, 20M-edge power-law graph, 1 GPU"
+HBM_PEAK_GBS = 8000.0
+PMC_FILE = os.path.join(ROOT, "profiles", "walk_kernel_cfg2_pmc.json")
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def make_cfg2(n_nodes, n_edges, n_ts, seed=44):
+    from tests import graphs
+    return graphs.powerlaw(n_nodes, n_edges, s=1.8, n_ts=n_ts, ts_hi=100_000_000, seed=seed)
+
+
+def index_algorithmic_bytes(E, Vc, T, g_o, g_i):
+    """Compulsory bytes of one ingest of E edges into an empty store
+    (directed): read batch 16E, write store 16E, node_ts_sorted 8E out + 8E in,
+    node-timestamp groups 8(g_o+g_i), four per-node size_t arrays 32 Vc,
+    active flags 4(Vc-1), timestamp groups 16T + 8."""
+    return 16 * E + 16 * E + 8 * E + 8 * E + 8 * (g_o + g_i) + 32 * Vc + 4 * (Vc - 1) + 16 * T + 8
+
+
+def cpu_baseline(src, dst, ts, n_walks, L, threads):
+    """The oracle (C restatement of the reference CPU path) on the host cores:
+    full ingest of the graph (single-threaded, as written) and a bounded
+    sample of walks (OpenMP over walks), draw generation included as in the
+    reference's CPU sampler."""
+    import numpy as np
+    from oracle import pyoracle as po
+
+    og = po.OracleGraph(True)
+    t0 = time.perf_counter()
+    og.add_edges(src, dst, ts)
+    t_build = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    draws = np.random.default_rng(1).random(n_walks * (1 + 2 * L))
+    starts = -np.ones(n_walks, dtype=np.int32)
+    w = og.walks(L, "ExponentialIndex", "Uniform", True, starts, draws, num_threads=threads)
+    t_walk = time.perf_counter() - t0
+    steps = int(w.lens.sum())
+    return {
+        "value": steps / t_walk,
+        "unit": "walk steps/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle/trw_oracle.c: {n_walks} walks (L={L}, ExponentialIndex/Uniform, fwd) "
+                   f"on the full cfg2 graph with {threads} OpenMP threads, draw generation "
+                   f"included; index build of all {len(src)} edges single-threaded"),
+        "index_build_edges_per_s": len(src) / t_build,
+        "index_build_cores": 1,
+        "walk_s": t_walk,
+        "build_s": t_build,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--edges", type=int, default=20_000_000)
+    ap.add_argument("--nodes", type=int, default=1_000_000)
+    ap.add_argument("--timestamps", type=int, default=100_000)
+    ap.add_argument("--walks", type=int, default=10_000_000)
+    ap.add_argument("--walk-len", type=int, default=80)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-walks", type=int, default=200_000)
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build measures one GPU only (no multi-GPU path); "
+                                   "run with --gpus 1"}))
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from temporal_random_walk import capi
+
+    log("generating cfg2 inputs")
+    t0 = time.perf_counter()
+    src, dst, ts = make_cfg2(args.nodes, args.edges, args.timestamps)
+    log(f"generated {len(src)} edges in {time.perf_counter() - t0:.1f}s")
+
+    dev = torch.device("cuda:0")
+    d_src = torch.from_numpy(src).to(dev)
+    d_dst = torch.from_numpy(dst).to(dev)
+    d_ts = torch.from_numpy(ts).to(dev)
+    torch.cuda.synchronize()
+
+    eng = capi.Engine(is_directed=True, global_seed=42, shuffle_walk_order=False)
+    E = len(src)
+
+    def step():
+        eng.clear()
+        t0 = time.perf_counter()
+        eng.add_edges_device(d_src.data_ptr(), d_dst.data_ptr(), d_ts.data_ptr(), E)
+        t1 = time.perf_counter()
+        eng.sample_device("total", args.walk_len, "ExponentialIndex", args.walks,
+                          initial_edge_bias="Uniform", direction="Forward_In_Time")
+        t2 = time.perf_counter()
+        return t1 - t0, t2 - t1, eng.timings()
+
+    for i in range(args.warmup):
+        b, s, _ = step()
+        log(f"warmup {i}: build {b * 1e3:.1f} ms, sample {s * 1e3:.1f} ms")
+
+    torch.cuda.synchronize()
+    T0 = time.perf_counter()
+    builds, samples, tims = [], [], []
+    for i in range(args.steps):
+        b, s, tm = step()
+        builds.append(b)
+        samples.append(s)
+        tims.append(tm)
+        log(f"step {i}: build {b * 1e3:.1f} ms, sample {s * 1e3:.1f} ms, "
+            f"walk kernel {tm['walk_kernel_ms']:.1f} ms")
+    torch.cuda.synchronize()
+    T1 = time.perf_counter()
+
+    stats = eng.walk_stats()  # identical every step (fixed seed), computed untimed
+    steps_per_call = stats["total_len"]
+    value = steps_per_call * args.steps / sum(samples)
+    build_eps = E * args.steps / sum(builds)
+    walk_kernel_ms = sum(t["walk_kernel_ms"] for t in tims) / len(tims)
+    build_dev_ms = sum(t["build_ms"] for t in tims) / len(tims)
+    achieved = stats["algorithmic_bytes"] / (walk_kernel_ms * 1e-3) / 1e9
+
+    g_o = len(eng.array("node_ts_group_outbound_offsets"))
+    g_i = len(eng.array("node_ts_group_inbound_offsets"))
+    Vc = len(eng.array("node_group_outbound_offsets"))
+    T = len(eng.array("unique_timestamps"))
+    idx_bytes = index_algorithmic_bytes(E, Vc, T, g_o, g_i)
+
+    traffic = None
+    if os.path.exists(PMC_FILE):
+        with open(PMC_FILE) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    result = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "walk steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": (T1 - T0) * 1e3 / args.steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int64",
+        "data": "synthetic (seeded numpy PCG64, BASELINE configs[1] shape)",
+        "config": {
+            "workload": "cfg2: directed Zipf(1.8) 1M ids / 20M edges, 1e5 distinct ts; "
+                        "10M walks L=80 ExponentialIndex/Uniform forward",
+            "edges": E,
+            "num_walks": args.walks,
+            "max_walk_len": args.walk_len,
+            "parallelism": "1 GPU",
+        },
+        "index_build_edges_per_s": build_eps,
+        "index_build_ms": sum(builds) * 1e3 / args.steps,
+        "index_build_device_ms": build_dev_ms,
+        "index_roofline": {"bound": "hbm", "achieved": idx_bytes / (build_dev_ms * 1e-3) / 1e9,
+                           "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                           "frac": idx_bytes / (build_dev_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                           "algorithmic_bytes": idx_bytes},
+        "walk_steps_per_call": steps_per_call,
+        "mean_walk_len": steps_per_call / args.walks,
+        "sample_ms": sum(samples) * 1e3 / args.steps,
+        "walk_kernel_ms": walk_kernel_ms,
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": traffic,
+            "kernel": "walk_kernel<true,true>",
+            "algorithmic_bytes_per_launch": stats["algorithmic_bytes"],
+        },
+    }
+
+    if not args.no_cpu_baseline:
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
+        log(f"cpu baseline ({threads} threads)")
+        result["cpu_baseline"] = cpu_baseline(src, dst, ts, args.cpu_walks, args.walk_len,
+                                              threads)
+    else:
+        result["cpu_baseline"] = None
+
+    eng.close()
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

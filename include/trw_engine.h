@@ -1,0 +1,249 @@
+/*
+ * trw_engine.h -- C ABI of the MI355X temporal random walk engine.
+ *
+ * This is the seam under the reference's public C++ class: every
+ * `#ifdef HAS_CUDA / if (use_gpu)` branch of core::TemporalRandomWalk
+ * (reference: temporal_random_walk/src/core/temporal_random_walk.cu:920-1104)
+ * becomes one call below.  Plain C types only: pointers, sizes, enums and POD
+ * structs; no C++ or torch types cross this boundary.
+ *
+ * Conventions
+ *  - Every function returns trw_status; on failure trw_last_error() gives the
+ *    message (thread-local).  TRW_ERR_INVALID_ARGUMENT maps to the reference's
+ *    std::invalid_argument / ValueError, TRW_ERR_RUNTIME to std::runtime_error.
+ *  - One handle = one device + one HIP stream.  Calls are synchronous on
+ *    return.  Concurrent calls on one handle are not supported (as in the
+ *    reference).  The caller's current device is restored on return.
+ *  - Host-pointer entry points copy their inputs before returning.  Output
+ *    host buffers are allocated with malloc() and owned by the caller
+ *    (release with trw_walks_free or free()), matching the reference's
+ *    HostRelease capsules (py_interface/buffer_to_numpy.cuh:13-22).
+ */
+#ifndef TRW_ENGINE_H
+#define TRW_ENGINE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TRW_ABI_VERSION 1
+
+typedef enum trw_status {
+    TRW_OK = 0,
+    TRW_ERR_INVALID_ARGUMENT = 1,
+    TRW_ERR_RUNTIME = 2,
+    TRW_ERR_OUT_OF_MEMORY = 3,
+    TRW_ERR_NO_DEVICE = 4
+} trw_status;
+
+/* RandomPickerType (reference: src/data/enums.cuh:4-15). */
+typedef enum trw_picker {
+    TRW_PICKER_UNIFORM = 0,
+    TRW_PICKER_LINEAR = 1,
+    TRW_PICKER_EXPONENTIAL_INDEX = 2,
+    TRW_PICKER_EXPONENTIAL_WEIGHT = 3,
+    TRW_PICKER_TEMPORAL_NODE2VEC = 4,
+    TRW_PICKER_TEST_FIRST = 5,
+    TRW_PICKER_TEST_LAST = 6
+} trw_picker;
+
+/* WalkDirection (reference: src/data/enums.cuh:17-20). */
+typedef enum trw_direction {
+    TRW_FORWARD_IN_TIME = 0,
+    TRW_BACKWARD_IN_TIME = 1
+} trw_direction;
+
+/* Which of the reference's four samplers builds the start array. */
+typedef enum trw_start_mode {
+    TRW_START_TOTAL = 0,      /* get_random_walks_and_times: n unconstrained walks */
+    TRW_START_ALL_NODES = 1,  /* ..._for_all_nodes: active ids x num_walks_per_node */
+    TRW_START_LAST_BATCH = 2, /* ..._for_last_batch: last batch's unique endpoints */
+    TRW_START_NODES = 3       /* ..._for_nodes: given seeds (+ optional cutoffs) */
+} trw_start_mode;
+
+/* Constructor arguments of the reference's TemporalRandomWalk
+ * (src/proxies/TemporalRandomWalk.cuh:21-36). */
+typedef struct trw_config {
+    int32_t is_directed;
+    int32_t enable_weight_computation;
+    int32_t enable_temporal_node2vec;
+    int32_t walk_padding_value;
+    int64_t max_time_capacity; /* <= 0: no window */
+    double timescale_bound;    /* <= 0: unscaled */
+    double node2vec_p;
+    double node2vec_q;
+    uint64_t global_seed;      /* UINT64_MAX: fresh seed per call */
+    int32_t shuffle_walk_order;
+    int32_t device_id;
+} trw_config;
+
+typedef struct trw_sample_params {
+    int32_t mode;               /* trw_start_mode */
+    int32_t max_walk_len;
+    int32_t walk_bias;          /* trw_picker */
+    int32_t initial_edge_bias;  /* trw_picker, or -1 = same as walk_bias */
+    int32_t direction;          /* trw_direction */
+    int32_t num_walks_per_node; /* ALL_NODES, LAST_BATCH, NODES */
+    int64_t num_walks_total;    /* TOTAL */
+    const int32_t* seed_nodes;  /* NODES: host array of num_seed_nodes ids */
+    const int64_t* cutoff_times;/* NODES: host array or NULL (exclusive upper bounds) */
+    uint64_t num_seed_nodes;
+    /* Replay mode: host array of num_walks * (1 + 2 * max_walk_len) uniforms
+     * in the reference CPU layout (slot 0/1 start group/edge, slot 2
+     * undirected start endpoint, slots 2k+1/2k+2 hop k).  NULL = in-kernel
+     * Philox4x32-10 keyed by the seed. */
+    const double* replay_draws;
+    uint64_t replay_draws_len;
+    int32_t shuffle;            /* -1 = the handle's shuffle_walk_order, 0/1 = override */
+    int32_t reserved;
+} trw_sample_params;
+
+/* Walk output.  nodes/timestamps: [num_walks, max_walk_len]; edge_ids:
+ * [num_walks, max_walk_len - 1]; walk_lens: [num_walks]; edge_features:
+ * [num_walks, max_walk_len - 1, feature_dim] or NULL when feature_dim == 0.
+ * Host results: malloc'd, caller-owned.  Device results (trw_sample_device):
+ * device pointers owned by the handle, valid until its next sample call. */
+typedef struct trw_walks {
+    uint64_t num_walks;
+    int32_t max_walk_len;
+    int32_t feature_dim;
+    int32_t* nodes;
+    int64_t* timestamps;
+    uint64_t* walk_lens;
+    int64_t* edge_ids;
+    float* edge_features;
+} trw_walks;
+
+/* Device-side timings of the last call, in milliseconds (HIP events on the
+ * handle's stream). */
+typedef struct trw_timings {
+    double build_ms;       /* whole device-side ingest of the last add_edges */
+    double sort_ms;        /* timestamp sort + gather inside it */
+    double index_ms;       /* node index (sort, groups, offsets) inside it */
+    double sample_ms;      /* whole device-side sample of the last sample call */
+    double walk_kernel_ms; /* the walk kernel(s) inside it */
+    uint64_t walk_kernel_launches;
+} trw_timings;
+
+/* Array ids for trw_get_array.  Values are widened to the reference's
+ * element types: size_t arrays come back as uint64, int arrays as int32,
+ * timestamps as int64, weights as double, features as float.  The layout and
+ * sizes are those of TemporalGraphData (src/data/temporal_graph_data.cuh). */
+typedef enum trw_array_id {
+    TRW_ARR_SOURCES = 0,
+    TRW_ARR_TARGETS = 1,
+    TRW_ARR_TIMESTAMPS = 2,
+    TRW_ARR_TIMESTAMP_GROUP_OFFSETS = 3,
+    TRW_ARR_UNIQUE_TIMESTAMPS = 4,
+    TRW_ARR_ACTIVE_NODE_IDS = 5,
+    TRW_ARR_NODE_GROUP_OUTBOUND_OFFSETS = 6,
+    TRW_ARR_NODE_GROUP_INBOUND_OFFSETS = 7,
+    TRW_ARR_NODE_TS_SORTED_OUTBOUND_INDICES = 8,
+    TRW_ARR_NODE_TS_SORTED_INBOUND_INDICES = 9,
+    TRW_ARR_COUNT_TS_GROUP_PER_NODE_OUTBOUND = 10,
+    TRW_ARR_COUNT_TS_GROUP_PER_NODE_INBOUND = 11,
+    TRW_ARR_NODE_TS_GROUP_OUTBOUND_OFFSETS = 12,
+    TRW_ARR_NODE_TS_GROUP_INBOUND_OFFSETS = 13,
+    TRW_ARR_FORWARD_CUMULATIVE_WEIGHTS = 14,
+    TRW_ARR_BACKWARD_CUMULATIVE_WEIGHTS = 15,
+    TRW_ARR_OUTBOUND_FORWARD_CUMULATIVE_WEIGHTS = 16,
+    TRW_ARR_OUTBOUND_BACKWARD_CUMULATIVE_WEIGHTS = 17,
+    TRW_ARR_INBOUND_BACKWARD_CUMULATIVE_WEIGHTS = 18,
+    TRW_ARR_NODE_ADJ_OFFSETS = 19,
+    TRW_ARR_NODE_ADJ_NEIGHBORS = 20,
+    TRW_ARR_EDGE_FEATURES = 21,
+    TRW_ARR_COUNT = 22
+} trw_array_id;
+
+/* ---- lifecycle -------------------------------------------------------- */
+
+/* Replaces the constructor: core/temporal_random_walk.cu:38-82. */
+trw_status trw_create(const trw_config* config, void** out_handle);
+/* Replaces the destructor: core/temporal_random_walk.cu:84-102. */
+trw_status trw_destroy(void* handle);
+/* Message of the last failed call on this thread. */
+const char* trw_last_error(void);
+int32_t trw_abi_version(void);
+
+/* ---- ingest ------------------------------------------------------------ */
+
+/* Replaces temporal_random_walk::add_multiple_edges
+ * (core/temporal_random_walk.cu:276-329): append, stable sort by
+ * (timestamp, insertion position), window eviction, full index rebuild,
+ * optional weights, last-batch uniques.  Host pointers; features are
+ * [n, feature_dim] row-major or NULL.  Validation messages follow
+ * graph/edge_data.cu:71-89. */
+trw_status trw_add_edges(void* handle, const int32_t* sources, const int32_t* targets,
+                         const int64_t* timestamps, uint64_t n, const float* edge_features,
+                         uint64_t feature_dim);
+/* Same, with the batch already resident in device memory (HBM). */
+trw_status trw_add_edges_device(void* handle, const int32_t* d_sources,
+                                const int32_t* d_targets, const int64_t* d_timestamps,
+                                uint64_t n, const float* d_edge_features,
+                                uint64_t feature_dim);
+
+/* ---- sampling ------------------------------------------------------------ */
+
+/* Replaces the four get_random_walks_and_times*_cuda samplers
+ * (core/temporal_random_walk.cu:657-916) and finalize_host_walks (:381-390):
+ * outputs are copied to malloc'd host buffers owned by the caller. */
+trw_status trw_sample(void* handle, const trw_sample_params* params, trw_walks* out);
+/* Same, leaving the walks in device memory owned by the handle. */
+trw_status trw_sample_device(void* handle, const trw_sample_params* params, trw_walks* out);
+/* free() of the host buffers of a trw_walks returned by trw_sample. */
+void trw_walks_free(trw_walks* walks);
+
+/* ---- queries (core/temporal_random_walk.cu:331-377) ------------------------ */
+
+trw_status trw_get_node_count(void* handle, uint64_t* out);
+trw_status trw_get_edge_count(void* handle, uint64_t* out);
+/* Active node ids ascending (graph/edge_data.cu:144-208).  If out is NULL only
+ * *len is set. */
+trw_status trw_get_node_ids(void* handle, int32_t* out, uint64_t cap, uint64_t* len);
+/* Degrees of the given nodes (graph/node_edge_index.cu:89-145). */
+trw_status trw_get_node_degrees(void* handle, const int32_t* nodes, uint64_t n,
+                                int32_t direction, int64_t* out);
+/* Edge store as three arrays (graph/edge_data.cu:101-142); NULL outputs query
+ * the length only. */
+trw_status trw_get_edges(void* handle, int32_t* sources, int32_t* targets, int64_t* timestamps,
+                         uint64_t cap, uint64_t* len);
+trw_status trw_get_is_directed(void* handle, int32_t* out);
+trw_status trw_get_memory_used(void* handle, uint64_t* out);
+trw_status trw_get_feature_dim(void* handle, uint64_t* out);
+trw_status trw_get_latest_timestamp(void* handle, int64_t* out);
+/* Replaces temporal_random_walk::clear (core/temporal_random_walk.cu:358-373). */
+trw_status trw_clear(void* handle);
+
+/* Snapshot of one index array, widened to the reference's element type
+ * (size in bytes: 8 except int32/float arrays: 4).  dst NULL = query *len. */
+trw_status trw_get_array(void* handle, int32_t array_id, void* dst, uint64_t cap_elems,
+                         uint64_t* len, uint32_t* elem_size);
+
+/* ---- measurement ----------------------------------------------------------- */
+
+trw_status trw_get_timings(void* handle, trw_timings* out);
+/* The handle's HIP stream (a hipStream_t), for callers that time or order
+ * work against it. */
+trw_status trw_get_stream(void* handle, void** out_stream);
+/* Statistics of the last sample, computed on the device after the fact (not
+ * part of any timing).  algorithmic_bytes is the compulsory traffic of the
+ * walk kernel: per walk 40 B (start reads + length) and 12 B for slot 0; per
+ * emitted slot after the start 20 B; per hop selected at node u
+ * 72 + 8*ceil(log2(G_u + 1)) B (G_u = u's timestamp groups in the sampled
+ * direction; the 72 include that hop's 20 B of output); 20 B per padding
+ * slot. */
+typedef struct trw_walk_stats {
+    uint64_t total_len;         /* sum of walk_lens: walk steps (reference metric) */
+    uint64_t transitions;       /* sum of max(len - 1, 0) */
+    uint64_t nonempty_walks;
+    uint64_t algorithmic_bytes;
+} trw_walk_stats;
+trw_status trw_get_walk_stats(void* handle, trw_walk_stats* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TRW_ENGINE_H */

@@ -109,6 +109,8 @@ def lib():
         L.orc_array.restype = _P
         L.orc_array.argtypes = [_P, C.c_char_p, C.POINTER(C.c_size_t),
                                 C.POINTER(C.c_size_t)]
+        L.orc_set_weights.restype = C.c_int
+        L.orc_set_weights.argtypes = [_P, C.c_char_p, _P, C.c_size_t]
         L.orc_latest_timestamp.restype = C.c_int64
         L.orc_latest_timestamp.argtypes = [_P]
         L.orc_max_node_id.restype = C.c_int32
@@ -117,6 +119,9 @@ def lib():
         L.orc_feature_dim.argtypes = [_P]
         L.orc_walks.argtypes = [_P, C.c_int, C.c_int, C.c_int, C.c_int, _P, _P,
                                 C.c_size_t, _P, C.c_int, _P, _P, _P, _P, C.c_int]
+        L.orc_node_edge_at.argtypes = [_P, C.c_int, C.c_int, C.c_int, C.c_int64, C.c_int64,
+                                       C.c_int, C.c_double, C.c_double, _P]
+        L.orc_edge_at.argtypes = [_P, C.c_int, C.c_int, C.c_double, C.c_double, _P]
         L.orc_pick_linear.restype = C.c_int
         L.orc_pick_linear.argtypes = [C.c_int, C.c_int, C.c_int, C.c_double]
         L.orc_pick_exponential_index.restype = C.c_int
@@ -222,6 +227,25 @@ class OracleGraph:
 
     def array(self, name):
         return _copy_array(self._L.orc_array, self.h, name)
+
+    def set_weights(self, name, values):
+        v = np.ascontiguousarray(values, dtype=np.float64)
+        if self._L.orc_set_weights(self.h, name.encode(), _ptr(v), v.size) != 0:
+            raise ValueError(f"cannot set {name} ({v.size} values)")
+
+    def node_edge_at(self, node, picker, timestamp=-1, cutoff=-1, prev=-1, forward=True,
+                     rg=0.5, re=0.5):
+        out = np.zeros(4, dtype=np.int64)
+        self._L.orc_node_edge_at(self.h, int(forward), PICKERS[picker], int(node),
+                                 int(timestamp), int(cutoff), int(prev), float(rg), float(re),
+                                 _ptr(out))
+        return tuple(int(x) for x in out)
+
+    def edge_at(self, picker, forward=True, rg=0.5, re=0.5):
+        out = np.zeros(4, dtype=np.int64)
+        self._L.orc_edge_at(self.h, int(forward), PICKERS[picker], float(rg), float(re),
+                            _ptr(out))
+        return tuple(int(x) for x in out)
 
     @property
     def max_node_id(self):

@@ -518,6 +518,25 @@ int orc_add_edges(orc_graph* g, const int32_t* src, const int32_t* dst,
     return 0;
 }
 
+/* Overwrite one cumulative-weight array (same length required).  fp64
+ * weights are only reproducible to ~1e-15 across summation orders and libm
+ * exp implementations, and picks on the flat tail of a cumulative array turn
+ * ulp differences into different groups; tests therefore compare the weight
+ * arrays within 1e-12 and then check the sampler bit-exactly on identical
+ * weights by injecting the engine's arrays here. */
+int orc_set_weights(orc_graph* g, const char* name, const double* data, size_t len) {
+    double* dst = NULL;
+    size_t n = 0;
+    if (strcmp(name, "forward_cumulative_weights_exponential") == 0) { dst = g->fwd_cum; n = g->w_size; }
+    else if (strcmp(name, "backward_cumulative_weights_exponential") == 0) { dst = g->bwd_cum; n = g->w_size; }
+    else if (strcmp(name, "outbound_forward_cumulative_weights_exponential") == 0) { dst = g->out_fwd_w; n = g->g_out; }
+    else if (strcmp(name, "outbound_backward_cumulative_weights_exponential") == 0) { dst = g->out_bwd_w; n = g->g_out; }
+    else if (strcmp(name, "inbound_backward_cumulative_weights_exponential") == 0) { dst = g->in_bwd_w; n = g->g_in; }
+    if (dst == NULL || n != len) return 1;
+    memcpy(dst, data, len * sizeof(double));
+    return 0;
+}
+
 int64_t orc_latest_timestamp(const orc_graph* g) { return g->latest_timestamp; }
 int32_t orc_max_node_id(const orc_graph* g) { return g->max_node_id; }
 size_t orc_feature_dim(const orc_graph* g) { return g->feat_dim; }
@@ -664,6 +683,8 @@ static orc_edge edge_at(const orc_graph* g, int forward, int picker, double rg, 
         size_t ws = g->enable_weight ? g->w_size : 0;
         group = pick_weight(picker, w, ws, 0, g->T, rg, 0);
         if (group == -1) return NO_EDGE;
+        /* edge_selectors.cuh:38-43: a group index past the end is an empty range */
+        if ((size_t)group >= g->T) return NO_EDGE;
     }
     size_t from = g->ts_group_offsets[group], to = g->ts_group_offsets[group + 1];
     if (from == to) return NO_EDGE;
@@ -766,6 +787,10 @@ static long tn2v_pick(const orc_graph* g, const orc_dir_view* v, int forward, in
         double ar = orc_derive_uniform(rg, re, retry * 3 + 2);
         long gp = orc_pick_exponential_weights(v->w, v->w_size, vb, ve, gr, gb);
         if (gp == -1) return -1;
+        /* one past the node's last group: the reference reads an empty range
+         * (walk_step_helpers.cuh:19-38) -- except for the globally last group,
+         * where it reads past the array */
+        if ((size_t)gp >= ge) continue;
         size_t es = v->grp[gp];
         size_t ee = ((size_t)gp + 1 < ge) ? v->grp[gp + 1] : v->off[node + 1];
         if (es >= ee) continue;
@@ -822,12 +847,30 @@ static orc_edge node_edge_at(const orc_graph* g, int forward, int picker, int no
         }
         gpos = local + (long)gb;
     }
+    /* one past the node's last group reads as an empty range in the reference
+     * (edge_selectors.cuh:416-426), except past the globally last group */
+    if ((size_t)gpos >= ge) return NO_EDGE;
     size_t es = v.grp[gpos];
     size_t ee = ((size_t)gpos + 1 < ge) ? v.grp[gpos + 1] : v.off[node + 1];
     if (es >= ee || es >= v.idx_size || ee > v.idx_size) return NO_EDGE;
     long eid = (long)v.idx[es + (size_t)(int)(re * (int)(ee - es))];
     orc_edge out = {g->src[eid], g->dst[eid], g->ts[eid], eid};
     return out;
+}
+
+/* Selector entry points for tests (the reference's test shims
+ * test/test_temporal_graph_utils.h:56-213 call the selectors with given
+ * draws).  out = {u, i, ts, edge_id}. */
+void orc_node_edge_at(const orc_graph* g, int forward, int picker, int node, int64_t t,
+                      int64_t cutoff, int prev, double rg, double re, int64_t* out) {
+    orc_edge e = node_edge_at(g, forward, picker, node, t, cutoff, prev, rg, re);
+    out[0] = e.u; out[1] = e.i; out[2] = e.ts; out[3] = e.eid;
+}
+
+void orc_edge_at(const orc_graph* g, int forward, int picker, double rg, double re,
+                 int64_t* out) {
+    orc_edge e = edge_at(g, forward, picker, rg, re);
+    out[0] = e.u; out[1] = e.i; out[2] = e.ts; out[3] = e.eid;
 }
 
 /* core/temporal_random_walk_cpu.cuh:19-131 plus WalkSetView::add_hop /

@@ -65,6 +65,9 @@ const char* orc_last_error(void);
  * node_adj_offsets node_adj_neighbors edge_features */
 const void* orc_array(const orc_graph* g, const char* name, size_t* len,
                       size_t* elem_size);
+/* Replace a cumulative-weight array by name (length must match); 0 on
+ * success.  Lets a test run the walk loop on another engine's weights. */
+int orc_set_weights(orc_graph* g, const char* name, const double* data, size_t len);
 int64_t orc_latest_timestamp(const orc_graph* g);
 int32_t orc_max_node_id(const orc_graph* g);
 size_t orc_feature_dim(const orc_graph* g);
@@ -80,6 +83,13 @@ void orc_walks(const orc_graph* g, int max_walk_len, int walk_bias,
                const int64_t* cutoffs, size_t num_walks, const double* draws,
                int walk_padding_value, int32_t* nodes, int64_t* timestamps,
                uint64_t* lens, int64_t* edge_ids, int num_threads);
+
+/* Single selector calls with given draws (graph/edge_selectors.cuh:177-443);
+ * out = {u, i, ts, edge_id}, all -1 when no edge. */
+void orc_node_edge_at(const orc_graph* g, int forward, int picker, int node, int64_t t,
+                      int64_t cutoff, int prev, double rg, double re, int64_t* out);
+void orc_edge_at(const orc_graph* g, int forward, int picker, double rg, double re,
+                 int64_t* out);
 
 /* Pickers (random/pickers.cuh:15-126). */
 int orc_pick_linear(int start, int end, int prioritize_end, double r);

@@ -1,0 +1,577 @@
+// build.hip -- edge store and index build on the device.
+//
+// One ingest = one pass of this pipeline over the store (reference order,
+// graph/temporal_graph.cu:158-220):
+//   1. stable LSD radix sort of (ts - ts_min, position) over the old store
+//      followed by the batch -- identical to the reference's "sort the batch,
+//      stable-merge it after the old store" (temporal_graph.cu:67-134) because
+//      the old store is already sorted and precedes the batch;
+//   2. window eviction as an upper_bound on the sorted keys, folded into the
+//      gather so evicted edges are never copied (temporal_graph.cu:136-156);
+//   3. gather of src/dst/ts/features;
+//   4. max node id, dense active flags (edge_data.cu:256-296);
+//   5. timestamp groups by flag + scan + scatter (edge_data.cu:394-438);
+//   6. per direction: stable radix sort of entries by node id, CSR offsets by
+//      lower_bound, node-timestamp groups by flag + scan, per-node group counts
+//      read straight off the flag scan at each node's first entry
+//      (node_edge_index.cu:254-494);
+//   7. node2vec adjacency (edge_data.cu:298-392) and weights
+//      (edge_data.cu:440-514, node_edge_index.cu:500-684) when enabled.
+// All of it is integer/byte work bound by HBM bandwidth; no MFMA.
+#include <math.h>
+
+#include <algorithm>
+
+#include "engine.h"
+
+namespace trw {
+namespace {
+
+constexpr int kB = 256;
+
+inline unsigned grid_for(size_t n) {
+    const size_t g = (n + kB - 1) / kB;
+    return static_cast<unsigned>(g ? g : 1);
+}
+
+inline int bit_length_u64(uint64_t v) { return v ? 64 - __builtin_clzll(v) : 0; }
+
+__global__ void make_ts_keys_kernel(const int64_t* __restrict__ old_ts, size_t e_old,
+                                    const int64_t* __restrict__ new_ts, size_t n_new,
+                                    int64_t tmin, uint64_t* __restrict__ keys,
+                                    uint32_t* __restrict__ vals) {
+    const size_t i = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (i >= e_old + n_new) return;
+    const int64_t t = i < e_old ? old_ts[i] : new_ts[i - e_old];
+    keys[i] = static_cast<uint64_t>(t) - static_cast<uint64_t>(tmin);
+    vals[i] = static_cast<uint32_t>(i);
+}
+
+// out[0] = number of sorted keys <= target (upper_bound), out[1] = key at
+// that position (or 0), out[2] = last key.  target < 0 means "none".
+__global__ void evict_search_kernel(const uint64_t* __restrict__ keys, size_t n, int64_t target,
+                                    int64_t* out) {
+    size_t del = 0;
+    if (target >= 0) {
+        size_t lo = 0, hi = n;
+        const uint64_t t = static_cast<uint64_t>(target);
+        while (lo < hi) {
+            const size_t mid = lo + ((hi - lo) >> 1);
+            if (t < keys[mid]) hi = mid;
+            else lo = mid + 1;
+        }
+        del = lo;
+    }
+    out[0] = static_cast<int64_t>(del);
+    out[1] = del < n ? static_cast<int64_t>(keys[del]) : 0;
+    out[2] = n ? static_cast<int64_t>(keys[n - 1]) : 0;
+}
+
+__global__ void gather_store_kernel(const uint32_t* __restrict__ perm, size_t del, size_t kept,
+                                    const int32_t* __restrict__ os, const int32_t* __restrict__ od,
+                                    const int64_t* __restrict__ ot, size_t e_old,
+                                    const int32_t* __restrict__ ns, const int32_t* __restrict__ nd,
+                                    const int64_t* __restrict__ nt, int32_t* __restrict__ s,
+                                    int32_t* __restrict__ d, int64_t* __restrict__ t) {
+    const size_t j = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (j >= kept) return;
+    const uint32_t id = perm[del + j];
+    if (id < e_old) {
+        s[j] = os[id];
+        d[j] = od[id];
+        t[j] = ot[id];
+    } else {
+        const size_t k = id - e_old;
+        s[j] = ns[k];
+        d[j] = nd[k];
+        t[j] = nt[k];
+    }
+}
+
+__global__ void gather_feat_kernel(const uint32_t* __restrict__ perm, size_t del, size_t kept,
+                                   size_t dim, const float* __restrict__ of, size_t e_old,
+                                   const float* __restrict__ nf, float* __restrict__ f) {
+    const size_t x = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (x >= kept * dim) return;
+    const size_t j = x / dim, c = x - j * dim;
+    const uint32_t id = perm[del + j];
+    f[x] = id < e_old ? of[static_cast<size_t>(id) * dim + c]
+                      : nf[(static_cast<size_t>(id) - e_old) * dim + c];
+}
+
+__global__ void ts_group_flags_kernel(const int64_t* __restrict__ ts, size_t n,
+                                      uint32_t* __restrict__ flags) {
+    const size_t i = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (i >= n) return;
+    flags[i] = (i == 0 || ts[i] != ts[i - 1]) ? 1u : 0u;
+}
+
+__global__ void ts_group_scatter_kernel(const int64_t* __restrict__ ts, size_t n,
+                                        const uint32_t* __restrict__ flags,
+                                        const uint32_t* __restrict__ scan,
+                                        uint32_t* __restrict__ off, int64_t* __restrict__ uq) {
+    const size_t i = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (i >= n) return;
+    if (flags[i]) {
+        off[scan[i]] = static_cast<uint32_t>(i);
+        uq[scan[i]] = ts[i];
+    }
+    if (i == n - 1) off[scan[n]] = static_cast<uint32_t>(n);
+}
+
+__global__ void node_keys_kernel(const int32_t* __restrict__ nodes, size_t n,
+                                 uint32_t* __restrict__ keys, uint32_t* __restrict__ vals) {
+    const size_t i = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (i >= n) return;
+    keys[i] = static_cast<uint32_t>(nodes[i]);
+    vals[i] = static_cast<uint32_t>(i);
+}
+
+// Undirected: entry 2i = (edge i, src_i), entry 2i+1 = (edge i, dst_i)
+// (node_edge_index.cu:306-321).
+__global__ void node_keys_pairs_kernel(const int32_t* __restrict__ s, const int32_t* __restrict__ d,
+                                       size_t e, uint32_t* __restrict__ keys,
+                                       uint32_t* __restrict__ vals) {
+    const size_t i = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (i >= e) return;
+    keys[2 * i] = static_cast<uint32_t>(s[i]);
+    keys[2 * i + 1] = static_cast<uint32_t>(d[i]);
+    vals[2 * i] = static_cast<uint32_t>(i);
+    vals[2 * i + 1] = static_cast<uint32_t>(i);
+}
+
+// off[u] = first sorted position whose node >= u, u in [0, vc).
+__global__ void lower_bound_offsets_kernel(const uint32_t* __restrict__ keys, size_t n, size_t vc,
+                                           uint32_t* __restrict__ off) {
+    const size_t u = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (u >= vc) return;
+    size_t lo = 0, hi = n;
+    while (lo < hi) {
+        const size_t mid = lo + ((hi - lo) >> 1);
+        if (keys[mid] < u) lo = mid + 1;
+        else hi = mid;
+    }
+    off[u] = static_cast<uint32_t>(lo);
+}
+
+__global__ void node_group_flags_kernel(const uint32_t* __restrict__ keys,
+                                        const uint32_t* __restrict__ idx,
+                                        const int64_t* __restrict__ ts, size_t n,
+                                        uint32_t* __restrict__ flags) {
+    const size_t k = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (k >= n) return;
+    flags[k] = (k == 0 || keys[k] != keys[k - 1] || ts[idx[k]] != ts[idx[k - 1]]) ? 1u : 0u;
+}
+
+__global__ void node_group_scatter_kernel(const uint32_t* __restrict__ flags,
+                                          const uint32_t* __restrict__ scan,
+                                          const uint32_t* __restrict__ idx,
+                                          const int64_t* __restrict__ ts, size_t n,
+                                          uint32_t* __restrict__ grp,
+                                          int64_t* __restrict__ first_ts) {
+    const size_t k = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (k >= n) return;
+    if (flags[k]) {
+        const uint32_t g = scan[k];
+        grp[g] = static_cast<uint32_t>(k);
+        first_ts[g] = ts[idx[k]];
+    }
+    if (k == n - 1) grp[scan[n]] = static_cast<uint32_t>(n);
+}
+
+// cnt[u] = number of groups of nodes < u = flag scan at u's first entry.
+__global__ void node_group_counts_kernel(const uint32_t* __restrict__ off,
+                                         const uint32_t* __restrict__ scan, size_t vc,
+                                         uint32_t* __restrict__ cnt) {
+    const size_t u = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (u >= vc) return;
+    cnt[u] = scan[off[u]];
+}
+
+__global__ void active_flags_kernel(const uint32_t* __restrict__ out_off,
+                                    const uint32_t* __restrict__ in_off, size_t v,
+                                    uint8_t* __restrict__ active) {
+    const size_t u = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (u >= v) return;
+    bool a = out_off[u + 1] > out_off[u];
+    if (in_off) a = a || in_off[u + 1] > in_off[u];
+    active[u] = a ? 1 : 0;
+}
+
+// node2vec adjacency: key = owner << b | neighbour for both directions of
+// every edge; sorting it orders lists by owner and each list ascending.
+__global__ void adj_keys_kernel(const int32_t* __restrict__ s, const int32_t* __restrict__ d,
+                                size_t e, int b, uint64_t* __restrict__ keys) {
+    const size_t i = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (i >= e) return;
+    const uint64_t u = static_cast<uint32_t>(s[i]), v = static_cast<uint32_t>(d[i]);
+    keys[2 * i] = (u << b) | v;
+    keys[2 * i + 1] = (v << b) | u;
+}
+
+__global__ void adj_finish_kernel(const uint64_t* __restrict__ keys, size_t n, uint64_t mask,
+                                  int32_t* __restrict__ nbr) {
+    const size_t k = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (k >= n) return;
+    nbr[k] = static_cast<int32_t>(keys[k] & mask);
+}
+
+__global__ void adj_offsets_kernel(const uint64_t* __restrict__ keys, size_t n, int b, size_t cnt,
+                                   uint32_t* __restrict__ off) {
+    const size_t u = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (u >= cnt) return;
+    const uint64_t target = static_cast<uint64_t>(u) << b;
+    size_t lo = 0, hi = n;
+    while (lo < hi) {
+        const size_t mid = lo + ((hi - lo) >> 1);
+        if (keys[mid] < target) lo = mid + 1;
+        else hi = mid;
+    }
+    off[u] = static_cast<uint32_t>(lo);
+}
+
+// Global per-timestamp-group weights before normalisation
+// (edge_data.cu:477-492).
+__global__ void global_weights_kernel(const uint32_t* __restrict__ off,
+                                      const int64_t* __restrict__ uq, size_t t_groups,
+                                      int64_t tmin, int64_t tmax, double bound, double scale,
+                                      double* __restrict__ fwd, double* __restrict__ bwd) {
+    const size_t g = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (g >= t_groups) return;
+    const double size = static_cast<double>(off[g + 1] - off[g]);
+    const int64_t t = uq[g];
+    const double tf = static_cast<double>(tmin - t);
+    const double tb = static_cast<double>(t - tmax);
+    const double fs = bound > 0 ? tf * scale : tf;
+    const double bs = bound > 0 ? tb * scale : tb;
+    fwd[g] = size * exp(fs);
+    bwd[g] = size * exp(bs);
+}
+
+__global__ void divide_kernel(double* __restrict__ a, double* __restrict__ b, size_t n,
+                              const double* __restrict__ sums_a, const double* __restrict__ sums_b) {
+    const size_t i = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (i >= n) return;
+    a[i] = a[i] / sums_a[0];
+    b[i] = b[i] / sums_b[0];
+}
+
+// Per-node cumulative exponential weights (node_edge_index.cu:500-640): one
+// thread per node; within a node the normalised weights are accumulated
+// sequentially in group order, exactly as the reference does, so the
+// cumulative array is monotone per node.
+__global__ void node_weights_kernel(const uint32_t* __restrict__ cnt,
+                                    const uint32_t* __restrict__ grp,
+                                    const int64_t* __restrict__ first_ts, size_t nodes,
+                                    double bound, int compute_forward, double* __restrict__ wf,
+                                    double* __restrict__ wb) {
+    const size_t u = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (u >= nodes) return;
+    const uint32_t s = cnt[u], e = cnt[u + 1];
+    if (s >= e) return;
+    const int64_t mn = first_ts[s], mx = first_ts[e - 1];
+    const double diff = static_cast<double>(mx - mn);
+    const double scale = (bound > 0 && diff > 0) ? bound / diff : 1.0;
+    double fsum = 0.0, bsum = 0.0;
+    for (uint32_t p = s; p < e; ++p) {
+        const double sz = static_cast<double>(grp[p + 1] - grp[p]);
+        const int64_t t = first_ts[p];
+        const double bsc = bound > 0 ? static_cast<double>(t - mx) * scale
+                                     : static_cast<double>(t - mx);
+        const double b = sz * exp(bsc);
+        wb[p] = b;
+        bsum += b;
+        if (compute_forward) {
+            const double fsc = bound > 0 ? static_cast<double>(mn - t) * scale
+                                         : static_cast<double>(mn - t);
+            const double f = sz * exp(fsc);
+            wf[p] = f;
+            fsum += f;
+        }
+    }
+    double fc = 0.0, bc = 0.0;
+    for (uint32_t p = s; p < e; ++p) {
+        bc += wb[p] / bsum;
+        wb[p] = bc;
+        if (compute_forward) {
+            fc += wf[p] / fsum;
+            wf[p] = fc;
+        }
+    }
+}
+
+}  // namespace
+
+void validate_batch(const Engine& e, const void* feat, size_t n, size_t dim) {
+    // graph/edge_data.cu:71-89
+    if (feat != nullptr && dim == 0)
+        throw std::runtime_error("edge_features provided but feature_dim is 0");
+    if (e.E != 0 && dim != e.feat_dim)
+        throw std::runtime_error("feature_dim mismatch with existing data.feature_dim");
+    const size_t eff = e.E == 0 ? dim : e.feat_dim;
+    if (feat == nullptr && dim != 0)
+        throw std::runtime_error("feature_dim must be 0 when edge_features is not provided");
+    if (eff > 0 && feat == nullptr && n > 0)
+        throw std::runtime_error(
+            "edge features enabled; non-empty ingestion must provide edge_features");
+    if (e.E + n > 0x7fffffffull)
+        throw std::runtime_error("edge store would exceed 2^31-1 edges");
+}
+
+namespace {
+
+// Stable per-direction node index from `keys`/`vals` already generated in
+// e.k32a / e.v32a (n entries).
+void build_direction(Engine& e, DirIndex& dir, size_t n, int key_bits, size_t vc,
+                     int64_t* host_scratch) {
+    hipStream_t s = e.stream;
+    dir.present = true;
+    dir.n_entries = n;
+    const int which = radix_sort_u32(e.k32a.p, e.v32a.p, e.k32b.p, e.v32b.p, n, 0, key_bits,
+                                     e.hist.p, e.hist_scratch.p, s);
+    DBuf<uint32_t>& ks = which ? e.k32b : e.k32a;
+    DBuf<uint32_t>& vs = which ? e.v32b : e.v32a;
+    dir.key.resize(n);
+    dir.idx.resize(n);
+    if (n) {
+        check_hip(hipMemcpyAsync(dir.key.p, ks.p, n * 4, hipMemcpyDeviceToDevice, s), "copy keys");
+        check_hip(hipMemcpyAsync(dir.idx.p, vs.p, n * 4, hipMemcpyDeviceToDevice, s), "copy idx");
+    }
+    dir.off.resize(vc);
+    hipLaunchKernelGGL(lower_bound_offsets_kernel, dim3(grid_for(vc)), dim3(kB), 0, s, dir.key.p,
+                       n, vc, dir.off.p);
+    hipLaunchKernelGGL(node_group_flags_kernel, dim3(grid_for(n)), dim3(kB), 0, s, dir.key.p,
+                       dir.idx.p, e.ts.p, n, e.flags.p);
+    exclusive_scan_u32(e.flags.p, e.scan.p, n, e.scan_scratch.p, s);
+    uint32_t g = 0;
+    check_hip(hipMemcpyAsync(host_scratch, e.scan.p + n, 4, hipMemcpyDeviceToHost, s), "read g");
+    e.sync();
+    std::memcpy(&g, host_scratch, 4);
+    dir.n_groups = g;
+    dir.grp.resize(static_cast<size_t>(g) + 1);
+    dir.first_ts.resize(g);
+    if (n) {
+        hipLaunchKernelGGL(node_group_scatter_kernel, dim3(grid_for(n)), dim3(kB), 0, s,
+                           e.flags.p, e.scan.p, dir.idx.p, e.ts.p, n, dir.grp.p, dir.first_ts.p);
+    } else {
+        check_hip(hipMemsetAsync(dir.grp.p, 0, 4, s), "grp terminator");
+    }
+    dir.cnt.resize(vc);
+    hipLaunchKernelGGL(node_group_counts_kernel, dim3(grid_for(vc)), dim3(kB), 0, s, dir.off.p,
+                       e.scan.p, vc, dir.cnt.p);
+    check_hip(hipGetLastError(), "direction index launch");
+}
+
+}  // namespace
+
+void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_ts,
+                   const float* d_feat, size_t n, size_t dim) {
+    if (n == 0) return;
+    hipStream_t s = stream;
+    int64_t* hs = reinterpret_cast<int64_t*>(host_scalars);
+    check_hip(hipEventRecord(ev[0], s), "event");
+
+    if (E == 0) feat_dim = dim;
+    const size_t e_old = E, etot = E + n;
+
+    // the batch's endpoints, for ..._for_last_batch
+    last_src.resize(n);
+    last_dst.resize(n);
+    check_hip(hipMemcpyAsync(last_src.p, d_src, n * 4, hipMemcpyDeviceToDevice, s), "last src");
+    check_hip(hipMemcpyAsync(last_dst.p, d_dst, n * 4, hipMemcpyDeviceToDevice, s), "last dst");
+    last_n = n;
+
+    // ---- 1. key range and latest timestamp
+    red64.ensure(2 + 2 * 1024);
+    minmax_i64(d_ts, n, red64.p, s);
+    check_hip(hipMemcpyAsync(hs, red64.p, 16, hipMemcpyDeviceToHost, s), "read minmax");
+    sync();
+    int64_t tmin = hs[0], tmax = hs[1];
+    if (e_old) {
+        tmin = std::min(tmin, store_tmin);
+        tmax = std::max(tmax, store_tmax);
+    }
+    latest_ts = std::max(latest_ts, hs[1]);
+
+    // ---- 2. stable radix sort by (ts, position)
+    k64a.ensure(etot);
+    k64b.ensure(etot);
+    v32a.ensure(std::max(etot, 2 * etot));
+    v32b.ensure(std::max(etot, 2 * etot));
+    hist.ensure(radix_hist_elems(2 * etot));
+    hist_scratch.ensure(scan_scratch_elems(radix_hist_elems(2 * etot)));
+    hipLaunchKernelGGL(make_ts_keys_kernel, dim3(grid_for(etot)), dim3(kB), 0, s, ts.p, e_old,
+                       d_ts, n, tmin, k64a.p, v32a.p);
+    const int bits = bit_length_u64(static_cast<uint64_t>(tmax) - static_cast<uint64_t>(tmin));
+    const int which = radix_sort_u64(k64a.p, v32a.p, k64b.p, v32b.p, etot, 0, bits, hist.p,
+                                     hist_scratch.p, s);
+    uint64_t* keys = which ? k64b.p : k64a.p;
+    uint32_t* perm = which ? v32b.p : v32a.p;
+
+    // ---- 3. window eviction: drop ts <= latest - capacity
+    int64_t target = -1;
+    if (cfg.max_time_capacity > 0) {
+        const int64_t cutoff = latest_ts - cfg.max_time_capacity;
+        if (cutoff >= tmin) target = static_cast<int64_t>(static_cast<uint64_t>(cutoff) -
+                                                          static_cast<uint64_t>(tmin));
+    }
+    hipLaunchKernelGGL(evict_search_kernel, dim3(1), dim3(1), 0, s, keys, etot, target, red64.p);
+    check_hip(hipMemcpyAsync(hs, red64.p, 24, hipMemcpyDeviceToHost, s), "read evict");
+    sync();
+    const size_t del = static_cast<size_t>(hs[0]);
+    const size_t kept = etot - del;
+    store_tmin = static_cast<int64_t>(static_cast<uint64_t>(tmin) + static_cast<uint64_t>(hs[1]));
+    store_tmax = static_cast<int64_t>(static_cast<uint64_t>(tmin) + static_cast<uint64_t>(hs[2]));
+
+    // ---- 4. gather the kept suffix into the new store
+    src2.resize(kept);
+    dst2.resize(kept);
+    ts2.resize(kept);
+    hipLaunchKernelGGL(gather_store_kernel, dim3(grid_for(kept)), dim3(kB), 0, s, perm, del, kept,
+                       src.p, dst.p, ts.p, e_old, d_src, d_dst, d_ts, src2.p, dst2.p, ts2.p);
+    if (feat_dim > 0) {
+        feat2.resize(kept * feat_dim);
+        hipLaunchKernelGGL(gather_feat_kernel, dim3(grid_for(kept * feat_dim)), dim3(kB), 0, s,
+                           perm, del, kept, feat_dim, feat.p, e_old, d_feat, feat2.p);
+        feat.swap(feat2);
+    }
+    src.swap(src2);
+    dst.swap(dst2);
+    ts.swap(ts2);
+    E = kept;
+    check_hip(hipGetLastError(), "gather launch");
+    check_hip(hipEventRecord(ev[1], s), "event");
+
+    // ---- 5. max node id, timestamp groups
+    red32.ensure(4);
+    max_i32_pair(src.p, dst.p, E, red32.p, s);
+    flags.ensure(2 * E + 1);
+    scan.ensure(2 * E + 1);
+    scan_scratch.ensure(scan_scratch_elems(2 * E + 1));
+    hipLaunchKernelGGL(ts_group_flags_kernel, dim3(grid_for(E)), dim3(kB), 0, s, ts.p, E, flags.p);
+    exclusive_scan_u32(flags.p, scan.p, E, scan_scratch.p, s);
+    check_hip(hipMemcpyAsync(hs, red32.p, 4, hipMemcpyDeviceToHost, s), "read max id");
+    check_hip(hipMemcpyAsync(hs + 1, scan.p + E, 4, hipMemcpyDeviceToHost, s), "read T");
+    sync();
+    int32_t mx;
+    uint32_t tg;
+    std::memcpy(&mx, hs, 4);
+    std::memcpy(&tg, hs + 1, 4);
+    max_node_id = mx;
+    T = tg;
+    tsg_off.resize(T + 1);
+    uniq_ts.resize(T);
+    hipLaunchKernelGGL(ts_group_scatter_kernel, dim3(grid_for(E)), dim3(kB), 0, s, ts.p, E,
+                       flags.p, scan.p, tsg_off.p, uniq_ts.p);
+
+    // ---- 6. node index
+    const size_t v = static_cast<size_t>(max_node_id) + 1;  // active_node_ids size
+    const size_t vc = v + 1;                                // node_index_capacity
+    const int key_bits = std::max(1, bit_length_u64(static_cast<uint64_t>(max_node_id)));
+    k32a.ensure(2 * E);
+    k32b.ensure(2 * E);
+    if (cfg.is_directed) {
+        hipLaunchKernelGGL(node_keys_kernel, dim3(grid_for(E)), dim3(kB), 0, s, src.p, E, k32a.p,
+                           v32a.p);
+        build_direction(*this, out, E, key_bits, vc, hs);
+        hipLaunchKernelGGL(node_keys_kernel, dim3(grid_for(E)), dim3(kB), 0, s, dst.p, E, k32a.p,
+                           v32a.p);
+        build_direction(*this, in, E, key_bits, vc, hs);
+    } else {
+        hipLaunchKernelGGL(node_keys_pairs_kernel, dim3(grid_for(E)), dim3(kB), 0, s, src.p, dst.p,
+                           E, k32a.p, v32a.p);
+        build_direction(*this, out, 2 * E, key_bits, vc, hs);
+        in.clear();
+    }
+    active.resize(v);
+    hipLaunchKernelGGL(active_flags_kernel, dim3(grid_for(v)), dim3(kB), 0, s, out.off.p,
+                       cfg.is_directed ? in.off.p : nullptr, v, active.p);
+    check_hip(hipGetLastError(), "index launch");
+    check_hip(hipEventRecord(ev[2], s), "event");
+
+    // ---- 7. node2vec adjacency
+    adj_ready = false;
+    if (cfg.enable_temporal_node2vec) {
+        const int b = key_bits;
+        const size_t m2 = 2 * E;
+        k64a.ensure(m2);
+        k64b.ensure(m2);
+        hipLaunchKernelGGL(adj_keys_kernel, dim3(grid_for(E)), dim3(kB), 0, s, src.p, dst.p, E, b,
+                           k64a.p);
+        const int w = radix_sort_u64(k64a.p, nullptr, k64b.p, nullptr, m2, 0, 2 * b, hist.p,
+                                     hist_scratch.p, s);
+        uint64_t* ak = w ? k64b.p : k64a.p;
+        adj_nbr.resize(m2);
+        hipLaunchKernelGGL(adj_finish_kernel, dim3(grid_for(m2)), dim3(kB), 0, s, ak, m2,
+                           (1ull << b) - 1, adj_nbr.p);
+        adj_off.resize(v + 1);
+        hipLaunchKernelGGL(adj_offsets_kernel, dim3(grid_for(v + 1)), dim3(kB), 0, s, ak, m2, b,
+                           v + 1, adj_off.p);
+        check_hip(hipGetLastError(), "adjacency launch");
+        adj_ready = true;
+    }
+
+    // ---- 8. weights
+    weights_ready = false;
+    const bool weights = cfg.enable_weight_computation || cfg.enable_temporal_node2vec;
+    if (weights) {
+        const double bound = cfg.timescale_bound;
+        // global (edge_data.cu:440-514): pivots are the store's min/max ts
+        const double diff = static_cast<double>(store_tmax - store_tmin);
+        const double scale = (bound > 0 && diff > 0) ? bound / diff : 1.0;
+        fwd_cum.resize(T);
+        bwd_cum.resize(T);
+        hipLaunchKernelGGL(global_weights_kernel, dim3(grid_for(T)), dim3(kB), 0, s, tsg_off.p,
+                           uniq_ts.p, T, store_tmin, store_tmax, bound, scale, fwd_cum.p,
+                           bwd_cum.p);
+        dscratch.ensure(2 * (2 + 1024));
+        sum_f64(fwd_cum.p, T, dscratch.p, s);
+        sum_f64(bwd_cum.p, T, dscratch.p + 2 + 1024, s);
+        hipLaunchKernelGGL(divide_kernel, dim3(grid_for(T)), dim3(kB), 0, s, fwd_cum.p, bwd_cum.p,
+                           T, dscratch.p, dscratch.p + 2 + 1024);
+        fscan_scratch.ensure(scan_scratch_elems(std::max<size_t>(T, out.n_groups)));
+        inclusive_scan_f64(fwd_cum.p, T, fscan_scratch.p, s);
+        inclusive_scan_f64(bwd_cum.p, T, fscan_scratch.p, s);
+        // per node (node_edge_index.cu:644-684)
+        out.w_fwd.resize(out.n_groups);
+        out.w_bwd.resize(out.n_groups);
+        hipLaunchKernelGGL(node_weights_kernel, dim3(grid_for(v)), dim3(kB), 0, s, out.cnt.p,
+                           out.grp.p, out.first_ts.p, v, bound, 1, out.w_fwd.p, out.w_bwd.p);
+        if (cfg.is_directed) {
+            in.w_bwd.resize(in.n_groups);
+            hipLaunchKernelGGL(node_weights_kernel, dim3(grid_for(v)), dim3(kB), 0, s, in.cnt.p,
+                               in.grp.p, in.first_ts.p, v, bound, 0, nullptr, in.w_bwd.p);
+        }
+        check_hip(hipGetLastError(), "weights launch");
+        weights_ready = true;
+    }
+
+    check_hip(hipEventRecord(ev[3], s), "event");
+    sync();
+    float ms = 0;
+    check_hip(hipEventElapsedTime(&ms, ev[0], ev[3]), "elapsed");
+    timings.build_ms = ms;
+    check_hip(hipEventElapsedTime(&ms, ev[0], ev[1]), "elapsed");
+    timings.sort_ms = ms;
+    check_hip(hipEventElapsedTime(&ms, ev[1], ev[2]), "elapsed");
+    timings.index_ms = ms;
+}
+
+void Engine::clear() {
+    // core/temporal_random_walk.cu:358-373: a fresh store with the same config
+    E = 0;
+    feat_dim = 0;
+    latest_ts = 0;
+    T = 0;
+    max_node_id = -1;
+    store_tmin = store_tmax = 0;
+    src.n = dst.n = ts.n = feat.n = tsg_off.n = uniq_ts.n = active.n = 0;
+    fwd_cum.n = bwd_cum.n = adj_off.n = adj_nbr.n = 0;
+    weights_ready = adj_ready = false;
+    out.clear();
+    in.clear();
+    last_n = 0;
+    last_src.n = last_dst.n = 0;
+}
+
+}  // namespace trw

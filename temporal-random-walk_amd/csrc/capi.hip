@@ -1,0 +1,388 @@
+// capi.hip -- the extern "C" boundary declared in include/trw_engine.h.
+//
+// Every entry point: pins the handle's device (restoring the caller's on
+// return, like the reference's CudaDeviceGuard, common/error_handlers.cuh:
+// 111-139), runs the engine, maps C++ exceptions to trw_status and keeps the
+// message in a thread-local buffer for trw_last_error().
+#include <stdlib.h>
+
+#include <new>
+#include <string>
+#include <vector>
+
+#include "engine.h"
+
+namespace trw {
+
+Engine::Engine(const trw_config& c) : cfg(c), device(c.device_id) {
+    check_hip(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
+    for (auto& e : ev) check_hip(hipEventCreate(&e), "hipEventCreate");
+    check_hip(hipHostMalloc(&host_scalars, 256, hipHostMallocDefault), "hipHostMalloc");
+}
+
+Engine::~Engine() {
+    if (stream) (void)hipStreamSynchronize(stream);
+    for (auto& e : ev)
+        if (e) (void)hipEventDestroy(e);
+    if (host_scalars) (void)hipHostFree(host_scalars);
+    if (stream) (void)hipStreamDestroy(stream);
+}
+
+size_t Engine::memory_used() const {
+    size_t b = src.bytes() + dst.bytes() + ts.bytes() + feat.bytes() + tsg_off.bytes() +
+               uniq_ts.bytes() + active.bytes() + fwd_cum.bytes() + bwd_cum.bytes() +
+               adj_off.bytes() + adj_nbr.bytes();
+    for (const DirIndex* d : {&out, &in}) {
+        b += d->off.bytes() + d->idx.bytes() + d->cnt.bytes() + d->grp.bytes() +
+             d->first_ts.bytes() + d->w_fwd.bytes() + d->w_bwd.bytes();
+    }
+    return b;
+}
+
+}  // namespace trw
+
+using trw::Engine;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+struct DeviceGuard {
+    int prev = -1;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        trw::check_hip(hipSetDevice(dev), "hipSetDevice");
+    }
+    ~DeviceGuard() {
+        if (prev >= 0) (void)hipSetDevice(prev);
+    }
+};
+
+template <typename F>
+trw_status guarded(void* h, F&& f) {
+    try {
+        if (!h) throw trw::InvalidArgument("null handle");
+        Engine* e = static_cast<Engine*>(h);
+        DeviceGuard g(e->device);
+        f(*e);
+        return TRW_OK;
+    } catch (const trw::InvalidArgument& ex) {
+        g_last_error = ex.what();
+        return TRW_ERR_INVALID_ARGUMENT;
+    } catch (const std::bad_alloc& ex) {
+        g_last_error = ex.what();
+        return TRW_ERR_OUT_OF_MEMORY;
+    } catch (const std::exception& ex) {
+        g_last_error = ex.what();
+        return TRW_ERR_RUNTIME;
+    }
+}
+
+template <typename T>
+T* host_alloc(size_t n) {
+    void* p = malloc(n ? n * sizeof(T) : 1);
+    if (!p) throw std::bad_alloc();
+    return static_cast<T*>(p);
+}
+
+template <typename T>
+void d2h(T* dst, const T* src, size_t n, hipStream_t s) {
+    if (n) trw::check_hip(hipMemcpyAsync(dst, src, n * sizeof(T), hipMemcpyDeviceToHost, s), "D2H");
+}
+
+template <typename D, typename S>
+void widen_from_device(void* out, const S* dsrc, size_t n, hipStream_t s) {
+    std::vector<S> tmp(n);
+    d2h(tmp.data(), dsrc, n, s);
+    trw::check_hip(hipStreamSynchronize(s), "sync");
+    D* o = static_cast<D*>(out);
+    for (size_t i = 0; i < n; ++i) o[i] = static_cast<D>(tmp[i]);
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t trw_abi_version(void) { return TRW_ABI_VERSION; }
+
+const char* trw_last_error(void) { return g_last_error.c_str(); }
+
+trw_status trw_create(const trw_config* config, void** out_handle) {
+    try {
+        if (!config || !out_handle) throw trw::InvalidArgument("null argument");
+        int count = 0;
+        if (hipGetDeviceCount(&count) != hipSuccess || count == 0) {
+            g_last_error = "no HIP device available: this engine runs only on the GPU";
+            return TRW_ERR_NO_DEVICE;
+        }
+        if (config->device_id < 0 || config->device_id >= count)
+            throw trw::InvalidArgument("device_id out of range");
+        if (config->node2vec_p == 0.0 || config->node2vec_q == 0.0)
+            throw trw::InvalidArgument("node2vec p and q must be non-zero");
+        DeviceGuard g(config->device_id);
+        *out_handle = new Engine(*config);
+        return TRW_OK;
+    } catch (const trw::InvalidArgument& ex) {
+        g_last_error = ex.what();
+        return TRW_ERR_INVALID_ARGUMENT;
+    } catch (const std::exception& ex) {
+        g_last_error = ex.what();
+        return TRW_ERR_RUNTIME;
+    }
+}
+
+trw_status trw_destroy(void* handle) {
+    if (!handle) return TRW_OK;
+    Engine* e = static_cast<Engine*>(handle);
+    try {
+        DeviceGuard g(e->device);
+        delete e;
+    } catch (const std::exception& ex) {
+        g_last_error = ex.what();
+        return TRW_ERR_RUNTIME;
+    }
+    return TRW_OK;
+}
+
+trw_status trw_add_edges(void* handle, const int32_t* sources, const int32_t* targets,
+                         const int64_t* timestamps, uint64_t n, const float* edge_features,
+                         uint64_t feature_dim) {
+    return guarded(handle, [&](Engine& e) {
+        if (n == 0) return;  // core/temporal_random_walk.cu:285
+        if (!sources || !targets || !timestamps) throw trw::InvalidArgument("null edge arrays");
+        trw::validate_batch(e, edge_features, n, feature_dim);
+        hipStream_t s = e.stream;
+        e.stage_src.resize(n);
+        e.stage_dst.resize(n);
+        e.stage_ts.resize(n);
+        trw::check_hip(hipMemcpyAsync(e.stage_src.p, sources, n * 4, hipMemcpyHostToDevice, s), "H2D");
+        trw::check_hip(hipMemcpyAsync(e.stage_dst.p, targets, n * 4, hipMemcpyHostToDevice, s), "H2D");
+        trw::check_hip(hipMemcpyAsync(e.stage_ts.p, timestamps, n * 8, hipMemcpyHostToDevice, s), "H2D");
+        const float* df = nullptr;
+        if (edge_features && feature_dim) {
+            e.stage_feat.resize(n * feature_dim);
+            trw::check_hip(hipMemcpyAsync(e.stage_feat.p, edge_features, n * feature_dim * 4,
+                                          hipMemcpyHostToDevice, s),
+                           "H2D");
+            df = e.stage_feat.p;
+        }
+        e.build(e.stage_src.p, e.stage_dst.p, e.stage_ts.p, df, n, feature_dim);
+    });
+}
+
+trw_status trw_add_edges_device(void* handle, const int32_t* d_sources, const int32_t* d_targets,
+                                const int64_t* d_timestamps, uint64_t n,
+                                const float* d_edge_features, uint64_t feature_dim) {
+    return guarded(handle, [&](Engine& e) {
+        if (n == 0) return;
+        if (!d_sources || !d_targets || !d_timestamps) throw trw::InvalidArgument("null edge arrays");
+        trw::validate_batch(e, d_edge_features, n, feature_dim);
+        e.build(d_sources, d_targets, d_timestamps, d_edge_features, n, feature_dim);
+    });
+}
+
+trw_status trw_sample_device(void* handle, const trw_sample_params* params, trw_walks* out) {
+    return guarded(handle, [&](Engine& e) {
+        if (!params || !out) throw trw::InvalidArgument("null argument");
+        e.sample(*params);
+        out->num_walks = e.w_num;
+        out->max_walk_len = e.w_len;
+        out->feature_dim = static_cast<int32_t>(e.w_feat.n ? e.feat_dim : 0);
+        out->nodes = e.w_nodes.p;
+        out->timestamps = e.w_ts.p;
+        out->walk_lens = e.w_lens.p;
+        out->edge_ids = e.w_eids.p;
+        out->edge_features = e.w_feat.n ? e.w_feat.p : nullptr;
+    });
+}
+
+trw_status trw_sample(void* handle, const trw_sample_params* params, trw_walks* out) {
+    return guarded(handle, [&](Engine& e) {
+        if (!params || !out) throw trw::InvalidArgument("null argument");
+        e.sample(*params);
+        hipStream_t s = e.stream;
+        const size_t nw = e.w_num, L = static_cast<size_t>(e.w_len);
+        const size_t el = L ? L - 1 : 0;
+        trw_walks r{};
+        r.num_walks = nw;
+        r.max_walk_len = e.w_len;
+        r.nodes = host_alloc<int32_t>(nw * L);
+        r.timestamps = host_alloc<int64_t>(nw * L);
+        r.walk_lens = host_alloc<uint64_t>(nw);
+        r.edge_ids = host_alloc<int64_t>(nw * el);
+        d2h(r.nodes, e.w_nodes.p, nw * L, s);
+        d2h(r.timestamps, e.w_ts.p, nw * L, s);
+        d2h(r.walk_lens, e.w_lens.p, nw, s);
+        d2h(r.edge_ids, e.w_eids.p, nw * el, s);
+        if (e.w_feat.n) {
+            r.feature_dim = static_cast<int32_t>(e.feat_dim);
+            r.edge_features = host_alloc<float>(e.w_feat.n);
+            d2h(r.edge_features, e.w_feat.p, e.w_feat.n, s);
+        }
+        e.sync();
+        *out = r;
+    });
+}
+
+void trw_walks_free(trw_walks* w) {
+    if (!w) return;
+    free(w->nodes);
+    free(w->timestamps);
+    free(w->walk_lens);
+    free(w->edge_ids);
+    free(w->edge_features);
+    w->nodes = nullptr;
+    w->timestamps = nullptr;
+    w->walk_lens = nullptr;
+    w->edge_ids = nullptr;
+    w->edge_features = nullptr;
+}
+
+trw_status trw_get_node_count(void* handle, uint64_t* out) {
+    return guarded(handle, [&](Engine& e) {
+        std::vector<uint8_t> a(e.active.n);
+        d2h(a.data(), e.active.p, a.size(), e.stream);
+        e.sync();
+        uint64_t c = 0;
+        for (uint8_t x : a) c += x;
+        *out = c;
+    });
+}
+
+trw_status trw_get_edge_count(void* handle, uint64_t* out) {
+    return guarded(handle, [&](Engine& e) { *out = e.E; });
+}
+
+trw_status trw_get_node_ids(void* handle, int32_t* out, uint64_t cap, uint64_t* len) {
+    return guarded(handle, [&](Engine& e) {
+        std::vector<uint8_t> a(e.active.n);
+        d2h(a.data(), e.active.p, a.size(), e.stream);
+        e.sync();
+        uint64_t c = 0;
+        for (size_t i = 0; i < a.size(); ++i) {
+            if (a[i]) {
+                if (out && c < cap) out[c] = static_cast<int32_t>(i);
+                ++c;
+            }
+        }
+        *len = c;
+    });
+}
+
+trw_status trw_get_node_degrees(void* handle, const int32_t* nodes, uint64_t n,
+                                int32_t direction, int64_t* out) {
+    return guarded(handle, [&](Engine& e) {
+        if (n && (!nodes || !out)) throw trw::InvalidArgument("null argument");
+        const bool forward = direction == TRW_FORWARD_IN_TIME;
+        const trw::DirIndex& d = (e.cfg.is_directed && !forward) ? e.in : e.out;
+        std::vector<uint32_t> off(d.off.n);
+        d2h(off.data(), d.off.p, off.size(), e.stream);
+        e.sync();
+        const int64_t osz = static_cast<int64_t>(off.size());
+        for (uint64_t i = 0; i < n; ++i) {
+            const int32_t u = nodes[i];
+            out[i] = (u < 0 || u >= osz - 1) ? 0 : static_cast<int64_t>(off[u + 1] - off[u]);
+        }
+    });
+}
+
+trw_status trw_get_edges(void* handle, int32_t* sources, int32_t* targets, int64_t* timestamps,
+                         uint64_t cap, uint64_t* len) {
+    return guarded(handle, [&](Engine& e) {
+        *len = e.E;
+        if (!sources || !targets || !timestamps) return;
+        if (cap < e.E) throw trw::InvalidArgument("output capacity too small");
+        d2h(sources, e.src.p, e.E, e.stream);
+        d2h(targets, e.dst.p, e.E, e.stream);
+        d2h(timestamps, e.ts.p, e.E, e.stream);
+        e.sync();
+    });
+}
+
+trw_status trw_get_is_directed(void* handle, int32_t* out) {
+    return guarded(handle, [&](Engine& e) { *out = e.cfg.is_directed ? 1 : 0; });
+}
+
+trw_status trw_get_memory_used(void* handle, uint64_t* out) {
+    return guarded(handle, [&](Engine& e) { *out = e.memory_used(); });
+}
+
+trw_status trw_get_feature_dim(void* handle, uint64_t* out) {
+    return guarded(handle, [&](Engine& e) { *out = e.feat_dim; });
+}
+
+trw_status trw_get_latest_timestamp(void* handle, int64_t* out) {
+    return guarded(handle, [&](Engine& e) { *out = e.latest_ts; });
+}
+
+trw_status trw_clear(void* handle) {
+    return guarded(handle, [&](Engine& e) {
+        e.sync();
+        e.clear();
+    });
+}
+
+trw_status trw_get_array(void* handle, int32_t id, void* dst, uint64_t cap, uint64_t* len,
+                         uint32_t* elem_size) {
+    return guarded(handle, [&](Engine& e) {
+        hipStream_t s = e.stream;
+        const bool w = e.weights_ready;
+        const bool dir = e.cfg.is_directed != 0;
+        size_t n = 0;
+        uint32_t es = 8;
+        // resolve (pointer, count, source width)
+        const void* p = nullptr;
+        int kind = 0;  // 0: u32->u64, 1: i32, 2: i64, 3: f64, 4: f32, 5: u8->i32
+        switch (id) {
+            case TRW_ARR_SOURCES: p = e.src.p; n = e.E; kind = 1; es = 4; break;
+            case TRW_ARR_TARGETS: p = e.dst.p; n = e.E; kind = 1; es = 4; break;
+            case TRW_ARR_TIMESTAMPS: p = e.ts.p; n = e.E; kind = 2; break;
+            case TRW_ARR_TIMESTAMP_GROUP_OFFSETS: p = e.tsg_off.p; n = e.T ? e.T + 1 : 0; break;
+            case TRW_ARR_UNIQUE_TIMESTAMPS: p = e.uniq_ts.p; n = e.T; kind = 2; break;
+            case TRW_ARR_ACTIVE_NODE_IDS: p = e.active.p; n = e.active.n; kind = 5; es = 4; break;
+            case TRW_ARR_NODE_GROUP_OUTBOUND_OFFSETS: p = e.out.off.p; n = e.out.off.n; break;
+            case TRW_ARR_NODE_GROUP_INBOUND_OFFSETS: p = e.in.off.p; n = dir ? e.in.off.n : 0; break;
+            case TRW_ARR_NODE_TS_SORTED_OUTBOUND_INDICES: p = e.out.idx.p; n = e.out.idx.n; break;
+            case TRW_ARR_NODE_TS_SORTED_INBOUND_INDICES: p = e.in.idx.p; n = dir ? e.in.idx.n : 0; break;
+            case TRW_ARR_COUNT_TS_GROUP_PER_NODE_OUTBOUND: p = e.out.cnt.p; n = e.out.cnt.n; break;
+            case TRW_ARR_COUNT_TS_GROUP_PER_NODE_INBOUND: p = e.in.cnt.p; n = dir ? e.in.cnt.n : 0; break;
+            case TRW_ARR_NODE_TS_GROUP_OUTBOUND_OFFSETS: p = e.out.grp.p; n = e.out.n_groups; break;
+            case TRW_ARR_NODE_TS_GROUP_INBOUND_OFFSETS: p = e.in.grp.p; n = dir ? e.in.n_groups : 0; break;
+            case TRW_ARR_FORWARD_CUMULATIVE_WEIGHTS: p = e.fwd_cum.p; n = w ? e.T : 0; kind = 3; break;
+            case TRW_ARR_BACKWARD_CUMULATIVE_WEIGHTS: p = e.bwd_cum.p; n = w ? e.T : 0; kind = 3; break;
+            case TRW_ARR_OUTBOUND_FORWARD_CUMULATIVE_WEIGHTS: p = e.out.w_fwd.p; n = w ? e.out.n_groups : 0; kind = 3; break;
+            case TRW_ARR_OUTBOUND_BACKWARD_CUMULATIVE_WEIGHTS: p = e.out.w_bwd.p; n = w ? e.out.n_groups : 0; kind = 3; break;
+            case TRW_ARR_INBOUND_BACKWARD_CUMULATIVE_WEIGHTS: p = e.in.w_bwd.p; n = (w && dir) ? e.in.n_groups : 0; kind = 3; break;
+            case TRW_ARR_NODE_ADJ_OFFSETS: p = e.adj_off.p; n = e.adj_ready ? e.adj_off.n : 0; break;
+            case TRW_ARR_NODE_ADJ_NEIGHBORS: p = e.adj_nbr.p; n = e.adj_ready ? e.adj_nbr.n : 0; kind = 1; es = 4; break;
+            case TRW_ARR_EDGE_FEATURES: p = e.feat.p; n = e.E * e.feat_dim; kind = 4; es = 4; break;
+            default: throw trw::InvalidArgument("unknown array id");
+        }
+        *len = n;
+        if (elem_size) *elem_size = es;
+        if (!dst || n == 0) return;
+        if (cap < n) throw trw::InvalidArgument("output capacity too small");
+        switch (kind) {
+            case 0: widen_from_device<uint64_t>(dst, static_cast<const uint32_t*>(p), n, s); break;
+            case 1: widen_from_device<int32_t>(dst, static_cast<const int32_t*>(p), n, s); break;
+            case 2: widen_from_device<int64_t>(dst, static_cast<const int64_t*>(p), n, s); break;
+            case 3: widen_from_device<double>(dst, static_cast<const double*>(p), n, s); break;
+            case 4: widen_from_device<float>(dst, static_cast<const float*>(p), n, s); break;
+            case 5: widen_from_device<int32_t>(dst, static_cast<const uint8_t*>(p), n, s); break;
+        }
+    });
+}
+
+trw_status trw_get_timings(void* handle, trw_timings* out) {
+    return guarded(handle, [&](Engine& e) { *out = e.timings; });
+}
+
+trw_status trw_get_stream(void* handle, void** out_stream) {
+    return guarded(handle, [&](Engine& e) { *out_stream = e.stream; });
+}
+
+trw_status trw_get_walk_stats(void* handle, trw_walk_stats* out) {
+    return guarded(handle, [&](Engine& e) { trw::walk_stats(e, out); });
+}
+
+}  // extern "C"

@@ -1,0 +1,58 @@
+// primitives.h -- device-wide scan and stable radix sort for the index build.
+//
+// Hand-written for CDNA4 (wave64): no rocPRIM / hipCUB.  The radix sort is a
+// classic LSD sort with three launches per 8-bit digit pass (tile histogram,
+// digit-major scan of the histograms, stable scatter).  Stable ranking inside
+// a tile uses wave-level multisplit: eight 64-lane ballots give every lane the
+// mask of lanes holding the same digit, so the in-row rank is a popcount and a
+// single leader lane per digit bumps the wave's LDS counter.  Waves own
+// consecutive rows of the tile, so the scatter keeps input order among equal
+// digits -- which is what makes the edge-store order "stable by (timestamp,
+// insertion position)" and the node index "stable by (node, position)".
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace trw {
+
+void check_hip(hipError_t e, const char* what);
+
+// ---- scan ------------------------------------------------------------------
+// Exclusive scan of n values given by an input functor; writes n + 1 outputs,
+// out[n] = total.  `scratch` must hold scan_scratch_elems(n) elements of T.
+size_t scan_scratch_elems(size_t n);
+
+// Exclusive scan of a plain array: out[0..n] (out may alias in only if
+// out != in is not required: in-place is supported).
+void exclusive_scan_u32(const uint32_t* in, uint32_t* out, size_t n, uint32_t* scratch,
+                        hipStream_t s);
+void exclusive_scan_u64(const uint64_t* in, uint64_t* out, size_t n, uint64_t* scratch,
+                        hipStream_t s);
+// Inclusive scan of doubles in place (out[i] = in[0] + ... + in[i]).
+void inclusive_scan_f64(double* data, size_t n, double* scratch, hipStream_t s);
+
+// ---- radix sort --------------------------------------------------------------
+// Stable sort of (key, value) pairs by key bits [begin_bit, end_bit).  Values
+// may be null (keys only).  Buffers are ping-ponged; the function returns 0 if
+// the sorted result ended in (keys0, vals0) and 1 if in (keys1, vals1).
+// `hist` must hold radix_hist_elems(n) uint32 and `hist_scratch`
+// scan_scratch_elems(radix_hist_elems(n)) uint32.
+size_t radix_hist_elems(size_t n);
+int radix_sort_u64(uint64_t* keys0, uint32_t* vals0, uint64_t* keys1, uint32_t* vals1, size_t n,
+                   int begin_bit, int end_bit, uint32_t* hist, uint32_t* hist_scratch,
+                   hipStream_t s);
+int radix_sort_u32(uint32_t* keys0, uint32_t* vals0, uint32_t* keys1, uint32_t* vals1, size_t n,
+                   int begin_bit, int end_bit, uint32_t* hist, uint32_t* hist_scratch,
+                   hipStream_t s);
+
+// ---- reductions ---------------------------------------------------------------
+// min and max of int64 values -> out[0] = min, out[1] = max (device memory).
+void minmax_i64(const int64_t* v, size_t n, int64_t* out, hipStream_t s);
+// max of two int32 arrays -> *out (device memory); -1 when n == 0.
+void max_i32_pair(const int32_t* a, const int32_t* b, size_t n, int32_t* out, hipStream_t s);
+// sum of doubles -> *out (device memory).
+void sum_f64(const double* v, size_t n, double* out, hipStream_t s);
+
+}  // namespace trw

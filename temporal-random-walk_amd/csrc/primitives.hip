@@ -1,0 +1,435 @@
+// primitives.hip -- device-wide scan, stable LSD radix sort and reductions.
+// See primitives.h for the design notes.
+#include "primitives.h"
+
+#include <stdexcept>
+#include <string>
+
+namespace trw {
+
+void check_hip(hipError_t e, const char* what) {
+    if (e != hipSuccess) {
+        throw std::runtime_error(std::string("HIP error in ") + what + ": " +
+                                 hipGetErrorString(e));
+    }
+}
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kWaves = kBlock / 64;
+
+// ---------------------------------------------------------------------------
+// block-level helpers (256 threads = 4 wave64)
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ T wave_inclusive_scan(T x, int lane) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const T y = __shfl_up(x, off, 64);
+        if (lane >= off) x += y;
+    }
+    return x;
+}
+
+// Exclusive block scan of one value per thread; *total receives the block sum.
+template <typename T>
+__device__ __forceinline__ T block_exclusive_scan(T v, T* total, T* s_wave) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const T inc = wave_inclusive_scan(v, lane);
+    if (lane == 63) s_wave[wave] = inc;
+    __syncthreads();
+    T wp = T(0), tot = T(0);
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+        const T sw = s_wave[w];
+        if (w < wave) wp += sw;
+        tot += sw;
+    }
+    __syncthreads();
+    *total = tot;
+    return wp + inc - v;
+}
+
+template <typename T>
+__device__ __forceinline__ T block_sum(T v, T* s_wave) {
+    T tot;
+    (void)block_exclusive_scan(v, &tot, s_wave);
+    return tot;
+}
+
+// ---------------------------------------------------------------------------
+// scan: tile = 256 threads x 16 consecutive items per thread
+// ---------------------------------------------------------------------------
+constexpr int kScanItems = 16;
+constexpr size_t kScanTile = static_cast<size_t>(kBlock) * kScanItems;
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void scan_reduce_kernel(const T* __restrict__ in, size_t n,
+                                                             T* __restrict__ sums) {
+    __shared__ T s_wave[kWaves];
+    const size_t base = blockIdx.x * kScanTile + static_cast<size_t>(threadIdx.x) * kScanItems;
+    T acc = T(0);
+#pragma unroll
+    for (int j = 0; j < kScanItems; ++j) {
+        const size_t i = base + j;
+        if (i < n) acc += in[i];
+    }
+    const T tot = block_sum(acc, s_wave);
+    if (threadIdx.x == 0) sums[blockIdx.x] = tot;
+}
+
+// Single block: exclusive scan of sums[0..nb) in place; sums[nb] = total.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void scan_sums_kernel(T* __restrict__ sums, size_t nb) {
+    __shared__ T s_wave[kWaves];
+    T carry = T(0);
+    for (size_t chunk = 0; chunk < nb; chunk += kScanTile) {
+        const size_t base = chunk + static_cast<size_t>(threadIdx.x) * kScanItems;
+        T v[kScanItems];
+        T acc = T(0);
+#pragma unroll
+        for (int j = 0; j < kScanItems; ++j) {
+            const size_t i = base + j;
+            v[j] = i < nb ? sums[i] : T(0);
+            acc += v[j];
+        }
+        T tot;
+        T run = carry + block_exclusive_scan(acc, &tot, s_wave);
+#pragma unroll
+        for (int j = 0; j < kScanItems; ++j) {
+            const size_t i = base + j;
+            if (i < nb) sums[i] = run;
+            run += v[j];
+        }
+        carry += tot;
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) sums[nb] = carry;
+}
+
+template <typename T, bool Inclusive>
+__global__ __launch_bounds__(kBlock) void scan_apply_kernel(const T* in, T* out, size_t n,
+                                                            const T* __restrict__ sums) {
+    __shared__ T s_wave[kWaves];
+    const size_t base = blockIdx.x * kScanTile + static_cast<size_t>(threadIdx.x) * kScanItems;
+    T v[kScanItems];
+    T acc = T(0);
+#pragma unroll
+    for (int j = 0; j < kScanItems; ++j) {
+        const size_t i = base + j;
+        v[j] = i < n ? in[i] : T(0);
+        acc += v[j];
+    }
+    T tot;
+    T run = sums[blockIdx.x] + block_exclusive_scan(acc, &tot, s_wave);
+#pragma unroll
+    for (int j = 0; j < kScanItems; ++j) {
+        const size_t i = base + j;
+        if (Inclusive) run += v[j];
+        if (i < n) out[i] = run;
+        if (!Inclusive) run += v[j];
+    }
+    if (!Inclusive && blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) out[n] = sums[gridDim.x];
+}
+
+template <typename T, bool Inclusive>
+void scan_impl(const T* in, T* out, size_t n, T* scratch, hipStream_t s) {
+    if (n == 0) {
+        if (!Inclusive) check_hip(hipMemsetAsync(out, 0, sizeof(T), s), "scan memset");
+        return;
+    }
+    const size_t nb = (n + kScanTile - 1) / kScanTile;
+    hipLaunchKernelGGL((scan_reduce_kernel<T>), dim3(nb), dim3(kBlock), 0, s, in, n, scratch);
+    hipLaunchKernelGGL((scan_sums_kernel<T>), dim3(1), dim3(kBlock), 0, s, scratch, nb);
+    hipLaunchKernelGGL((scan_apply_kernel<T, Inclusive>), dim3(nb), dim3(kBlock), 0, s, in, out, n,
+                       scratch);
+    check_hip(hipGetLastError(), "scan launch");
+}
+
+// ---------------------------------------------------------------------------
+// radix sort: 8-bit digits, tile = 4 waves x 8 rows x 64 keys = 2048 keys
+// ---------------------------------------------------------------------------
+constexpr int kRadixBits = 8;
+constexpr int kRadix = 1 << kRadixBits;
+constexpr int kRows = 8;
+constexpr size_t kSortTile = static_cast<size_t>(kBlock) * kRows;
+
+static_assert(kRadix == kBlock, "one thread per digit in the tile epilogue");
+
+__device__ __forceinline__ uint64_t lanes_below(int lane) {
+    return lane == 0 ? 0ull : (~0ull >> (64 - lane));
+}
+
+// Mask of the valid lanes of this wave whose digit equals mine.
+__device__ __forceinline__ uint64_t match_digit(uint32_t d, bool valid) {
+    uint64_t m = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < kRadixBits; ++b) {
+        const bool bit = (d >> b) & 1u;
+        const uint64_t vote = __ballot(bit);
+        m &= bit ? vote : ~vote;
+    }
+    return m;
+}
+
+template <typename K>
+__global__ __launch_bounds__(kBlock) void radix_upsweep_kernel(const K* __restrict__ keys,
+                                                               size_t n, int bit,
+                                                               uint32_t* __restrict__ hist,
+                                                               size_t nb) {
+    __shared__ uint32_t s_cnt[kWaves][kRadix];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int i = threadIdx.x; i < kWaves * kRadix; i += kBlock) (&s_cnt[0][0])[i] = 0;
+    __syncthreads();
+    const size_t wave_base = blockIdx.x * kSortTile + static_cast<size_t>(wave) * kRows * 64;
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+        const size_t i = wave_base + static_cast<size_t>(r) * 64 + lane;
+        const bool valid = i < n;
+        const uint32_t d = valid ? static_cast<uint32_t>((keys[i] >> bit) & (kRadix - 1)) : 0u;
+        const uint64_t m = match_digit(d, valid);
+        if (valid && (m & lanes_below(lane)) == 0) s_cnt[wave][d] += __popcll(m);
+    }
+    __syncthreads();
+    const int d = threadIdx.x;
+    uint32_t tot = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) tot += s_cnt[w][d];
+    hist[static_cast<size_t>(d) * nb + blockIdx.x] = tot;
+}
+
+template <typename K>
+__global__ __launch_bounds__(kBlock) void radix_scatter_kernel(
+    const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, K* __restrict__ keys_out,
+    uint32_t* __restrict__ vals_out, size_t n, int bit, const uint32_t* __restrict__ offsets,
+    size_t nb) {
+    __shared__ uint32_t s_cnt[kWaves][kRadix];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int i = threadIdx.x; i < kWaves * kRadix; i += kBlock) (&s_cnt[0][0])[i] = 0;
+    __syncthreads();
+    const size_t wave_base = blockIdx.x * kSortTile + static_cast<size_t>(wave) * kRows * 64;
+    K key[kRows];
+    uint32_t val[kRows];
+    uint32_t dig[kRows];
+    uint32_t rank[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+        const size_t i = wave_base + static_cast<size_t>(r) * 64 + lane;
+        const bool valid = i < n;
+        key[r] = valid ? keys_in[i] : K(0);
+        val[r] = (valid && vals_in) ? vals_in[i] : 0u;
+        const uint32_t d = static_cast<uint32_t>((key[r] >> bit) & (kRadix - 1));
+        dig[r] = d;
+        const uint64_t m = match_digit(d, valid);
+        const uint32_t before = __popcll(m & lanes_below(lane));
+        const uint32_t prior = s_cnt[wave][d];
+        rank[r] = prior + before;
+        if (valid && before == 0) s_cnt[wave][d] = prior + __popcll(m);
+    }
+    __syncthreads();
+    {
+        const int d = threadIdx.x;
+        uint32_t run = offsets[static_cast<size_t>(d) * nb + blockIdx.x];
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const uint32_t c = s_cnt[w][d];
+            s_cnt[w][d] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+        const size_t i = wave_base + static_cast<size_t>(r) * 64 + lane;
+        if (i < n) {
+            const uint32_t pos = s_cnt[wave][dig[r]] + rank[r];
+            keys_out[pos] = key[r];
+            if (vals_out) vals_out[pos] = val[r];
+        }
+    }
+}
+
+template <typename K>
+int radix_sort_impl(K* keys0, uint32_t* vals0, K* keys1, uint32_t* vals1, size_t n,
+                    int begin_bit, int end_bit, uint32_t* hist, uint32_t* hist_scratch,
+                    hipStream_t s) {
+    if (n <= 1 || end_bit <= begin_bit) return 0;
+    const size_t nb = (n + kSortTile - 1) / kSortTile;
+    int cur = 0;
+    K* kb[2] = {keys0, keys1};
+    uint32_t* vb[2] = {vals0, vals1};
+    for (int bit = begin_bit; bit < end_bit; bit += kRadixBits) {
+        hipLaunchKernelGGL((radix_upsweep_kernel<K>), dim3(nb), dim3(kBlock), 0, s, kb[cur], n,
+                           bit, hist, nb);
+        scan_impl<uint32_t, false>(hist, hist, nb * kRadix, hist_scratch, s);
+        hipLaunchKernelGGL((radix_scatter_kernel<K>), dim3(nb), dim3(kBlock), 0, s, kb[cur],
+                           vb[cur], kb[cur ^ 1], vb[cur ^ 1], n, bit, hist, nb);
+        check_hip(hipGetLastError(), "radix sort launch");
+        cur ^= 1;
+    }
+    return cur;
+}
+
+// ---------------------------------------------------------------------------
+// reductions (grid-stride, per-block partials, then one block)
+// ---------------------------------------------------------------------------
+constexpr int kReduceBlocks = 1024;
+
+__global__ __launch_bounds__(kBlock) void minmax_partial_kernel(const int64_t* __restrict__ v,
+                                                                size_t n, int64_t* part) {
+    __shared__ int64_t s_min[kBlock], s_max[kBlock];
+    int64_t mn = INT64_MAX, mx = INT64_MIN;
+    for (size_t i = blockIdx.x * static_cast<size_t>(kBlock) + threadIdx.x; i < n;
+         i += static_cast<size_t>(gridDim.x) * kBlock) {
+        const int64_t x = v[i];
+        mn = x < mn ? x : mn;
+        mx = x > mx ? x : mx;
+    }
+    s_min[threadIdx.x] = mn;
+    s_max[threadIdx.x] = mx;
+    __syncthreads();
+    for (int st = kBlock / 2; st > 0; st >>= 1) {
+        if (threadIdx.x < st) {
+            const int64_t a = s_min[threadIdx.x + st], b = s_max[threadIdx.x + st];
+            if (a < s_min[threadIdx.x]) s_min[threadIdx.x] = a;
+            if (b > s_max[threadIdx.x]) s_max[threadIdx.x] = b;
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        part[2 * blockIdx.x] = s_min[0];
+        part[2 * blockIdx.x + 1] = s_max[0];
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void minmax_final_kernel(const int64_t* part, int np,
+                                                              int64_t* out) {
+    __shared__ int64_t s_min[kBlock], s_max[kBlock];
+    int64_t mn = INT64_MAX, mx = INT64_MIN;
+    for (int i = threadIdx.x; i < np; i += kBlock) {
+        mn = part[2 * i] < mn ? part[2 * i] : mn;
+        mx = part[2 * i + 1] > mx ? part[2 * i + 1] : mx;
+    }
+    s_min[threadIdx.x] = mn;
+    s_max[threadIdx.x] = mx;
+    __syncthreads();
+    for (int st = kBlock / 2; st > 0; st >>= 1) {
+        if (threadIdx.x < st) {
+            const int64_t a = s_min[threadIdx.x + st], b = s_max[threadIdx.x + st];
+            if (a < s_min[threadIdx.x]) s_min[threadIdx.x] = a;
+            if (b > s_max[threadIdx.x]) s_max[threadIdx.x] = b;
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        out[0] = s_min[0];
+        out[1] = s_max[0];
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void max_pair_kernel(const int32_t* __restrict__ a,
+                                                          const int32_t* __restrict__ b, size_t n,
+                                                          int32_t* out) {
+    __shared__ int32_t s[kBlock];
+    int32_t mx = -1;
+    for (size_t i = blockIdx.x * static_cast<size_t>(kBlock) + threadIdx.x; i < n;
+         i += static_cast<size_t>(gridDim.x) * kBlock) {
+        mx = max(mx, max(a[i], b[i]));
+    }
+    s[threadIdx.x] = mx;
+    __syncthreads();
+    for (int st = kBlock / 2; st > 0; st >>= 1) {
+        if (threadIdx.x < st) s[threadIdx.x] = max(s[threadIdx.x], s[threadIdx.x + st]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) atomicMax(out, s[0]);
+}
+
+__global__ void set_i32_kernel(int32_t* p, int32_t v) { *p = v; }
+
+__global__ __launch_bounds__(kBlock) void sum_partial_kernel(const double* __restrict__ v,
+                                                             size_t n, double* part) {
+    __shared__ double s_wave[kWaves];
+    double acc = 0.0;
+    for (size_t i = blockIdx.x * static_cast<size_t>(kBlock) + threadIdx.x; i < n;
+         i += static_cast<size_t>(gridDim.x) * kBlock) {
+        acc += v[i];
+    }
+    const double tot = block_sum(acc, s_wave);
+    if (threadIdx.x == 0) part[blockIdx.x] = tot;
+}
+
+__global__ __launch_bounds__(kBlock) void sum_final_kernel(const double* part, int np,
+                                                           double* out) {
+    __shared__ double s_wave[kWaves];
+    double acc = 0.0;
+    for (int i = threadIdx.x; i < np; i += kBlock) acc += part[i];
+    const double tot = block_sum(acc, s_wave);
+    if (threadIdx.x == 0) out[0] = tot;
+}
+
+int reduce_blocks(size_t n) {
+    const size_t b = (n + kBlock - 1) / kBlock;
+    return static_cast<int>(b < kReduceBlocks ? (b ? b : 1) : kReduceBlocks);
+}
+
+}  // namespace
+
+size_t scan_scratch_elems(size_t n) { return (n + kScanTile - 1) / kScanTile + 1; }
+size_t radix_hist_elems(size_t n) { return ((n + kSortTile - 1) / kSortTile) * kRadix + 1; }
+
+void exclusive_scan_u32(const uint32_t* in, uint32_t* out, size_t n, uint32_t* scratch,
+                        hipStream_t s) {
+    scan_impl<uint32_t, false>(in, out, n, scratch, s);
+}
+void exclusive_scan_u64(const uint64_t* in, uint64_t* out, size_t n, uint64_t* scratch,
+                        hipStream_t s) {
+    scan_impl<uint64_t, false>(in, out, n, scratch, s);
+}
+void inclusive_scan_f64(double* data, size_t n, double* scratch, hipStream_t s) {
+    scan_impl<double, true>(data, data, n, scratch, s);
+}
+
+int radix_sort_u64(uint64_t* keys0, uint32_t* vals0, uint64_t* keys1, uint32_t* vals1, size_t n,
+                   int begin_bit, int end_bit, uint32_t* hist, uint32_t* hist_scratch,
+                   hipStream_t s) {
+    return radix_sort_impl<uint64_t>(keys0, vals0, keys1, vals1, n, begin_bit, end_bit, hist,
+                                     hist_scratch, s);
+}
+int radix_sort_u32(uint32_t* keys0, uint32_t* vals0, uint32_t* keys1, uint32_t* vals1, size_t n,
+                   int begin_bit, int end_bit, uint32_t* hist, uint32_t* hist_scratch,
+                   hipStream_t s) {
+    return radix_sort_impl<uint32_t>(keys0, vals0, keys1, vals1, n, begin_bit, end_bit, hist,
+                                     hist_scratch, s);
+}
+
+// Scratch for the reductions lives in a small per-call static device buffer
+// provided by the caller through `out` (2 * kReduceBlocks int64 / doubles
+// beyond out[0..1]).
+void minmax_i64(const int64_t* v, size_t n, int64_t* out, hipStream_t s) {
+    const int nb = reduce_blocks(n);
+    int64_t* part = out + 2;
+    hipLaunchKernelGGL(minmax_partial_kernel, dim3(nb), dim3(kBlock), 0, s, v, n, part);
+    hipLaunchKernelGGL(minmax_final_kernel, dim3(1), dim3(kBlock), 0, s, part, nb, out);
+    check_hip(hipGetLastError(), "minmax launch");
+}
+
+void max_i32_pair(const int32_t* a, const int32_t* b, size_t n, int32_t* out, hipStream_t s) {
+    hipLaunchKernelGGL(set_i32_kernel, dim3(1), dim3(1), 0, s, out, -1);
+    if (n) {
+        hipLaunchKernelGGL(max_pair_kernel, dim3(reduce_blocks(n)), dim3(kBlock), 0, s, a, b, n,
+                           out);
+    }
+    check_hip(hipGetLastError(), "max launch");
+}
+
+void sum_f64(const double* v, size_t n, double* out, hipStream_t s) {
+    const int nb = reduce_blocks(n);
+    double* part = out + 2;
+    hipLaunchKernelGGL(sum_partial_kernel, dim3(nb), dim3(kBlock), 0, s, v, n, part);
+    hipLaunchKernelGGL(sum_final_kernel, dim3(1), dim3(kBlock), 0, s, part, nb, out);
+    check_hip(hipGetLastError(), "sum launch");
+}
+
+}  // namespace trw

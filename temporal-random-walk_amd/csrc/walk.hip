@@ -1,0 +1,747 @@
+// walk.hip -- the walk sampler.
+//
+// Semantics restate the reference CPU walk loop
+// (core/temporal_random_walk_cpu.cuh:19-131) with its selectors
+// (graph/edge_selectors.cuh:66-443), pickers (random/pickers.cuh) and the
+// node2vec rejection sampler (graph/temporal_node2vec_helpers.cuh:127-199).
+// Each walk is one lane; the walk state (current node, time, previous node,
+// draws) lives in registers for the whole walk, so there is no per-step
+// scheduler and no host round trip between steps.
+//
+// Per hop the lane reads the node's group range, binary-searches the
+// node-timestamp group panel first_ts[] (one 8-byte load per probe instead of
+// the reference's three dependent loads ts[idx[grp[p]]]), applies the picker,
+// reads the group's edge range and the chosen edge.  The dominant cost is the
+// dependent-load latency of the search; hub panels stay resident in L2 /
+// Infinity Cache because every walk crossing the hub probes the same keys.
+#include <math.h>
+
+#include <algorithm>
+#include <random>
+
+#include "engine.h"
+#include "trw_device.h"
+
+namespace trw {
+namespace {
+
+constexpr int kB = 256;
+
+inline unsigned grid_for(size_t n) {
+    const size_t g = (n + kB - 1) / kB;
+    return static_cast<unsigned>(g ? g : 1);
+}
+
+struct DirView {
+    const uint32_t* cnt;
+    const uint32_t* grp;  // g + 1 entries (terminator)
+    const uint32_t* idx;
+    const int64_t* first_ts;
+    uint32_t idx_size;
+    const double* w;  // per-node cumulative weights of the sampled direction
+    uint64_t w_size;
+};
+
+struct WalkGraph {
+    const int32_t* src;
+    const int32_t* dst;
+    const int64_t* ts;
+    uint32_t E;
+    const uint32_t* tsg_off;
+    uint32_t T;
+    const double* gw;  // global cumulative weights of the sampled direction
+    uint64_t gw_size;
+    const uint8_t* active;
+    int32_t active_size;
+    DirView d;
+    const uint32_t* adj_off;
+    const int32_t* adj_nbr;
+    uint32_t adj_off_size;
+    int tn2v;
+    double inv_p, inv_q;
+};
+
+struct WalkArgs {
+    int L;
+    int walk_bias;
+    int start_bias;
+    int pad;
+    const int32_t* starts;   // nullptr => all unconstrained
+    const int64_t* cutoffs;  // nullptr => none
+    uint64_t n;
+    DrawSource ds;
+    int32_t* nodes;
+    int64_t* ts;
+    uint64_t* lens;
+    int64_t* eids;
+};
+
+struct Sel {
+    int32_t u, v;
+    int64_t t;
+    int64_t e;
+};
+
+__device__ __forceinline__ Sel no_edge() { return Sel{-1, -1, -1, -1}; }
+
+__device__ __forceinline__ Sel edge_of(const WalkGraph& g, uint32_t e) {
+    return Sel{g.src[e], g.dst[e], g.ts[e], static_cast<int64_t>(e)};
+}
+
+// Unconstrained start (edge_selectors.cuh:177-275 with timestamp == -1).
+template <bool Fwd>
+__device__ Sel start_edge(const WalkGraph& g, int picker, double rg, double re) {
+    if (g.E == 0 || g.T == 0) return no_edge();
+    long group;
+    if (is_index_picker(picker)) {
+        const int idx = pick_index(picker, 0, static_cast<int>(g.T), !Fwd, rg);
+        if (idx == -1 || static_cast<uint32_t>(idx) >= g.T) return no_edge();
+        group = idx;
+    } else {
+        if (picker != kExponentialWeight && picker != kTemporalNode2Vec) return no_edge();
+        group = pick_exponential_weights(g.gw, g.gw_size, 0, g.T, rg, 0);
+        // an index past the last group reads as an empty range in the
+        // reference (get_timestamp_group_range_host, edge_selectors.cuh:38-43)
+        if (group == -1 || static_cast<uint32_t>(group) >= g.T) return no_edge();
+    }
+    const uint32_t from = g.tsg_off[group], to = g.tsg_off[group + 1];
+    if (from == to) return no_edge();
+    const uint32_t e = from + static_cast<uint32_t>(static_cast<int>(re * static_cast<int>(to - from)));
+    return edge_of(g, e);
+}
+
+__device__ __forceinline__ bool adjacent(const WalkGraph& g, int prev, int cand) {
+    if (!g.tn2v || g.adj_off == nullptr) return false;
+    if (prev < 0 || static_cast<uint32_t>(prev) + 1 >= g.adj_off_size) return false;
+    uint32_t lo = g.adj_off[prev];
+    const uint32_t end = g.adj_off[prev + 1];
+    uint32_t hi = end;
+    if (lo >= hi) return false;
+    while (lo < hi) {
+        const uint32_t mid = lo + ((hi - lo) >> 1);
+        if (g.adj_nbr[mid] < cand) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo < end && g.adj_nbr[lo] == cand;
+}
+
+// graph/temporal_node2vec_helpers.cuh:127-199; vb/ve/gb/ge are global group
+// positions.  Returns an edge id or -1.
+template <bool Fwd, bool Dir>
+__device__ long tn2v_pick(const WalkGraph& g, int node, int prev, uint32_t vb, uint32_t ve,
+                          uint32_t gb, uint32_t ge, double rg, double re) {
+    if (vb >= ve || prev == -1) return -1;
+    double bmax = 1.0;
+    if (g.inv_p > bmax) bmax = g.inv_p;
+    if (g.inv_q > bmax) bmax = g.inv_q;
+    const double inv_bmax = 1.0 / bmax;
+    long last = -1;
+    for (int retry = 0; retry < kNode2VecMaxRetries; ++retry) {
+        const double gr = derive_uniform(rg, re, retry * 3 + 0);
+        const double er = derive_uniform(rg, re, retry * 3 + 1);
+        const double ar = derive_uniform(rg, re, retry * 3 + 2);
+        const int gp = pick_exponential_weights(g.d.w, g.d.w_size, vb, ve, gr, gb);
+        if (gp == -1) return -1;
+        // a pick one past the node's last group is an empty range in the
+        // reference (get_node_group_edge_end, walk_step_helpers.cuh:19-38)
+        if (static_cast<uint32_t>(gp) >= ge) continue;
+        const uint32_t es = g.d.grp[gp], ee = g.d.grp[gp + 1];
+        if (es >= ee) continue;
+        const uint64_t local = static_cast<uint64_t>(er * static_cast<double>(ee - es));
+        const uint32_t pick = es + static_cast<uint32_t>(local < ee - es ? local : ee - es - 1);
+        const uint32_t eid = g.d.idx[pick];
+        int cand;
+        if (Dir) cand = Fwd ? g.dst[eid] : g.src[eid];
+        else cand = g.src[eid] == node ? g.dst[eid] : g.src[eid];
+        const double beta = (cand == prev) ? g.inv_p : (adjacent(g, prev, cand) ? 1.0 : g.inv_q);
+        last = eid;
+        if (ar < beta * inv_bmax) return eid;
+    }
+    return last;
+}
+
+// Per-hop selector (edge_selectors.cuh:277-443).
+template <bool Fwd, bool Dir>
+__device__ Sel node_edge_at(const WalkGraph& g, int picker, int node, int64_t t, int64_t cutoff,
+                            int prev, double rg, double re) {
+    if (!(node >= 0 && node < g.active_size && g.active[node] == 1)) return no_edge();
+    const uint32_t gb = g.d.cnt[node], ge = g.d.cnt[node + 1];
+    if (gb == ge) return no_edge();
+    const int G = static_cast<int>(ge - gb);
+    const int64_t* fts = g.d.first_ts + gb;
+    // filter_valid_groups_by_timestamp_slice (edge_selectors.cuh:66-120)
+    int vb = 0, ve = G;
+    if (!(t == -1 && cutoff == kNoCutoff)) {
+        if (t != -1) {
+            int lo = 0, hi = G;
+            if (Fwd) {
+                while (lo < hi) {
+                    const int mid = lo + ((hi - lo) >> 1);
+                    if (t < fts[mid]) hi = mid;
+                    else lo = mid + 1;
+                }
+                vb = lo;
+            } else {
+                while (lo < hi) {
+                    const int mid = lo + ((hi - lo) >> 1);
+                    if (fts[mid] < t) lo = mid + 1;
+                    else hi = mid;
+                }
+                ve = lo;
+            }
+        }
+        if (cutoff != kNoCutoff) {
+            int lo = vb, hi = ve;
+            while (lo < hi) {
+                const int mid = lo + ((hi - lo) >> 1);
+                if (fts[mid] < cutoff) lo = mid + 1;
+                else hi = mid;
+            }
+            ve = lo;
+        }
+    }
+    if (vb >= ve) return no_edge();
+    uint32_t gpos;
+    if (picker == kTemporalNode2Vec) {
+        if (prev == -1) {
+            const int p = pick_exponential_weights(g.d.w, g.d.w_size, gb + vb, gb + ve, rg, gb);
+            if (p == -1) return no_edge();
+            gpos = static_cast<uint32_t>(p);
+        } else {
+            const long e = tn2v_pick<Fwd, Dir>(g, node, prev, gb + vb, gb + ve, gb, ge, rg, re);
+            if (e == -1) return no_edge();
+            return edge_of(g, static_cast<uint32_t>(e));
+        }
+    } else if (is_index_picker(picker)) {
+        const int avail = ve - vb;
+        const int index = pick_index(picker, 0, avail, !Fwd, rg);
+        if (index == -1 || index >= avail) return no_edge();
+        gpos = gb + static_cast<uint32_t>(vb + index);
+    } else {
+        if (picker != kExponentialWeight) return no_edge();
+        const int p = pick_exponential_weights(g.d.w, g.d.w_size, gb + vb, gb + ve, rg, gb);
+        if (p == -1) return no_edge();
+        gpos = static_cast<uint32_t>(p);
+    }
+    // A weight pick one past the node's last group reads, in the reference, the
+    // next node's first group start for both ends: an empty range.
+    if (gpos >= ge) return no_edge();
+    const uint32_t es = g.d.grp[gpos], ee = g.d.grp[gpos + 1];
+    if (es >= ee || es >= g.d.idx_size || ee > g.d.idx_size) return no_edge();
+    const uint32_t e =
+        g.d.idx[es + static_cast<uint32_t>(static_cast<int>(re * static_cast<int>(ee - es)))];
+    return edge_of(g, e);
+}
+
+template <bool Fwd, bool Dir>
+__global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
+    const uint64_t w = blockIdx.x * static_cast<uint64_t>(kB) + threadIdx.x;
+    if (w >= a.n) return;
+    const int L = a.L;
+    if (L == 0) {
+        a.lens[w] = 0;
+        return;
+    }
+    int32_t* wn = a.nodes + w * L;
+    int64_t* wt = a.ts + w * L;
+    int64_t* we = a.eids + w * (L - 1);
+    const int start = a.starts ? a.starts[w] : -1;
+    const int64_t cutoff = a.cutoffs ? a.cutoffs[w] : kNoCutoff;
+
+    const double r0 = draw_slot0(a.ds, w);
+    const DrawPair r12 = draw_pair(a.ds, w, 1);
+    Sel se = (start == -1)
+                 ? start_edge<Fwd>(g, a.start_bias, r0, r12.a)
+                 : node_edge_at<Fwd, Dir>(g, a.start_bias, start, -1, cutoff, -1, r0, r12.a);
+    int len = 0;
+    if (se.v != -1) {
+        int cur, prev = -1;
+        if (Dir) {
+            wn[0] = Fwd ? se.u : se.v;
+            cur = Fwd ? se.v : se.u;
+        } else {
+            const int picked = start != -1 ? start : (r12.b >= 0.5 ? se.u : se.v);
+            wn[0] = picked;
+            cur = picked == se.u ? se.v : se.u;
+        }
+        wt[0] = Fwd ? INT64_MIN : INT64_MAX;
+        len = 1;
+        int64_t cur_t = se.t;
+        int64_t cur_e = se.e;
+        int walk_len = 1;
+        while (walk_len < L && cur != a.pad) {
+            wn[len] = cur;
+            wt[len] = cur_t;
+            if (cur_e != -1) we[len - 1] = cur_e;
+            ++len;
+            // The reference draws and selects once more after the last slot is
+            // written; that selection cannot change the output, so it is skipped.
+            if (walk_len == L - 1) break;
+            const DrawPair r = draw_pair(a.ds, w, static_cast<uint32_t>(walk_len) + 1);
+            const Sel ne = node_edge_at<Fwd, Dir>(g, a.walk_bias, cur, cur_t, cutoff, prev, r.a, r.b);
+            if (ne.t == -1) break;
+            prev = cur;
+            if (Dir) cur = Fwd ? ne.v : ne.u;
+            else cur = (cur == ne.u) ? ne.v : ne.u;
+            cur_t = ne.t;
+            cur_e = ne.e;
+            ++walk_len;
+        }
+    }
+    for (int k = len; k < L; ++k) {
+        wn[k] = a.pad;
+        wt[k] = -1;
+    }
+    for (int k = len > 0 ? len - 1 : 0; k < L - 1; ++k) we[k] = -1;
+    a.lens[w] = static_cast<uint64_t>(len);
+    if (!Fwd && len > 1) {  // data/walk_set/walk_set_view.cuh:50-80
+        for (int i = 0; i < len / 2; ++i) {
+            const int j = len - 1 - i;
+            const int32_t tn = wn[i];
+            wn[i] = wn[j];
+            wn[j] = tn;
+            const int64_t tt = wt[i];
+            wt[i] = wt[j];
+            wt[j] = tt;
+        }
+        const int ec = len - 1;
+        for (int i = 0; i < ec / 2; ++i) {
+            const int j = ec - 1 - i;
+            const int64_t te = we[i];
+            we[i] = we[j];
+            we[j] = te;
+        }
+    }
+}
+
+// ---- start arrays ----------------------------------------------------------
+__global__ void flags_from_u8_kernel(const uint8_t* __restrict__ a, size_t n,
+                                     uint32_t* __restrict__ f) {
+    const size_t i = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (i < n) f[i] = a[i] ? 1u : 0u;
+}
+
+__global__ void compact_ids_kernel(const uint32_t* __restrict__ f, const uint32_t* __restrict__ scan,
+                                   size_t n, int32_t* __restrict__ out) {
+    const size_t i = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (i < n && f[i]) out[scan[i]] = static_cast<int32_t>(i);
+}
+
+__global__ void unique_flags_kernel(const uint32_t* __restrict__ k, size_t n,
+                                    uint32_t* __restrict__ f) {
+    const size_t i = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (i < n) f[i] = (i == 0 || k[i] != k[i - 1]) ? 1u : 0u;
+}
+
+__global__ void compact_keys_kernel(const uint32_t* __restrict__ k, const uint32_t* __restrict__ f,
+                                    const uint32_t* __restrict__ scan, size_t n,
+                                    int32_t* __restrict__ out) {
+    const size_t i = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (i < n && f[i]) out[scan[i]] = static_cast<int32_t>(k[i]);
+}
+
+template <typename T>
+__global__ void repeat_kernel(const T* __restrict__ in, uint64_t n_out, int times,
+                              T* __restrict__ out) {
+    const uint64_t i = blockIdx.x * static_cast<uint64_t>(kB) + threadIdx.x;
+    if (i < n_out) out[i] = in[i / times];
+}
+
+__global__ void random_keys_kernel(uint64_t n, uint32_t k0, uint32_t k1, uint32_t* __restrict__ keys,
+                                   uint32_t* __restrict__ vals) {
+    const uint64_t i = blockIdx.x * static_cast<uint64_t>(kB) + threadIdx.x;
+    if (i >= n) return;
+    const U4 o = philox4x32_10(U4{static_cast<uint32_t>(i), static_cast<uint32_t>(i >> 32),
+                                  0x5348u /* shuffle stream */, 0u},
+                               k0, k1);
+    keys[i] = o.x;
+    vals[i] = static_cast<uint32_t>(i);
+}
+
+template <typename T>
+__global__ void permute_kernel(const T* __restrict__ in, const uint32_t* __restrict__ perm,
+                               uint64_t n, T* __restrict__ out) {
+    const uint64_t i = blockIdx.x * static_cast<uint64_t>(kB) + threadIdx.x;
+    if (i < n) out[i] = in[perm[i]];
+}
+
+__global__ void u32_from_i32_kernel(const int32_t* __restrict__ a, uint64_t n,
+                                    uint32_t* __restrict__ out) {
+    const uint64_t i = blockIdx.x * static_cast<uint64_t>(kB) + threadIdx.x;
+    if (i < n) out[i] = static_cast<uint32_t>(a[i]);
+}
+
+// ---- outputs ----------------------------------------------------------------
+__global__ void gather_walk_features_kernel(const int64_t* __restrict__ eids, uint64_t slots,
+                                            uint32_t dim, const float* __restrict__ feat,
+                                            float* __restrict__ out) {
+    const uint64_t x = blockIdx.x * static_cast<uint64_t>(kB) + threadIdx.x;
+    if (x >= slots * dim) return;
+    const uint64_t slot = x / dim, c = x - slot * dim;
+    const int64_t e = eids[slot];
+    out[x] = e >= 0 ? feat[static_cast<uint64_t>(e) * dim + c] : 0.0f;
+}
+
+// Walk statistics and algorithmic bytes of the walk kernel (trw_get_walk_stats).
+__global__ void walk_stats_kernel(const int32_t* __restrict__ nodes,
+                                  const uint64_t* __restrict__ lens, uint64_t n, int L,
+                                  const uint32_t* __restrict__ cnt, int32_t active_size,
+                                  unsigned long long* acc) {
+    const uint64_t w = blockIdx.x * static_cast<uint64_t>(kB) + threadIdx.x;
+    unsigned long long bytes = 0, trans = 0, total = 0, nonempty = 0;
+    if (w < n && L > 0) {
+        const int len = static_cast<int>(lens[w]);
+        bytes = 40 + 12;
+        if (len >= 2) bytes += 20;
+        for (int k = 1; k + 1 < len; ++k) {
+            const int u = nodes[w * L + k];
+            uint32_t G = 0;
+            if (u >= 0 && u < active_size) G = cnt[u + 1] - cnt[u];
+            const int probes = G ? 32 - __clz(G) : 0;  // ceil(log2(G + 1))
+            bytes += 72 + 8 * probes;
+        }
+        bytes += 20ull * static_cast<unsigned long long>(L - (len > 0 ? len : 1));
+        trans = len > 0 ? len - 1 : 0;
+        total = len;
+        nonempty = len > 0;
+    }
+    // wave reduction then one atomic per wave
+    for (int off = 32; off > 0; off >>= 1) {
+        bytes += __shfl_down(bytes, off, 64);
+        trans += __shfl_down(trans, off, 64);
+        total += __shfl_down(total, off, 64);
+        nonempty += __shfl_down(nonempty, off, 64);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        atomicAdd(acc + 0, total);
+        atomicAdd(acc + 1, trans);
+        atomicAdd(acc + 2, nonempty);
+        atomicAdd(acc + 3, bytes);
+    }
+}
+
+}  // namespace
+
+void Engine::sample(const trw_sample_params& p) {
+    hipStream_t s = stream;
+    int64_t* hs = reinterpret_cast<int64_t*>(host_scalars);
+    const int L = p.max_walk_len;
+    if (L < 0) throw InvalidArgument("max_walk_len must be >= 0");
+    const int walk_bias = p.walk_bias;
+    int start_bias = p.initial_edge_bias < 0 ? walk_bias : p.initial_edge_bias;
+    if (walk_bias < 0 || walk_bias > kTestLast || start_bias > kTestLast)
+        throw InvalidArgument("Invalid picker type");
+    if (p.direction != 0 && p.direction != 1) throw InvalidArgument("Invalid walk direction");
+    // core/temporal_random_walk_cpu.cuh:168-171
+    if (start_bias == kTemporalNode2Vec) start_bias = kExponentialWeight;
+    const bool forward = p.direction == 0;
+    const bool shuffle = p.shuffle < 0 ? cfg.shuffle_walk_order != 0 : p.shuffle != 0;
+    uint64_t seed = cfg.global_seed;
+    if (seed == UINT64_MAX) {
+        std::random_device rd;
+        seed = (static_cast<uint64_t>(rd()) << 32) | rd();
+    }
+
+    check_hip(hipEventRecord(ev[4], s), "event");
+
+    // ---- start array (core/temporal_random_walk.cu:394-588)
+    uint64_t nw = 0;
+    bool have_starts = false, have_cutoffs = false;
+    if (p.num_walks_per_node < 0 && p.mode != TRW_START_TOTAL)
+        throw InvalidArgument("num_walks_per_node must be >= 0");
+    const int wpn = p.num_walks_per_node;
+    switch (p.mode) {
+        case TRW_START_TOTAL: {
+            if (p.num_walks_total < 0) throw InvalidArgument("num_walks_total must be >= 0");
+            nw = static_cast<uint64_t>(p.num_walks_total);
+            break;
+        }
+        case TRW_START_ALL_NODES:
+        case TRW_START_LAST_BATCH: {
+            size_t count = 0;
+            DBuf<int32_t> ids;
+            if (p.mode == TRW_START_ALL_NODES) {
+                const size_t v = active.n;
+                flags.ensure(v + 1);
+                scan.ensure(v + 1);
+                scan_scratch.ensure(scan_scratch_elems(v + 1));
+                if (v) {
+                    hipLaunchKernelGGL(flags_from_u8_kernel, dim3(grid_for(v)), dim3(kB), 0, s,
+                                       active.p, v, flags.p);
+                }
+                exclusive_scan_u32(flags.p, scan.p, v, scan_scratch.p, s);
+                check_hip(hipMemcpyAsync(hs, scan.p + v, 4, hipMemcpyDeviceToHost, s), "count");
+                sync();
+                uint32_t c;
+                std::memcpy(&c, hs, 4);
+                count = c;
+                ids.resize(count);
+                if (v) {
+                    hipLaunchKernelGGL(compact_ids_kernel, dim3(grid_for(v)), dim3(kB), 0, s,
+                                       flags.p, scan.p, v, ids.p);
+                }
+            } else {
+                // unique sources (directed) or unique endpoints (undirected) of the
+                // last batch, ascending (core/temporal_random_walk.cu:157-272)
+                const size_t m = cfg.is_directed ? last_n : 2 * last_n;
+                k32a.ensure(m);
+                k32b.ensure(m);
+                hist.ensure(radix_hist_elems(m));
+                hist_scratch.ensure(scan_scratch_elems(radix_hist_elems(m)));
+                flags.ensure(m + 1);
+                scan.ensure(m + 1);
+                scan_scratch.ensure(scan_scratch_elems(m + 1));
+                if (last_n) {
+                    hipLaunchKernelGGL(u32_from_i32_kernel, dim3(grid_for(last_n)), dim3(kB), 0, s,
+                                       last_src.p, last_n, k32a.p);
+                    if (!cfg.is_directed) {
+                        hipLaunchKernelGGL(u32_from_i32_kernel, dim3(grid_for(last_n)), dim3(kB),
+                                           0, s, last_dst.p, last_n, k32a.p + last_n);
+                    }
+                }
+                const int w = radix_sort_u32(k32a.p, nullptr, k32b.p, nullptr, m, 0, 32, hist.p,
+                                             hist_scratch.p, s);
+                uint32_t* keys = w ? k32b.p : k32a.p;
+                if (m) {
+                    hipLaunchKernelGGL(unique_flags_kernel, dim3(grid_for(m)), dim3(kB), 0, s,
+                                       keys, m, flags.p);
+                }
+                exclusive_scan_u32(flags.p, scan.p, m, scan_scratch.p, s);
+                check_hip(hipMemcpyAsync(hs, scan.p + m, 4, hipMemcpyDeviceToHost, s), "count");
+                sync();
+                uint32_t c;
+                std::memcpy(&c, hs, 4);
+                count = c;
+                ids.resize(count);
+                if (m) {
+                    hipLaunchKernelGGL(compact_keys_kernel, dim3(grid_for(m)), dim3(kB), 0, s,
+                                       keys, flags.p, scan.p, m, ids.p);
+                }
+            }
+            nw = static_cast<uint64_t>(count) * static_cast<uint64_t>(wpn);
+            starts.resize(nw);
+            if (nw) {
+                hipLaunchKernelGGL((repeat_kernel<int32_t>), dim3(grid_for(nw)), dim3(kB), 0, s,
+                                   ids.p, nw, wpn, starts.p);
+            }
+            sync();  // `ids` is released at scope exit
+            have_starts = true;
+            break;
+        }
+        case TRW_START_NODES: {
+            const size_t ns = p.num_seed_nodes;
+            if (ns && !p.seed_nodes) throw InvalidArgument("seed_nodes is null");
+            nw = static_cast<uint64_t>(ns) * static_cast<uint64_t>(wpn);
+            DBuf<int32_t> seeds;
+            DBuf<int64_t> cuts;
+            seeds.resize(ns);
+            if (ns) {
+                check_hip(hipMemcpyAsync(seeds.p, p.seed_nodes, ns * 4, hipMemcpyHostToDevice, s),
+                          "seeds H2D");
+            }
+            starts.resize(nw);
+            if (nw) {
+                hipLaunchKernelGGL((repeat_kernel<int32_t>), dim3(grid_for(nw)), dim3(kB), 0, s,
+                                   seeds.p, nw, wpn, starts.p);
+            }
+            if (p.cutoff_times) {
+                cuts.resize(ns);
+                if (ns) {
+                    check_hip(hipMemcpyAsync(cuts.p, p.cutoff_times, ns * 8,
+                                             hipMemcpyHostToDevice, s),
+                              "cutoffs H2D");
+                }
+                cutoffs.resize(nw);
+                if (nw) {
+                    hipLaunchKernelGGL((repeat_kernel<int64_t>), dim3(grid_for(nw)), dim3(kB), 0,
+                                       s, cuts.p, nw, wpn, cutoffs.p);
+                }
+                have_cutoffs = true;
+            }
+            sync();
+            have_starts = true;
+            break;
+        }
+        default:
+            throw InvalidArgument("unknown start mode");
+    }
+    if (nw > (1ull << 40)) throw InvalidArgument("too many walks");
+
+    // ---- optional shuffle of the walk order (same permutation for cutoffs)
+    if (have_starts && shuffle && nw > 1) {
+        if (nw > 0xffffffffull) throw InvalidArgument("shuffle supports < 2^32 walks");
+        k32a.ensure(nw);
+        k32b.ensure(nw);
+        v32a.ensure(nw);
+        v32b.ensure(nw);
+        hist.ensure(radix_hist_elems(nw));
+        hist_scratch.ensure(scan_scratch_elems(radix_hist_elems(nw)));
+        hipLaunchKernelGGL(random_keys_kernel, dim3(grid_for(nw)), dim3(kB), 0, s, nw,
+                           static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32), k32a.p,
+                           v32a.p);
+        const int w = radix_sort_u32(k32a.p, v32a.p, k32b.p, v32b.p, nw, 0, 32, hist.p,
+                                     hist_scratch.p, s);
+        const uint32_t* perm = w ? v32b.p : v32a.p;
+        DBuf<int32_t> tmp;
+        tmp.resize(nw);
+        hipLaunchKernelGGL((permute_kernel<int32_t>), dim3(grid_for(nw)), dim3(kB), 0, s,
+                           starts.p, perm, nw, tmp.p);
+        starts.swap(tmp);
+        if (have_cutoffs) {
+            DBuf<int64_t> tmpc;
+            tmpc.resize(nw);
+            hipLaunchKernelGGL((permute_kernel<int64_t>), dim3(grid_for(nw)), dim3(kB), 0, s,
+                               cutoffs.p, perm, nw, tmpc.p);
+            cutoffs.swap(tmpc);
+            sync();
+        } else {
+            sync();
+        }
+    }
+
+    // ---- draws
+    DrawSource ds{};
+    ds.stride = 1u + 2u * static_cast<uint32_t>(L);
+    ds.k0 = static_cast<uint32_t>(seed);
+    ds.k1 = static_cast<uint32_t>(seed >> 32);
+    ds.replay = nullptr;
+    if (p.replay_draws) {
+        const uint64_t need = nw * (1ull + 2ull * static_cast<uint64_t>(L));
+        if (p.replay_draws_len != need)
+            throw InvalidArgument("replay_draws must hold num_walks * (1 + 2 * max_walk_len) values");
+        // every draw is turned into an in-range index only if it lies in [0, 1)
+        for (uint64_t i = 0; i < need; ++i) {
+            const double r = p.replay_draws[i];
+            if (!(r >= 0.0 && r < 1.0)) throw InvalidArgument("replay_draws must lie in [0, 1)");
+        }
+        replay.resize(need);
+        if (need) {
+            check_hip(hipMemcpyAsync(replay.p, p.replay_draws, need * 8, hipMemcpyHostToDevice, s),
+                      "replay H2D");
+        }
+        ds.replay = replay.p;
+    }
+
+    // ---- outputs
+    const uint64_t slots = nw * static_cast<uint64_t>(L);
+    const uint64_t eslots = nw * static_cast<uint64_t>(L > 0 ? L - 1 : 0);
+    w_nodes.resize(slots);
+    w_ts.resize(slots);
+    w_eids.resize(eslots);
+    w_lens.resize(nw);
+    w_num = nw;
+    w_len = L;
+    w_dir_forward = forward ? 1 : 0;
+
+    // ---- graph view of the sampled direction
+    const bool use_in = !forward && cfg.is_directed;
+    const DirIndex& d = use_in ? in : out;
+    WalkGraph g{};
+    g.src = src.p;
+    g.dst = dst.p;
+    g.ts = ts.p;
+    g.E = static_cast<uint32_t>(E);
+    g.tsg_off = tsg_off.p;
+    g.T = static_cast<uint32_t>(T);
+    g.gw = forward ? fwd_cum.p : bwd_cum.p;
+    g.gw_size = weights_ready ? T : 0;
+    g.active = active.p;
+    g.active_size = static_cast<int32_t>(active.n);
+    g.d.cnt = d.cnt.p;
+    g.d.grp = d.grp.p;
+    g.d.idx = d.idx.p;
+    g.d.first_ts = d.first_ts.p;
+    g.d.idx_size = static_cast<uint32_t>(d.n_entries);
+    if (forward) {
+        g.d.w = out.w_fwd.p;
+        g.d.w_size = weights_ready ? out.n_groups : 0;
+    } else if (cfg.is_directed) {
+        g.d.w = in.w_bwd.p;
+        g.d.w_size = weights_ready ? in.n_groups : 0;
+    } else {
+        g.d.w = out.w_bwd.p;
+        g.d.w_size = weights_ready ? out.n_groups : 0;
+    }
+    g.adj_off = adj_ready ? adj_off.p : nullptr;
+    g.adj_nbr = adj_nbr.p;
+    g.adj_off_size = adj_ready ? static_cast<uint32_t>(adj_off.n) : 0;
+    g.tn2v = cfg.enable_temporal_node2vec;
+    g.inv_p = 1.0 / cfg.node2vec_p;
+    g.inv_q = 1.0 / cfg.node2vec_q;
+
+    WalkArgs a{};
+    a.L = L;
+    a.walk_bias = walk_bias;
+    a.start_bias = start_bias;
+    a.pad = cfg.walk_padding_value;
+    a.starts = have_starts ? starts.p : nullptr;
+    a.cutoffs = have_cutoffs ? cutoffs.p : nullptr;
+    a.n = nw;
+    a.ds = ds;
+    a.nodes = w_nodes.p;
+    a.ts = w_ts.p;
+    a.lens = w_lens.p;
+    a.eids = w_eids.p;
+
+    check_hip(hipEventRecord(ev[5], s), "event");
+    if (nw) {
+        if (E == 0) {
+            // empty graph: every start fails; the kernel still writes the padding
+            g.T = 0;
+            g.active_size = 0;
+        }
+        const dim3 grid(grid_for(nw));
+        if (forward && cfg.is_directed)
+            hipLaunchKernelGGL((walk_kernel<true, true>), grid, dim3(kB), 0, s, g, a);
+        else if (forward)
+            hipLaunchKernelGGL((walk_kernel<true, false>), grid, dim3(kB), 0, s, g, a);
+        else if (cfg.is_directed)
+            hipLaunchKernelGGL((walk_kernel<false, true>), grid, dim3(kB), 0, s, g, a);
+        else
+            hipLaunchKernelGGL((walk_kernel<false, false>), grid, dim3(kB), 0, s, g, a);
+        check_hip(hipGetLastError(), "walk kernel launch");
+    }
+    check_hip(hipEventRecord(ev[6], s), "event");
+
+    // ---- edge features of every walk slot (finalize_host_walks, on device)
+    if (feat_dim > 0 && eslots) {
+        w_feat.resize(eslots * feat_dim);
+        hipLaunchKernelGGL(gather_walk_features_kernel, dim3(grid_for(eslots * feat_dim)), dim3(kB),
+                           0, s, w_eids.p, eslots, static_cast<uint32_t>(feat_dim), feat.p,
+                           w_feat.p);
+        check_hip(hipGetLastError(), "feature gather launch");
+    } else {
+        w_feat.n = 0;
+    }
+    check_hip(hipEventRecord(ev[7], s), "event");
+    sync();
+    float ms = 0;
+    check_hip(hipEventElapsedTime(&ms, ev[4], ev[7]), "elapsed");
+    timings.sample_ms = ms;
+    check_hip(hipEventElapsedTime(&ms, ev[5], ev[6]), "elapsed");
+    timings.walk_kernel_ms = ms;
+    timings.walk_kernel_launches = nw ? 1 : 0;
+}
+
+void walk_stats(Engine& e, trw_walk_stats* out) {
+    hipStream_t s = e.stream;
+    e.acc64.ensure(4);
+    check_hip(hipMemsetAsync(e.acc64.p, 0, 32, s), "memset");
+    const bool use_in = !e.w_dir_forward && e.cfg.is_directed;
+    const DirIndex& d = use_in ? e.in : e.out;
+    if (e.w_num && e.w_len > 0) {
+        hipLaunchKernelGGL(walk_stats_kernel, dim3(grid_for(e.w_num)), dim3(kB), 0, s, e.w_nodes.p,
+                           e.w_lens.p, e.w_num, e.w_len, d.cnt.p,
+                           static_cast<int32_t>(e.active.n),
+                           reinterpret_cast<unsigned long long*>(e.acc64.p));
+    }
+    uint64_t h[4];
+    check_hip(hipMemcpyAsync(h, e.acc64.p, 32, hipMemcpyDeviceToHost, s), "read stats");
+    e.sync();
+    out->total_len = h[0];
+    out->transitions = h[1];
+    out->nonempty_walks = h[2];
+    out->algorithmic_bytes = h[3];
+}
+
+}  // namespace trw

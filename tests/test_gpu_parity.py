@@ -1,0 +1,198 @@
+"""GPU parity: the HIP engine (through the C ABI) against the oracle.
+
+Index arrays must be bit-exact; cumulative weights within 1e-12 relative;
+replay-mode walks (injected uniform draws in the reference layout) bit-exact.
+"""
+import numpy as np
+import pytest
+
+from oracle import pyoracle as po
+from tests import graphs
+
+pytestmark = pytest.mark.gpu
+
+INDEX_ARRAYS = [
+    "sources", "targets", "timestamps", "timestamp_group_offsets", "unique_timestamps",
+    "active_node_ids", "node_group_outbound_offsets", "node_group_inbound_offsets",
+    "node_ts_sorted_outbound_indices", "node_ts_sorted_inbound_indices",
+    "count_ts_group_per_node_outbound", "count_ts_group_per_node_inbound",
+    "node_ts_group_outbound_offsets", "node_ts_group_inbound_offsets",
+]
+WEIGHT_ARRAYS = [
+    "forward_cumulative_weights_exponential", "backward_cumulative_weights_exponential",
+    "outbound_forward_cumulative_weights_exponential",
+    "outbound_backward_cumulative_weights_exponential",
+    "inbound_backward_cumulative_weights_exponential",
+]
+ADJ_ARRAYS = ["node_adj_offsets", "node_adj_neighbors"]
+
+
+def _engine(**kw):
+    from temporal_random_walk import capi
+    return capi.Engine(**kw)
+
+
+def _pair(is_directed, batches, max_time_capacity=-1, weights=False, tn2v=False,
+          timescale_bound=-1.0, p=1.0, q=1.0, features=None):
+    og = po.OracleGraph(is_directed, max_time_capacity, weights, tn2v, timescale_bound, p, q)
+    eng = _engine(is_directed=is_directed, max_time_capacity=max_time_capacity,
+                  enable_weight_computation=weights, enable_temporal_node2vec=tn2v,
+                  timescale_bound=timescale_bound, node2vec_p=p, node2vec_q=q,
+                  shuffle_walk_order=False, global_seed=1234)
+    for k, (s, d, t) in enumerate(batches):
+        f = None if features is None else features[k]
+        og.add_edges(s, d, t, f)
+        eng.add_edges(s, d, t, f)
+    return og, eng
+
+
+def _assert_index_equal(og, eng, weights=False, tn2v=False):
+    for name in INDEX_ARRAYS:
+        a, b = og.array(name), eng.array(name)
+        assert a.dtype == b.dtype, name
+        assert np.array_equal(a, b), f"{name}: oracle {a[:8]} engine {b[:8]} sizes {a.size} {b.size}"
+    if weights:
+        for name in WEIGHT_ARRAYS:
+            a, b = og.array(name), eng.array(name)
+            assert a.shape == b.shape, name
+            np.testing.assert_allclose(b, a, rtol=1e-12, atol=0, err_msg=name)
+            # cumulative arrays must stay monotone within every node
+    if tn2v:
+        for name in ADJ_ARRAYS:
+            assert np.array_equal(og.array(name), eng.array(name)), name
+
+
+def test_index_sample_data_directed():
+    s, d, t = graphs.sample_data()
+    og, eng = _pair(True, [(s, d, t)])
+    _assert_index_equal(og, eng)
+
+
+def test_index_cfg1_directed_and_undirected():
+    s, d, t = graphs.cfg1()
+    for directed in (True, False):
+        og, eng = _pair(directed, [(s, d, t)])
+        _assert_index_equal(og, eng)
+
+
+def test_index_powerlaw_ties_multibatch():
+    s, d, t = graphs.powerlaw(20_000, 200_000, s=1.8, n_ts=2_000, seed=3)
+    batches = [(s[i:i + 50_000], d[i:i + 50_000], t[i:i + 50_000]) for i in range(0, 200_000, 50_000)]
+    og, eng = _pair(True, batches)
+    _assert_index_equal(og, eng)
+
+
+def test_index_streaming_window_eviction():
+    rng = np.random.default_rng(11)
+    batches = []
+    for k in range(5):
+        n = 30_000
+        s = graphs.zipf_ids(rng, n, 5_000, 1.6)
+        d = graphs.zipf_ids(rng, n, 5_000, 1.6)
+        t = rng.integers(k * 1000, (k + 1) * 1000, n).astype(np.int64)
+        batches.append((s, d, t))
+    og, eng = _pair(True, batches, max_time_capacity=2500)
+    _assert_index_equal(og, eng)
+    assert eng.latest_timestamp() == og.latest_timestamp
+
+
+def test_index_weights_and_adjacency():
+    s, d, t = graphs.powerlaw(5_000, 60_000, s=1.6, seed=5, ts_hi=10_000_000)
+    for directed in (True, False):
+        og, eng = _pair(directed, [(s, d, t)], weights=True, tn2v=True, timescale_bound=50.0)
+        _assert_index_equal(og, eng, weights=True, tn2v=True)
+
+
+def _walk_case(og, eng, picker, start_picker, forward, mode, L, n_or_wpn, seed_nodes=None,
+               cutoffs=None, seed=0):
+    direction = "Forward_In_Time" if forward else "Backward_In_Time"
+    if mode == "total":
+        starts = -np.ones(n_or_wpn, dtype=np.int32)
+        cut = None
+    elif mode == "all_nodes":
+        ids = np.nonzero(og.array("active_node_ids"))[0].astype(np.int32)
+        starts = np.repeat(ids, n_or_wpn)
+        cut = None
+    else:
+        starts = np.repeat(np.asarray(seed_nodes, dtype=np.int32), n_or_wpn)
+        cut = None if cutoffs is None else np.repeat(np.asarray(cutoffs, dtype=np.int64), n_or_wpn)
+    dr = graphs.draws(len(starts), L, seed=seed)
+    ref = og.walks(L, picker, start_picker, forward, starts, dr, cutoffs=cut)
+    got = eng.sample(mode, L, picker, n_or_wpn, initial_edge_bias=start_picker,
+                     direction=direction, seed_nodes=seed_nodes, cutoff_times=cutoffs,
+                     replay=dr, shuffle=False)
+    for k in ("nodes", "timestamps", "lens", "edge_ids"):
+        a = getattr(ref, k)
+        b = getattr(got, k)
+        assert a.shape == b.shape, k
+        bad = np.nonzero((a != b).reshape(len(starts), -1).any(axis=1))[0] if a.ndim > 1 else \
+            np.nonzero(a != b)[0]
+        assert bad.size == 0, (f"{picker}/{start_picker} fwd={forward} {mode}: {k} differs in "
+                               f"{bad.size} walks, first {bad[:5]}")
+    return got
+
+
+@pytest.mark.parametrize("directed", [True, False])
+@pytest.mark.parametrize("forward", [True, False])
+@pytest.mark.parametrize("picker", ["Uniform", "Linear", "ExponentialIndex"])
+def test_replay_walks_index_pickers(directed, forward, picker):
+    s, d, t = graphs.cfg1(n_nodes=2_000, n_edges=40_000, seed=42)
+    t = t // 50  # many tied timestamps
+    og, eng = _pair(directed, [(s, d, t)])
+    _walk_case(og, eng, picker, "Uniform", forward, "total", 20, 4_000, seed=1)
+    _walk_case(og, eng, picker, picker, forward, "all_nodes", 20, 2, seed=2)
+    seeds = np.arange(0, 2_000, 3, dtype=np.int32)
+    cuts = np.where(np.arange(seeds.size) % 3 == 0, -1,
+                    np.random.default_rng(3).integers(0, 20_000, seeds.size)).astype(np.int64)
+    _walk_case(og, eng, picker, picker, forward, "nodes", 16, 3, seed_nodes=seeds, cutoffs=cuts,
+               seed=3)
+
+
+@pytest.mark.parametrize("directed", [True, False])
+@pytest.mark.parametrize("forward", [True, False])
+@pytest.mark.parametrize("picker", ["ExponentialWeight", "TemporalNode2Vec"])
+def test_replay_walks_weight_pickers(directed, forward, picker):
+    s, d, t = graphs.powerlaw(3_000, 50_000, s=1.6, seed=9, ts_hi=1_000_000)
+    og, eng = _pair(directed, [(s, d, t)], weights=True, tn2v=picker == "TemporalNode2Vec",
+                    timescale_bound=50.0, p=0.5, q=2.0)
+    # the weights agree to 1e-12; the sampler is then checked bit-exactly on
+    # identical weights (picks on a flat cumulative tail amplify ulp noise)
+    _assert_index_equal(og, eng, weights=True)
+    for name in WEIGHT_ARRAYS:
+        w = eng.array(name)
+        if w.size:
+            og.set_weights(name, w)
+    _walk_case(og, eng, picker, picker, forward, "total", 24, 4_000, seed=4)
+    _walk_case(og, eng, picker, picker, forward, "all_nodes", 12, 1, seed=5)
+
+
+def test_replay_walks_powerlaw_exponential_index():
+    s, d, t = graphs.powerlaw(100_000, 400_000, s=1.8, n_ts=5_000, seed=44)
+    og, eng = _pair(True, [(s, d, t)])
+    _walk_case(og, eng, "ExponentialIndex", "Uniform", True, "total", 80, 20_000, seed=6)
+
+
+def test_normal_mode_invariants_and_features():
+    s, d, t = graphs.cfg1(n_nodes=3_000, n_edges=30_000, seed=8)
+    rng = np.random.default_rng(8)
+    feat = rng.standard_normal((len(s), 4)).astype(np.float32)
+    og, eng = _pair(True, [(s, d, t)], features=[feat])
+    L = 20
+    w = eng.sample("total", L, "Linear", 5_000, initial_edge_bias="Uniform")
+    store_s, store_d, store_t = eng.array("sources"), eng.array("targets"), eng.array("timestamps")
+    store_f = eng.array("edge_features").reshape(-1, 4)
+    lens = w.lens.astype(np.int64)
+    assert np.all((lens == 0) | ((lens >= 2) & (lens <= L)))
+    for i in range(0, 5_000, 7):
+        n = lens[i]
+        if n == 0:
+            continue
+        e = w.edge_ids[i, :n - 1]
+        assert np.all(e >= 0)
+        assert np.array_equal(store_s[e], w.nodes[i, :n - 1])
+        assert np.array_equal(store_d[e], w.nodes[i, 1:n])
+        assert np.array_equal(store_t[e], w.timestamps[i, 1:n])
+        assert np.all(np.diff(w.timestamps[i, 1:n]) > 0)
+        assert np.all(w.nodes[i, n:] == -1) and np.all(w.edge_ids[i, n - 1:] == -1)
+        np.testing.assert_array_equal(w.edge_features[i, :n - 1], store_f[e])
+        assert np.all(w.edge_features[i, n - 1:] == 0)
