@@ -95,6 +95,10 @@ def main():
     ap.add_argument("--walk-len", type=int, default=80)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-walks", type=int, default=200_000)
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="first run one plain device copy of this many MiB (torch copy_ "
+                         "kernel): the reference point that scales the HBM byte counters of "
+                         "a --pmc profile")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -114,6 +118,15 @@ def main():
     log(f"generated {len(src)} edges in {time.perf_counter() - t0:.1f}s")
 
     dev = torch.device("cuda:0")
+    if args.copy_calibration_mib > 0:
+        n = args.copy_calibration_mib * (1 << 20) // 4
+        a = torch.ones(n, dtype=torch.float32, device=dev)
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        b.copy_(a)
+        torch.cuda.synchronize()
+        log(f"copy calibration: {args.copy_calibration_mib} MiB read + written")
+        del a, b
     d_src = torch.from_numpy(src).to(dev)
     d_dst = torch.from_numpy(dst).to(dev)
     d_ts = torch.from_numpy(ts).to(dev)

@@ -179,6 +179,26 @@ __global__ void node_group_scatter_kernel(const uint32_t* __restrict__ flags,
     if (k == n - 1) grp[scan[n]] = static_cast<uint32_t>(n);
 }
 
+// Walk-order edge records.  mode 0: neighbour = target (out-lists of a
+// directed graph), 1: source (in-lists), 2: the other endpoint of an undirected
+// edge, (src == node) ? dst : src -- the reference's pick_other_number
+// (utils/utils.cuh:102-104) seen from the list's node.
+__global__ void make_records_kernel(const uint32_t* __restrict__ keys,
+                                    const uint32_t* __restrict__ idx,
+                                    const int32_t* __restrict__ src,
+                                    const int32_t* __restrict__ dst,
+                                    const int64_t* __restrict__ ts, size_t n, int mode,
+                                    EdgeRec* __restrict__ rec) {
+    const size_t k = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (k >= n) return;
+    const uint32_t e = idx[k];
+    int32_t nbr;
+    if (mode == 0) nbr = dst[e];
+    else if (mode == 1) nbr = src[e];
+    else nbr = (src[e] == static_cast<int32_t>(keys[k])) ? dst[e] : src[e];
+    rec[k] = EdgeRec{nbr, e, ts[e]};
+}
+
 // cnt[u] = number of groups of nodes < u = flag scan at u's first entry.
 __global__ void node_group_counts_kernel(const uint32_t* __restrict__ off,
                                          const uint32_t* __restrict__ scan, size_t vc,
@@ -322,7 +342,7 @@ namespace {
 
 // Stable per-direction node index from `keys`/`vals` already generated in
 // e.k32a / e.v32a (n entries).
-void build_direction(Engine& e, DirIndex& dir, size_t n, int key_bits, size_t vc,
+void build_direction(Engine& e, DirIndex& dir, size_t n, int key_bits, size_t vc, int rec_mode,
                      int64_t* host_scratch) {
     hipStream_t s = e.stream;
     dir.present = true;
@@ -337,6 +357,9 @@ void build_direction(Engine& e, DirIndex& dir, size_t n, int key_bits, size_t vc
         check_hip(hipMemcpyAsync(dir.key.p, ks.p, n * 4, hipMemcpyDeviceToDevice, s), "copy keys");
         check_hip(hipMemcpyAsync(dir.idx.p, vs.p, n * 4, hipMemcpyDeviceToDevice, s), "copy idx");
     }
+    dir.rec.resize(n);
+    hipLaunchKernelGGL(make_records_kernel, dim3(grid_for(n)), dim3(kB), 0, s, dir.key.p, dir.idx.p,
+                       e.src.p, e.dst.p, e.ts.p, n, rec_mode, dir.rec.p);
     dir.off.resize(vc);
     hipLaunchKernelGGL(lower_bound_offsets_kernel, dim3(grid_for(vc)), dim3(kB), 0, s, dir.key.p,
                        n, vc, dir.off.p);
@@ -473,14 +496,14 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
     if (cfg.is_directed) {
         hipLaunchKernelGGL(node_keys_kernel, dim3(grid_for(E)), dim3(kB), 0, s, src.p, E, k32a.p,
                            v32a.p);
-        build_direction(*this, out, E, key_bits, vc, hs);
+        build_direction(*this, out, E, key_bits, vc, 0, hs);
         hipLaunchKernelGGL(node_keys_kernel, dim3(grid_for(E)), dim3(kB), 0, s, dst.p, E, k32a.p,
                            v32a.p);
-        build_direction(*this, in, E, key_bits, vc, hs);
+        build_direction(*this, in, E, key_bits, vc, 1, hs);
     } else {
         hipLaunchKernelGGL(node_keys_pairs_kernel, dim3(grid_for(E)), dim3(kB), 0, s, src.p, dst.p,
                            E, k32a.p, v32a.p);
-        build_direction(*this, out, 2 * E, key_bits, vc, hs);
+        build_direction(*this, out, 2 * E, key_bits, vc, 2, hs);
         in.clear();
     }
     active.resize(v);

@@ -12,6 +12,7 @@
 //   per direction (out = by source / both endpoints if undirected, in = by target)
 //     off           uint32[V_c]    CSR offsets, V_c = max_id + 2
 //     idx           uint32[n]      edge ids ordered stably by (node, position)
+//     rec           EdgeRec[n]     (neighbour, edge id, ts) in the same order
 //     cnt           uint32[V_c]    exclusive prefix of per-node group counts
 //     grp           uint32[g+1]    group starts into idx, plus a terminator
 //     first_ts      int64[g]       timestamp of every node-timestamp group
@@ -76,9 +77,21 @@ struct DBuf {
     size_t bytes() const { return n * sizeof(T); }
 };
 
+// One entry of a node's edge list in walk order: the node reached over the
+// edge, the edge id and its timestamp -- everything a hop needs from the edge
+// in one aligned 16-byte load (instead of idx -> dst -> ts, three dependent
+// cache-line misses).
+struct alignas(16) EdgeRec {
+    int32_t nbr;
+    uint32_t eid;
+    int64_t ts;
+};
+static_assert(sizeof(EdgeRec) == 16, "EdgeRec must be 16 bytes");
+
 struct DirIndex {
     DBuf<uint32_t> off;      // V_c
     DBuf<uint32_t> idx;      // n entries
+    DBuf<EdgeRec> rec;       // n entries, same order as idx
     DBuf<uint32_t> key;      // node of every entry (sorted)
     DBuf<uint32_t> cnt;      // V_c
     DBuf<uint32_t> grp;      // g + 1
@@ -90,7 +103,7 @@ struct DirIndex {
     bool present = false;
 
     void clear() {
-        off.n = idx.n = key.n = cnt.n = grp.n = first_ts.n = w_fwd.n = w_bwd.n = 0;
+        off.n = idx.n = rec.n = key.n = cnt.n = grp.n = first_ts.n = w_fwd.n = w_bwd.n = 0;
         n_entries = n_groups = 0;
         present = false;
     }

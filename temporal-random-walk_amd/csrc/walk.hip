@@ -35,12 +35,18 @@ inline unsigned grid_for(size_t n) {
 struct DirView {
     const uint32_t* cnt;
     const uint32_t* grp;  // g + 1 entries (terminator)
-    const uint32_t* idx;
+    const EdgeRec* rec;   // walk-order edge records
     const int64_t* first_ts;
     uint32_t idx_size;
     const double* w;  // per-node cumulative weights of the sampled direction
     uint64_t w_size;
 };
+
+// Picker families the walk kernel is specialised for: only index pickers
+// (Uniform / Linear / ExponentialIndex / TEST_*) -- no weight or node2vec code,
+// so fewer registers and more waves in flight -- or any picker.
+constexpr int kFamIndex = 0;
+constexpr int kFamAny = 1;
 
 struct WalkGraph {
     const int32_t* src;
@@ -82,7 +88,18 @@ struct Sel {
     int64_t e;
 };
 
+// Result of a per-node selection: the node reached, the edge time and id.
+struct Hop {
+    int32_t nbr;
+    int64_t t;
+    int64_t e;
+};
+
 __device__ __forceinline__ Sel no_edge() { return Sel{-1, -1, -1, -1}; }
+__device__ __forceinline__ Hop no_hop() { return Hop{-1, -1, -1}; }
+__device__ __forceinline__ Hop hop_of(const EdgeRec& r) {
+    return Hop{r.nbr, r.ts, static_cast<int64_t>(r.eid)};
+}
 
 __device__ __forceinline__ Sel edge_of(const WalkGraph& g, uint32_t e) {
     return Sel{g.src[e], g.dst[e], g.ts[e], static_cast<int64_t>(e)};
@@ -126,22 +143,22 @@ __device__ __forceinline__ bool adjacent(const WalkGraph& g, int prev, int cand)
 }
 
 // graph/temporal_node2vec_helpers.cuh:127-199; vb/ve/gb/ge are global group
-// positions.  Returns an edge id or -1.
-template <bool Fwd, bool Dir>
-__device__ long tn2v_pick(const WalkGraph& g, int node, int prev, uint32_t vb, uint32_t ve,
-                          uint32_t gb, uint32_t ge, double rg, double re) {
-    if (vb >= ve || prev == -1) return -1;
+// positions.  The candidate node of a proposal is its record's neighbour
+// (get_candidate_node, walk_step_helpers.cuh:40-54).
+__device__ Hop tn2v_pick(const WalkGraph& g, int prev, uint32_t vb, uint32_t ve, uint32_t gb,
+                         uint32_t ge, double rg, double re) {
+    if (vb >= ve || prev == -1) return no_hop();
     double bmax = 1.0;
     if (g.inv_p > bmax) bmax = g.inv_p;
     if (g.inv_q > bmax) bmax = g.inv_q;
     const double inv_bmax = 1.0 / bmax;
-    long last = -1;
+    Hop last = no_hop();
     for (int retry = 0; retry < kNode2VecMaxRetries; ++retry) {
         const double gr = derive_uniform(rg, re, retry * 3 + 0);
         const double er = derive_uniform(rg, re, retry * 3 + 1);
         const double ar = derive_uniform(rg, re, retry * 3 + 2);
         const int gp = pick_exponential_weights(g.d.w, g.d.w_size, vb, ve, gr, gb);
-        if (gp == -1) return -1;
+        if (gp == -1) return no_hop();
         // a pick one past the node's last group is an empty range in the
         // reference (get_node_group_edge_end, walk_step_helpers.cuh:19-38)
         if (static_cast<uint32_t>(gp) >= ge) continue;
@@ -149,24 +166,24 @@ __device__ long tn2v_pick(const WalkGraph& g, int node, int prev, uint32_t vb, u
         if (es >= ee) continue;
         const uint64_t local = static_cast<uint64_t>(er * static_cast<double>(ee - es));
         const uint32_t pick = es + static_cast<uint32_t>(local < ee - es ? local : ee - es - 1);
-        const uint32_t eid = g.d.idx[pick];
-        int cand;
-        if (Dir) cand = Fwd ? g.dst[eid] : g.src[eid];
-        else cand = g.src[eid] == node ? g.dst[eid] : g.src[eid];
+        const EdgeRec r = g.d.rec[pick];
+        const int cand = r.nbr;
         const double beta = (cand == prev) ? g.inv_p : (adjacent(g, prev, cand) ? 1.0 : g.inv_q);
-        last = eid;
-        if (ar < beta * inv_bmax) return eid;
+        last = hop_of(r);
+        if (ar < beta * inv_bmax) return last;
     }
     return last;
 }
 
-// Per-hop selector (edge_selectors.cuh:277-443).
-template <bool Fwd, bool Dir>
-__device__ Sel node_edge_at(const WalkGraph& g, int picker, int node, int64_t t, int64_t cutoff,
+// Per-hop selector (edge_selectors.cuh:277-443).  The reference first checks
+// the dense active flag; an inactive node has no entries in either direction,
+// so the empty group range below rejects it identically without that load.
+template <bool Fwd, int Fam>
+__device__ Hop node_edge_at(const WalkGraph& g, int picker, int node, int64_t t, int64_t cutoff,
                             int prev, double rg, double re) {
-    if (!(node >= 0 && node < g.active_size && g.active[node] == 1)) return no_edge();
+    if (!(node >= 0 && node < g.active_size)) return no_hop();
     const uint32_t gb = g.d.cnt[node], ge = g.d.cnt[node + 1];
-    if (gb == ge) return no_edge();
+    if (gb == ge) return no_hop();
     const int G = static_cast<int>(ge - gb);
     const int64_t* fts = g.d.first_ts + gb;
     // filter_valid_groups_by_timestamp_slice (edge_selectors.cuh:66-120)
@@ -200,40 +217,32 @@ __device__ Sel node_edge_at(const WalkGraph& g, int picker, int node, int64_t t,
             ve = lo;
         }
     }
-    if (vb >= ve) return no_edge();
+    if (vb >= ve) return no_hop();
     uint32_t gpos;
-    if (picker == kTemporalNode2Vec) {
-        if (prev == -1) {
-            const int p = pick_exponential_weights(g.d.w, g.d.w_size, gb + vb, gb + ve, rg, gb);
-            if (p == -1) return no_edge();
-            gpos = static_cast<uint32_t>(p);
-        } else {
-            const long e = tn2v_pick<Fwd, Dir>(g, node, prev, gb + vb, gb + ve, gb, ge, rg, re);
-            if (e == -1) return no_edge();
-            return edge_of(g, static_cast<uint32_t>(e));
-        }
-    } else if (is_index_picker(picker)) {
+    if (Fam == kFamIndex || is_index_picker(picker)) {
         const int avail = ve - vb;
         const int index = pick_index(picker, 0, avail, !Fwd, rg);
-        if (index == -1 || index >= avail) return no_edge();
+        if (index == -1 || index >= avail) return no_hop();
         gpos = gb + static_cast<uint32_t>(vb + index);
+    } else if (picker == kTemporalNode2Vec && prev != -1) {
+        return tn2v_pick(g, prev, gb + vb, gb + ve, gb, ge, rg, re);
     } else {
-        if (picker != kExponentialWeight) return no_edge();
+        // ExponentialWeight, or node2vec's first hop (no previous node)
+        if (picker != kExponentialWeight && picker != kTemporalNode2Vec) return no_hop();
         const int p = pick_exponential_weights(g.d.w, g.d.w_size, gb + vb, gb + ve, rg, gb);
-        if (p == -1) return no_edge();
+        if (p == -1) return no_hop();
         gpos = static_cast<uint32_t>(p);
     }
     // A weight pick one past the node's last group reads, in the reference, the
     // next node's first group start for both ends: an empty range.
-    if (gpos >= ge) return no_edge();
+    if (gpos >= ge) return no_hop();
     const uint32_t es = g.d.grp[gpos], ee = g.d.grp[gpos + 1];
-    if (es >= ee || es >= g.d.idx_size || ee > g.d.idx_size) return no_edge();
-    const uint32_t e =
-        g.d.idx[es + static_cast<uint32_t>(static_cast<int>(re * static_cast<int>(ee - es)))];
-    return edge_of(g, e);
+    if (es >= ee || es >= g.d.idx_size || ee > g.d.idx_size) return no_hop();
+    return hop_of(
+        g.d.rec[es + static_cast<uint32_t>(static_cast<int>(re * static_cast<int>(ee - es)))]);
 }
 
-template <bool Fwd, bool Dir>
+template <bool Fwd, bool Dir, int Fam>
 __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
     const uint64_t w = blockIdx.x * static_cast<uint64_t>(kB) + threadIdx.x;
     if (w >= a.n) return;
@@ -250,24 +259,40 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
 
     const double r0 = draw_slot0(a.ds, w);
     const DrawPair r12 = draw_pair(a.ds, w, 1);
-    Sel se = (start == -1)
-                 ? start_edge<Fwd>(g, a.start_bias, r0, r12.a)
-                 : node_edge_at<Fwd, Dir>(g, a.start_bias, start, -1, cutoff, -1, r0, r12.a);
-    int len = 0;
-    if (se.v != -1) {
-        int cur, prev = -1;
-        if (Dir) {
-            wn[0] = Fwd ? se.u : se.v;
-            cur = Fwd ? se.v : se.u;
-        } else {
-            const int picked = start != -1 ? start : (r12.b >= 0.5 ? se.u : se.v);
-            wn[0] = picked;
-            cur = picked == se.u ? se.v : se.u;
+    // Start edge: the first slot holds the walk's origin and `cur` the node
+    // reached over the start edge (temporal_random_walk_cpu.cuh:39-90).
+    int first = -1, cur = -1;
+    int64_t cur_t = -1, cur_e = -1;
+    if (start == -1) {
+        const Sel se = start_edge<Fwd>(g, a.start_bias, r0, r12.a);
+        if (se.v != -1) {
+            if (Dir) {
+                first = Fwd ? se.u : se.v;
+                cur = Fwd ? se.v : se.u;
+            } else {
+                first = r12.b >= 0.5 ? se.u : se.v;
+                cur = first == se.u ? se.v : se.u;
+            }
+            cur_t = se.t;
+            cur_e = se.e;
         }
+    } else {
+        // a node's own list: the node is the edge's source (out), target (in)
+        // or one endpoint (undirected) -- the record's neighbour is the other
+        const Hop h = node_edge_at<Fwd, Fam>(g, a.start_bias, start, -1, cutoff, -1, r0, r12.a);
+        if (h.e != -1) {
+            first = start;
+            cur = h.nbr;
+            cur_t = h.t;
+            cur_e = h.e;
+        }
+    }
+    int len = 0;
+    if (cur_e != -1) {
+        int prev = -1;
+        wn[0] = first;
         wt[0] = Fwd ? INT64_MIN : INT64_MAX;
         len = 1;
-        int64_t cur_t = se.t;
-        int64_t cur_e = se.e;
         int walk_len = 1;
         while (walk_len < L && cur != a.pad) {
             wn[len] = cur;
@@ -278,13 +303,12 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
             // written; that selection cannot change the output, so it is skipped.
             if (walk_len == L - 1) break;
             const DrawPair r = draw_pair(a.ds, w, static_cast<uint32_t>(walk_len) + 1);
-            const Sel ne = node_edge_at<Fwd, Dir>(g, a.walk_bias, cur, cur_t, cutoff, prev, r.a, r.b);
-            if (ne.t == -1) break;
+            const Hop h = node_edge_at<Fwd, Fam>(g, a.walk_bias, cur, cur_t, cutoff, prev, r.a, r.b);
+            if (h.t == -1) break;  // the reference's failure test is ts == -1
             prev = cur;
-            if (Dir) cur = Fwd ? ne.v : ne.u;
-            else cur = (cur == ne.u) ? ne.v : ne.u;
-            cur_t = ne.t;
-            cur_e = ne.e;
+            cur = h.nbr;
+            cur_t = h.t;
+            cur_e = h.e;
             ++walk_len;
         }
     }
@@ -649,7 +673,7 @@ void Engine::sample(const trw_sample_params& p) {
     g.active_size = static_cast<int32_t>(active.n);
     g.d.cnt = d.cnt.p;
     g.d.grp = d.grp.p;
-    g.d.idx = d.idx.p;
+    g.d.rec = d.rec.p;
     g.d.first_ts = d.first_ts.p;
     g.d.idx_size = static_cast<uint32_t>(d.n_entries);
     if (forward) {
@@ -691,14 +715,19 @@ void Engine::sample(const trw_sample_params& p) {
             g.active_size = 0;
         }
         const dim3 grid(grid_for(nw));
-        if (forward && cfg.is_directed)
-            hipLaunchKernelGGL((walk_kernel<true, true>), grid, dim3(kB), 0, s, g, a);
-        else if (forward)
-            hipLaunchKernelGGL((walk_kernel<true, false>), grid, dim3(kB), 0, s, g, a);
-        else if (cfg.is_directed)
-            hipLaunchKernelGGL((walk_kernel<false, true>), grid, dim3(kB), 0, s, g, a);
-        else
-            hipLaunchKernelGGL((walk_kernel<false, false>), grid, dim3(kB), 0, s, g, a);
+        const bool index_only = is_index_picker(walk_bias) && is_index_picker(start_bias);
+#define TRW_LAUNCH_WALK(F, D)                                                                  \
+    do {                                                                                       \
+        if (index_only)                                                                        \
+            hipLaunchKernelGGL((walk_kernel<F, D, kFamIndex>), grid, dim3(kB), 0, s, g, a);     \
+        else                                                                                   \
+            hipLaunchKernelGGL((walk_kernel<F, D, kFamAny>), grid, dim3(kB), 0, s, g, a);       \
+    } while (0)
+        if (forward && cfg.is_directed) TRW_LAUNCH_WALK(true, true);
+        else if (forward) TRW_LAUNCH_WALK(true, false);
+        else if (cfg.is_directed) TRW_LAUNCH_WALK(false, true);
+        else TRW_LAUNCH_WALK(false, false);
+#undef TRW_LAUNCH_WALK
         check_hip(hipGetLastError(), "walk kernel launch");
     }
     check_hip(hipEventRecord(ev[6], s), "event");
