@@ -230,11 +230,11 @@ trw_status trw_get_timings(void* handle, trw_timings* out);
 trw_status trw_get_stream(void* handle, void** out_stream);
 /* Statistics of the last sample, computed on the device after the fact (not
  * part of any timing).  algorithmic_bytes is the compulsory traffic of the
- * walk kernel: per walk 40 B (start reads + length) and 12 B for slot 0; per
- * emitted slot after the start 20 B; per hop selected at node u
+ * walk kernel: per walk 40 B (start-edge reads + length); 12 B for slot 0 and
+ * 20 B for slot 1 when written; per hop selected at node u
  * 72 + 8*ceil(log2(G_u + 1)) B (G_u = u's timestamp groups in the sampled
- * direction; the 72 include that hop's 20 B of output); 20 B per padding
- * slot. */
+ * direction; the 72 include that hop's 20 B of output).  Padding is written
+ * by the layout pass, not the walk kernel. */
 typedef struct trw_walk_stats {
     uint64_t total_len;         /* sum of walk_lens: walk steps (reference metric) */
     uint64_t transitions;       /* sum of max(len - 1, 0) */

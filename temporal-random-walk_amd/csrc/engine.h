@@ -163,7 +163,10 @@ struct Engine {
     DBuf<double> replay;
     DBuf<uint64_t> acc64;
 
-    // walks (device)
+    // walks (device): slot-major scratch written by the walk kernel, then the
+    // row-major output [num_walks, L] the reference's API returns
+    DBuf<int32_t> sw_nodes;
+    DBuf<int64_t> sw_ts, sw_eids;
     DBuf<int32_t> w_nodes;
     DBuf<int64_t> w_ts, w_eids;
     DBuf<uint64_t> w_lens;

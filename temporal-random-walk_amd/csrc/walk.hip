@@ -251,9 +251,14 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
         a.lens[w] = 0;
         return;
     }
-    int32_t* wn = a.nodes + w * L;
-    int64_t* wt = a.ts + w * L;
-    int64_t* we = a.eids + w * (L - 1);
+    // Slot-major scratch: slot k of walk w lives at [k * n + w], so the 64
+    // lanes of a wave store 256 B (nodes) / 512 B (ts, edge ids) contiguously
+    // per slot.  transpose_walks_kernel produces the row-major output, the
+    // padding and the chronological order of backward walks.
+    const uint64_t n = a.n;
+    int32_t* wn = a.nodes + w;
+    int64_t* wt = a.ts + w;
+    int64_t* we = a.eids + w;
     const int start = a.starts ? a.starts[w] : -1;
     const int64_t cutoff = a.cutoffs ? a.cutoffs[w] : kNoCutoff;
 
@@ -295,9 +300,9 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
         len = 1;
         int walk_len = 1;
         while (walk_len < L && cur != a.pad) {
-            wn[len] = cur;
-            wt[len] = cur_t;
-            if (cur_e != -1) we[len - 1] = cur_e;
+            wn[len * n] = cur;
+            wt[len * n] = cur_t;
+            we[(len - 1) * n] = cur_e;
             ++len;
             // The reference draws and selects once more after the last slot is
             // written; that selection cannot change the output, so it is skipped.
@@ -312,29 +317,49 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
             ++walk_len;
         }
     }
-    for (int k = len; k < L; ++k) {
-        wn[k] = a.pad;
-        wt[k] = -1;
-    }
-    for (int k = len > 0 ? len - 1 : 0; k < L - 1; ++k) we[k] = -1;
     a.lens[w] = static_cast<uint64_t>(len);
-    if (!Fwd && len > 1) {  // data/walk_set/walk_set_view.cuh:50-80
-        for (int i = 0; i < len / 2; ++i) {
-            const int j = len - 1 - i;
-            const int32_t tn = wn[i];
-            wn[i] = wn[j];
-            wn[j] = tn;
-            const int64_t tt = wt[i];
-            wt[i] = wt[j];
-            wt[j] = tt;
+}
+
+// Slot-major scratch [K][n] -> row-major output [n][K] for one walk array,
+// 64 walks x 64 slots per workgroup through LDS.  `count` of walk w is the
+// number of written slots (len for nodes/timestamps, len - 1 for edge ids);
+// slots at or beyond it become `pad` (data/walk_set/walk_set_host.cu:25-29).
+// Backward walks come out reversed into chronological order
+// (data/walk_set/walk_set_view.cuh:50-80).
+template <typename T, int CountOffset>
+__global__ __launch_bounds__(256) void transpose_walks_kernel(const T* __restrict__ in,
+                                                              T* __restrict__ out,
+                                                              const uint64_t* __restrict__ lens,
+                                                              uint64_t n, int K, int reverse,
+                                                              T pad) {
+    __shared__ T tile[64][65];
+    __shared__ int cnt[64];
+    const uint64_t w0 = static_cast<uint64_t>(blockIdx.x) * 64;
+    const int k0 = blockIdx.y * 64;
+    const int tid = threadIdx.x;
+    if (tid < 64) {
+        const uint64_t w = w0 + tid;
+        const int c = w < n ? static_cast<int>(lens[w]) + CountOffset : 0;
+        cnt[tid] = c > 0 ? c : 0;
+    }
+    __syncthreads();
+    for (int idx = tid; idx < 64 * 64; idx += 256) {
+        const int i = idx >> 6, wl = idx & 63;  // slot in chunk, walk in tile
+        const uint64_t w = w0 + wl;
+        const int k = k0 + i;
+        T v = pad;
+        if (w < n && k < K && k < cnt[wl]) {
+            const int src = reverse ? cnt[wl] - 1 - k : k;
+            v = in[static_cast<uint64_t>(src) * n + w];
         }
-        const int ec = len - 1;
-        for (int i = 0; i < ec / 2; ++i) {
-            const int j = ec - 1 - i;
-            const int64_t te = we[i];
-            we[i] = we[j];
-            we[j] = te;
-        }
+        tile[i][wl] = v;
+    }
+    __syncthreads();
+    for (int idx = tid; idx < 64 * 64; idx += 256) {
+        const int wl = idx >> 6, i = idx & 63;
+        const uint64_t w = w0 + wl;
+        const int k = k0 + i;
+        if (w < n && k < K) out[w * K + k] = tile[i][wl];
     }
 }
 
@@ -415,7 +440,8 @@ __global__ void walk_stats_kernel(const int32_t* __restrict__ nodes,
     unsigned long long bytes = 0, trans = 0, total = 0, nonempty = 0;
     if (w < n && L > 0) {
         const int len = static_cast<int>(lens[w]);
-        bytes = 40 + 12;
+        bytes = 40;
+        if (len >= 1) bytes += 12;
         if (len >= 2) bytes += 20;
         for (int k = 1; k + 1 < len; ++k) {
             const int u = nodes[w * L + k];
@@ -424,7 +450,6 @@ __global__ void walk_stats_kernel(const int32_t* __restrict__ nodes,
             const int probes = G ? 32 - __clz(G) : 0;  // ceil(log2(G + 1))
             bytes += 72 + 8 * probes;
         }
-        bytes += 20ull * static_cast<unsigned long long>(L - (len > 0 ? len : 1));
         trans = len > 0 ? len - 1 : 0;
         total = len;
         nonempty = len > 0;
@@ -649,6 +674,9 @@ void Engine::sample(const trw_sample_params& p) {
     // ---- outputs
     const uint64_t slots = nw * static_cast<uint64_t>(L);
     const uint64_t eslots = nw * static_cast<uint64_t>(L > 0 ? L - 1 : 0);
+    sw_nodes.resize(slots);
+    sw_ts.resize(slots);
+    sw_eids.resize(eslots);
     w_nodes.resize(slots);
     w_ts.resize(slots);
     w_eids.resize(eslots);
@@ -702,10 +730,10 @@ void Engine::sample(const trw_sample_params& p) {
     a.cutoffs = have_cutoffs ? cutoffs.p : nullptr;
     a.n = nw;
     a.ds = ds;
-    a.nodes = w_nodes.p;
-    a.ts = w_ts.p;
+    a.nodes = sw_nodes.p;
+    a.ts = sw_ts.p;
     a.lens = w_lens.p;
-    a.eids = w_eids.p;
+    a.eids = sw_eids.p;
 
     check_hip(hipEventRecord(ev[5], s), "event");
     if (nw) {
@@ -731,6 +759,21 @@ void Engine::sample(const trw_sample_params& p) {
         check_hip(hipGetLastError(), "walk kernel launch");
     }
     check_hip(hipEventRecord(ev[6], s), "event");
+    if (nw && L > 0) {
+        const unsigned gx = static_cast<unsigned>((nw + 63) / 64);
+        const int rev = forward ? 0 : 1;
+        hipLaunchKernelGGL((transpose_walks_kernel<int32_t, 0>), dim3(gx, (L + 63) / 64), dim3(256),
+                           0, s, sw_nodes.p, w_nodes.p, w_lens.p, nw, L, rev,
+                           static_cast<int32_t>(cfg.walk_padding_value));
+        hipLaunchKernelGGL((transpose_walks_kernel<int64_t, 0>), dim3(gx, (L + 63) / 64), dim3(256),
+                           0, s, sw_ts.p, w_ts.p, w_lens.p, nw, L, rev, static_cast<int64_t>(-1));
+        if (L > 1) {
+            hipLaunchKernelGGL((transpose_walks_kernel<int64_t, -1>), dim3(gx, (L - 1 + 63) / 64),
+                               dim3(256), 0, s, sw_eids.p, w_eids.p, w_lens.p, nw, L - 1, rev,
+                               static_cast<int64_t>(-1));
+        }
+        check_hip(hipGetLastError(), "transpose launch");
+    }
 
     // ---- edge features of every walk slot (finalize_host_walks, on device)
     if (feat_dim > 0 && eslots) {

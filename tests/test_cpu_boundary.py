@@ -1,0 +1,70 @@
+"""CPU checks of the drop-in boundary: the C-ABI library loads and exports
+every symbol include/trw_engine.h declares; the Python module imports and,
+without a GPU, fails loudly instead of falling back to a CPU path."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "trw_engine.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(trw_[a-z_]+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    names = _declared_functions()
+    for required in ("trw_create", "trw_destroy", "trw_add_edges", "trw_add_edges_device",
+                     "trw_sample", "trw_sample_device", "trw_get_array", "trw_last_error"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    from temporal_random_walk import capi
+
+    lib = ctypes.CDLL(capi.LIB_PATH)
+    missing = [n for n in _declared_functions() if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+    assert sorted(capi.EXPORTS) == _declared_functions()
+    assert capi.lib().trw_abi_version() == 1
+
+
+def test_library_carries_gfx950_code():
+    from temporal_random_walk import capi
+
+    blob = open(capi.LIB_PATH, "rb").read()
+    assert b"gfx950" in blob
+
+
+def test_python_surface_matches_reference_names():
+    import temporal_random_walk as trw
+
+    cls = trw.TemporalRandomWalk
+    for m in ("add_multiple_edges", "get_random_walks_and_times_for_all_nodes",
+              "get_random_walks_and_times_for_last_batch", "get_random_walks_and_times_for_nodes",
+              "get_random_walks_and_times", "get_node_count", "get_edge_count", "get_node_ids",
+              "get_node_degrees", "clear", "get_memory_used", "set_node_features",
+              "get_node_features", "add_edges_from_networkx", "to_networkx"):
+        assert hasattr(cls, m), m
+
+
+def _has_gpu():
+    import torch
+
+    return torch.cuda.device_count() > 0
+
+
+@pytest.mark.skipif(_has_gpu(), reason="checks the no-GPU behaviour")
+def test_no_gpu_fails_loudly():
+    import temporal_random_walk as trw
+    from temporal_random_walk import capi
+
+    with pytest.raises(RuntimeError, match="no HIP device"):
+        trw.TemporalRandomWalk(is_directed=True, use_gpu=False)
+    with pytest.raises(capi.EngineError, match="no HIP device"):
+        capi.Engine(is_directed=True)

@@ -1,0 +1,187 @@
+"""The drop-in Python surface on the GPU: the reference's own Python tests
+(py_tests/test_edge_features.py) restated, plus its C++ tests' behaviours for
+cutoffs, padding, last-batch starts, queries and errors
+(test/test_walk_cutoff_times.cpp, test_walk_padding_value.cpp,
+test_temporal_random_walk.cpp)."""
+import numpy as np
+import pytest
+
+from tests import graphs
+
+pytestmark = pytest.mark.gpu
+
+
+def _trw(**kw):
+    from temporal_random_walk import TemporalRandomWalk
+    kw.setdefault("use_gpu", True)
+    return TemporalRandomWalk(**kw)
+
+
+def _features_graph():
+    tw = _trw(is_directed=True)
+    tw.add_multiple_edges(np.array([0, 1, 2], np.int32), np.array([1, 2, 3], np.int32),
+                          np.array([10, 20, 30], np.int64),
+                          np.array([[1.0, 1.5], [2.0, 2.5], [3.0, 3.5]], np.float32))
+    feat = {(0, 1, 10): [1.0, 1.5], (1, 2, 20): [2.0, 2.5], (2, 3, 30): [3.0, 3.5]}
+    return tw, feat
+
+
+def test_walks_include_edge_features_and_zero_unused_slots():
+    tw, feat = _features_graph()
+    L = 4
+    nodes, ts, lens, wf = tw.get_random_walks_and_times_for_all_nodes(
+        max_walk_len=L, walk_bias="Uniform", num_walks_per_node=1,
+        walk_direction="Forward_In_Time")
+    assert wf is not None and wf.shape == (len(lens), L - 1, 2)
+    for w, n in enumerate(lens):
+        n = int(n)
+        for j in range(max(0, n - 1)):
+            key = (int(nodes[w, j]), int(nodes[w, j + 1]), int(ts[w, j + 1]))
+            np.testing.assert_allclose(wf[w, j], feat[key])
+        for j in range(max(0, n - 1), L - 1):
+            np.testing.assert_allclose(wf[w, j], [0.0, 0.0])
+
+
+def test_walks_return_none_without_features():
+    tw = _trw(is_directed=True)
+    tw.add_multiple_edges(np.array([0, 1], np.int32), np.array([1, 2], np.int32),
+                          np.array([10, 20], np.int64))
+    _, _, _, wf = tw.get_random_walks_and_times(max_walk_len=3, walk_bias="Uniform",
+                                                 num_walks_total=2)
+    assert wf is None
+
+
+def test_feature_validation_errors():
+    tw, _ = _features_graph()
+    with pytest.raises(RuntimeError, match="feature_dim mismatch"):
+        tw.add_multiple_edges(np.array([4], np.int32), np.array([5], np.int32),
+                              np.array([40], np.int64), np.array([[9.0, 9.1, 9.2]], np.float32))
+    # edge_data.cu:75-89 checks the dimension before the missing features, so a
+    # featureless batch on a featured store reports the dimension mismatch
+    with pytest.raises(RuntimeError, match="feature_dim mismatch"):
+        tw.add_multiple_edges(np.array([4], np.int32), np.array([5], np.int32),
+                              np.array([40], np.int64))
+    with pytest.raises(RuntimeError, match="same length"):
+        tw.add_multiple_edges(np.array([4, 5], np.int32), np.array([5], np.int32),
+                              np.array([40], np.int64))
+
+
+def test_invalid_strings_raise_value_error():
+    tw = _trw(is_directed=True)
+    tw.add_multiple_edges(np.array([0], np.int32), np.array([1], np.int32),
+                          np.array([1], np.int64))
+    with pytest.raises(ValueError, match="Invalid picker type"):
+        tw.get_random_walks_and_times(max_walk_len=3, walk_bias="Bogus", num_walks_total=1)
+    with pytest.raises(ValueError, match="Invalid walk direction"):
+        tw.get_random_walks_and_times(max_walk_len=3, walk_bias="Uniform", num_walks_total=1,
+                                      walk_direction="Sideways")
+    with pytest.raises(ValueError, match="kernel_launch_type"):
+        tw.get_random_walks_and_times(max_walk_len=3, walk_bias="Uniform", num_walks_total=1,
+                                      kernel_launch_type="WARP")
+
+
+def test_queries_match_store():
+    s, d, t = graphs.sample_data()
+    tw = _trw(is_directed=True)
+    tw.add_multiple_edges(s, d, t)
+    assert tw.get_edge_count() == len(s)
+    ids = tw.get_node_ids()
+    assert np.array_equal(ids, np.unique(np.concatenate([s, d])))
+    assert tw.get_node_count() == len(ids)
+    deg_out = tw.get_node_degrees(ids, "Forward_In_Time")
+    deg_in = tw.get_node_degrees(ids, "Backward_In_Time")
+    assert np.array_equal(deg_out, np.bincount(s, minlength=ids.max() + 1)[ids])
+    assert np.array_equal(deg_in, np.bincount(d, minlength=ids.max() + 1)[ids])
+    assert list(tw.get_node_degrees(np.array([-1, 10**6], np.int32), "Forward_In_Time")) == [0, 0]
+    assert tw.get_memory_used() > 0
+    tw.clear()
+    assert tw.get_edge_count() == 0 and tw.get_node_count() == 0
+    nodes, _, lens, _ = tw.get_random_walks_and_times(max_walk_len=5, walk_bias="Uniform",
+                                                      num_walks_total=4)
+    assert np.all(lens == 0) and np.all(nodes == -1)
+
+
+def test_padding_value_and_short_lengths():
+    tw = _trw(is_directed=True, walk_padding_value=-7)
+    tw.add_multiple_edges(np.array([1, 2], np.int32), np.array([2, 3], np.int32),
+                          np.array([10, 20], np.int64))
+    nodes, ts, lens, _ = tw.get_random_walks_and_times_for_all_nodes(
+        max_walk_len=6, walk_bias="Linear", num_walks_per_node=3)
+    for w, n in enumerate(lens):
+        assert np.all(nodes[w, int(n):] == -7) and np.all(ts[w, int(n):] == -1)
+    nodes, ts, lens, _ = tw.get_random_walks_and_times(max_walk_len=1, walk_bias="Uniform",
+                                                       num_walks_total=5)
+    assert nodes.shape == (5, 1) and np.all(lens == 1)
+    nodes, ts, lens, _ = tw.get_random_walks_and_times(max_walk_len=0, walk_bias="Uniform",
+                                                       num_walks_total=5)
+    assert nodes.shape == (5, 0) and np.all(lens == 0)
+
+
+def test_cutoff_times_bound_every_hop():
+    # test_walk_cutoff_times.cpp: a cutoff is an exclusive upper bound on the
+    # time of every edge of the walk, in both directions; -1 is unbounded
+    s, d, t = graphs.cfg1(n_nodes=500, n_edges=20_000, seed=3)
+    tw = _trw(is_directed=True, global_seed=11, shuffle_walk_order=False)
+    tw.add_multiple_edges(s, d, t)
+    seeds = np.arange(0, 500, 2, dtype=np.int32)
+    cut = np.full(seeds.size, 400_000, np.int64)
+    cut[::4] = -1
+    wpn = 4
+    for direction in ("Forward_In_Time", "Backward_In_Time"):
+        nodes, ts, lens, _ = tw.get_random_walks_and_times_for_nodes(
+            seeds, max_walk_len=12, walk_bias="Uniform", num_walks_per_node=wpn,
+            walk_direction=direction, cutoff_times=cut)
+        assert nodes.shape == (seeds.size * wpn, 12)
+        bounded_hops = 0
+        late_hops_unbounded = 0
+        for w, n in enumerate(lens):
+            n = int(n)
+            if n < 2:
+                continue
+            c = int(cut[w // wpn])
+            origin = nodes[w, 0] if direction == "Forward_In_Time" else nodes[w, n - 1]
+            assert origin == seeds[w // wpn]
+            if c != -1:
+                assert np.all(ts[w, 1:n] < c) if direction == "Forward_In_Time" else \
+                    np.all(ts[w, :n - 1] < c)
+                bounded_hops += n - 1
+            else:
+                late_hops_unbounded += int(np.sum(ts[w] >= 400_000))
+        assert bounded_hops > 0 and late_hops_unbounded > 0
+
+
+def test_last_batch_starts_only_from_batch_sources():
+    tw = _trw(is_directed=True, global_seed=3)
+    tw.add_multiple_edges(np.array([1, 2], np.int32), np.array([2, 3], np.int32),
+                          np.array([10, 20], np.int64))
+    tw.add_multiple_edges(np.array([7, 7, 8], np.int32), np.array([1, 2, 9], np.int32),
+                          np.array([30, 40, 50], np.int64))
+    nodes, _, lens, _ = tw.get_random_walks_and_times_for_last_batch(
+        max_walk_len=4, walk_bias="Uniform", num_walks_per_node=5)
+    assert nodes.shape == (2 * 5, 4)
+    assert set(int(x) for x in nodes[:, 0] if x != -1) <= {7, 8}
+
+
+def test_seed_reproducibility_and_shuffle():
+    s, d, t = graphs.cfg1(n_nodes=1_000, n_edges=20_000, seed=5)
+    out = []
+    for _ in range(2):
+        tw = _trw(is_directed=True, global_seed=99)
+        tw.add_multiple_edges(s, d, t)
+        out.append(tw.get_random_walks_and_times_for_all_nodes(
+            max_walk_len=10, walk_bias="ExponentialIndex", num_walks_per_node=2))
+    for a, b in zip(out[0][:3], out[1][:3]):
+        assert np.array_equal(a, b)
+    starts = out[0][0][:, 0]
+    assert not np.all(np.diff(starts[starts >= 0]) >= 0), "walk order should be shuffled"
+
+
+def test_networkx_round_trip():
+    nx = pytest.importorskip("networkx")
+    g = nx.DiGraph()
+    g.add_edge(1, 2, timestamp=5)
+    g.add_edge(2, 3, timestamp=7)
+    tw = _trw(is_directed=True)
+    tw.add_edges_from_networkx(g)
+    h = tw.to_networkx()
+    assert sorted(h.edges(data="timestamp")) == [(1, 2, 5), (2, 3, 7)]
