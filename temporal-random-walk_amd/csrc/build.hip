@@ -276,35 +276,57 @@ __global__ void divide_kernel(double* __restrict__ a, double* __restrict__ b, si
     b[i] = b[i] / sums_b[0];
 }
 
-// Per-node cumulative exponential weights (node_edge_index.cu:500-640): one
-// thread per node; within a node the normalised weights are accumulated
-// sequentially in group order, exactly as the reference does, so the
-// cumulative array is monotone per node.
-__global__ void node_weights_kernel(const uint32_t* __restrict__ cnt,
-                                    const uint32_t* __restrict__ grp,
-                                    const int64_t* __restrict__ first_ts, size_t nodes,
-                                    double bound, int compute_forward, double* __restrict__ wf,
-                                    double* __restrict__ wb) {
+// Per-node cumulative exponential weights (node_edge_index.cu:500-640).
+// Raw weights: group size * exp(scaled distance to the node's pivot):
+// backward pivots on the node's latest time, forward on its earliest.
+struct NodeWeightParams {
+    int64_t mn, mx;
+    double scale;
+};
+
+__device__ __forceinline__ NodeWeightParams node_weight_params(const int64_t* first_ts,
+                                                               uint32_t s, uint32_t e,
+                                                               double bound) {
+    const int64_t mn = first_ts[s], mx = first_ts[e - 1];
+    const double diff = static_cast<double>(mx - mn);
+    return NodeWeightParams{mn, mx, (bound > 0 && diff > 0) ? bound / diff : 1.0};
+}
+
+__device__ __forceinline__ void raw_node_weights(const NodeWeightParams& q, const uint32_t* grp,
+                                                 const int64_t* first_ts, uint32_t p,
+                                                 double bound, double* f, double* b) {
+    const double sz = static_cast<double>(grp[p + 1] - grp[p]);
+    const int64_t t = first_ts[p];
+    const double bsc = bound > 0 ? static_cast<double>(t - q.mx) * q.scale
+                                 : static_cast<double>(t - q.mx);
+    const double fsc = bound > 0 ? static_cast<double>(q.mn - t) * q.scale
+                                 : static_cast<double>(q.mn - t);
+    *b = sz * exp(bsc);
+    *f = sz * exp(fsc);
+}
+
+// Nodes with at most kHeavyGroups groups: one thread per node; the normalised
+// weights are accumulated sequentially in group order, exactly as the
+// reference does (node_edge_index.cu:617-639).
+constexpr uint32_t kHeavyGroups = 4096;
+
+__global__ void node_weights_light_kernel(const uint32_t* __restrict__ cnt,
+                                          const uint32_t* __restrict__ grp,
+                                          const int64_t* __restrict__ first_ts, size_t nodes,
+                                          double bound, int compute_forward,
+                                          double* __restrict__ wf, double* __restrict__ wb) {
     const size_t u = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
     if (u >= nodes) return;
     const uint32_t s = cnt[u], e = cnt[u + 1];
-    if (s >= e) return;
-    const int64_t mn = first_ts[s], mx = first_ts[e - 1];
-    const double diff = static_cast<double>(mx - mn);
-    const double scale = (bound > 0 && diff > 0) ? bound / diff : 1.0;
+    if (s >= e || e - s > kHeavyGroups) return;
+    const NodeWeightParams q = node_weight_params(first_ts, s, e, bound);
     double fsum = 0.0, bsum = 0.0;
     for (uint32_t p = s; p < e; ++p) {
-        const double sz = static_cast<double>(grp[p + 1] - grp[p]);
-        const int64_t t = first_ts[p];
-        const double bsc = bound > 0 ? static_cast<double>(t - mx) * scale
-                                     : static_cast<double>(t - mx);
-        const double b = sz * exp(bsc);
+        double f, b;
+        raw_node_weights(q, grp, first_ts, p, bound, &f, &b);
         wb[p] = b;
         bsum += b;
         if (compute_forward) {
-            const double fsc = bound > 0 ? static_cast<double>(mn - t) * scale
-                                         : static_cast<double>(mn - t);
-            const double f = sz * exp(fsc);
             wf[p] = f;
             fsum += f;
         }
@@ -316,6 +338,124 @@ __global__ void node_weights_kernel(const uint32_t* __restrict__ cnt,
         if (compute_forward) {
             fc += wf[p] / fsum;
             wf[p] = fc;
+        }
+    }
+}
+
+__global__ void heavy_node_flags_kernel(const uint32_t* __restrict__ cnt, size_t nodes,
+                                        uint32_t* __restrict__ flags) {
+    const size_t u = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (u < nodes) flags[u] = (cnt[u + 1] - cnt[u] > kHeavyGroups) ? 1u : 0u;
+}
+
+__global__ void compact_nodes_kernel(const uint32_t* __restrict__ flags,
+                                     const uint32_t* __restrict__ scan, size_t nodes,
+                                     uint32_t* __restrict__ out) {
+    const size_t u = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (u < nodes && flags[u]) out[scan[u]] = static_cast<uint32_t>(u);
+}
+
+__device__ __forceinline__ double wave_sum_f64(double x) {
+    for (int off = 32; off > 0; off >>= 1) x += __shfl_down(x, off, 64);
+    return x;
+}
+
+// Block-wide (256 threads) sum; every thread receives the total.
+__device__ double block_sum_f64(double x, double* s4) {
+    x = wave_sum_f64(x);
+    if ((threadIdx.x & 63) == 0) s4[threadIdx.x >> 6] = x;
+    __syncthreads();
+    const double t = s4[0] + s4[1] + s4[2] + s4[3];
+    __syncthreads();
+    return t;
+}
+
+// Exclusive block scan (sum or max) of one value per thread.
+template <bool Max>
+__device__ double block_excl_scan_f64(double v, double* s4, double* total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    double x = v;
+    for (int off = 1; off < 64; off <<= 1) {
+        const double y = __shfl_up(x, off, 64);
+        if (lane >= off) x = Max ? fmax(x, y) : x + y;
+    }
+    if (lane == 63) s4[wave] = x;
+    __syncthreads();
+    double before = Max ? -1.0 : 0.0, tot = Max ? -1.0 : 0.0;
+    for (int w = 0; w < 4; ++w) {
+        const double sw = s4[w];
+        if (w < wave) before = Max ? fmax(before, sw) : before + sw;
+        tot = Max ? fmax(tot, sw) : tot + sw;
+    }
+    __syncthreads();
+    *total = tot;
+    const double excl_in_wave = __shfl_up(x, 1, 64);
+    if (Max) return lane == 0 ? before : fmax(before, excl_in_wave);
+    return before + (lane == 0 ? 0.0 : excl_in_wave);
+}
+
+// Nodes with more than kHeavyGroups groups (hubs): one workgroup per node.
+// Pass 1 writes raw weights and block-reduces the node's sums; pass 2 scans
+// the normalised weights in chunks of 256 x 16 with a running carry and then
+// takes a running maximum, so the cumulative array is non-decreasing by
+// construction (the picker's end_sum < start_sum guard, random/pickers.cuh:
+// 109-111, must never fire on a rounding artefact).  Values agree with the
+// sequential reference sum to a few ulps.
+constexpr int kHeavyItems = 16;
+
+__global__ __launch_bounds__(256) void node_weights_heavy_kernel(
+    const uint32_t* __restrict__ heavy, const uint32_t* __restrict__ cnt,
+    const uint32_t* __restrict__ grp, const int64_t* __restrict__ first_ts, double bound,
+    int compute_forward, double* __restrict__ wf, double* __restrict__ wb) {
+    __shared__ double s4[4];
+    const uint32_t u = heavy[blockIdx.x];
+    const uint32_t s = cnt[u], e = cnt[u + 1];
+    const NodeWeightParams q = node_weight_params(first_ts, s, e, bound);
+    double fs = 0.0, bs = 0.0;
+    for (uint32_t p = s + threadIdx.x; p < e; p += 256) {
+        double f, b;
+        raw_node_weights(q, grp, first_ts, p, bound, &f, &b);
+        wb[p] = b;
+        bs += b;
+        if (compute_forward) {
+            wf[p] = f;
+            fs += f;
+        }
+    }
+    const double bsum = block_sum_f64(bs, s4);
+    const double fsum = compute_forward ? block_sum_f64(fs, s4) : 1.0;
+    for (int dir = 0; dir < (compute_forward ? 2 : 1); ++dir) {
+        double* w = dir == 0 ? wb : wf;
+        const double sum = dir == 0 ? bsum : fsum;
+        double carry = 0.0;
+        for (uint32_t base = s; base < e; base += 256 * kHeavyItems) {
+            const uint32_t p0 = base + threadIdx.x * kHeavyItems;
+            double v[kHeavyItems];
+            double run = 0.0;
+#pragma unroll
+            for (int j = 0; j < kHeavyItems; ++j) {
+                const uint32_t p = p0 + j;
+                run += p < e ? w[p] / sum : 0.0;
+                v[j] = run;
+            }
+            double tot;
+            const double before = block_excl_scan_f64<false>(run, s4, &tot);
+            double mx = 0.0;
+#pragma unroll
+            for (int j = 0; j < kHeavyItems; ++j) {
+                v[j] = carry + (before + v[j]);
+                mx = fmax(mx, v[j]);
+            }
+            double mtot;
+            const double mbefore = block_excl_scan_f64<true>(mx, s4, &mtot);
+            double m = fmax(mbefore, carry);
+#pragma unroll
+            for (int j = 0; j < kHeavyItems; ++j) {
+                const uint32_t p = p0 + j;
+                m = fmax(m, v[j]);
+                if (p < e) w[p] = m;
+            }
+            carry = fmax(mtot, carry);
         }
     }
 }
@@ -383,6 +523,35 @@ void build_direction(Engine& e, DirIndex& dir, size_t n, int key_bits, size_t vc
     hipLaunchKernelGGL(node_group_counts_kernel, dim3(grid_for(vc)), dim3(kB), 0, s, dir.off.p,
                        e.scan.p, vc, dir.cnt.p);
     check_hip(hipGetLastError(), "direction index launch");
+}
+
+void node_weights(Engine& e, DirIndex& dir, size_t v, double bound, bool compute_forward,
+                  int64_t* host_scratch) {
+    hipStream_t s = e.stream;
+    double* wf = compute_forward ? dir.w_fwd.p : nullptr;
+    hipLaunchKernelGGL(node_weights_light_kernel, dim3(grid_for(v)), dim3(kB), 0, s, dir.cnt.p,
+                       dir.grp.p, dir.first_ts.p, v, bound, compute_forward ? 1 : 0, wf,
+                       dir.w_bwd.p);
+    // hubs: list them on the device, then one workgroup each
+    e.flags.ensure(v + 1);
+    e.scan.ensure(v + 1);
+    e.scan_scratch.ensure(scan_scratch_elems(v + 1));
+    hipLaunchKernelGGL(heavy_node_flags_kernel, dim3(grid_for(v)), dim3(kB), 0, s, dir.cnt.p, v,
+                       e.flags.p);
+    exclusive_scan_u32(e.flags.p, e.scan.p, v, e.scan_scratch.p, s);
+    check_hip(hipMemcpyAsync(host_scratch, e.scan.p + v, 4, hipMemcpyDeviceToHost, s), "heavy n");
+    e.sync();
+    uint32_t nh;
+    std::memcpy(&nh, host_scratch, 4);
+    if (nh) {
+        e.k32b.ensure(nh);
+        hipLaunchKernelGGL(compact_nodes_kernel, dim3(grid_for(v)), dim3(kB), 0, s, e.flags.p,
+                           e.scan.p, v, e.k32b.p);
+        hipLaunchKernelGGL(node_weights_heavy_kernel, dim3(nh), dim3(256), 0, s, e.k32b.p,
+                           dir.cnt.p, dir.grp.p, dir.first_ts.p, bound, compute_forward ? 1 : 0,
+                           wf, dir.w_bwd.p);
+    }
+    check_hip(hipGetLastError(), "node weights launch");
 }
 
 }  // namespace
@@ -555,15 +724,14 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
         fscan_scratch.ensure(scan_scratch_elems(std::max<size_t>(T, out.n_groups)));
         inclusive_scan_f64(fwd_cum.p, T, fscan_scratch.p, s);
         inclusive_scan_f64(bwd_cum.p, T, fscan_scratch.p, s);
-        // per node (node_edge_index.cu:644-684)
+        // per node (node_edge_index.cu:644-684): outbound forward + backward,
+        // inbound backward (directed)
         out.w_fwd.resize(out.n_groups);
         out.w_bwd.resize(out.n_groups);
-        hipLaunchKernelGGL(node_weights_kernel, dim3(grid_for(v)), dim3(kB), 0, s, out.cnt.p,
-                           out.grp.p, out.first_ts.p, v, bound, 1, out.w_fwd.p, out.w_bwd.p);
+        node_weights(*this, out, v, bound, true, hs);
         if (cfg.is_directed) {
             in.w_bwd.resize(in.n_groups);
-            hipLaunchKernelGGL(node_weights_kernel, dim3(grid_for(v)), dim3(kB), 0, s, in.cnt.p,
-                               in.grp.p, in.first_ts.p, v, bound, 0, nullptr, in.w_bwd.p);
+            node_weights(*this, in, v, bound, false, hs);
         }
         check_hip(hipGetLastError(), "weights launch");
         weights_ready = true;

@@ -56,7 +56,18 @@ def _assert_index_equal(og, eng, weights=False, tn2v=False):
             a, b = og.array(name), eng.array(name)
             assert a.shape == b.shape, name
             np.testing.assert_allclose(b, a, rtol=1e-12, atol=0, err_msg=name)
-            # cumulative arrays must stay monotone within every node
+        # per-node cumulative arrays must be non-decreasing inside every node
+        for name, cnt_name in [
+                ("outbound_forward_cumulative_weights_exponential", "count_ts_group_per_node_outbound"),
+                ("outbound_backward_cumulative_weights_exponential", "count_ts_group_per_node_outbound"),
+                ("inbound_backward_cumulative_weights_exponential", "count_ts_group_per_node_inbound")]:
+            w, cnt = eng.array(name), eng.array(cnt_name)
+            if w.size == 0:
+                continue
+            same_node = np.ones(w.size, bool)
+            same_node[cnt[(cnt > 0) & (cnt < w.size)].astype(np.int64)] = False
+            same_node[0] = False
+            assert np.all(np.diff(w)[same_node[1:]] >= 0), name
     if tn2v:
         for name in ADJ_ARRAYS:
             assert np.array_equal(og.array(name), eng.array(name)), name
