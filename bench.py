@@ -95,6 +95,10 @@ def main():
     ap.add_argument("--walk-len", type=int, default=80)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-walks", type=int, default=200_000)
+    ap.add_argument("--host-boundary", action="store_true",
+                    help="also time the reference's host boundary once through the drop-in "
+                         "Python class: numpy edges in (host->device copy included) and "
+                         "numpy walks out (device->host copy included)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run one plain device copy of this many MiB (torch copy_ "
                          "kernel): the reference point that scales the HBM byte counters of "
@@ -225,6 +229,30 @@ def main():
         },
     }
 
+    eng.close()
+    if args.host_boundary:
+        from temporal_random_walk import TemporalRandomWalk
+
+        log("host boundary (PCIe-inclusive) run")
+        trw = TemporalRandomWalk(is_directed=True, use_gpu=True, global_seed=42,
+                                 shuffle_walk_order=False)
+        t0 = time.perf_counter()
+        trw.add_multiple_edges(src, dst, ts)
+        t1 = time.perf_counter()
+        nodes, times, lens, _ = trw.get_random_walks_and_times(
+            max_walk_len=args.walk_len, walk_bias="ExponentialIndex",
+            num_walks_total=args.walks, initial_edge_bias="Uniform")
+        t2 = time.perf_counter()
+        result["host_boundary"] = {
+            "walk_steps_per_s": float(lens.sum()) / (t2 - t1),
+            "index_build_edges_per_s": E / (t1 - t0),
+            "sample_s": t2 - t1,
+            "ingest_s": t1 - t0,
+            "note": "numpy in / numpy out through the pybind11 class; includes H2D of the "
+                    "batch and D2H of all walk arrays into pageable host memory",
+        }
+        del nodes, times, lens, trw
+
     if not args.no_cpu_baseline:
         threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
         log(f"cpu baseline ({threads} threads)")
@@ -233,7 +261,6 @@ def main():
     else:
         result["cpu_baseline"] = None
 
-    eng.close()
     print(json.dumps(result))
 
 

@@ -88,15 +88,24 @@ __global__ void gather_store_kernel(const uint32_t* __restrict__ perm, size_t de
     }
 }
 
+// Grid-stride over kept * dim values (can exceed one dispatch's 32-bit
+// work-item count).
 __global__ void gather_feat_kernel(const uint32_t* __restrict__ perm, size_t del, size_t kept,
                                    size_t dim, const float* __restrict__ of, size_t e_old,
                                    const float* __restrict__ nf, float* __restrict__ f) {
-    const size_t x = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
-    if (x >= kept * dim) return;
-    const size_t j = x / dim, c = x - j * dim;
-    const uint32_t id = perm[del + j];
-    f[x] = id < e_old ? of[static_cast<size_t>(id) * dim + c]
-                      : nf[(static_cast<size_t>(id) - e_old) * dim + c];
+    const size_t total = kept * dim;
+    const size_t stride = static_cast<size_t>(gridDim.x) * kB;
+    for (size_t x = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x; x < total; x += stride) {
+        const size_t j = x / dim, c = x - j * dim;
+        const uint32_t id = perm[del + j];
+        f[x] = id < e_old ? of[static_cast<size_t>(id) * dim + c]
+                          : nf[(static_cast<size_t>(id) - e_old) * dim + c];
+    }
+}
+
+inline unsigned grid_capped(size_t n) {
+    const size_t g = (n + kB - 1) / kB;
+    return static_cast<unsigned>(g == 0 ? 1 : (g > (1u << 20) ? (1u << 20) : g));
 }
 
 __global__ void ts_group_flags_kernel(const int64_t* __restrict__ ts, size_t n,
@@ -623,7 +632,7 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
                        src.p, dst.p, ts.p, e_old, d_src, d_dst, d_ts, src2.p, dst2.p, ts2.p);
     if (feat_dim > 0) {
         feat2.resize(kept * feat_dim);
-        hipLaunchKernelGGL(gather_feat_kernel, dim3(grid_for(kept * feat_dim)), dim3(kB), 0, s,
+        hipLaunchKernelGGL(gather_feat_kernel, dim3(grid_capped(kept * feat_dim)), dim3(kB), 0, s,
                            perm, del, kept, feat_dim, feat.p, e_old, d_feat, feat2.p);
         feat.swap(feat2);
     }

@@ -421,14 +421,25 @@ __global__ void u32_from_i32_kernel(const int32_t* __restrict__ a, uint64_t n,
 }
 
 // ---- outputs ----------------------------------------------------------------
+// Grid-stride: slots * dim reaches 1.6e10 at configs[2], beyond the 32-bit
+// work-item count of one dispatch.
 __global__ void gather_walk_features_kernel(const int64_t* __restrict__ eids, uint64_t slots,
                                             uint32_t dim, const float* __restrict__ feat,
                                             float* __restrict__ out) {
-    const uint64_t x = blockIdx.x * static_cast<uint64_t>(kB) + threadIdx.x;
-    if (x >= slots * dim) return;
-    const uint64_t slot = x / dim, c = x - slot * dim;
-    const int64_t e = eids[slot];
-    out[x] = e >= 0 ? feat[static_cast<uint64_t>(e) * dim + c] : 0.0f;
+    const uint64_t total = slots * dim;
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kB;
+    for (uint64_t x = blockIdx.x * static_cast<uint64_t>(kB) + threadIdx.x; x < total;
+         x += stride) {
+        const uint64_t slot = x / dim, c = x - slot * dim;
+        const int64_t e = eids[slot];
+        out[x] = e >= 0 ? feat[static_cast<uint64_t>(e) * dim + c] : 0.0f;
+    }
+}
+
+// Blocks for a grid-stride launch over n items (at most 2^20 blocks).
+inline unsigned grid_capped(uint64_t n) {
+    const uint64_t g = (n + kB - 1) / kB;
+    return static_cast<unsigned>(g == 0 ? 1 : (g > (1u << 20) ? (1u << 20) : g));
 }
 
 // Walk statistics and algorithmic bytes of the walk kernel (trw_get_walk_stats).
@@ -614,7 +625,8 @@ void Engine::sample(const trw_sample_params& p) {
         default:
             throw InvalidArgument("unknown start mode");
     }
-    if (nw > (1ull << 40)) throw InvalidArgument("too many walks");
+    // one lane per walk: a dispatch holds fewer than 2^32 work-items
+    if (nw >= (1ull << 32) - kB) throw InvalidArgument("too many walks (limit 2^32 - 256)");
 
     // ---- optional shuffle of the walk order (same permutation for cutoffs)
     if (have_starts && shuffle && nw > 1) {
@@ -778,7 +790,7 @@ void Engine::sample(const trw_sample_params& p) {
     // ---- edge features of every walk slot (finalize_host_walks, on device)
     if (feat_dim > 0 && eslots) {
         w_feat.resize(eslots * feat_dim);
-        hipLaunchKernelGGL(gather_walk_features_kernel, dim3(grid_for(eslots * feat_dim)), dim3(kB),
+        hipLaunchKernelGGL(gather_walk_features_kernel, dim3(grid_capped(eslots * feat_dim)), dim3(kB),
                            0, s, w_eids.p, eslots, static_cast<uint32_t>(feat_dim), feat.p,
                            w_feat.p);
         check_hip(hipGetLastError(), "feature gather launch");

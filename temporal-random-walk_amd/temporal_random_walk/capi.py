@@ -181,6 +181,27 @@ def lib():
     return _lib
 
 
+_hip = None
+
+
+def device_to_host(dptr, count, dtype, offset_elems=0):
+    """Copy `count` elements of `dtype` starting `offset_elems` into a device
+    buffer returned by trw_sample_device (hipMemcpy, device -> host)."""
+    global _hip
+    if _hip is None:
+        lib()  # the engine pulls in the HIP runtime
+        _hip = C.CDLL("libamdhip64.so")
+        _hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+        _hip.hipMemcpy.restype = C.c_int
+    out = np.empty(int(count), dtype=dtype)
+    if count:
+        src = int(dptr) + int(offset_elems) * out.itemsize
+        rc = _hip.hipMemcpy(out.ctypes.data, src, out.nbytes, 2)  # hipMemcpyDeviceToHost
+        if rc != 0:
+            raise EngineError(f"hipMemcpy failed ({rc})")
+    return out
+
+
 def _check(rc):
     if rc != 0:
         msg = lib().trw_last_error().decode()
@@ -296,10 +317,10 @@ class Engine:
             el = max(L - 1, 0)
 
             def arr(ptr, count, dt):
-                if count == 0:
-                    return np.zeros(0, dtype=dt)
-                buf = (C.c_char * (count * np.dtype(dt).itemsize)).from_address(ptr)
-                return np.frombuffer(bytes(buf), dtype=dt).copy()
+                out = np.empty(count, dtype=dt)
+                if count:
+                    C.memmove(out.ctypes.data, ptr, out.nbytes)
+                return out
 
             nodes = arr(w.nodes, n * L, np.int32).reshape(n, L)
             ts = arr(w.timestamps, n * L, np.int64).reshape(n, L)
