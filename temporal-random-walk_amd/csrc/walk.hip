@@ -101,6 +101,60 @@ __device__ __forceinline__ Hop hop_of(const EdgeRec& r) {
     return Hop{r.nbr, r.ts, static_cast<int64_t>(r.eid)};
 }
 
+__device__ __forceinline__ EdgeRec load_rec(const EdgeRec* p) { return *p; }
+
+// The slot-major walk scratch is written once and read once by the layout
+// pass: non-temporal stores keep it from evicting the node panels from L2.
+template <typename T>
+__device__ __forceinline__ void store_out(T* p, T v) {
+    __builtin_nontemporal_store(v, p);
+}
+
+// First index i in [lo, hi) with f[i] > t (Strict) or f[i] >= t, hi if none,
+// over a sorted panel -- i.e. upper_bound / lower_bound.  The answer is
+// unique, so the way it is found does not change any result.  Long panels
+// (hubs) are first narrowed by up to three interpolation probes between the
+// values known to lie on either side of t -- node timestamps are spread
+// fairly evenly, so this lands within a few slots -- and the rest is a plain
+// binary search, so the worst case stays log2(G) + 5 probes.
+template <bool Strict>
+__device__ __forceinline__ int first_after(const int64_t* f, int lo, int hi, int64_t t) {
+    auto pred = [t](int64_t v) { return Strict ? (v > t) : (v >= t); };
+    if (hi - lo > 16) {
+        const int64_t a0 = f[lo];
+        if (pred(a0)) return lo;
+        const int64_t b0 = f[hi - 1];
+        if (!pred(b0)) return hi;
+        // answer in [l, h]; f[l - 1] = a is on the false side, f[h] = b on the true side
+        int l = lo + 1, h = hi - 1;
+        double a = static_cast<double>(a0), b = static_cast<double>(b0);
+        const double td = static_cast<double>(t);
+#pragma unroll 1
+        for (int round = 0; round < 3 && h - l > 8; ++round) {
+            double frac = (td - a) / (b - a);
+            frac = frac < 0.0 ? 0.0 : (frac > 1.0 ? 1.0 : frac);
+            int p = (l - 1) + static_cast<int>(frac * static_cast<double>(h - l + 1));
+            p = p < l ? l : (p > h - 1 ? h - 1 : p);
+            const int64_t v = f[p];
+            if (pred(v)) {
+                h = p;
+                b = static_cast<double>(v);
+            } else {
+                l = p + 1;
+                a = static_cast<double>(v);
+            }
+        }
+        lo = l;
+        hi = h;  // f[h] is true: search [l, h)
+    }
+    while (lo < hi) {
+        const int mid = lo + ((hi - lo) >> 1);
+        if (pred(f[mid])) hi = mid;
+        else lo = mid + 1;
+    }
+    return lo;
+}
+
 __device__ __forceinline__ Sel edge_of(const WalkGraph& g, uint32_t e) {
     return Sel{g.src[e], g.dst[e], g.ts[e], static_cast<int64_t>(e)};
 }
@@ -166,7 +220,7 @@ __device__ Hop tn2v_pick(const WalkGraph& g, int prev, uint32_t vb, uint32_t ve,
         if (es >= ee) continue;
         const uint64_t local = static_cast<uint64_t>(er * static_cast<double>(ee - es));
         const uint32_t pick = es + static_cast<uint32_t>(local < ee - es ? local : ee - es - 1);
-        const EdgeRec r = g.d.rec[pick];
+        const EdgeRec r = load_rec(g.d.rec + pick);
         const int cand = r.nbr;
         const double beta = (cand == prev) ? g.inv_p : (adjacent(g, prev, cand) ? 1.0 : g.inv_q);
         last = hop_of(r);
@@ -190,32 +244,10 @@ __device__ Hop node_edge_at(const WalkGraph& g, int picker, int node, int64_t t,
     int vb = 0, ve = G;
     if (!(t == -1 && cutoff == kNoCutoff)) {
         if (t != -1) {
-            int lo = 0, hi = G;
-            if (Fwd) {
-                while (lo < hi) {
-                    const int mid = lo + ((hi - lo) >> 1);
-                    if (t < fts[mid]) hi = mid;
-                    else lo = mid + 1;
-                }
-                vb = lo;
-            } else {
-                while (lo < hi) {
-                    const int mid = lo + ((hi - lo) >> 1);
-                    if (fts[mid] < t) lo = mid + 1;
-                    else hi = mid;
-                }
-                ve = lo;
-            }
+            if (Fwd) vb = first_after<true>(fts, 0, G, t);   // upper_bound
+            else ve = first_after<false>(fts, 0, G, t);      // lower_bound
         }
-        if (cutoff != kNoCutoff) {
-            int lo = vb, hi = ve;
-            while (lo < hi) {
-                const int mid = lo + ((hi - lo) >> 1);
-                if (fts[mid] < cutoff) lo = mid + 1;
-                else hi = mid;
-            }
-            ve = lo;
-        }
+        if (cutoff != kNoCutoff) ve = first_after<false>(fts, vb, ve, cutoff);
     }
     if (vb >= ve) return no_hop();
     uint32_t gpos;
@@ -238,8 +270,8 @@ __device__ Hop node_edge_at(const WalkGraph& g, int picker, int node, int64_t t,
     if (gpos >= ge) return no_hop();
     const uint32_t es = g.d.grp[gpos], ee = g.d.grp[gpos + 1];
     if (es >= ee || es >= g.d.idx_size || ee > g.d.idx_size) return no_hop();
-    return hop_of(
-        g.d.rec[es + static_cast<uint32_t>(static_cast<int>(re * static_cast<int>(ee - es)))]);
+    return hop_of(load_rec(
+        g.d.rec + es + static_cast<uint32_t>(static_cast<int>(re * static_cast<int>(ee - es)))));
 }
 
 template <bool Fwd, bool Dir, int Fam>
@@ -295,14 +327,14 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
     int len = 0;
     if (cur_e != -1) {
         int prev = -1;
-        wn[0] = first;
-        wt[0] = Fwd ? INT64_MIN : INT64_MAX;
+        store_out(wn, first);
+        store_out(wt, static_cast<int64_t>(Fwd ? INT64_MIN : INT64_MAX));
         len = 1;
         int walk_len = 1;
         while (walk_len < L && cur != a.pad) {
-            wn[len * n] = cur;
-            wt[len * n] = cur_t;
-            we[(len - 1) * n] = cur_e;
+            store_out(wn + len * n, cur);
+            store_out(wt + len * n, cur_t);
+            store_out(we + (len - 1) * n, cur_e);
             ++len;
             // The reference draws and selects once more after the last slot is
             // written; that selection cannot change the output, so it is skipped.
