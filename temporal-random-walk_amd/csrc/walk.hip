@@ -358,6 +358,10 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
 // slots at or beyond it become `pad` (data/walk_set/walk_set_host.cu:25-29).
 // Backward walks come out reversed into chronological order
 // (data/walk_set/walk_set_view.cuh:50-80).
+//
+// A workgroup owns 64 consecutive walks x 64 slots.  Reads are 64-walk runs of
+// one slot (coalesced); each thread issues its 16 loads back to back so they
+// are in flight together; writes are runs of up to 64 slots of one walk row.
 template <typename T, int CountOffset>
 __global__ __launch_bounds__(256) void transpose_walks_kernel(const T* __restrict__ in,
                                                               T* __restrict__ out,
@@ -368,6 +372,7 @@ __global__ __launch_bounds__(256) void transpose_walks_kernel(const T* __restric
     __shared__ int cnt[64];
     const uint64_t w0 = static_cast<uint64_t>(blockIdx.x) * 64;
     const int k0 = blockIdx.y * 64;
+    const int kc = min(64, K - k0);  // slots in this chunk
     const int tid = threadIdx.x;
     if (tid < 64) {
         const uint64_t w = w0 + tid;
@@ -375,24 +380,32 @@ __global__ __launch_bounds__(256) void transpose_walks_kernel(const T* __restric
         cnt[tid] = c > 0 ? c : 0;
     }
     __syncthreads();
-    for (int idx = tid; idx < 64 * 64; idx += 256) {
-        const int i = idx >> 6, wl = idx & 63;  // slot in chunk, walk in tile
-        const uint64_t w = w0 + wl;
-        const int k = k0 + i;
-        T v = pad;
-        if (w < n && k < K && k < cnt[wl]) {
-            const int src = reverse ? cnt[wl] - 1 - k : k;
-            v = in[static_cast<uint64_t>(src) * n + w];
+    const int wl = tid & 63, srow = tid >> 6;
+    const uint64_t w = w0 + wl;
+    const int c = cnt[wl];
+    T v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int k = k0 + srow + 4 * j;
+        v[j] = pad;
+        if (w < n && k < c) {
+            const int src = reverse ? c - 1 - k : k;
+            v[j] = in[static_cast<uint64_t>(src) * n + w];
         }
-        tile[i][wl] = v;
     }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) tile[srow + 4 * j][wl] = v[j];
     __syncthreads();
-    for (int idx = tid; idx < 64 * 64; idx += 256) {
-        const int wl = idx >> 6, i = idx & 63;
-        const uint64_t w = w0 + wl;
-        const int k = k0 + i;
-        if (w < n && k < K) out[w * K + k] = tile[i][wl];
+    for (int idx = tid; idx < kc * 64; idx += 256) {
+        const int wl2 = idx / kc, i = idx - wl2 * kc;
+        const uint64_t w2 = w0 + wl2;
+        if (w2 < n) out[w2 * K + k0 + i] = tile[i][wl2];
     }
+}
+
+template <typename T>
+constexpr int transpose_chunk() {
+    return 64;
 }
 
 // ---- start arrays ----------------------------------------------------------
@@ -806,15 +819,17 @@ void Engine::sample(const trw_sample_params& p) {
     if (nw && L > 0) {
         const unsigned gx = static_cast<unsigned>((nw + 63) / 64);
         const int rev = forward ? 0 : 1;
-        hipLaunchKernelGGL((transpose_walks_kernel<int32_t, 0>), dim3(gx, (L + 63) / 64), dim3(256),
-                           0, s, sw_nodes.p, w_nodes.p, w_lens.p, nw, L, rev,
+        constexpr int c32 = transpose_chunk<int32_t>(), c64 = transpose_chunk<int64_t>();
+        hipLaunchKernelGGL((transpose_walks_kernel<int32_t, 0>), dim3(gx, (L + c32 - 1) / c32),
+                           dim3(256), 0, s, sw_nodes.p, w_nodes.p, w_lens.p, nw, L, rev,
                            static_cast<int32_t>(cfg.walk_padding_value));
-        hipLaunchKernelGGL((transpose_walks_kernel<int64_t, 0>), dim3(gx, (L + 63) / 64), dim3(256),
-                           0, s, sw_ts.p, w_ts.p, w_lens.p, nw, L, rev, static_cast<int64_t>(-1));
+        hipLaunchKernelGGL((transpose_walks_kernel<int64_t, 0>), dim3(gx, (L + c64 - 1) / c64),
+                           dim3(256), 0, s, sw_ts.p, w_ts.p, w_lens.p, nw, L, rev,
+                           static_cast<int64_t>(-1));
         if (L > 1) {
-            hipLaunchKernelGGL((transpose_walks_kernel<int64_t, -1>), dim3(gx, (L - 1 + 63) / 64),
-                               dim3(256), 0, s, sw_eids.p, w_eids.p, w_lens.p, nw, L - 1, rev,
-                               static_cast<int64_t>(-1));
+            hipLaunchKernelGGL((transpose_walks_kernel<int64_t, -1>),
+                               dim3(gx, (L - 1 + c64 - 1) / c64), dim3(256), 0, s, sw_eids.p,
+                               w_eids.p, w_lens.p, nw, L - 1, rev, static_cast<int64_t>(-1));
         }
         check_hip(hipGetLastError(), "transpose launch");
     }
