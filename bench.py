@@ -243,15 +243,31 @@ def main():
             max_walk_len=args.walk_len, walk_bias="ExponentialIndex",
             num_walks_total=args.walks, initial_edge_bias="Uniform")
         t2 = time.perf_counter()
+        steps = float(lens.sum())
+        del nodes, times, lens, trw
+        # the same call through the C ABI, for the handoff's own timing
+        heng = capi.Engine(is_directed=True, global_seed=42, shuffle_walk_order=False)
+        heng.add_edges(src, dst, ts)
+        t3 = time.perf_counter()
+        hw = heng.sample("total", args.walk_len, "ExponentialIndex", args.walks,
+                         initial_edge_bias="Uniform", direction="Forward_In_Time")
+        t4 = time.perf_counter()
+        ht = heng.timings()
+        del hw
+        heng.close()
         result["host_boundary"] = {
-            "walk_steps_per_s": float(lens.sum()) / (t2 - t1),
+            "walk_steps_per_s": steps / (t2 - t1),
             "index_build_edges_per_s": E / (t1 - t0),
             "sample_s": t2 - t1,
             "ingest_s": t1 - t0,
+            "capi_sample_s": t4 - t3,
+            "handoff_ms": ht["handoff_ms"],
+            "handoff_bytes": ht["handoff_bytes"],
+            "handoff_GB_per_s": ht["handoff_bytes"] / (ht["handoff_ms"] * 1e6),
             "note": "numpy in / numpy out through the pybind11 class; includes H2D of the "
-                    "batch and D2H of all walk arrays into pageable host memory",
+                    "batch and D2H of all walk arrays into caller-owned host memory; "
+                    "handoff_* is trw_sample's device->host delivery alone",
         }
-        del nodes, times, lens, trw
 
     if not args.no_cpu_baseline:
         threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TRW_ABI_VERSION 1
+#define TRW_ABI_VERSION 2
 
 typedef enum trw_status {
     TRW_OK = 0,
@@ -126,6 +126,9 @@ typedef struct trw_timings {
     double sample_ms;      /* whole device-side sample of the last sample call */
     double walk_kernel_ms; /* the walk kernel(s) inside it */
     uint64_t walk_kernel_launches;
+    double handoff_ms;     /* host wall time of trw_sample's copy into host
+                              arrays (allocation, PCIe and host copy) */
+    uint64_t handoff_bytes; /* bytes that copy delivered */
 } trw_timings;
 
 /* Array ids for trw_get_array.  Values are widened to the reference's

@@ -43,7 +43,7 @@ HIP_FLAGS = [
     f"-I{INCLUDE}",
 ]
 
-HIP_SOURCES = ["primitives.hip", "build.hip", "walk.hip", "capi.hip"]
+HIP_SOURCES = ["primitives.hip", "build.hip", "walk.hip", "handoff.hip", "capi.hip"]
 
 
 def _run(cmd):
@@ -64,11 +64,11 @@ def build_engine() -> str:
         _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
         return obj
 
-    with ThreadPoolExecutor(max_workers=min(4, len(HIP_SOURCES))) as ex:
+    with ThreadPoolExecutor(max_workers=min(5, len(HIP_SOURCES))) as ex:
         objs = list(ex.map(compile_one, HIP_SOURCES))
     lib = os.path.join(OUT_DIR, "libtrw_engine.so")
     tmp = lib + ".tmp"
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp])
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-pthread", *objs, "-o", tmp])
     os.replace(tmp, lib)
     return lib
 

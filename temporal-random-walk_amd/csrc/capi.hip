@@ -7,6 +7,7 @@
 #include <stdlib.h>
 
 #include <new>
+#include <type_traits>
 #include <string>
 #include <vector>
 
@@ -206,20 +207,27 @@ trw_status trw_sample(void* handle, const trw_sample_params* params, trw_walks* 
         trw_walks r{};
         r.num_walks = nw;
         r.max_walk_len = e.w_len;
-        r.nodes = host_alloc<int32_t>(nw * L);
-        r.timestamps = host_alloc<int64_t>(nw * L);
-        r.walk_lens = host_alloc<uint64_t>(nw);
-        r.edge_ids = host_alloc<int64_t>(nw * el);
-        d2h(r.nodes, e.w_nodes.p, nw * L, s);
-        d2h(r.timestamps, e.w_ts.p, nw * L, s);
-        d2h(r.walk_lens, e.w_lens.p, nw, s);
-        d2h(r.edge_ids, e.w_eids.p, nw * el, s);
-        if (e.w_feat.n) {
-            r.feature_dim = static_cast<int32_t>(e.feat_dim);
-            r.edge_features = host_alloc<float>(e.w_feat.n);
-            d2h(r.edge_features, e.w_feat.p, e.w_feat.n, s);
+        std::vector<trw::HostCopy> segs;
+        // caller-owned (free()); a failure below releases what was taken
+        auto take = [&](auto*& field, const auto* dsrc, size_t n) {
+            using T = std::remove_pointer_t<std::remove_reference_t<decltype(field)>>;
+            field = static_cast<T*>(trw::host_output_alloc(n * sizeof(T)));
+            segs.push_back({field, dsrc, n * sizeof(T)});
+        };
+        try {
+            take(r.nodes, e.w_nodes.p, nw * L);
+            take(r.timestamps, e.w_ts.p, nw * L);
+            take(r.walk_lens, e.w_lens.p, nw);
+            take(r.edge_ids, e.w_eids.p, nw * el);
+            if (e.w_feat.n) {
+                r.feature_dim = static_cast<int32_t>(e.feat_dim);
+                take(r.edge_features, e.w_feat.p, e.w_feat.n);
+            }
+            e.copy_to_host(segs.data(), segs.size());
+        } catch (...) {
+            trw_walks_free(&r);
+            throw;
         }
-        e.sync();
         *out = r;
     });
 }

@@ -27,6 +27,7 @@
 #include <stdint.h>
 
 #include <cstring>
+#include <memory>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -109,6 +110,29 @@ struct DirIndex {
     }
 };
 
+// One device -> host span of a handoff.
+struct HostCopy {
+    void* dst;
+    const void* src;
+    size_t bytes;
+};
+
+// Per-thread resources of the host handoff: a stream and two pinned staging
+// buffers (double buffering), created on first use.
+struct HostLane {
+    hipStream_t stream = nullptr;
+    void* stage[2] = {nullptr, nullptr};
+    hipEvent_t done[2] = {nullptr, nullptr};
+    HostLane() = default;
+    HostLane(const HostLane&) = delete;
+    HostLane& operator=(const HostLane&) = delete;
+    ~HostLane();
+    void init();
+};
+
+// Caller-owned host output buffer (released with free()).
+void* host_output_alloc(size_t bytes);
+
 struct Engine {
     trw_config cfg{};
     int device = 0;
@@ -178,6 +202,9 @@ struct Engine {
     // pinned host scalars for the few readbacks that size allocations
     void* host_scalars = nullptr;
 
+    // host handoff lanes
+    std::vector<std::unique_ptr<HostLane>> lanes;
+
     // timings
     hipEvent_t ev[8] = {};
     trw_timings timings{};
@@ -196,6 +223,10 @@ struct Engine {
     void sample(const trw_sample_params& p);
 
     size_t memory_used() const;
+
+    // Waits for the engine stream, then copies every span to the host
+    // (pinned staging, several threads); records timings.handoff_*.
+    void copy_to_host(const HostCopy* segs, size_t nseg);
 };
 
 // ---- launchers implemented in build.hip / walk.hip -------------------------

@@ -123,6 +123,8 @@ class TrwTimings(C.Structure):
         ("sample_ms", C.c_double),
         ("walk_kernel_ms", C.c_double),
         ("walk_kernel_launches", C.c_uint64),
+        ("handoff_ms", C.c_double),
+        ("handoff_bytes", C.c_uint64),
     ]
 
 
@@ -135,6 +137,7 @@ class TrwWalkStats(C.Structure):
     ]
 
 
+ABI_VERSION = 2  # TRW_ABI_VERSION of include/trw_engine.h
 _lib = None
 
 
@@ -177,8 +180,41 @@ def lib():
         L.trw_get_timings.argtypes = [P, C.POINTER(TrwTimings)]
         L.trw_get_stream.argtypes = [P, C.POINTER(C.c_void_p)]
         L.trw_get_walk_stats.argtypes = [P, C.POINTER(TrwWalkStats)]
+        if L.trw_abi_version() != ABI_VERSION:
+            raise ImportError(f"{LIB_PATH} has ABI {L.trw_abi_version()}, these bindings "
+                              f"expect {ABI_VERSION}: rebuild the HIP engine")
         _lib = L
     return _lib
+
+
+_free = None
+
+
+class _HostBuffer:
+    """Owner of one malloc'd host result array (caller-owned per the C ABI)."""
+
+    def __init__(self, ptr, shape, dtype):
+        self.ptr = ptr
+        self.__array_interface__ = {"shape": tuple(int(x) for x in shape),
+                                    "typestr": np.dtype(dtype).str,
+                                    "data": (int(ptr or 0), False), "version": 3}
+
+    def __del__(self):
+        if self.ptr:
+            _free(self.ptr)
+            self.ptr = None
+
+
+def _adopt(ptr, shape, dtype):
+    global _free
+    if _free is None:
+        f = C.CDLL(None).free
+        f.argtypes = [C.c_void_p]
+        f.restype = None
+        _free = f
+    if not ptr:
+        return np.zeros(shape, dtype=dtype)
+    return np.asarray(_HostBuffer(ptr, shape, dtype))
 
 
 _hip = None
@@ -312,27 +348,17 @@ class Engine:
         p, keep = self._params(mode, max_walk_len, walk_bias, num_walks, **kw)
         w = TrwWalks()
         _check(self._L.trw_sample(self.h, C.byref(p), C.byref(w)))
-        try:
-            n, L = int(w.num_walks), int(w.max_walk_len)
-            el = max(L - 1, 0)
-
-            def arr(ptr, count, dt):
-                out = np.empty(count, dtype=dt)
-                if count:
-                    C.memmove(out.ctypes.data, ptr, out.nbytes)
-                return out
-
-            nodes = arr(w.nodes, n * L, np.int32).reshape(n, L)
-            ts = arr(w.timestamps, n * L, np.int64).reshape(n, L)
-            lens = arr(w.walk_lens, n, np.uint64)
-            eids = arr(w.edge_ids, n * el, np.int64).reshape(n, el)
-            feats = None
-            if w.feature_dim > 0 and w.edge_features:
-                d = int(w.feature_dim)
-                feats = arr(w.edge_features, n * el * d, np.float32).reshape(n, el, d)
-            return Walks(nodes, ts, lens, eids, feats)
-        finally:
-            self._L.trw_walks_free(C.byref(w))
+        n, L = int(w.num_walks), int(w.max_walk_len)
+        el = max(L - 1, 0)
+        d = int(w.feature_dim) if w.edge_features else 0
+        # each array adopts its malloc'd buffer (no copy); free() runs when
+        # the last view of it goes away
+        nodes = _adopt(w.nodes, (n, L), np.int32)
+        ts = _adopt(w.timestamps, (n, L), np.int64)
+        lens = _adopt(w.walk_lens, (n,), np.uint64)
+        eids = _adopt(w.edge_ids, (n, el), np.int64)
+        feats = _adopt(w.edge_features, (n, el, d), np.float32) if d else None
+        return Walks(nodes, ts, lens, eids, feats)
 
     def sample_device(self, mode, max_walk_len, walk_bias, num_walks=0, **kw):
         """Walks stay in HBM; returns the TrwWalks with device pointers."""

@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
     missing = [n for n in _declared_functions() if not hasattr(lib, n)]
     assert not missing, f"declared but not exported: {missing}"
     assert sorted(capi.EXPORTS) == _declared_functions()
-    assert capi.lib().trw_abi_version() == 1
+    assert capi.lib().trw_abi_version() == capi.ABI_VERSION == 2
 
 
 def test_library_carries_gfx950_code():
@@ -68,3 +68,30 @@ def test_no_gpu_fails_loudly():
         trw.TemporalRandomWalk(is_directed=True, use_gpu=False)
     with pytest.raises(capi.EngineError, match="no HIP device"):
         capi.Engine(is_directed=True)
+
+
+def test_host_results_are_adopted_and_freed():
+    """trw_sample's arrays are malloc'd and caller-owned: the Python binding
+    wraps them without a copy and free()s each when its last view dies."""
+    import gc
+
+    import numpy as np
+
+    from temporal_random_walk import capi
+
+    libc = ctypes.CDLL(None)
+    libc.malloc.restype = ctypes.c_void_p
+    libc.malloc.argtypes = [ctypes.c_size_t]
+    ptr = libc.malloc(6 * 8)
+    ctypes.memmove(ptr, np.arange(6, dtype=np.int64).ctypes.data, 48)
+    a = capi._adopt(ptr, (2, 3), np.int64)
+    assert a.ctypes.data == ptr and a.shape == (2, 3)
+    np.testing.assert_array_equal(a, np.arange(6).reshape(2, 3))
+    view = a[1]
+    del a
+    gc.collect()
+    np.testing.assert_array_equal(view, [3, 4, 5])  # still owned through the view
+    del view
+    gc.collect()
+    empty = capi._adopt(None, (0, 4), np.int32)
+    assert empty.shape == (0, 4)

@@ -207,3 +207,35 @@ def test_normal_mode_invariants_and_features():
         assert np.all(w.nodes[i, n:] == -1) and np.all(w.edge_ids[i, n - 1:] == -1)
         np.testing.assert_array_equal(w.edge_features[i, :n - 1], store_f[e])
         assert np.all(w.edge_features[i, n - 1:] == 0)
+
+
+def test_host_handoff_matches_device_buffers():
+    """trw_sample's staged, multi-threaded host delivery (used above 32 MiB)
+    returns exactly the bytes trw_sample_device leaves in HBM; a fixed
+    global seed makes the two calls sample the same walks."""
+    from temporal_random_walk import capi
+
+    s, d, t = graphs.cfg1(n_nodes=10_000, n_edges=100_000, seed=9)
+    rng = np.random.default_rng(9)
+    feat = rng.standard_normal((len(s), 3)).astype(np.float32)
+    eng = capi.Engine(is_directed=True, global_seed=77, shuffle_walk_order=False)
+    eng.add_edges(s, d, t, feat)
+    L, n = 40, 100_000
+    host = eng.sample("total", L, "ExponentialIndex", n, initial_edge_bias="Uniform")
+    tm = eng.timings()
+    expect_bytes = n * L * (4 + 8) + n * 8 + n * (L - 1) * (8 + 3 * 4)
+    assert tm["handoff_bytes"] == expect_bytes > (32 << 20)
+    dev = eng.sample_device("total", L, "ExponentialIndex", n, initial_edge_bias="Uniform")
+    assert int(dev.num_walks) == n and int(dev.feature_dim) == 3
+    np.testing.assert_array_equal(capi.device_to_host(dev.nodes, n * L, np.int32),
+                                  host.nodes.ravel())
+    np.testing.assert_array_equal(capi.device_to_host(dev.timestamps, n * L, np.int64),
+                                  host.timestamps.ravel())
+    np.testing.assert_array_equal(capi.device_to_host(dev.walk_lens, n, np.uint64), host.lens)
+    np.testing.assert_array_equal(capi.device_to_host(dev.edge_ids, n * (L - 1), np.int64),
+                                  host.edge_ids.ravel())
+    np.testing.assert_array_equal(
+        capi.device_to_host(dev.edge_features, n * (L - 1) * 3, np.float32),
+        host.edge_features.ravel())
+    assert host.lens.sum() > n  # non-trivial walks
+    eng.close()
