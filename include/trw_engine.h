@@ -233,11 +233,13 @@ trw_status trw_get_timings(void* handle, trw_timings* out);
 trw_status trw_get_stream(void* handle, void** out_stream);
 /* Statistics of the last sample, computed on the device after the fact (not
  * part of any timing).  algorithmic_bytes is the compulsory traffic of the
- * walk kernel: per walk 40 B (start-edge reads + length); 12 B for slot 0 and
- * 20 B for slot 1 when written; per hop selected at node u
- * 72 + 8*ceil(log2(G_u + 1)) B (G_u = u's timestamp groups in the sampled
- * direction; the 72 include that hop's 20 B of output).  Padding is written
- * by the layout pass, not the walk kernel. */
+ * walk kernel: per walk 24 B (start-edge reads + length); 8 B for slot 0 and
+ * 12 B for slot 1 when written (node, timestamp rank, 32-bit edge id); per hop
+ * selected at node u 36 + 4*ceil(log2(G_u + 1)) B (G_u = u's timestamp groups
+ * in the sampled direction: the node's group range 8 B, one 4 B rank per
+ * binary-search probe, the picked group's range 8 B, the edge record 8 B and
+ * that hop's 12 B of output).  Padding and the int64 widening are the layout
+ * pass's, not the walk kernel's. */
 typedef struct trw_walk_stats {
     uint64_t total_len;         /* sum of walk_lens: walk steps (reference metric) */
     uint64_t transitions;       /* sum of max(len - 1, 0) */

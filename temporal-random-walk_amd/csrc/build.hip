@@ -118,14 +118,30 @@ __global__ void ts_group_flags_kernel(const int64_t* __restrict__ ts, size_t n,
 __global__ void ts_group_scatter_kernel(const int64_t* __restrict__ ts, size_t n,
                                         const uint32_t* __restrict__ flags,
                                         const uint32_t* __restrict__ scan,
-                                        uint32_t* __restrict__ off, int64_t* __restrict__ uq) {
+                                        uint32_t* __restrict__ off, int64_t* __restrict__ uq,
+                                        uint32_t* __restrict__ erank) {
     const size_t i = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
     if (i >= n) return;
+    // exclusive scan of the group-start flags: the group index of position i
+    erank[i] = scan[i] + flags[i] - 1u;
     if (flags[i]) {
         off[scan[i]] = static_cast<uint32_t>(i);
         uq[scan[i]] = ts[i];
     }
     if (i == n - 1) off[scan[n]] = static_cast<uint32_t>(n);
+}
+
+// Rank of timestamp -1 among the unique timestamps, or -2 when no edge has it:
+// the walk compares ranks with it for the reference's `ts == -1` tests.
+__global__ void neg1_rank_kernel(const int64_t* __restrict__ uq, uint32_t T,
+                                 int32_t* __restrict__ out) {
+    uint32_t lo = 0, hi = T;
+    while (lo < hi) {
+        const uint32_t mid = lo + ((hi - lo) >> 1);
+        if (uq[mid] < -1) lo = mid + 1;
+        else hi = mid;
+    }
+    *out = (lo < T && uq[lo] == -1) ? static_cast<int32_t>(lo) : -2;
 }
 
 __global__ void node_keys_kernel(const int32_t* __restrict__ nodes, size_t n,
@@ -175,17 +191,24 @@ __global__ void node_group_flags_kernel(const uint32_t* __restrict__ keys,
 __global__ void node_group_scatter_kernel(const uint32_t* __restrict__ flags,
                                           const uint32_t* __restrict__ scan,
                                           const uint32_t* __restrict__ idx,
-                                          const int64_t* __restrict__ ts, size_t n,
+                                          const int64_t* __restrict__ ts,
+                                          const uint32_t* __restrict__ erank, size_t n,
                                           uint32_t* __restrict__ grp,
-                                          int64_t* __restrict__ first_ts) {
+                                          int64_t* __restrict__ first_ts,
+                                          PanelRec* __restrict__ pan) {
     const size_t k = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
     if (k >= n) return;
     if (flags[k]) {
         const uint32_t g = scan[k];
+        const uint32_t e = idx[k];
         grp[g] = static_cast<uint32_t>(k);
-        first_ts[g] = ts[idx[k]];
+        first_ts[g] = ts[e];
+        pan[g] = PanelRec{erank[e], static_cast<uint32_t>(k)};
     }
-    if (k == n - 1) grp[scan[n]] = static_cast<uint32_t>(n);
+    if (k == n - 1) {
+        grp[scan[n]] = static_cast<uint32_t>(n);
+        pan[scan[n]] = PanelRec{0xffffffffu, static_cast<uint32_t>(n)};
+    }
 }
 
 // Walk-order edge records.  mode 0: neighbour = target (out-lists of a
@@ -195,8 +218,7 @@ __global__ void node_group_scatter_kernel(const uint32_t* __restrict__ flags,
 __global__ void make_records_kernel(const uint32_t* __restrict__ keys,
                                     const uint32_t* __restrict__ idx,
                                     const int32_t* __restrict__ src,
-                                    const int32_t* __restrict__ dst,
-                                    const int64_t* __restrict__ ts, size_t n, int mode,
+                                    const int32_t* __restrict__ dst, size_t n, int mode,
                                     EdgeRec* __restrict__ rec) {
     const size_t k = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
     if (k >= n) return;
@@ -205,7 +227,7 @@ __global__ void make_records_kernel(const uint32_t* __restrict__ keys,
     if (mode == 0) nbr = dst[e];
     else if (mode == 1) nbr = src[e];
     else nbr = (src[e] == static_cast<int32_t>(keys[k])) ? dst[e] : src[e];
-    rec[k] = EdgeRec{nbr, e, ts[e]};
+    rec[k] = EdgeRec{nbr, e};
 }
 
 // cnt[u] = number of groups of nodes < u = flag scan at u's first entry.
@@ -215,6 +237,71 @@ __global__ void node_group_counts_kernel(const uint32_t* __restrict__ off,
     const size_t u = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
     if (u >= vc) return;
     cnt[u] = scan[off[u]];
+}
+
+// Bucket shift of a node with G > kTabMin groups whose ranks span `span`:
+// the smallest power-of-two bucket width giving at most G / 4 buckets (about
+// four groups per bucket when the node's timestamps are spread evenly).
+__device__ __forceinline__ uint32_t table_shift(uint32_t G, uint32_t span) {
+    const uint32_t target = G >> 2;
+    uint32_t shift = 0;
+    while ((span >> shift) + 1 > target) ++shift;
+    return shift;
+}
+
+// Entries of every node's bucket table: B + 1 for a node with B buckets,
+// 0 for nodes with at most kTabMin groups.
+__global__ void node_table_sizes_kernel(const uint32_t* __restrict__ cnt,
+                                        const PanelRec* __restrict__ pan, size_t v,
+                                        uint32_t* __restrict__ sizes) {
+    const size_t u = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (u >= v) return;
+    const uint32_t gb = cnt[u], ge = cnt[u + 1];
+    uint32_t size = 0;
+    if (ge - gb > kTabMin) {
+        const uint32_t span = pan[ge - 1].rank - pan[gb].rank;
+        size = (span >> table_shift(ge - gb, span)) + 2;
+    }
+    sizes[u] = size;
+}
+
+__global__ void node_headers_kernel(const uint32_t* __restrict__ cnt,
+                                    const PanelRec* __restrict__ pan,
+                                    const uint32_t* __restrict__ base, size_t vc,
+                                    NodeHdr* __restrict__ hdr) {
+    const size_t u = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (u >= vc) return;
+    const uint32_t gb = cnt[u];
+    NodeHdr h{gb, base[u], 0, 0};
+    if (u + 1 < vc) {
+        const uint32_t ge = cnt[u + 1];
+        if (ge - gb > kTabMin) {
+            h.r0 = pan[gb].rank;
+            h.shift = table_shift(ge - gb, pan[ge - 1].rank - h.r0);
+        }
+    }
+    hdr[u] = h;
+}
+
+// One thread per group: group i of node u (local index) fills the buckets
+// from the one after its predecessor's bucket up to its own; the last group
+// also writes the closing entry G.
+__global__ void node_table_fill_kernel(const uint32_t* __restrict__ key,
+                                       const uint32_t* __restrict__ grp,
+                                       const NodeHdr* __restrict__ hdr,
+                                       const PanelRec* __restrict__ pan, size_t ng,
+                                       uint32_t* __restrict__ tab) {
+    const size_t g = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (g >= ng) return;
+    const uint32_t u = key[grp[g]];
+    const NodeHdr h = hdr[u];
+    const uint32_t G = hdr[u + 1].gb - h.gb;
+    if (G <= kTabMin) return;
+    const uint32_t i = static_cast<uint32_t>(g) - h.gb;
+    const uint32_t bi = (pan[g].rank - h.r0) >> h.shift;
+    const uint32_t from = i == 0 ? 0u : ((pan[g - 1].rank - h.r0) >> h.shift) + 1;
+    for (uint32_t b = from; b <= bi; ++b) tab[h.tab + b] = i;
+    if (i == G - 1) tab[h.tab + bi + 1] = G;
 }
 
 __global__ void active_flags_kernel(const uint32_t* __restrict__ out_off,
@@ -508,7 +595,7 @@ void build_direction(Engine& e, DirIndex& dir, size_t n, int key_bits, size_t vc
     }
     dir.rec.resize(n);
     hipLaunchKernelGGL(make_records_kernel, dim3(grid_for(n)), dim3(kB), 0, s, dir.key.p, dir.idx.p,
-                       e.src.p, e.dst.p, e.ts.p, n, rec_mode, dir.rec.p);
+                       e.src.p, e.dst.p, n, rec_mode, dir.rec.p);
     dir.off.resize(vc);
     hipLaunchKernelGGL(lower_bound_offsets_kernel, dim3(grid_for(vc)), dim3(kB), 0, s, dir.key.p,
                        n, vc, dir.off.p);
@@ -522,15 +609,38 @@ void build_direction(Engine& e, DirIndex& dir, size_t n, int key_bits, size_t vc
     dir.n_groups = g;
     dir.grp.resize(static_cast<size_t>(g) + 1);
     dir.first_ts.resize(g);
+    dir.pan.resize(static_cast<size_t>(g) + 1);
     if (n) {
         hipLaunchKernelGGL(node_group_scatter_kernel, dim3(grid_for(n)), dim3(kB), 0, s,
-                           e.flags.p, e.scan.p, dir.idx.p, e.ts.p, n, dir.grp.p, dir.first_ts.p);
+                           e.flags.p, e.scan.p, dir.idx.p, e.ts.p, e.erank.p, n, dir.grp.p,
+                           dir.first_ts.p, dir.pan.p);
     } else {
         check_hip(hipMemsetAsync(dir.grp.p, 0, 4, s), "grp terminator");
+        check_hip(hipMemsetAsync(dir.pan.p, 0, sizeof(PanelRec), s), "panel terminator");
     }
     dir.cnt.resize(vc);
     hipLaunchKernelGGL(node_group_counts_kernel, dim3(grid_for(vc)), dim3(kB), 0, s, dir.off.p,
                        e.scan.p, vc, dir.cnt.p);
+
+    // walk search headers and bucket tables
+    const size_t v = vc - 1;
+    e.flags.ensure(vc);
+    e.scan.ensure(vc);
+    e.scan_scratch.ensure(scan_scratch_elems(vc));
+    hipLaunchKernelGGL(node_table_sizes_kernel, dim3(grid_for(v)), dim3(kB), 0, s, dir.cnt.p,
+                       dir.pan.p, v, e.flags.p);
+    exclusive_scan_u32(e.flags.p, e.scan.p, v, e.scan_scratch.p, s);
+    dir.hdr.resize(vc);
+    hipLaunchKernelGGL(node_headers_kernel, dim3(grid_for(vc)), dim3(kB), 0, s, dir.cnt.p,
+                       dir.pan.p, e.scan.p, vc, dir.hdr.p);
+    uint32_t tab_n = 0;
+    check_hip(hipMemcpyAsync(host_scratch, e.scan.p + v, 4, hipMemcpyDeviceToHost, s), "read tab");
+    e.sync();
+    std::memcpy(&tab_n, host_scratch, 4);
+    dir.tab.resize(tab_n);
+    if (tab_n && g)
+        hipLaunchKernelGGL(node_table_fill_kernel, dim3(grid_for(g)), dim3(kB), 0, s, dir.key.p,
+                           dir.grp.p, dir.hdr.p, dir.pan.p, static_cast<size_t>(g), dir.tab.p);
     check_hip(hipGetLastError(), "direction index launch");
 }
 
@@ -662,8 +772,10 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
     T = tg;
     tsg_off.resize(T + 1);
     uniq_ts.resize(T);
+    erank.resize(E);
     hipLaunchKernelGGL(ts_group_scatter_kernel, dim3(grid_for(E)), dim3(kB), 0, s, ts.p, E,
-                       flags.p, scan.p, tsg_off.p, uniq_ts.p);
+                       flags.p, scan.p, tsg_off.p, uniq_ts.p, erank.p);
+    update_neg1_rank(*this);
 
     // ---- 6. node index
     const size_t v = static_cast<size_t>(max_node_id) + 1;  // active_node_ids size
@@ -765,13 +877,20 @@ void Engine::clear() {
     T = 0;
     max_node_id = -1;
     store_tmin = store_tmax = 0;
-    src.n = dst.n = ts.n = feat.n = tsg_off.n = uniq_ts.n = active.n = 0;
+    src.n = dst.n = ts.n = feat.n = tsg_off.n = uniq_ts.n = erank.n = neg1_rank.n = active.n = 0;
     fwd_cum.n = bwd_cum.n = adj_off.n = adj_nbr.n = 0;
     weights_ready = adj_ready = false;
     out.clear();
     in.clear();
     last_n = 0;
     last_src.n = last_dst.n = 0;
+}
+
+void update_neg1_rank(Engine& e) {
+    e.neg1_rank.resize(1);
+    hipLaunchKernelGGL(neg1_rank_kernel, dim3(1), dim3(1), 0, e.stream, e.uniq_ts.p,
+                       static_cast<uint32_t>(e.E ? e.T : 0), e.neg1_rank.p);
+    check_hip(hipGetLastError(), "neg1 rank launch");
 }
 
 }  // namespace trw

@@ -8,15 +8,29 @@
 //     src, dst      int32[E]      ts   int64[E]      feat fp32[E*dim]
 //   timestamp groups
 //     tsg_off       uint32[T+1]   uniq_ts int64[T]
+//     erank         uint32[E]     rank of every stored edge's timestamp
 //   node map        active uint8[max_id+1]   (dense flags, as the reference)
 //   per direction (out = by source / both endpoints if undirected, in = by target)
 //     off           uint32[V_c]    CSR offsets, V_c = max_id + 2
 //     idx           uint32[n]      edge ids ordered stably by (node, position)
-//     rec           EdgeRec[n]     (neighbour, edge id, ts) in the same order
+//     rec           EdgeRec[n]     (neighbour, edge id) in the same order
 //     cnt           uint32[V_c]    exclusive prefix of per-node group counts
+//     hdr           NodeHdr[V_c]   the walk's per-node header: first group,
+//                                  bucket table base, first rank, bucket shift
+//     tab           uint32[..]     bucket tables of nodes with > kTabMin groups:
+//                                  bucket b of node u covers the ranks
+//                                  [r0 + (b << shift), r0 + ((b + 1) << shift))
+//                                  and holds the first of u's groups that
+//                                  reaches it; the last entry is G
 //     grp           uint32[g+1]    group starts into idx, plus a terminator
 //     first_ts      int64[g]       timestamp of every node-timestamp group
-//                                  (the binary-search panel: one load/probe)
+//     pan           PanelRec[g+1]  (ts rank, start) of every group, plus a
+//                                  terminator: the walk's search panel; the
+//                                  rank is the group's timestamp's position
+//                                  among the unique timestamps, so it orders
+//                                  exactly as the timestamp does, and the
+//                                  picked group's range usually shares the
+//                                  line of the search's last probe
 //     w_fwd, w_bwd  fp64[g]        per-node cumulative exponential weights
 //   global weights  fwd_cum, bwd_cum fp64[T]
 //   node2vec        adj_off uint32[max_id+2], adj_nbr int32[2E]
@@ -82,12 +96,36 @@ struct DBuf {
 // edge, the edge id and its timestamp -- everything a hop needs from the edge
 // in one aligned 16-byte load (instead of idx -> dst -> ts, three dependent
 // cache-line misses).
-struct alignas(16) EdgeRec {
+// One entry of a node's list as the walk reads it.  Its timestamp is the
+// group's (every entry of a node-timestamp group shares it), carried by the
+// walk as the group's rank.
+struct alignas(8) EdgeRec {
     int32_t nbr;
     uint32_t eid;
-    int64_t ts;
 };
-static_assert(sizeof(EdgeRec) == 16, "EdgeRec must be 16 bytes");
+static_assert(sizeof(EdgeRec) == 8, "EdgeRec must be 8 bytes");
+
+// Nodes with more groups than this get a bucket table for the walk's search;
+// smaller ones are binary-searched directly (at most two panel lines).
+constexpr uint32_t kTabMin = 16;
+
+// Per-node header of the walk's group search.  The next node's header closes
+// the node: its gb is this node's group end and its tab this table's end.
+struct alignas(16) NodeHdr {
+    uint32_t gb;     // first group of the node
+    uint32_t tab;    // first entry of its bucket table
+    uint32_t r0;     // rank of its first group (tabled nodes)
+    uint32_t shift;  // log2 of its bucket width in ranks (tabled nodes)
+};
+static_assert(sizeof(NodeHdr) == 16, "NodeHdr must be 16 bytes");
+
+// One node-timestamp group in the walk's search panel.
+struct alignas(8) PanelRec {
+    uint32_t rank;   // index of the group's timestamp in uniq_ts
+    uint32_t start;  // first entry (position in idx / rec); the next record's
+                     // start ends the group
+};
+static_assert(sizeof(PanelRec) == 8, "PanelRec must be 8 bytes");
 
 struct DirIndex {
     DBuf<uint32_t> off;      // V_c
@@ -97,6 +135,9 @@ struct DirIndex {
     DBuf<uint32_t> cnt;      // V_c
     DBuf<uint32_t> grp;      // g + 1
     DBuf<int64_t> first_ts;  // g
+    DBuf<PanelRec> pan;      // g + 1
+    DBuf<NodeHdr> hdr;       // V_c
+    DBuf<uint32_t> tab;      // bucket tables
     DBuf<double> w_fwd;      // g (outbound only)
     DBuf<double> w_bwd;      // g
     size_t n_entries = 0;
@@ -104,7 +145,8 @@ struct DirIndex {
     bool present = false;
 
     void clear() {
-        off.n = idx.n = rec.n = key.n = cnt.n = grp.n = first_ts.n = w_fwd.n = w_bwd.n = 0;
+        off.n = idx.n = rec.n = key.n = cnt.n = grp.n = first_ts.n = pan.n = hdr.n = tab.n = w_fwd.n =
+            w_bwd.n = 0;
         n_entries = n_groups = 0;
         present = false;
     }
@@ -150,6 +192,8 @@ struct Engine {
     // timestamp groups
     DBuf<uint32_t> tsg_off;
     DBuf<int64_t> uniq_ts;
+    DBuf<uint32_t> erank;
+    DBuf<int32_t> neg1_rank;  // rank of timestamp -1 if stored, else -2
     size_t T = 0;
 
     // node map
@@ -187,10 +231,11 @@ struct Engine {
     DBuf<double> replay;
     DBuf<uint64_t> acc64;
 
-    // walks (device): slot-major scratch written by the walk kernel, then the
-    // row-major output [num_walks, L] the reference's API returns
+    // walks (device): slot-major scratch written by the walk kernel (node,
+    // timestamp rank, 32-bit edge id), then the row-major output
+    // [num_walks, L] in the reference's types
     DBuf<int32_t> sw_nodes;
-    DBuf<int64_t> sw_ts, sw_eids;
+    DBuf<uint32_t> sw_rank, sw_eids;
     DBuf<int32_t> w_nodes;
     DBuf<int64_t> w_ts, w_eids;
     DBuf<uint64_t> w_lens;
@@ -232,5 +277,8 @@ struct Engine {
 // ---- launchers implemented in build.hip / walk.hip -------------------------
 void validate_batch(const Engine& e, const void* feat, size_t n, size_t dim);
 void walk_stats(Engine& e, trw_walk_stats* out);
+// Rank of timestamp -1 among the stored unique timestamps (-2 if absent) into
+// e.neg1_rank, on the engine stream.
+void update_neg1_rank(Engine& e);
 
 }  // namespace trw

@@ -8,12 +8,20 @@
 // draws) lives in registers for the whole walk, so there is no per-step
 // scheduler and no host round trip between steps.
 //
-// Per hop the lane reads the node's group range, binary-searches the
-// node-timestamp group panel first_ts[] (one 8-byte load per probe instead of
-// the reference's three dependent loads ts[idx[grp[p]]]), applies the picker,
-// reads the group's edge range and the chosen edge.  The dominant cost is the
-// dependent-load latency of the search; hub panels stay resident in L2 /
-// Infinity Cache because every walk crossing the hub probes the same keys.
+// Per hop the lane reads the node's group range, searches the node's panel of
+// 8-byte (timestamp rank, start) group records -- one load per probe instead
+// of the reference's three dependent loads ts[idx[grp[p]]] -- applies the
+// picker, and takes the picked group's edge range from the panel: pickers
+// favour groups next to the boundary the search found, so that range is
+// usually on a line the search has just read.  Then it reads the chosen edge
+// record (neighbour, edge id).  Ranks (the timestamp's index among the
+// graph's unique timestamps) order exactly as the timestamps do, so every
+// comparison of the reference is kept; the walk carries the rank of its
+// current time, which is the rank of the group it picked, and writes ranks
+// and 32-bit edge ids to its scratch; the layout pass turns them into the
+// reference's int64 timestamps and edge ids.  The cost is the number of distinct cache lines per
+// hop and their dependent latency; hub panels stay resident in L2 / Infinity
+// Cache because every walk crossing the hub probes the same keys.
 #include <math.h>
 
 #include <algorithm>
@@ -33,10 +41,10 @@ inline unsigned grid_for(size_t n) {
 }
 
 struct DirView {
-    const uint32_t* cnt;
-    const uint32_t* grp;  // g + 1 entries (terminator)
+    const NodeHdr* hdr;   // V_c node headers
+    const uint32_t* tab;  // bucket tables
+    const PanelRec* pan;  // g + 1 group records (terminator)
     const EdgeRec* rec;   // walk-order edge records
-    const int64_t* first_ts;
     uint32_t idx_size;
     const double* w;  // per-node cumulative weights of the sampled direction
     uint64_t w_size;
@@ -54,6 +62,8 @@ struct WalkGraph {
     const int64_t* ts;
     uint32_t E;
     const uint32_t* tsg_off;
+    const int64_t* uniq_ts;
+    const int32_t* neg1_rank;  // rank of timestamp -1, -2 if no edge has it
     uint32_t T;
     const double* gw;  // global cumulative weights of the sampled direction
     uint64_t gw_size;
@@ -77,28 +87,34 @@ struct WalkArgs {
     uint64_t n;
     DrawSource ds;
     int32_t* nodes;
-    int64_t* ts;
+    uint32_t* ranks;
     uint64_t* lens;
-    int64_t* eids;
+    uint32_t* eids;
 };
 
+// Scratch rank of a walk's first slot, whose timestamp is the direction's
+// sentinel (INT64_MIN forward, INT64_MAX backward) rather than an edge time.
+constexpr uint32_t kStartRank = 0xffffffffu;
+
+// A start edge: endpoints, edge id (-1 for none) and the rank of its time.
 struct Sel {
     int32_t u, v;
-    int64_t t;
-    int64_t e;
+    int32_t e;
+    int32_t r;
 };
 
-// Result of a per-node selection: the node reached, the edge time and id.
+// Result of a per-node selection: the node reached, the rank of the edge's
+// time and the edge id (-1 for none).
 struct Hop {
     int32_t nbr;
-    int64_t t;
-    int64_t e;
+    int32_t r;
+    int32_t e;
 };
 
 __device__ __forceinline__ Sel no_edge() { return Sel{-1, -1, -1, -1}; }
 __device__ __forceinline__ Hop no_hop() { return Hop{-1, -1, -1}; }
-__device__ __forceinline__ Hop hop_of(const EdgeRec& r) {
-    return Hop{r.nbr, r.ts, static_cast<int64_t>(r.eid)};
+__device__ __forceinline__ Hop hop_of(const EdgeRec& rec, uint32_t rank) {
+    return Hop{rec.nbr, static_cast<int32_t>(rank), static_cast<int32_t>(rec.eid)};
 }
 
 __device__ __forceinline__ EdgeRec load_rec(const EdgeRec* p) { return *p; }
@@ -110,53 +126,44 @@ __device__ __forceinline__ void store_out(T* p, T v) {
     __builtin_nontemporal_store(v, p);
 }
 
-// First index i in [lo, hi) with f[i] > t (Strict) or f[i] >= t, hi if none,
-// over a sorted panel -- i.e. upper_bound / lower_bound.  The answer is
-// unique, so the way it is found does not change any result.  Long panels
-// (hubs) are first narrowed by up to three interpolation probes between the
-// values known to lie on either side of t -- node timestamps are spread
-// fairly evenly, so this lands within a few slots -- and the rest is a plain
-// binary search, so the worst case stays log2(G) + 5 probes.
-template <bool Strict>
-__device__ __forceinline__ int first_after(const int64_t* f, int lo, int hi, int64_t t) {
-    auto pred = [t](int64_t v) { return Strict ? (v > t) : (v >= t); };
-    if (hi - lo > 16) {
-        const int64_t a0 = f[lo];
-        if (pred(a0)) return lo;
-        const int64_t b0 = f[hi - 1];
-        if (!pred(b0)) return hi;
-        // answer in [l, h]; f[l - 1] = a is on the false side, f[h] = b on the true side
-        int l = lo + 1, h = hi - 1;
-        double a = static_cast<double>(a0), b = static_cast<double>(b0);
-        const double td = static_cast<double>(t);
-#pragma unroll 1
-        for (int round = 0; round < 3 && h - l > 8; ++round) {
-            double frac = (td - a) / (b - a);
-            frac = frac < 0.0 ? 0.0 : (frac > 1.0 ? 1.0 : frac);
-            int p = (l - 1) + static_cast<int>(frac * static_cast<double>(h - l + 1));
-            p = p < l ? l : (p > h - 1 ? h - 1 : p);
-            const int64_t v = f[p];
-            if (pred(v)) {
-                h = p;
-                b = static_cast<double>(v);
-            } else {
-                l = p + 1;
-                a = static_cast<double>(v);
-            }
-        }
-        lo = l;
-        hi = h;  // f[h] is true: search [l, h)
+// First local index i in [0, G) whose group rank is >= x, G if none: a
+// lower_bound over the node's sorted panel, so the answer is unique and the
+// way it is found does not change any result.  A node with more than kTabMin
+// groups first takes the bracket [tab[b], tab[b + 1]] of x's bucket b from
+// its table (about four groups); the rest is a binary search over at most
+// kTabMin groups.
+__device__ __forceinline__ int first_ge(const uint32_t* tab, const NodeHdr& h, uint32_t tab_end,
+                                        const PanelRec* f, int G, uint32_t x) {
+    int lo = 0, hi = G;
+    if (G > static_cast<int>(kTabMin)) {
+        if (x <= h.r0) return 0;
+        const uint32_t b = (x - h.r0) >> h.shift;
+        if (b >= tab_end - h.tab - 1) return G;  // past the last bucket
+        lo = static_cast<int>(tab[h.tab + b]);
+        hi = static_cast<int>(tab[h.tab + b + 1]);
     }
     while (lo < hi) {
         const int mid = lo + ((hi - lo) >> 1);
-        if (pred(f[mid])) hi = mid;
+        if (f[mid].rank >= x) hi = mid;
         else lo = mid + 1;
     }
     return lo;
 }
 
-__device__ __forceinline__ Sel edge_of(const WalkGraph& g, uint32_t e) {
-    return Sel{g.src[e], g.dst[e], g.ts[e], static_cast<int64_t>(e)};
+__device__ __forceinline__ Sel edge_of(const WalkGraph& g, uint32_t e, long group) {
+    return Sel{g.src[e], g.dst[e], static_cast<int32_t>(e), static_cast<int32_t>(group)};
+}
+
+// Number of unique timestamps below t: groups at or past this rank have
+// timestamps >= t.
+__device__ __forceinline__ int32_t rank_lower_bound(const WalkGraph& g, int64_t t) {
+    uint32_t lo = 0, hi = g.T;
+    while (lo < hi) {
+        const uint32_t mid = lo + ((hi - lo) >> 1);
+        if (g.uniq_ts[mid] < t) lo = mid + 1;
+        else hi = mid;
+    }
+    return static_cast<int32_t>(lo);
 }
 
 // Unconstrained start (edge_selectors.cuh:177-275 with timestamp == -1).
@@ -178,7 +185,7 @@ __device__ Sel start_edge(const WalkGraph& g, int picker, double rg, double re) 
     const uint32_t from = g.tsg_off[group], to = g.tsg_off[group + 1];
     if (from == to) return no_edge();
     const uint32_t e = from + static_cast<uint32_t>(static_cast<int>(re * static_cast<int>(to - from)));
-    return edge_of(g, e);
+    return edge_of(g, e, group);
 }
 
 __device__ __forceinline__ bool adjacent(const WalkGraph& g, int prev, int cand) {
@@ -216,14 +223,15 @@ __device__ Hop tn2v_pick(const WalkGraph& g, int prev, uint32_t vb, uint32_t ve,
         // a pick one past the node's last group is an empty range in the
         // reference (get_node_group_edge_end, walk_step_helpers.cuh:19-38)
         if (static_cast<uint32_t>(gp) >= ge) continue;
-        const uint32_t es = g.d.grp[gp], ee = g.d.grp[gp + 1];
+        const PanelRec pr = g.d.pan[gp];
+        const uint32_t es = pr.start, ee = g.d.pan[gp + 1].start;
         if (es >= ee) continue;
         const uint64_t local = static_cast<uint64_t>(er * static_cast<double>(ee - es));
         const uint32_t pick = es + static_cast<uint32_t>(local < ee - es ? local : ee - es - 1);
         const EdgeRec r = load_rec(g.d.rec + pick);
         const int cand = r.nbr;
         const double beta = (cand == prev) ? g.inv_p : (adjacent(g, prev, cand) ? 1.0 : g.inv_q);
-        last = hop_of(r);
+        last = hop_of(r, pr.rank);
         if (ar < beta * inv_bmax) return last;
     }
     return last;
@@ -232,22 +240,30 @@ __device__ Hop tn2v_pick(const WalkGraph& g, int prev, uint32_t vb, uint32_t ve,
 // Per-hop selector (edge_selectors.cuh:277-443).  The reference first checks
 // the dense active flag; an inactive node has no entries in either direction,
 // so the empty group range below rejects it identically without that load.
+// t: rank of the current time, -1 for none (a start, or a current time of
+// -1, which the reference also reads as unconstrained); cut: rank bound of
+// the walk's cutoff time (groups at or past it are excluded), -1 for none.
 template <bool Fwd, int Fam>
-__device__ Hop node_edge_at(const WalkGraph& g, int picker, int node, int64_t t, int64_t cutoff,
+__device__ Hop node_edge_at(const WalkGraph& g, int picker, int node, int32_t t, int32_t cut,
                             int prev, double rg, double re) {
     if (!(node >= 0 && node < g.active_size)) return no_hop();
-    const uint32_t gb = g.d.cnt[node], ge = g.d.cnt[node + 1];
+    const NodeHdr h = g.d.hdr[node];
+    const NodeHdr hn = g.d.hdr[node + 1];
+    const uint32_t gb = h.gb, ge = hn.gb;
     if (gb == ge) return no_hop();
     const int G = static_cast<int>(ge - gb);
-    const int64_t* fts = g.d.first_ts + gb;
+    const PanelRec* fts = g.d.pan + gb;
     // filter_valid_groups_by_timestamp_slice (edge_selectors.cuh:66-120)
     int vb = 0, ve = G;
-    if (!(t == -1 && cutoff == kNoCutoff)) {
-        if (t != -1) {
-            if (Fwd) vb = first_after<true>(fts, 0, G, t);   // upper_bound
-            else ve = first_after<false>(fts, 0, G, t);      // lower_bound
-        }
-        if (cutoff != kNoCutoff) ve = first_after<false>(fts, vb, ve, cutoff);
+    if (t != -1) {
+        const uint32_t x = static_cast<uint32_t>(t);
+        if (Fwd) vb = first_ge(g.d.tab, h, hn.tab, fts, G, x + 1);  // upper_bound
+        else ve = first_ge(g.d.tab, h, hn.tab, fts, G, x);         // lower_bound
+    }
+    if (cut != -1) {
+        // the first group at or past the cutoff, within [vb, ve]
+        const int c = first_ge(g.d.tab, h, hn.tab, fts, G, static_cast<uint32_t>(cut));
+        ve = c < vb ? vb : (c < ve ? c : ve);
     }
     if (vb >= ve) return no_hop();
     uint32_t gpos;
@@ -268,10 +284,12 @@ __device__ Hop node_edge_at(const WalkGraph& g, int picker, int node, int64_t t,
     // A weight pick one past the node's last group reads, in the reference, the
     // next node's first group start for both ends: an empty range.
     if (gpos >= ge) return no_hop();
-    const uint32_t es = g.d.grp[gpos], ee = g.d.grp[gpos + 1];
+    const PanelRec pr = g.d.pan[gpos];
+    const uint32_t es = pr.start, ee = g.d.pan[gpos + 1].start;
     if (es >= ee || es >= g.d.idx_size || ee > g.d.idx_size) return no_hop();
-    return hop_of(load_rec(
-        g.d.rec + es + static_cast<uint32_t>(static_cast<int>(re * static_cast<int>(ee - es)))));
+    return hop_of(load_rec(g.d.rec + es +
+                           static_cast<uint32_t>(static_cast<int>(re * static_cast<int>(ee - es)))),
+                  pr.rank);
 }
 
 template <bool Fwd, bool Dir, int Fam>
@@ -284,22 +302,25 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
         return;
     }
     // Slot-major scratch: slot k of walk w lives at [k * n + w], so the 64
-    // lanes of a wave store 256 B (nodes) / 512 B (ts, edge ids) contiguously
-    // per slot.  transpose_walks_kernel produces the row-major output, the
-    // padding and the chronological order of backward walks.
+    // lanes of a wave store 256 B per slot and array contiguously.
+    // transpose_walks_kernel produces the row-major output in the reference's
+    // types, the padding and the chronological order of backward walks.
     const uint64_t n = a.n;
     int32_t* wn = a.nodes + w;
-    int64_t* wt = a.ts + w;
-    int64_t* we = a.eids + w;
+    uint32_t* wt = a.ranks + w;
+    uint32_t* we = a.eids + w;
     const int start = a.starts ? a.starts[w] : -1;
     const int64_t cutoff = a.cutoffs ? a.cutoffs[w] : kNoCutoff;
+    const int32_t cut = cutoff != kNoCutoff ? rank_lower_bound(g, cutoff) : -1;
+    // the reference's tests of a current time of -1, on ranks
+    const int32_t neg1 = *g.neg1_rank;
 
     const double r0 = draw_slot0(a.ds, w);
     const DrawPair r12 = draw_pair(a.ds, w, 1);
     // Start edge: the first slot holds the walk's origin and `cur` the node
     // reached over the start edge (temporal_random_walk_cpu.cuh:39-90).
     int first = -1, cur = -1;
-    int64_t cur_t = -1, cur_e = -1;
+    int32_t cur_r = -1, cur_e = -1;
     if (start == -1) {
         const Sel se = start_edge<Fwd>(g, a.start_bias, r0, r12.a);
         if (se.v != -1) {
@@ -310,17 +331,17 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
                 first = r12.b >= 0.5 ? se.u : se.v;
                 cur = first == se.u ? se.v : se.u;
             }
-            cur_t = se.t;
+            cur_r = se.r;
             cur_e = se.e;
         }
     } else {
         // a node's own list: the node is the edge's source (out), target (in)
         // or one endpoint (undirected) -- the record's neighbour is the other
-        const Hop h = node_edge_at<Fwd, Fam>(g, a.start_bias, start, -1, cutoff, -1, r0, r12.a);
+        const Hop h = node_edge_at<Fwd, Fam>(g, a.start_bias, start, -1, cut, -1, r0, r12.a);
         if (h.e != -1) {
             first = start;
             cur = h.nbr;
-            cur_t = h.t;
+            cur_r = h.r;
             cur_e = h.e;
         }
     }
@@ -328,23 +349,25 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
     if (cur_e != -1) {
         int prev = -1;
         store_out(wn, first);
-        store_out(wt, static_cast<int64_t>(Fwd ? INT64_MIN : INT64_MAX));
+        store_out(wt, kStartRank);
         len = 1;
         int walk_len = 1;
         while (walk_len < L && cur != a.pad) {
             store_out(wn + len * n, cur);
-            store_out(wt + len * n, cur_t);
-            store_out(we + (len - 1) * n, cur_e);
+            store_out(wt + len * n, static_cast<uint32_t>(cur_r));
+            store_out(we + (len - 1) * n, static_cast<uint32_t>(cur_e));
             ++len;
             // The reference draws and selects once more after the last slot is
             // written; that selection cannot change the output, so it is skipped.
             if (walk_len == L - 1) break;
             const DrawPair r = draw_pair(a.ds, w, static_cast<uint32_t>(walk_len) + 1);
-            const Hop h = node_edge_at<Fwd, Fam>(g, a.walk_bias, cur, cur_t, cutoff, prev, r.a, r.b);
-            if (h.t == -1) break;  // the reference's failure test is ts == -1
+            const Hop h = node_edge_at<Fwd, Fam>(g, a.walk_bias, cur, cur_r == neg1 ? -1 : cur_r,
+                                                 cut, prev, r.a, r.b);
+            // the reference's failure test is ts == -1: no edge, or an edge at -1
+            if (h.e == -1 || h.r == neg1) break;
             prev = cur;
             cur = h.nbr;
-            cur_t = h.t;
+            cur_r = h.r;
             cur_e = h.e;
             ++walk_len;
         }
@@ -353,7 +376,10 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
 }
 
 // Slot-major scratch [K][n] -> row-major output [n][K] for one walk array,
-// 64 walks x 64 slots per workgroup through LDS.  `count` of walk w is the
+// 64 walks x 64 slots per workgroup through LDS, converting each value to the
+// reference's type on the way: Conv 0 copies (nodes), 1 turns a timestamp
+// rank into the timestamp (uniq_ts; kStartRank into the first slot's
+// sentinel), 2 widens a 32-bit edge id.  `count` of walk w is the
 // number of written slots (len for nodes/timestamps, len - 1 for edge ids);
 // slots at or beyond it become `pad` (data/walk_set/walk_set_host.cu:25-29).
 // Backward walks come out reversed into chronological order
@@ -362,12 +388,14 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
 // A workgroup owns 64 consecutive walks x 64 slots.  Reads are 64-walk runs of
 // one slot (coalesced); each thread issues its 16 loads back to back so they
 // are in flight together; writes are runs of up to 64 slots of one walk row.
-template <typename T, int CountOffset>
-__global__ __launch_bounds__(256) void transpose_walks_kernel(const T* __restrict__ in,
+template <typename Tin, typename T, int CountOffset, int Conv>
+__global__ __launch_bounds__(256) void transpose_walks_kernel(const Tin* __restrict__ in,
                                                               T* __restrict__ out,
                                                               const uint64_t* __restrict__ lens,
                                                               uint64_t n, int K, int reverse,
-                                                              T pad) {
+                                                              T pad,
+                                                              const int64_t* __restrict__ uniq_ts,
+                                                              int64_t start_ts) {
     __shared__ T tile[64][65];
     __shared__ int cnt[64];
     const uint64_t w0 = static_cast<uint64_t>(blockIdx.x) * 64;
@@ -390,7 +418,10 @@ __global__ __launch_bounds__(256) void transpose_walks_kernel(const T* __restric
         v[j] = pad;
         if (w < n && k < c) {
             const int src = reverse ? c - 1 - k : k;
-            v[j] = in[static_cast<uint64_t>(src) * n + w];
+            const Tin x = in[static_cast<uint64_t>(src) * n + w];
+            if (Conv == 0) v[j] = static_cast<T>(x);
+            else if (Conv == 2) v[j] = static_cast<T>(static_cast<uint32_t>(x));
+            else v[j] = static_cast<uint32_t>(x) == kStartRank ? start_ts : uniq_ts[x];
         }
     }
 #pragma unroll
@@ -496,15 +527,15 @@ __global__ void walk_stats_kernel(const int32_t* __restrict__ nodes,
     unsigned long long bytes = 0, trans = 0, total = 0, nonempty = 0;
     if (w < n && L > 0) {
         const int len = static_cast<int>(lens[w]);
-        bytes = 40;
-        if (len >= 1) bytes += 12;
-        if (len >= 2) bytes += 20;
+        bytes = 24;
+        if (len >= 1) bytes += 8;
+        if (len >= 2) bytes += 12;
         for (int k = 1; k + 1 < len; ++k) {
             const int u = nodes[w * L + k];
             uint32_t G = 0;
             if (u >= 0 && u < active_size) G = cnt[u + 1] - cnt[u];
             const int probes = G ? 32 - __clz(G) : 0;  // ceil(log2(G + 1))
-            bytes += 72 + 8 * probes;
+            bytes += 36 + 4 * probes;
         }
         trans = len > 0 ? len - 1 : 0;
         total = len;
@@ -732,7 +763,7 @@ void Engine::sample(const trw_sample_params& p) {
     const uint64_t slots = nw * static_cast<uint64_t>(L);
     const uint64_t eslots = nw * static_cast<uint64_t>(L > 0 ? L - 1 : 0);
     sw_nodes.resize(slots);
-    sw_ts.resize(slots);
+    sw_rank.resize(slots);
     sw_eids.resize(eslots);
     w_nodes.resize(slots);
     w_ts.resize(slots);
@@ -751,15 +782,18 @@ void Engine::sample(const trw_sample_params& p) {
     g.ts = ts.p;
     g.E = static_cast<uint32_t>(E);
     g.tsg_off = tsg_off.p;
+    g.uniq_ts = uniq_ts.p;
+    if (neg1_rank.n == 0) update_neg1_rank(*this);  // no build since the last clear
+    g.neg1_rank = neg1_rank.p;
     g.T = static_cast<uint32_t>(T);
     g.gw = forward ? fwd_cum.p : bwd_cum.p;
     g.gw_size = weights_ready ? T : 0;
     g.active = active.p;
     g.active_size = static_cast<int32_t>(active.n);
-    g.d.cnt = d.cnt.p;
-    g.d.grp = d.grp.p;
+    g.d.hdr = d.hdr.p;
+    g.d.tab = d.tab.p;
+    g.d.pan = d.pan.p;
     g.d.rec = d.rec.p;
-    g.d.first_ts = d.first_ts.p;
     g.d.idx_size = static_cast<uint32_t>(d.n_entries);
     if (forward) {
         g.d.w = out.w_fwd.p;
@@ -788,7 +822,7 @@ void Engine::sample(const trw_sample_params& p) {
     a.n = nw;
     a.ds = ds;
     a.nodes = sw_nodes.p;
-    a.ts = sw_ts.p;
+    a.ranks = sw_rank.p;
     a.lens = w_lens.p;
     a.eids = sw_eids.p;
 
@@ -820,16 +854,19 @@ void Engine::sample(const trw_sample_params& p) {
         const unsigned gx = static_cast<unsigned>((nw + 63) / 64);
         const int rev = forward ? 0 : 1;
         constexpr int c32 = transpose_chunk<int32_t>(), c64 = transpose_chunk<int64_t>();
-        hipLaunchKernelGGL((transpose_walks_kernel<int32_t, 0>), dim3(gx, (L + c32 - 1) / c32),
-                           dim3(256), 0, s, sw_nodes.p, w_nodes.p, w_lens.p, nw, L, rev,
-                           static_cast<int32_t>(cfg.walk_padding_value));
-        hipLaunchKernelGGL((transpose_walks_kernel<int64_t, 0>), dim3(gx, (L + c64 - 1) / c64),
-                           dim3(256), 0, s, sw_ts.p, w_ts.p, w_lens.p, nw, L, rev,
-                           static_cast<int64_t>(-1));
+        const int64_t start_ts = forward ? INT64_MIN : INT64_MAX;
+        hipLaunchKernelGGL((transpose_walks_kernel<int32_t, int32_t, 0, 0>),
+                           dim3(gx, (L + c32 - 1) / c32), dim3(256), 0, s, sw_nodes.p, w_nodes.p,
+                           w_lens.p, nw, L, rev, static_cast<int32_t>(cfg.walk_padding_value),
+                           nullptr, start_ts);
+        hipLaunchKernelGGL((transpose_walks_kernel<uint32_t, int64_t, 0, 1>),
+                           dim3(gx, (L + c64 - 1) / c64), dim3(256), 0, s, sw_rank.p, w_ts.p,
+                           w_lens.p, nw, L, rev, static_cast<int64_t>(-1), uniq_ts.p, start_ts);
         if (L > 1) {
-            hipLaunchKernelGGL((transpose_walks_kernel<int64_t, -1>),
+            hipLaunchKernelGGL((transpose_walks_kernel<uint32_t, int64_t, -1, 2>),
                                dim3(gx, (L - 1 + c64 - 1) / c64), dim3(256), 0, s, sw_eids.p,
-                               w_eids.p, w_lens.p, nw, L - 1, rev, static_cast<int64_t>(-1));
+                               w_eids.p, w_lens.p, nw, L - 1, rev, static_cast<int64_t>(-1),
+                               nullptr, start_ts);
         }
         check_hip(hipGetLastError(), "transpose launch");
     }

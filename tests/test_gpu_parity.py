@@ -239,3 +239,37 @@ def test_host_handoff_matches_device_buffers():
         host.edge_features.ravel())
     assert host.lens.sum() > n  # non-trivial walks
     eng.close()
+
+
+@pytest.mark.parametrize("forward", [True, False])
+@pytest.mark.parametrize("picker", ["Uniform", "ExponentialIndex"])
+def test_replay_walks_bursty_hubs_with_cutoffs(forward, picker):
+    """Hubs whose timestamps come in bursts (uneven bucket tables: most
+    buckets empty, a few crowded) with per-walk cutoffs."""
+    rng = np.random.default_rng(21)
+    s, d, _ = graphs.powerlaw(20_000, 300_000, s=1.7, seed=21)
+    centers = rng.integers(0, 10_000_000, 40)
+    t = (centers[rng.integers(0, 40, s.size)] +
+         rng.exponential(2_000.0, s.size).astype(np.int64)).astype(np.int64)
+    og, eng = _pair(True, [(s, d, t)])
+    _walk_case(og, eng, picker, "Uniform", forward, "total", 30, 6_000, seed=11)
+    seeds = np.unique(s[:5_000]).astype(np.int32)
+    cuts = np.where(np.arange(seeds.size) % 4 == 0, -1,
+                    rng.integers(0, 10_000_000, seeds.size)).astype(np.int64)
+    _walk_case(og, eng, picker, picker, forward, "nodes", 30, 2, seed_nodes=seeds, cutoffs=cuts,
+               seed=12)
+
+
+@pytest.mark.parametrize("directed", [True, False])
+@pytest.mark.parametrize("forward", [True, False])
+def test_replay_walks_negative_and_minus_one_timestamps(directed, forward):
+    """Edges at timestamp -1 end a walk where the reference tests `ts == -1`
+    (and a start at -1 leaves the next hop unconstrained); other negative
+    timestamps are ordinary."""
+    s, d, t = graphs.cfg1(n_nodes=500, n_edges=20_000, seed=31)
+    t = (t % 40) - 20  # ts in [-20, 20): many ties, -1 among them
+    assert np.any(t == -1)
+    og, eng = _pair(directed, [(s, d, t)])
+    for picker in ("Uniform", "ExponentialIndex", "Linear"):
+        _walk_case(og, eng, picker, "Uniform", forward, "total", 16, 3_000, seed=13)
+        _walk_case(og, eng, picker, picker, forward, "all_nodes", 16, 2, seed=14)
