@@ -303,7 +303,7 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
     }
     // Slot-major scratch: slot k of walk w lives at [k * n + w], so the 64
     // lanes of a wave store 256 B per slot and array contiguously.
-    // transpose_walks_kernel produces the row-major output in the reference's
+    // layout_walks_kernel produces the row-major output in the reference's
     // types, the padding and the chronological order of backward walks.
     const uint64_t n = a.n;
     int32_t* wn = a.nodes + w;
@@ -375,68 +375,110 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
     a.lens[w] = static_cast<uint64_t>(len);
 }
 
-// Slot-major scratch [K][n] -> row-major output [n][K] for one walk array,
-// 64 walks x 64 slots per workgroup through LDS, converting each value to the
-// reference's type on the way: Conv 0 copies (nodes), 1 turns a timestamp
-// rank into the timestamp (uniq_ts; kStartRank into the first slot's
-// sentinel), 2 widens a 32-bit edge id.  `count` of walk w is the
-// number of written slots (len for nodes/timestamps, len - 1 for edge ids);
-// slots at or beyond it become `pad` (data/walk_set/walk_set_host.cu:25-29).
-// Backward walks come out reversed into chronological order
-// (data/walk_set/walk_set_view.cuh:50-80).
+// Layout pass: slot-major scratch [K][n] -> the row-major output [n][K] the
+// reference returns, for all three walk arrays in one pass.  Values become the
+// reference's types on the way: nodes are copied, a timestamp rank becomes the
+// timestamp (uniq_ts; kStartRank becomes the first slot's sentinel), a 32-bit
+// edge id is widened.  `count` of walk w is its number of written slots (len
+// for nodes and timestamps, len - 1 for edge ids); slots at or beyond it get
+// the padding (data/walk_set/walk_set_host.cu:25-29).  Backward walks come
+// out reversed into chronological order (data/walk_set/walk_set_view.cuh:
+// 50-80).
 //
-// A workgroup owns 64 consecutive walks x 64 slots.  Reads are 64-walk runs of
-// one slot (coalesced); each thread issues its 16 loads back to back so they
-// are in flight together; writes are runs of up to 64 slots of one walk row.
-template <typename Tin, typename T, int CountOffset, int Conv>
-__global__ __launch_bounds__(256) void transpose_walks_kernel(const Tin* __restrict__ in,
-                                                              T* __restrict__ out,
-                                                              const uint64_t* __restrict__ lens,
-                                                              uint64_t n, int K, int reverse,
-                                                              T pad,
-                                                              const int64_t* __restrict__ uniq_ts,
-                                                              int64_t start_ts) {
-    __shared__ T tile[64][65];
-    __shared__ int cnt[64];
-    const uint64_t w0 = static_cast<uint64_t>(blockIdx.x) * 64;
-    const int k0 = blockIdx.y * 64;
-    const int kc = min(64, K - k0);  // slots in this chunk
+// A workgroup owns 64 consecutive walks and a chunk of slots -- the whole row
+// when L <= kLayoutMaxSlots, so the 64 rows it writes are one contiguous span
+// of the output and no cache line is shared with another workgroup.  Per array
+// it reads 64-walk runs of one slot (256 B, coalesced) into an LDS tile of the
+// 32-bit scratch values, then each wave writes whole row runs, converting as
+// it writes (a walk's ranks increase along its row, so the timestamp lookups
+// of one run are close together).  One tile is reused by the three arrays.
+constexpr int kLayoutWalks = 64;
+constexpr int kLayoutMaxSlots = 128;  // tile <= 33 KB of LDS
+
+struct LayoutArgs {
+    const int32_t* sn;   // scratch nodes
+    const uint32_t* sr;  // scratch timestamp ranks
+    const uint32_t* se;  // scratch edge ids
+    int32_t* on;
+    int64_t* ot;
+    int64_t* oe;
+    const uint64_t* lens;
+    uint64_t n;
+    int L;
+    int C;  // slots per chunk
+    int reverse;
+    int32_t pad;
+    const int64_t* uniq_ts;
+    int64_t start_ts;
+};
+
+// Arr 0: nodes, 1: timestamps, 2: edge ids.
+template <int Arr>
+__device__ __forceinline__ void layout_array(const LayoutArgs& a, uint32_t* tile, const int* cnt,
+                                             uint64_t w0, int k0) {
+    const int K = Arr == 2 ? a.L - 1 : a.L;
+    const int kc = min(a.C, K - k0);
+    if (kc <= 0) return;  // uniform over the workgroup
+    constexpr int P = kLayoutWalks + 1;
     const int tid = threadIdx.x;
-    if (tid < 64) {
-        const uint64_t w = w0 + tid;
-        const int c = w < n ? static_cast<int>(lens[w]) + CountOffset : 0;
-        cnt[tid] = c > 0 ? c : 0;
-    }
-    __syncthreads();
     const int wl = tid & 63, srow = tid >> 6;
     const uint64_t w = w0 + wl;
-    const int c = cnt[wl];
-    T v[16];
+    int c = cnt[wl] - (Arr == 2 ? 1 : 0);
+    c = c > 0 ? c : 0;
+    // slots at or past the count are not read; the writer pads them
+    const uint32_t* in = Arr == 0 ? reinterpret_cast<const uint32_t*>(a.sn) : (Arr == 1 ? a.sr : a.se);
+    for (int j0 = 0; j0 < kc; j0 += 32) {
+        uint32_t v[8];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const int k = k0 + srow + 4 * j;
-        v[j] = pad;
-        if (w < n && k < c) {
-            const int src = reverse ? c - 1 - k : k;
-            const Tin x = in[static_cast<uint64_t>(src) * n + w];
-            if (Conv == 0) v[j] = static_cast<T>(x);
-            else if (Conv == 2) v[j] = static_cast<T>(static_cast<uint32_t>(x));
-            else v[j] = static_cast<uint32_t>(x) == kStartRank ? start_ts : uniq_ts[x];
+        for (int j = 0; j < 8; ++j) {
+            const int r = j0 + srow + 4 * j;
+            const int k = k0 + r;
+            uint32_t x = 0;
+            if (r < kc && w < a.n && k < c)
+                x = in[static_cast<uint64_t>(a.reverse ? c - 1 - k : k) * a.n + w];
+            v[j] = x;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int r = j0 + srow + 4 * j;
+            if (r < kc) tile[r * P + wl] = v[j];
         }
     }
-#pragma unroll
-    for (int j = 0; j < 16; ++j) tile[srow + 4 * j][wl] = v[j];
     __syncthreads();
-    for (int idx = tid; idx < kc * 64; idx += 256) {
-        const int wl2 = idx / kc, i = idx - wl2 * kc;
+    const int wave = tid >> 6, lane = tid & 63;
+    for (int wl2 = wave; wl2 < kLayoutWalks; wl2 += 4) {
         const uint64_t w2 = w0 + wl2;
-        if (w2 < n) out[w2 * K + k0 + i] = tile[i][wl2];
+        if (w2 >= a.n) break;
+        const uint64_t base = w2 * static_cast<uint64_t>(K) + k0;
+        const int cw = cnt[wl2] - (Arr == 2 ? 1 : 0) - k0;  // slots of the row below the count
+        for (int i = lane; i < kc; i += 64) {
+            const uint32_t x = tile[i * P + wl2];
+            if (Arr == 0) {
+                a.on[base + i] = i < cw ? static_cast<int32_t>(x) : a.pad;
+            } else if (Arr == 1) {
+                a.ot[base + i] = i >= cw ? -1 : (x == kStartRank ? a.start_ts : a.uniq_ts[x]);
+            } else {
+                a.oe[base + i] = i < cw ? static_cast<int64_t>(x) : -1;
+            }
+        }
     }
+    __syncthreads();
 }
 
-template <typename T>
-constexpr int transpose_chunk() {
-    return 64;
+__global__ __launch_bounds__(256) void layout_walks_kernel(LayoutArgs a) {
+    extern __shared__ uint32_t layout_lds[];
+    uint32_t* tile = layout_lds;
+    int* cnt = reinterpret_cast<int*>(layout_lds + a.C * (kLayoutWalks + 1));
+    const uint64_t w0 = static_cast<uint64_t>(blockIdx.x) * kLayoutWalks;
+    const int k0 = blockIdx.y * a.C;
+    if (threadIdx.x < kLayoutWalks) {
+        const uint64_t w = w0 + threadIdx.x;
+        cnt[threadIdx.x] = w < a.n ? static_cast<int>(a.lens[w]) : 0;
+    }
+    __syncthreads();
+    layout_array<0>(a, tile, cnt, w0, k0);
+    layout_array<1>(a, tile, cnt, w0, k0);
+    layout_array<2>(a, tile, cnt, w0, k0);
 }
 
 // ---- start arrays ----------------------------------------------------------
@@ -853,22 +895,26 @@ void Engine::sample(const trw_sample_params& p) {
     if (nw && L > 0) {
         const unsigned gx = static_cast<unsigned>((nw + 63) / 64);
         const int rev = forward ? 0 : 1;
-        constexpr int c32 = transpose_chunk<int32_t>(), c64 = transpose_chunk<int64_t>();
-        const int64_t start_ts = forward ? INT64_MIN : INT64_MAX;
-        hipLaunchKernelGGL((transpose_walks_kernel<int32_t, int32_t, 0, 0>),
-                           dim3(gx, (L + c32 - 1) / c32), dim3(256), 0, s, sw_nodes.p, w_nodes.p,
-                           w_lens.p, nw, L, rev, static_cast<int32_t>(cfg.walk_padding_value),
-                           nullptr, start_ts);
-        hipLaunchKernelGGL((transpose_walks_kernel<uint32_t, int64_t, 0, 1>),
-                           dim3(gx, (L + c64 - 1) / c64), dim3(256), 0, s, sw_rank.p, w_ts.p,
-                           w_lens.p, nw, L, rev, static_cast<int64_t>(-1), uniq_ts.p, start_ts);
-        if (L > 1) {
-            hipLaunchKernelGGL((transpose_walks_kernel<uint32_t, int64_t, -1, 2>),
-                               dim3(gx, (L - 1 + c64 - 1) / c64), dim3(256), 0, s, sw_eids.p,
-                               w_eids.p, w_lens.p, nw, L - 1, rev, static_cast<int64_t>(-1),
-                               nullptr, start_ts);
-        }
-        check_hip(hipGetLastError(), "transpose launch");
+        LayoutArgs la{};
+        la.sn = sw_nodes.p;
+        la.sr = sw_rank.p;
+        la.se = sw_eids.p;
+        la.on = w_nodes.p;
+        la.ot = w_ts.p;
+        la.oe = w_eids.p;
+        la.lens = w_lens.p;
+        la.n = nw;
+        la.L = L;
+        const int chunks = (L + kLayoutMaxSlots - 1) / kLayoutMaxSlots;
+        la.C = (L + chunks - 1) / chunks;
+        la.reverse = rev;
+        la.pad = static_cast<int32_t>(cfg.walk_padding_value);
+        la.uniq_ts = uniq_ts.p;
+        la.start_ts = forward ? INT64_MIN : INT64_MAX;
+        const size_t lds = static_cast<size_t>(la.C) * (kLayoutWalks + 1) * sizeof(uint32_t) +
+                           kLayoutWalks * sizeof(int);
+        hipLaunchKernelGGL(layout_walks_kernel, dim3(gx, chunks), dim3(256), lds, s, la);
+        check_hip(hipGetLastError(), "layout launch");
     }
 
     // ---- edge features of every walk slot (finalize_host_walks, on device)

@@ -273,3 +273,14 @@ def test_replay_walks_negative_and_minus_one_timestamps(directed, forward):
     for picker in ("Uniform", "ExponentialIndex", "Linear"):
         _walk_case(og, eng, picker, "Uniform", forward, "total", 16, 3_000, seed=13)
         _walk_case(og, eng, picker, picker, forward, "all_nodes", 16, 2, seed=14)
+
+
+@pytest.mark.parametrize("forward", [True, False])
+def test_replay_long_walks_span_layout_chunks(forward):
+    """Walks longer than one layout chunk (rows of more than 96 slots are
+    laid out in several chunks), padded and reversed like short ones."""
+    s, d, t = graphs.cfg1(n_nodes=200, n_edges=100_000, seed=41)
+    og, eng = _pair(True, [(s, d, t)])
+    got = _walk_case(og, eng, "ExponentialIndex", "Uniform", forward, "total", 150, 2_000, seed=15)
+    lens = got.lens.astype(np.int64)
+    assert lens.max() == 150 and (lens > 96).mean() > 0.5
