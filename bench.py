@@ -94,7 +94,8 @@ def main():
     ap.add_argument("--walks", type=int, default=10_000_000)
     ap.add_argument("--walk-len", type=int, default=80)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-walks", type=int, default=200_000)
+    ap.add_argument("--cpu-walks", type=int, default=2_500_000,
+                    help="walks of the bounded CPU-baseline sample (about 10 s on 16 threads)")
     ap.add_argument("--host-boundary", action="store_true",
                     help="also time the reference's host boundary once through the drop-in "
                          "Python class: numpy edges in (host->device copy included) and "
@@ -224,7 +225,7 @@ def main():
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": traffic,
-            "kernel": "walk_kernel<true,true>",
+            "kernel": "walk_kernel<true,true,0>",
             "algorithmic_bytes_per_launch": stats["algorithmic_bytes"],
         },
     }
