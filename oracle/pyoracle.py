@@ -133,8 +133,40 @@ def lib():
                                                    C.c_double, C.c_size_t]
         L.orc_derive_uniform.restype = C.c_double
         L.orc_derive_uniform.argtypes = [C.c_double, C.c_double, C.c_int]
+        L.orc_philox4x32_10.restype = None
+        L.orc_philox4x32_10.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p]
+        L.orc_philox_draws.restype = None
+        L.orc_philox_draws.argtypes = [C.c_uint64, C.c_uint64, C.c_uint64, C.c_int, C.c_void_p]
+        L.orc_philox_shuffle_keys.restype = None
+        L.orc_philox_shuffle_keys.argtypes = [C.c_uint64, C.c_uint64, C.c_void_p]
         _lib = L
     return _lib
+
+
+def philox4x32_10(ctr, key):
+    """One Philox4x32-10 block (the engine's draw generator)."""
+    c = np.ascontiguousarray(ctr, dtype=np.uint32)
+    k = np.ascontiguousarray(key, dtype=np.uint32)
+    out = np.zeros(4, dtype=np.uint32)
+    lib().orc_philox4x32_10(c.ctypes.data, k.ctypes.data, out.ctypes.data)
+    return out
+
+
+def philox_draws(seed, n_walks, max_walk_len, walk0=0):
+    """The engine's normal-mode draws of walks [walk0, walk0 + n) in the
+    replay layout, n * (1 + 2L) doubles."""
+    out = np.empty(int(n_walks) * (1 + 2 * int(max_walk_len)), dtype=np.float64)
+    lib().orc_philox_draws(int(seed), int(walk0), int(n_walks), int(max_walk_len),
+                           out.ctypes.data)
+    return out
+
+
+def philox_shuffle_order(seed, n):
+    """The engine's walk-order shuffle: position i of the shuffled start
+    array holds the unshuffled entry order[i]."""
+    keys = np.empty(int(n), dtype=np.uint32)
+    lib().orc_philox_shuffle_keys(int(seed), int(n), keys.ctypes.data)
+    return np.argsort(keys, kind="stable")
 
 
 def ref_available() -> bool:

@@ -957,3 +957,58 @@ void orc_walks(const orc_graph* g, int L, int walk_bias, int start_bias, int for
         one_walk(g, (size_t)w, L, walk_bias, start_bias, forward, starts, cutoffs, draws, pad,
                  nodes, tss, lens, eids);
 }
+
+/* ---- the engine's normal-mode draw stream (see trw_oracle.h) ------------- */
+
+void orc_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {
+    uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3];
+    uint32_t k0 = key[0], k1 = key[1];
+    for (int r = 0; r < 10; r++) {
+        const uint64_t p0 = (uint64_t)0xD2511F53u * c0;
+        const uint64_t p1 = (uint64_t)0xCD9E8D57u * c2;
+        const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0;
+        const uint32_t n1 = (uint32_t)p1;
+        const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
+        const uint32_t n3 = (uint32_t)p0;
+        c0 = n0; c1 = n1; c2 = n2; c3 = n3;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+    out[0] = c0; out[1] = c1; out[2] = c2; out[3] = c3;
+}
+
+static double unit_from_bits(uint32_t lo, uint32_t hi) {
+    const uint64_t m = (((uint64_t)hi << 32) | lo) >> 12;
+    return ((double)m + 0.5) * 0x1p-52;
+}
+
+void orc_philox_draws(uint64_t seed, uint64_t walk0, uint64_t n, int L, double* out) {
+    const uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+    const size_t stride = 1 + 2 * (size_t)L;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+    for (long i = 0; i < (long)n; i++) {
+        const uint64_t w = walk0 + (uint64_t)i;
+        double* d = out + (size_t)i * stride;
+        uint32_t ctr[4] = {0u, (uint32_t)w, (uint32_t)(w >> 32), 0u}, o[4];
+        orc_philox4x32_10(ctr, key, o);
+        d[0] = unit_from_bits(o[0], o[1]);
+        for (int p = 1; p <= L; p++) {
+            ctr[0] = (uint32_t)p;
+            orc_philox4x32_10(ctr, key, o);
+            d[2 * p - 1] = unit_from_bits(o[0], o[1]);
+            d[2 * p] = unit_from_bits(o[2], o[3]);
+        }
+    }
+}
+
+void orc_philox_shuffle_keys(uint64_t seed, uint64_t n, uint32_t* out) {
+    const uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+    for (uint64_t i = 0; i < n; i++) {
+        const uint32_t ctr[4] = {(uint32_t)i, (uint32_t)(i >> 32), 0x5348u, 0u};
+        uint32_t o[4];
+        orc_philox4x32_10(ctr, key, o);
+        out[i] = o[0];
+    }
+}

@@ -100,6 +100,27 @@ int orc_pick_exponential_weights(const double* weights, size_t weights_size,
                                  size_t slice_start);
 double orc_derive_uniform(double a, double b, int counter);
 
+/* ---- the engine's normal-mode draw stream --------------------------------
+ * Not a reference function: the reference CPU path draws from std::mt19937
+ * seeded by random_device and is not reproducible.  The engine instead derives
+ * every draw from Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random
+ * numbers: as easy as 1, 2, 3", SC'11) keyed by the 64-bit seed; these
+ * restate that derivation so normal-mode walks can be replayed here. */
+
+/* One Philox4x32-10 block: 10 rounds, key bumped by the Weyl constants
+ * (0x9E3779B9, 0xBB67AE85) between rounds. */
+void orc_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
+
+/* The draws of walks [walk0, walk0 + n) in the replay layout (1 + 2L per
+ * walk): counter (pair, walk_lo, walk_hi, 0), key (seed_lo, seed_hi); pair 0
+ * gives slot 0 from words (x, y), pair p >= 1 slots 2p-1 from (x, y) and 2p
+ * from (z, w); 64 bits (hi:lo) >> 12 = m map to (m + 0.5) * 2^-52. */
+void orc_philox_draws(uint64_t seed, uint64_t walk0, uint64_t n, int max_walk_len, double* out);
+
+/* Keys of the walk-order shuffle: word x of counter (i_lo, i_hi, 0x5348, 0);
+ * the shuffled order is a stable sort of positions by key. */
+void orc_philox_shuffle_keys(uint64_t seed, uint64_t n, uint32_t* out);
+
 #ifdef __cplusplus
 }
 #endif

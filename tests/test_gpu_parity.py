@@ -284,3 +284,111 @@ def test_replay_long_walks_span_layout_chunks(forward):
     got = _walk_case(og, eng, "ExponentialIndex", "Uniform", forward, "total", 150, 2_000, seed=15)
     lens = got.lens.astype(np.int64)
     assert lens.max() == 150 and (lens > 96).mean() > 0.5
+
+
+# ---- normal mode: the in-kernel Philox stream -----------------------------
+
+GLOBAL_SEED = 1234  # the seed _pair gives the engine
+
+
+def _starts(og, mode, n_or_wpn, seed_nodes=None):
+    if mode == "total":
+        return -np.ones(n_or_wpn, dtype=np.int32)
+    if mode == "all_nodes":
+        ids = np.nonzero(og.array("active_node_ids"))[0].astype(np.int32)
+        return np.repeat(ids, n_or_wpn)
+    return np.repeat(np.asarray(seed_nodes, dtype=np.int32), n_or_wpn)
+
+
+def _normal_case(og, eng, picker, start_picker, forward, mode, L, n_or_wpn, seed_nodes=None,
+                 cutoffs=None, shuffle=False):
+    """Normal-mode walks (no injected draws) must equal the oracle's replay
+    of the engine's Philox draws, in the shuffled start order if shuffled."""
+    direction = "Forward_In_Time" if forward else "Backward_In_Time"
+    starts = _starts(og, mode, n_or_wpn, seed_nodes)
+    cut = None if cutoffs is None else np.repeat(np.asarray(cutoffs, dtype=np.int64), n_or_wpn)
+    if shuffle and mode != "total":
+        order = po.philox_shuffle_order(GLOBAL_SEED, starts.size)
+        starts = starts[order]
+        cut = None if cut is None else cut[order]
+    got = eng.sample(mode, L, picker, n_or_wpn, initial_edge_bias=start_picker,
+                     direction=direction, seed_nodes=seed_nodes, cutoff_times=cutoffs,
+                     shuffle=shuffle)
+    dr = po.philox_draws(GLOBAL_SEED, starts.size, L)
+    ref = og.walks(L, picker, start_picker, forward, starts, dr, cutoffs=cut)
+    for k in ("nodes", "timestamps", "lens", "edge_ids"):
+        a, b = getattr(ref, k), getattr(got, k)
+        assert a.shape == b.shape, k
+        assert np.array_equal(a, b), (f"{picker}/{start_picker} fwd={forward} {mode} "
+                                      f"shuffle={shuffle}: {k} differs")
+    return got
+
+
+@pytest.mark.parametrize("directed", [True, False])
+@pytest.mark.parametrize("forward", [True, False])
+def test_normal_mode_walks_are_the_philox_replay(directed, forward):
+    s, d, t = graphs.powerlaw(5_000, 80_000, s=1.7, n_ts=20_000, seed=51)
+    og, eng = _pair(directed, [(s, d, t)])
+    _normal_case(og, eng, "ExponentialIndex", "Uniform", forward, "total", 40, 20_000)
+    _normal_case(og, eng, "Linear", "Linear", forward, "all_nodes", 20, 2)
+    _normal_case(og, eng, "Uniform", "ExponentialIndex", forward, "all_nodes", 20, 2,
+                 shuffle=True)
+    seeds = np.unique(s[:2_000]).astype(np.int32)
+    cuts = np.where(np.arange(seeds.size) % 3 == 0, -1,
+                    np.random.default_rng(52).integers(0, 100_000_000, seeds.size)).astype(np.int64)
+    _normal_case(og, eng, "ExponentialIndex", "ExponentialIndex", forward, "nodes", 30, 3,
+                 seed_nodes=seeds, cutoffs=cuts, shuffle=True)
+
+
+@pytest.mark.parametrize("forward", [True, False])
+@pytest.mark.parametrize("picker", ["ExponentialWeight", "TemporalNode2Vec"])
+def test_normal_mode_weight_pickers_are_the_philox_replay(forward, picker):
+    s, d, t = graphs.powerlaw(3_000, 50_000, s=1.6, seed=53, ts_hi=1_000_000)
+    og, eng = _pair(True, [(s, d, t)], weights=True, tn2v=picker == "TemporalNode2Vec",
+                    timescale_bound=50.0, p=0.5, q=2.0)
+    for name in WEIGHT_ARRAYS:
+        w = eng.array(name)
+        if w.size:
+            og.set_weights(name, w)
+    _normal_case(og, eng, picker, picker, forward, "total", 24, 8_000)
+    _normal_case(og, eng, picker, picker, forward, "all_nodes", 12, 1, shuffle=True)
+
+
+def _chi2_two_sample(a, b, min_expected=5.0):
+    """Two-sample chi-square on category samples a, b (equal sizes): categories
+    with small expected counts are pooled into one bin.  Returns the p-value."""
+    from scipy.stats import chi2_contingency
+    cats, inv = np.unique(np.concatenate([a, b]), return_inverse=True)
+    ca = np.bincount(inv[:a.size], minlength=cats.size)
+    cb = np.bincount(inv[a.size:], minlength=cats.size)
+    small = (ca + cb) / 2.0 < min_expected
+    table = np.stack([ca[~small], cb[~small]])
+    if small.any():
+        table = np.concatenate([table, [[ca[small].sum()], [cb[small].sum()]]], axis=1)
+    return chi2_contingency(table)[1]
+
+
+@pytest.mark.parametrize("picker", ["Uniform", "Linear", "ExponentialIndex", "ExponentialWeight",
+                                    "TemporalNode2Vec"])
+def test_normal_mode_chi_square_against_independent_draws(picker):
+    """The distribution of normal-mode walks matches the oracle's walks under
+    independent numpy uniforms (two-sample chi-square, p > 0.01) on the start
+    edge, the first hop's edge, the fifth slot's node and the walk length."""
+    s, d, t = graphs.cfg1(n_nodes=60, n_edges=1_500, seed=61)
+    weights = picker in ("ExponentialWeight", "TemporalNode2Vec")
+    og, eng = _pair(True, [(s, d, t)], weights=weights, tn2v=picker == "TemporalNode2Vec",
+                    timescale_bound=20.0, p=0.5, q=2.0)
+    if weights:
+        for name in WEIGHT_ARRAYS:
+            w = eng.array(name)
+            if w.size:
+                og.set_weights(name, w)
+    n, L = 200_000, 8
+    got = eng.sample("total", L, picker, n, initial_edge_bias=picker)
+    ref = og.walks(L, picker, picker, True, -np.ones(n, np.int32), graphs.draws(n, L, seed=62))
+    for name, a, b in [("start edge", ref.edge_ids[:, 0], got.edge_ids[:, 0]),
+                       ("hop-1 edge", ref.edge_ids[:, 1], got.edge_ids[:, 1]),
+                       ("slot-4 node", ref.nodes[:, 4], got.nodes[:, 4]),
+                       ("length", ref.lens.astype(np.int64), got.lens.astype(np.int64))]:
+        pv = _chi2_two_sample(np.asarray(a), np.asarray(b))
+        assert pv > 0.01, f"{picker}: {name} p = {pv:.3g}"

@@ -328,3 +328,53 @@ def test_oracle_matches_compiled_reference(directed):
                 b = rg.walks(L, picker, picker, forward, starts, dr, cutoffs=cut)
                 for k in ("nodes", "timestamps", "lens", "edge_ids"):
                     assert np.array_equal(getattr(a, k), getattr(b, k)), (picker, forward, k)
+
+
+def test_philox_known_answers():
+    """Philox4x32-10 against the known-answer vectors published with
+    Random123 (kat_vectors: philox4x32 10 rounds)."""
+    kat = [
+        ([0, 0, 0, 0], [0, 0], [0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8]),
+        ([0xFFFFFFFF] * 4, [0xFFFFFFFF] * 2, [0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD]),
+        ([0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344], [0xA4093822, 0x299F31D0],
+         [0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1]),
+    ]
+    for ctr, key, want in kat:
+        assert list(po.philox4x32_10(ctr, key)) == want
+
+
+def test_philox_draw_layout():
+    """Slot layout of the normal-mode draws: slot 0 from pair 0's (x, y),
+    slots 2p-1 / 2p from pair p's (x, y) / (z, w); counter (pair, walk_lo,
+    walk_hi, 0), key = the seed's halves; (m + 0.5) * 2^-52 with m the top 52
+    of the 64 bits."""
+    seed, L = 0x0123456789ABCDEF, 5
+    walks = [0, 1, 7, (1 << 32) + 3]
+    key = [seed & 0xFFFFFFFF, seed >> 32]
+
+    def unit(lo, hi):
+        m = ((int(hi) << 32) | int(lo)) >> 12
+        return (m + 0.5) / 2.0 ** 52
+
+    for w in walks:
+        d = po.philox_draws(seed, 1, L, walk0=w)
+        ctr = [0, w & 0xFFFFFFFF, w >> 32, 0]
+        o = po.philox4x32_10(ctr, key)
+        assert d[0] == unit(o[0], o[1])
+        for p in range(1, L + 1):
+            o = po.philox4x32_10([p] + ctr[1:], key)
+            assert d[2 * p - 1] == unit(o[0], o[1]) and d[2 * p] == unit(o[2], o[3])
+    # many draws: strictly inside (0, 1), mean 1/2, no two equal
+    d = po.philox_draws(seed, 20_000, 8)
+    assert d.min() > 0.0 and d.max() < 1.0
+    assert abs(d.mean() - 0.5) < 5 * math.sqrt(1 / 12 / d.size)
+    assert np.unique(d).size == d.size
+    # the unit map's extremes: m = 0 and m = 2^52 - 1 stay inside (0, 1)
+    assert unit(0, 0) == 2.0 ** -53 and unit(0xFFFFFFFF, 0xFFFFFFFF) == 1 - 2.0 ** -53
+
+
+def test_philox_shuffle_order_is_a_permutation():
+    order = po.philox_shuffle_order(99, 10_000)
+    assert np.array_equal(np.sort(order), np.arange(10_000))
+    assert not np.array_equal(order, np.arange(10_000))
+    assert np.array_equal(order, po.philox_shuffle_order(99, 10_000))
