@@ -304,6 +304,43 @@ __global__ void node_table_fill_kernel(const uint32_t* __restrict__ key,
     if (i == G - 1) tab[h.tab + bi + 1] = G;
 }
 
+// Weight search index (see engine.h): entries per node, then one thread per
+// group writes its cumulative weight into every level whose stride divides
+// its local index; the segment's last group writes the +inf padding.  With
+// key == nullptr the whole array [0, ng) is one segment (global weights).
+__global__ void wx_sizes_kernel(const uint32_t* __restrict__ cnt, size_t v,
+                                uint32_t* __restrict__ sizes) {
+    const size_t u = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (u >= v) return;
+    sizes[u] = wx_size(cnt[u + 1] - cnt[u]);
+}
+
+__global__ void wx_fill_kernel(const double* __restrict__ w, const uint32_t* __restrict__ key,
+                               const uint32_t* __restrict__ grp, const uint32_t* __restrict__ cnt,
+                               const uint32_t* __restrict__ off, size_t ng,
+                               double* __restrict__ wx) {
+    const size_t g = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (g >= ng) return;
+    uint32_t gb = 0, G = static_cast<uint32_t>(ng), base = 0;
+    if (key) {
+        const uint32_t u = key[grp[g]];
+        gb = cnt[u];
+        G = cnt[u + 1] - gb;
+        base = off[u];
+    }
+    if (G <= kWIdxMin) return;
+    const uint32_t i = static_cast<uint32_t>(g) - gb;
+    uint32_t loff = 0;
+    for (uint64_t span = wx_top_span(G);; span >>= 4) {
+        const uint32_t n = wx_level_entries(G, span);
+        if (i % span == 0) wx[base + loff + static_cast<uint32_t>(i / span)] = w[g];
+        if (i == G - 1)
+            for (uint32_t p = n; p < wx_pad16(n); ++p) wx[base + loff + p] = __builtin_huge_val();
+        loff += wx_pad16(n);
+        if (span == 16) break;
+    }
+}
+
 __global__ void active_flags_kernel(const uint32_t* __restrict__ out_off,
                                     const uint32_t* __restrict__ in_off, size_t v,
                                     uint8_t* __restrict__ active) {
@@ -673,6 +710,45 @@ void node_weights(Engine& e, DirIndex& dir, size_t v, double bound, bool compute
     check_hip(hipGetLastError(), "node weights launch");
 }
 
+// Weight search indexes of one direction's per-node cumulative weights.
+void build_weight_index(Engine& e, DirIndex& dir, size_t v, int64_t* host_scratch) {
+    hipStream_t s = e.stream;
+    const size_t vc = v + 1;
+    e.flags.ensure(vc);
+    e.scan.ensure(vc);
+    e.scan_scratch.ensure(scan_scratch_elems(vc));
+    hipLaunchKernelGGL(wx_sizes_kernel, dim3(grid_for(v)), dim3(kB), 0, s, dir.cnt.p, v, e.flags.p);
+    exclusive_scan_u32(e.flags.p, e.scan.p, v, e.scan_scratch.p, s);
+    dir.wx_off.resize(vc);
+    check_hip(hipMemcpyAsync(dir.wx_off.p, e.scan.p, vc * 4, hipMemcpyDeviceToDevice, s),
+              "copy wx offsets");
+    check_hip(hipMemcpyAsync(host_scratch, e.scan.p + v, 4, hipMemcpyDeviceToHost, s), "read wx");
+    e.sync();
+    uint32_t total = 0;
+    std::memcpy(&total, host_scratch, 4);
+    const size_t g = dir.n_groups;
+    DBuf<double>* dst[2] = {&dir.wx_fwd, &dir.wx_bwd};
+    const DBuf<double>* src[2] = {&dir.w_fwd, &dir.w_bwd};
+    for (int k = 0; k < 2; ++k) {
+        const bool have = src[k]->n == g && g > 0;
+        dst[k]->resize(have ? total : 0);
+        if (have && total)
+            hipLaunchKernelGGL(wx_fill_kernel, dim3(grid_for(g)), dim3(kB), 0, s, src[k]->p,
+                               dir.key.p, dir.grp.p, dir.cnt.p, dir.wx_off.p, g, dst[k]->p);
+    }
+    check_hip(hipGetLastError(), "weight index launch");
+}
+
+// Weight search index of a global cumulative array (one segment of n).
+void build_global_weight_index(Engine& e, const DBuf<double>& w, size_t n, DBuf<double>& wx) {
+    const uint32_t total = wx_size(static_cast<uint32_t>(n));
+    wx.resize(total);
+    if (total)
+        hipLaunchKernelGGL(wx_fill_kernel, dim3(grid_for(n)), dim3(kB), 0, e.stream, w.p, nullptr,
+                           nullptr, nullptr, nullptr, n, wx.p);
+    check_hip(hipGetLastError(), "global weight index launch");
+}
+
 }  // namespace
 
 void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_ts,
@@ -845,6 +921,12 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
         fscan_scratch.ensure(scan_scratch_elems(std::max<size_t>(T, out.n_groups)));
         inclusive_scan_f64(fwd_cum.p, T, fscan_scratch.p, s);
         inclusive_scan_f64(bwd_cum.p, T, fscan_scratch.p, s);
+        // the weight search counts entries below its target, which is the
+        // lower_bound only on a non-decreasing array
+        running_max_f64(fwd_cum.p, T, fscan_scratch.p, s);
+        running_max_f64(bwd_cum.p, T, fscan_scratch.p, s);
+        build_global_weight_index(*this, fwd_cum, T, gwx_fwd);
+        build_global_weight_index(*this, bwd_cum, T, gwx_bwd);
         // per node (node_edge_index.cu:644-684): outbound forward + backward,
         // inbound backward (directed)
         out.w_fwd.resize(out.n_groups);
@@ -854,6 +936,8 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
             in.w_bwd.resize(in.n_groups);
             node_weights(*this, in, v, bound, false, hs);
         }
+        build_weight_index(*this, out, v, hs);
+        if (cfg.is_directed) build_weight_index(*this, in, v, hs);
         check_hip(hipGetLastError(), "weights launch");
         weights_ready = true;
     }
@@ -878,7 +962,7 @@ void Engine::clear() {
     max_node_id = -1;
     store_tmin = store_tmax = 0;
     src.n = dst.n = ts.n = feat.n = tsg_off.n = uniq_ts.n = erank.n = neg1_rank.n = active.n = 0;
-    fwd_cum.n = bwd_cum.n = adj_off.n = adj_nbr.n = 0;
+    fwd_cum.n = bwd_cum.n = gwx_fwd.n = gwx_bwd.n = adj_off.n = adj_nbr.n = 0;
     weights_ready = adj_ready = false;
     out.clear();
     in.clear();

@@ -32,7 +32,15 @@
 //                                  picked group's range usually shares the
 //                                  line of the search's last probe
 //     w_fwd, w_bwd  fp64[g]        per-node cumulative exponential weights
-//   global weights  fwd_cum, bwd_cum fp64[T]
+//     wx_off        uint32[V_c]    each node's base in the weight search index
+//     wx_fwd/wx_bwd fp64[..]       weight search index of nodes with > kWIdxMin
+//                                  groups: level k (k = 1..K) holds every
+//                                  16^k-th cumulative weight, K the first level
+//                                  of at most 16 entries; every level padded
+//                                  with +inf to whole 16-entry (128-byte)
+//                                  blocks; top level first
+//   global weights  fwd_cum, bwd_cum fp64[T] (+ gwx_fwd, gwx_bwd: their
+//                   search index, one segment of T)
 //   node2vec        adj_off uint32[max_id+2], adj_nbr int32[2E]
 #pragma once
 
@@ -105,6 +113,33 @@ struct alignas(8) EdgeRec {
 };
 static_assert(sizeof(EdgeRec) == 8, "EdgeRec must be 8 bytes");
 
+// Cumulative-weight segments longer than this get a search index (levels of
+// every 16^k-th value); shorter ones are binary-searched directly.
+constexpr uint32_t kWIdxMin = 16;
+
+// Geometry of the weight search index of a segment of G cumulative weights:
+// level k has ceil(G / 16^k) entries; the top level K is the first with at
+// most 16; each level is padded to whole 16-entry blocks.
+__host__ __device__ inline uint32_t wx_level_entries(uint32_t G, uint64_t span) {
+    return static_cast<uint32_t>((G + span - 1) / span);
+}
+__host__ __device__ inline uint32_t wx_pad16(uint32_t n) { return (n + 15u) & ~15u; }
+__host__ __device__ inline uint64_t wx_top_span(uint32_t G) {
+    uint64_t span = 16;
+    while ((G + span - 1) / span > 16) span <<= 4;
+    return span;
+}
+__host__ __device__ inline uint32_t wx_size(uint32_t G) {
+    if (G <= kWIdxMin) return 0;
+    uint32_t total = 0;
+    for (uint64_t span = 16;; span <<= 4) {
+        const uint32_t n = wx_level_entries(G, span);
+        total += wx_pad16(n);
+        if (n <= 16) break;
+    }
+    return total;
+}
+
 // Nodes with more groups than this get a bucket table for the walk's search;
 // smaller ones are binary-searched directly (at most two panel lines).
 constexpr uint32_t kTabMin = 16;
@@ -140,13 +175,15 @@ struct DirIndex {
     DBuf<uint32_t> tab;      // bucket tables
     DBuf<double> w_fwd;      // g (outbound only)
     DBuf<double> w_bwd;      // g
+    DBuf<uint32_t> wx_off;   // V_c
+    DBuf<double> wx_fwd, wx_bwd;
     size_t n_entries = 0;
     size_t n_groups = 0;
     bool present = false;
 
     void clear() {
         off.n = idx.n = rec.n = key.n = cnt.n = grp.n = first_ts.n = pan.n = hdr.n = tab.n = w_fwd.n =
-            w_bwd.n = 0;
+            w_bwd.n = wx_off.n = wx_fwd.n = wx_bwd.n = 0;
         n_entries = n_groups = 0;
         present = false;
     }
@@ -202,6 +239,7 @@ struct Engine {
 
     // global weights
     DBuf<double> fwd_cum, bwd_cum;
+    DBuf<double> gwx_fwd, gwx_bwd;
     bool weights_ready = false;
 
     // node2vec adjacency

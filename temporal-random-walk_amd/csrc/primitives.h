@@ -32,6 +32,10 @@ void exclusive_scan_u64(const uint64_t* in, uint64_t* out, size_t n, uint64_t* s
                         hipStream_t s);
 // Inclusive scan of doubles in place (out[i] = in[0] + ... + in[i]).
 void inclusive_scan_f64(double* data, size_t n, double* scratch, hipStream_t s);
+// Running maximum of doubles in place (out[i] = max(in[0..i])): makes a
+// cumulative array non-decreasing to the last ulp, whatever order its partial
+// sums were rounded in.
+void running_max_f64(double* data, size_t n, double* scratch, hipStream_t s);
 
 // ---- radix sort --------------------------------------------------------------
 // Stable sort of (key, value) pairs by key bits [begin_bit, end_bit).  Values

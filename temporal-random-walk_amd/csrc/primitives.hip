@@ -19,42 +19,59 @@ namespace {
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / 64;
 
+// Scan operators: a sum, and a running maximum (identity -inf).
+struct OpSum {
+    template <typename T>
+    __device__ static T identity() { return T(0); }
+    template <typename T>
+    __device__ static T apply(T a, T b) { return a + b; }
+};
+struct OpMax {
+    template <typename T>
+    __device__ static T identity() { return -__builtin_huge_val(); }
+    template <typename T>
+    __device__ static T apply(T a, T b) { return a > b ? a : b; }
+};
+
 // ---------------------------------------------------------------------------
 // block-level helpers (256 threads = 4 wave64)
 // ---------------------------------------------------------------------------
-template <typename T>
+template <typename T, typename Op = OpSum>
 __device__ __forceinline__ T wave_inclusive_scan(T x, int lane) {
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
         const T y = __shfl_up(x, off, 64);
-        if (lane >= off) x += y;
+        if (lane >= off) x = Op::apply(x, y);
     }
     return x;
 }
 
-// Exclusive block scan of one value per thread; *total receives the block sum.
-template <typename T>
+// Exclusive block scan of one value per thread; *total receives the block
+// total.  The exclusive value is built from the wave prefix and the shifted
+// inclusive scan, so it is exact for the maximum as well as for integers.
+template <typename T, typename Op = OpSum>
 __device__ __forceinline__ T block_exclusive_scan(T v, T* total, T* s_wave) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const T inc = wave_inclusive_scan(v, lane);
+    const T inc = wave_inclusive_scan<T, Op>(v, lane);
+    const T below = __shfl_up(inc, 1, 64);
     if (lane == 63) s_wave[wave] = inc;
     __syncthreads();
-    T wp = T(0), tot = T(0);
+    T wp = Op::template identity<T>(), tot = Op::template identity<T>();
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
         const T sw = s_wave[w];
-        if (w < wave) wp += sw;
-        tot += sw;
+        if (w < wave) wp = Op::apply(wp, sw);
+        tot = Op::apply(tot, sw);
     }
     __syncthreads();
     *total = tot;
-    return wp + inc - v;
+    return lane == 0 ? wp : Op::apply(wp, below);
 }
 
-template <typename T>
+template <typename T, typename Op = OpSum>
 __device__ __forceinline__ T block_sum(T v, T* s_wave) {
     T tot;
-    (void)block_exclusive_scan(v, &tot, s_wave);
+    (void)block_exclusive_scan<T, Op>(v, &tot, s_wave);
     return tot;
 }
 
@@ -64,86 +81,86 @@ __device__ __forceinline__ T block_sum(T v, T* s_wave) {
 constexpr int kScanItems = 16;
 constexpr size_t kScanTile = static_cast<size_t>(kBlock) * kScanItems;
 
-template <typename T>
+template <typename T, typename Op>
 __global__ __launch_bounds__(kBlock) void scan_reduce_kernel(const T* __restrict__ in, size_t n,
                                                              T* __restrict__ sums) {
     __shared__ T s_wave[kWaves];
     const size_t base = blockIdx.x * kScanTile + static_cast<size_t>(threadIdx.x) * kScanItems;
-    T acc = T(0);
+    T acc = Op::template identity<T>();
 #pragma unroll
     for (int j = 0; j < kScanItems; ++j) {
         const size_t i = base + j;
-        if (i < n) acc += in[i];
+        if (i < n) acc = Op::apply(acc, in[i]);
     }
-    const T tot = block_sum(acc, s_wave);
+    const T tot = block_sum<T, Op>(acc, s_wave);
     if (threadIdx.x == 0) sums[blockIdx.x] = tot;
 }
 
 // Single block: exclusive scan of sums[0..nb) in place; sums[nb] = total.
-template <typename T>
+template <typename T, typename Op>
 __global__ __launch_bounds__(kBlock) void scan_sums_kernel(T* __restrict__ sums, size_t nb) {
     __shared__ T s_wave[kWaves];
-    T carry = T(0);
+    T carry = Op::template identity<T>();
     for (size_t chunk = 0; chunk < nb; chunk += kScanTile) {
         const size_t base = chunk + static_cast<size_t>(threadIdx.x) * kScanItems;
         T v[kScanItems];
-        T acc = T(0);
+        T acc = Op::template identity<T>();
 #pragma unroll
         for (int j = 0; j < kScanItems; ++j) {
             const size_t i = base + j;
-            v[j] = i < nb ? sums[i] : T(0);
-            acc += v[j];
+            v[j] = i < nb ? sums[i] : Op::template identity<T>();
+            acc = Op::apply(acc, v[j]);
         }
         T tot;
-        T run = carry + block_exclusive_scan(acc, &tot, s_wave);
+        T run = Op::apply(carry, block_exclusive_scan<T, Op>(acc, &tot, s_wave));
 #pragma unroll
         for (int j = 0; j < kScanItems; ++j) {
             const size_t i = base + j;
             if (i < nb) sums[i] = run;
-            run += v[j];
+            run = Op::apply(run, v[j]);
         }
-        carry += tot;
+        carry = Op::apply(carry, tot);
         __syncthreads();
     }
     if (threadIdx.x == 0) sums[nb] = carry;
 }
 
-template <typename T, bool Inclusive>
+template <typename T, bool Inclusive, typename Op>
 __global__ __launch_bounds__(kBlock) void scan_apply_kernel(const T* in, T* out, size_t n,
                                                             const T* __restrict__ sums) {
     __shared__ T s_wave[kWaves];
     const size_t base = blockIdx.x * kScanTile + static_cast<size_t>(threadIdx.x) * kScanItems;
     T v[kScanItems];
-    T acc = T(0);
+    T acc = Op::template identity<T>();
 #pragma unroll
     for (int j = 0; j < kScanItems; ++j) {
         const size_t i = base + j;
-        v[j] = i < n ? in[i] : T(0);
-        acc += v[j];
+        v[j] = i < n ? in[i] : Op::template identity<T>();
+        acc = Op::apply(acc, v[j]);
     }
     T tot;
-    T run = sums[blockIdx.x] + block_exclusive_scan(acc, &tot, s_wave);
+    T run = Op::apply(sums[blockIdx.x], block_exclusive_scan<T, Op>(acc, &tot, s_wave));
 #pragma unroll
     for (int j = 0; j < kScanItems; ++j) {
         const size_t i = base + j;
-        if (Inclusive) run += v[j];
+        if (Inclusive) run = Op::apply(run, v[j]);
         if (i < n) out[i] = run;
-        if (!Inclusive) run += v[j];
+        if (!Inclusive) run = Op::apply(run, v[j]);
     }
     if (!Inclusive && blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) out[n] = sums[gridDim.x];
 }
 
-template <typename T, bool Inclusive>
+template <typename T, bool Inclusive, typename Op = OpSum>
 void scan_impl(const T* in, T* out, size_t n, T* scratch, hipStream_t s) {
     if (n == 0) {
         if (!Inclusive) check_hip(hipMemsetAsync(out, 0, sizeof(T), s), "scan memset");
         return;
     }
     const size_t nb = (n + kScanTile - 1) / kScanTile;
-    hipLaunchKernelGGL((scan_reduce_kernel<T>), dim3(nb), dim3(kBlock), 0, s, in, n, scratch);
-    hipLaunchKernelGGL((scan_sums_kernel<T>), dim3(1), dim3(kBlock), 0, s, scratch, nb);
-    hipLaunchKernelGGL((scan_apply_kernel<T, Inclusive>), dim3(nb), dim3(kBlock), 0, s, in, out, n,
-                       scratch);
+    hipLaunchKernelGGL((scan_reduce_kernel<T, Op>), dim3(nb), dim3(kBlock), 0, s, in, n, scratch);
+    hipLaunchKernelGGL((scan_sums_kernel<T, Op>), dim3(1), dim3(kBlock), 0, s, scratch, nb);
+    hipLaunchKernelGGL((scan_apply_kernel<T, Inclusive, Op>), dim3(nb), dim3(kBlock), 0, s, in,
+                       out, n, scratch);
     check_hip(hipGetLastError(), "scan launch");
 }
 
@@ -389,6 +406,9 @@ void exclusive_scan_u64(const uint64_t* in, uint64_t* out, size_t n, uint64_t* s
 }
 void inclusive_scan_f64(double* data, size_t n, double* scratch, hipStream_t s) {
     scan_impl<double, true>(data, data, n, scratch, s);
+}
+void running_max_f64(double* data, size_t n, double* scratch, hipStream_t s) {
+    scan_impl<double, true, OpMax>(data, data, n, scratch, s);
 }
 
 int radix_sort_u64(uint64_t* keys0, uint32_t* vals0, uint64_t* keys1, uint32_t* vals1, size_t n,

@@ -48,6 +48,8 @@ struct DirView {
     uint32_t idx_size;
     const double* w;  // per-node cumulative weights of the sampled direction
     uint64_t w_size;
+    const uint32_t* wx_off;  // their search index: per-node base ...
+    const double* wx;        // ... and levels (nullptr: none)
 };
 
 // Picker families the walk kernel is specialised for: only index pickers
@@ -67,6 +69,7 @@ struct WalkGraph {
     uint32_t T;
     const double* gw;  // global cumulative weights of the sampled direction
     uint64_t gw_size;
+    const double* gwx;  // their search index (nullptr: none)
     const uint8_t* active;
     int32_t active_size;
     DirView d;
@@ -154,6 +157,71 @@ __device__ __forceinline__ Sel edge_of(const WalkGraph& g, uint32_t e, long grou
     return Sel{g.src[e], g.dst[e], static_cast<int32_t>(e), static_cast<int32_t>(group)};
 }
 
+// Entries below `target` in an aligned block of 16 cumulative weights (one
+// 128-byte line; padding is +inf).
+__device__ __forceinline__ uint32_t count_below16(const double* p, double target) {
+    const double2* q = reinterpret_cast<const double2*>(p);
+    uint32_t c = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const double2 v = q[j];
+        c += (v.x < target ? 1u : 0u) + (v.y < target ? 1u : 0u);
+    }
+    return c;
+}
+
+// lower_bound over one segment's non-decreasing cumulative weights w[0, G),
+// i.e. the number of entries below target -- the same answer as the
+// reference's binary search.  A segment with a search index `lv` descends it
+// from the top level: if c entries of level k are below target, the answer's
+// level-(k-1) entries below target end inside block c - 1 (all 16 entries of
+// which lie in one aligned line), and so on down to w itself.
+__device__ __forceinline__ uint32_t weight_lower_bound(const double* w, uint32_t G,
+                                                       const double* lv, double target) {
+    if (lv == nullptr || G <= kWIdxMin) {
+        uint32_t lo = 0, hi = G;
+        while (lo < hi) {
+            const uint32_t mid = lo + ((hi - lo) >> 1);
+            if (w[mid] < target) lo = mid + 1;
+            else hi = mid;
+        }
+        return lo;
+    }
+    uint64_t span = wx_top_span(G);
+    uint32_t n = wx_level_entries(G, span);
+    const double* A = lv;
+    uint32_t c = count_below16(A, target);
+    if (c == 0) return 0;
+    while (span > 16) {
+        A += wx_pad16(n);
+        span >>= 4;
+        n = wx_level_entries(G, span);
+        const uint32_t b = (c - 1) * 16;
+        c = b + count_below16(A + b, target);
+    }
+    const uint32_t b = (c - 1) * 16;
+    const uint32_t m = G - b < 16 ? G - b : 16;
+    uint32_t k = 0;
+    for (uint32_t j = 0; j < m; ++j) k += w[b + j] < target ? 1u : 0u;
+    return b + k;
+}
+
+// pick_exponential_weights (random/pickers.cuh:84-126) over the slice
+// [gs, ge) of the segment [seg, seg + G) that holds it: the lower_bound over
+// the whole segment, clamped to the slice, is the slice's lower_bound because
+// the segment is non-decreasing.
+__device__ __forceinline__ int pick_weights(const double* w, uint64_t wsize, uint64_t gs,
+                                            uint64_t ge, double r, uint64_t slice_start,
+                                            uint64_t seg, uint32_t G, const double* lv) {
+    if (gs >= ge || ge > wsize) return -1;
+    const double start_sum = gs > slice_start ? w[gs - 1] : 0.0;
+    const double end_sum = w[ge - 1];
+    if (end_sum < start_sum) return -1;
+    const double target = start_sum + r * (end_sum - start_sum);
+    const uint64_t x = seg + weight_lower_bound(w + seg, G, lv, target);
+    return static_cast<int>(x < gs ? gs : (x > ge ? ge : x));
+}
+
 // Number of unique timestamps below t: groups at or past this rank have
 // timestamps >= t.
 __device__ __forceinline__ int32_t rank_lower_bound(const WalkGraph& g, int64_t t) {
@@ -177,7 +245,7 @@ __device__ Sel start_edge(const WalkGraph& g, int picker, double rg, double re) 
         group = idx;
     } else {
         if (picker != kExponentialWeight && picker != kTemporalNode2Vec) return no_edge();
-        group = pick_exponential_weights(g.gw, g.gw_size, 0, g.T, rg, 0);
+        group = pick_weights(g.gw, g.gw_size, 0, g.T, rg, 0, 0, g.T, g.gwx);
         // an index past the last group reads as an empty range in the
         // reference (get_timestamp_group_range_host, edge_selectors.cuh:38-43)
         if (group == -1 || static_cast<uint32_t>(group) >= g.T) return no_edge();
@@ -207,7 +275,7 @@ __device__ __forceinline__ bool adjacent(const WalkGraph& g, int prev, int cand)
 // positions.  The candidate node of a proposal is its record's neighbour
 // (get_candidate_node, walk_step_helpers.cuh:40-54).
 __device__ Hop tn2v_pick(const WalkGraph& g, int prev, uint32_t vb, uint32_t ve, uint32_t gb,
-                         uint32_t ge, double rg, double re) {
+                         uint32_t ge, const double* lv, double rg, double re) {
     if (vb >= ve || prev == -1) return no_hop();
     double bmax = 1.0;
     if (g.inv_p > bmax) bmax = g.inv_p;
@@ -218,7 +286,7 @@ __device__ Hop tn2v_pick(const WalkGraph& g, int prev, uint32_t vb, uint32_t ve,
         const double gr = derive_uniform(rg, re, retry * 3 + 0);
         const double er = derive_uniform(rg, re, retry * 3 + 1);
         const double ar = derive_uniform(rg, re, retry * 3 + 2);
-        const int gp = pick_exponential_weights(g.d.w, g.d.w_size, vb, ve, gr, gb);
+        const int gp = pick_weights(g.d.w, g.d.w_size, vb, ve, gr, gb, gb, ge - gb, lv);
         if (gp == -1) return no_hop();
         // a pick one past the node's last group is an empty range in the
         // reference (get_node_group_edge_end, walk_step_helpers.cuh:19-38)
@@ -272,12 +340,15 @@ __device__ Hop node_edge_at(const WalkGraph& g, int picker, int node, int32_t t,
         const int index = pick_index(picker, 0, avail, !Fwd, rg);
         if (index == -1 || index >= avail) return no_hop();
         gpos = gb + static_cast<uint32_t>(vb + index);
-    } else if (picker == kTemporalNode2Vec && prev != -1) {
-        return tn2v_pick(g, prev, gb + vb, gb + ve, gb, ge, rg, re);
     } else {
+        const double* lv =
+            (g.d.wx && G > static_cast<int>(kWIdxMin)) ? g.d.wx + g.d.wx_off[node] : nullptr;
+        if (picker == kTemporalNode2Vec && prev != -1)
+            return tn2v_pick(g, prev, gb + vb, gb + ve, gb, ge, lv, rg, re);
         // ExponentialWeight, or node2vec's first hop (no previous node)
         if (picker != kExponentialWeight && picker != kTemporalNode2Vec) return no_hop();
-        const int p = pick_exponential_weights(g.d.w, g.d.w_size, gb + vb, gb + ve, rg, gb);
+        const int p = pick_weights(g.d.w, g.d.w_size, gb + vb, gb + ve, rg, gb, gb,
+                                   static_cast<uint32_t>(G), lv);
         if (p == -1) return no_hop();
         gpos = static_cast<uint32_t>(p);
     }
@@ -830,6 +901,10 @@ void Engine::sample(const trw_sample_params& p) {
     g.T = static_cast<uint32_t>(T);
     g.gw = forward ? fwd_cum.p : bwd_cum.p;
     g.gw_size = weights_ready ? T : 0;
+    {
+        const DBuf<double>& gx = forward ? gwx_fwd : gwx_bwd;
+        g.gwx = weights_ready && gx.n ? gx.p : nullptr;
+    }
     g.active = active.p;
     g.active_size = static_cast<int32_t>(active.n);
     g.d.hdr = d.hdr.p;
@@ -837,15 +912,15 @@ void Engine::sample(const trw_sample_params& p) {
     g.d.pan = d.pan.p;
     g.d.rec = d.rec.p;
     g.d.idx_size = static_cast<uint32_t>(d.n_entries);
-    if (forward) {
-        g.d.w = out.w_fwd.p;
-        g.d.w_size = weights_ready ? out.n_groups : 0;
-    } else if (cfg.is_directed) {
-        g.d.w = in.w_bwd.p;
-        g.d.w_size = weights_ready ? in.n_groups : 0;
-    } else {
-        g.d.w = out.w_bwd.p;
-        g.d.w_size = weights_ready ? out.n_groups : 0;
+    {
+        // per-node weights of the sampled direction and their search index
+        const DirIndex& wd = (!forward && cfg.is_directed) ? in : out;
+        const DBuf<double>& w = forward ? wd.w_fwd : wd.w_bwd;
+        const DBuf<double>& wx = forward ? wd.wx_fwd : wd.wx_bwd;
+        g.d.w = w.p;
+        g.d.w_size = weights_ready ? wd.n_groups : 0;
+        g.d.wx_off = wd.wx_off.p;
+        g.d.wx = weights_ready && wx.n ? wx.p : nullptr;
     }
     g.adj_off = adj_ready ? adj_off.p : nullptr;
     g.adj_nbr = adj_nbr.p;
