@@ -153,21 +153,20 @@ trw_status trw_add_edges(void* handle, const int32_t* sources, const int32_t* ta
         if (n == 0) return;  // core/temporal_random_walk.cu:285
         if (!sources || !targets || !timestamps) throw trw::InvalidArgument("null edge arrays");
         trw::validate_batch(e, edge_features, n, feature_dim);
-        hipStream_t s = e.stream;
+        e.sync();  // the staging buffers may still feed earlier work
         e.stage_src.resize(n);
         e.stage_dst.resize(n);
         e.stage_ts.resize(n);
-        trw::check_hip(hipMemcpyAsync(e.stage_src.p, sources, n * 4, hipMemcpyHostToDevice, s), "H2D");
-        trw::check_hip(hipMemcpyAsync(e.stage_dst.p, targets, n * 4, hipMemcpyHostToDevice, s), "H2D");
-        trw::check_hip(hipMemcpyAsync(e.stage_ts.p, timestamps, n * 8, hipMemcpyHostToDevice, s), "H2D");
+        std::vector<trw::HostCopy> segs = {{e.stage_src.p, sources, n * 4},
+                                           {e.stage_dst.p, targets, n * 4},
+                                           {e.stage_ts.p, timestamps, n * 8}};
         const float* df = nullptr;
         if (edge_features && feature_dim) {
             e.stage_feat.resize(n * feature_dim);
-            trw::check_hip(hipMemcpyAsync(e.stage_feat.p, edge_features, n * feature_dim * 4,
-                                          hipMemcpyHostToDevice, s),
-                           "H2D");
+            segs.push_back({e.stage_feat.p, edge_features, n * feature_dim * 4});
             df = e.stage_feat.p;
         }
+        e.copy_staged(segs.data(), segs.size(), true);
         e.build(e.stage_src.p, e.stage_dst.p, e.stage_ts.p, df, n, feature_dim);
     });
 }
@@ -224,7 +223,7 @@ trw_status trw_sample(void* handle, const trw_sample_params* params, trw_walks* 
                 r.feature_dim = static_cast<int32_t>(e.feat_dim);
                 take(r.edge_features, e.w_feat.p, e.w_feat.n);
             }
-            e.copy_to_host(segs.data(), segs.size());
+            e.copy_staged(segs.data(), segs.size(), false);
         } catch (...) {
             trw_walks_free(&r);
             throw;

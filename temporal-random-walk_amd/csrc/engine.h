@@ -307,9 +307,10 @@ struct Engine {
 
     size_t memory_used() const;
 
-    // Waits for the engine stream, then copies every span to the host
-    // (pinned staging, several threads); records timings.handoff_*.
-    void copy_to_host(const HostCopy* segs, size_t nseg);
+    // Waits for the engine stream, then copies every span between host and
+    // device (pinned staging, several threads); a device -> host copy records
+    // timings.handoff_*.  Returns when every byte has landed.
+    void copy_staged(const HostCopy* segs, size_t nseg, bool to_device);
 };
 
 // ---- launchers implemented in build.hip / walk.hip -------------------------

@@ -1,4 +1,5 @@
-// handoff.hip -- delivery of device walk buffers into caller-owned host arrays.
+// handoff.hip -- staged copies between caller host memory and HBM: walk
+// buffers out to caller-owned host arrays, edge batches in.
 //
 // The reference fills its host walk set with one blocking cudaMemcpy per array
 // into malloc'd memory (data/walk_set/walk_set_host.cu:55-85).  On this host a
@@ -12,6 +13,9 @@
 //    queue; each thread owns a HIP stream and two pinned staging buffers, so
 //    the DMA of its next chunk overlaps its memcpy of the current one, and
 //    the page faults of the destination are taken by all threads at once.
+// Host-pointer ingest (trw_add_edges) uses the same lanes in the other
+// direction: the reference copies each batch array with one blocking
+// cudaMemcpy (data/buffer.cuh:135-149).
 #include <stdlib.h>
 #include <string.h>
 #include <sys/mman.h>
@@ -75,18 +79,19 @@ void HostLane::init() {
     for (auto& e : done) check_hip(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate");
 }
 
-void Engine::copy_to_host(const HostCopy* segs, size_t nseg) {
+void Engine::copy_staged(const HostCopy* segs, size_t nseg, bool to_device) {
     size_t total = 0;
     for (size_t i = 0; i < nseg; ++i) total += segs[i].bytes;
-    // producers of the device buffers run on the engine stream
+    // earlier work on the engine stream may still read or write these buffers
     sync();
     const auto t0 = std::chrono::steady_clock::now();
+    const hipMemcpyKind kind = to_device ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost;
 
     if (total < kDirectBelow) {
         for (size_t i = 0; i < nseg; ++i)
             if (segs[i].bytes)
-                check_hip(hipMemcpyAsync(segs[i].dst, segs[i].src, segs[i].bytes,
-                                         hipMemcpyDeviceToHost, stream), "D2H");
+                check_hip(hipMemcpyAsync(segs[i].dst, segs[i].src, segs[i].bytes, kind, stream),
+                          "copy");
         sync();
     } else {
         // chunk c of the whole transfer: segment seg_of[c], offset off_of[c]
@@ -105,38 +110,69 @@ void Engine::copy_to_host(const HostCopy* segs, size_t nseg) {
         std::atomic<bool> failed{false};
         std::mutex err_mu;
         std::string err;
+        auto chunk = [&](size_t c, size_t* n) {
+            const HostCopy& s = segs[seg_of[c]];
+            *n = std::min(kChunk, s.bytes - off_of[c]);
+            return s;
+        };
+        // device -> host: the DMA of a lane's next chunk into one staging
+        // buffer overlaps its memcpy of the other out to the destination
+        auto to_host = [&](HostLane& ln) {
+            size_t held[2];
+            size_t bytes_of[2] = {0, 0};
+            auto issue = [&](int b) -> bool {
+                const size_t c = next.fetch_add(1);
+                if (c >= nchunks || failed.load()) return false;
+                size_t n;
+                const HostCopy& s = chunk(c, &n);
+                check_hip(hipMemcpyAsync(ln.stage[b], static_cast<const char*>(s.src) + off_of[c], n,
+                                         hipMemcpyDeviceToHost, ln.stream),
+                          "D2H stage");
+                check_hip(hipEventRecord(ln.done[b], ln.stream), "hipEventRecord");
+                held[b] = c;
+                bytes_of[b] = n;
+                return true;
+            };
+            bool more[2] = {issue(0), false};
+            if (more[0]) more[1] = issue(1);
+            int live = more[0] + more[1];
+            for (int b = 0; live > 0; b ^= 1) {
+                if (!more[b]) continue;
+                check_hip(hipEventSynchronize(ln.done[b]), "hipEventSynchronize");
+                const size_t c = held[b];
+                memcpy(static_cast<char*>(segs[seg_of[c]].dst) + off_of[c], ln.stage[b], bytes_of[b]);
+                more[b] = issue(b);
+                if (!more[b]) --live;
+            }
+        };
+        // host -> device: a lane fills one staging buffer while the DMA of
+        // the other is in flight, waiting only before it refills a buffer
+        auto to_dev = [&](HostLane& ln) {
+            bool pending[2] = {false, false};
+            for (int b = 0;; b ^= 1) {
+                const size_t c = next.fetch_add(1);
+                if (c >= nchunks || failed.load()) break;
+                size_t n;
+                const HostCopy& s = chunk(c, &n);
+                if (pending[b]) check_hip(hipEventSynchronize(ln.done[b]), "hipEventSynchronize");
+                memcpy(ln.stage[b], static_cast<const char*>(s.src) + off_of[c], n);
+                check_hip(hipMemcpyAsync(static_cast<char*>(s.dst) + off_of[c], ln.stage[b], n,
+                                         hipMemcpyHostToDevice, ln.stream),
+                          "H2D stage");
+                check_hip(hipEventRecord(ln.done[b], ln.stream), "hipEventRecord");
+                pending[b] = true;
+            }
+            check_hip(hipStreamSynchronize(ln.stream), "hipStreamSynchronize");
+        };
         auto worker = [&](int t) {
             HostLane& ln = *lanes[t];
             try {
                 check_hip(hipSetDevice(device), "hipSetDevice");
-                size_t held[2];
-                size_t bytes_of[2] = {0, 0};
-                int live = 0;
-                auto issue = [&](int b) -> bool {
-                    const size_t c = next.fetch_add(1);
-                    if (c >= nchunks || failed.load()) return false;
-                    const HostCopy& s = segs[seg_of[c]];
-                    const size_t n = std::min(kChunk, s.bytes - off_of[c]);
-                    check_hip(hipMemcpyAsync(ln.stage[b], static_cast<const char*>(s.src) + off_of[c],
-                                             n, hipMemcpyDeviceToHost, ln.stream), "D2H stage");
-                    check_hip(hipEventRecord(ln.done[b], ln.stream), "hipEventRecord");
-                    held[b] = c;
-                    bytes_of[b] = n;
-                    return true;
-                };
-                bool more[2] = {issue(0), false};
-                if (more[0]) more[1] = issue(1);
-                live = more[0] + more[1];
-                for (int b = 0; live > 0; b ^= 1) {
-                    if (!more[b]) continue;
-                    check_hip(hipEventSynchronize(ln.done[b]), "hipEventSynchronize");
-                    const size_t c = held[b];
-                    memcpy(static_cast<char*>(segs[seg_of[c]].dst) + off_of[c], ln.stage[b], bytes_of[b]);
-                    more[b] = issue(b);
-                    if (!more[b]) --live;
-                }
+                if (to_device) to_dev(ln);
+                else to_host(ln);
             } catch (const std::exception& ex) {
                 failed.store(true);
+                (void)hipStreamSynchronize(ln.stream);  // no DMA may outlive the call
                 std::lock_guard<std::mutex> g(err_mu);
                 if (err.empty()) err = ex.what();
             }
@@ -148,9 +184,12 @@ void Engine::copy_to_host(const HostCopy* segs, size_t nseg) {
         for (auto& th : pool) th.join();
         if (failed.load()) throw std::runtime_error("host copy: " + err);
     }
-    timings.handoff_ms =
+    const double ms =
         std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
-    timings.handoff_bytes = total;
+    if (!to_device) {
+        timings.handoff_ms = ms;
+        timings.handoff_bytes = total;
+    }
 }
 
 }  // namespace trw

@@ -392,3 +392,26 @@ def test_normal_mode_chi_square_against_independent_draws(picker):
                        ("length", ref.lens.astype(np.int64), got.lens.astype(np.int64))]:
         pv = _chi2_two_sample(np.asarray(a), np.asarray(b))
         assert pv > 0.01, f"{picker}: {name} p = {pv:.3g}"
+
+
+def test_staged_host_ingest_matches_device_ingest():
+    """trw_add_edges copies batches above 32 MiB through the staged lanes
+    (pinned buffers, several threads); the store and index must equal those
+    of the same batch handed over in HBM (trw_add_edges_device)."""
+    import torch
+
+    from temporal_random_walk import capi
+
+    s, d, t = graphs.powerlaw(200_000, 5_000_000, s=1.7, n_ts=50_000, seed=71)
+    feat = np.random.default_rng(71).standard_normal((s.size, 3)).astype(np.float32)
+    a = capi.Engine(is_directed=True, global_seed=5, shuffle_walk_order=False)
+    a.add_edges(s, d, t, feat)
+    b = capi.Engine(is_directed=True, global_seed=5, shuffle_walk_order=False)
+    dv = [torch.from_numpy(x).cuda() for x in (s, d, t, feat)]
+    torch.cuda.synchronize()
+    b.add_edges_device(dv[0].data_ptr(), dv[1].data_ptr(), dv[2].data_ptr(), s.size,
+                       dv[3].data_ptr(), 3)
+    for name in ("sources", "targets", "timestamps", "edge_features", *INDEX_ARRAYS):
+        assert np.array_equal(a.array(name), b.array(name)), name
+    a.close()
+    b.close()
