@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TRW_ABI_VERSION 2
+#define TRW_ABI_VERSION 3
 
 typedef enum trw_status {
     TRW_OK = 0,
@@ -232,19 +232,35 @@ trw_status trw_get_timings(void* handle, trw_timings* out);
  * work against it. */
 trw_status trw_get_stream(void* handle, void** out_stream);
 /* Statistics of the last sample, computed on the device after the fact (not
- * part of any timing).  algorithmic_bytes is the compulsory traffic of the
- * walk kernel: per walk 24 B (start-edge reads + length); 8 B for slot 0 and
- * 12 B for slot 1 when written (node, timestamp rank, 32-bit edge id); per hop
- * selected at node u 36 + 4*ceil(log2(G_u + 1)) B (G_u = u's timestamp groups
- * in the sampled direction: the node's group range 8 B, one 4 B rank per
- * binary-search probe, the picked group's range 8 B, the edge record 8 B and
- * that hop's 12 B of output).  Padding and the int64 widening are the layout
+ * part of any timing).  Both byte counts are compulsory traffic of the walk
+ * path, summed over the walks of the last sample; G_u is the number of
+ * timestamp groups of the node u a hop is selected at, in the sampled
+ * direction, and p_u = ceil(log2(G_u + 1)) the probes of a binary search over
+ * them.
+ *
+ * reference_bytes uses the reference's element types (size_t offsets and
+ * indices, int64 timestamps): per hop 72 + 8 p_u B (the node's group range
+ * 16, one 8 B timestamp per probe, the picked group's edge range 16, the
+ * sorted edge index 8, next node + timestamp 12, the hop's output node 4 +
+ * timestamp 8 + edge id 8); per walk 8 B for the length, the start (32 B
+ * unconstrained: timestamp-group range 16, edge endpoints and time 16; 52 B
+ * from a given node: group range 16, edge range 16, edge index 8, next node
+ * and time 12) and the output of slot 0 (12 B) and slot 1 (20 B) when
+ * written.
+ *
+ * algorithmic_bytes is the same sum restated for this engine's 4-byte
+ * positions and timestamp ranks: per walk 24 B (start-edge reads + length);
+ * 8 B for slot 0 and 12 B for slot 1 when written (node, timestamp rank,
+ * 32-bit edge id); per hop 36 + 4 p_u B (the node's group range 8 B, one 4 B
+ * rank per probe, the picked group's range 8 B, the edge record 8 B and that
+ * hop's 12 B of output).  Padding and the int64 widening are the layout
  * pass's, not the walk kernel's. */
 typedef struct trw_walk_stats {
     uint64_t total_len;         /* sum of walk_lens: walk steps (reference metric) */
     uint64_t transitions;       /* sum of max(len - 1, 0) */
     uint64_t nonempty_walks;
     uint64_t algorithmic_bytes;
+    uint64_t reference_bytes;
 } trw_walk_stats;
 trw_status trw_get_walk_stats(void* handle, trw_walk_stats* out);
 

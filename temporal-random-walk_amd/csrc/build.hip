@@ -36,20 +36,35 @@ inline unsigned grid_for(size_t n) {
 
 inline int bit_length_u64(uint64_t v) { return v ? 64 - __builtin_clzll(v) : 0; }
 
-__global__ void make_ts_keys_kernel(const int64_t* __restrict__ old_ts, size_t e_old,
-                                    const int64_t* __restrict__ new_ts, size_t n_new,
-                                    int64_t tmin, uint64_t* __restrict__ keys,
-                                    uint32_t* __restrict__ vals) {
+// Sort keys (ts - ts_min, 32-bit when the store's key range fits), positions,
+// and each edge's endpoints packed into one 8-byte word, so that the gather
+// after the sort costs one random load per edge instead of three.
+template <typename K>
+__global__ void make_ts_keys_kernel(const int64_t* __restrict__ old_ts,
+                                    const int32_t* __restrict__ old_src,
+                                    const int32_t* __restrict__ old_dst, size_t e_old,
+                                    const int64_t* __restrict__ new_ts,
+                                    const int32_t* __restrict__ new_src,
+                                    const int32_t* __restrict__ new_dst, size_t n_new,
+                                    int64_t tmin, K* __restrict__ keys,
+                                    uint32_t* __restrict__ vals, uint64_t* __restrict__ ends) {
     const size_t i = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
     if (i >= e_old + n_new) return;
-    const int64_t t = i < e_old ? old_ts[i] : new_ts[i - e_old];
-    keys[i] = static_cast<uint64_t>(t) - static_cast<uint64_t>(tmin);
+    const bool old = i < e_old;
+    const size_t k = old ? i : i - e_old;
+    const int64_t t = old ? old_ts[k] : new_ts[k];
+    const int32_t a = old ? old_src[k] : new_src[k];
+    const int32_t b = old ? old_dst[k] : new_dst[k];
+    keys[i] = static_cast<K>(static_cast<uint64_t>(t) - static_cast<uint64_t>(tmin));
     vals[i] = static_cast<uint32_t>(i);
+    ends[i] = static_cast<uint64_t>(static_cast<uint32_t>(a)) |
+              (static_cast<uint64_t>(static_cast<uint32_t>(b)) << 32);
 }
 
 // out[0] = number of sorted keys <= target (upper_bound), out[1] = key at
 // that position (or 0), out[2] = last key.  target < 0 means "none".
-__global__ void evict_search_kernel(const uint64_t* __restrict__ keys, size_t n, int64_t target,
+template <typename K>
+__global__ void evict_search_kernel(const K* __restrict__ keys, size_t n, int64_t target,
                                     int64_t* out) {
     size_t del = 0;
     if (target >= 0) {
@@ -57,7 +72,7 @@ __global__ void evict_search_kernel(const uint64_t* __restrict__ keys, size_t n,
         const uint64_t t = static_cast<uint64_t>(target);
         while (lo < hi) {
             const size_t mid = lo + ((hi - lo) >> 1);
-            if (t < keys[mid]) hi = mid;
+            if (t < static_cast<uint64_t>(keys[mid])) hi = mid;
             else lo = mid + 1;
         }
         del = lo;
@@ -67,25 +82,20 @@ __global__ void evict_search_kernel(const uint64_t* __restrict__ keys, size_t n,
     out[2] = n ? static_cast<int64_t>(keys[n - 1]) : 0;
 }
 
-__global__ void gather_store_kernel(const uint32_t* __restrict__ perm, size_t del, size_t kept,
-                                    const int32_t* __restrict__ os, const int32_t* __restrict__ od,
-                                    const int64_t* __restrict__ ot, size_t e_old,
-                                    const int32_t* __restrict__ ns, const int32_t* __restrict__ nd,
-                                    const int64_t* __restrict__ nt, int32_t* __restrict__ s,
+// The kept suffix [del, del + kept) of the sorted order: the timestamp is the
+// sorted key plus ts_min (exact in 64-bit wrap-around arithmetic), the
+// endpoints one packed load at the edge's old position.
+template <typename K>
+__global__ void gather_store_kernel(const K* __restrict__ keys, const uint32_t* __restrict__ perm,
+                                    const uint64_t* __restrict__ ends, size_t del, size_t kept,
+                                    int64_t tmin, int32_t* __restrict__ s,
                                     int32_t* __restrict__ d, int64_t* __restrict__ t) {
     const size_t j = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
     if (j >= kept) return;
-    const uint32_t id = perm[del + j];
-    if (id < e_old) {
-        s[j] = os[id];
-        d[j] = od[id];
-        t[j] = ot[id];
-    } else {
-        const size_t k = id - e_old;
-        s[j] = ns[k];
-        d[j] = nd[k];
-        t[j] = nt[k];
-    }
+    const uint64_t sd = ends[perm[del + j]];
+    s[j] = static_cast<int32_t>(static_cast<uint32_t>(sd));
+    d[j] = static_cast<int32_t>(static_cast<uint32_t>(sd >> 32));
+    t[j] = static_cast<int64_t>(static_cast<uint64_t>(keys[del + j]) + static_cast<uint64_t>(tmin));
 }
 
 // Grid-stride over kept * dim values (can exceed one dispatch's 32-bit
@@ -622,14 +632,12 @@ void build_direction(Engine& e, DirIndex& dir, size_t n, int key_bits, size_t vc
     dir.n_entries = n;
     const int which = radix_sort_u32(e.k32a.p, e.v32a.p, e.k32b.p, e.v32b.p, n, 0, key_bits,
                                      e.hist.p, e.hist_scratch.p, s);
-    DBuf<uint32_t>& ks = which ? e.k32b : e.k32a;
-    DBuf<uint32_t>& vs = which ? e.v32b : e.v32a;
-    dir.key.resize(n);
-    dir.idx.resize(n);
-    if (n) {
-        check_hip(hipMemcpyAsync(dir.key.p, ks.p, n * 4, hipMemcpyDeviceToDevice, s), "copy keys");
-        check_hip(hipMemcpyAsync(dir.idx.p, vs.p, n * 4, hipMemcpyDeviceToDevice, s), "copy idx");
-    }
+    // the sorted buffers become the direction's arrays (the scratch takes the
+    // old ones, which every user sizes again before writing)
+    dir.key.swap(which ? e.k32b : e.k32a);
+    dir.idx.swap(which ? e.v32b : e.v32a);
+    dir.key.n = n;
+    dir.idx.n = n;
     dir.rec.resize(n);
     hipLaunchKernelGGL(make_records_kernel, dim3(grid_for(n)), dim3(kB), 0, s, dir.key.p, dir.idx.p,
                        e.src.p, e.dst.p, n, rec_mode, dir.rec.p);
@@ -780,19 +788,32 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
     }
     latest_ts = std::max(latest_ts, hs[1]);
 
-    // ---- 2. stable radix sort by (ts, position)
+    // ---- 2. stable radix sort by (ts, position); 32-bit keys when the key
+    // range fits (4-byte key traffic per pass instead of 8)
+    const int bits = bit_length_u64(static_cast<uint64_t>(tmax) - static_cast<uint64_t>(tmin));
+    const bool keys32 = bits <= 32;
     k64a.ensure(etot);
     k64b.ensure(etot);
+    ends64.ensure(etot);
     v32a.ensure(std::max(etot, 2 * etot));
     v32b.ensure(std::max(etot, 2 * etot));
     hist.ensure(radix_hist_elems(2 * etot));
     hist_scratch.ensure(scan_scratch_elems(radix_hist_elems(2 * etot)));
-    hipLaunchKernelGGL(make_ts_keys_kernel, dim3(grid_for(etot)), dim3(kB), 0, s, ts.p, e_old,
-                       d_ts, n, tmin, k64a.p, v32a.p);
-    const int bits = bit_length_u64(static_cast<uint64_t>(tmax) - static_cast<uint64_t>(tmin));
-    const int which = radix_sort_u64(k64a.p, v32a.p, k64b.p, v32b.p, etot, 0, bits, hist.p,
-                                     hist_scratch.p, s);
-    uint64_t* keys = which ? k64b.p : k64a.p;
+    uint32_t* k32s[2] = {reinterpret_cast<uint32_t*>(k64a.p), reinterpret_cast<uint32_t*>(k64b.p)};
+    int which;
+    if (keys32) {
+        hipLaunchKernelGGL((make_ts_keys_kernel<uint32_t>), dim3(grid_for(etot)), dim3(kB), 0, s,
+                           ts.p, src.p, dst.p, e_old, d_ts, d_src, d_dst, n, tmin, k32s[0],
+                           v32a.p, ends64.p);
+        which = radix_sort_u32(k32s[0], v32a.p, k32s[1], v32b.p, etot, 0, bits, hist.p,
+                               hist_scratch.p, s);
+    } else {
+        hipLaunchKernelGGL((make_ts_keys_kernel<uint64_t>), dim3(grid_for(etot)), dim3(kB), 0, s,
+                           ts.p, src.p, dst.p, e_old, d_ts, d_src, d_dst, n, tmin, k64a.p,
+                           v32a.p, ends64.p);
+        which = radix_sort_u64(k64a.p, v32a.p, k64b.p, v32b.p, etot, 0, bits, hist.p,
+                               hist_scratch.p, s);
+    }
     uint32_t* perm = which ? v32b.p : v32a.p;
 
     // ---- 3. window eviction: drop ts <= latest - capacity
@@ -802,7 +823,12 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
         if (cutoff >= tmin) target = static_cast<int64_t>(static_cast<uint64_t>(cutoff) -
                                                           static_cast<uint64_t>(tmin));
     }
-    hipLaunchKernelGGL(evict_search_kernel, dim3(1), dim3(1), 0, s, keys, etot, target, red64.p);
+    if (keys32)
+        hipLaunchKernelGGL((evict_search_kernel<uint32_t>), dim3(1), dim3(1), 0, s, k32s[which],
+                           etot, target, red64.p);
+    else
+        hipLaunchKernelGGL((evict_search_kernel<uint64_t>), dim3(1), dim3(1), 0, s,
+                           which ? k64b.p : k64a.p, etot, target, red64.p);
     check_hip(hipMemcpyAsync(hs, red64.p, 24, hipMemcpyDeviceToHost, s), "read evict");
     sync();
     const size_t del = static_cast<size_t>(hs[0]);
@@ -814,8 +840,16 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
     src2.resize(kept);
     dst2.resize(kept);
     ts2.resize(kept);
-    hipLaunchKernelGGL(gather_store_kernel, dim3(grid_for(kept)), dim3(kB), 0, s, perm, del, kept,
-                       src.p, dst.p, ts.p, e_old, d_src, d_dst, d_ts, src2.p, dst2.p, ts2.p);
+    if (kept) {
+        if (keys32)
+            hipLaunchKernelGGL((gather_store_kernel<uint32_t>), dim3(grid_for(kept)), dim3(kB), 0,
+                               s, k32s[which], perm, ends64.p, del, kept, tmin, src2.p, dst2.p,
+                               ts2.p);
+        else
+            hipLaunchKernelGGL((gather_store_kernel<uint64_t>), dim3(grid_for(kept)), dim3(kB), 0,
+                               s, which ? k64b.p : k64a.p, perm, ends64.p, del, kept, tmin,
+                               src2.p, dst2.p, ts2.p);
+    }
     if (feat_dim > 0) {
         feat2.resize(kept * feat_dim);
         hipLaunchKernelGGL(gather_feat_kernel, dim3(grid_capped(kept * feat_dim)), dim3(kB), 0, s,
@@ -863,6 +897,10 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
         hipLaunchKernelGGL(node_keys_kernel, dim3(grid_for(E)), dim3(kB), 0, s, src.p, E, k32a.p,
                            v32a.p);
         build_direction(*this, out, E, key_bits, vc, 0, hs);
+        k32a.ensure(E);
+        k32b.ensure(E);
+        v32a.ensure(E);
+        v32b.ensure(E);
         hipLaunchKernelGGL(node_keys_kernel, dim3(grid_for(E)), dim3(kB), 0, s, dst.p, E, k32a.p,
                            v32a.p);
         build_direction(*this, in, E, key_bits, vc, 1, hs);

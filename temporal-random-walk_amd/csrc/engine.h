@@ -255,6 +255,7 @@ struct Engine {
 
     // scratch
     DBuf<uint64_t> k64a, k64b;
+    DBuf<uint64_t> ends64;  // packed (src, dst) of the timestamp sort's input
     DBuf<uint32_t> k32a, k32b, v32a, v32b;
     DBuf<uint32_t> hist, hist_scratch, flags, scan, scan_scratch;
     DBuf<uint64_t> scan64_scratch;
@@ -281,6 +282,7 @@ struct Engine {
     uint64_t w_num = 0;
     int w_len = 0;
     int w_dir_forward = 1;
+    int w_constrained = 0;  // the last sample started from given nodes
 
     // pinned host scalars for the few readbacks that size allocations
     void* host_scalars = nullptr;

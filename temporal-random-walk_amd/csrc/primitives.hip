@@ -165,12 +165,17 @@ void scan_impl(const T* in, T* out, size_t n, T* scratch, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
-// radix sort: 8-bit digits, tile = 4 waves x 8 rows x 64 keys = 2048 keys
+// radix sort: 8-bit digits, tile = 4 waves x 8 rows x 64 keys = 2048 keys; a
+// workgroup owns kTilesPerBlock consecutive tiles, so the digit-major
+// histogram has one column per workgroup (fewer scattered histogram writes and
+// a shorter histogram scan per pass)
 // ---------------------------------------------------------------------------
 constexpr int kRadixBits = 8;
 constexpr int kRadix = 1 << kRadixBits;
 constexpr int kRows = 8;
 constexpr size_t kSortTile = static_cast<size_t>(kBlock) * kRows;
+constexpr int kTilesPerBlock = 4;
+constexpr size_t kSortSpan = kSortTile * kTilesPerBlock;
 
 static_assert(kRadix == kBlock, "one thread per digit in the tile epilogue");
 
@@ -199,14 +204,24 @@ __global__ __launch_bounds__(kBlock) void radix_upsweep_kernel(const K* __restri
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     for (int i = threadIdx.x; i < kWaves * kRadix; i += kBlock) (&s_cnt[0][0])[i] = 0;
     __syncthreads();
-    const size_t wave_base = blockIdx.x * kSortTile + static_cast<size_t>(wave) * kRows * 64;
+    for (int t = 0; t < kTilesPerBlock; ++t) {
+        const size_t wave_base = blockIdx.x * kSortSpan + t * kSortTile +
+                                 static_cast<size_t>(wave) * kRows * 64;
+        if (wave_base >= n) break;  // uniform over the wave
+        K key[kRows];
 #pragma unroll
-    for (int r = 0; r < kRows; ++r) {
-        const size_t i = wave_base + static_cast<size_t>(r) * 64 + lane;
-        const bool valid = i < n;
-        const uint32_t d = valid ? static_cast<uint32_t>((keys[i] >> bit) & (kRadix - 1)) : 0u;
-        const uint64_t m = match_digit(d, valid);
-        if (valid && (m & lanes_below(lane)) == 0) s_cnt[wave][d] += __popcll(m);
+        for (int r = 0; r < kRows; ++r) {
+            const size_t i = wave_base + static_cast<size_t>(r) * 64 + lane;
+            key[r] = i < n ? keys[i] : K(0);
+        }
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) {
+            const size_t i = wave_base + static_cast<size_t>(r) * 64 + lane;
+            const bool valid = i < n;
+            const uint32_t d = static_cast<uint32_t>((key[r] >> bit) & (kRadix - 1));
+            const uint64_t m = match_digit(d, valid);
+            if (valid && (m & lanes_below(lane)) == 0) s_cnt[wave][d] += __popcll(m);
+        }
     }
     __syncthreads();
     const int d = threadIdx.x;
@@ -222,48 +237,63 @@ __global__ __launch_bounds__(kBlock) void radix_scatter_kernel(
     uint32_t* __restrict__ vals_out, size_t n, int bit, const uint32_t* __restrict__ offsets,
     size_t nb) {
     __shared__ uint32_t s_cnt[kWaves][kRadix];
+    __shared__ uint32_t s_run[kRadix];  // the workgroup's next output position per digit
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (int i = threadIdx.x; i < kWaves * kRadix; i += kBlock) (&s_cnt[0][0])[i] = 0;
-    __syncthreads();
-    const size_t wave_base = blockIdx.x * kSortTile + static_cast<size_t>(wave) * kRows * 64;
-    K key[kRows];
-    uint32_t val[kRows];
-    uint32_t dig[kRows];
-    uint32_t rank[kRows];
+    s_run[threadIdx.x] = offsets[static_cast<size_t>(threadIdx.x) * nb + blockIdx.x];
+    for (int t = 0; t < kTilesPerBlock; ++t) {
+        const size_t tile_base = blockIdx.x * kSortSpan + t * kSortTile;
+        if (tile_base >= n) break;  // uniform over the workgroup
+        for (int i = threadIdx.x; i < kWaves * kRadix; i += kBlock) (&s_cnt[0][0])[i] = 0;
+        __syncthreads();
+        const size_t wave_base = tile_base + static_cast<size_t>(wave) * kRows * 64;
+        K key[kRows];
+        uint32_t val[kRows];
+        uint32_t dig[kRows];
+        uint32_t rank[kRows];
 #pragma unroll
-    for (int r = 0; r < kRows; ++r) {
-        const size_t i = wave_base + static_cast<size_t>(r) * 64 + lane;
-        const bool valid = i < n;
-        key[r] = valid ? keys_in[i] : K(0);
-        val[r] = (valid && vals_in) ? vals_in[i] : 0u;
-        const uint32_t d = static_cast<uint32_t>((key[r] >> bit) & (kRadix - 1));
-        dig[r] = d;
-        const uint64_t m = match_digit(d, valid);
-        const uint32_t before = __popcll(m & lanes_below(lane));
-        const uint32_t prior = s_cnt[wave][d];
-        rank[r] = prior + before;
-        if (valid && before == 0) s_cnt[wave][d] = prior + __popcll(m);
-    }
-    __syncthreads();
-    {
-        const int d = threadIdx.x;
-        uint32_t run = offsets[static_cast<size_t>(d) * nb + blockIdx.x];
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            const uint32_t c = s_cnt[w][d];
-            s_cnt[w][d] = run;
-            run += c;
+        for (int r = 0; r < kRows; ++r) {
+            const size_t i = wave_base + static_cast<size_t>(r) * 64 + lane;
+            const bool valid = i < n;
+            key[r] = valid ? keys_in[i] : K(0);
+            val[r] = (valid && vals_in) ? vals_in[i] : 0u;
         }
-    }
-    __syncthreads();
 #pragma unroll
-    for (int r = 0; r < kRows; ++r) {
-        const size_t i = wave_base + static_cast<size_t>(r) * 64 + lane;
-        if (i < n) {
-            const uint32_t pos = s_cnt[wave][dig[r]] + rank[r];
-            keys_out[pos] = key[r];
-            if (vals_out) vals_out[pos] = val[r];
+        for (int r = 0; r < kRows; ++r) {
+            const size_t i = wave_base + static_cast<size_t>(r) * 64 + lane;
+            const bool valid = i < n;
+            const uint32_t d = static_cast<uint32_t>((key[r] >> bit) & (kRadix - 1));
+            dig[r] = d;
+            const uint64_t m = match_digit(d, valid);
+            const uint32_t before = __popcll(m & lanes_below(lane));
+            const uint32_t prior = s_cnt[wave][d];
+            rank[r] = prior + before;
+            if (valid && before == 0) s_cnt[wave][d] = prior + __popcll(m);
         }
+        __syncthreads();
+        {
+            // tile epilogue: wave-major exclusive offsets of every digit, then
+            // the running position moves past this tile's keys of the digit
+            const int d = threadIdx.x;
+            uint32_t run = s_run[d];
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                const uint32_t c = s_cnt[w][d];
+                s_cnt[w][d] = run;
+                run += c;
+            }
+            s_run[d] = run;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) {
+            const size_t i = wave_base + static_cast<size_t>(r) * 64 + lane;
+            if (i < n) {
+                const uint32_t pos = s_cnt[wave][dig[r]] + rank[r];
+                keys_out[pos] = key[r];
+                if (vals_out) vals_out[pos] = val[r];
+            }
+        }
+        __syncthreads();  // s_cnt is cleared for the next tile
     }
 }
 
@@ -272,7 +302,7 @@ int radix_sort_impl(K* keys0, uint32_t* vals0, K* keys1, uint32_t* vals1, size_t
                     int begin_bit, int end_bit, uint32_t* hist, uint32_t* hist_scratch,
                     hipStream_t s) {
     if (n <= 1 || end_bit <= begin_bit) return 0;
-    const size_t nb = (n + kSortTile - 1) / kSortTile;
+    const size_t nb = (n + kSortSpan - 1) / kSortSpan;
     int cur = 0;
     K* kb[2] = {keys0, keys1};
     uint32_t* vb[2] = {vals0, vals1};
@@ -394,7 +424,7 @@ int reduce_blocks(size_t n) {
 }  // namespace
 
 size_t scan_scratch_elems(size_t n) { return (n + kScanTile - 1) / kScanTile + 1; }
-size_t radix_hist_elems(size_t n) { return ((n + kSortTile - 1) / kSortTile) * kRadix + 1; }
+size_t radix_hist_elems(size_t n) { return ((n + kSortSpan - 1) / kSortSpan) * kRadix + 1; }
 
 void exclusive_scan_u32(const uint32_t* in, uint32_t* out, size_t n, uint32_t* scratch,
                         hipStream_t s) {

@@ -631,24 +631,34 @@ inline unsigned grid_capped(uint64_t n) {
     return static_cast<unsigned>(g == 0 ? 1 : (g > (1u << 20) ? (1u << 20) : g));
 }
 
-// Walk statistics and algorithmic bytes of the walk kernel (trw_get_walk_stats).
+// Walk statistics and algorithmic bytes of the walk path (trw_get_walk_stats):
+// acc[3] with this engine's 4-byte positions and ranks, acc[4] with the
+// reference's element types.
 __global__ void walk_stats_kernel(const int32_t* __restrict__ nodes,
                                   const uint64_t* __restrict__ lens, uint64_t n, int L,
                                   const uint32_t* __restrict__ cnt, int32_t active_size,
-                                  unsigned long long* acc) {
+                                  int constrained, unsigned long long* acc) {
     const uint64_t w = blockIdx.x * static_cast<uint64_t>(kB) + threadIdx.x;
-    unsigned long long bytes = 0, trans = 0, total = 0, nonempty = 0;
+    unsigned long long bytes = 0, ref = 0, trans = 0, total = 0, nonempty = 0;
     if (w < n && L > 0) {
         const int len = static_cast<int>(lens[w]);
         bytes = 24;
-        if (len >= 1) bytes += 8;
-        if (len >= 2) bytes += 12;
+        ref = 8 + (constrained ? 52 : 32);
+        if (len >= 1) {
+            bytes += 8;
+            ref += 12;
+        }
+        if (len >= 2) {
+            bytes += 12;
+            ref += 20;
+        }
         for (int k = 1; k + 1 < len; ++k) {
             const int u = nodes[w * L + k];
             uint32_t G = 0;
             if (u >= 0 && u < active_size) G = cnt[u + 1] - cnt[u];
             const int probes = G ? 32 - __clz(G) : 0;  // ceil(log2(G + 1))
             bytes += 36 + 4 * probes;
+            ref += 72 + 8 * probes;
         }
         trans = len > 0 ? len - 1 : 0;
         total = len;
@@ -657,6 +667,7 @@ __global__ void walk_stats_kernel(const int32_t* __restrict__ nodes,
     // wave reduction then one atomic per wave
     for (int off = 32; off > 0; off >>= 1) {
         bytes += __shfl_down(bytes, off, 64);
+        ref += __shfl_down(ref, off, 64);
         trans += __shfl_down(trans, off, 64);
         total += __shfl_down(total, off, 64);
         nonempty += __shfl_down(nonempty, off, 64);
@@ -666,6 +677,7 @@ __global__ void walk_stats_kernel(const int32_t* __restrict__ nodes,
         atomicAdd(acc + 1, trans);
         atomicAdd(acc + 2, nonempty);
         atomicAdd(acc + 3, bytes);
+        atomicAdd(acc + 4, ref);
     }
 }
 
@@ -885,6 +897,7 @@ void Engine::sample(const trw_sample_params& p) {
     w_num = nw;
     w_len = L;
     w_dir_forward = forward ? 1 : 0;
+    w_constrained = have_starts ? 1 : 0;
 
     // ---- graph view of the sampled direction
     const bool use_in = !forward && cfg.is_directed;
@@ -1014,23 +1027,24 @@ void Engine::sample(const trw_sample_params& p) {
 
 void walk_stats(Engine& e, trw_walk_stats* out) {
     hipStream_t s = e.stream;
-    e.acc64.ensure(4);
-    check_hip(hipMemsetAsync(e.acc64.p, 0, 32, s), "memset");
+    e.acc64.ensure(5);
+    check_hip(hipMemsetAsync(e.acc64.p, 0, 40, s), "memset");
     const bool use_in = !e.w_dir_forward && e.cfg.is_directed;
     const DirIndex& d = use_in ? e.in : e.out;
     if (e.w_num && e.w_len > 0) {
         hipLaunchKernelGGL(walk_stats_kernel, dim3(grid_for(e.w_num)), dim3(kB), 0, s, e.w_nodes.p,
                            e.w_lens.p, e.w_num, e.w_len, d.cnt.p,
-                           static_cast<int32_t>(e.active.n),
+                           static_cast<int32_t>(e.active.n), e.w_constrained,
                            reinterpret_cast<unsigned long long*>(e.acc64.p));
     }
-    uint64_t h[4];
-    check_hip(hipMemcpyAsync(h, e.acc64.p, 32, hipMemcpyDeviceToHost, s), "read stats");
+    uint64_t h[5];
+    check_hip(hipMemcpyAsync(h, e.acc64.p, 40, hipMemcpyDeviceToHost, s), "read stats");
     e.sync();
     out->total_len = h[0];
     out->transitions = h[1];
     out->nonempty_walks = h[2];
     out->algorithmic_bytes = h[3];
+    out->reference_bytes = h[4];
 }
 
 }  // namespace trw

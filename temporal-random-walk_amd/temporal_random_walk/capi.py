@@ -134,10 +134,11 @@ class TrwWalkStats(C.Structure):
         ("transitions", C.c_uint64),
         ("nonempty_walks", C.c_uint64),
         ("algorithmic_bytes", C.c_uint64),
+        ("reference_bytes", C.c_uint64),
     ]
 
 
-ABI_VERSION = 2  # TRW_ABI_VERSION of include/trw_engine.h
+ABI_VERSION = 3  # TRW_ABI_VERSION of include/trw_engine.h
 _lib = None
 
 

@@ -31,7 +31,9 @@ def test_library_exports_every_declared_symbol():
     missing = [n for n in _declared_functions() if not hasattr(lib, n)]
     assert not missing, f"declared but not exported: {missing}"
     assert sorted(capi.EXPORTS) == _declared_functions()
-    assert capi.lib().trw_abi_version() == capi.ABI_VERSION == 2
+    header = open(HEADER).read()
+    declared = int(re.search(r"#define TRW_ABI_VERSION (\d+)", header).group(1))
+    assert capi.lib().trw_abi_version() == capi.ABI_VERSION == declared
 
 
 def test_library_carries_gfx950_code():
