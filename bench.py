@@ -93,6 +93,8 @@ def main():
     ap.add_argument("--timestamps", type=int, default=100_000)
     ap.add_argument("--walks", type=int, default=10_000_000)
     ap.add_argument("--walk-len", type=int, default=80)
+    ap.add_argument("--walk-order", default="auto", choices=["auto", "walk_id", "start_time"],
+                    help="order the walks run in on the device (the output is the same)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-walks", type=int, default=2_500_000,
                     help="walks of the bounded CPU-baseline sample (about 10 s on 16 threads)")
@@ -146,7 +148,8 @@ def main():
         eng.add_edges_device(d_src.data_ptr(), d_dst.data_ptr(), d_ts.data_ptr(), E)
         t1 = time.perf_counter()
         eng.sample_device("total", args.walk_len, "ExponentialIndex", args.walks,
-                          initial_edge_bias="Uniform", direction="Forward_In_Time")
+                          initial_edge_bias="Uniform", direction="Forward_In_Time",
+                          walk_order=args.walk_order)
         t2 = time.perf_counter()
         return t1 - t0, t2 - t1, eng.timings()
 
@@ -212,6 +215,7 @@ def main():
             "num_walks": args.walks,
             "max_walk_len": args.walk_len,
             "parallelism": "1 GPU",
+            "walk_order": args.walk_order,
         },
         "index_build_edges_per_s": build_eps,
         "index_build_ms": sum(builds) * 1e3 / args.steps,

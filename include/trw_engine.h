@@ -98,8 +98,19 @@ typedef struct trw_sample_params {
     const double* replay_draws;
     uint64_t replay_draws_len;
     int32_t shuffle;            /* -1 = the handle's shuffle_walk_order, 0/1 = override */
-    int32_t reserved;
+    /* Order the walks run in on the device; the output is the same in every
+     * order (each walk depends only on the graph and its own draws).
+     * 0 = automatic (TRW_ORDER_START_TIME from 2^16 walks on), 1 = walk id
+     * order, 2 = sorted by the time of the start edge, so that walks running
+     * side by side read the same parts of the index. */
+    int32_t walk_order;
 } trw_sample_params;
+
+typedef enum trw_walk_order {
+    TRW_ORDER_AUTO = 0,
+    TRW_ORDER_WALK_ID = 1,
+    TRW_ORDER_START_TIME = 2
+} trw_walk_order;
 
 /* Walk output.  nodes/timestamps: [num_walks, max_walk_len]; edge_ids:
  * [num_walks, max_walk_len - 1]; walk_lens: [num_walks]; edge_features:

@@ -265,6 +265,7 @@ struct Engine {
     DBuf<int32_t> stage_src, stage_dst;
     DBuf<int64_t> stage_ts;
     DBuf<float> stage_feat;
+    DBuf<uint32_t> walk_st;  // 16-byte start state per walk (time-ordered sampling)
     DBuf<int32_t> starts;
     DBuf<int64_t> cutoffs;
     DBuf<double> replay;

@@ -35,6 +35,9 @@ namespace {
 
 constexpr int kB = 256;
 
+// Samples of at least this many walks run sorted by start time (TRW_ORDER_AUTO).
+constexpr uint64_t kTimeOrderMinWalks = 1ull << 16;
+
 inline unsigned grid_for(size_t n) {
     const size_t g = (n + kB - 1) / kB;
     return static_cast<unsigned>(g ? g : 1);
@@ -80,6 +83,14 @@ struct WalkGraph {
     double inv_p, inv_q;
 };
 
+// A walk's state after its start edge: the walk's origin (slot 0), the node
+// reached over the start edge, the rank of the edge's time and the edge id
+// (-1: no start edge, the walk is empty).
+struct StartState {
+    int32_t first, cur, r, e;
+};
+static_assert(sizeof(StartState) == 16, "StartState must be 16 bytes");
+
 struct WalkArgs {
     int L;
     int walk_bias;
@@ -93,6 +104,12 @@ struct WalkArgs {
     uint32_t* ranks;
     uint64_t* lens;
     uint32_t* eids;
+    // Processing order (nullptr: walk id order).  Position q of the grid runs
+    // walk order[q] and writes its scratch column q; outputs indexed by walk
+    // (lengths, and the rows the layout pass writes) use the walk id.
+    const uint32_t* order;
+    const StartState* st;  // start states of the pre-pass (nullptr: computed here)
+    int xcd_remap;                // spread the order over the XCDs in contiguous slices
 };
 
 // Scratch rank of a walk's first slot, whose timestamp is the direction's
@@ -363,59 +380,107 @@ __device__ Hop node_edge_at(const WalkGraph& g, int picker, int node, int32_t t,
                   pr.rank);
 }
 
-template <bool Fwd, bool Dir, int Fam>
-__global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
-    const uint64_t w = blockIdx.x * static_cast<uint64_t>(kB) + threadIdx.x;
-    if (w >= a.n) return;
-    const int L = a.L;
-    if (L == 0) {
-        a.lens[w] = 0;
-        return;
-    }
-    // Slot-major scratch: slot k of walk w lives at [k * n + w], so the 64
-    // lanes of a wave store 256 B per slot and array contiguously.
-    // layout_walks_kernel produces the row-major output in the reference's
-    // types, the padding and the chronological order of backward walks.
-    const uint64_t n = a.n;
-    int32_t* wn = a.nodes + w;
-    uint32_t* wt = a.ranks + w;
-    uint32_t* we = a.eids + w;
-    const int start = a.starts ? a.starts[w] : -1;
+// Rank bound of a walk's cutoff time: groups at or past it are excluded
+// (-1: no cutoff).
+__device__ __forceinline__ int32_t cutoff_rank(const WalkGraph& g, const WalkArgs& a,
+                                               uint64_t w) {
     const int64_t cutoff = a.cutoffs ? a.cutoffs[w] : kNoCutoff;
-    const int32_t cut = cutoff != kNoCutoff ? rank_lower_bound(g, cutoff) : -1;
-    // the reference's tests of a current time of -1, on ranks
-    const int32_t neg1 = *g.neg1_rank;
+    return cutoff != kNoCutoff ? rank_lower_bound(g, cutoff) : -1;
+}
 
+// Start edge of walk w (temporal_random_walk_cpu.cuh:39-90): the first slot
+// holds the walk's origin and `cur` the node reached over the start edge.
+template <bool Fwd, bool Dir, int Fam>
+__device__ __forceinline__ StartState walk_start(const WalkGraph& g, const WalkArgs& a,
+                                                 uint64_t w, int32_t cut) {
+    const int start = a.starts ? a.starts[w] : -1;
     const double r0 = draw_slot0(a.ds, w);
     const DrawPair r12 = draw_pair(a.ds, w, 1);
-    // Start edge: the first slot holds the walk's origin and `cur` the node
-    // reached over the start edge (temporal_random_walk_cpu.cuh:39-90).
-    int first = -1, cur = -1;
-    int32_t cur_r = -1, cur_e = -1;
+    StartState st{-1, -1, -1, -1};
     if (start == -1) {
         const Sel se = start_edge<Fwd>(g, a.start_bias, r0, r12.a);
         if (se.v != -1) {
             if (Dir) {
-                first = Fwd ? se.u : se.v;
-                cur = Fwd ? se.v : se.u;
+                st.first = Fwd ? se.u : se.v;
+                st.cur = Fwd ? se.v : se.u;
             } else {
-                first = r12.b >= 0.5 ? se.u : se.v;
-                cur = first == se.u ? se.v : se.u;
+                st.first = r12.b >= 0.5 ? se.u : se.v;
+                st.cur = st.first == se.u ? se.v : se.u;
             }
-            cur_r = se.r;
-            cur_e = se.e;
+            st.r = se.r;
+            st.e = se.e;
         }
     } else {
         // a node's own list: the node is the edge's source (out), target (in)
         // or one endpoint (undirected) -- the record's neighbour is the other
         const Hop h = node_edge_at<Fwd, Fam>(g, a.start_bias, start, -1, cut, -1, r0, r12.a);
         if (h.e != -1) {
-            first = start;
-            cur = h.nbr;
-            cur_r = h.r;
-            cur_e = h.e;
+            st.first = start;
+            st.cur = h.nbr;
+            st.r = h.r;
+            st.e = h.e;
         }
     }
+    return st;
+}
+
+// Pre-pass of the time-ordered walk: every walk's start state, and the sort
+// key that orders walks by the time their first hop starts from (the rank of
+// the start edge's time; `none` for walks without a start edge).
+template <bool Fwd, bool Dir, int Fam>
+__global__ __launch_bounds__(kB) void walk_start_kernel(WalkGraph g, WalkArgs a,
+                                                        StartState* __restrict__ st,
+                                                        uint32_t* __restrict__ keys,
+                                                        uint32_t* __restrict__ vals,
+                                                        uint32_t none) {
+    const uint64_t w = blockIdx.x * static_cast<uint64_t>(kB) + threadIdx.x;
+    if (w >= a.n) return;
+    const StartState s0 = walk_start<Fwd, Dir, Fam>(g, a, w, cutoff_rank(g, a, w));
+    st[w] = s0;
+    keys[w] = s0.e != -1 ? static_cast<uint32_t>(s0.r) : none;
+    vals[w] = static_cast<uint32_t>(w);
+}
+
+// Workgroup b runs on XCD b % 8 (round-robin dispatch).  With the remap, XCD
+// x runs the x-th contiguous slice of the grid's positions, so the walks
+// resident on one XCD -- and sharing its L2 -- are neighbours in the order.
+constexpr unsigned kXcds = 8;
+__device__ __forceinline__ uint64_t grid_position(int remap) {
+    unsigned b = blockIdx.x;
+    if (remap) {
+        const unsigned nb = gridDim.x, x = b % kXcds, i = b / kXcds;
+        const unsigned per = nb / kXcds, extra = nb % kXcds;
+        b = x * per + (x < extra ? x : extra) + i;
+    }
+    return b * static_cast<uint64_t>(kB) + threadIdx.x;
+}
+
+template <bool Fwd, bool Dir, int Fam>
+__global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
+    const uint64_t q = grid_position(a.xcd_remap);
+    if (q >= a.n) return;
+    const uint64_t w = a.order ? a.order[q] : q;
+    const int L = a.L;
+    if (L == 0) {
+        a.lens[w] = 0;
+        return;
+    }
+    // Slot-major scratch: slot k of grid position q lives at [k * n + q], so
+    // the 64 lanes of a wave store 256 B per slot and array contiguously.
+    // layout_walks_kernel produces the row-major output in the reference's
+    // types, the padding and the chronological order of backward walks.
+    const uint64_t n = a.n;
+    int32_t* wn = a.nodes + q;
+    uint32_t* wt = a.ranks + q;
+    uint32_t* we = a.eids + q;
+    const int32_t cut = cutoff_rank(g, a, w);
+    // the reference's tests of a current time of -1, on ranks
+    const int32_t neg1 = *g.neg1_rank;
+
+    const StartState s0 = a.st ? a.st[w] : walk_start<Fwd, Dir, Fam>(g, a, w, cut);
+    const int first = s0.first;
+    int cur = s0.cur;
+    int32_t cur_r = s0.r, cur_e = s0.e;
     int len = 0;
     if (cur_e != -1) {
         int prev = -1;
@@ -456,13 +521,15 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
 // out reversed into chronological order (data/walk_set/walk_set_view.cuh:
 // 50-80).
 //
-// A workgroup owns 64 consecutive walks and a chunk of slots -- the whole row
-// when L <= kLayoutMaxSlots, so the 64 rows it writes are one contiguous span
-// of the output and no cache line is shared with another workgroup.  Per array
-// it reads 64-walk runs of one slot (256 B, coalesced) into an LDS tile of the
-// 32-bit scratch values, then each wave writes whole row runs, converting as
-// it writes (a walk's ranks increase along its row, so the timestamp lookups
-// of one run are close together).  One tile is reused by the three arrays.
+// A workgroup owns 64 consecutive scratch columns and a chunk of slots -- the
+// whole row when L <= kLayoutMaxSlots.  Per array it reads 64-column runs of
+// one slot (256 B, coalesced) into an LDS tile of the 32-bit scratch values,
+// then each wave writes whole row runs, converting as it writes (a walk's
+// ranks increase along its row, so the timestamp lookups of one run are close
+// together).  One tile is reused by the three arrays.  Column q holds walk
+// order[q] when the walks ran in another order than their ids; its row goes to
+// that walk's place.  In walk-id order the 64 rows are one contiguous span of
+// the output, so no cache line is shared with another workgroup.
 constexpr int kLayoutWalks = 64;
 constexpr int kLayoutMaxSlots = 128;  // tile <= 33 KB of LDS
 
@@ -481,12 +548,13 @@ struct LayoutArgs {
     int32_t pad;
     const int64_t* uniq_ts;
     int64_t start_ts;
+    const uint32_t* order;  // walk of each scratch column (nullptr: the column index)
 };
 
 // Arr 0: nodes, 1: timestamps, 2: edge ids.
 template <int Arr>
 __device__ __forceinline__ void layout_array(const LayoutArgs& a, uint32_t* tile, const int* cnt,
-                                             uint64_t w0, int k0) {
+                                             const uint32_t* row, uint64_t w0, int k0) {
     const int K = Arr == 2 ? a.L - 1 : a.L;
     const int kc = min(a.C, K - k0);
     if (kc <= 0) return;  // uniform over the workgroup
@@ -518,8 +586,8 @@ __device__ __forceinline__ void layout_array(const LayoutArgs& a, uint32_t* tile
     __syncthreads();
     const int wave = tid >> 6, lane = tid & 63;
     for (int wl2 = wave; wl2 < kLayoutWalks; wl2 += 4) {
-        const uint64_t w2 = w0 + wl2;
-        if (w2 >= a.n) break;
+        if (w0 + wl2 >= a.n) break;
+        const uint64_t w2 = row[wl2];
         const uint64_t base = w2 * static_cast<uint64_t>(K) + k0;
         const int cw = cnt[wl2] - (Arr == 2 ? 1 : 0) - k0;  // slots of the row below the count
         for (int i = lane; i < kc; i += 64) {
@@ -540,16 +608,19 @@ __global__ __launch_bounds__(256) void layout_walks_kernel(LayoutArgs a) {
     extern __shared__ uint32_t layout_lds[];
     uint32_t* tile = layout_lds;
     int* cnt = reinterpret_cast<int*>(layout_lds + a.C * (kLayoutWalks + 1));
+    uint32_t* row = reinterpret_cast<uint32_t*>(cnt + kLayoutWalks);
     const uint64_t w0 = static_cast<uint64_t>(blockIdx.x) * kLayoutWalks;
     const int k0 = blockIdx.y * a.C;
     if (threadIdx.x < kLayoutWalks) {
-        const uint64_t w = w0 + threadIdx.x;
-        cnt[threadIdx.x] = w < a.n ? static_cast<int>(a.lens[w]) : 0;
+        const uint64_t q = w0 + threadIdx.x;
+        const uint64_t w = q < a.n ? (a.order ? a.order[q] : q) : 0;
+        row[threadIdx.x] = static_cast<uint32_t>(w);
+        cnt[threadIdx.x] = q < a.n ? static_cast<int>(a.lens[w]) : 0;
     }
     __syncthreads();
-    layout_array<0>(a, tile, cnt, w0, k0);
-    layout_array<1>(a, tile, cnt, w0, k0);
-    layout_array<2>(a, tile, cnt, w0, k0);
+    layout_array<0>(a, tile, cnt, row, w0, k0);
+    layout_array<1>(a, tile, cnt, row, w0, k0);
+    layout_array<2>(a, tile, cnt, row, w0, k0);
 }
 
 // ---- start arrays ----------------------------------------------------------
@@ -956,29 +1027,63 @@ void Engine::sample(const trw_sample_params& p) {
     a.lens = w_lens.p;
     a.eids = sw_eids.p;
 
-    check_hip(hipEventRecord(ev[5], s), "event");
-    if (nw) {
-        if (E == 0) {
-            // empty graph: every start fails; the kernel still writes the padding
-            g.T = 0;
-            g.active_size = 0;
-        }
-        const dim3 grid(grid_for(nw));
-        const bool index_only = is_index_picker(walk_bias) && is_index_picker(start_bias);
-#define TRW_LAUNCH_WALK(F, D)                                                                  \
+    if (nw && E == 0) {
+        // empty graph: every start fails; the kernel still writes the padding
+        g.T = 0;
+        g.active_size = 0;
+    }
+    const dim3 grid(grid_for(nw));
+    const bool index_only = is_index_picker(walk_bias) && is_index_picker(start_bias);
+#define TRW_LAUNCH_FAMILY(K, F, D, ...)                                                        \
     do {                                                                                       \
         if (index_only)                                                                        \
-            hipLaunchKernelGGL((walk_kernel<F, D, kFamIndex>), grid, dim3(kB), 0, s, g, a);     \
+            hipLaunchKernelGGL((K<F, D, kFamIndex>), grid, dim3(kB), 0, s, __VA_ARGS__);        \
         else                                                                                   \
-            hipLaunchKernelGGL((walk_kernel<F, D, kFamAny>), grid, dim3(kB), 0, s, g, a);       \
+            hipLaunchKernelGGL((K<F, D, kFamAny>), grid, dim3(kB), 0, s, __VA_ARGS__);          \
     } while (0)
-        if (forward && cfg.is_directed) TRW_LAUNCH_WALK(true, true);
-        else if (forward) TRW_LAUNCH_WALK(true, false);
-        else if (cfg.is_directed) TRW_LAUNCH_WALK(false, true);
-        else TRW_LAUNCH_WALK(false, false);
-#undef TRW_LAUNCH_WALK
+#define TRW_LAUNCH(K, ...)                                                                     \
+    do {                                                                                       \
+        if (forward && cfg.is_directed) TRW_LAUNCH_FAMILY(K, true, true, __VA_ARGS__);         \
+        else if (forward) TRW_LAUNCH_FAMILY(K, true, false, __VA_ARGS__);                      \
+        else if (cfg.is_directed) TRW_LAUNCH_FAMILY(K, false, true, __VA_ARGS__);              \
+        else TRW_LAUNCH_FAMILY(K, false, false, __VA_ARGS__);                                  \
+    } while (0)
+
+    // ---- processing order: walks sorted by the time rank of their start
+    // edge, so the walks of one wave -- and of one XCD -- search the same
+    // stretch of a hub's panel and read neighbouring records
+    const int order_mode = p.walk_order == TRW_ORDER_AUTO
+                               ? (nw >= kTimeOrderMinWalks ? TRW_ORDER_START_TIME : TRW_ORDER_WALK_ID)
+                               : p.walk_order;
+    if (order_mode != TRW_ORDER_WALK_ID && order_mode != TRW_ORDER_START_TIME)
+        throw InvalidArgument("Invalid walk order");
+    if (order_mode == TRW_ORDER_START_TIME && nw > 1 && L > 1) {
+        walk_st.ensure(4 * nw);
+        k32a.ensure(nw);
+        k32b.ensure(nw);
+        v32a.ensure(nw);
+        v32b.ensure(nw);
+        hist.ensure(radix_hist_elems(nw));
+        hist_scratch.ensure(scan_scratch_elems(radix_hist_elems(nw)));
+        StartState* st = reinterpret_cast<StartState*>(walk_st.p);
+        const uint32_t none = g.T;  // past every rank: walks without a start run last
+        TRW_LAUNCH(walk_start_kernel, g, a, st, k32a.p, v32a.p, none);
+        const int bits = std::max(1, 32 - __builtin_clz(none | 1u));
+        const int wsort = radix_sort_u32(k32a.p, v32a.p, k32b.p, v32b.p, nw, 0, bits, hist.p,
+                                         hist_scratch.p, s);
+        a.order = wsort ? v32b.p : v32a.p;
+        a.st = st;
+        a.xcd_remap = 1;
+        check_hip(hipGetLastError(), "walk order launch");
+    }
+
+    check_hip(hipEventRecord(ev[5], s), "event");
+    if (nw) {
+        TRW_LAUNCH(walk_kernel, g, a);
         check_hip(hipGetLastError(), "walk kernel launch");
     }
+#undef TRW_LAUNCH
+#undef TRW_LAUNCH_FAMILY
     check_hip(hipEventRecord(ev[6], s), "event");
     if (nw && L > 0) {
         const unsigned gx = static_cast<unsigned>((nw + 63) / 64);
@@ -999,8 +1104,9 @@ void Engine::sample(const trw_sample_params& p) {
         la.pad = static_cast<int32_t>(cfg.walk_padding_value);
         la.uniq_ts = uniq_ts.p;
         la.start_ts = forward ? INT64_MIN : INT64_MAX;
+        la.order = a.order;
         const size_t lds = static_cast<size_t>(la.C) * (kLayoutWalks + 1) * sizeof(uint32_t) +
-                           kLayoutWalks * sizeof(int);
+                           kLayoutWalks * (sizeof(int) + sizeof(uint32_t));
         hipLaunchKernelGGL(layout_walks_kernel, dim3(gx, chunks), dim3(256), lds, s, la);
         check_hip(hipGetLastError(), "layout launch");
     }

@@ -28,6 +28,8 @@ PICKERS = {
     "TEST_LAST": 6,
 }
 DIRECTIONS = {"Forward_In_Time": 0, "Backward_In_Time": 1}
+# trw_walk_order: the order walks run in on the device (the output is the same)
+WALK_ORDERS = {"auto": 0, "walk_id": 1, "start_time": 2}
 MODES = {"total": 0, "all_nodes": 1, "last_batch": 2, "nodes": 3}
 
 # (id, numpy dtype) in the order of trw_array_id
@@ -98,7 +100,7 @@ class TrwSampleParams(C.Structure):
         ("replay_draws", C.c_void_p),
         ("replay_draws_len", C.c_uint64),
         ("shuffle", C.c_int32),
-        ("reserved", C.c_int32),
+        ("walk_order", C.c_int32),
     ]
 
 
@@ -239,6 +241,18 @@ def device_to_host(dptr, count, dtype, offset_elems=0):
     return out
 
 
+def device_copy(dst_ptr, src_ptr, nbytes):
+    """hipMemcpy of nbytes between two device buffers (e.g. a buffer returned
+    by trw_sample_device into a torch tensor)."""
+    global _hip
+    if _hip is None:
+        device_to_host(0, 0, np.uint8)  # loads the HIP runtime
+    if nbytes:
+        rc = _hip.hipMemcpy(int(dst_ptr), int(src_ptr), int(nbytes), 3)  # hipMemcpyDeviceToDevice
+        if rc != 0:
+            raise EngineError(f"hipMemcpy failed ({rc})")
+
+
 def _check(rc):
     if rc != 0:
         msg = lib().trw_last_error().decode()
@@ -316,7 +330,7 @@ class Engine:
     # ---- sampling
     def _params(self, mode, max_walk_len, walk_bias, num_walks=0, initial_edge_bias=None,
                 direction="Forward_In_Time", seed_nodes=None, cutoff_times=None, replay=None,
-                shuffle=None):
+                shuffle=None, walk_order="auto"):
         keep = []
         p = TrwSampleParams()
         p.mode = MODES[mode]
@@ -343,6 +357,7 @@ class Engine:
             p.replay_draws = r.ctypes.data
             p.replay_draws_len = r.size
         p.shuffle = -1 if shuffle is None else int(bool(shuffle))
+        p.walk_order = WALK_ORDERS[walk_order]
         return p, keep
 
     def sample(self, mode, max_walk_len, walk_bias, num_walks=0, **kw):

@@ -101,6 +101,22 @@ def _check_index(eng, directed):
     return s, d, t
 
 
+def _device_arrays(w, L):
+    """Device copies (torch) of a device sample's nodes, timestamps, lengths
+    and edge ids."""
+    import torch
+    from temporal_random_walk import capi
+    n = int(w.num_walks)
+    out = []
+    for ptr, count, dt in ((w.nodes, n * L, torch.int32), (w.timestamps, n * L, torch.int64),
+                           (w.walk_lens, n, torch.int64), (w.edge_ids, n * (L - 1), torch.int64)):
+        t = torch.empty(count, dtype=dt, device="cuda")
+        capi.device_copy(t.data_ptr(), ptr, t.numel() * t.element_size())
+        out.append(t)
+    torch.cuda.synchronize()
+    return out
+
+
 def _check_walks(nodes, ts, lens, eids, s, d, t, L, directed, forward, feats=None,
                  store_feats=None):
     assert np.all((lens == 0) | ((lens >= 2) & (lens <= L)))
@@ -172,8 +188,18 @@ def test_cfg2_full_parity():
                      replay=dr, shuffle=False)
     for k in ("nodes", "timestamps", "lens", "edge_ids"):
         assert np.array_equal(getattr(ref, k), getattr(got, k)), k
+    # the full sample, run in walk-id order and sorted by start time: the
+    # outputs are the same bytes
+    import torch
     w = eng.sample_device("total", L, "ExponentialIndex", 10_000_000,
-                          initial_edge_bias="Uniform")
+                          initial_edge_bias="Uniform", walk_order="walk_id")
+    by_id = _device_arrays(w, L)
+    w = eng.sample_device("total", L, "ExponentialIndex", 10_000_000,
+                          initial_edge_bias="Uniform", walk_order="start_time")
+    by_time = _device_arrays(w, L)
+    for name, x, y in zip(("nodes", "timestamps", "lens", "edge_ids"), by_id, by_time):
+        assert torch.equal(x, y), name
+    del by_id, by_time
     st = eng.walk_stats()
     assert st["total_len"] > 70 * 10_000_000  # mean walk length ~76
     s, d, t = eng.array("sources"), eng.array("targets"), eng.array("timestamps")

@@ -129,17 +129,19 @@ def _walk_case(og, eng, picker, start_picker, forward, mode, L, n_or_wpn, seed_n
         cut = None if cutoffs is None else np.repeat(np.asarray(cutoffs, dtype=np.int64), n_or_wpn)
     dr = graphs.draws(len(starts), L, seed=seed)
     ref = og.walks(L, picker, start_picker, forward, starts, dr, cutoffs=cut)
-    got = eng.sample(mode, L, picker, n_or_wpn, initial_edge_bias=start_picker,
-                     direction=direction, seed_nodes=seed_nodes, cutoff_times=cutoffs,
-                     replay=dr, shuffle=False)
-    for k in ("nodes", "timestamps", "lens", "edge_ids"):
-        a = getattr(ref, k)
-        b = getattr(got, k)
-        assert a.shape == b.shape, k
-        bad = np.nonzero((a != b).reshape(len(starts), -1).any(axis=1))[0] if a.ndim > 1 else \
-            np.nonzero(a != b)[0]
-        assert bad.size == 0, (f"{picker}/{start_picker} fwd={forward} {mode}: {k} differs in "
-                               f"{bad.size} walks, first {bad[:5]}")
+    # both device processing orders give the reference's walks, row for row
+    for order in ("walk_id", "start_time"):
+        got = eng.sample(mode, L, picker, n_or_wpn, initial_edge_bias=start_picker,
+                         direction=direction, seed_nodes=seed_nodes, cutoff_times=cutoffs,
+                         replay=dr, shuffle=False, walk_order=order)
+        for k in ("nodes", "timestamps", "lens", "edge_ids"):
+            a = getattr(ref, k)
+            b = getattr(got, k)
+            assert a.shape == b.shape, k
+            bad = np.nonzero((a != b).reshape(len(starts), -1).any(axis=1))[0] if a.ndim > 1 \
+                else np.nonzero(a != b)[0]
+            assert bad.size == 0, (f"{picker}/{start_picker} fwd={forward} {mode} {order}: {k} "
+                                   f"differs in {bad.size} walks, first {bad[:5]}")
     return got
 
 
@@ -311,16 +313,17 @@ def _normal_case(og, eng, picker, start_picker, forward, mode, L, n_or_wpn, seed
         order = po.philox_shuffle_order(GLOBAL_SEED, starts.size)
         starts = starts[order]
         cut = None if cut is None else cut[order]
-    got = eng.sample(mode, L, picker, n_or_wpn, initial_edge_bias=start_picker,
-                     direction=direction, seed_nodes=seed_nodes, cutoff_times=cutoffs,
-                     shuffle=shuffle)
     dr = po.philox_draws(GLOBAL_SEED, starts.size, L)
     ref = og.walks(L, picker, start_picker, forward, starts, dr, cutoffs=cut)
-    for k in ("nodes", "timestamps", "lens", "edge_ids"):
-        a, b = getattr(ref, k), getattr(got, k)
-        assert a.shape == b.shape, k
-        assert np.array_equal(a, b), (f"{picker}/{start_picker} fwd={forward} {mode} "
-                                      f"shuffle={shuffle}: {k} differs")
+    for order in ("walk_id", "start_time"):
+        got = eng.sample(mode, L, picker, n_or_wpn, initial_edge_bias=start_picker,
+                         direction=direction, seed_nodes=seed_nodes, cutoff_times=cutoffs,
+                         shuffle=shuffle, walk_order=order)
+        for k in ("nodes", "timestamps", "lens", "edge_ids"):
+            a, b = getattr(ref, k), getattr(got, k)
+            assert a.shape == b.shape, k
+            assert np.array_equal(a, b), (f"{picker}/{start_picker} fwd={forward} {mode} "
+                                          f"shuffle={shuffle} {order}: {k} differs")
     return got
 
 
