@@ -108,8 +108,9 @@ struct WalkArgs {
     // walk order[q] and writes its scratch column q; outputs indexed by walk
     // (lengths, and the rows the layout pass writes) use the walk id.
     const uint32_t* order;
-    const StartState* st;  // start states of the pre-pass (nullptr: computed here)
+    const StartState* st;  // start state of every walk (walk_start_kernel)
     int xcd_remap;                // spread the order over the XCDs in contiguous slices
+    uint64_t q0, q_end;           // grid positions [q0, q_end) of this launch
 };
 
 // Scratch rank of a walk's first slot, whose timestamp is the direction's
@@ -424,9 +425,9 @@ __device__ __forceinline__ StartState walk_start(const WalkGraph& g, const WalkA
     return st;
 }
 
-// Pre-pass of the time-ordered walk: every walk's start state, and the sort
-// key that orders walks by the time their first hop starts from (the rank of
-// the start edge's time; `none` for walks without a start edge).
+// Pre-pass of the walk: every walk's start state, and the key that orders
+// walks by the time their first hop starts from (the rank of the start edge's
+// time; `none` for walks without a start edge).
 template <bool Fwd, bool Dir, int Fam>
 __global__ __launch_bounds__(kB) void walk_start_kernel(WalkGraph g, WalkArgs a,
                                                         StartState* __restrict__ st,
@@ -457,8 +458,8 @@ __device__ __forceinline__ uint64_t grid_position(int remap) {
 
 template <bool Fwd, bool Dir, int Fam>
 __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
-    const uint64_t q = grid_position(a.xcd_remap);
-    if (q >= a.n) return;
+    const uint64_t q = a.q0 + grid_position(a.xcd_remap);
+    if (q >= a.q_end) return;
     const uint64_t w = a.order ? a.order[q] : q;
     const int L = a.L;
     if (L == 0) {
@@ -477,7 +478,7 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
     // the reference's tests of a current time of -1, on ranks
     const int32_t neg1 = *g.neg1_rank;
 
-    const StartState s0 = a.st ? a.st[w] : walk_start<Fwd, Dir, Fam>(g, a, w, cut);
+    const StartState s0 = a.st[w];
     const int first = s0.first;
     int cur = s0.cur;
     int32_t cur_r = s0.r, cur_e = s0.e;
@@ -549,9 +550,18 @@ struct LayoutArgs {
     const int64_t* uniq_ts;
     int64_t start_ts;
     const uint32_t* order;  // walk of each scratch column (nullptr: the column index)
+    uint64_t q0, q_end;     // scratch columns [q0, q_end) of this launch (q0 % 64 == 0)
 };
 
-// Arr 0: nodes, 1: timestamps, 2: edge ids.
+// Value of output slot i of a row whose first `cw` slots were written (x: the
+// scratch value).  Arr 0: nodes, 1: timestamps, 2: edge ids.
+template <int Arr>
+__device__ __forceinline__ int64_t layout_value(const LayoutArgs& a, uint32_t x, int i, int cw) {
+    if (Arr == 0) return i < cw ? static_cast<int32_t>(x) : a.pad;
+    if (Arr == 1) return i >= cw ? -1 : (x == kStartRank ? a.start_ts : a.uniq_ts[x]);
+    return i < cw ? static_cast<int64_t>(x) : -1;
+}
+
 template <int Arr>
 __device__ __forceinline__ void layout_array(const LayoutArgs& a, uint32_t* tile, const int* cnt,
                                              const uint32_t* row, uint64_t w0, int k0) {
@@ -564,6 +574,11 @@ __device__ __forceinline__ void layout_array(const LayoutArgs& a, uint32_t* tile
     const uint64_t w = w0 + wl;
     int c = cnt[wl] - (Arr == 2 ? 1 : 0);
     c = c > 0 ? c : 0;
+    // A reversed row held whole by the tile (one chunk) is read in slot order
+    // -- every load a 256-byte run -- and reversed on its way out of LDS; rows
+    // laid out in several chunks read their reversed slots directly.
+    const bool whole = k0 == 0 && kc == K;
+    const bool rev_in = a.reverse && !whole;
     // slots at or past the count are not read; the writer pads them
     const uint32_t* in = Arr == 0 ? reinterpret_cast<const uint32_t*>(a.sn) : (Arr == 1 ? a.sr : a.se);
     for (int j0 = 0; j0 < kc; j0 += 32) {
@@ -573,8 +588,8 @@ __device__ __forceinline__ void layout_array(const LayoutArgs& a, uint32_t* tile
             const int r = j0 + srow + 4 * j;
             const int k = k0 + r;
             uint32_t x = 0;
-            if (r < kc && w < a.n && k < c)
-                x = in[static_cast<uint64_t>(a.reverse ? c - 1 - k : k) * a.n + w];
+            if (r < kc && w < a.q_end && k < c)
+                x = in[static_cast<uint64_t>(rev_in ? c - 1 - k : k) * a.n + w];
             v[j] = x;
         }
 #pragma unroll
@@ -585,19 +600,41 @@ __device__ __forceinline__ void layout_array(const LayoutArgs& a, uint32_t* tile
     }
     __syncthreads();
     const int wave = tid >> 6, lane = tid & 63;
+    const bool rev_out = a.reverse && whole;
+    // 16-byte stores (4 nodes or 2 timestamps / edge ids per lane) when every
+    // row chunk starts on a 16-byte boundary and holds whole vectors
+    constexpr int V = Arr == 0 ? 4 : 2;
+    const bool vec = (K % V) == 0 && (k0 % V) == 0 && (kc % V) == 0;
     for (int wl2 = wave; wl2 < kLayoutWalks; wl2 += 4) {
-        if (w0 + wl2 >= a.n) break;
+        if (w0 + wl2 >= a.q_end) break;
         const uint64_t w2 = row[wl2];
         const uint64_t base = w2 * static_cast<uint64_t>(K) + k0;
         const int cw = cnt[wl2] - (Arr == 2 ? 1 : 0) - k0;  // slots of the row below the count
-        for (int i = lane; i < kc; i += 64) {
-            const uint32_t x = tile[i * P + wl2];
-            if (Arr == 0) {
-                a.on[base + i] = i < cw ? static_cast<int32_t>(x) : a.pad;
-            } else if (Arr == 1) {
-                a.ot[base + i] = i >= cw ? -1 : (x == kStartRank ? a.start_ts : a.uniq_ts[x]);
-            } else {
-                a.oe[base + i] = i < cw ? static_cast<int64_t>(x) : -1;
+        // tile slot of output slot i (reversed rows: slot cw - 1 - i)
+        auto src = [&](int i) { return tile[(rev_out && i < cw ? cw - 1 - i : i) * P + wl2]; };
+        if (vec) {
+            for (int i = lane * V; i < kc; i += 64 * V) {
+                if (Arr == 0) {
+                    int4 o;
+                    o.x = static_cast<int32_t>(layout_value<0>(a, src(i), i, cw));
+                    o.y = static_cast<int32_t>(layout_value<0>(a, src(i + 1), i + 1, cw));
+                    o.z = static_cast<int32_t>(layout_value<0>(a, src(i + 2), i + 2, cw));
+                    o.w = static_cast<int32_t>(layout_value<0>(a, src(i + 3), i + 3, cw));
+                    *reinterpret_cast<int4*>(a.on + base + i) = o;
+                } else {
+                    longlong2 o;
+                    o.x = layout_value<Arr>(a, src(i), i, cw);
+                    o.y = layout_value<Arr>(a, src(i + 1), i + 1, cw);
+                    int64_t* out = Arr == 1 ? a.ot : a.oe;
+                    *reinterpret_cast<longlong2*>(out + base + i) = o;
+                }
+            }
+        } else {
+            for (int i = lane; i < kc; i += 64) {
+                const int64_t y = layout_value<Arr>(a, src(i), i, cw);
+                if (Arr == 0) a.on[base + i] = static_cast<int32_t>(y);
+                else if (Arr == 1) a.ot[base + i] = y;
+                else a.oe[base + i] = y;
             }
         }
     }
@@ -609,13 +646,13 @@ __global__ __launch_bounds__(256) void layout_walks_kernel(LayoutArgs a) {
     uint32_t* tile = layout_lds;
     int* cnt = reinterpret_cast<int*>(layout_lds + a.C * (kLayoutWalks + 1));
     uint32_t* row = reinterpret_cast<uint32_t*>(cnt + kLayoutWalks);
-    const uint64_t w0 = static_cast<uint64_t>(blockIdx.x) * kLayoutWalks;
+    const uint64_t w0 = a.q0 + static_cast<uint64_t>(blockIdx.x) * kLayoutWalks;
     const int k0 = blockIdx.y * a.C;
     if (threadIdx.x < kLayoutWalks) {
         const uint64_t q = w0 + threadIdx.x;
-        const uint64_t w = q < a.n ? (a.order ? a.order[q] : q) : 0;
+        const uint64_t w = q < a.q_end ? (a.order ? a.order[q] : q) : 0;
         row[threadIdx.x] = static_cast<uint32_t>(w);
-        cnt[threadIdx.x] = q < a.n ? static_cast<int>(a.lens[w]) : 0;
+        cnt[threadIdx.x] = q < a.q_end ? static_cast<int>(a.lens[w]) : 0;
     }
     __syncthreads();
     layout_array<0>(a, tile, cnt, row, w0, k0);
@@ -1032,21 +1069,20 @@ void Engine::sample(const trw_sample_params& p) {
         g.T = 0;
         g.active_size = 0;
     }
-    const dim3 grid(grid_for(nw));
     const bool index_only = is_index_picker(walk_bias) && is_index_picker(start_bias);
-#define TRW_LAUNCH_FAMILY(K, F, D, ...)                                                        \
+#define TRW_LAUNCH_FAMILY(K, F, D, G, ...)                                                     \
     do {                                                                                       \
         if (index_only)                                                                        \
-            hipLaunchKernelGGL((K<F, D, kFamIndex>), grid, dim3(kB), 0, s, __VA_ARGS__);        \
+            hipLaunchKernelGGL((K<F, D, kFamIndex>), G, dim3(kB), 0, s, __VA_ARGS__);           \
         else                                                                                   \
-            hipLaunchKernelGGL((K<F, D, kFamAny>), grid, dim3(kB), 0, s, __VA_ARGS__);          \
+            hipLaunchKernelGGL((K<F, D, kFamAny>), G, dim3(kB), 0, s, __VA_ARGS__);             \
     } while (0)
-#define TRW_LAUNCH(K, ...)                                                                     \
+#define TRW_LAUNCH(K, G, ...)                                                                  \
     do {                                                                                       \
-        if (forward && cfg.is_directed) TRW_LAUNCH_FAMILY(K, true, true, __VA_ARGS__);         \
-        else if (forward) TRW_LAUNCH_FAMILY(K, true, false, __VA_ARGS__);                      \
-        else if (cfg.is_directed) TRW_LAUNCH_FAMILY(K, false, true, __VA_ARGS__);              \
-        else TRW_LAUNCH_FAMILY(K, false, false, __VA_ARGS__);                                  \
+        if (forward && cfg.is_directed) TRW_LAUNCH_FAMILY(K, true, true, G, __VA_ARGS__);      \
+        else if (forward) TRW_LAUNCH_FAMILY(K, true, false, G, __VA_ARGS__);                   \
+        else if (cfg.is_directed) TRW_LAUNCH_FAMILY(K, false, true, G, __VA_ARGS__);           \
+        else TRW_LAUNCH_FAMILY(K, false, false, G, __VA_ARGS__);                               \
     } while (0)
 
     // ---- processing order: walks sorted by the time rank of their start
@@ -1057,37 +1093,43 @@ void Engine::sample(const trw_sample_params& p) {
                                : p.walk_order;
     if (order_mode != TRW_ORDER_WALK_ID && order_mode != TRW_ORDER_START_TIME)
         throw InvalidArgument("Invalid walk order");
-    if (order_mode == TRW_ORDER_START_TIME && nw > 1 && L > 1) {
+    if (nw && L > 0) {
         walk_st.ensure(4 * nw);
         k32a.ensure(nw);
-        k32b.ensure(nw);
         v32a.ensure(nw);
-        v32b.ensure(nw);
-        hist.ensure(radix_hist_elems(nw));
-        hist_scratch.ensure(scan_scratch_elems(radix_hist_elems(nw)));
         StartState* st = reinterpret_cast<StartState*>(walk_st.p);
         const uint32_t none = g.T;  // past every rank: walks without a start run last
-        TRW_LAUNCH(walk_start_kernel, g, a, st, k32a.p, v32a.p, none);
-        const int bits = std::max(1, 32 - __builtin_clz(none | 1u));
-        const int wsort = radix_sort_u32(k32a.p, v32a.p, k32b.p, v32b.p, nw, 0, bits, hist.p,
-                                         hist_scratch.p, s);
-        a.order = wsort ? v32b.p : v32a.p;
+        TRW_LAUNCH(walk_start_kernel, dim3(grid_for(nw)), g, a, st, k32a.p, v32a.p, none);
         a.st = st;
-        a.xcd_remap = 1;
-        check_hip(hipGetLastError(), "walk order launch");
+        if (order_mode == TRW_ORDER_START_TIME && nw > 1 && L > 1) {
+            k32b.ensure(nw);
+            v32b.ensure(nw);
+            hist.ensure(radix_hist_elems(nw));
+            hist_scratch.ensure(scan_scratch_elems(radix_hist_elems(nw)));
+            const int bits = std::max(1, 32 - __builtin_clz(none | 1u));
+            const int wsort = radix_sort_u32(k32a.p, v32a.p, k32b.p, v32b.p, nw, 0, bits, hist.p,
+                                             hist_scratch.p, s);
+            a.order = wsort ? v32b.p : v32a.p;
+            a.xcd_remap = 1;
+        }
+        check_hip(hipGetLastError(), "walk start launch");
     }
 
+    // ---- walk kernel, then the layout pass.  (Running the layout of finished
+    // grid chunks on a second stream beside the remaining walks was measured
+    // slower: the layout's streaming traffic evicts the hub lines the walks
+    // hit in L2.)
     check_hip(hipEventRecord(ev[5], s), "event");
     if (nw) {
-        TRW_LAUNCH(walk_kernel, g, a);
+        a.q0 = 0;
+        a.q_end = nw;
+        TRW_LAUNCH(walk_kernel, dim3(grid_for(nw)), g, a);
         check_hip(hipGetLastError(), "walk kernel launch");
     }
 #undef TRW_LAUNCH
 #undef TRW_LAUNCH_FAMILY
     check_hip(hipEventRecord(ev[6], s), "event");
     if (nw && L > 0) {
-        const unsigned gx = static_cast<unsigned>((nw + 63) / 64);
-        const int rev = forward ? 0 : 1;
         LayoutArgs la{};
         la.sn = sw_nodes.p;
         la.sr = sw_rank.p;
@@ -1098,16 +1140,19 @@ void Engine::sample(const trw_sample_params& p) {
         la.lens = w_lens.p;
         la.n = nw;
         la.L = L;
-        const int chunks = (L + kLayoutMaxSlots - 1) / kLayoutMaxSlots;
-        la.C = (L + chunks - 1) / chunks;
-        la.reverse = rev;
+        const int slot_chunks = (L + kLayoutMaxSlots - 1) / kLayoutMaxSlots;
+        la.C = (L + slot_chunks - 1) / slot_chunks;
+        la.reverse = forward ? 0 : 1;
         la.pad = static_cast<int32_t>(cfg.walk_padding_value);
         la.uniq_ts = uniq_ts.p;
         la.start_ts = forward ? INT64_MIN : INT64_MAX;
         la.order = a.order;
+        la.q0 = 0;
+        la.q_end = nw;
         const size_t lds = static_cast<size_t>(la.C) * (kLayoutWalks + 1) * sizeof(uint32_t) +
                            kLayoutWalks * (sizeof(int) + sizeof(uint32_t));
-        hipLaunchKernelGGL(layout_walks_kernel, dim3(gx, chunks), dim3(256), lds, s, la);
+        const unsigned gx = static_cast<unsigned>((nw + kLayoutWalks - 1) / kLayoutWalks);
+        hipLaunchKernelGGL(layout_walks_kernel, dim3(gx, slot_chunks), dim3(256), lds, s, la);
         check_hip(hipGetLastError(), "layout launch");
     }
 

@@ -288,6 +288,16 @@ def test_replay_long_walks_span_layout_chunks(forward):
     assert lens.max() == 150 and (lens > 96).mean() > 0.5
 
 
+def test_replay_walks_million_scale():
+    """2^20 + a ragged remainder of walks (time-ordered by default at this
+    size) against the oracle, forward and backward."""
+    s, d, t = graphs.powerlaw(20_000, 300_000, s=1.7, n_ts=30_000, seed=81)
+    og, eng = _pair(True, [(s, d, t)])
+    n = (1 << 20) + 4_321
+    _walk_case(og, eng, "ExponentialIndex", "Uniform", True, "total", 12, n, seed=82)
+    _walk_case(og, eng, "Linear", "Uniform", False, "total", 9, n, seed=83)
+
+
 # ---- normal mode: the in-kernel Philox stream -----------------------------
 
 GLOBAL_SEED = 1234  # the seed _pair gives the engine
