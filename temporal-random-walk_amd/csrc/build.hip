@@ -250,45 +250,32 @@ __global__ void node_group_counts_kernel(const uint32_t* __restrict__ off,
 }
 
 // Bucket shift of a node with G > kTabMin groups whose ranks span `span`:
-// the smallest power-of-two bucket width giving at most G / 4 buckets (about
-// four groups per bucket when the node's timestamps are spread evenly).
+// the smallest power-of-two bucket width giving at most kTabBucketsPerGroup * G
+// buckets.  A hub holding most ranks of its span gets width 1.
 __device__ __forceinline__ uint32_t table_shift(uint32_t G, uint32_t span) {
-    const uint32_t target = G >> 2;
+    const uint64_t target = static_cast<uint64_t>(G) * kTabBucketsPerGroup;
     uint32_t shift = 0;
-    while ((span >> shift) + 1 > target) ++shift;
+    while ((span >> shift) + 1ull > target) ++shift;
     return shift;
 }
 
-// Entries of every node's bucket table: B + 1 for a node with B buckets,
-// 0 for nodes with at most kTabMin groups.
-__global__ void node_table_sizes_kernel(const uint32_t* __restrict__ cnt,
-                                        const PanelRec* __restrict__ pan, size_t v,
-                                        uint32_t* __restrict__ sizes) {
-    const size_t u = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
-    if (u >= v) return;
-    const uint32_t gb = cnt[u], ge = cnt[u + 1];
-    uint32_t size = 0;
-    if (ge - gb > kTabMin) {
-        const uint32_t span = pan[ge - 1].rank - pan[gb].rank;
-        size = (span >> table_shift(ge - gb, span)) + 2;
-    }
-    sizes[u] = size;
-}
-
 __global__ void node_headers_kernel(const uint32_t* __restrict__ cnt,
-                                    const PanelRec* __restrict__ pan,
-                                    const uint32_t* __restrict__ base, size_t vc,
+                                    const PanelRec* __restrict__ pan, size_t vc,
                                     NodeHdr* __restrict__ hdr) {
     const size_t u = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
     if (u >= vc) return;
     const uint32_t gb = cnt[u];
-    NodeHdr h{gb, base[u], 0, 0};
+    NodeHdr h{gb, 0, 0, 0};
     if (u + 1 < vc) {
-        const uint32_t ge = cnt[u + 1];
-        if (ge - gb > kTabMin) {
+        const uint32_t G = cnt[u + 1] - gb;
+        uint32_t shift = 0;
+        if (G > kTabMin) {
             h.r0 = pan[gb].rank;
-            h.shift = table_shift(ge - gb, pan[ge - 1].rank - h.r0);
+            const uint32_t span = pan[gb + G - 1].rank - h.r0;
+            shift = table_shift(G, span);
+            h.nb = (span >> shift) + 1;
         }
+        h.meta = (G < kHdrGMask ? G : kHdrGMask) | (shift << 24);
     }
     hdr[u] = h;
 }
@@ -307,11 +294,13 @@ __global__ void node_table_fill_kernel(const uint32_t* __restrict__ key,
     const NodeHdr h = hdr[u];
     const uint32_t G = hdr[u + 1].gb - h.gb;
     if (G <= kTabMin) return;
+    const uint32_t shift = hdr_shift(h);
+    uint32_t* t = tab + hdr_tab_base(h, u);
     const uint32_t i = static_cast<uint32_t>(g) - h.gb;
-    const uint32_t bi = (pan[g].rank - h.r0) >> h.shift;
-    const uint32_t from = i == 0 ? 0u : ((pan[g - 1].rank - h.r0) >> h.shift) + 1;
-    for (uint32_t b = from; b <= bi; ++b) tab[h.tab + b] = i;
-    if (i == G - 1) tab[h.tab + bi + 1] = G;
+    const uint32_t bi = (pan[g].rank - h.r0) >> shift;
+    const uint32_t from = i == 0 ? 0u : ((pan[g - 1].rank - h.r0) >> shift) + 1;
+    for (uint32_t b = from; b <= bi; ++b) t[b] = i;
+    if (i == G - 1) t[bi + 1] = G;
 }
 
 // Weight search index (see engine.h): entries per node, then one thread per
@@ -668,22 +657,11 @@ void build_direction(Engine& e, DirIndex& dir, size_t n, int key_bits, size_t vc
                        e.scan.p, vc, dir.cnt.p);
 
     // walk search headers and bucket tables
-    const size_t v = vc - 1;
-    e.flags.ensure(vc);
-    e.scan.ensure(vc);
-    e.scan_scratch.ensure(scan_scratch_elems(vc));
-    hipLaunchKernelGGL(node_table_sizes_kernel, dim3(grid_for(v)), dim3(kB), 0, s, dir.cnt.p,
-                       dir.pan.p, v, e.flags.p);
-    exclusive_scan_u32(e.flags.p, e.scan.p, v, e.scan_scratch.p, s);
     dir.hdr.resize(vc);
     hipLaunchKernelGGL(node_headers_kernel, dim3(grid_for(vc)), dim3(kB), 0, s, dir.cnt.p,
-                       dir.pan.p, e.scan.p, vc, dir.hdr.p);
-    uint32_t tab_n = 0;
-    check_hip(hipMemcpyAsync(host_scratch, e.scan.p + v, 4, hipMemcpyDeviceToHost, s), "read tab");
-    e.sync();
-    std::memcpy(&tab_n, host_scratch, 4);
-    dir.tab.resize(tab_n);
-    if (tab_n && g)
+                       dir.pan.p, vc, dir.hdr.p);
+    dir.tab.resize(2 * (static_cast<size_t>(g) + vc));
+    if (g)
         hipLaunchKernelGGL(node_table_fill_kernel, dim3(grid_for(g)), dim3(kB), 0, s, dir.key.p,
                            dir.grp.p, dir.hdr.p, dir.pan.p, static_cast<size_t>(g), dir.tab.p);
     check_hip(hipGetLastError(), "direction index launch");

@@ -16,12 +16,14 @@
 //     rec           EdgeRec[n]     (neighbour, edge id) in the same order
 //     cnt           uint32[V_c]    exclusive prefix of per-node group counts
 //     hdr           NodeHdr[V_c]   the walk's per-node header: first group,
-//                                  bucket table base, first rank, bucket shift
-//     tab           uint32[..]     bucket tables of nodes with > kTabMin groups:
-//                                  bucket b of node u covers the ranks
-//                                  [r0 + (b << shift), r0 + ((b + 1) << shift))
-//                                  and holds the first of u's groups that
-//                                  reaches it; the last entry is G
+//                                  group count, bucket shift, first rank,
+//                                  bucket count
+//     tab           uint32[2(g+V_c)] bucket tables of nodes with > kTabMin
+//                                  groups, node u's at 2 (gb + u): bucket b
+//                                  covers the ranks [r0 + (b << shift),
+//                                  r0 + ((b + 1) << shift)) and holds the
+//                                  first of u's groups that reaches it; a
+//                                  closing entry G follows the last bucket
 //     grp           uint32[g+1]    group starts into idx, plus a terminator
 //     first_ts      int64[g]       timestamp of every node-timestamp group
 //     pan           PanelRec[g+1]  (ts rank, start) of every group, plus a
@@ -143,15 +145,26 @@ __host__ __device__ inline uint32_t wx_size(uint32_t G) {
 // Nodes with more groups than this get a bucket table for the walk's search;
 // smaller ones are binary-searched directly (at most two panel lines).
 constexpr uint32_t kTabMin = 16;
+// A node's table has at most this many buckets per group: hubs whose groups
+// cover most ranks of their span get single-rank buckets, whose entry is the
+// search's answer.
+constexpr uint32_t kTabBucketsPerGroup = 2;
 
-// Per-node header of the walk's group search.  The next node's header closes
-// the node: its gb is this node's group end and its tab this table's end.
+// Per-node header of the walk's group search, read with one 16-byte load.
+// Node u's bucket table starts at entry 2 * (gb + u) of `tab` (room for the
+// 2 * G + 1 entries its at most 2 * G buckets need, so no base is stored).
 struct alignas(16) NodeHdr {
-    uint32_t gb;     // first group of the node
-    uint32_t tab;    // first entry of its bucket table
-    uint32_t r0;     // rank of its first group (tabled nodes)
-    uint32_t shift;  // log2 of its bucket width in ranks (tabled nodes)
+    uint32_t gb;    // first group of the node
+    uint32_t meta;  // G (bits 0-23, kHdrGMask if larger: read the next gb),
+                    // bucket shift (bits 24-28)
+    uint32_t r0;    // rank of its first group (tabled nodes)
+    uint32_t nb;    // number of buckets (tabled nodes)
 };
+constexpr uint32_t kHdrGMask = 0xffffffu;
+__host__ __device__ inline uint32_t hdr_shift(const NodeHdr& h) { return (h.meta >> 24) & 31u; }
+__host__ __device__ inline uint64_t hdr_tab_base(const NodeHdr& h, uint32_t u) {
+    return 2ull * (static_cast<uint64_t>(h.gb) + u);
+}
 static_assert(sizeof(NodeHdr) == 16, "NodeHdr must be 16 bytes");
 
 // One node-timestamp group in the walk's search panel.

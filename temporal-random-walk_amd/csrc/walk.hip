@@ -140,6 +140,17 @@ __device__ __forceinline__ Hop hop_of(const EdgeRec& rec, uint32_t rank) {
 
 __device__ __forceinline__ EdgeRec load_rec(const EdgeRec* p) { return *p; }
 
+// A group's panel record and the next group's start (its end), read as one
+// 16-byte load at the record's 8-byte alignment.
+struct PanelPair {
+    uint32_t rank, start, next_rank, next_start;
+};
+typedef uint32_t u32x4_a8 __attribute__((ext_vector_type(4), aligned(8)));
+__device__ __forceinline__ PanelPair load_pair(const PanelRec* p) {
+    const u32x4_a8 v = *reinterpret_cast<const u32x4_a8*>(p);
+    return PanelPair{v.x, v.y, v.z, v.w};
+}
+
 // The slot-major walk scratch is written once and read once by the layout
 // pass: non-temporal stores keep it from evicting the node panels from L2.
 template <typename T>
@@ -147,21 +158,27 @@ __device__ __forceinline__ void store_out(T* p, T v) {
     __builtin_nontemporal_store(v, p);
 }
 
+typedef uint32_t u32x2_a4 __attribute__((ext_vector_type(2), aligned(4)));
+
 // First local index i in [0, G) whose group rank is >= x, G if none: a
 // lower_bound over the node's sorted panel, so the answer is unique and the
 // way it is found does not change any result.  A node with more than kTabMin
-// groups first takes the bracket [tab[b], tab[b + 1]] of x's bucket b from
-// its table (about four groups); the rest is a binary search over at most
-// kTabMin groups.
-__device__ __forceinline__ int first_ge(const uint32_t* tab, const NodeHdr& h, uint32_t tab_end,
-                                        const PanelRec* f, int G, uint32_t x) {
+// groups first looks up x's bucket b in its table: a single-rank bucket holds
+// the answer itself; a wider one gives the bracket [tab[b], tab[b + 1]]
+// (about one group).  The rest is a binary search over at most kTabMin groups.
+__device__ __forceinline__ int first_ge(const uint32_t* tab, const NodeHdr& h, uint32_t u, int G,
+                                        const PanelRec* f, uint32_t x) {
     int lo = 0, hi = G;
     if (G > static_cast<int>(kTabMin)) {
         if (x <= h.r0) return 0;
-        const uint32_t b = (x - h.r0) >> h.shift;
-        if (b >= tab_end - h.tab - 1) return G;  // past the last bucket
-        lo = static_cast<int>(tab[h.tab + b]);
-        hi = static_cast<int>(tab[h.tab + b + 1]);
+        const uint32_t shift = hdr_shift(h);
+        const uint32_t b = (x - h.r0) >> shift;
+        if (b >= h.nb) return G;  // past the last bucket
+        const uint32_t* t = tab + hdr_tab_base(h, u) + b;
+        if (shift == 0) return static_cast<int>(t[0]);
+        const u32x2_a4 br = *reinterpret_cast<const u32x2_a4*>(t);  // one 8-byte load
+        lo = static_cast<int>(br.x);
+        hi = static_cast<int>(br.y);
     }
     while (lo < hi) {
         const int mid = lo + ((hi - lo) >> 1);
@@ -309,8 +326,8 @@ __device__ Hop tn2v_pick(const WalkGraph& g, int prev, uint32_t vb, uint32_t ve,
         // a pick one past the node's last group is an empty range in the
         // reference (get_node_group_edge_end, walk_step_helpers.cuh:19-38)
         if (static_cast<uint32_t>(gp) >= ge) continue;
-        const PanelRec pr = g.d.pan[gp];
-        const uint32_t es = pr.start, ee = g.d.pan[gp + 1].start;
+        const PanelPair pr = load_pair(g.d.pan + gp);
+        const uint32_t es = pr.start, ee = pr.next_start;
         if (es >= ee) continue;
         const uint64_t local = static_cast<uint64_t>(er * static_cast<double>(ee - es));
         const uint32_t pick = es + static_cast<uint32_t>(local < ee - es ? local : ee - es - 1);
@@ -333,22 +350,24 @@ template <bool Fwd, int Fam>
 __device__ Hop node_edge_at(const WalkGraph& g, int picker, int node, int32_t t, int32_t cut,
                             int prev, double rg, double re) {
     if (!(node >= 0 && node < g.active_size)) return no_hop();
-    const NodeHdr h = g.d.hdr[node];
-    const NodeHdr hn = g.d.hdr[node + 1];
-    const uint32_t gb = h.gb, ge = hn.gb;
-    if (gb == ge) return no_hop();
-    const int G = static_cast<int>(ge - gb);
+    const uint32_t u = static_cast<uint32_t>(node);
+    const NodeHdr h = g.d.hdr[u];
+    uint32_t Gu = h.meta & kHdrGMask;
+    if (Gu == kHdrGMask) Gu = g.d.hdr[u + 1].gb - h.gb;  // more groups than 24 bits hold
+    if (Gu == 0) return no_hop();
+    const uint32_t gb = h.gb, ge = gb + Gu;
+    const int G = static_cast<int>(Gu);
     const PanelRec* fts = g.d.pan + gb;
     // filter_valid_groups_by_timestamp_slice (edge_selectors.cuh:66-120)
     int vb = 0, ve = G;
     if (t != -1) {
         const uint32_t x = static_cast<uint32_t>(t);
-        if (Fwd) vb = first_ge(g.d.tab, h, hn.tab, fts, G, x + 1);  // upper_bound
-        else ve = first_ge(g.d.tab, h, hn.tab, fts, G, x);         // lower_bound
+        if (Fwd) vb = first_ge(g.d.tab, h, u, G, fts, x + 1);  // upper_bound
+        else ve = first_ge(g.d.tab, h, u, G, fts, x);         // lower_bound
     }
     if (cut != -1) {
         // the first group at or past the cutoff, within [vb, ve]
-        const int c = first_ge(g.d.tab, h, hn.tab, fts, G, static_cast<uint32_t>(cut));
+        const int c = first_ge(g.d.tab, h, u, G, fts, static_cast<uint32_t>(cut));
         ve = c < vb ? vb : (c < ve ? c : ve);
     }
     if (vb >= ve) return no_hop();
@@ -373,12 +392,12 @@ __device__ Hop node_edge_at(const WalkGraph& g, int picker, int node, int32_t t,
     // A weight pick one past the node's last group reads, in the reference, the
     // next node's first group start for both ends: an empty range.
     if (gpos >= ge) return no_hop();
-    const PanelRec pr = g.d.pan[gpos];
-    const uint32_t es = pr.start, ee = g.d.pan[gpos + 1].start;
+    const PanelPair pp = load_pair(g.d.pan + gpos);
+    const uint32_t es = pp.start, ee = pp.next_start;
     if (es >= ee || es >= g.d.idx_size || ee > g.d.idx_size) return no_hop();
     return hop_of(load_rec(g.d.rec + es +
                            static_cast<uint32_t>(static_cast<int>(re * static_cast<int>(ee - es)))),
-                  pr.rank);
+                  pp.rank);
 }
 
 // Rank bound of a walk's cutoff time: groups at or past it are excluded
