@@ -35,6 +35,9 @@ namespace {
 
 constexpr int kB = 256;
 
+// Walks per tile of the walk scratch (one wave).
+constexpr uint64_t kScratchTile = 64;
+
 // Samples of at least this many walks run sorted by start time (TRW_ORDER_AUTO).
 constexpr uint64_t kTimeOrderMinWalks = 1ull << 16;
 
@@ -485,14 +488,17 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
         a.lens[w] = 0;
         return;
     }
-    // Slot-major scratch: slot k of grid position q lives at [k * n + q], so
-    // the 64 lanes of a wave store 256 B per slot and array contiguously.
-    // layout_walks_kernel produces the row-major output in the reference's
+    // Tile-major scratch: grid positions come in tiles of 64 (one wave), and
+    // slot k of position q lives at [(q / 64) * 64 * K + k * 64 + q % 64] (K
+    // slots per row), so the wave stores 256 B per slot and array
+    // contiguously and a tile's whole scratch is one contiguous run for the
+    // layout pass, which produces the row-major output in the reference's
     // types, the padding and the chronological order of backward walks.
-    const uint64_t n = a.n;
-    int32_t* wn = a.nodes + q;
-    uint32_t* wt = a.ranks + q;
-    uint32_t* we = a.eids + q;
+    constexpr uint64_t n = kScratchTile;
+    const uint64_t tile = q / kScratchTile, lane = q % kScratchTile;
+    int32_t* wn = a.nodes + tile * kScratchTile * static_cast<uint64_t>(L) + lane;
+    uint32_t* wt = a.ranks + tile * kScratchTile * static_cast<uint64_t>(L) + lane;
+    uint32_t* we = a.eids + tile * kScratchTile * static_cast<uint64_t>(L - 1) + lane;
     const int32_t cut = cutoff_rank(g, a, w);
     // the reference's tests of a current time of -1, on ranks
     const int32_t neg1 = *g.neg1_rank;
@@ -549,8 +555,10 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
 // together).  One tile is reused by the three arrays.  Column q holds walk
 // order[q] when the walks ran in another order than their ids; its row goes to
 // that walk's place.  In walk-id order the 64 rows are one contiguous span of
-// the output, so no cache line is shared with another workgroup.
+// the output, so no cache line is shared with another workgroup.  Scratch is
+// read and output written once, with non-temporal hints.
 constexpr int kLayoutWalks = 64;
+static_assert(kLayoutWalks == kScratchTile, "a layout workgroup owns one scratch tile");
 constexpr int kLayoutMaxSlots = 128;  // tile <= 33 KB of LDS
 
 struct LayoutArgs {
@@ -561,7 +569,6 @@ struct LayoutArgs {
     int64_t* ot;
     int64_t* oe;
     const uint64_t* lens;
-    uint64_t n;
     int L;
     int C;  // slots per chunk
     int reverse;
@@ -571,6 +578,9 @@ struct LayoutArgs {
     const uint32_t* order;  // walk of each scratch column (nullptr: the column index)
     uint64_t q0, q_end;     // scratch columns [q0, q_end) of this launch (q0 % 64 == 0)
 };
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int64_t i64x2 __attribute__((ext_vector_type(2)));
 
 // Value of output slot i of a row whose first `cw` slots were written (x: the
 // scratch value).  Arr 0: nodes, 1: timestamps, 2: edge ids.
@@ -600,6 +610,7 @@ __device__ __forceinline__ void layout_array(const LayoutArgs& a, uint32_t* tile
     const bool rev_in = a.reverse && !whole;
     // slots at or past the count are not read; the writer pads them
     const uint32_t* in = Arr == 0 ? reinterpret_cast<const uint32_t*>(a.sn) : (Arr == 1 ? a.sr : a.se);
+    const uint64_t tile_base = w0 * static_cast<uint64_t>(K);  // w0 % kScratchTile == 0
     for (int j0 = 0; j0 < kc; j0 += 32) {
         uint32_t v[8];
 #pragma unroll
@@ -608,7 +619,8 @@ __device__ __forceinline__ void layout_array(const LayoutArgs& a, uint32_t* tile
             const int k = k0 + r;
             uint32_t x = 0;
             if (r < kc && w < a.q_end && k < c)
-                x = in[static_cast<uint64_t>(rev_in ? c - 1 - k : k) * a.n + w];
+                x = __builtin_nontemporal_load(
+                    in + tile_base + static_cast<uint64_t>(rev_in ? c - 1 - k : k) * kScratchTile + wl);
             v[j] = x;
         }
 #pragma unroll
@@ -634,26 +646,24 @@ __device__ __forceinline__ void layout_array(const LayoutArgs& a, uint32_t* tile
         if (vec) {
             for (int i = lane * V; i < kc; i += 64 * V) {
                 if (Arr == 0) {
-                    int4 o;
-                    o.x = static_cast<int32_t>(layout_value<0>(a, src(i), i, cw));
-                    o.y = static_cast<int32_t>(layout_value<0>(a, src(i + 1), i + 1, cw));
-                    o.z = static_cast<int32_t>(layout_value<0>(a, src(i + 2), i + 2, cw));
-                    o.w = static_cast<int32_t>(layout_value<0>(a, src(i + 3), i + 3, cw));
-                    *reinterpret_cast<int4*>(a.on + base + i) = o;
+                    const i32x4 o = {static_cast<int32_t>(layout_value<0>(a, src(i), i, cw)),
+                                     static_cast<int32_t>(layout_value<0>(a, src(i + 1), i + 1, cw)),
+                                     static_cast<int32_t>(layout_value<0>(a, src(i + 2), i + 2, cw)),
+                                     static_cast<int32_t>(layout_value<0>(a, src(i + 3), i + 3, cw))};
+                    __builtin_nontemporal_store(o, reinterpret_cast<i32x4*>(a.on + base + i));
                 } else {
-                    longlong2 o;
-                    o.x = layout_value<Arr>(a, src(i), i, cw);
-                    o.y = layout_value<Arr>(a, src(i + 1), i + 1, cw);
+                    const i64x2 o = {layout_value<Arr>(a, src(i), i, cw),
+                                     layout_value<Arr>(a, src(i + 1), i + 1, cw)};
                     int64_t* out = Arr == 1 ? a.ot : a.oe;
-                    *reinterpret_cast<longlong2*>(out + base + i) = o;
+                    __builtin_nontemporal_store(o, reinterpret_cast<i64x2*>(out + base + i));
                 }
             }
         } else {
             for (int i = lane; i < kc; i += 64) {
                 const int64_t y = layout_value<Arr>(a, src(i), i, cw);
-                if (Arr == 0) a.on[base + i] = static_cast<int32_t>(y);
-                else if (Arr == 1) a.ot[base + i] = y;
-                else a.oe[base + i] = y;
+                if (Arr == 0) __builtin_nontemporal_store(static_cast<int32_t>(y), a.on + base + i);
+                else if (Arr == 1) __builtin_nontemporal_store(y, a.ot + base + i);
+                else __builtin_nontemporal_store(y, a.oe + base + i);
             }
         }
     }
@@ -1014,9 +1024,11 @@ void Engine::sample(const trw_sample_params& p) {
     // ---- outputs
     const uint64_t slots = nw * static_cast<uint64_t>(L);
     const uint64_t eslots = nw * static_cast<uint64_t>(L > 0 ? L - 1 : 0);
-    sw_nodes.resize(slots);
-    sw_rank.resize(slots);
-    sw_eids.resize(eslots);
+    // scratch: whole tiles of kScratchTile walks
+    const uint64_t padded = (nw + kScratchTile - 1) / kScratchTile * kScratchTile;
+    sw_nodes.resize(padded * L);
+    sw_rank.resize(padded * L);
+    sw_eids.resize(padded * (L > 0 ? L - 1 : 0));
     w_nodes.resize(slots);
     w_ts.resize(slots);
     w_eids.resize(eslots);
@@ -1157,7 +1169,6 @@ void Engine::sample(const trw_sample_params& p) {
         la.ot = w_ts.p;
         la.oe = w_eids.p;
         la.lens = w_lens.p;
-        la.n = nw;
         la.L = L;
         const int slot_chunks = (L + kLayoutMaxSlots - 1) / kLayoutMaxSlots;
         la.C = (L + slot_chunks - 1) / slot_chunks;
