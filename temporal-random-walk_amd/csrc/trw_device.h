@@ -49,8 +49,12 @@ __device__ __forceinline__ U4 philox4x32_10(U4 c, uint32_t k0, uint32_t k1) {
     constexpr uint32_t W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
 #pragma unroll
     for (int r = 0; r < 10; ++r) {
-        const uint32_t lo0 = M0 * c.x, hi0 = __umulhi(M0, c.x);
-        const uint32_t lo1 = M1 * c.z, hi1 = __umulhi(M1, c.z);
+        // one 32 x 32 -> 64-bit multiply per product (v_mad_u64_u32) gives
+        // both halves
+        const uint64_t p0 = static_cast<uint64_t>(M0) * c.x;
+        const uint64_t p1 = static_cast<uint64_t>(M1) * c.z;
+        const uint32_t lo0 = static_cast<uint32_t>(p0), hi0 = static_cast<uint32_t>(p0 >> 32);
+        const uint32_t lo1 = static_cast<uint32_t>(p1), hi1 = static_cast<uint32_t>(p1 >> 32);
         c = U4{hi1 ^ c.y ^ k0, lo1, hi0 ^ c.w ^ k1, lo0};
         k0 += W0;
         k1 += W1;
@@ -58,10 +62,13 @@ __device__ __forceinline__ U4 philox4x32_10(U4 c, uint32_t k0, uint32_t k1) {
     return c;
 }
 
-// 52 random bits -> a double strictly inside (0, 1): (m + 0.5) * 2^-52.
+// 52 random bits -> a double strictly inside (0, 1): (m + 0.5) * 2^-52, built
+// from the bits: 1 + m * 2^-52 has m as its mantissa, subtracting 1 is exact
+// (Sterbenz), and adding 2^-53 is exact because (2m + 1) * 2^-53 fits 53 bits.
 __device__ __forceinline__ double bits_to_unit(uint32_t lo, uint32_t hi) {
-    const uint64_t v = ((static_cast<uint64_t>(hi) << 32) | lo) >> 12;
-    return (static_cast<double>(v) + 0.5) * 2.220446049250313080847263336181640625e-16;
+    const uint64_t m = ((static_cast<uint64_t>(hi) << 32) | lo) >> 12;
+    const double one_m = __longlong_as_double(static_cast<long long>(0x3ff0000000000000ull | m));
+    return (one_m - 1.0) + 1.1102230246251565404236316680908203125e-16;
 }
 
 // ---------------------------------------------------------------------------
@@ -119,13 +126,18 @@ __device__ __forceinline__ int pick_linear(int start, int end, bool prioritize_e
     return start + max(0, len - 1 - index);
 }
 
+// Lengths below this take the expm1 branch of the exponential index picker.
+constexpr int kExpm1Table = 710;
+
+// em1: expm1(len) for len in [0, kExpm1Table) (the same values expm1 returns
+// here), or nullptr to evaluate it.
 __device__ __forceinline__ int pick_exponential_index(int start, int end, bool prioritize_end,
-                                                      double r) {
+                                                      double r, const double* em1 = nullptr) {
     if (start >= end) return -1;
     const int len = end - start;
     double k;
-    if (len < 710) {
-        k = log1p(r * expm1(static_cast<double>(len))) - 1;
+    if (len < kExpm1Table) {
+        k = log1p(r * (em1 ? em1[len] : expm1(static_cast<double>(len)))) - 1;
     } else {
         k = len + log(r) - 1;
     }
@@ -139,10 +151,10 @@ __device__ __forceinline__ int pick_uniform(int start, int end, double r) {
 }
 
 __device__ __forceinline__ int pick_index(int picker, int start, int end, bool prioritize_end,
-                                          double r) {
+                                          double r, const double* em1 = nullptr) {
     switch (picker) {
         case kLinear: return pick_linear(start, end, prioritize_end, r);
-        case kExponentialIndex: return pick_exponential_index(start, end, prioritize_end, r);
+        case kExponentialIndex: return pick_exponential_index(start, end, prioritize_end, r, em1);
         case kUniform: return pick_uniform(start, end, r);
         case kTestFirst: return start;
         case kTestLast: return end - 1;

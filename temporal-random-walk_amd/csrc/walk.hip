@@ -351,7 +351,7 @@ __device__ Hop tn2v_pick(const WalkGraph& g, int prev, uint32_t vb, uint32_t ve,
 // the walk's cutoff time (groups at or past it are excluded), -1 for none.
 template <bool Fwd, int Fam>
 __device__ Hop node_edge_at(const WalkGraph& g, int picker, int node, int32_t t, int32_t cut,
-                            int prev, double rg, double re) {
+                            int prev, double rg, double re, const double* em1 = nullptr) {
     if (!(node >= 0 && node < g.active_size)) return no_hop();
     const uint32_t u = static_cast<uint32_t>(node);
     const NodeHdr h = g.d.hdr[u];
@@ -377,7 +377,7 @@ __device__ Hop node_edge_at(const WalkGraph& g, int picker, int node, int32_t t,
     uint32_t gpos;
     if (Fam == kFamIndex || is_index_picker(picker)) {
         const int avail = ve - vb;
-        const int index = pick_index(picker, 0, avail, !Fwd, rg);
+        const int index = pick_index(picker, 0, avail, !Fwd, rg, em1);
         if (index == -1 || index >= avail) return no_hop();
         gpos = gb + static_cast<uint32_t>(vb + index);
     } else {
@@ -480,6 +480,15 @@ __device__ __forceinline__ uint64_t grid_position(int remap) {
 
 template <bool Fwd, bool Dir, int Fam>
 __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
+    // expm1 of every length the exponential index picker evaluates it for,
+    // once per workgroup instead of once per hop
+    __shared__ double s_em1[kExpm1Table];
+    const bool use_em1 = a.walk_bias == kExponentialIndex;
+    if (use_em1) {
+        for (int i = threadIdx.x; i < kExpm1Table; i += kB) s_em1[i] = expm1(static_cast<double>(i));
+        __syncthreads();
+    }
+    const double* em1 = use_em1 ? s_em1 : nullptr;
     const uint64_t q = a.q0 + grid_position(a.xcd_remap);
     if (q >= a.q_end) return;
     const uint64_t w = a.order ? a.order[q] : q;
@@ -524,7 +533,7 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
             if (walk_len == L - 1) break;
             const DrawPair r = draw_pair(a.ds, w, static_cast<uint32_t>(walk_len) + 1);
             const Hop h = node_edge_at<Fwd, Fam>(g, a.walk_bias, cur, cur_r == neg1 ? -1 : cur_r,
-                                                 cut, prev, r.a, r.b);
+                                                 cut, prev, r.a, r.b, em1);
             // the reference's failure test is ts == -1: no edge, or an edge at -1
             if (h.e == -1 || h.r == neg1) break;
             prev = cur;
