@@ -154,25 +154,37 @@ __global__ void neg1_rank_kernel(const int64_t* __restrict__ uq, uint32_t T,
     *out = (lo < T && uq[lo] == -1) ? static_cast<int32_t>(lo) : -2;
 }
 
-__global__ void node_keys_kernel(const int32_t* __restrict__ nodes, size_t n,
-                                 uint32_t* __restrict__ keys, uint32_t* __restrict__ vals) {
-    const size_t i = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
-    if (i >= n) return;
-    keys[i] = static_cast<uint32_t>(nodes[i]);
-    vals[i] = static_cast<uint32_t>(i);
+// Node-index entries: key = the list's node, value = the entry's walk record
+// (neighbour in the low word, edge id in the high word: EdgeRec's layout),
+// carried through the node sort so no record needs a gather afterwards.
+// mode 0: out-lists (node = source, neighbour = target); 1: in-lists (node =
+// target, neighbour = source); 2: undirected, entry 2i = (src_i; dst_i) and
+// entry 2i+1 = (dst_i; src_i) (node_edge_index.cu:306-321) -- the neighbour is
+// the reference's pick_other_number (utils/utils.cuh:102-104) seen from the
+// entry's node.
+__device__ __forceinline__ uint64_t pack_rec(int32_t nbr, uint32_t eid) {
+    return static_cast<uint64_t>(static_cast<uint32_t>(nbr)) | (static_cast<uint64_t>(eid) << 32);
 }
 
-// Undirected: entry 2i = (edge i, src_i), entry 2i+1 = (edge i, dst_i)
-// (node_edge_index.cu:306-321).
-__global__ void node_keys_pairs_kernel(const int32_t* __restrict__ s, const int32_t* __restrict__ d,
-                                       size_t e, uint32_t* __restrict__ keys,
-                                       uint32_t* __restrict__ vals) {
+__global__ void node_entries_kernel(const int32_t* __restrict__ src,
+                                    const int32_t* __restrict__ dst, size_t e, int mode,
+                                    uint32_t* __restrict__ keys, uint64_t* __restrict__ vals) {
     const size_t i = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
     if (i >= e) return;
-    keys[2 * i] = static_cast<uint32_t>(s[i]);
-    keys[2 * i + 1] = static_cast<uint32_t>(d[i]);
-    vals[2 * i] = static_cast<uint32_t>(i);
-    vals[2 * i + 1] = static_cast<uint32_t>(i);
+    const int32_t a = src[i], b = dst[i];
+    const uint32_t id = static_cast<uint32_t>(i);
+    if (mode == 0) {
+        keys[i] = static_cast<uint32_t>(a);
+        vals[i] = pack_rec(b, id);
+    } else if (mode == 1) {
+        keys[i] = static_cast<uint32_t>(b);
+        vals[i] = pack_rec(a, id);
+    } else {
+        keys[2 * i] = static_cast<uint32_t>(a);
+        vals[2 * i] = pack_rec(b, id);
+        keys[2 * i + 1] = static_cast<uint32_t>(b);
+        vals[2 * i + 1] = pack_rec(a, id);
+    }
 }
 
 // off[u] = first sorted position whose node >= u, u in [0, vc).
@@ -189,20 +201,34 @@ __global__ void lower_bound_offsets_kernel(const uint32_t* __restrict__ keys, si
     off[u] = static_cast<uint32_t>(lo);
 }
 
-__global__ void node_group_flags_kernel(const uint32_t* __restrict__ keys,
-                                        const uint32_t* __restrict__ idx,
-                                        const int64_t* __restrict__ ts, size_t n,
-                                        uint32_t* __restrict__ flags) {
+// Group-start flags of the sorted entries (a new node, or a new timestamp
+// rank within a node) and the sorted edge ids (node_ts_sorted_*_indices).  The
+// previous entry's node and rank come from the lane below.
+__global__ __launch_bounds__(kB) void node_group_flags_kernel(const uint32_t* __restrict__ keys,
+                                                              const EdgeRec* __restrict__ rec,
+                                                              const uint32_t* __restrict__ erank,
+                                                              size_t n,
+                                                              uint32_t* __restrict__ flags,
+                                                              uint32_t* __restrict__ idx) {
     const size_t k = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
-    if (k >= n) return;
-    flags[k] = (k == 0 || keys[k] != keys[k - 1] || ts[idx[k]] != ts[idx[k - 1]]) ? 1u : 0u;
+    if (k >= n) return;  // the active lanes of a wave are a prefix
+    const uint32_t key = keys[k];
+    const uint32_t e = rec[k].eid;
+    const uint32_t r = erank[e];
+    idx[k] = e;
+    uint32_t kp = __shfl_up(key, 1, 64), rp = __shfl_up(r, 1, 64);
+    if ((threadIdx.x & 63) == 0 && k > 0) {
+        kp = keys[k - 1];
+        rp = erank[rec[k - 1].eid];
+    }
+    flags[k] = (k == 0 || key != kp || r != rp) ? 1u : 0u;
 }
 
 __global__ void node_group_scatter_kernel(const uint32_t* __restrict__ flags,
                                           const uint32_t* __restrict__ scan,
                                           const uint32_t* __restrict__ idx,
-                                          const int64_t* __restrict__ ts,
-                                          const uint32_t* __restrict__ erank, size_t n,
+                                          const uint32_t* __restrict__ erank,
+                                          const int64_t* __restrict__ uniq_ts, size_t n,
                                           uint32_t* __restrict__ grp,
                                           int64_t* __restrict__ first_ts,
                                           PanelRec* __restrict__ pan) {
@@ -210,34 +236,15 @@ __global__ void node_group_scatter_kernel(const uint32_t* __restrict__ flags,
     if (k >= n) return;
     if (flags[k]) {
         const uint32_t g = scan[k];
-        const uint32_t e = idx[k];
+        const uint32_t r = erank[idx[k]];
         grp[g] = static_cast<uint32_t>(k);
-        first_ts[g] = ts[e];
-        pan[g] = PanelRec{erank[e], static_cast<uint32_t>(k)};
+        first_ts[g] = uniq_ts[r];
+        pan[g] = PanelRec{r, static_cast<uint32_t>(k)};
     }
     if (k == n - 1) {
         grp[scan[n]] = static_cast<uint32_t>(n);
         pan[scan[n]] = PanelRec{0xffffffffu, static_cast<uint32_t>(n)};
     }
-}
-
-// Walk-order edge records.  mode 0: neighbour = target (out-lists of a
-// directed graph), 1: source (in-lists), 2: the other endpoint of an undirected
-// edge, (src == node) ? dst : src -- the reference's pick_other_number
-// (utils/utils.cuh:102-104) seen from the list's node.
-__global__ void make_records_kernel(const uint32_t* __restrict__ keys,
-                                    const uint32_t* __restrict__ idx,
-                                    const int32_t* __restrict__ src,
-                                    const int32_t* __restrict__ dst, size_t n, int mode,
-                                    EdgeRec* __restrict__ rec) {
-    const size_t k = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
-    if (k >= n) return;
-    const uint32_t e = idx[k];
-    int32_t nbr;
-    if (mode == 0) nbr = dst[e];
-    else if (mode == 1) nbr = src[e];
-    else nbr = (src[e] == static_cast<int32_t>(keys[k])) ? dst[e] : src[e];
-    rec[k] = EdgeRec{nbr, e};
 }
 
 // cnt[u] = number of groups of nodes < u = flag scan at u's first entry.
@@ -612,29 +619,39 @@ void validate_batch(const Engine& e, const void* feat, size_t n, size_t dim) {
 
 namespace {
 
-// Stable per-direction node index from `keys`/`vals` already generated in
-// e.k32a / e.v32a (n entries).
-void build_direction(Engine& e, DirIndex& dir, size_t n, int key_bits, size_t vc, int rec_mode,
+// Stable per-direction node index of the store's n entries (mode: see
+// node_entries_kernel).
+void build_direction(Engine& e, DirIndex& dir, size_t n, int key_bits, size_t vc, int mode,
                      int64_t* host_scratch) {
     hipStream_t s = e.stream;
     dir.present = true;
     dir.n_entries = n;
-    const int which = radix_sort_u32(e.k32a.p, e.v32a.p, e.k32b.p, e.v32b.p, n, 0, key_bits,
-                                     e.hist.p, e.hist_scratch.p, s);
-    // the sorted buffers become the direction's arrays (the scratch takes the
-    // old ones, which every user sizes again before writing)
-    dir.key.swap(which ? e.k32b : e.k32a);
-    dir.idx.swap(which ? e.v32b : e.v32a);
-    dir.key.n = n;
-    dir.idx.n = n;
+    // the sorted records land in dir.rec: start in the buffer set the last
+    // digit pass does not write into
     dir.rec.resize(n);
-    hipLaunchKernelGGL(make_records_kernel, dim3(grid_for(n)), dim3(kB), 0, s, dir.key.p, dir.idx.p,
-                       e.src.p, e.dst.p, n, rec_mode, dir.rec.p);
+    e.k32a.ensure(n);
+    e.k32b.ensure(n);
+    e.k64a.ensure(n);
+    const int passes = n > 1 ? radix_passes(0, key_bits) : 0;
+    uint64_t* recs = reinterpret_cast<uint64_t*>(dir.rec.p);
+    uint64_t* v0 = passes % 2 == 0 ? recs : e.k64a.p;
+    uint64_t* v1 = passes % 2 == 0 ? e.k64a.p : recs;
+    const size_t edges = mode == 2 ? n / 2 : n;
+    if (edges)
+        hipLaunchKernelGGL(node_entries_kernel, dim3(grid_for(edges)), dim3(kB), 0, s, e.src.p,
+                           e.dst.p, edges, mode, e.k32a.p, v0);
+    const int which = radix_sort_u32_v64(e.k32a.p, v0, e.k32b.p, v1, n, 0, key_bits, e.hist.p,
+                                         e.hist_scratch.p, s);
+    // the sorted keys become the direction's (the scratch takes the old
+    // buffer, which every user sizes again before writing)
+    dir.key.swap(which ? e.k32b : e.k32a);
+    dir.key.n = n;
+    dir.idx.resize(n);
     dir.off.resize(vc);
     hipLaunchKernelGGL(lower_bound_offsets_kernel, dim3(grid_for(vc)), dim3(kB), 0, s, dir.key.p,
                        n, vc, dir.off.p);
     hipLaunchKernelGGL(node_group_flags_kernel, dim3(grid_for(n)), dim3(kB), 0, s, dir.key.p,
-                       dir.idx.p, e.ts.p, n, e.flags.p);
+                       dir.rec.p, e.erank.p, n, e.flags.p, dir.idx.p);
     exclusive_scan_u32(e.flags.p, e.scan.p, n, e.scan_scratch.p, s);
     uint32_t g = 0;
     check_hip(hipMemcpyAsync(host_scratch, e.scan.p + n, 4, hipMemcpyDeviceToHost, s), "read g");
@@ -646,7 +663,7 @@ void build_direction(Engine& e, DirIndex& dir, size_t n, int key_bits, size_t vc
     dir.pan.resize(static_cast<size_t>(g) + 1);
     if (n) {
         hipLaunchKernelGGL(node_group_scatter_kernel, dim3(grid_for(n)), dim3(kB), 0, s,
-                           e.flags.p, e.scan.p, dir.idx.p, e.ts.p, e.erank.p, n, dir.grp.p,
+                           e.flags.p, e.scan.p, dir.idx.p, e.erank.p, e.uniq_ts.p, n, dir.grp.p,
                            dir.first_ts.p, dir.pan.p);
     } else {
         check_hip(hipMemsetAsync(dir.grp.p, 0, 4, s), "grp terminator");
@@ -869,22 +886,10 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
     const size_t v = static_cast<size_t>(max_node_id) + 1;  // active_node_ids size
     const size_t vc = v + 1;                                // node_index_capacity
     const int key_bits = std::max(1, bit_length_u64(static_cast<uint64_t>(max_node_id)));
-    k32a.ensure(2 * E);
-    k32b.ensure(2 * E);
     if (cfg.is_directed) {
-        hipLaunchKernelGGL(node_keys_kernel, dim3(grid_for(E)), dim3(kB), 0, s, src.p, E, k32a.p,
-                           v32a.p);
         build_direction(*this, out, E, key_bits, vc, 0, hs);
-        k32a.ensure(E);
-        k32b.ensure(E);
-        v32a.ensure(E);
-        v32b.ensure(E);
-        hipLaunchKernelGGL(node_keys_kernel, dim3(grid_for(E)), dim3(kB), 0, s, dst.p, E, k32a.p,
-                           v32a.p);
         build_direction(*this, in, E, key_bits, vc, 1, hs);
     } else {
-        hipLaunchKernelGGL(node_keys_pairs_kernel, dim3(grid_for(E)), dim3(kB), 0, s, src.p, dst.p,
-                           E, k32a.p, v32a.p);
         build_direction(*this, out, 2 * E, key_bits, vc, 2, hs);
         in.clear();
     }

@@ -231,10 +231,10 @@ __global__ __launch_bounds__(kBlock) void radix_upsweep_kernel(const K* __restri
     hist[static_cast<size_t>(d) * nb + blockIdx.x] = tot;
 }
 
-template <typename K>
+template <typename K, typename V>
 __global__ __launch_bounds__(kBlock) void radix_scatter_kernel(
-    const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, K* __restrict__ keys_out,
-    uint32_t* __restrict__ vals_out, size_t n, int bit, const uint32_t* __restrict__ offsets,
+    const K* __restrict__ keys_in, const V* __restrict__ vals_in, K* __restrict__ keys_out,
+    V* __restrict__ vals_out, size_t n, int bit, const uint32_t* __restrict__ offsets,
     size_t nb) {
     __shared__ uint32_t s_cnt[kWaves][kRadix];
     __shared__ uint32_t s_run[kRadix];  // the workgroup's next output position per digit
@@ -247,7 +247,7 @@ __global__ __launch_bounds__(kBlock) void radix_scatter_kernel(
         __syncthreads();
         const size_t wave_base = tile_base + static_cast<size_t>(wave) * kRows * 64;
         K key[kRows];
-        uint32_t val[kRows];
+        V val[kRows];
         uint32_t dig[kRows];
         uint32_t rank[kRows];
 #pragma unroll
@@ -255,7 +255,7 @@ __global__ __launch_bounds__(kBlock) void radix_scatter_kernel(
             const size_t i = wave_base + static_cast<size_t>(r) * 64 + lane;
             const bool valid = i < n;
             key[r] = valid ? keys_in[i] : K(0);
-            val[r] = (valid && vals_in) ? vals_in[i] : 0u;
+            val[r] = (valid && vals_in) ? vals_in[i] : V(0);
         }
 #pragma unroll
         for (int r = 0; r < kRows; ++r) {
@@ -297,20 +297,20 @@ __global__ __launch_bounds__(kBlock) void radix_scatter_kernel(
     }
 }
 
-template <typename K>
-int radix_sort_impl(K* keys0, uint32_t* vals0, K* keys1, uint32_t* vals1, size_t n,
+template <typename K, typename V = uint32_t>
+int radix_sort_impl(K* keys0, V* vals0, K* keys1, V* vals1, size_t n,
                     int begin_bit, int end_bit, uint32_t* hist, uint32_t* hist_scratch,
                     hipStream_t s) {
     if (n <= 1 || end_bit <= begin_bit) return 0;
     const size_t nb = (n + kSortSpan - 1) / kSortSpan;
     int cur = 0;
     K* kb[2] = {keys0, keys1};
-    uint32_t* vb[2] = {vals0, vals1};
+    V* vb[2] = {vals0, vals1};
     for (int bit = begin_bit; bit < end_bit; bit += kRadixBits) {
         hipLaunchKernelGGL((radix_upsweep_kernel<K>), dim3(nb), dim3(kBlock), 0, s, kb[cur], n,
                            bit, hist, nb);
         scan_impl<uint32_t, false>(hist, hist, nb * kRadix, hist_scratch, s);
-        hipLaunchKernelGGL((radix_scatter_kernel<K>), dim3(nb), dim3(kBlock), 0, s, kb[cur],
+        hipLaunchKernelGGL((radix_scatter_kernel<K, V>), dim3(nb), dim3(kBlock), 0, s, kb[cur],
                            vb[cur], kb[cur ^ 1], vb[cur ^ 1], n, bit, hist, nb);
         check_hip(hipGetLastError(), "radix sort launch");
         cur ^= 1;
@@ -452,6 +452,15 @@ int radix_sort_u32(uint32_t* keys0, uint32_t* vals0, uint32_t* keys1, uint32_t* 
                    hipStream_t s) {
     return radix_sort_impl<uint32_t>(keys0, vals0, keys1, vals1, n, begin_bit, end_bit, hist,
                                      hist_scratch, s);
+}
+int radix_sort_u32_v64(uint32_t* keys0, uint64_t* vals0, uint32_t* keys1, uint64_t* vals1,
+                       size_t n, int begin_bit, int end_bit, uint32_t* hist,
+                       uint32_t* hist_scratch, hipStream_t s) {
+    return radix_sort_impl<uint32_t, uint64_t>(keys0, vals0, keys1, vals1, n, begin_bit, end_bit,
+                                               hist, hist_scratch, s);
+}
+int radix_passes(int begin_bit, int end_bit) {
+    return end_bit > begin_bit ? (end_bit - begin_bit + kRadixBits - 1) / kRadixBits : 0;
 }
 
 // Scratch for the reductions lives in a small per-call static device buffer
