@@ -190,10 +190,12 @@ def main():
     T = len(eng.array("unique_timestamps"))
     idx_bytes = index_algorithmic_bytes(E, Vc, T, g_o, g_i)
 
-    traffic = None
+    traffic = l2_hit = None
     if os.path.exists(PMC_FILE):
         with open(PMC_FILE) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+            pmc = json.load(f)
+        traffic = pmc.get("hbm_bytes_per_launch")
+        l2_hit = pmc.get("l2_hit_rate")
 
     result = {
         "metric": METRIC,
@@ -239,6 +241,12 @@ def main():
             "algorithmic_bytes_per_launch": stats["reference_bytes"],
             "engine_types_bytes_per_launch": stats["algorithmic_bytes"],
             "engine_types_achieved": achieved_engine,
+            "traffic_GB_per_s": (traffic / (walk_kernel_ms * 1e-3) / 1e9) if traffic else None,
+            "l2_hit_rate": l2_hit,
+            "note": "algorithmic bytes count every walk's per-hop index reads (72 + 8*probes B "
+                    "with the reference's types); walks run in start-time order share those "
+                    "lines, so most are L2 hits and frac can exceed 1. traffic (PMC, L2 <-> "
+                    "fabric bytes of one launch) over the launch time is the HBM-side rate.",
         },
     }
 
