@@ -275,6 +275,26 @@ typedef struct trw_walk_stats {
 } trw_walk_stats;
 trw_status trw_get_walk_stats(void* handle, trw_walk_stats* out);
 
+/* ---- standalone pickers (proxies/RandomPicker.cu:11-313) --------------------- */
+
+/* n picks of an index picker (Uniform, Linear, ExponentialIndex, or the test
+ * pickers) over [start[i], end[i]), -1 for an empty range, each with one
+ * uniform draw: draws[i] (host, in [0, 1); pick_random_with_provided_number),
+ * or, with draws NULL, Philox4x32-10 keyed by seed (pick_random).  Host
+ * arrays; one launch on device_id (-1: the current device).  Replaces
+ * {Linear,ExponentialIndex,Uniform}RandomPicker (proxies/RandomPicker.cu:
+ * 11-215), which launch one single-thread kernel per pick. */
+trw_status trw_pick_index(int32_t device_id, int32_t picker, const int32_t* start,
+                          const int32_t* end, uint64_t n, int32_t prioritize_end,
+                          const double* draws, uint64_t seed, int32_t* out);
+/* n picks of WeightBasedRandomPicker (proxies/RandomPicker.cu:218-313) over one
+ * cumulative-weight array of `size` values: the lower_bound of
+ * start_sum + r * (end_sum - start_sum) in [group_start[i], group_end[i])
+ * (random/pickers.cuh:84-126), -1 for an invalid range.  Draws as above. */
+trw_status trw_pick_weights(int32_t device_id, const double* cumulative, uint64_t size,
+                            const uint64_t* group_start, const uint64_t* group_end, uint64_t n,
+                            const double* draws, uint64_t seed, int32_t* out);
+
 #ifdef __cplusplus
 }
 #endif

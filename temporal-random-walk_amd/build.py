@@ -43,7 +43,7 @@ HIP_FLAGS = [
     f"-I{INCLUDE}",
 ]
 
-HIP_SOURCES = ["primitives.hip", "build.hip", "walk.hip", "handoff.hip", "capi.hip"]
+HIP_SOURCES = ["primitives.hip", "build.hip", "walk.hip", "handoff.hip", "pickers.hip", "capi.hip"]
 
 
 def _run(cmd):
@@ -64,7 +64,7 @@ def build_engine() -> str:
         _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
         return obj
 
-    with ThreadPoolExecutor(max_workers=min(5, len(HIP_SOURCES))) as ex:
+    with ThreadPoolExecutor(max_workers=min(6, len(HIP_SOURCES))) as ex:
         objs = list(ex.map(compile_one, HIP_SOURCES))
     lib = os.path.join(OUT_DIR, "libtrw_engine.so")
     tmp = lib + ".tmp"
@@ -84,6 +84,7 @@ def build_python_module() -> str:
         "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
         f"-I{INCLUDE}", f"-I{HOST}", f"-I{pybind11.get_include()}", f"-I{py_inc}",
         os.path.join(HOST, "TemporalRandomWalk.cpp"),
+        os.path.join(HOST, "RandomPicker.cpp"),
         os.path.join(HOST, "py_module.cpp"),
         f"-L{OUT_DIR}", "-ltrw_engine", "-Wl,-rpath,$ORIGIN",
         "-o", tmp,

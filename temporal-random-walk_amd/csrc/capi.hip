@@ -80,6 +80,33 @@ trw_status guarded(void* h, F&& f) {
     }
 }
 
+// A call that needs no engine handle: on device_id (-1: the current device).
+template <typename F>
+trw_status guarded_device(int32_t device_id, F&& f) {
+    try {
+        int count = 0;
+        if (hipGetDeviceCount(&count) != hipSuccess || count == 0) {
+            g_last_error = "no HIP device available: this engine runs only on the GPU";
+            return TRW_ERR_NO_DEVICE;
+        }
+        int dev = device_id;
+        if (dev < 0) trw::check_hip(hipGetDevice(&dev), "hipGetDevice");
+        if (dev >= count) throw trw::InvalidArgument("device_id out of range");
+        DeviceGuard g(dev);
+        f();
+        return TRW_OK;
+    } catch (const trw::InvalidArgument& ex) {
+        g_last_error = ex.what();
+        return TRW_ERR_INVALID_ARGUMENT;
+    } catch (const std::bad_alloc& ex) {
+        g_last_error = ex.what();
+        return TRW_ERR_OUT_OF_MEMORY;
+    } catch (const std::exception& ex) {
+        g_last_error = ex.what();
+        return TRW_ERR_RUNTIME;
+    }
+}
+
 template <typename T>
 T* host_alloc(size_t n) {
     void* p = malloc(n ? n * sizeof(T) : 1);
@@ -391,6 +418,22 @@ trw_status trw_get_stream(void* handle, void** out_stream) {
 
 trw_status trw_get_walk_stats(void* handle, trw_walk_stats* out) {
     return guarded(handle, [&](Engine& e) { trw::walk_stats(e, out); });
+}
+
+trw_status trw_pick_index(int32_t device_id, int32_t picker, const int32_t* start,
+                          const int32_t* end, uint64_t n, int32_t prioritize_end,
+                          const double* draws, uint64_t seed, int32_t* out) {
+    return guarded_device(device_id, [&] {
+        trw::pick_index_batch(picker, start, end, n, prioritize_end != 0, draws, seed, out);
+    });
+}
+
+trw_status trw_pick_weights(int32_t device_id, const double* cumulative, uint64_t size,
+                            const uint64_t* group_start, const uint64_t* group_end, uint64_t n,
+                            const double* draws, uint64_t seed, int32_t* out) {
+    return guarded_device(device_id, [&] {
+        trw::pick_weights_batch(cumulative, size, group_start, group_end, n, draws, seed, out);
+    });
 }
 
 }  // extern "C"

@@ -332,6 +332,13 @@ struct Engine {
 // ---- launchers implemented in build.hip / walk.hip -------------------------
 void validate_batch(const Engine& e, const void* feat, size_t n, size_t dim);
 void walk_stats(Engine& e, trw_walk_stats* out);
+
+// Standalone pickers (pickers.hip): batches of picks, host arrays in and out.
+void pick_index_batch(int picker, const int32_t* start, const int32_t* end, uint64_t n,
+                      bool prioritize_end, const double* draws, uint64_t seed, int32_t* out);
+void pick_weights_batch(const double* cumulative, uint64_t size, const uint64_t* group_start,
+                        const uint64_t* group_end, uint64_t n, const double* draws, uint64_t seed,
+                        int32_t* out);
 // Rank of timestamp -1 among the stored unique timestamps (-2 if absent) into
 // e.neg1_rank, on the engine stream.
 void update_neg1_rank(Engine& e);

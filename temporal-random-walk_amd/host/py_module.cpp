@@ -11,6 +11,7 @@
 #include <optional>
 #include <stdexcept>
 
+#include "RandomPicker.h"
 #include "TemporalRandomWalk.h"
 
 namespace py = pybind11;
@@ -56,6 +57,54 @@ py::tuple walks_to_numpy(WalksWithEdgeFeaturesHost& walks, int max_walk_len) {
             static_cast<float*>(re.ptr), make_capsule(re));
     }
     return py::make_tuple(nodes, ts, lens, feats);
+}
+
+// numpy int32 array of a batch of picks
+py::array_t<int32_t> to_numpy(const std::vector<int32_t>& v) {
+    py::array_t<int32_t> out(static_cast<py::ssize_t>(v.size()));
+    std::copy(v.begin(), v.end(), out.mutable_data());
+    return out;
+}
+
+// Optional batch of uniforms, one per pick.
+const double* optional_draws(const std::optional<py::array_t<double, py::array::c_style |
+                                                                        py::array::forcecast>>& r,
+                             size_t n) {
+    if (!r.has_value()) return nullptr;
+    if (static_cast<size_t>(r->size()) != n)
+        throw std::invalid_argument("random_numbers must hold one value per pick");
+    return r->data();
+}
+
+// The reference's index-picker classes (py_interface/_temporal_random_walk.cu:
+// 904-984): same constructor and pick_random; pick_random_batch goes beyond it.
+template <typename Picker>
+void bind_index_picker(py::module& m, const char* name, const char* what) {
+    using Draws = std::optional<py::array_t<double, py::array::c_style | py::array::forcecast>>;
+    py::class_<Picker>(m, name)
+        .def(py::init([](bool use_gpu) { return Picker(use_gpu); }),
+             (std::string("Initialize ") + what + " random picker.\n\nArgs:\n    use_gpu (bool): "
+              "accepted for the reference's interface; picks run on the GPU.").c_str(),
+             py::arg("use_gpu") = false)
+        .def("pick_random", &Picker::pick_random,
+             (std::string("Pick a random index in [start, end) with ") + what +
+              " probability.\n\nArgs:\n    start (int): Start index inclusive\n    end (int): "
+              "End index exclusive\n    prioritize_end (bool, optional): Prioritize recent "
+              "timestamps. Default: True\n\nReturns:\n    int: Selected index")
+                 .c_str(),
+             py::arg("start"), py::arg("end"), py::arg("prioritize_end") = true)
+        .def(
+            "pick_random_batch",
+            [](const Picker& p, const std::vector<int32_t>& starts,
+               const std::vector<int32_t>& ends, bool prioritize_end, const Draws& r) {
+                return to_numpy(
+                    p.pick_random_batch(starts, ends, prioritize_end, optional_draws(r, starts.size())));
+            },
+            "One pick per [starts[i], ends[i]) range in one GPU launch; random_numbers "
+            "(uniforms in [0, 1), one per pick) replaces the in-kernel draws. Returns int32 "
+            "indices, -1 for an empty range.",
+            py::arg("starts"), py::arg("ends"), py::arg("prioritize_end") = true,
+            py::arg("random_numbers") = py::none());
 }
 
 }  // namespace
@@ -331,4 +380,39 @@ PYBIND11_MODULE(_temporal_random_walk, m) {
                 return g;
             },
             "Export graph to NetworkX format.");
+
+    bind_index_picker<LinearRandomPicker>(m, "LinearRandomPicker", "linear time decay");
+    bind_index_picker<ExponentialIndexRandomPicker>(m, "ExponentialIndexRandomPicker",
+                                                    "index based exponential time decay");
+    bind_index_picker<UniformRandomPicker>(m, "UniformRandomPicker", "uniform");
+
+    using Draws = std::optional<py::array_t<double, py::array::c_style | py::array::forcecast>>;
+    py::class_<WeightBasedRandomPicker>(m, "WeightBasedRandomPicker")
+        .def(py::init([](bool use_gpu) { return WeightBasedRandomPicker(use_gpu); }),
+             "Initialize weight-based exponential time decay random picker.\n\nArgs:\n    "
+             "use_gpu (bool): accepted for the reference's interface; picks run on the GPU.",
+             py::arg("use_gpu") = false)
+        .def(
+            "pick_random",
+            [](const WeightBasedRandomPicker& p, const std::vector<double>& cumulative_weights,
+               int group_start, int group_end) {
+                return p.pick_random(cumulative_weights, group_start, group_end);
+            },
+            "Pick random index with exponential weight-based probability using cumulative "
+            "weights.\n\nArgs:\n    cumulative_weights (List[float]): List of cumulative "
+            "weights\n    group_start (int): Start index inclusive\n    group_end (int): End "
+            "index exclusive\n\nReturns:\n    int: Selected index",
+            py::arg("cumulative_weights"), py::arg("group_start"), py::arg("group_end"))
+        .def(
+            "pick_random_batch",
+            [](const WeightBasedRandomPicker& p, const std::vector<double>& cumulative_weights,
+               const std::vector<uint64_t>& group_starts, const std::vector<uint64_t>& group_ends,
+               const Draws& r) {
+                return to_numpy(p.pick_random_batch(cumulative_weights, group_starts, group_ends,
+                                                    optional_draws(r, group_starts.size())));
+            },
+            "One pick per [group_starts[i], group_ends[i]) range of one cumulative-weight "
+            "array, in one GPU launch; random_numbers as for the index pickers.",
+            py::arg("cumulative_weights"), py::arg("group_starts"), py::arg("group_ends"),
+            py::arg("random_numbers") = py::none());
 }

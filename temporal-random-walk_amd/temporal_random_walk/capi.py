@@ -65,7 +65,7 @@ EXPORTS = [
     "trw_get_node_count", "trw_get_edge_count", "trw_get_node_ids", "trw_get_node_degrees",
     "trw_get_edges", "trw_get_is_directed", "trw_get_memory_used", "trw_get_feature_dim",
     "trw_get_latest_timestamp", "trw_clear", "trw_get_array", "trw_get_timings",
-    "trw_get_stream", "trw_get_walk_stats",
+    "trw_get_stream", "trw_get_walk_stats", "trw_pick_index", "trw_pick_weights",
 ]
 
 
@@ -183,6 +183,10 @@ def lib():
         L.trw_get_timings.argtypes = [P, C.POINTER(TrwTimings)]
         L.trw_get_stream.argtypes = [P, C.POINTER(C.c_void_p)]
         L.trw_get_walk_stats.argtypes = [P, C.POINTER(TrwWalkStats)]
+        L.trw_pick_index.argtypes = [C.c_int32, C.c_int32, P, P, C.c_uint64, C.c_int32, P,
+                                     C.c_uint64, P]
+        L.trw_pick_weights.argtypes = [C.c_int32, P, C.c_uint64, P, P, C.c_uint64, P,
+                                       C.c_uint64, P]
         if L.trw_abi_version() != ABI_VERSION:
             raise ImportError(f"{LIB_PATH} has ABI {L.trw_abi_version()}, these bindings "
                               f"expect {ABI_VERSION}: rebuild the HIP engine")
@@ -251,6 +255,48 @@ def device_copy(dst_ptr, src_ptr, nbytes):
         rc = _hip.hipMemcpy(int(dst_ptr), int(src_ptr), int(nbytes), 3)  # hipMemcpyDeviceToDevice
         if rc != 0:
             raise EngineError(f"hipMemcpy failed ({rc})")
+
+
+def _fresh_seed():
+    return int.from_bytes(os.urandom(8), "little")
+
+
+def pick_index(picker, starts, ends, prioritize_end=True, draws=None, seed=None, device_id=-1):
+    """trw_pick_index: one pick per (start, end) range with the named index
+    picker; draws (uniforms in [0, 1)) or in-kernel Philox keyed by seed (a
+    fresh one if None).  Returns int32 picks, -1 for an empty range."""
+    s = np.ascontiguousarray(starts, dtype=np.int32).ravel()
+    e = np.ascontiguousarray(ends, dtype=np.int32).ravel()
+    if s.size != e.size:
+        raise ValueError("starts and ends must have the same length")
+    d = None if draws is None else np.ascontiguousarray(draws, dtype=np.float64).ravel()
+    if d is not None and d.size != s.size:
+        raise ValueError("one random number per pick is required")
+    out = np.empty(s.size, dtype=np.int32)
+    _check(lib().trw_pick_index(int(device_id), PICKERS[picker], s.ctypes.data, e.ctypes.data,
+                                s.size, int(bool(prioritize_end)),
+                                None if d is None else d.ctypes.data,
+                                _fresh_seed() if seed is None else int(seed), out.ctypes.data))
+    return out
+
+
+def pick_weights(cumulative, group_starts, group_ends, draws=None, seed=None, device_id=-1):
+    """trw_pick_weights: one weight-based pick per [group_start, group_end)
+    range of one cumulative-weight array; draws as for pick_index."""
+    w = np.ascontiguousarray(cumulative, dtype=np.float64).ravel()
+    gs = np.ascontiguousarray(group_starts, dtype=np.uint64).ravel()
+    ge = np.ascontiguousarray(group_ends, dtype=np.uint64).ravel()
+    if gs.size != ge.size:
+        raise ValueError("group_starts and group_ends must have the same length")
+    d = None if draws is None else np.ascontiguousarray(draws, dtype=np.float64).ravel()
+    if d is not None and d.size != gs.size:
+        raise ValueError("one random number per pick is required")
+    out = np.empty(gs.size, dtype=np.int32)
+    _check(lib().trw_pick_weights(int(device_id), w.ctypes.data if w.size else None, w.size,
+                                  gs.ctypes.data, ge.ctypes.data, gs.size,
+                                  None if d is None else d.ctypes.data,
+                                  _fresh_seed() if seed is None else int(seed), out.ctypes.data))
+    return out
 
 
 def _check(rc):

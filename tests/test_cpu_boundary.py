@@ -53,6 +53,25 @@ def test_python_surface_matches_reference_names():
               "get_node_degrees", "clear", "get_memory_used", "set_node_features",
               "get_node_features", "add_edges_from_networkx", "to_networkx"):
         assert hasattr(cls, m), m
+    # the standalone pickers (py_interface/_temporal_random_walk.cu:904-1016)
+    for name in ("LinearRandomPicker", "ExponentialIndexRandomPicker", "UniformRandomPicker",
+                 "WeightBasedRandomPicker"):
+        picker = getattr(trw, name)(use_gpu=False)
+        assert hasattr(picker, "pick_random") and hasattr(picker, "pick_random_batch"), name
+    doc = trw.LinearRandomPicker.pick_random.__doc__
+    assert "start" in doc and "end" in doc and "prioritize_end" in doc
+    assert "cumulative_weights" in trw.WeightBasedRandomPicker.pick_random.__doc__
+
+
+def test_pickers_fail_loudly_without_gpu():
+    import temporal_random_walk as trw
+
+    if _has_gpu():
+        pytest.skip("a GPU is present")
+    with pytest.raises(RuntimeError, match="only on the GPU"):
+        trw.ExponentialIndexRandomPicker(use_gpu=True).pick_random(0, 10)
+    with pytest.raises(RuntimeError, match="only on the GPU"):
+        trw.WeightBasedRandomPicker().pick_random([0.2, 0.5, 1.0], 0, 3)
 
 
 def _has_gpu():
