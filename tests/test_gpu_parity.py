@@ -298,6 +298,29 @@ def test_replay_walks_million_scale():
     _walk_case(og, eng, "Linear", "Uniform", False, "total", 9, n, seed=83)
 
 
+def test_replay_walks_hub_with_more_groups_than_the_header_holds():
+    """A node with 2^24 + 100 timestamp groups: more than the 24 bits the walk's
+    node header keeps for the group count, so the count comes from the next
+    header.  Walks from it and through it, forward and backward."""
+    rng = np.random.default_rng(91)
+    g = (1 << 24) + 100
+    hub_t = rng.permutation(g).astype(np.int64)
+    hub_d = rng.integers(1, 2_000, g).astype(np.int32)
+    s_o = rng.integers(1, 2_000, 200_000).astype(np.int32)
+    d_o = np.where(rng.random(200_000) < 0.3, 0, rng.integers(1, 2_000, 200_000)).astype(np.int32)
+    t_o = rng.integers(0, g, 200_000).astype(np.int64)
+    s = np.concatenate([np.zeros(g, np.int32), s_o])
+    d = np.concatenate([hub_d, d_o])
+    t = np.concatenate([hub_t, t_o])
+    og, eng = _pair(True, [(s, d, t)])
+    assert int(eng.array("count_ts_group_per_node_outbound")[1]) == g
+    for forward in (True, False):
+        for picker in ("ExponentialIndex", "Uniform"):
+            _walk_case(og, eng, picker, "Uniform", forward, "nodes", 12, 500,
+                       seed_nodes=np.array([0, 5], np.int32), seed=92)
+            _walk_case(og, eng, picker, "Uniform", forward, "total", 12, 3_000, seed=93)
+
+
 # ---- normal mode: the in-kernel Philox stream -----------------------------
 
 GLOBAL_SEED = 1234  # the seed _pair gives the engine
