@@ -83,6 +83,98 @@ def cpu_baseline(src, dst, ts, n_walks, L, threads):
     }
 
 
+def run_other_config(k, args):
+    """One of BASELINE.json's other workloads (configs[k-1]), timed on the
+    device (HIP events of the engine): index build and sampling.  These are
+    parity-test configs; the bench line proper is cfg2."""
+    import torch
+    from temporal_random_walk import capi
+    from tests import configs
+
+    dev = torch.device("cuda:0")
+
+    def resident(*arrs):
+        out = [torch.from_numpy(a).to(dev) for a in arrs]
+        torch.cuda.synchronize()
+        return out
+
+    res = {"config": f"cfg{k}", "unit": "walk steps/s"}
+    log(f"generating cfg{k} inputs")
+    if k in (1, 3, 4):
+        if k == 1:
+            src, dst, ts = configs.cfg1()
+            feats = None
+            eng = capi.Engine(is_directed=True, global_seed=42, shuffle_walk_order=False)
+            call = ("all_nodes", 20, "Uniform", 10, "Uniform", "Forward_In_Time")
+        elif k == 3:
+            src, dst, ts, feats = configs.cfg3()
+            eng = capi.Engine(is_directed=False, global_seed=42, shuffle_walk_order=False)
+            call = ("all_nodes", 40, "Linear", 5, "Linear", "Backward_In_Time")
+        else:
+            src, dst, ts = configs.cfg4()
+            feats = None
+            eng = capi.Engine(is_directed=True, global_seed=42, shuffle_walk_order=False,
+                              enable_weight_computation=True, timescale_bound=50.0)
+            call = ("total", 80, "ExponentialWeight", 20_000_000, "ExponentialWeight",
+                    "Forward_In_Time")
+        arrs = resident(src, dst, ts) + ([] if feats is None else resident(feats))
+        E = len(src)
+        dim = 0 if feats is None else feats.shape[1]
+        builds, samples, kernels = [], [], []
+        for i in range(1 + args.steps):
+            eng.clear()
+            eng.add_edges_device(arrs[0].data_ptr(), arrs[1].data_ptr(), arrs[2].data_ptr(), E,
+                                 arrs[3].data_ptr() if feats is not None else None, dim)
+            tb = eng.timings()["build_ms"]
+            mode, L, bias, n, start, direction = call
+            eng.sample_device(mode, L, bias, n, initial_edge_bias=start, direction=direction,
+                              walk_order=args.walk_order)
+            tm = eng.timings()
+            if i:  # the first round warms up
+                builds.append(tb)
+                samples.append(tm["sample_ms"])
+                kernels.append(tm["walk_kernel_ms"])
+            log(f"round {i}: build {tb:.2f} ms, sample {tm['sample_ms']:.2f} ms, "
+                f"walk kernel {tm['walk_kernel_ms']:.2f} ms")
+        st = eng.walk_stats()
+        res.update(edges=E, walks=int(st["nonempty_walks"]), walk_steps=int(st["total_len"]),
+                   build_ms=sum(builds) / len(builds), sample_ms=sum(samples) / len(samples),
+                   walk_kernel_ms=sum(kernels) / len(kernels))
+        res["index_build_edges_per_s"] = E / (res["build_ms"] * 1e-3)
+        res["value"] = st["total_len"] / (res["sample_ms"] * 1e-3)
+        eng.close()
+    elif k == 5:
+        eng = capi.Engine(is_directed=True, global_seed=42, shuffle_walk_order=False,
+                          max_time_capacity=3_000_000, enable_temporal_node2vec=True,
+                          node2vec_p=0.5, node2vec_q=2.0)
+        builds, samples, kernels, steps, edges = [], [], [], 0, 0
+        for b, (src, dst, ts) in enumerate(configs.cfg5_batches()):
+            arrs = resident(src, dst, ts)
+            eng.add_edges_device(arrs[0].data_ptr(), arrs[1].data_ptr(), arrs[2].data_ptr(),
+                                 len(src))
+            tb = eng.timings()["build_ms"]
+            eng.sample_device("total", 40, "TemporalNode2Vec", 5_000_000,
+                              initial_edge_bias="Uniform", direction="Forward_In_Time",
+                              walk_order=args.walk_order)
+            tm = eng.timings()
+            builds.append(tb)
+            samples.append(tm["sample_ms"])
+            kernels.append(tm["walk_kernel_ms"])
+            steps += int(eng.walk_stats()["total_len"])
+            edges += len(src)
+            log(f"batch {b}: store {eng.edge_count()} edges, build {tb:.2f} ms, sample "
+                f"{tm['sample_ms']:.2f} ms, walk kernel {tm['walk_kernel_ms']:.2f} ms")
+        res.update(batches=len(builds), batch_edges=edges // len(builds),
+                   build_ms=sum(builds) / len(builds), sample_ms=sum(samples) / len(samples),
+                   walk_kernel_ms=sum(kernels) / len(kernels))
+        res["index_build_edges_per_s"] = edges / (sum(builds) * 1e-3)
+        res["value"] = steps / (sum(samples) * 1e-3)
+        eng.close()
+    else:
+        raise SystemExit("--config takes 1, 3, 4 or 5 (2 is the default bench line)")
+    print(json.dumps(res))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -95,6 +187,9 @@ def main():
     ap.add_argument("--walk-len", type=int, default=80)
     ap.add_argument("--walk-order", default="auto", choices=["auto", "walk_id", "start_time"],
                     help="order the walks run in on the device (the output is the same)")
+    ap.add_argument("--config", type=int, default=2,
+                    help="2 (default): the cfg2 bench line; 1, 3, 4 or 5: time that BASELINE "
+                         "workload instead (device timings, one JSON line)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-walks", type=int, default=2_500_000,
                     help="walks of the bounded CPU-baseline sample (about 10 s on 16 threads)")
@@ -113,6 +208,10 @@ def main():
         print(json.dumps({"error": "this build measures one GPU only (no multi-GPU path); "
                                    "run with --gpus 1"}))
         sys.exit(2)
+
+    if args.config != 2:
+        run_other_config(args.config, args)
+        return
 
     import numpy as np
     import torch

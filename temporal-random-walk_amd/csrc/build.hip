@@ -447,7 +447,7 @@ __device__ __forceinline__ void raw_node_weights(const NodeWeightParams& q, cons
 // Nodes with at most kHeavyGroups groups: one thread per node; the normalised
 // weights are accumulated sequentially in group order, exactly as the
 // reference does (node_edge_index.cu:617-639).
-constexpr uint32_t kHeavyGroups = 4096;
+constexpr uint32_t kHeavyGroups = 512;
 
 __global__ void node_weights_light_kernel(const uint32_t* __restrict__ cnt,
                                           const uint32_t* __restrict__ grp,
@@ -487,26 +487,20 @@ __global__ void heavy_node_flags_kernel(const uint32_t* __restrict__ cnt, size_t
     if (u < nodes) flags[u] = (cnt[u + 1] - cnt[u] > kHeavyGroups) ? 1u : 0u;
 }
 
-__global__ void compact_nodes_kernel(const uint32_t* __restrict__ flags,
-                                     const uint32_t* __restrict__ scan, size_t nodes,
-                                     uint32_t* __restrict__ out) {
+// Heavy nodes are cut into tiles of kHeavyTile groups (256 threads x 16); the
+// i-th heavy node (in id order) owns tiles [tile_base[i], tile_base[i + 1]).
+constexpr int kHeavyItems = 16;
+constexpr uint32_t kHeavyTile = 256 * kHeavyItems;
+
+__global__ void compact_heavy_kernel(const uint32_t* __restrict__ flags,
+                                     const uint32_t* __restrict__ scan,
+                                     const uint32_t* __restrict__ cnt, size_t nodes,
+                                     uint32_t* __restrict__ heavy, uint32_t* __restrict__ tiles) {
     const size_t u = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
-    if (u < nodes && flags[u]) out[scan[u]] = static_cast<uint32_t>(u);
-}
-
-__device__ __forceinline__ double wave_sum_f64(double x) {
-    for (int off = 32; off > 0; off >>= 1) x += __shfl_down(x, off, 64);
-    return x;
-}
-
-// Block-wide (256 threads) sum; every thread receives the total.
-__device__ double block_sum_f64(double x, double* s4) {
-    x = wave_sum_f64(x);
-    if ((threadIdx.x & 63) == 0) s4[threadIdx.x >> 6] = x;
-    __syncthreads();
-    const double t = s4[0] + s4[1] + s4[2] + s4[3];
-    __syncthreads();
-    return t;
+    if (u < nodes && flags[u]) {
+        heavy[scan[u]] = static_cast<uint32_t>(u);
+        tiles[scan[u]] = (cnt[u + 1] - cnt[u] + kHeavyTile - 1) / kHeavyTile;
+    }
 }
 
 // Exclusive block scan (sum or max) of one value per thread.
@@ -533,69 +527,112 @@ __device__ double block_excl_scan_f64(double v, double* s4, double* total) {
     return before + (lane == 0 ? 0.0 : excl_in_wave);
 }
 
-// Nodes with more than kHeavyGroups groups (hubs): one workgroup per node.
-// Pass 1 writes raw weights and block-reduces the node's sums; pass 2 scans
-// the normalised weights in chunks of 256 x 16 with a running carry and then
-// takes a running maximum, so the cumulative array is non-decreasing by
-// construction (the picker's end_sum < start_sum guard, random/pickers.cuh:
-// 109-111, must never fire on a rounding artefact).  Values agree with the
-// sequential reference sum to a few ulps.
-constexpr int kHeavyItems = 16;
+// The heavy node and the tile's first group of tile t (-1: past the last tile).
+__device__ __forceinline__ int heavy_tile_node(const uint32_t* tile_base, uint32_t nh, uint32_t t) {
+    if (t >= tile_base[nh]) return -1;
+    uint32_t lo = 0, hi = nh;  // last i with tile_base[i] <= t
+    while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (tile_base[mid] <= t) lo = mid;
+        else hi = mid;
+    }
+    return static_cast<int>(lo);
+}
 
-__global__ __launch_bounds__(256) void node_weights_heavy_kernel(
-    const uint32_t* __restrict__ heavy, const uint32_t* __restrict__ cnt,
-    const uint32_t* __restrict__ grp, const int64_t* __restrict__ first_ts, double bound,
-    int compute_forward, double* __restrict__ wf, double* __restrict__ wb) {
+// Pass 1 of a heavy node's weights, one workgroup per tile: the raw weights
+// of the tile's groups and their running sum within the tile -- per-thread
+// sequential sums of 16, a block scan, then a block running maximum so the
+// tile's values are non-decreasing -- written in place; the tile's last
+// value goes to tsum.  Both directions (f is skipped when wf is null).
+__global__ __launch_bounds__(256) void heavy_tile_scan_kernel(
+    const uint32_t* __restrict__ heavy, const uint32_t* __restrict__ tile_base, uint32_t nh,
+    const uint32_t* __restrict__ cnt, const uint32_t* __restrict__ grp,
+    const int64_t* __restrict__ first_ts, double bound, double* __restrict__ wf,
+    double* __restrict__ wb, double* __restrict__ tsum_f, double* __restrict__ tsum_b) {
     __shared__ double s4[4];
-    const uint32_t u = heavy[blockIdx.x];
+    const int i = heavy_tile_node(tile_base, nh, blockIdx.x);
+    if (i < 0) return;  // uniform over the workgroup
+    const uint32_t u = heavy[i];
     const uint32_t s = cnt[u], e = cnt[u + 1];
     const NodeWeightParams q = node_weight_params(first_ts, s, e, bound);
-    double fs = 0.0, bs = 0.0;
-    for (uint32_t p = s + threadIdx.x; p < e; p += 256) {
-        double f, b;
-        raw_node_weights(q, grp, first_ts, p, bound, &f, &b);
-        wb[p] = b;
-        bs += b;
-        if (compute_forward) {
-            wf[p] = f;
-            fs += f;
-        }
+    const uint32_t t0 = s + (blockIdx.x - tile_base[i]) * kHeavyTile;
+    const uint32_t p0 = t0 + threadIdx.x * kHeavyItems;
+    double vf[kHeavyItems], vb[kHeavyItems];
+    double rf = 0.0, rb = 0.0;
+#pragma unroll
+    for (int j = 0; j < kHeavyItems; ++j) {
+        const uint32_t p = p0 + j;
+        double f = 0.0, b = 0.0;
+        if (p < e) raw_node_weights(q, grp, first_ts, p, bound, &f, &b);
+        rf += f;
+        rb += b;
+        vf[j] = rf;
+        vb[j] = rb;
     }
-    const double bsum = block_sum_f64(bs, s4);
-    const double fsum = compute_forward ? block_sum_f64(fs, s4) : 1.0;
-    for (int dir = 0; dir < (compute_forward ? 2 : 1); ++dir) {
+    for (int dir = 0; dir < (wf ? 2 : 1); ++dir) {
+        double* v = dir == 0 ? vb : vf;
         double* w = dir == 0 ? wb : wf;
-        const double sum = dir == 0 ? bsum : fsum;
-        double carry = 0.0;
-        for (uint32_t base = s; base < e; base += 256 * kHeavyItems) {
-            const uint32_t p0 = base + threadIdx.x * kHeavyItems;
-            double v[kHeavyItems];
-            double run = 0.0;
+        double tot;
+        const double before = block_excl_scan_f64<false>(dir == 0 ? rb : rf, s4, &tot);
+        double mx = 0.0;
 #pragma unroll
-            for (int j = 0; j < kHeavyItems; ++j) {
-                const uint32_t p = p0 + j;
-                run += p < e ? w[p] / sum : 0.0;
-                v[j] = run;
-            }
-            double tot;
-            const double before = block_excl_scan_f64<false>(run, s4, &tot);
-            double mx = 0.0;
-#pragma unroll
-            for (int j = 0; j < kHeavyItems; ++j) {
-                v[j] = carry + (before + v[j]);
-                mx = fmax(mx, v[j]);
-            }
-            double mtot;
-            const double mbefore = block_excl_scan_f64<true>(mx, s4, &mtot);
-            double m = fmax(mbefore, carry);
-#pragma unroll
-            for (int j = 0; j < kHeavyItems; ++j) {
-                const uint32_t p = p0 + j;
-                m = fmax(m, v[j]);
-                if (p < e) w[p] = m;
-            }
-            carry = fmax(mtot, carry);
+        for (int j = 0; j < kHeavyItems; ++j) {
+            v[j] = before + v[j];
+            mx = fmax(mx, v[j]);
         }
+        double mtot;
+        double m = block_excl_scan_f64<true>(mx, s4, &mtot);
+        m = fmax(m, 0.0);
+#pragma unroll
+        for (int j = 0; j < kHeavyItems; ++j) {
+            const uint32_t p = p0 + j;
+            m = fmax(m, v[j]);
+            if (p < e) w[p] = m;
+        }
+        if (threadIdx.x == 0) (dir == 0 ? tsum_b : tsum_f)[blockIdx.x] = mtot;
+    }
+}
+
+// Pass 2, one thread per heavy node: its tiles' exclusive prefixes, each the
+// previous prefix plus the previous tile's last value, so consecutive tiles
+// stay non-decreasing across their boundary; the node's total follows.
+__global__ void heavy_tile_prefix_kernel(const uint32_t* __restrict__ tile_base, uint32_t nh,
+                                         double* __restrict__ tsum_f, double* __restrict__ tsum_b,
+                                         double* __restrict__ total_f,
+                                         double* __restrict__ total_b, int compute_forward) {
+    const uint32_t i = blockIdx.x * kB + threadIdx.x;
+    if (i >= nh) return;
+    for (int dir = 0; dir < (compute_forward ? 2 : 1); ++dir) {
+        double* ts = dir == 0 ? tsum_b : tsum_f;
+        double run = 0.0;
+        for (uint32_t t = tile_base[i]; t < tile_base[i + 1]; ++t) {
+            const double x = ts[t];
+            ts[t] = run;
+            run = run + x;
+        }
+        (dir == 0 ? total_b : total_f)[i] = run;
+    }
+}
+
+// Pass 3, one workgroup per tile: cumulative = (tile prefix + running sum) /
+// node total, the normalisation of node_edge_index.cu:617-639 applied to the
+// prefix sums (non-decreasing, the node's last value exactly 1).
+__global__ __launch_bounds__(256) void heavy_tile_finish_kernel(
+    const uint32_t* __restrict__ heavy, const uint32_t* __restrict__ tile_base, uint32_t nh,
+    const uint32_t* __restrict__ cnt, const double* __restrict__ tsum_f,
+    const double* __restrict__ tsum_b, const double* __restrict__ total_f,
+    const double* __restrict__ total_b, double* __restrict__ wf, double* __restrict__ wb) {
+    const int i = heavy_tile_node(tile_base, nh, blockIdx.x);
+    if (i < 0) return;
+    const uint32_t u = heavy[i];
+    const uint32_t s = cnt[u], e = cnt[u + 1];
+    const uint32_t t0 = s + (blockIdx.x - tile_base[i]) * kHeavyTile;
+    for (int dir = 0; dir < (wf ? 2 : 1); ++dir) {
+        double* w = dir == 0 ? wb : wf;
+        const double pre = (dir == 0 ? tsum_b : tsum_f)[blockIdx.x];
+        const double tot = (dir == 0 ? total_b : total_f)[i];
+        for (uint32_t p = t0 + threadIdx.x; p < e && p < t0 + kHeavyTile; p += 256)
+            w[p] = (pre + w[p]) / tot;
     }
 }
 
@@ -691,7 +728,7 @@ void node_weights(Engine& e, DirIndex& dir, size_t v, double bound, bool compute
     hipLaunchKernelGGL(node_weights_light_kernel, dim3(grid_for(v)), dim3(kB), 0, s, dir.cnt.p,
                        dir.grp.p, dir.first_ts.p, v, bound, compute_forward ? 1 : 0, wf,
                        dir.w_bwd.p);
-    // hubs: list them on the device, then one workgroup each
+    // heavier nodes: list them on the device, then tiles of kHeavyTile groups
     e.flags.ensure(v + 1);
     e.scan.ensure(v + 1);
     e.scan_scratch.ensure(scan_scratch_elems(v + 1));
@@ -703,12 +740,29 @@ void node_weights(Engine& e, DirIndex& dir, size_t v, double bound, bool compute
     uint32_t nh;
     std::memcpy(&nh, host_scratch, 4);
     if (nh) {
+        // heavy ids in k32b, their tile counts then tile bases in v32b
         e.k32b.ensure(nh);
-        hipLaunchKernelGGL(compact_nodes_kernel, dim3(grid_for(v)), dim3(kB), 0, s, e.flags.p,
-                           e.scan.p, v, e.k32b.p);
-        hipLaunchKernelGGL(node_weights_heavy_kernel, dim3(nh), dim3(256), 0, s, e.k32b.p,
-                           dir.cnt.p, dir.grp.p, dir.first_ts.p, bound, compute_forward ? 1 : 0,
-                           wf, dir.w_bwd.p);
+        e.v32b.ensure(nh + 1);
+        e.v32a.ensure(nh + 1);
+        hipLaunchKernelGGL(compact_heavy_kernel, dim3(grid_for(v)), dim3(kB), 0, s, e.flags.p,
+                           e.scan.p, dir.cnt.p, v, e.k32b.p, e.v32a.p);
+        e.scan_scratch.ensure(scan_scratch_elems(nh + 1));
+        exclusive_scan_u32(e.v32a.p, e.v32b.p, nh, e.scan_scratch.p, s);
+        // at most g / kHeavyTile + nh tiles: launch that many, the rest exit
+        const size_t tiles = dir.n_groups / kHeavyTile + nh + 1;
+        e.dscratch.ensure(4 * tiles + 2 * nh);
+        double* tsum_f = e.dscratch.p;
+        double* tsum_b = tsum_f + tiles;
+        double* total_f = tsum_b + tiles;
+        double* total_b = total_f + nh;
+        hipLaunchKernelGGL(heavy_tile_scan_kernel, dim3(tiles), dim3(256), 0, s, e.k32b.p,
+                           e.v32b.p, nh, dir.cnt.p, dir.grp.p, dir.first_ts.p, bound, wf,
+                           dir.w_bwd.p, tsum_f, tsum_b);
+        hipLaunchKernelGGL(heavy_tile_prefix_kernel, dim3(grid_for(nh)), dim3(kB), 0, s, e.v32b.p,
+                           nh, tsum_f, tsum_b, total_f, total_b, compute_forward ? 1 : 0);
+        hipLaunchKernelGGL(heavy_tile_finish_kernel, dim3(tiles), dim3(256), 0, s, e.k32b.p,
+                           e.v32b.p, nh, dir.cnt.p, tsum_f, tsum_b, total_f, total_b, wf,
+                           dir.w_bwd.p);
     }
     check_hip(hipGetLastError(), "node weights launch");
 }

@@ -63,6 +63,8 @@ struct DirView {
 // so fewer registers and more waves in flight -- or any picker.
 constexpr int kFamIndex = 0;
 constexpr int kFamAny = 1;
+// Index pickers and ExponentialWeight: no node2vec rejection loop.
+constexpr int kFamWeight = 2;
 
 struct WalkGraph {
     const int32_t* src;
@@ -383,7 +385,7 @@ __device__ Hop node_edge_at(const WalkGraph& g, int picker, int node, int32_t t,
     } else {
         const double* lv =
             (g.d.wx && G > static_cast<int>(kWIdxMin)) ? g.d.wx + g.d.wx_off[node] : nullptr;
-        if (picker == kTemporalNode2Vec && prev != -1)
+        if (Fam != kFamWeight && picker == kTemporalNode2Vec && prev != -1)
             return tn2v_pick(g, prev, gb + vb, gb + ve, gb, ge, lv, rg, re);
         // ExponentialWeight, or node2vec's first hop (no previous node)
         if (picker != kExponentialWeight && picker != kTemporalNode2Vec) return no_hop();
@@ -1110,10 +1112,13 @@ void Engine::sample(const trw_sample_params& p) {
         g.active_size = 0;
     }
     const bool index_only = is_index_picker(walk_bias) && is_index_picker(start_bias);
+    const bool no_node2vec = walk_bias != kTemporalNode2Vec;  // start_bias never is (above)
 #define TRW_LAUNCH_FAMILY(K, F, D, G, ...)                                                     \
     do {                                                                                       \
         if (index_only)                                                                        \
             hipLaunchKernelGGL((K<F, D, kFamIndex>), G, dim3(kB), 0, s, __VA_ARGS__);           \
+        else if (no_node2vec)                                                                  \
+            hipLaunchKernelGGL((K<F, D, kFamWeight>), G, dim3(kB), 0, s, __VA_ARGS__);          \
         else                                                                                   \
             hipLaunchKernelGGL((K<F, D, kFamAny>), G, dim3(kB), 0, s, __VA_ARGS__);             \
     } while (0)
