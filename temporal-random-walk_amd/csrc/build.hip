@@ -113,6 +113,29 @@ __global__ void gather_feat_kernel(const uint32_t* __restrict__ perm, size_t del
     }
 }
 
+// Same, 16 bytes per work-item for rows of dim % 4 == 0 floats in 16-byte
+// aligned arrays: a workgroup of V * R threads (V = dim / 4 vectors per row,
+// R = 256 / V rows) covers R consecutive rows, grid-stride over rows.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void gather_feat_vec_kernel(
+    const uint32_t* __restrict__ perm, size_t del, size_t kept, uint32_t V,
+    const f32x4* __restrict__ of, size_t e_old, const f32x4* __restrict__ nf,
+    f32x4* __restrict__ f) {
+    const uint32_t R = blockDim.x / V;
+    const uint32_t c = threadIdx.x % V, r = threadIdx.x / V;
+    if (r >= R) return;
+    for (size_t j = blockIdx.x * static_cast<size_t>(R) + r; j < kept;
+         j += static_cast<size_t>(gridDim.x) * R) {
+        const uint32_t id = perm[del + j];
+        const f32x4 v = id < e_old ? of[static_cast<size_t>(id) * V + c]
+                                   : nf[(static_cast<size_t>(id) - e_old) * V + c];
+        f[j * V + c] = v;
+    }
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 inline unsigned grid_capped(size_t n) {
     const size_t g = (n + kB - 1) / kB;
     return static_cast<unsigned>(g == 0 ? 1 : (g > (1u << 20) ? (1u << 20) : g));
@@ -209,13 +232,15 @@ __global__ __launch_bounds__(kB) void node_group_flags_kernel(const uint32_t* __
                                                               const uint32_t* __restrict__ erank,
                                                               size_t n,
                                                               uint32_t* __restrict__ flags,
-                                                              uint32_t* __restrict__ idx) {
+                                                              uint32_t* __restrict__ idx,
+                                                              uint32_t* __restrict__ rank) {
     const size_t k = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
     if (k >= n) return;  // the active lanes of a wave are a prefix
     const uint32_t key = keys[k];
     const uint32_t e = rec[k].eid;
     const uint32_t r = erank[e];
     idx[k] = e;
+    rank[k] = r;
     uint32_t kp = __shfl_up(key, 1, 64), rp = __shfl_up(r, 1, 64);
     if ((threadIdx.x & 63) == 0 && k > 0) {
         kp = keys[k - 1];
@@ -224,10 +249,12 @@ __global__ __launch_bounds__(kB) void node_group_flags_kernel(const uint32_t* __
     flags[k] = (k == 0 || key != kp || r != rp) ? 1u : 0u;
 }
 
+// Group starts, panel records and (for the weights, when first_ts is given)
+// each group's timestamp, from the flags, their scan and the entries' ranks
+// (all read in entry order).
 __global__ void node_group_scatter_kernel(const uint32_t* __restrict__ flags,
                                           const uint32_t* __restrict__ scan,
-                                          const uint32_t* __restrict__ idx,
-                                          const uint32_t* __restrict__ erank,
+                                          const uint32_t* __restrict__ rank,
                                           const int64_t* __restrict__ uniq_ts, size_t n,
                                           uint32_t* __restrict__ grp,
                                           int64_t* __restrict__ first_ts,
@@ -236,9 +263,9 @@ __global__ void node_group_scatter_kernel(const uint32_t* __restrict__ flags,
     if (k >= n) return;
     if (flags[k]) {
         const uint32_t g = scan[k];
-        const uint32_t r = erank[idx[k]];
+        const uint32_t r = rank[k];
         grp[g] = static_cast<uint32_t>(k);
-        first_ts[g] = uniq_ts[r];
+        if (first_ts) first_ts[g] = uniq_ts[r];
         pan[g] = PanelRec{r, static_cast<uint32_t>(k)};
     }
     if (k == n - 1) {
@@ -687,8 +714,9 @@ void build_direction(Engine& e, DirIndex& dir, size_t n, int key_bits, size_t vc
     dir.off.resize(vc);
     hipLaunchKernelGGL(lower_bound_offsets_kernel, dim3(grid_for(vc)), dim3(kB), 0, s, dir.key.p,
                        n, vc, dir.off.p);
+    e.v32a.ensure(n);  // the entries' timestamp ranks
     hipLaunchKernelGGL(node_group_flags_kernel, dim3(grid_for(n)), dim3(kB), 0, s, dir.key.p,
-                       dir.rec.p, e.erank.p, n, e.flags.p, dir.idx.p);
+                       dir.rec.p, e.erank.p, n, e.flags.p, dir.idx.p, e.v32a.p);
     exclusive_scan_u32(e.flags.p, e.scan.p, n, e.scan_scratch.p, s);
     uint32_t g = 0;
     check_hip(hipMemcpyAsync(host_scratch, e.scan.p + n, 4, hipMemcpyDeviceToHost, s), "read g");
@@ -696,12 +724,14 @@ void build_direction(Engine& e, DirIndex& dir, size_t n, int key_bits, size_t vc
     std::memcpy(&g, host_scratch, 4);
     dir.n_groups = g;
     dir.grp.resize(static_cast<size_t>(g) + 1);
-    dir.first_ts.resize(g);
+    // group timestamps feed only the per-node weights
+    const bool weights = e.cfg.enable_weight_computation || e.cfg.enable_temporal_node2vec;
+    dir.first_ts.resize(weights ? g : 0);
     dir.pan.resize(static_cast<size_t>(g) + 1);
     if (n) {
         hipLaunchKernelGGL(node_group_scatter_kernel, dim3(grid_for(n)), dim3(kB), 0, s,
-                           e.flags.p, e.scan.p, dir.idx.p, e.erank.p, e.uniq_ts.p, n, dir.grp.p,
-                           dir.first_ts.p, dir.pan.p);
+                           e.flags.p, e.scan.p, e.v32a.p, e.uniq_ts.p, n, dir.grp.p,
+                           weights ? dir.first_ts.p : nullptr, dir.pan.p);
     } else {
         check_hip(hipMemsetAsync(dir.grp.p, 0, 4, s), "grp terminator");
         check_hip(hipMemsetAsync(dir.pan.p, 0, sizeof(PanelRec), s), "panel terminator");
@@ -901,8 +931,18 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
     }
     if (feat_dim > 0) {
         feat2.resize(kept * feat_dim);
-        hipLaunchKernelGGL(gather_feat_kernel, dim3(grid_capped(kept * feat_dim)), dim3(kB), 0, s,
-                           perm, del, kept, feat_dim, feat.p, e_old, d_feat, feat2.p);
+        const uint32_t V = static_cast<uint32_t>(feat_dim / 4);
+        if (feat_dim % 4 == 0 && V <= 256 && aligned16(d_feat)) {
+            const uint32_t R = 256 / V;
+            const size_t blocks = std::min<size_t>((kept + R - 1) / R, 65536);
+            hipLaunchKernelGGL(gather_feat_vec_kernel, dim3(blocks ? blocks : 1), dim3(V * R), 0, s,
+                               perm, del, kept, V, reinterpret_cast<const f32x4*>(feat.p), e_old,
+                               reinterpret_cast<const f32x4*>(d_feat),
+                               reinterpret_cast<f32x4*>(feat2.p));
+        } else {
+            hipLaunchKernelGGL(gather_feat_kernel, dim3(grid_capped(kept * feat_dim)), dim3(kB), 0,
+                               s, perm, del, kept, feat_dim, feat.p, e_old, d_feat, feat2.p);
+        }
         feat.swap(feat2);
     }
     src.swap(src2);

@@ -773,6 +773,27 @@ __global__ void gather_walk_features_kernel(const int64_t* __restrict__ eids, ui
     }
 }
 
+// Same, 16 bytes per work-item for rows of dim % 4 == 0 floats: a workgroup of
+// V * R threads (V = dim / 4 vectors per row, R = 256 / V rows) covers R
+// consecutive slots, grid-stride over slots; the output is written once, with
+// non-temporal stores.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void gather_walk_features_vec_kernel(
+    const int64_t* __restrict__ eids, uint64_t slots, uint32_t V, const f32x4* __restrict__ feat,
+    f32x4* __restrict__ out) {
+    const uint32_t R = blockDim.x / V;
+    const uint32_t c = threadIdx.x % V, r = threadIdx.x / V;
+    if (r >= R) return;
+    for (uint64_t slot = blockIdx.x * static_cast<uint64_t>(R) + r; slot < slots;
+         slot += static_cast<uint64_t>(gridDim.x) * R) {
+        const int64_t e = eids[slot];
+        const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+        const f32x4 v = e >= 0 ? feat[static_cast<uint64_t>(e) * V + c] : zero;
+        __builtin_nontemporal_store(v, out + slot * V + c);
+    }
+}
+
 // Blocks for a grid-stride launch over n items (at most 2^20 blocks).
 inline unsigned grid_capped(uint64_t n) {
     const uint64_t g = (n + kB - 1) / kB;
@@ -1203,9 +1224,18 @@ void Engine::sample(const trw_sample_params& p) {
     // ---- edge features of every walk slot (finalize_host_walks, on device)
     if (feat_dim > 0 && eslots) {
         w_feat.resize(eslots * feat_dim);
-        hipLaunchKernelGGL(gather_walk_features_kernel, dim3(grid_capped(eslots * feat_dim)), dim3(kB),
-                           0, s, w_eids.p, eslots, static_cast<uint32_t>(feat_dim), feat.p,
-                           w_feat.p);
+        const uint32_t V = static_cast<uint32_t>(feat_dim / 4);
+        if (feat_dim % 4 == 0 && V <= 256) {  // device buffers: 256-byte aligned
+            const uint32_t R = 256 / V;
+            const uint64_t blocks = std::min<uint64_t>((eslots + R - 1) / R, 65536);
+            hipLaunchKernelGGL(gather_walk_features_vec_kernel, dim3(blocks), dim3(V * R), 0, s,
+                               w_eids.p, eslots, V, reinterpret_cast<const f32x4*>(feat.p),
+                               reinterpret_cast<f32x4*>(w_feat.p));
+        } else {
+            hipLaunchKernelGGL(gather_walk_features_kernel, dim3(grid_capped(eslots * feat_dim)),
+                               dim3(kB), 0, s, w_eids.p, eslots, static_cast<uint32_t>(feat_dim),
+                               feat.p, w_feat.p);
+        }
         check_hip(hipGetLastError(), "feature gather launch");
     } else {
         w_feat.n = 0;
