@@ -704,8 +704,7 @@ void build_direction(Engine& e, DirIndex& dir, size_t n, int key_bits, size_t vc
     if (edges)
         hipLaunchKernelGGL(node_entries_kernel, dim3(grid_for(edges)), dim3(kB), 0, s, e.src.p,
                            e.dst.p, edges, mode, e.k32a.p, v0);
-    const int which = radix_sort_u32_v64(e.k32a.p, v0, e.k32b.p, v1, n, 0, key_bits, e.hist.p,
-                                         e.hist_scratch.p, s);
+    const int which = radix_sort_u32_v64(e.k32a.p, v0, e.k32b.p, v1, n, 0, key_bits, e.hist.p, s);
     // the sorted keys become the direction's (the scratch takes the old
     // buffer, which every user sizes again before writing)
     dir.key.swap(which ? e.k32b : e.k32a);
@@ -877,21 +876,18 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
     v32a.ensure(std::max(etot, 2 * etot));
     v32b.ensure(std::max(etot, 2 * etot));
     hist.ensure(radix_hist_elems(2 * etot));
-    hist_scratch.ensure(scan_scratch_elems(radix_hist_elems(2 * etot)));
     uint32_t* k32s[2] = {reinterpret_cast<uint32_t*>(k64a.p), reinterpret_cast<uint32_t*>(k64b.p)};
     int which;
     if (keys32) {
         hipLaunchKernelGGL((make_ts_keys_kernel<uint32_t>), dim3(grid_for(etot)), dim3(kB), 0, s,
                            ts.p, src.p, dst.p, e_old, d_ts, d_src, d_dst, n, tmin, k32s[0],
                            v32a.p, ends64.p);
-        which = radix_sort_u32(k32s[0], v32a.p, k32s[1], v32b.p, etot, 0, bits, hist.p,
-                               hist_scratch.p, s);
+        which = radix_sort_u32(k32s[0], v32a.p, k32s[1], v32b.p, etot, 0, bits, hist.p, s);
     } else {
         hipLaunchKernelGGL((make_ts_keys_kernel<uint64_t>), dim3(grid_for(etot)), dim3(kB), 0, s,
                            ts.p, src.p, dst.p, e_old, d_ts, d_src, d_dst, n, tmin, k64a.p,
                            v32a.p, ends64.p);
-        which = radix_sort_u64(k64a.p, v32a.p, k64b.p, v32b.p, etot, 0, bits, hist.p,
-                               hist_scratch.p, s);
+        which = radix_sort_u64(k64a.p, v32a.p, k64b.p, v32b.p, etot, 0, bits, hist.p, s);
     }
     uint32_t* perm = which ? v32b.p : v32a.p;
 
@@ -1002,8 +998,7 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
         k64b.ensure(m2);
         hipLaunchKernelGGL(adj_keys_kernel, dim3(grid_for(E)), dim3(kB), 0, s, src.p, dst.p, E, b,
                            k64a.p);
-        const int w = radix_sort_u64(k64a.p, nullptr, k64b.p, nullptr, m2, 0, 2 * b, hist.p,
-                                     hist_scratch.p, s);
+        const int w = radix_sort_u64(k64a.p, nullptr, k64b.p, nullptr, m2, 0, 2 * b, hist.p, s);
         uint64_t* ak = w ? k64b.p : k64a.p;
         adj_nbr.resize(m2);
         hipLaunchKernelGGL(adj_finish_kernel, dim3(grid_for(m2)), dim3(kB), 0, s, ak, m2,

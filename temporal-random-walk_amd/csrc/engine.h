@@ -270,7 +270,7 @@ struct Engine {
     DBuf<uint64_t> k64a, k64b;
     DBuf<uint64_t> ends64;  // packed (src, dst) of the timestamp sort's input
     DBuf<uint32_t> k32a, k32b, v32a, v32b;
-    DBuf<uint32_t> hist, hist_scratch, flags, scan, scan_scratch;
+    DBuf<uint32_t> hist, flags, scan, scan_scratch;
     DBuf<uint64_t> scan64_scratch;
     DBuf<double> dscratch, fscan_scratch;
     DBuf<int64_t> red64;    // reduction results + partials

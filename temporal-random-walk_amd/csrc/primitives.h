@@ -1,8 +1,9 @@
 // primitives.h -- device-wide scan and stable radix sort for the index build.
 //
 // Hand-written for CDNA4 (wave64): no rocPRIM / hipCUB.  The radix sort is a
-// classic LSD sort with three launches per 8-bit digit pass (tile histogram,
-// digit-major scan of the histograms, stable scatter).  Stable ranking inside
+// classic LSD sort with three launches per 8-bit digit pass (tile histograms
+// plus digit totals, one workgroup per digit scanning its histogram row,
+// stable scatter).  Stable ranking inside
 // a tile uses wave-level multisplit: eight 64-lane ballots give every lane the
 // mask of lanes holding the same digit, so the in-row rank is a popcount and a
 // single leader lane per digit bumps the wave's LDS counter.  Waves own
@@ -41,19 +42,15 @@ void running_max_f64(double* data, size_t n, double* scratch, hipStream_t s);
 // Stable sort of (key, value) pairs by key bits [begin_bit, end_bit).  Values
 // may be null (keys only).  Buffers are ping-ponged; the function returns 0 if
 // the sorted result ended in (keys0, vals0) and 1 if in (keys1, vals1).
-// `hist` must hold radix_hist_elems(n) uint32 and `hist_scratch`
-// scan_scratch_elems(radix_hist_elems(n)) uint32.
+// `hist` must hold radix_hist_elems(n) uint32.
 size_t radix_hist_elems(size_t n);
 int radix_sort_u64(uint64_t* keys0, uint32_t* vals0, uint64_t* keys1, uint32_t* vals1, size_t n,
-                   int begin_bit, int end_bit, uint32_t* hist, uint32_t* hist_scratch,
-                   hipStream_t s);
+                   int begin_bit, int end_bit, uint32_t* hist, hipStream_t s);
 int radix_sort_u32(uint32_t* keys0, uint32_t* vals0, uint32_t* keys1, uint32_t* vals1, size_t n,
-                   int begin_bit, int end_bit, uint32_t* hist, uint32_t* hist_scratch,
-                   hipStream_t s);
+                   int begin_bit, int end_bit, uint32_t* hist, hipStream_t s);
 // 32-bit keys with 64-bit values (a record carried through the sort).
 int radix_sort_u32_v64(uint32_t* keys0, uint64_t* vals0, uint32_t* keys1, uint64_t* vals1,
-                       size_t n, int begin_bit, int end_bit, uint32_t* hist,
-                       uint32_t* hist_scratch, hipStream_t s);
+                       size_t n, int begin_bit, int end_bit, uint32_t* hist, hipStream_t s);
 // Digit passes of a sort of bits [begin_bit, end_bit): the result lands in
 // buffer set (passes % 2) when n > 1.
 int radix_passes(int begin_bit, int end_bit);

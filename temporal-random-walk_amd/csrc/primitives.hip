@@ -199,7 +199,8 @@ template <typename K>
 __global__ __launch_bounds__(kBlock) void radix_upsweep_kernel(const K* __restrict__ keys,
                                                                size_t n, int bit,
                                                                uint32_t* __restrict__ hist,
-                                                               size_t nb) {
+                                                               size_t nb,
+                                                               uint32_t* __restrict__ digit_tot) {
     __shared__ uint32_t s_cnt[kWaves][kRadix];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     for (int i = threadIdx.x; i < kWaves * kRadix; i += kBlock) (&s_cnt[0][0])[i] = 0;
@@ -229,6 +230,47 @@ __global__ __launch_bounds__(kBlock) void radix_upsweep_kernel(const K* __restri
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) tot += s_cnt[w][d];
     hist[static_cast<size_t>(d) * nb + blockIdx.x] = tot;
+    if (tot) atomicAdd(digit_tot + d, tot);
+}
+
+// One workgroup per digit d: the exclusive scan of the workgroups' counts of
+// digit d (hist[d * nb + b], in place), offset by the number of keys with a
+// smaller digit -- the scatter positions of every (workgroup, digit).
+__global__ __launch_bounds__(kBlock) void radix_offsets_kernel(uint32_t* __restrict__ hist,
+                                                               size_t nb,
+                                                               const uint32_t* __restrict__ digit_tot) {
+    __shared__ uint32_t s_wave[kWaves];
+    const int d = blockIdx.x;
+    uint32_t carry = block_sum<uint32_t, OpSum>(
+        threadIdx.x < static_cast<unsigned>(d) ? digit_tot[threadIdx.x] : 0u, s_wave);
+    __syncthreads();
+    uint32_t* row = hist + static_cast<size_t>(d) * nb;
+    for (size_t chunk = 0; chunk < nb; chunk += kScanTile) {
+        const size_t base = chunk + static_cast<size_t>(threadIdx.x) * kScanItems;
+        uint32_t v[kScanItems];
+        uint32_t acc = 0;
+#pragma unroll
+        for (int j = 0; j < kScanItems; ++j) {
+            const size_t i = base + j;
+            v[j] = i < nb ? row[i] : 0u;
+            acc += v[j];
+        }
+        uint32_t tot;
+        uint32_t run = carry + block_exclusive_scan<uint32_t, OpSum>(acc, &tot, s_wave);
+#pragma unroll
+        for (int j = 0; j < kScanItems; ++j) {
+            const size_t i = base + j;
+            if (i < nb) row[i] = run;
+            run += v[j];
+        }
+        carry += tot;
+        __syncthreads();
+    }
+}
+
+__global__ void fill_u32_kernel(uint32_t* __restrict__ p, size_t n, uint32_t v) {
+    const size_t i = blockIdx.x * static_cast<size_t>(kBlock) + threadIdx.x;
+    if (i < n) p[i] = v;
 }
 
 template <typename K, typename V>
@@ -297,19 +339,26 @@ __global__ __launch_bounds__(kBlock) void radix_scatter_kernel(
     }
 }
 
+// hist layout: nb * kRadix per-workgroup counts, then kMaxPasses * kRadix
+// digit totals (one row per pass, cleared once per sort).
+constexpr int kMaxPasses = 64 / kRadixBits;
+
 template <typename K, typename V = uint32_t>
 int radix_sort_impl(K* keys0, V* vals0, K* keys1, V* vals1, size_t n,
-                    int begin_bit, int end_bit, uint32_t* hist, uint32_t* hist_scratch,
-                    hipStream_t s) {
+                    int begin_bit, int end_bit, uint32_t* hist, hipStream_t s) {
     if (n <= 1 || end_bit <= begin_bit) return 0;
     const size_t nb = (n + kSortSpan - 1) / kSortSpan;
-    int cur = 0;
+    uint32_t* totals = hist + nb * kRadix;
+    hipLaunchKernelGGL(fill_u32_kernel, dim3((kMaxPasses * kRadix + kBlock - 1) / kBlock),
+                       dim3(kBlock), 0, s, totals, static_cast<size_t>(kMaxPasses * kRadix), 0u);
+    int cur = 0, pass = 0;
     K* kb[2] = {keys0, keys1};
     V* vb[2] = {vals0, vals1};
-    for (int bit = begin_bit; bit < end_bit; bit += kRadixBits) {
+    for (int bit = begin_bit; bit < end_bit; bit += kRadixBits, ++pass) {
+        uint32_t* tot = totals + pass * kRadix;
         hipLaunchKernelGGL((radix_upsweep_kernel<K>), dim3(nb), dim3(kBlock), 0, s, kb[cur], n,
-                           bit, hist, nb);
-        scan_impl<uint32_t, false>(hist, hist, nb * kRadix, hist_scratch, s);
+                           bit, hist, nb, tot);
+        hipLaunchKernelGGL(radix_offsets_kernel, dim3(kRadix), dim3(kBlock), 0, s, hist, nb, tot);
         hipLaunchKernelGGL((radix_scatter_kernel<K, V>), dim3(nb), dim3(kBlock), 0, s, kb[cur],
                            vb[cur], kb[cur ^ 1], vb[cur ^ 1], n, bit, hist, nb);
         check_hip(hipGetLastError(), "radix sort launch");
@@ -424,7 +473,9 @@ int reduce_blocks(size_t n) {
 }  // namespace
 
 size_t scan_scratch_elems(size_t n) { return (n + kScanTile - 1) / kScanTile + 1; }
-size_t radix_hist_elems(size_t n) { return ((n + kSortSpan - 1) / kSortSpan) * kRadix + 1; }
+size_t radix_hist_elems(size_t n) {
+    return ((n + kSortSpan - 1) / kSortSpan) * kRadix + kMaxPasses * kRadix;
+}
 
 void exclusive_scan_u32(const uint32_t* in, uint32_t* out, size_t n, uint32_t* scratch,
                         hipStream_t s) {
@@ -442,22 +493,17 @@ void running_max_f64(double* data, size_t n, double* scratch, hipStream_t s) {
 }
 
 int radix_sort_u64(uint64_t* keys0, uint32_t* vals0, uint64_t* keys1, uint32_t* vals1, size_t n,
-                   int begin_bit, int end_bit, uint32_t* hist, uint32_t* hist_scratch,
-                   hipStream_t s) {
-    return radix_sort_impl<uint64_t>(keys0, vals0, keys1, vals1, n, begin_bit, end_bit, hist,
-                                     hist_scratch, s);
+                   int begin_bit, int end_bit, uint32_t* hist, hipStream_t s) {
+    return radix_sort_impl<uint64_t>(keys0, vals0, keys1, vals1, n, begin_bit, end_bit, hist, s);
 }
 int radix_sort_u32(uint32_t* keys0, uint32_t* vals0, uint32_t* keys1, uint32_t* vals1, size_t n,
-                   int begin_bit, int end_bit, uint32_t* hist, uint32_t* hist_scratch,
-                   hipStream_t s) {
-    return radix_sort_impl<uint32_t>(keys0, vals0, keys1, vals1, n, begin_bit, end_bit, hist,
-                                     hist_scratch, s);
+                   int begin_bit, int end_bit, uint32_t* hist, hipStream_t s) {
+    return radix_sort_impl<uint32_t>(keys0, vals0, keys1, vals1, n, begin_bit, end_bit, hist, s);
 }
 int radix_sort_u32_v64(uint32_t* keys0, uint64_t* vals0, uint32_t* keys1, uint64_t* vals1,
-                       size_t n, int begin_bit, int end_bit, uint32_t* hist,
-                       uint32_t* hist_scratch, hipStream_t s) {
+                       size_t n, int begin_bit, int end_bit, uint32_t* hist, hipStream_t s) {
     return radix_sort_impl<uint32_t, uint64_t>(keys0, vals0, keys1, vals1, n, begin_bit, end_bit,
-                                               hist, hist_scratch, s);
+                                               hist, s);
 }
 int radix_passes(int begin_bit, int end_bit) {
     return end_bit > begin_bit ? (end_bit - begin_bit + kRadixBits - 1) / kRadixBits : 0;

@@ -917,7 +917,6 @@ void Engine::sample(const trw_sample_params& p) {
                 k32a.ensure(m);
                 k32b.ensure(m);
                 hist.ensure(radix_hist_elems(m));
-                hist_scratch.ensure(scan_scratch_elems(radix_hist_elems(m)));
                 flags.ensure(m + 1);
                 scan.ensure(m + 1);
                 scan_scratch.ensure(scan_scratch_elems(m + 1));
@@ -929,8 +928,7 @@ void Engine::sample(const trw_sample_params& p) {
                                            0, s, last_dst.p, last_n, k32a.p + last_n);
                     }
                 }
-                const int w = radix_sort_u32(k32a.p, nullptr, k32b.p, nullptr, m, 0, 32, hist.p,
-                                             hist_scratch.p, s);
+                const int w = radix_sort_u32(k32a.p, nullptr, k32b.p, nullptr, m, 0, 32, hist.p, s);
                 uint32_t* keys = w ? k32b.p : k32a.p;
                 if (m) {
                     hipLaunchKernelGGL(unique_flags_kernel, dim3(grid_for(m)), dim3(kB), 0, s,
@@ -1006,12 +1004,10 @@ void Engine::sample(const trw_sample_params& p) {
         v32a.ensure(nw);
         v32b.ensure(nw);
         hist.ensure(radix_hist_elems(nw));
-        hist_scratch.ensure(scan_scratch_elems(radix_hist_elems(nw)));
         hipLaunchKernelGGL(random_keys_kernel, dim3(grid_for(nw)), dim3(kB), 0, s, nw,
                            static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32), k32a.p,
                            v32a.p);
-        const int w = radix_sort_u32(k32a.p, v32a.p, k32b.p, v32b.p, nw, 0, 32, hist.p,
-                                     hist_scratch.p, s);
+        const int w = radix_sort_u32(k32a.p, v32a.p, k32b.p, v32b.p, nw, 0, 32, hist.p, s);
         const uint32_t* perm = w ? v32b.p : v32a.p;
         DBuf<int32_t> tmp;
         tmp.resize(nw);
@@ -1171,10 +1167,8 @@ void Engine::sample(const trw_sample_params& p) {
             k32b.ensure(nw);
             v32b.ensure(nw);
             hist.ensure(radix_hist_elems(nw));
-            hist_scratch.ensure(scan_scratch_elems(radix_hist_elems(nw)));
             const int bits = std::max(1, 32 - __builtin_clz(none | 1u));
-            const int wsort = radix_sort_u32(k32a.p, v32a.p, k32b.p, v32b.p, nw, 0, bits, hist.p,
-                                             hist_scratch.p, s);
+            const int wsort = radix_sort_u32(k32a.p, v32a.p, k32b.p, v32b.p, nw, 0, bits, hist.p, s);
             a.order = wsort ? v32b.p : v32a.p;
             a.xcd_remap = 1;
         }
