@@ -56,7 +56,7 @@ __global__ void make_ts_keys_kernel(const int64_t* __restrict__ old_ts,
     const int32_t a = old ? old_src[k] : new_src[k];
     const int32_t b = old ? old_dst[k] : new_dst[k];
     keys[i] = static_cast<K>(static_cast<uint64_t>(t) - static_cast<uint64_t>(tmin));
-    vals[i] = static_cast<uint32_t>(i);
+    if (vals) vals[i] = static_cast<uint32_t>(i);
     ends[i] = static_cast<uint64_t>(static_cast<uint32_t>(a)) |
               (static_cast<uint64_t>(static_cast<uint32_t>(b)) << 32);
 }
@@ -93,6 +93,21 @@ __global__ void gather_store_kernel(const K* __restrict__ keys, const uint32_t* 
     const size_t j = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
     if (j >= kept) return;
     const uint64_t sd = ends[perm[del + j]];
+    s[j] = static_cast<int32_t>(static_cast<uint32_t>(sd));
+    d[j] = static_cast<int32_t>(static_cast<uint32_t>(sd >> 32));
+    t[j] = static_cast<int64_t>(static_cast<uint64_t>(keys[del + j]) + static_cast<uint64_t>(tmin));
+}
+
+// The kept suffix when the endpoints travelled through the sort as its values:
+// every read is in order.
+template <typename K>
+__global__ void store_from_sorted_kernel(const K* __restrict__ keys,
+                                         const uint64_t* __restrict__ ends, size_t del,
+                                         size_t kept, int64_t tmin, int32_t* __restrict__ s,
+                                         int32_t* __restrict__ d, int64_t* __restrict__ t) {
+    const size_t j = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (j >= kept) return;
+    const uint64_t sd = ends[del + j];
     s[j] = static_cast<int32_t>(static_cast<uint32_t>(sd));
     d[j] = static_cast<int32_t>(static_cast<uint32_t>(sd >> 32));
     t[j] = static_cast<int64_t>(static_cast<uint64_t>(keys[del + j]) + static_cast<uint64_t>(tmin));
@@ -867,29 +882,42 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
     latest_ts = std::max(latest_ts, hs[1]);
 
     // ---- 2. stable radix sort by (ts, position); 32-bit keys when the key
-    // range fits (4-byte key traffic per pass instead of 8)
+    // range fits (4-byte key traffic per pass instead of 8).  Without edge
+    // features the sort's values are the packed endpoints themselves, so the
+    // store is written from the sorted values in order; with features they are
+    // the positions the feature rows are gathered by.
     const int bits = bit_length_u64(static_cast<uint64_t>(tmax) - static_cast<uint64_t>(tmin));
     const bool keys32 = bits <= 32;
+    const bool carry_ends = feat_dim == 0;
     k64a.ensure(etot);
     k64b.ensure(etot);
     ends64.ensure(etot);
+    if (carry_ends) ends64b.ensure(etot);
     v32a.ensure(std::max(etot, 2 * etot));
     v32b.ensure(std::max(etot, 2 * etot));
     hist.ensure(radix_hist_elems(2 * etot));
     uint32_t* k32s[2] = {reinterpret_cast<uint32_t*>(k64a.p), reinterpret_cast<uint32_t*>(k64b.p)};
+    uint32_t* pos0 = carry_ends ? nullptr : v32a.p;
     int which;
     if (keys32) {
         hipLaunchKernelGGL((make_ts_keys_kernel<uint32_t>), dim3(grid_for(etot)), dim3(kB), 0, s,
-                           ts.p, src.p, dst.p, e_old, d_ts, d_src, d_dst, n, tmin, k32s[0],
-                           v32a.p, ends64.p);
-        which = radix_sort_u32(k32s[0], v32a.p, k32s[1], v32b.p, etot, 0, bits, hist.p, s);
+                           ts.p, src.p, dst.p, e_old, d_ts, d_src, d_dst, n, tmin, k32s[0], pos0,
+                           ends64.p);
+        which = carry_ends
+                    ? radix_sort_u32_v64(k32s[0], ends64.p, k32s[1], ends64b.p, etot, 0, bits,
+                                         hist.p, s)
+                    : radix_sort_u32(k32s[0], v32a.p, k32s[1], v32b.p, etot, 0, bits, hist.p, s);
     } else {
         hipLaunchKernelGGL((make_ts_keys_kernel<uint64_t>), dim3(grid_for(etot)), dim3(kB), 0, s,
-                           ts.p, src.p, dst.p, e_old, d_ts, d_src, d_dst, n, tmin, k64a.p,
-                           v32a.p, ends64.p);
-        which = radix_sort_u64(k64a.p, v32a.p, k64b.p, v32b.p, etot, 0, bits, hist.p, s);
+                           ts.p, src.p, dst.p, e_old, d_ts, d_src, d_dst, n, tmin, k64a.p, pos0,
+                           ends64.p);
+        which = carry_ends
+                    ? radix_sort_u64_v64(k64a.p, ends64.p, k64b.p, ends64b.p, etot, 0, bits,
+                                         hist.p, s)
+                    : radix_sort_u64(k64a.p, v32a.p, k64b.p, v32b.p, etot, 0, bits, hist.p, s);
     }
     uint32_t* perm = which ? v32b.p : v32a.p;
+    const uint64_t* sorted_ends = which ? ends64b.p : ends64.p;
 
     // ---- 3. window eviction: drop ts <= latest - capacity
     int64_t target = -1;
@@ -915,7 +943,16 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
     src2.resize(kept);
     dst2.resize(kept);
     ts2.resize(kept);
-    if (kept) {
+    if (kept && carry_ends) {
+        if (keys32)
+            hipLaunchKernelGGL((store_from_sorted_kernel<uint32_t>), dim3(grid_for(kept)), dim3(kB),
+                               0, s, k32s[which], sorted_ends, del, kept, tmin, src2.p, dst2.p,
+                               ts2.p);
+        else
+            hipLaunchKernelGGL((store_from_sorted_kernel<uint64_t>), dim3(grid_for(kept)), dim3(kB),
+                               0, s, which ? k64b.p : k64a.p, sorted_ends, del, kept, tmin,
+                               src2.p, dst2.p, ts2.p);
+    } else if (kept) {
         if (keys32)
             hipLaunchKernelGGL((gather_store_kernel<uint32_t>), dim3(grid_for(kept)), dim3(kB), 0,
                                s, k32s[which], perm, ends64.p, del, kept, tmin, src2.p, dst2.p,

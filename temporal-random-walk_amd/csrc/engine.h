@@ -268,7 +268,7 @@ struct Engine {
 
     // scratch
     DBuf<uint64_t> k64a, k64b;
-    DBuf<uint64_t> ends64;  // packed (src, dst) of the timestamp sort's input
+    DBuf<uint64_t> ends64, ends64b;  // packed (src, dst) of the timestamp sort's input
     DBuf<uint32_t> k32a, k32b, v32a, v32b;
     DBuf<uint32_t> hist, flags, scan, scan_scratch;
     DBuf<uint64_t> scan64_scratch;

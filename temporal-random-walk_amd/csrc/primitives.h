@@ -48,7 +48,9 @@ int radix_sort_u64(uint64_t* keys0, uint32_t* vals0, uint64_t* keys1, uint32_t* 
                    int begin_bit, int end_bit, uint32_t* hist, hipStream_t s);
 int radix_sort_u32(uint32_t* keys0, uint32_t* vals0, uint32_t* keys1, uint32_t* vals1, size_t n,
                    int begin_bit, int end_bit, uint32_t* hist, hipStream_t s);
-// 32-bit keys with 64-bit values (a record carried through the sort).
+// 64- and 32-bit keys with 64-bit values (a record carried through the sort).
+int radix_sort_u64_v64(uint64_t* keys0, uint64_t* vals0, uint64_t* keys1, uint64_t* vals1,
+                       size_t n, int begin_bit, int end_bit, uint32_t* hist, hipStream_t s);
 int radix_sort_u32_v64(uint32_t* keys0, uint64_t* vals0, uint32_t* keys1, uint64_t* vals1,
                        size_t n, int begin_bit, int end_bit, uint32_t* hist, hipStream_t s);
 // Digit passes of a sort of bits [begin_bit, end_bit): the result lands in

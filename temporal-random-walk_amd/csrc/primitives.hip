@@ -500,6 +500,11 @@ int radix_sort_u32(uint32_t* keys0, uint32_t* vals0, uint32_t* keys1, uint32_t* 
                    int begin_bit, int end_bit, uint32_t* hist, hipStream_t s) {
     return radix_sort_impl<uint32_t>(keys0, vals0, keys1, vals1, n, begin_bit, end_bit, hist, s);
 }
+int radix_sort_u64_v64(uint64_t* keys0, uint64_t* vals0, uint64_t* keys1, uint64_t* vals1,
+                       size_t n, int begin_bit, int end_bit, uint32_t* hist, hipStream_t s) {
+    return radix_sort_impl<uint64_t, uint64_t>(keys0, vals0, keys1, vals1, n, begin_bit, end_bit,
+                                               hist, s);
+}
 int radix_sort_u32_v64(uint32_t* keys0, uint64_t* vals0, uint32_t* keys1, uint64_t* vals1,
                        size_t n, int begin_bit, int end_bit, uint32_t* hist, hipStream_t s) {
     return radix_sort_impl<uint32_t, uint64_t>(keys0, vals0, keys1, vals1, n, begin_bit, end_bit,
