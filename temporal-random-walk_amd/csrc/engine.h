@@ -52,6 +52,7 @@
 
 #include <cstring>
 #include <memory>
+#include <new>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -86,7 +87,13 @@ struct DBuf {
         if (k > cap) {
             release();
             const size_t c = k + k / 4 + 64;
-            check_hip(hipMalloc(&p, c * sizeof(T)), "hipMalloc");
+            const hipError_t e = hipMalloc(&p, c * sizeof(T));
+            if (e == hipErrorOutOfMemory) {
+                (void)hipGetLastError();  // clear the sticky error
+                p = nullptr;
+                throw std::bad_alloc();  // TRW_ERR_OUT_OF_MEMORY / MemoryError
+            }
+            check_hip(e, "hipMalloc");
             cap = c;
         }
     }

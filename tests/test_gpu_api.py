@@ -80,6 +80,21 @@ def test_invalid_strings_raise_value_error():
                                       kernel_launch_type="WARP")
 
 
+def test_device_allocation_failure_raises_memory_error_and_engine_recovers():
+    """A sample whose walk buffers exceed HBM (2^31 - 1 walks of 2,000 slots, about
+    17 TB of scratch) fails its allocation: MemoryError, as the reference's
+    std::bad_alloc maps, and the instance keeps working."""
+    tw = _trw(is_directed=True, global_seed=3)
+    tw.add_multiple_edges(np.array([0, 1, 2], np.int32), np.array([1, 2, 3], np.int32),
+                          np.arange(3, dtype=np.int64))
+    with pytest.raises(MemoryError):
+        tw.get_random_walks_and_times(max_walk_len=2_000, walk_bias="Uniform",
+                                      num_walks_total=(1 << 31) - 1)
+    nodes, ts, lens, _ = tw.get_random_walks_and_times(max_walk_len=4, walk_bias="Uniform",
+                                                       num_walks_total=100)
+    assert nodes.shape == (100, 4) and int(lens.max()) >= 2
+
+
 def test_queries_match_store():
     s, d, t = graphs.sample_data()
     tw = _trw(is_directed=True)
