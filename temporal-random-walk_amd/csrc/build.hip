@@ -317,14 +317,17 @@ __global__ void node_headers_kernel(const uint32_t* __restrict__ cnt,
     NodeHdr h{gb, 0, 0, 0};
     if (u + 1 < vc) {
         const uint32_t G = cnt[u + 1] - gb;
-        uint32_t shift = 0;
+        uint32_t shift = 0, dense = 0;
         if (G > kTabMin) {
             h.r0 = pan[gb].rank;
             const uint32_t span = pan[gb + G - 1].rank - h.r0;
             shift = table_shift(G, span);
             h.nb = (span >> shift) + 1;
+            // ranks are distinct and increasing, so G == span + 1 means every
+            // rank of the span has a group: group i has rank r0 + i
+            if (span == G - 1) dense = kHdrDense;
         }
-        h.meta = (G < kHdrGMask ? G : kHdrGMask) | (shift << 24);
+        h.meta = (G < kHdrGMask ? G : kHdrGMask) | (shift << 24) | dense;
     }
     hdr[u] = h;
 }
@@ -342,7 +345,7 @@ __global__ void node_table_fill_kernel(const uint32_t* __restrict__ key,
     const uint32_t u = key[grp[g]];
     const NodeHdr h = hdr[u];
     const uint32_t G = hdr[u + 1].gb - h.gb;
-    if (G <= kTabMin) return;
+    if (G <= kTabMin || (h.meta & kHdrDense)) return;  // dense nodes need no table
     const uint32_t shift = hdr_shift(h);
     uint32_t* t = tab + hdr_tab_base(h, u);
     const uint32_t i = static_cast<uint32_t>(g) - h.gb;

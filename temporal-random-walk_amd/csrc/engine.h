@@ -163,11 +163,13 @@ constexpr uint32_t kTabBucketsPerGroup = 2;
 struct alignas(16) NodeHdr {
     uint32_t gb;    // first group of the node
     uint32_t meta;  // G (bits 0-23, kHdrGMask if larger: read the next gb),
-                    // bucket shift (bits 24-28)
+                    // bucket shift (bits 24-28), dense flag (bit 31: a
+                    // tabled node with a group at every rank of its span)
     uint32_t r0;    // rank of its first group (tabled nodes)
     uint32_t nb;    // number of buckets (tabled nodes)
 };
 constexpr uint32_t kHdrGMask = 0xffffffu;
+constexpr uint32_t kHdrDense = 1u << 31;
 __host__ __device__ inline uint32_t hdr_shift(const NodeHdr& h) { return (h.meta >> 24) & 31u; }
 __host__ __device__ inline uint64_t hdr_tab_base(const NodeHdr& h, uint32_t u) {
     return 2ull * (static_cast<uint64_t>(h.gb) + u);

@@ -31,9 +31,16 @@ __global__ void pick_index_kernel(int picker, const int32_t* __restrict__ start,
                                   const int32_t* __restrict__ end, uint64_t n, int prioritize_end,
                                   const double* __restrict__ draws, uint32_t k0, uint32_t k1,
                                   int32_t* __restrict__ out) {
+    __shared__ double s_xt[kExpTables];
+    const bool use_xt = picker == kExponentialIndex;
+    if (use_xt) {
+        fill_exp_tables(s_xt, threadIdx.x, kB);
+        __syncthreads();
+    }
     const uint64_t i = blockIdx.x * static_cast<uint64_t>(kB) + threadIdx.x;
     if (i >= n) return;
-    out[i] = pick_index(picker, start[i], end[i], prioritize_end != 0, pick_draw(draws, i, k0, k1));
+    out[i] = pick_index(picker, start[i], end[i], prioritize_end != 0, pick_draw(draws, i, k0, k1),
+                        use_xt ? s_xt : nullptr);
 }
 
 // WeightBasedRandomPicker::pick_random over one cumulative array (slice start

@@ -93,15 +93,22 @@ struct DrawPair {
     double a, b;
 };
 
-// Draws for slots (2p-1, 2p) of walk w (p >= 1).
-__device__ __forceinline__ DrawPair draw_pair(const DrawSource& ds, uint64_t w, uint32_t p) {
-    if (ds.replay) {
-        const double* r = ds.replay + w * ds.stride;
-        return DrawPair{r[2 * p - 1], r[2 * p]};
-    }
+// Normal-mode draws for slots (2p-1, 2p) of walk w (p >= 1).
+__device__ __forceinline__ DrawPair philox_pair(const DrawSource& ds, uint64_t w, uint32_t p) {
     const U4 o = philox4x32_10(U4{p, static_cast<uint32_t>(w), static_cast<uint32_t>(w >> 32), 0u},
                                ds.k0, ds.k1);
     return DrawPair{bits_to_unit(o.x, o.y), bits_to_unit(o.z, o.w)};
+}
+
+// Replay-mode draws for slots (2p-1, 2p) of walk w (p >= 1).
+__device__ __forceinline__ DrawPair replay_pair(const DrawSource& ds, uint64_t w, uint32_t p) {
+    const double* r = ds.replay + w * ds.stride;
+    return DrawPair{r[2 * p - 1], r[2 * p]};
+}
+
+// Draws for slots (2p-1, 2p) of walk w (p >= 1).
+__device__ __forceinline__ DrawPair draw_pair(const DrawSource& ds, uint64_t w, uint32_t p) {
+    return ds.replay ? replay_pair(ds, w, p) : philox_pair(ds, w, p);
 }
 
 __device__ __forceinline__ double draw_slot0(const DrawSource& ds, uint64_t w) {
@@ -128,20 +135,88 @@ __device__ __forceinline__ int pick_linear(int start, int end, bool prioritize_e
 
 // Lengths below this take the expm1 branch of the exponential index picker.
 constexpr int kExpm1Table = 710;
+// exp(-j) for j in [0, kExpNegTable), after the expm1 values.
+constexpr int kExpNegTable = 40;
+constexpr int kExpTables = kExpm1Table + kExpNegTable;
 
-// em1: expm1(len) for len in [0, kExpm1Table) (the same values expm1 returns
-// here), or nullptr to evaluate it.
-__device__ __forceinline__ int pick_exponential_index(int start, int end, bool prioritize_end,
-                                                      double r, const double* em1 = nullptr) {
-    if (start >= end) return -1;
-    const int len = end - start;
+// Fills the exponential index picker's tables: xt[i] = expm1(i) for i <
+// kExpm1Table, then xt[kExpm1Table + j] = exp(-j).  Threads tid of nthreads
+// share the work.
+__device__ __forceinline__ void fill_exp_tables(double* xt, int tid, int nthreads) {
+    for (int i = tid; i < kExpTables; i += nthreads)
+        xt[i] = i < kExpm1Table ? expm1(static_cast<double>(i))
+                                : exp(-static_cast<double>(i - kExpm1Table));
+}
+
+// The exponential index picker's ri (random/pickers.cuh:47-71): with k =
+// log1p(r * expm1(len)) - 1 for len < kExpm1Table and k = len + log(r) - 1
+// above, ri = clamp((int)(k + 1), 0, len - 1).
+__device__ __forceinline__ int exp_index_ri_ref(int len, double r, const double* xt) {
     double k;
     if (len < kExpm1Table) {
-        k = log1p(r * (em1 ? em1[len] : expm1(static_cast<double>(len)))) - 1;
+        k = log1p(r * (xt ? xt[len] : expm1(static_cast<double>(len)))) - 1;
     } else {
         k = len + log(r) - 1;
     }
-    const int ri = max(0, min(static_cast<int>(k + 1), len - 1));
+    return max(0, min(static_cast<int>(k + 1), len - 1));
+}
+
+// The same ri from the tables, without a logarithm.  In exact arithmetic
+// ri = floor(log1p(x)) with x = r * expm1(len), the number of i in [1, len)
+// with expm1(i) <= x; above the table ri = len - 1 - j with j = floor(-log r),
+// where exp(-(j+1)) < r <= exp(-j).  The exponent of 1 + x (of r) brackets
+// the answer to two neighbours, one table entry decides between them.  The
+// reference's rounded log1p / log and sum agree with the exact floor unless
+// the exact value lies within a few ulps of an integer, i.e. unless x (r)
+// lies within a small relative margin of a table threshold: such a draw, or
+// one the estimate did not bracket (the margin test then fails too), takes
+// the reference expression itself.  Margins: log1p and log err by at most 2
+// ulps (<= 2^-41.5 absolute below 710, <= 2^-45 below 64), the sum len +
+// log(r) rounds by at most len * 2^-52, the table entries by 2^-52
+// relative; the margins below exceed their sum eightfold.
+__device__ __forceinline__ int exp_index_ri(int len, double r, const double* xt) {
+    if (xt == nullptr) return exp_index_ri_ref(len, r, xt);
+    constexpr float kLn2 = 0.693147182f;
+    if (len < kExpm1Table) {
+        const double x = r * xt[len];
+        const int e = __builtin_amdgcn_frexp_exp(1.0 + x) - 1;  // 1 + x in [2^e, 2^(e+1))
+        const int est = min(static_cast<int>(static_cast<float>(e) * kLn2), len - 1);
+        const double t1 = xt[min(est + 1, kExpm1Table - 1)];
+        const bool up = est + 1 < len && x >= t1;
+        const int i = est + (up ? 1 : 0);
+        const double lo = up ? t1 : xt[est];
+        const double hi = xt[min(i + 1, kExpm1Table - 1)];
+        const double m = 0x1p-38;
+        const bool near_lo = i > 0 && x - lo < m * (1.0 + lo);
+        const bool near_hi = i + 1 < len && hi - x < m * (1.0 + hi);
+        if (near_lo || near_hi || !(x >= 0.0)) return exp_index_ri_ref(len, r, xt);
+        return i;
+    }
+    const double* en = xt + kExpm1Table;
+    const int e = __builtin_amdgcn_frexp_exp(r);  // r in [2^(e-1), 2^e)
+    // -log r lies in (-e ln2, (1 - e) ln2]; r >= 2^-54 keeps the entries read
+    // inside the table
+    if (!(r >= 0x1p-54 && r < 1.0)) return exp_index_ri_ref(len, r, xt);
+    const int est = static_cast<int>(static_cast<float>(-e) * kLn2);
+    const double t1 = en[est + 1];
+    const bool up = r <= t1;
+    const int j = est + (up ? 1 : 0);
+    const double lo = up ? en[est + 2] : t1;  // exp(-(j+1))
+    const double hi = up ? t1 : en[est];      // exp(-j)
+    const double m = static_cast<double>(len + 64) * 0x1p-48;
+    const bool near_lo = r - lo < m * lo;
+    const bool near_hi = j > 0 && hi - r < m * hi;
+    if (near_lo || near_hi) return exp_index_ri_ref(len, r, xt);
+    return len - 1 - j;
+}
+
+// xt: the tables of fill_exp_tables, or nullptr to evaluate the reference
+// expression directly.
+__device__ __forceinline__ int pick_exponential_index(int start, int end, bool prioritize_end,
+                                                      double r, const double* xt = nullptr) {
+    if (start >= end) return -1;
+    const int len = end - start;
+    const int ri = exp_index_ri(len, r, xt);
     return prioritize_end ? start + ri : start + (len - 1 - ri);
 }
 
@@ -151,10 +226,10 @@ __device__ __forceinline__ int pick_uniform(int start, int end, double r) {
 }
 
 __device__ __forceinline__ int pick_index(int picker, int start, int end, bool prioritize_end,
-                                          double r, const double* em1 = nullptr) {
+                                          double r, const double* xt = nullptr) {
     switch (picker) {
         case kLinear: return pick_linear(start, end, prioritize_end, r);
-        case kExponentialIndex: return pick_exponential_index(start, end, prioritize_end, r, em1);
+        case kExponentialIndex: return pick_exponential_index(start, end, prioritize_end, r, xt);
         case kUniform: return pick_uniform(start, end, r);
         case kTestFirst: return start;
         case kTestLast: return end - 1;

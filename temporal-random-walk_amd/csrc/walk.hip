@@ -168,14 +168,17 @@ typedef uint32_t u32x2_a4 __attribute__((ext_vector_type(2), aligned(4)));
 // First local index i in [0, G) whose group rank is >= x, G if none: a
 // lower_bound over the node's sorted panel, so the answer is unique and the
 // way it is found does not change any result.  A node with more than kTabMin
-// groups first looks up x's bucket b in its table: a single-rank bucket holds
-// the answer itself; a wider one gives the bracket [tab[b], tab[b + 1]]
-// (about one group).  The rest is a binary search over at most kTabMin groups.
+// groups that has a group at every rank of its span (dense) answers from the
+// rank itself.  Another such node looks up x's bucket b in its table: a
+// single-rank bucket holds the answer itself; a wider one gives the bracket
+// [tab[b], tab[b + 1]] (about one group).  The rest is a binary search over
+// at most kTabMin groups.
 __device__ __forceinline__ int first_ge(const uint32_t* tab, const NodeHdr& h, uint32_t u, int G,
                                         const PanelRec* f, uint32_t x) {
     int lo = 0, hi = G;
     if (G > static_cast<int>(kTabMin)) {
         if (x <= h.r0) return 0;
+        if (h.meta & kHdrDense) return static_cast<int>(min(x - h.r0, static_cast<uint32_t>(G)));
         const uint32_t shift = hdr_shift(h);
         const uint32_t b = (x - h.r0) >> shift;
         if (b >= h.nb) return G;  // past the last bucket
@@ -351,13 +354,14 @@ __device__ Hop tn2v_pick(const WalkGraph& g, int prev, uint32_t vb, uint32_t ve,
 // t: rank of the current time, -1 for none (a start, or a current time of
 // -1, which the reference also reads as unconstrained); cut: rank bound of
 // the walk's cutoff time (groups at or past it are excluded), -1 for none.
+//
+// The selection after the header load of node u: ok is false for a node
+// outside the index (then the value of h is ignored).
 template <bool Fwd, int Fam>
-__device__ Hop node_edge_at(const WalkGraph& g, int picker, int node, int32_t t, int32_t cut,
-                            int prev, double rg, double re, const double* em1 = nullptr) {
-    if (!(node >= 0 && node < g.active_size)) return no_hop();
-    const uint32_t u = static_cast<uint32_t>(node);
-    const NodeHdr h = g.d.hdr[u];
-    uint32_t Gu = h.meta & kHdrGMask;
+__device__ __forceinline__ Hop node_edge_from(const WalkGraph& g, int picker, uint32_t u, bool ok,
+                                              const NodeHdr& h, int32_t t, int32_t cut, int prev,
+                                              double rg, double re, const double* em1) {
+    uint32_t Gu = ok ? (h.meta & kHdrGMask) : 0u;
     if (Gu == kHdrGMask) Gu = g.d.hdr[u + 1].gb - h.gb;  // more groups than 24 bits hold
     if (Gu == 0) return no_hop();
     const uint32_t gb = h.gb, ge = gb + Gu;
@@ -384,7 +388,7 @@ __device__ Hop node_edge_at(const WalkGraph& g, int picker, int node, int32_t t,
         gpos = gb + static_cast<uint32_t>(vb + index);
     } else {
         const double* lv =
-            (g.d.wx && G > static_cast<int>(kWIdxMin)) ? g.d.wx + g.d.wx_off[node] : nullptr;
+            (g.d.wx && G > static_cast<int>(kWIdxMin)) ? g.d.wx + g.d.wx_off[u] : nullptr;
         if (Fam != kFamWeight && picker == kTemporalNode2Vec && prev != -1)
             return tn2v_pick(g, prev, gb + vb, gb + ve, gb, ge, lv, rg, re);
         // ExponentialWeight, or node2vec's first hop (no previous node)
@@ -403,6 +407,14 @@ __device__ Hop node_edge_at(const WalkGraph& g, int picker, int node, int32_t t,
     return hop_of(load_rec(g.d.rec + es +
                            static_cast<uint32_t>(static_cast<int>(re * static_cast<int>(ee - es)))),
                   pp.rank);
+}
+
+template <bool Fwd, int Fam>
+__device__ Hop node_edge_at(const WalkGraph& g, int picker, int node, int32_t t, int32_t cut,
+                            int prev, double rg, double re, const double* em1 = nullptr) {
+    if (!(node >= 0 && node < g.active_size)) return no_hop();
+    const uint32_t u = static_cast<uint32_t>(node);
+    return node_edge_from<Fwd, Fam>(g, picker, u, true, g.d.hdr[u], t, cut, prev, rg, re, em1);
 }
 
 // Rank bound of a walk's cutoff time: groups at or past it are excluded
@@ -482,15 +494,15 @@ __device__ __forceinline__ uint64_t grid_position(int remap) {
 
 template <bool Fwd, bool Dir, int Fam>
 __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
-    // expm1 of every length the exponential index picker evaluates it for,
-    // once per workgroup instead of once per hop
-    __shared__ double s_em1[kExpm1Table];
-    const bool use_em1 = a.walk_bias == kExponentialIndex;
-    if (use_em1) {
-        for (int i = threadIdx.x; i < kExpm1Table; i += kB) s_em1[i] = expm1(static_cast<double>(i));
+    // the exponential index picker's thresholds (expm1 of every length it
+    // evaluates, exp(-j)), once per workgroup instead of a logarithm per hop
+    __shared__ double s_xt[kExpTables];
+    const bool use_xt = a.walk_bias == kExponentialIndex;
+    if (use_xt) {
+        fill_exp_tables(s_xt, threadIdx.x, kB);
         __syncthreads();
     }
-    const double* em1 = use_em1 ? s_em1 : nullptr;
+    const double* em1 = use_xt ? s_xt : nullptr;
     const uint64_t q = a.q0 + grid_position(a.xcd_remap);
     if (q >= a.q_end) return;
     const uint64_t w = a.order ? a.order[q] : q;
@@ -533,9 +545,22 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
             // The reference draws and selects once more after the last slot is
             // written; that selection cannot change the output, so it is skipped.
             if (walk_len == L - 1) break;
-            const DrawPair r = draw_pair(a.ds, w, static_cast<uint32_t>(walk_len) + 1);
-            const Hop h = node_edge_at<Fwd, Fam>(g, a.walk_bias, cur, cur_r == neg1 ? -1 : cur_r,
-                                                 cut, prev, r.a, r.b, em1);
+            // The header load is issued before the hop's Philox draws are
+            // computed, in the same basic block, so the rounds run while it
+            // is in flight (the empty asm keeps the compiler from sinking them
+            // below the load's first use; replay mode computes and discards
+            // them).  The walk reached cur over an edge, so the index is not
+            // empty and entry 0 is a valid address for a node outside it.
+            const bool ok = cur >= 0 && cur < g.active_size;
+            const uint32_t u = ok ? static_cast<uint32_t>(cur) : 0u;
+            const NodeHdr hd = g.d.hdr[u];
+            const uint32_t p = static_cast<uint32_t>(walk_len) + 1;
+            DrawPair r = philox_pair(a.ds, w, p);
+            asm volatile("" : "+v"(r.a), "+v"(r.b));
+            if (a.ds.replay) r = replay_pair(a.ds, w, p);
+            const Hop h = node_edge_from<Fwd, Fam>(g, a.walk_bias, u, ok, hd,
+                                                   cur_r == neg1 ? -1 : cur_r, cut, prev, r.a,
+                                                   r.b, em1);
             // the reference's failure test is ts == -1: no edge, or an edge at -1
             if (h.e == -1 || h.r == neg1) break;
             prev = cur;

@@ -48,6 +48,56 @@ def test_index_pickers_bit_exact_against_oracle():
                                                   draws=draws[:10]), ends[:10])
 
 
+def test_exponential_index_draws_at_thresholds_match_oracle():
+    """The device evaluates the exponential index picker from threshold tables
+    and falls back to the logarithm only near a threshold (expm1(i) /
+    expm1(len) below 710 groups, exp(-j) above).  Draws 1e-11 to 1e-5 away
+    from every threshold give the oracle's index bit-exactly.  Draws within
+    four ulps of one are decided by how log1p / log round a value that close
+    to an integer, where the device's libm and the C library's can differ by
+    an ulp (as the reference's CPU and GPU paths do): there the index may
+    differ by one, and only rarely."""
+    from temporal_random_walk import capi
+
+    L = _oracle()
+    far, near = [], []
+    for n in (1, 2, 3, 7, 50, 300, 708, 709):
+        i = np.arange(1, n + 1)
+        r0 = np.expm1(i.astype(np.float64)) / np.expm1(float(n))
+        for k in (-4, -1, 0, 1, 4):
+            near.append((r0 * (1.0 + k * 2.0 ** -52), np.full(i.size, n)))
+        for rel in (-1e-9, -1e-11, 1e-11, 1e-9):
+            far.append((r0 * (1.0 + rel), np.full(i.size, n)))
+    j = np.arange(0, 38, dtype=np.float64)
+    for n in (710, 5_000, 1 << 20, (1 << 31) - 1):
+        for rel in (-1e-5, -1e-9, 1e-9, 1e-5):
+            far.append((np.exp(-j) * (1.0 + rel), np.full(j.size, n)))
+        for rel in (-2.0 ** -50, 0.0, 2.0 ** -50):
+            near.append((np.exp(-j) * (1.0 + rel), np.full(j.size, n)))
+
+    def run(cases):
+        r = np.concatenate([c[0] for c in cases])
+        ends = np.concatenate([c[1] for c in cases]).astype(np.int32)
+        keep = (r >= 0.0) & (r < 1.0)
+        r, ends = r[keep], ends[keep]
+        starts = np.zeros(r.size, np.int32)
+        out = []
+        for pe in (True, False):
+            got = capi.pick_index("ExponentialIndex", starts, ends, prioritize_end=pe, draws=r)
+            want = np.array([L.orc_pick_exponential_index(0, int(e), int(pe), float(x))
+                             for e, x in zip(ends, r)], dtype=np.int32)
+            out.append((got, want, ends, r))
+        return out
+
+    for got, want, ends, r in run(far):
+        bad = np.nonzero(got != want)[0]
+        assert bad.size == 0, [(int(ends[b]), float(r[b]), int(got[b]), int(want[b]))
+                               for b in bad[:10]]
+    for got, want, ends, r in run(near):
+        assert np.all(np.abs(got.astype(np.int64) - want) <= 1)
+        assert np.count_nonzero(got != want) <= got.size // 100
+
+
 def test_weight_picker_bit_exact_against_oracle():
     from temporal_random_walk import capi
 
