@@ -348,6 +348,21 @@ __device__ Hop tn2v_pick(const WalkGraph& g, int prev, uint32_t vb, uint32_t ve,
     return last;
 }
 
+// The edge of the picked group gpos of a node whose groups end at ge
+// (edge_selectors.cuh:420-443): a uniform pick re within the group's range.
+// A weight pick one past the node's last group reads, in the reference, the
+// next node's first group start for both ends: an empty range.
+__device__ __forceinline__ Hop hop_from_group(const WalkGraph& g, uint32_t gpos, uint32_t ge,
+                                              double re) {
+    if (gpos >= ge) return no_hop();
+    const PanelPair pp = load_pair(g.d.pan + gpos);
+    const uint32_t es = pp.start, ee = pp.next_start;
+    if (es >= ee || es >= g.d.idx_size || ee > g.d.idx_size) return no_hop();
+    return hop_of(load_rec(g.d.rec + es +
+                           static_cast<uint32_t>(static_cast<int>(re * static_cast<int>(ee - es)))),
+                  pp.rank);
+}
+
 // Per-hop selector (edge_selectors.cuh:277-443).  The reference first checks
 // the dense active flag; an inactive node has no entries in either direction,
 // so the empty group range below rejects it identically without that load.
@@ -398,15 +413,7 @@ __device__ __forceinline__ Hop node_edge_from(const WalkGraph& g, int picker, ui
         if (p == -1) return no_hop();
         gpos = static_cast<uint32_t>(p);
     }
-    // A weight pick one past the node's last group reads, in the reference, the
-    // next node's first group start for both ends: an empty range.
-    if (gpos >= ge) return no_hop();
-    const PanelPair pp = load_pair(g.d.pan + gpos);
-    const uint32_t es = pp.start, ee = pp.next_start;
-    if (es >= ee || es >= g.d.idx_size || ee > g.d.idx_size) return no_hop();
-    return hop_of(load_rec(g.d.rec + es +
-                           static_cast<uint32_t>(static_cast<int>(re * static_cast<int>(ee - es)))),
-                  pp.rank);
+    return hop_from_group(g, gpos, ge, re);
 }
 
 template <bool Fwd, int Fam>
@@ -492,6 +499,231 @@ __device__ __forceinline__ uint64_t grid_position(int remap) {
     return b * static_cast<uint64_t>(kB) + threadIdx.x;
 }
 
+// ---- wave-cooperative weight search ---------------------------------------
+// A weight pick descends a 16-ary search index, one 16-entry block per level
+// (weight_lower_bound).  Read by its own lane, a block costs that lane eight
+// 16-byte accesses -- or sixteen 8-byte ones at the bottom level, whose block
+// need not be aligned -- and a wave of such lanes touches 64 lines per
+// access.  Shared by the wave, a block costs one access: in round j the 16
+// lanes of each quarter of the wave read one entry each of the block of the
+// quarter's lane j, and one ballot counts the four blocks of the round.
+
+// Number of the first lim (<= 16) entries of blk below target, for every lane
+// with need (0 for the others).  All lanes of the wave call it together;
+// safe is a readable address for lanes without a request.
+__device__ __forceinline__ uint32_t wave_count_below16(bool need, const double* blk,
+                                                       uint32_t lim, double target,
+                                                       const double* safe) {
+    if (__ballot(need) == 0) return 0;  // uniform: no request in the wave
+    const int lane = __lane_id();
+    const int sub = lane & 15, qbase = lane & 48;
+    const long long bp = reinterpret_cast<long long>(need ? blk : safe);
+    const int ln = need ? static_cast<int>(lim) : 0;
+    uint32_t mine = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int src = qbase | j;
+        const double* b = reinterpret_cast<const double*>(__shfl(bp, src));
+        const double t = __shfl(target, src);
+        const int l = __shfl(ln, src);
+        // every lane loads (entry 0 past the limit) so the rounds' loads need
+        // no branch and can all be in flight together
+        const double v = b[sub < l ? sub : 0];
+        const uint64_t m = __ballot(sub < l && v < t);
+        const uint32_t c = static_cast<uint32_t>(__popcll((m >> qbase) & 0xffffull));
+        mine = sub == j ? c : mine;
+    }
+    return mine;
+}
+
+// weight_lower_bound for every lane with need, the wave sharing each level's
+// block reads: the same descent, one wave_count_below16 per level.  A segment
+// of at most kWIdxMin weights is one block.  All lanes of the wave call it
+// together.
+__device__ __forceinline__ uint32_t wave_weight_lower_bound(bool need, const double* w, uint32_t G,
+                                                            const double* lv, double target,
+                                                            const double* safe) {
+    const bool indexed = need && G > kWIdxMin;
+    uint32_t res = 0;
+    bool pending = need;
+    if (indexed && lv == nullptr) {  // no index was built: the lane searches alone
+        res = weight_lower_bound(w, G, nullptr, target);
+        pending = false;
+    }
+    // state 0: the top level; 1: a lower index level; 2: the weights themselves
+    int state = indexed ? 0 : 2;
+    uint64_t span = indexed ? wx_top_span(G) : 0;
+    uint32_t n = indexed ? wx_level_entries(G, span) : 0;
+    const double* A = lv;
+    uint32_t b = 0;
+    while (__any(pending)) {
+        const double* blk = safe;
+        uint32_t lim = 0;
+        if (pending) {
+            blk = state == 2 ? w + b : A + b;
+            lim = state == 2 ? (G - b < 16u ? G - b : 16u) : 16u;
+        }
+        const uint32_t k = wave_count_below16(pending, blk, lim, target, safe);
+        if (pending) {
+            if (state == 2) {
+                res = b + k;
+                pending = false;
+            } else if (state == 0 && k == 0) {
+                res = 0;
+                pending = false;
+            } else {
+                const uint32_t c = b + k;  // entries of this level below target
+                if (span > 16) {
+                    A += wx_pad16(n);
+                    span >>= 4;
+                    n = wx_level_entries(G, span);
+                    state = 1;
+                } else {
+                    state = 2;
+                }
+                b = (c - 1) * 16;
+            }
+        }
+    }
+    return res;
+}
+
+// A weight-family hop up to its weight search.
+struct WeightHop {
+    bool fail;        // no hop
+    bool need;        // waits for the weight search over [gb, gb + G)
+    uint32_t gpos;    // the picked group (index pickers)
+    uint32_t gb, G;   // the node's groups
+    uint32_t gs, gse; // the valid slice [gs, gse)
+    uint32_t ge;      // the node's group end
+    const double* lv;
+    double target;
+};
+
+// node_edge_from's selection for the weight family (ExponentialWeight or an
+// index picker), stopping where pick_weights would search.
+template <bool Fwd>
+__device__ __forceinline__ WeightHop weight_hop_begin(const WalkGraph& g, int picker, uint32_t u,
+                                                      bool ok, const NodeHdr& h, int32_t t,
+                                                      int32_t cut, double rg, const double* em1) {
+    WeightHop s{true, false, 0, 0, 0, 0, 0, 0, nullptr, 0.0};
+    uint32_t Gu = ok ? (h.meta & kHdrGMask) : 0u;
+    if (Gu == kHdrGMask) Gu = g.d.hdr[u + 1].gb - h.gb;
+    if (Gu == 0) return s;
+    const uint32_t gb = h.gb, ge = gb + Gu;
+    const int G = static_cast<int>(Gu);
+    const PanelRec* fts = g.d.pan + gb;
+    int vb = 0, ve = G;
+    if (t != -1) {
+        const uint32_t x = static_cast<uint32_t>(t);
+        if (Fwd) vb = first_ge(g.d.tab, h, u, G, fts, x + 1);
+        else ve = first_ge(g.d.tab, h, u, G, fts, x);
+    }
+    if (cut != -1) {
+        const int c = first_ge(g.d.tab, h, u, G, fts, static_cast<uint32_t>(cut));
+        ve = c < vb ? vb : (c < ve ? c : ve);
+    }
+    if (vb >= ve) return s;
+    s.ge = ge;
+    if (is_index_picker(picker)) {
+        const int avail = ve - vb;
+        const int index = pick_index(picker, 0, avail, !Fwd, rg, em1);
+        if (index == -1 || index >= avail) return s;
+        s.gpos = gb + static_cast<uint32_t>(vb + index);
+        s.fail = false;
+        return s;
+    }
+    if (picker != kExponentialWeight) return s;
+    // pick_weights up to its search
+    const uint64_t gs = gb + vb, gse = gb + ve;
+    if (gs >= gse || gse > g.d.w_size) return s;
+    const double start_sum = gs > gb ? g.d.w[gs - 1] : 0.0;
+    const double end_sum = g.d.w[gse - 1];
+    if (end_sum < start_sum) return s;
+    s.target = start_sum + rg * (end_sum - start_sum);
+    s.lv = (g.d.wx && G > static_cast<int>(kWIdxMin)) ? g.d.wx + g.d.wx_off[u] : nullptr;
+    s.gb = gb;
+    s.G = Gu;
+    s.gs = static_cast<uint32_t>(gs);
+    s.gse = static_cast<uint32_t>(gse);
+    s.need = true;
+    s.fail = false;
+    return s;
+}
+
+// The walk loop of walk_kernel for the weight family, with the weight search
+// shared by the wave: a lane whose walk has ended (or that has no walk) keeps
+// taking part until every walk of its wave has, so the loop's control is
+// wave-uniform around the shared search.  Same walks as walk_kernel's loop.
+template <bool Fwd>
+__device__ __forceinline__ void walk_wave_weights(const WalkGraph& g, const WalkArgs& a,
+                                                  const double* em1) {
+    const uint64_t q = a.q0 + grid_position(a.xcd_remap);
+    const bool in_range = q < a.q_end;
+    const uint64_t w = in_range ? (a.order ? a.order[q] : q) : 0;
+    const int L = a.L;  // >= 1 (the caller returned for L == 0)
+    constexpr uint64_t n = kScratchTile;
+    const uint64_t tile = q / kScratchTile, lane = q % kScratchTile;
+    int32_t* wn = a.nodes + tile * kScratchTile * static_cast<uint64_t>(L) + lane;
+    uint32_t* wt = a.ranks + tile * kScratchTile * static_cast<uint64_t>(L) + lane;
+    uint32_t* we = a.eids + tile * kScratchTile * static_cast<uint64_t>(L - 1) + lane;
+    const int32_t cut = in_range ? cutoff_rank(g, a, w) : -1;
+    const int32_t neg1 = *g.neg1_rank;
+    const StartState s0 = in_range ? a.st[w] : StartState{-1, -1, -1, -1};
+    int cur = s0.cur;
+    int32_t cur_r = s0.r, cur_e = s0.e;
+    int len = 0, walk_len = 1;
+    bool active = in_range && cur_e != -1;
+    if (active) {
+        store_out(wn, s0.first);
+        store_out(wt, kStartRank);
+        len = 1;
+    }
+    active = active && walk_len < L && cur != a.pad;
+    while (__any(active)) {
+        WeightHop hs{true, false, 0, 0, 0, 0, 0, 0, nullptr, 0.0};
+        double re = 0.0;
+        if (active) {
+            store_out(wn + len * n, cur);
+            store_out(wt + len * n, static_cast<uint32_t>(cur_r));
+            store_out(we + (len - 1) * n, static_cast<uint32_t>(cur_e));
+            ++len;
+            if (walk_len == L - 1) {
+                active = false;  // the reference's last selection cannot change the output
+            } else {
+                const bool ok = cur >= 0 && cur < g.active_size;
+                const uint32_t u = ok ? static_cast<uint32_t>(cur) : 0u;
+                const NodeHdr hd = g.d.hdr[u];
+                const DrawPair r = draw_pair(a.ds, w, static_cast<uint32_t>(walk_len) + 1);
+                hs = weight_hop_begin<Fwd>(g, a.walk_bias, u, ok, hd, cur_r == neg1 ? -1 : cur_r,
+                                           cut, r.a, em1);
+                re = r.b;
+                if (hs.fail) active = false;
+            }
+        }
+        const uint32_t k = wave_weight_lower_bound(hs.need, g.d.w + hs.gb, hs.G, hs.lv, hs.target,
+                                                   g.d.w);
+        if (active) {
+            uint32_t gpos = hs.gpos;
+            if (hs.need) {
+                const uint32_t x = hs.gb + k;
+                gpos = x < hs.gs ? hs.gs : (x > hs.gse ? hs.gse : x);
+            }
+            const Hop h = hop_from_group(g, gpos, hs.ge, re);
+            if (h.e == -1 || h.r == neg1) {
+                active = false;
+            } else {
+                cur = h.nbr;
+                cur_r = h.r;
+                cur_e = h.e;
+                ++walk_len;
+                active = walk_len < L && cur != a.pad;
+            }
+        }
+    }
+    if (in_range) a.lens[w] = static_cast<uint64_t>(len);
+}
+
 template <bool Fwd, bool Dir, int Fam>
 __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
     // the exponential index picker's thresholds (expm1 of every length it
@@ -503,6 +735,12 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
         __syncthreads();
     }
     const double* em1 = use_xt ? s_xt : nullptr;
+    if constexpr (Fam == kFamWeight) {
+        if (a.L > 0) {  // uniform
+            walk_wave_weights<Fwd>(g, a, em1);
+            return;
+        }
+    }
     const uint64_t q = a.q0 + grid_position(a.xcd_remap);
     if (q >= a.q_end) return;
     const uint64_t w = a.order ? a.order[q] : q;

@@ -179,6 +179,38 @@ def test_replay_walks_weight_pickers(directed, forward, picker):
     _walk_case(og, eng, picker, picker, forward, "all_nodes", 12, 1, seed=5)
 
 
+@pytest.mark.parametrize("directed", [True, False])
+def test_replay_walks_exponential_weight_deep_search_index(directed):
+    """ExponentialWeight walks through a hub of 300k timestamp groups: its
+    weight search index has five levels above the weights, searched by the
+    wave together.  Walks of every length end at different hops, so waves
+    keep lanes with ended walks in the shared search.  Walk-picker index
+    families mixed with weight starts go through the same loop."""
+    rng = np.random.default_rng(71)
+    g = 300_000
+    hub_t = rng.permutation(g).astype(np.int64) * 3
+    hub_d = rng.integers(1, 3_000, g).astype(np.int32)
+    n_o = 150_000
+    s_o = rng.integers(1, 3_000, n_o).astype(np.int32)
+    d_o = np.where(rng.random(n_o) < 0.4, 0, rng.integers(1, 3_000, n_o)).astype(np.int32)
+    t_o = rng.integers(0, 3 * g, n_o).astype(np.int64)
+    s = np.concatenate([np.zeros(g, np.int32), s_o])
+    d = np.concatenate([hub_d, d_o])
+    t = np.concatenate([hub_t, t_o])
+    og, eng = _pair(directed, [(s, d, t)], weights=True, timescale_bound=30.0)
+    _assert_index_equal(og, eng, weights=True)
+    for name in WEIGHT_ARRAYS:
+        w = eng.array(name)
+        if w.size:
+            og.set_weights(name, w)
+    for forward in (True, False):
+        _walk_case(og, eng, "ExponentialWeight", "ExponentialWeight", forward, "total", 30,
+                   6_000, seed=72)
+        _walk_case(og, eng, "ExponentialWeight", "Uniform", forward, "nodes", 20, 400,
+                   seed_nodes=np.array([0, 7, 11], np.int32), seed=73)
+        _walk_case(og, eng, "Linear", "ExponentialWeight", forward, "total", 12, 3_000, seed=74)
+
+
 def test_replay_walks_powerlaw_exponential_index():
     s, d, t = graphs.powerlaw(100_000, 400_000, s=1.8, n_ts=5_000, seed=44)
     og, eng = _pair(True, [(s, d, t)])
