@@ -434,6 +434,21 @@ __global__ void adj_offsets_kernel(const uint64_t* __restrict__ keys, size_t n, 
     off[u] = static_cast<uint32_t>(lo);
 }
 
+// One slot of the adjacency pair set per distinct sorted key (linear probing;
+// the set is at most half full, so every probe sequence reaches a free slot).
+__global__ void adj_hash_insert_kernel(const uint64_t* __restrict__ keys, size_t n, int shift,
+                                       uint64_t mask, uint64_t* __restrict__ tab) {
+    const size_t i = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (i >= n) return;
+    const uint64_t k = keys[i];
+    if (i > 0 && keys[i - 1] == k) return;  // a repeated pair
+    uint64_t h = (k * kAdjHashMul) >> shift;
+    while (atomicCAS(reinterpret_cast<unsigned long long*>(tab + h),
+                     static_cast<unsigned long long>(kAdjEmpty),
+                     static_cast<unsigned long long>(k)) != kAdjEmpty)
+        h = (h + 1) & mask;
+}
+
 // Global per-timestamp-group weights before normalisation
 // (edge_data.cu:477-492).
 __global__ void global_weights_kernel(const uint32_t* __restrict__ off,
@@ -1046,6 +1061,18 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
         adj_off.resize(v + 1);
         hipLaunchKernelGGL(adj_offsets_kernel, dim3(grid_for(v + 1)), dim3(kB), 0, s, ak, m2, b,
                            v + 1, adj_off.p);
+        // the walks' membership tests (is a candidate adjacent to the previous
+        // node?) probe a hash set of the pairs instead of binary-searching a
+        // hub's list of millions of neighbours
+        int lg = 10;
+        while ((size_t{1} << lg) < 2 * m2) ++lg;
+        adj_hash.resize(size_t{1} << lg);
+        check_hip(hipMemsetAsync(adj_hash.p, 0xff, (size_t{1} << lg) * sizeof(uint64_t), s),
+                  "adjacency set clear");
+        hipLaunchKernelGGL(adj_hash_insert_kernel, dim3(grid_for(m2)), dim3(kB), 0, s, ak, m2,
+                           64 - lg, (uint64_t{1} << lg) - 1, adj_hash.p);
+        adj_hash_log = lg;
+        adj_bits = b;
         check_hip(hipGetLastError(), "adjacency launch");
         adj_ready = true;
     }
@@ -1112,7 +1139,7 @@ void Engine::clear() {
     max_node_id = -1;
     store_tmin = store_tmax = 0;
     src.n = dst.n = ts.n = feat.n = tsg_off.n = uniq_ts.n = erank.n = neg1_rank.n = active.n = 0;
-    fwd_cum.n = bwd_cum.n = gwx_fwd.n = gwx_bwd.n = adj_off.n = adj_nbr.n = 0;
+    fwd_cum.n = bwd_cum.n = gwx_fwd.n = gwx_bwd.n = adj_off.n = adj_nbr.n = adj_hash.n = 0;
     weights_ready = adj_ready = false;
     out.clear();
     in.clear();

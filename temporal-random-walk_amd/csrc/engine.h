@@ -43,7 +43,8 @@
 //                                  blocks; top level first
 //   global weights  fwd_cum, bwd_cum fp64[T] (+ gwx_fwd, gwx_bwd: their
 //                   search index, one segment of T)
-//   node2vec        adj_off uint32[max_id+2], adj_nbr int32[2E]
+//   node2vec        adj_off uint32[max_id+2], adj_nbr int32[2E],
+//                   adj_hash uint64[2^k >= 4E] (pair membership set)
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -125,6 +126,11 @@ static_assert(sizeof(EdgeRec) == 8, "EdgeRec must be 8 bytes");
 // Cumulative-weight segments longer than this get a search index (levels of
 // every 16^k-th value); shorter ones are binary-searched directly.
 constexpr uint32_t kWIdxMin = 16;
+
+// Adjacency pair set: an empty slot, and the multiplier of its Fibonacci
+// hash (slot = key * kAdjHashMul >> (64 - log2 slots)).
+constexpr uint64_t kAdjEmpty = ~0ull;
+constexpr uint64_t kAdjHashMul = 0x9E3779B97F4A7C15ull;
 
 // Geometry of the weight search index of a segment of G cumulative weights:
 // level k has ceil(G / 16^k) entries; the top level K is the first with at
@@ -267,6 +273,11 @@ struct Engine {
     // node2vec adjacency
     DBuf<uint32_t> adj_off;
     DBuf<int32_t> adj_nbr;
+    // membership set of the adjacency's (owner, neighbour) pairs: open
+    // addressing over 2^adj_hash_log slots, key owner << adj_bits | neighbour
+    DBuf<uint64_t> adj_hash;
+    int adj_hash_log = 0;
+    int adj_bits = 0;
     bool adj_ready = false;
 
     DirIndex out, in;

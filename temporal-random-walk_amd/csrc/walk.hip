@@ -84,6 +84,9 @@ struct WalkGraph {
     const uint32_t* adj_off;
     const int32_t* adj_nbr;
     uint32_t adj_off_size;
+    const uint64_t* adj_hash;  // pair set (nullptr: search the lists)
+    uint64_t adj_mask;
+    int adj_shift, adj_bits;
     int tn2v;
     double inv_p, inv_q;
 };
@@ -302,6 +305,16 @@ __device__ Sel start_edge(const WalkGraph& g, int picker, double rg, double re) 
 __device__ __forceinline__ bool adjacent(const WalkGraph& g, int prev, int cand) {
     if (!g.tn2v || g.adj_off == nullptr) return false;
     if (prev < 0 || static_cast<uint32_t>(prev) + 1 >= g.adj_off_size) return false;
+    if (g.adj_hash) {
+        // cand is a stored node id (a record's neighbour), below 2^adj_bits
+        if (cand < 0) return false;
+        const uint64_t key = (static_cast<uint64_t>(prev) << g.adj_bits) | static_cast<uint32_t>(cand);
+        for (uint64_t h = (key * kAdjHashMul) >> g.adj_shift;; h = (h + 1) & g.adj_mask) {
+            const uint64_t v = g.adj_hash[h];
+            if (v == key) return true;
+            if (v == kAdjEmpty) return false;
+        }
+    }
     uint32_t lo = g.adj_off[prev];
     const uint32_t end = g.adj_off[prev + 1];
     uint32_t hi = end;
@@ -1368,6 +1381,10 @@ void Engine::sample(const trw_sample_params& p) {
     g.adj_off = adj_ready ? adj_off.p : nullptr;
     g.adj_nbr = adj_nbr.p;
     g.adj_off_size = adj_ready ? static_cast<uint32_t>(adj_off.n) : 0;
+    g.adj_hash = adj_ready && adj_hash.n ? adj_hash.p : nullptr;
+    g.adj_mask = adj_hash.n ? adj_hash.n - 1 : 0;
+    g.adj_shift = 64 - adj_hash_log;
+    g.adj_bits = adj_bits;
     g.tn2v = cfg.enable_temporal_node2vec;
     g.inv_p = 1.0 / cfg.node2vec_p;
     g.inv_q = 1.0 / cfg.node2vec_q;
