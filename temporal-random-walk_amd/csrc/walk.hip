@@ -864,10 +864,16 @@ struct LayoutArgs {
     int64_t start_ts;
     const uint32_t* order;  // walk of each scratch column (nullptr: the column index)
     uint64_t q0, q_end;     // scratch columns [q0, q_end) of this launch (q0 % 64 == 0)
+    // edge features of the edge-id slots (fv = feature_dim / 4 vectors per
+    // slot; 0: written by a separate gather)
+    const float* feat;
+    float* of;
+    uint32_t fv;
 };
 
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef int64_t i64x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // Value of output slot i of a row whose first `cw` slots were written (x: the
 // scratch value).  Arr 0: nodes, 1: timestamps, 2: edge ids.
@@ -951,6 +957,22 @@ __device__ __forceinline__ void layout_array(const LayoutArgs& a, uint32_t* tile
                 if (Arr == 0) __builtin_nontemporal_store(static_cast<int32_t>(y), a.on + base + i);
                 else if (Arr == 1) __builtin_nontemporal_store(y, a.ot + base + i);
                 else __builtin_nontemporal_store(y, a.oe + base + i);
+            }
+        }
+        if (Arr == 2 && a.fv) {
+            // the slots' edge features (finalize_host_walks,
+            // walks_with_edge_features_host.cuh:44-62), from the edge ids in
+            // the tile: row [slot][dim] of the walk, zeros past the count
+            const uint32_t fv = a.fv;
+            const f32x4* feat = reinterpret_cast<const f32x4*>(a.feat);
+            f32x4* of = reinterpret_cast<f32x4*>(a.of) + base * fv;
+            const uint32_t units = static_cast<uint32_t>(kc) * fv;
+            for (uint32_t t = lane; t < units; t += 64) {
+                const int i = static_cast<int>(t / fv);
+                const uint32_t c = t - static_cast<uint32_t>(i) * fv;
+                f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (i < cw) v = __builtin_nontemporal_load(feat + static_cast<uint64_t>(src(i)) * fv + c);
+                __builtin_nontemporal_store(v, of + t);
             }
         }
     }
@@ -1046,27 +1068,6 @@ __global__ void gather_walk_features_kernel(const int64_t* __restrict__ eids, ui
         const uint64_t slot = x / dim, c = x - slot * dim;
         const int64_t e = eids[slot];
         out[x] = e >= 0 ? feat[static_cast<uint64_t>(e) * dim + c] : 0.0f;
-    }
-}
-
-// Same, 16 bytes per work-item for rows of dim % 4 == 0 floats: a workgroup of
-// V * R threads (V = dim / 4 vectors per row, R = 256 / V rows) covers R
-// consecutive slots, grid-stride over slots; the output is written once, with
-// non-temporal stores.
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-__global__ __launch_bounds__(256) void gather_walk_features_vec_kernel(
-    const int64_t* __restrict__ eids, uint64_t slots, uint32_t V, const f32x4* __restrict__ feat,
-    f32x4* __restrict__ out) {
-    const uint32_t R = blockDim.x / V;
-    const uint32_t c = threadIdx.x % V, r = threadIdx.x / V;
-    if (r >= R) return;
-    for (uint64_t slot = blockIdx.x * static_cast<uint64_t>(R) + r; slot < slots;
-         slot += static_cast<uint64_t>(gridDim.x) * R) {
-        const int64_t e = eids[slot];
-        const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-        const f32x4 v = e >= 0 ? feat[static_cast<uint64_t>(e) * V + c] : zero;
-        __builtin_nontemporal_store(v, out + slot * V + c);
     }
 }
 
@@ -1488,6 +1489,15 @@ void Engine::sample(const trw_sample_params& p) {
         la.order = a.order;
         la.q0 = 0;
         la.q_end = nw;
+        // edge features of dim % 4 == 0 are written by the layout pass, from
+        // the edge ids it holds in LDS (device buffers are 256-byte aligned)
+        const bool fused_feat = feat_dim > 0 && eslots && feat_dim % 4 == 0;
+        if (fused_feat) {
+            w_feat.resize(eslots * feat_dim);
+            la.feat = feat.p;
+            la.of = w_feat.p;
+            la.fv = static_cast<uint32_t>(feat_dim / 4);
+        }
         const size_t lds = static_cast<size_t>(la.C) * (kLayoutWalks + 1) * sizeof(uint32_t) +
                            kLayoutWalks * (sizeof(int) + sizeof(uint32_t));
         const unsigned gx = static_cast<unsigned>((nw + kLayoutWalks - 1) / kLayoutWalks);
@@ -1495,22 +1505,16 @@ void Engine::sample(const trw_sample_params& p) {
         check_hip(hipGetLastError(), "layout launch");
     }
 
-    // ---- edge features of every walk slot (finalize_host_walks, on device)
+    // ---- edge features of every walk slot (finalize_host_walks, on device):
+    // other dims than multiples of 4 gather from the laid-out edge ids
     if (feat_dim > 0 && eslots) {
-        w_feat.resize(eslots * feat_dim);
-        const uint32_t V = static_cast<uint32_t>(feat_dim / 4);
-        if (feat_dim % 4 == 0 && V <= 256) {  // device buffers: 256-byte aligned
-            const uint32_t R = 256 / V;
-            const uint64_t blocks = std::min<uint64_t>((eslots + R - 1) / R, 65536);
-            hipLaunchKernelGGL(gather_walk_features_vec_kernel, dim3(blocks), dim3(V * R), 0, s,
-                               w_eids.p, eslots, V, reinterpret_cast<const f32x4*>(feat.p),
-                               reinterpret_cast<f32x4*>(w_feat.p));
-        } else {
+        if (feat_dim % 4 != 0) {
+            w_feat.resize(eslots * feat_dim);
             hipLaunchKernelGGL(gather_walk_features_kernel, dim3(grid_capped(eslots * feat_dim)),
                                dim3(kB), 0, s, w_eids.p, eslots, static_cast<uint32_t>(feat_dim),
                                feat.p, w_feat.p);
+            check_hip(hipGetLastError(), "feature gather launch");
         }
-        check_hip(hipGetLastError(), "feature gather launch");
     } else {
         w_feat.n = 0;
     }
