@@ -1,12 +1,13 @@
 // primitives.h -- device-wide scan and stable radix sort for the index build.
 //
 // Hand-written for CDNA4 (wave64): no rocPRIM / hipCUB.  The radix sort is a
-// classic LSD sort with three launches per 8-bit digit pass (tile histograms
-// plus digit totals, one workgroup per digit scanning its histogram row,
-// stable scatter).  Stable ranking inside
-// a tile uses wave-level multisplit: eight 64-lane ballots give every lane the
-// mask of lanes holding the same digit, so the in-row rank is a popcount and a
-// single leader lane per digit bumps the wave's LDS counter.  Waves own
+// classic LSD sort with three launches per digit pass (tile histograms plus
+// digit totals, one workgroup per digit scanning its histogram row, stable
+// scatter); a sort of B key bits takes the fewest passes of at most 10-bit
+// digits, the bits split evenly.  Stable ranking inside a tile uses wave-level
+// multisplit: one 64-lane ballot per digit bit gives every lane the mask of
+// lanes holding the same digit, so the in-row rank is a popcount and a single
+// leader lane per digit bumps the wave's LDS counter.  Waves own
 // consecutive rows of the tile, so the scatter keeps input order among equal
 // digits -- which is what makes the edge-store order "stable by (timestamp,
 // insertion position)" and the node index "stable by (node, position)".

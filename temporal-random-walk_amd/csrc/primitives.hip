@@ -165,29 +165,28 @@ void scan_impl(const T* in, T* out, size_t n, T* scratch, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
-// radix sort: 8-bit digits, tile = 4 waves x 8 rows x 64 keys = 2048 keys; a
+// radix sort: a sort of B key bits takes the fewest passes of at most
+// kMaxDigitBits bits, the bits split evenly (27 bits: three 9-bit passes, 20
+// bits: two 10-bit passes); tile = 4 waves x 8 rows x 64 keys = 2048 keys; a
 // workgroup owns kTilesPerBlock consecutive tiles, so the digit-major
 // histogram has one column per workgroup (fewer scattered histogram writes and
 // a shorter histogram scan per pass)
 // ---------------------------------------------------------------------------
-constexpr int kRadixBits = 8;
-constexpr int kRadix = 1 << kRadixBits;
+constexpr int kMaxDigitBits = 10;
+constexpr int kMaxRadix = 1 << kMaxDigitBits;
 constexpr int kRows = 8;
 constexpr size_t kSortTile = static_cast<size_t>(kBlock) * kRows;
 constexpr int kTilesPerBlock = 4;
 constexpr size_t kSortSpan = kSortTile * kTilesPerBlock;
 
-static_assert(kRadix == kBlock, "one thread per digit in the tile epilogue");
-
 __device__ __forceinline__ uint64_t lanes_below(int lane) {
     return lane == 0 ? 0ull : (~0ull >> (64 - lane));
 }
 
-// Mask of the valid lanes of this wave whose digit equals mine.
-__device__ __forceinline__ uint64_t match_digit(uint32_t d, bool valid) {
+// Mask of the valid lanes of this wave whose digit (of db bits) equals mine.
+__device__ __forceinline__ uint64_t match_digit(uint32_t d, bool valid, int db) {
     uint64_t m = __ballot(valid);
-#pragma unroll
-    for (int b = 0; b < kRadixBits; ++b) {
+    for (int b = 0; b < db; ++b) {
         const bool bit = (d >> b) & 1u;
         const uint64_t vote = __ballot(bit);
         m &= bit ? vote : ~vote;
@@ -195,15 +194,20 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t d, bool valid) {
     return m;
 }
 
+// Per-workgroup digit counts of keys[...] >> bit (db-bit digits, the digit
+// masked to dmask), digit-major into hist, and the digit totals.  Dynamic
+// LDS: kWaves << db counters.
 template <typename K>
 __global__ __launch_bounds__(kBlock) void radix_upsweep_kernel(const K* __restrict__ keys,
-                                                               size_t n, int bit,
+                                                               size_t n, int bit, int db,
+                                                               uint32_t dmask,
                                                                uint32_t* __restrict__ hist,
                                                                size_t nb,
                                                                uint32_t* __restrict__ digit_tot) {
-    __shared__ uint32_t s_cnt[kWaves][kRadix];
+    extern __shared__ uint32_t s_cnt[];  // [kWaves][R]
+    const int R = 1 << db;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (int i = threadIdx.x; i < kWaves * kRadix; i += kBlock) (&s_cnt[0][0])[i] = 0;
+    for (int i = threadIdx.x; i < kWaves * R; i += kBlock) s_cnt[i] = 0;
     __syncthreads();
     for (int t = 0; t < kTilesPerBlock; ++t) {
         const size_t wave_base = blockIdx.x * kSortSpan + t * kSortTile +
@@ -219,18 +223,19 @@ __global__ __launch_bounds__(kBlock) void radix_upsweep_kernel(const K* __restri
         for (int r = 0; r < kRows; ++r) {
             const size_t i = wave_base + static_cast<size_t>(r) * 64 + lane;
             const bool valid = i < n;
-            const uint32_t d = static_cast<uint32_t>((key[r] >> bit) & (kRadix - 1));
-            const uint64_t m = match_digit(d, valid);
-            if (valid && (m & lanes_below(lane)) == 0) s_cnt[wave][d] += __popcll(m);
+            const uint32_t d = static_cast<uint32_t>(key[r] >> bit) & dmask;
+            const uint64_t m = match_digit(d, valid, db);
+            if (valid && (m & lanes_below(lane)) == 0) s_cnt[wave * R + d] += __popcll(m);
         }
     }
     __syncthreads();
-    const int d = threadIdx.x;
-    uint32_t tot = 0;
+    for (int d = threadIdx.x; d < R; d += kBlock) {
+        uint32_t tot = 0;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) tot += s_cnt[w][d];
-    hist[static_cast<size_t>(d) * nb + blockIdx.x] = tot;
-    if (tot) atomicAdd(digit_tot + d, tot);
+        for (int w = 0; w < kWaves; ++w) tot += s_cnt[w * R + d];
+        hist[static_cast<size_t>(d) * nb + blockIdx.x] = tot;
+        if (tot) atomicAdd(digit_tot + d, tot);
+    }
 }
 
 // One workgroup per digit d: the exclusive scan of the workgroups' counts of
@@ -241,8 +246,9 @@ __global__ __launch_bounds__(kBlock) void radix_offsets_kernel(uint32_t* __restr
                                                                const uint32_t* __restrict__ digit_tot) {
     __shared__ uint32_t s_wave[kWaves];
     const int d = blockIdx.x;
-    uint32_t carry = block_sum<uint32_t, OpSum>(
-        threadIdx.x < static_cast<unsigned>(d) ? digit_tot[threadIdx.x] : 0u, s_wave);
+    uint32_t below = 0;
+    for (int i = threadIdx.x; i < d; i += kBlock) below += digit_tot[i];
+    uint32_t carry = block_sum<uint32_t, OpSum>(below, s_wave);
     __syncthreads();
     uint32_t* row = hist + static_cast<size_t>(d) * nb;
     for (size_t chunk = 0; chunk < nb; chunk += kScanTile) {
@@ -273,19 +279,24 @@ __global__ void fill_u32_kernel(uint32_t* __restrict__ p, size_t n, uint32_t v) 
     if (i < n) p[i] = v;
 }
 
+// Stable scatter of one digit pass.  Dynamic LDS: kWaves << db counters, then
+// 1 << db running positions.
 template <typename K, typename V>
 __global__ __launch_bounds__(kBlock) void radix_scatter_kernel(
     const K* __restrict__ keys_in, const V* __restrict__ vals_in, K* __restrict__ keys_out,
-    V* __restrict__ vals_out, size_t n, int bit, const uint32_t* __restrict__ offsets,
-    size_t nb) {
-    __shared__ uint32_t s_cnt[kWaves][kRadix];
-    __shared__ uint32_t s_run[kRadix];  // the workgroup's next output position per digit
+    V* __restrict__ vals_out, size_t n, int bit, int db, uint32_t dmask,
+    const uint32_t* __restrict__ offsets, size_t nb) {
+    extern __shared__ uint32_t s_lds[];
+    const int R = 1 << db;
+    uint32_t* s_cnt = s_lds;           // [kWaves][R]
+    uint32_t* s_run = s_lds + kWaves * R;  // the workgroup's next output position per digit
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    s_run[threadIdx.x] = offsets[static_cast<size_t>(threadIdx.x) * nb + blockIdx.x];
+    for (int d = threadIdx.x; d < R; d += kBlock)
+        s_run[d] = offsets[static_cast<size_t>(d) * nb + blockIdx.x];
     for (int t = 0; t < kTilesPerBlock; ++t) {
         const size_t tile_base = blockIdx.x * kSortSpan + t * kSortTile;
         if (tile_base >= n) break;  // uniform over the workgroup
-        for (int i = threadIdx.x; i < kWaves * kRadix; i += kBlock) (&s_cnt[0][0])[i] = 0;
+        for (int i = threadIdx.x; i < kWaves * R; i += kBlock) s_cnt[i] = 0;
         __syncthreads();
         const size_t wave_base = tile_base + static_cast<size_t>(wave) * kRows * 64;
         K key[kRows];
@@ -303,24 +314,23 @@ __global__ __launch_bounds__(kBlock) void radix_scatter_kernel(
         for (int r = 0; r < kRows; ++r) {
             const size_t i = wave_base + static_cast<size_t>(r) * 64 + lane;
             const bool valid = i < n;
-            const uint32_t d = static_cast<uint32_t>((key[r] >> bit) & (kRadix - 1));
+            const uint32_t d = static_cast<uint32_t>(key[r] >> bit) & dmask;
             dig[r] = d;
-            const uint64_t m = match_digit(d, valid);
+            const uint64_t m = match_digit(d, valid, db);
             const uint32_t before = __popcll(m & lanes_below(lane));
-            const uint32_t prior = s_cnt[wave][d];
+            const uint32_t prior = s_cnt[wave * R + d];
             rank[r] = prior + before;
-            if (valid && before == 0) s_cnt[wave][d] = prior + __popcll(m);
+            if (valid && before == 0) s_cnt[wave * R + d] = prior + __popcll(m);
         }
         __syncthreads();
-        {
-            // tile epilogue: wave-major exclusive offsets of every digit, then
-            // the running position moves past this tile's keys of the digit
-            const int d = threadIdx.x;
+        // tile epilogue: wave-major exclusive offsets of every digit, then the
+        // running position moves past this tile's keys of the digit
+        for (int d = threadIdx.x; d < R; d += kBlock) {
             uint32_t run = s_run[d];
 #pragma unroll
             for (int w = 0; w < kWaves; ++w) {
-                const uint32_t c = s_cnt[w][d];
-                s_cnt[w][d] = run;
+                const uint32_t c = s_cnt[w * R + d];
+                s_cnt[w * R + d] = run;
                 run += c;
             }
             s_run[d] = run;
@@ -330,7 +340,7 @@ __global__ __launch_bounds__(kBlock) void radix_scatter_kernel(
         for (int r = 0; r < kRows; ++r) {
             const size_t i = wave_base + static_cast<size_t>(r) * 64 + lane;
             if (i < n) {
-                const uint32_t pos = s_cnt[wave][dig[r]] + rank[r];
+                const uint32_t pos = s_cnt[wave * R + dig[r]] + rank[r];
                 keys_out[pos] = key[r];
                 if (vals_out) vals_out[pos] = val[r];
             }
@@ -339,28 +349,45 @@ __global__ __launch_bounds__(kBlock) void radix_scatter_kernel(
     }
 }
 
-// hist layout: nb * kRadix per-workgroup counts, then kMaxPasses * kRadix
-// digit totals (one row per pass, cleared once per sort).
-constexpr int kMaxPasses = 64 / kRadixBits;
+// hist layout: nb * kMaxRadix per-workgroup counts, then kMaxPasses *
+// kMaxRadix digit totals (one row per pass, cleared once per sort).
+constexpr int kMaxPasses = (64 + kMaxDigitBits - 1) / kMaxDigitBits;
+
+// Passes and digit width of a sort of `bits` key bits.
+int sort_passes(int bits) { return (bits + kMaxDigitBits - 1) / kMaxDigitBits; }
+int sort_digit_bits(int bits) {
+    const int p = sort_passes(bits);
+    return (bits + p - 1) / p;
+}
 
 template <typename K, typename V = uint32_t>
 int radix_sort_impl(K* keys0, V* vals0, K* keys1, V* vals1, size_t n,
                     int begin_bit, int end_bit, uint32_t* hist, hipStream_t s) {
     if (n <= 1 || end_bit <= begin_bit) return 0;
     const size_t nb = (n + kSortSpan - 1) / kSortSpan;
-    uint32_t* totals = hist + nb * kRadix;
-    hipLaunchKernelGGL(fill_u32_kernel, dim3((kMaxPasses * kRadix + kBlock - 1) / kBlock),
-                       dim3(kBlock), 0, s, totals, static_cast<size_t>(kMaxPasses * kRadix), 0u);
-    int cur = 0, pass = 0;
+    const int passes = sort_passes(end_bit - begin_bit);
+    const int db = sort_digit_bits(end_bit - begin_bit);
+    const int R = 1 << db;
+    uint32_t* totals = hist + nb * kMaxRadix;
+    hipLaunchKernelGGL(fill_u32_kernel, dim3((passes * R + kBlock - 1) / kBlock), dim3(kBlock), 0,
+                       s, totals, static_cast<size_t>(passes * R), 0u);
+    const size_t lds_up = static_cast<size_t>(kWaves) * R * sizeof(uint32_t);
+    const size_t lds_sc = lds_up + static_cast<size_t>(R) * sizeof(uint32_t);
+    int cur = 0;
     K* kb[2] = {keys0, keys1};
     V* vb[2] = {vals0, vals1};
-    for (int bit = begin_bit; bit < end_bit; bit += kRadixBits, ++pass) {
-        uint32_t* tot = totals + pass * kRadix;
-        hipLaunchKernelGGL((radix_upsweep_kernel<K>), dim3(nb), dim3(kBlock), 0, s, kb[cur], n,
-                           bit, hist, nb, tot);
-        hipLaunchKernelGGL(radix_offsets_kernel, dim3(kRadix), dim3(kBlock), 0, s, hist, nb, tot);
-        hipLaunchKernelGGL((radix_scatter_kernel<K, V>), dim3(nb), dim3(kBlock), 0, s, kb[cur],
-                           vb[cur], kb[cur ^ 1], vb[cur ^ 1], n, bit, hist, nb);
+    for (int pass = 0; pass < passes; ++pass) {
+        const int bit = begin_bit + pass * db;
+        // the last digit stops at end_bit
+        const int w = end_bit - bit < db ? end_bit - bit : db;
+        const uint32_t dmask = (1u << w) - 1u;
+        uint32_t* tot = totals + pass * R;
+        hipLaunchKernelGGL((radix_upsweep_kernel<K>), dim3(nb), dim3(kBlock), lds_up, s, kb[cur],
+                           n, bit, db, dmask, hist, nb, tot);
+        hipLaunchKernelGGL(radix_offsets_kernel, dim3(R), dim3(kBlock), 0, s, hist, nb, tot);
+        hipLaunchKernelGGL((radix_scatter_kernel<K, V>), dim3(nb), dim3(kBlock), lds_sc, s,
+                           kb[cur], vb[cur], kb[cur ^ 1], vb[cur ^ 1], n, bit, db, dmask, hist,
+                           nb);
         check_hip(hipGetLastError(), "radix sort launch");
         cur ^= 1;
     }
@@ -474,7 +501,7 @@ int reduce_blocks(size_t n) {
 
 size_t scan_scratch_elems(size_t n) { return (n + kScanTile - 1) / kScanTile + 1; }
 size_t radix_hist_elems(size_t n) {
-    return ((n + kSortSpan - 1) / kSortSpan) * kRadix + kMaxPasses * kRadix;
+    return ((n + kSortSpan - 1) / kSortSpan) * kMaxRadix + kMaxPasses * kMaxRadix;
 }
 
 void exclusive_scan_u32(const uint32_t* in, uint32_t* out, size_t n, uint32_t* scratch,
@@ -511,7 +538,7 @@ int radix_sort_u32_v64(uint32_t* keys0, uint64_t* vals0, uint32_t* keys1, uint64
                                                hist, s);
 }
 int radix_passes(int begin_bit, int end_bit) {
-    return end_bit > begin_bit ? (end_bit - begin_bit + kRadixBits - 1) / kRadixBits : 0;
+    return end_bit > begin_bit ? sort_passes(end_bit - begin_bit) : 0;
 }
 
 // Scratch for the reductions lives in a small per-call static device buffer
