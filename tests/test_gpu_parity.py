@@ -294,6 +294,37 @@ def test_replay_walks_bursty_hubs_with_cutoffs(forward, picker):
                seed=12)
 
 
+@pytest.mark.parametrize("forward", [True, False])
+@pytest.mark.parametrize("picker", ["ExponentialIndex", "Uniform"])
+def test_replay_walks_dense_hubs_with_cutoffs(forward, picker):
+    """Hubs with a group at every timestamp rank of their span (their time
+    search answers from the rank, with no table) inside a graph whose other
+    edges reach before and after those spans, so the searched rank falls
+    before, inside and past a dense span; per-walk cutoffs bound it again."""
+    rng = np.random.default_rng(23)
+    T = 4_000
+    hubs = []
+    for hub, (lo, hi) in enumerate([(1_000, 3_000), (0, 2_500), (1_800, 4_000)]):
+        span = np.arange(lo, hi, dtype=np.int64)
+        extra = rng.integers(lo, hi, (hi - lo) // 2)  # repeated ranks: groups of 2+
+        ts = np.concatenate([span, extra])
+        hubs.append((np.full(ts.size, hub, np.int32), rng.integers(3, 600, ts.size).astype(np.int32), ts))
+    n_o = 40_000
+    s_o = rng.integers(3, 600, n_o).astype(np.int32)
+    d_o = np.where(rng.random(n_o) < 0.5, rng.integers(0, 3, n_o),
+                   rng.integers(3, 600, n_o)).astype(np.int32)
+    t_o = rng.integers(0, T, n_o).astype(np.int64)
+    s = np.concatenate([h[0] for h in hubs] + [s_o])
+    d = np.concatenate([h[1] for h in hubs] + [d_o])
+    t = np.concatenate([h[2] for h in hubs] + [t_o]) * 7  # distinct timestamps, not ranks
+    og, eng = _pair(True, [(s, d, t)])
+    _walk_case(og, eng, picker, "Uniform", forward, "total", 24, 8_000, seed=24)
+    seeds = np.array([0, 1, 2, 3, 4, 5], np.int32)
+    cuts = np.array([-1, 7 * 2_000, 7 * 500, 7 * 3_500, -1, 7 * 1_000], np.int64)
+    _walk_case(og, eng, picker, picker, forward, "nodes", 24, 300, seed_nodes=seeds,
+               cutoffs=cuts, seed=25)
+
+
 @pytest.mark.parametrize("directed", [True, False])
 @pytest.mark.parametrize("forward", [True, False])
 def test_replay_walks_negative_and_minus_one_timestamps(directed, forward):
