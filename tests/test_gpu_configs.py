@@ -277,8 +277,18 @@ def test_cfg4_full_weights_and_walks():
                                    rtol=1e-12, atol=0)
         assert np.all(np.diff(wf_all[a:b]) >= 0) and np.all(np.diff(wb_all[a:b]) >= 0)
     L = 80
+    # the wave-shared weight search groups other walks into each wave in
+    # walk-id order than in start-time order: the outputs are the same bytes
+    import torch
     w = eng.sample_device("total", L, "ExponentialWeight", 20_000_000,
-                          initial_edge_bias="ExponentialWeight")
+                          initial_edge_bias="ExponentialWeight", walk_order="walk_id")
+    by_id = _device_arrays(w, L)
+    w = eng.sample_device("total", L, "ExponentialWeight", 20_000_000,
+                          initial_edge_bias="ExponentialWeight", walk_order="start_time")
+    by_time = _device_arrays(w, L)
+    for name, x, y in zip(("nodes", "timestamps", "lens", "edge_ids"), by_id, by_time):
+        assert torch.equal(x, y), name
+    del by_id, by_time
     nodes, wts, lens, eids, _ = _fetch_rows(w, range(10_000_000, 10_001_500), L)
     _check_walks(nodes, wts, lens, eids, s, d, t, L, True, True)
     assert eng.walk_stats()["nonempty_walks"] == 20_000_000
