@@ -150,6 +150,84 @@ __global__ __launch_bounds__(kBlock) void scan_apply_kernel(const T* in, T* out,
     if (!Inclusive && blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) out[n] = sums[gridDim.x];
 }
 
+// ---------------------------------------------------------------------------
+// uint32 exclusive scan with coalesced accesses: the same 4096-item tiles, but
+// wave w of a tile owns items [1024 w, 1024 w + 1024) as four rows of 256, and
+// lane l holds items 4l..4l+3 of each row (one 16-byte access per lane and
+// row, 1 KiB contiguous per wave access).  Integer sums are exact in any
+// order, so the tile totals equal the blocked kernels'.
+// ---------------------------------------------------------------------------
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ u32x4_t load_u32x4(const uint32_t* in, size_t i, size_t n) {
+    if (i + 4 <= n) return *reinterpret_cast<const u32x4_t*>(in + i);
+    u32x4_t v = {0u, 0u, 0u, 0u};
+    if (i < n) v.x = in[i];
+    if (i + 1 < n) v.y = in[i + 1];
+    if (i + 2 < n) v.z = in[i + 2];
+    return v;
+}
+
+__global__ __launch_bounds__(kBlock) void scan_reduce_u32_kernel(const uint32_t* __restrict__ in,
+                                                                 size_t n,
+                                                                 uint32_t* __restrict__ sums) {
+    __shared__ uint32_t s_wave[kWaves];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const size_t wbase = blockIdx.x * kScanTile + static_cast<size_t>(wave) * 1024 + lane * 4;
+    uint32_t acc = 0;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const u32x4_t v = load_u32x4(in, wbase + r * 256, n);
+        acc += v.x + v.y + v.z + v.w;
+    }
+    const uint32_t tot = block_sum<uint32_t, OpSum>(acc, s_wave);
+    if (threadIdx.x == 0) sums[blockIdx.x] = tot;
+}
+
+__global__ __launch_bounds__(kBlock) void scan_apply_u32_kernel(const uint32_t* in,
+                                                                uint32_t* out, size_t n,
+                                                                const uint32_t* __restrict__ sums) {
+    __shared__ uint32_t s_wave[kWaves];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const size_t wbase = blockIdx.x * kScanTile + static_cast<size_t>(wave) * 1024 + lane * 4;
+    u32x4_t v[4];
+    uint32_t excl[4], row_tot[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] = load_u32x4(in, wbase + r * 256, n);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint32_t ls = v[r].x + v[r].y + v[r].z + v[r].w;
+        const uint32_t inc = wave_inclusive_scan<uint32_t, OpSum>(ls, lane);
+        excl[r] = inc - ls;
+        row_tot[r] = __shfl(inc, 63, 64);
+    }
+    const uint32_t wave_tot = row_tot[0] + row_tot[1] + row_tot[2] + row_tot[3];
+    if (lane == 0) s_wave[wave] = wave_tot;
+    __syncthreads();
+    uint32_t carry = sums[blockIdx.x];
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w)
+        if (w < wave) carry += s_wave[w];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const size_t i = wbase + r * 256;
+        u32x4_t o;
+        o.x = carry + excl[r];
+        o.y = o.x + v[r].x;
+        o.z = o.y + v[r].y;
+        o.w = o.z + v[r].z;
+        if (i + 4 <= n) {
+            *reinterpret_cast<u32x4_t*>(out + i) = o;
+        } else {
+            if (i < n) out[i] = o.x;
+            if (i + 1 < n) out[i + 1] = o.y;
+            if (i + 2 < n) out[i + 2] = o.z;
+        }
+        carry += row_tot[r];
+    }
+    if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) out[n] = sums[gridDim.x];
+}
+
 template <typename T, bool Inclusive, typename Op = OpSum>
 void scan_impl(const T* in, T* out, size_t n, T* scratch, hipStream_t s) {
     if (n == 0) {
@@ -506,7 +584,17 @@ size_t radix_hist_elems(size_t n) {
 
 void exclusive_scan_u32(const uint32_t* in, uint32_t* out, size_t n, uint32_t* scratch,
                         hipStream_t s) {
-    scan_impl<uint32_t, false>(in, out, n, scratch, s);
+    // the coalesced kernels need 16-byte aligned arrays
+    if (n == 0 || (reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) % 16) {
+        scan_impl<uint32_t, false>(in, out, n, scratch, s);
+        return;
+    }
+    const size_t nb = (n + kScanTile - 1) / kScanTile;
+    hipLaunchKernelGGL(scan_reduce_u32_kernel, dim3(nb), dim3(kBlock), 0, s, in, n, scratch);
+    hipLaunchKernelGGL((scan_sums_kernel<uint32_t, OpSum>), dim3(1), dim3(kBlock), 0, s, scratch,
+                       nb);
+    hipLaunchKernelGGL(scan_apply_u32_kernel, dim3(nb), dim3(kBlock), 0, s, in, out, n, scratch);
+    check_hip(hipGetLastError(), "scan launch");
 }
 void exclusive_scan_u64(const uint64_t* in, uint64_t* out, size_t n, uint64_t* scratch,
                         hipStream_t s) {
