@@ -665,7 +665,22 @@ __global__ void heavy_tile_prefix_kernel(const uint32_t* __restrict__ tile_base,
     for (int dir = 0; dir < (compute_forward ? 2 : 1); ++dir) {
         double* ts = dir == 0 ? tsum_b : tsum_f;
         double run = 0.0;
-        for (uint32_t t = tile_base[i]; t < tile_base[i + 1]; ++t) {
+        uint32_t t = tile_base[i];
+        const uint32_t te = tile_base[i + 1];
+        // 16 tile sums are loaded before the running sum consumes them, so the
+        // loads are in flight together; the additions keep tile order
+        constexpr int kBatch = 16;
+        for (; t + kBatch <= te; t += kBatch) {
+            double x[kBatch];
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) x[j] = ts[t + j];
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) {
+                ts[t + j] = run;
+                run = run + x[j];
+            }
+        }
+        for (; t < te; ++t) {
             const double x = ts[t];
             ts[t] = run;
             run = run + x;
