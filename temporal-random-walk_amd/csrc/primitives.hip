@@ -357,18 +357,29 @@ __global__ void fill_u32_kernel(uint32_t* __restrict__ p, size_t n, uint32_t v) 
     if (i < n) p[i] = v;
 }
 
-// Stable scatter of one digit pass.  Dynamic LDS: kWaves << db counters, then
-// 1 << db running positions.
+// Stable scatter of one digit pass.  A tile's keys are first placed in LDS in
+// their sorted order within the tile (digit, then wave, then rank), then
+// written out by consecutive threads: the keys of one digit leave as one
+// contiguous run instead of one scattered store per key.  Dynamic LDS
+// (radix_scatter_lds): kWaves << db counters, 1 << db running positions,
+// 1 << db output bases, then the tile's staged keys and values.
 template <typename K, typename V>
 __global__ __launch_bounds__(kBlock) void radix_scatter_kernel(
     const K* __restrict__ keys_in, const V* __restrict__ vals_in, K* __restrict__ keys_out,
     V* __restrict__ vals_out, size_t n, int bit, int db, uint32_t dmask,
     const uint32_t* __restrict__ offsets, size_t nb) {
-    extern __shared__ uint32_t s_lds[];
+    extern __shared__ __align__(16) uint32_t s_lds[];
+    __shared__ uint32_t s_wave[kWaves];
     const int R = 1 << db;
-    uint32_t* s_cnt = s_lds;           // [kWaves][R]
-    uint32_t* s_run = s_lds + kWaves * R;  // the workgroup's next output position per digit
+    uint32_t* s_cnt = s_lds;                // [kWaves][R]: counts, then tile-local offsets
+    uint32_t* s_run = s_cnt + kWaves * R;   // the workgroup's next output position per digit
+    uint32_t* s_base = s_run + R;           // output position of tile-local position 0, per digit
+    K* s_key = reinterpret_cast<K*>(s_base + R);
+    V* s_val = reinterpret_cast<V*>(s_key + kSortTile);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // digits [d0, d0 + per) of this thread in the tile epilogue
+    const int per = (R + kBlock - 1) / kBlock;
+    const int d0 = threadIdx.x * per;
     for (int d = threadIdx.x; d < R; d += kBlock)
         s_run[d] = offsets[static_cast<size_t>(d) * nb + blockIdx.x];
     for (int t = 0; t < kTilesPerBlock; ++t) {
@@ -401,30 +412,66 @@ __global__ __launch_bounds__(kBlock) void radix_scatter_kernel(
             if (valid && before == 0) s_cnt[wave * R + d] = prior + __popcll(m);
         }
         __syncthreads();
-        // tile epilogue: wave-major exclusive offsets of every digit, then the
-        // running position moves past this tile's keys of the digit
-        for (int d = threadIdx.x; d < R; d += kBlock) {
-            uint32_t run = s_run[d];
+        {
+            // tile epilogue: the tile-local start of every digit (an exclusive
+            // scan of the tile's digit counts), its waves' offsets after it,
+            // and the output position of local position 0 for the digit
+            uint32_t cnt_mine = 0;
+            for (int j = 0; j < per; ++j) {
+                const int d = d0 + j;
+                if (d < R) {
 #pragma unroll
-            for (int w = 0; w < kWaves; ++w) {
-                const uint32_t c = s_cnt[w * R + d];
-                s_cnt[w * R + d] = run;
-                run += c;
+                    for (int w = 0; w < kWaves; ++w) cnt_mine += s_cnt[w * R + d];
+                }
             }
-            s_run[d] = run;
+            uint32_t tot;
+            uint32_t start = block_exclusive_scan<uint32_t, OpSum>(cnt_mine, &tot, s_wave);
+            for (int j = 0; j < per; ++j) {
+                const int d = d0 + j;
+                if (d < R) {
+                    const uint32_t first = start;
+#pragma unroll
+                    for (int w = 0; w < kWaves; ++w) {
+                        const uint32_t c = s_cnt[w * R + d];
+                        s_cnt[w * R + d] = start;
+                        start += c;
+                    }
+                    s_base[d] = s_run[d] - first;  // wraps back in pos = base + local
+                    s_run[d] += start - first;
+                }
+            }
         }
         __syncthreads();
 #pragma unroll
         for (int r = 0; r < kRows; ++r) {
             const size_t i = wave_base + static_cast<size_t>(r) * 64 + lane;
             if (i < n) {
-                const uint32_t pos = s_cnt[wave * R + dig[r]] + rank[r];
-                keys_out[pos] = key[r];
-                if (vals_out) vals_out[pos] = val[r];
+                const uint32_t lp = s_cnt[wave * R + dig[r]] + rank[r];
+                s_key[lp] = key[r];
+                if (vals_out) s_val[lp] = val[r];
             }
         }
-        __syncthreads();  // s_cnt is cleared for the next tile
+        __syncthreads();
+        const size_t tile_n = n - tile_base < kSortTile ? n - tile_base : kSortTile;
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) {
+            const uint32_t lp = static_cast<uint32_t>(r) * kBlock + threadIdx.x;
+            if (lp < tile_n) {
+                const K k = s_key[lp];
+                const uint32_t d = static_cast<uint32_t>(k >> bit) & dmask;
+                const uint32_t pos = s_base[d] + lp;
+                keys_out[pos] = k;
+                if (vals_out) vals_out[pos] = s_val[lp];
+            }
+        }
+        __syncthreads();  // s_cnt and the staging are reused by the next tile
     }
+}
+
+template <typename K, typename V>
+size_t radix_scatter_lds(int R) {
+    return (static_cast<size_t>(kWaves) + 2) * R * sizeof(uint32_t) +
+           kSortTile * (sizeof(K) + sizeof(V));
 }
 
 // hist layout: nb * kMaxRadix per-workgroup counts, then kMaxPasses *
@@ -450,7 +497,7 @@ int radix_sort_impl(K* keys0, V* vals0, K* keys1, V* vals1, size_t n,
     hipLaunchKernelGGL(fill_u32_kernel, dim3((passes * R + kBlock - 1) / kBlock), dim3(kBlock), 0,
                        s, totals, static_cast<size_t>(passes * R), 0u);
     const size_t lds_up = static_cast<size_t>(kWaves) * R * sizeof(uint32_t);
-    const size_t lds_sc = lds_up + static_cast<size_t>(R) * sizeof(uint32_t);
+    const size_t lds_sc = radix_scatter_lds<K, V>(R);
     int cur = 0;
     K* kb[2] = {keys0, keys1};
     V* vb[2] = {vals0, vals1};
