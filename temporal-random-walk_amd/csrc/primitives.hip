@@ -297,13 +297,13 @@ __global__ __launch_bounds__(kBlock) void radix_upsweep_kernel(const K* __restri
             const size_t i = wave_base + static_cast<size_t>(r) * 64 + lane;
             key[r] = i < n ? keys[i] : K(0);
         }
+        // counts only (no ranks): an LDS atomic per key, which a wave's
+        // same-digit lanes serialise only among themselves
 #pragma unroll
         for (int r = 0; r < kRows; ++r) {
             const size_t i = wave_base + static_cast<size_t>(r) * 64 + lane;
-            const bool valid = i < n;
             const uint32_t d = static_cast<uint32_t>(key[r] >> bit) & dmask;
-            const uint64_t m = match_digit(d, valid, db);
-            if (valid && (m & lanes_below(lane)) == 0) s_cnt[wave * R + d] += __popcll(m);
+            if (i < n) atomicAdd(&s_cnt[wave * R + d], 1u);
         }
     }
     __syncthreads();
