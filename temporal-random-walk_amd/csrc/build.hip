@@ -895,11 +895,14 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
     if (E == 0) feat_dim = dim;
     const size_t e_old = E, etot = E + n;
 
-    // the batch's endpoints, for ..._for_last_batch
+    // the batch's endpoints, for ..._for_last_batch: copied on the side
+    // stream beside the build (the batch is ready when the call is made); the
+    // build's end waits for them
     last_src.resize(n);
     last_dst.resize(n);
-    check_hip(hipMemcpyAsync(last_src.p, d_src, n * 4, hipMemcpyDeviceToDevice, s), "last src");
-    check_hip(hipMemcpyAsync(last_dst.p, d_dst, n * 4, hipMemcpyDeviceToDevice, s), "last dst");
+    check_hip(hipMemcpyAsync(last_src.p, d_src, n * 4, hipMemcpyDeviceToDevice, side), "last src");
+    check_hip(hipMemcpyAsync(last_dst.p, d_dst, n * 4, hipMemcpyDeviceToDevice, side), "last dst");
+    check_hip(hipEventRecord(side_done, side), "event");
     last_n = n;
 
     // ---- 1. key range and latest timestamp
@@ -959,18 +962,25 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
         if (cutoff >= tmin) target = static_cast<int64_t>(static_cast<uint64_t>(cutoff) -
                                                           static_cast<uint64_t>(tmin));
     }
-    if (keys32)
-        hipLaunchKernelGGL((evict_search_kernel<uint32_t>), dim3(1), dim3(1), 0, s, k32s[which],
-                           etot, target, red64.p);
-    else
-        hipLaunchKernelGGL((evict_search_kernel<uint64_t>), dim3(1), dim3(1), 0, s,
-                           which ? k64b.p : k64a.p, etot, target, red64.p);
-    check_hip(hipMemcpyAsync(hs, red64.p, 24, hipMemcpyDeviceToHost, s), "read evict");
-    sync();
-    const size_t del = static_cast<size_t>(hs[0]);
+    size_t del = 0;
+    if (target >= 0) {
+        if (keys32)
+            hipLaunchKernelGGL((evict_search_kernel<uint32_t>), dim3(1), dim3(1), 0, s,
+                               k32s[which], etot, target, red64.p);
+        else
+            hipLaunchKernelGGL((evict_search_kernel<uint64_t>), dim3(1), dim3(1), 0, s,
+                               which ? k64b.p : k64a.p, etot, target, red64.p);
+        check_hip(hipMemcpyAsync(hs, red64.p, 24, hipMemcpyDeviceToHost, s), "read evict");
+        sync();
+        del = static_cast<size_t>(hs[0]);
+        store_tmin = static_cast<int64_t>(static_cast<uint64_t>(tmin) + static_cast<uint64_t>(hs[1]));
+        store_tmax = static_cast<int64_t>(static_cast<uint64_t>(tmin) + static_cast<uint64_t>(hs[2]));
+    } else {
+        // nothing is evicted: the store spans the merged key range
+        store_tmin = tmin;
+        store_tmax = tmax;
+    }
     const size_t kept = etot - del;
-    store_tmin = static_cast<int64_t>(static_cast<uint64_t>(tmin) + static_cast<uint64_t>(hs[1]));
-    store_tmax = static_cast<int64_t>(static_cast<uint64_t>(tmin) + static_cast<uint64_t>(hs[2]));
 
     // ---- 4. gather the kept suffix into the new store
     src2.resize(kept);
@@ -1134,6 +1144,7 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
         weights_ready = true;
     }
 
+    check_hip(hipStreamWaitEvent(s, side_done, 0), "wait side");
     check_hip(hipEventRecord(ev[3], s), "event");
     sync();
     float ms = 0;

@@ -17,15 +17,20 @@ namespace trw {
 
 Engine::Engine(const trw_config& c) : cfg(c), device(c.device_id) {
     check_hip(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
+    check_hip(hipStreamCreateWithFlags(&side, hipStreamNonBlocking), "hipStreamCreate");
+    check_hip(hipEventCreateWithFlags(&side_done, hipEventDisableTiming), "hipEventCreate");
     for (auto& e : ev) check_hip(hipEventCreate(&e), "hipEventCreate");
     check_hip(hipHostMalloc(&host_scalars, 256, hipHostMallocDefault), "hipHostMalloc");
 }
 
 Engine::~Engine() {
     if (stream) (void)hipStreamSynchronize(stream);
+    if (side) (void)hipStreamSynchronize(side);
     for (auto& e : ev)
         if (e) (void)hipEventDestroy(e);
+    if (side_done) (void)hipEventDestroy(side_done);
     if (host_scalars) (void)hipHostFree(host_scalars);
+    if (side) (void)hipStreamDestroy(side);
     if (stream) (void)hipStreamDestroy(stream);
 }
 

@@ -244,6 +244,10 @@ struct Engine {
     trw_config cfg{};
     int device = 0;
     hipStream_t stream = nullptr;
+    // a second stream for copies that overlap the build (same priority), and
+    // the event the build's end waits on
+    hipStream_t side = nullptr;
+    hipEvent_t side_done = nullptr;
 
     // edge store (+ the second half of a ping-pong pair for the gather)
     DBuf<int32_t> src, dst, src2, dst2;
