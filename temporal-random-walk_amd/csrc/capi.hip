@@ -233,7 +233,6 @@ trw_status trw_sample(void* handle, const trw_sample_params* params, trw_walks* 
     return guarded(handle, [&](Engine& e) {
         if (!params || !out) throw trw::InvalidArgument("null argument");
         e.sample(*params);
-        hipStream_t s = e.stream;
         const size_t nw = e.w_num, L = static_cast<size_t>(e.w_len);
         const size_t el = L ? L - 1 : 0;
         trw_walks r{};

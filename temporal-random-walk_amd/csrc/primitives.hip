@@ -538,7 +538,7 @@ __global__ __launch_bounds__(kBlock) void minmax_partial_kernel(const int64_t* _
     s_max[threadIdx.x] = mx;
     __syncthreads();
     for (int st = kBlock / 2; st > 0; st >>= 1) {
-        if (threadIdx.x < st) {
+        if (static_cast<int>(threadIdx.x) < st) {
             const int64_t a = s_min[threadIdx.x + st], b = s_max[threadIdx.x + st];
             if (a < s_min[threadIdx.x]) s_min[threadIdx.x] = a;
             if (b > s_max[threadIdx.x]) s_max[threadIdx.x] = b;
@@ -563,7 +563,7 @@ __global__ __launch_bounds__(kBlock) void minmax_final_kernel(const int64_t* par
     s_max[threadIdx.x] = mx;
     __syncthreads();
     for (int st = kBlock / 2; st > 0; st >>= 1) {
-        if (threadIdx.x < st) {
+        if (static_cast<int>(threadIdx.x) < st) {
             const int64_t a = s_min[threadIdx.x + st], b = s_max[threadIdx.x + st];
             if (a < s_min[threadIdx.x]) s_min[threadIdx.x] = a;
             if (b > s_max[threadIdx.x]) s_max[threadIdx.x] = b;
@@ -588,7 +588,7 @@ __global__ __launch_bounds__(kBlock) void max_pair_kernel(const int32_t* __restr
     s[threadIdx.x] = mx;
     __syncthreads();
     for (int st = kBlock / 2; st > 0; st >>= 1) {
-        if (threadIdx.x < st) s[threadIdx.x] = max(s[threadIdx.x], s[threadIdx.x + st]);
+        if (static_cast<int>(threadIdx.x) < st) s[threadIdx.x] = max(s[threadIdx.x], s[threadIdx.x + st]);
         __syncthreads();
     }
     if (threadIdx.x == 0) atomicMax(out, s[0]);
