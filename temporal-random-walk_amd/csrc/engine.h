@@ -313,6 +313,7 @@ struct Engine {
     // [num_walks, L] in the reference's types
     DBuf<int32_t> sw_nodes;
     DBuf<uint32_t> sw_rank, sw_eids;
+    DBuf<uint64_t> sw_packed;
     DBuf<int32_t> w_nodes;
     DBuf<int64_t> w_ts, w_eids;
     DBuf<uint64_t> w_lens;

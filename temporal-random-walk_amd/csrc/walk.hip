@@ -112,6 +112,10 @@ struct WalkArgs {
     uint32_t* ranks;
     uint64_t* lens;
     uint32_t* eids;
+    // packed scratch (nullptr: the three arrays above): one 64-bit word per
+    // slot, node | rank << pk_nb | (edge id into the slot) << (pk_nb + pk_rb)
+    uint64_t* packed;
+    int pk_nb, pk_rb;
     // Processing order (nullptr: walk id order).  Position q of the grid runs
     // walk order[q] and writes its scratch column q; outputs indexed by walk
     // (lengths, and the rows the layout pass writes) use the walk id.
@@ -124,6 +128,57 @@ struct WalkArgs {
 // Scratch rank of a walk's first slot, whose timestamp is the direction's
 // sentinel (INT64_MIN forward, INT64_MAX backward) rather than an edge time.
 constexpr uint32_t kStartRank = 0xffffffffu;
+
+// The walk scratch of one grid position.  Tile-major: grid positions come in
+// tiles of 64 (one wave), and slot k of position q lives at
+// [(q / 64) * 64 * K + k * 64 + q % 64] (K slots per row), so the wave stores
+// 256 B per slot and array contiguously and a tile's whole scratch is one
+// contiguous run for the layout pass.  Either three 32-bit arrays (node,
+// timestamp rank, edge id; K = L, L, L - 1), or -- when a node id, a rank and
+// an edge id fit in 64 bits together -- one 64-bit word per slot holding the
+// slot's node and rank and the id of the edge into the slot (K = L; rank
+// field all ones for the first slot): one store per hop instead of three, and
+// 8 instead of 12 scratch bytes per slot for the layout pass to read.
+struct SlotWriter {
+    int32_t* wn;
+    uint32_t* wt;
+    uint32_t* we;
+    uint64_t* wp;
+    int nb, rb;
+    __device__ __forceinline__ SlotWriter(const WalkArgs& a, uint64_t q) {
+        const uint64_t tile = q / 64, lane = q % 64, L = static_cast<uint64_t>(a.L);
+        wp = a.packed ? a.packed + tile * 64 * L + lane : nullptr;
+        wn = a.nodes + tile * 64 * L + lane;
+        wt = a.ranks + tile * 64 * L + lane;
+        we = a.eids + tile * 64 * (L - 1) + lane;
+        nb = a.pk_nb;
+        rb = a.pk_rb;
+    }
+    // slot 0: the walk's origin at the direction's sentinel time
+    __device__ __forceinline__ void first(int32_t node) {
+        if (wp) {
+            __builtin_nontemporal_store(static_cast<uint64_t>(static_cast<uint32_t>(node)) |
+                                            (((1ull << rb) - 1) << nb),
+                                        wp);
+        } else {
+            __builtin_nontemporal_store(node, wn);
+            __builtin_nontemporal_store(kStartRank, wt);
+        }
+    }
+    // slot k >= 1: its node and rank and the edge that reached it
+    __device__ __forceinline__ void slot(int k, int32_t node, uint32_t rank, uint32_t eid) {
+        if (wp) {
+            __builtin_nontemporal_store(static_cast<uint64_t>(static_cast<uint32_t>(node)) |
+                                            (static_cast<uint64_t>(rank) << nb) |
+                                            (static_cast<uint64_t>(eid) << (nb + rb)),
+                                        wp + static_cast<uint64_t>(k) * 64);
+        } else {
+            __builtin_nontemporal_store(node, wn + static_cast<uint64_t>(k) * 64);
+            __builtin_nontemporal_store(rank, wt + static_cast<uint64_t>(k) * 64);
+            __builtin_nontemporal_store(eid, we + static_cast<uint64_t>(k - 1) * 64);
+        }
+    }
+};
 
 // A start edge: endpoints, edge id (-1 for none) and the rank of its time.
 struct Sel {
@@ -675,11 +730,7 @@ __device__ __forceinline__ void walk_wave_weights(const WalkGraph& g, const Walk
     const bool in_range = q < a.q_end;
     const uint64_t w = in_range ? (a.order ? a.order[q] : q) : 0;
     const int L = a.L;  // >= 1 (the caller returned for L == 0)
-    constexpr uint64_t n = kScratchTile;
-    const uint64_t tile = q / kScratchTile, lane = q % kScratchTile;
-    int32_t* wn = a.nodes + tile * kScratchTile * static_cast<uint64_t>(L) + lane;
-    uint32_t* wt = a.ranks + tile * kScratchTile * static_cast<uint64_t>(L) + lane;
-    uint32_t* we = a.eids + tile * kScratchTile * static_cast<uint64_t>(L - 1) + lane;
+    SlotWriter out(a, q);
     const int32_t cut = in_range ? cutoff_rank(g, a, w) : -1;
     const int32_t neg1 = *g.neg1_rank;
     const StartState s0 = in_range ? a.st[w] : StartState{-1, -1, -1, -1};
@@ -688,8 +739,7 @@ __device__ __forceinline__ void walk_wave_weights(const WalkGraph& g, const Walk
     int len = 0, walk_len = 1;
     bool active = in_range && cur_e != -1;
     if (active) {
-        store_out(wn, s0.first);
-        store_out(wt, kStartRank);
+        out.first(s0.first);
         len = 1;
     }
     active = active && walk_len < L && cur != a.pad;
@@ -697,9 +747,7 @@ __device__ __forceinline__ void walk_wave_weights(const WalkGraph& g, const Walk
         WeightHop hs{true, false, 0, 0, 0, 0, 0, 0, nullptr, 0.0};
         double re = 0.0;
         if (active) {
-            store_out(wn + len * n, cur);
-            store_out(wt + len * n, static_cast<uint32_t>(cur_r));
-            store_out(we + (len - 1) * n, static_cast<uint32_t>(cur_e));
+            out.slot(len, cur, static_cast<uint32_t>(cur_r), static_cast<uint32_t>(cur_e));
             ++len;
             if (walk_len == L - 1) {
                 active = false;  // the reference's last selection cannot change the output
@@ -762,17 +810,10 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
         a.lens[w] = 0;
         return;
     }
-    // Tile-major scratch: grid positions come in tiles of 64 (one wave), and
-    // slot k of position q lives at [(q / 64) * 64 * K + k * 64 + q % 64] (K
-    // slots per row), so the wave stores 256 B per slot and array
-    // contiguously and a tile's whole scratch is one contiguous run for the
-    // layout pass, which produces the row-major output in the reference's
-    // types, the padding and the chronological order of backward walks.
-    constexpr uint64_t n = kScratchTile;
-    const uint64_t tile = q / kScratchTile, lane = q % kScratchTile;
-    int32_t* wn = a.nodes + tile * kScratchTile * static_cast<uint64_t>(L) + lane;
-    uint32_t* wt = a.ranks + tile * kScratchTile * static_cast<uint64_t>(L) + lane;
-    uint32_t* we = a.eids + tile * kScratchTile * static_cast<uint64_t>(L - 1) + lane;
+    // the scratch feeds the layout pass, which produces the row-major output
+    // in the reference's types, the padding and the chronological order of
+    // backward walks
+    SlotWriter out(a, q);
     const int32_t cut = cutoff_rank(g, a, w);
     // the reference's tests of a current time of -1, on ranks
     const int32_t neg1 = *g.neg1_rank;
@@ -784,14 +825,11 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
     int len = 0;
     if (cur_e != -1) {
         int prev = -1;
-        store_out(wn, first);
-        store_out(wt, kStartRank);
+        out.first(first);
         len = 1;
         int walk_len = 1;
         while (walk_len < L && cur != a.pad) {
-            store_out(wn + len * n, cur);
-            store_out(wt + len * n, static_cast<uint32_t>(cur_r));
-            store_out(we + (len - 1) * n, static_cast<uint32_t>(cur_e));
+            out.slot(len, cur, static_cast<uint32_t>(cur_r), static_cast<uint32_t>(cur_e));
             ++len;
             // The reference draws and selects once more after the last slot is
             // written; that selection cannot change the output, so it is skipped.
@@ -847,11 +885,17 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
 constexpr int kLayoutWalks = 64;
 static_assert(kLayoutWalks == kScratchTile, "a layout workgroup owns one scratch tile");
 constexpr int kLayoutMaxSlots = 128;  // tile <= 33 KB of LDS
+// 64-bit tile <= 64 KB of LDS.  A row split into chunks costs more than the
+// occupancy a smaller tile buys: 80-slot rows in two chunks of 40 were
+// measured 1.3 ms slower over 10M walks than in one.
+constexpr int kLayoutPackedMaxSlots = 120;
 
 struct LayoutArgs {
     const int32_t* sn;   // scratch nodes
     const uint32_t* sr;  // scratch timestamp ranks
     const uint32_t* se;  // scratch edge ids
+    const uint64_t* sp;  // packed scratch (replaces the three above when set)
+    int pk_nb, pk_rb;    // its node and rank field widths
     int32_t* on;
     int64_t* ot;
     int64_t* oe;
@@ -884,6 +928,81 @@ __device__ __forceinline__ int64_t layout_value(const LayoutArgs& a, uint32_t x,
     return i < cw ? static_cast<int64_t>(x) : -1;
 }
 
+// Writes the chunk's output rows of one array: each wave owns whole rows and
+// converts values as it writes them.  src_at(wl2, n, cw, i) is the 32-bit
+// scratch value of output slot i of tile column wl2, whose walk wrote n node
+// slots and has cw slots of this array's chunk below its count.
+template <int Arr, class Src>
+__device__ __forceinline__ void layout_rows(const LayoutArgs& a, const int* cnt, const uint32_t* row,
+                                            uint64_t w0, int k0, Src src_at) {
+    const int K = Arr == 2 ? a.L - 1 : a.L;
+    const int kc = min(a.C, K - k0);
+    if (kc <= 0) return;  // uniform over the workgroup
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // 16-byte stores (4 nodes or 2 timestamps / edge ids per lane) when every
+    // row chunk starts on a 16-byte boundary and holds whole vectors
+    constexpr int V = Arr == 0 ? 4 : 2;
+    const bool vec = (K % V) == 0 && (k0 % V) == 0 && (kc % V) == 0;
+    // The wave's 16 rows (columns wave, wave + 4, ...) are cut into store
+    // units (a vector or one value) and the wave's lanes take consecutive
+    // units, so a row shorter than 64 units shares a store instruction with
+    // the next row instead of leaving lanes idle.
+    const int S = vec ? V : 1;
+    const int U = kc / S;  // units per row
+    constexpr int kRows = kLayoutWalks / 4;
+    for (int t = lane; t < kRows * U; t += 64) {
+        const int j = t / U;
+        const int i = (t - j * U) * S;
+        const int wl2 = wave + 4 * j;
+        if (w0 + wl2 >= a.q_end) continue;
+        const uint64_t base = static_cast<uint64_t>(row[wl2]) * static_cast<uint64_t>(K) + k0;
+        const int n = cnt[wl2];
+        const int cw = n - (Arr == 2 ? 1 : 0) - k0;  // slots of the row below the count
+        auto src = [&](int x) { return src_at(wl2, n, cw, x); };
+        if (vec) {
+            if (Arr == 0) {
+                const i32x4 o = {static_cast<int32_t>(layout_value<0>(a, src(i), i, cw)),
+                                 static_cast<int32_t>(layout_value<0>(a, src(i + 1), i + 1, cw)),
+                                 static_cast<int32_t>(layout_value<0>(a, src(i + 2), i + 2, cw)),
+                                 static_cast<int32_t>(layout_value<0>(a, src(i + 3), i + 3, cw))};
+                __builtin_nontemporal_store(o, reinterpret_cast<i32x4*>(a.on + base + i));
+            } else {
+                const i64x2 o = {layout_value<Arr>(a, src(i), i, cw),
+                                 layout_value<Arr>(a, src(i + 1), i + 1, cw)};
+                int64_t* out = Arr == 1 ? a.ot : a.oe;
+                __builtin_nontemporal_store(o, reinterpret_cast<i64x2*>(out + base + i));
+            }
+        } else {
+            const int64_t y = layout_value<Arr>(a, src(i), i, cw);
+            if (Arr == 0) __builtin_nontemporal_store(static_cast<int32_t>(y), a.on + base + i);
+            else if (Arr == 1) __builtin_nontemporal_store(y, a.ot + base + i);
+            else __builtin_nontemporal_store(y, a.oe + base + i);
+        }
+    }
+    if (Arr != 2 || !a.fv) return;
+    for (int wl2 = wave; wl2 < kLayoutWalks; wl2 += 4) {
+        if (w0 + wl2 >= a.q_end) break;
+        const uint64_t base = static_cast<uint64_t>(row[wl2]) * static_cast<uint64_t>(K) + k0;
+        const int n = cnt[wl2];
+        const int cw = n - 1 - k0;
+        auto src = [&](int x) { return src_at(wl2, n, cw, x); };
+        // the slots' edge features (finalize_host_walks,
+        // walks_with_edge_features_host.cuh:44-62), from the edge ids in
+        // the tile: row [slot][dim] of the walk, zeros past the count
+        const uint32_t fv = a.fv;
+        const f32x4* feat = reinterpret_cast<const f32x4*>(a.feat);
+        f32x4* of = reinterpret_cast<f32x4*>(a.of) + base * fv;
+        const uint32_t units = static_cast<uint32_t>(kc) * fv;
+        for (uint32_t t = lane; t < units; t += 64) {
+            const int i = static_cast<int>(t / fv);
+            const uint32_t c = t - static_cast<uint32_t>(i) * fv;
+            f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (i < cw) v = __builtin_nontemporal_load(feat + static_cast<uint64_t>(src(i)) * fv + c);
+            __builtin_nontemporal_store(v, of + t);
+        }
+    }
+}
+
 template <int Arr>
 __device__ __forceinline__ void layout_array(const LayoutArgs& a, uint32_t* tile, const int* cnt,
                                              const uint32_t* row, uint64_t w0, int k0) {
@@ -903,7 +1022,7 @@ __device__ __forceinline__ void layout_array(const LayoutArgs& a, uint32_t* tile
     const bool rev_in = a.reverse && !whole;
     // slots at or past the count are not read; the writer pads them
     const uint32_t* in = Arr == 0 ? reinterpret_cast<const uint32_t*>(a.sn) : (Arr == 1 ? a.sr : a.se);
-    const uint64_t tile_base = w0 * static_cast<uint64_t>(K);  // w0 % kScratchTile == 0
+    in += w0 * static_cast<uint64_t>(K);  // w0 % kScratchTile == 0
     for (int j0 = 0; j0 < kc; j0 += 32) {
         uint32_t v[8];
 #pragma unroll
@@ -912,8 +1031,7 @@ __device__ __forceinline__ void layout_array(const LayoutArgs& a, uint32_t* tile
             const int k = k0 + r;
             uint32_t x = 0;
             if (r < kc && w < a.q_end && k < c)
-                x = __builtin_nontemporal_load(
-                    in + tile_base + static_cast<uint64_t>(rev_in ? c - 1 - k : k) * kScratchTile + wl);
+                x = __builtin_nontemporal_load(in + static_cast<uint64_t>(rev_in ? c - 1 - k : k) * kScratchTile + wl);
             v[j] = x;
         }
 #pragma unroll
@@ -923,58 +1041,21 @@ __device__ __forceinline__ void layout_array(const LayoutArgs& a, uint32_t* tile
         }
     }
     __syncthreads();
-    const int wave = tid >> 6, lane = tid & 63;
     const bool rev_out = a.reverse && whole;
-    // 16-byte stores (4 nodes or 2 timestamps / edge ids per lane) when every
-    // row chunk starts on a 16-byte boundary and holds whole vectors
-    constexpr int V = Arr == 0 ? 4 : 2;
-    const bool vec = (K % V) == 0 && (k0 % V) == 0 && (kc % V) == 0;
-    for (int wl2 = wave; wl2 < kLayoutWalks; wl2 += 4) {
-        if (w0 + wl2 >= a.q_end) break;
-        const uint64_t w2 = row[wl2];
-        const uint64_t base = w2 * static_cast<uint64_t>(K) + k0;
-        const int cw = cnt[wl2] - (Arr == 2 ? 1 : 0) - k0;  // slots of the row below the count
-        // tile slot of output slot i (reversed rows: slot cw - 1 - i)
-        auto src = [&](int i) { return tile[(rev_out && i < cw ? cw - 1 - i : i) * P + wl2]; };
-        if (vec) {
-            for (int i = lane * V; i < kc; i += 64 * V) {
-                if (Arr == 0) {
-                    const i32x4 o = {static_cast<int32_t>(layout_value<0>(a, src(i), i, cw)),
-                                     static_cast<int32_t>(layout_value<0>(a, src(i + 1), i + 1, cw)),
-                                     static_cast<int32_t>(layout_value<0>(a, src(i + 2), i + 2, cw)),
-                                     static_cast<int32_t>(layout_value<0>(a, src(i + 3), i + 3, cw))};
-                    __builtin_nontemporal_store(o, reinterpret_cast<i32x4*>(a.on + base + i));
-                } else {
-                    const i64x2 o = {layout_value<Arr>(a, src(i), i, cw),
-                                     layout_value<Arr>(a, src(i + 1), i + 1, cw)};
-                    int64_t* out = Arr == 1 ? a.ot : a.oe;
-                    __builtin_nontemporal_store(o, reinterpret_cast<i64x2*>(out + base + i));
-                }
-            }
-        } else {
-            for (int i = lane; i < kc; i += 64) {
-                const int64_t y = layout_value<Arr>(a, src(i), i, cw);
-                if (Arr == 0) __builtin_nontemporal_store(static_cast<int32_t>(y), a.on + base + i);
-                else if (Arr == 1) __builtin_nontemporal_store(y, a.ot + base + i);
-                else __builtin_nontemporal_store(y, a.oe + base + i);
-            }
-        }
-        if (Arr == 2 && a.fv) {
-            // the slots' edge features (finalize_host_walks,
-            // walks_with_edge_features_host.cuh:44-62), from the edge ids in
-            // the tile: row [slot][dim] of the walk, zeros past the count
-            const uint32_t fv = a.fv;
-            const f32x4* feat = reinterpret_cast<const f32x4*>(a.feat);
-            f32x4* of = reinterpret_cast<f32x4*>(a.of) + base * fv;
-            const uint32_t units = static_cast<uint32_t>(kc) * fv;
-            for (uint32_t t = lane; t < units; t += 64) {
-                const int i = static_cast<int>(t / fv);
-                const uint32_t c = t - static_cast<uint32_t>(i) * fv;
-                f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-                if (i < cw) v = __builtin_nontemporal_load(feat + static_cast<uint64_t>(src(i)) * fv + c);
-                __builtin_nontemporal_store(v, of + t);
-            }
-        }
+    // tile slot of output slot i (reversed rows: slot cw - 1 - i)
+    layout_rows<Arr>(a, cnt, row, w0, k0, [&](int wl2, int, int cw, int i) {
+        return tile[(rev_out && i < cw ? cw - 1 - i : i) * P + wl2];
+    });
+    __syncthreads();
+}
+
+// Loads the walk count and destination row of the workgroup's 64 columns.
+__device__ __forceinline__ void layout_columns(const LayoutArgs& a, uint64_t w0, int* cnt, uint32_t* row) {
+    if (threadIdx.x < kLayoutWalks) {
+        const uint64_t q = w0 + threadIdx.x;
+        const uint64_t w = q < a.q_end ? (a.order ? a.order[q] : q) : 0;
+        row[threadIdx.x] = static_cast<uint32_t>(w);
+        cnt[threadIdx.x] = q < a.q_end ? static_cast<int>(a.lens[w]) : 0;
     }
     __syncthreads();
 }
@@ -986,16 +1067,77 @@ __global__ __launch_bounds__(256) void layout_walks_kernel(LayoutArgs a) {
     uint32_t* row = reinterpret_cast<uint32_t*>(cnt + kLayoutWalks);
     const uint64_t w0 = a.q0 + static_cast<uint64_t>(blockIdx.x) * kLayoutWalks;
     const int k0 = blockIdx.y * a.C;
-    if (threadIdx.x < kLayoutWalks) {
-        const uint64_t q = w0 + threadIdx.x;
-        const uint64_t w = q < a.q_end ? (a.order ? a.order[q] : q) : 0;
-        row[threadIdx.x] = static_cast<uint32_t>(w);
-        cnt[threadIdx.x] = q < a.q_end ? static_cast<int>(a.lens[w]) : 0;
-    }
-    __syncthreads();
+    layout_columns(a, w0, cnt, row);
     layout_array<0>(a, tile, cnt, row, w0, k0);
     layout_array<1>(a, tile, cnt, row, w0, k0);
     layout_array<2>(a, tile, cnt, row, w0, k0);
+}
+
+// Field of a packed scratch word: the node, the rank (all ones: the first
+// slot's sentinel, kStartRank) or the id of the edge into the slot.
+template <int Arr>
+__device__ __forceinline__ uint32_t packed_field(const LayoutArgs& a, uint64_t word) {
+    if (Arr == 2) return static_cast<uint32_t>(word >> (a.pk_nb + a.pk_rb));
+    const int sh = Arr == 0 ? 0 : a.pk_nb;
+    const uint64_t m = (1ull << (Arr == 0 ? a.pk_nb : a.pk_rb)) - 1;
+    const uint64_t f = (word >> sh) & m;
+    return Arr == 1 && f == m ? kStartRank : static_cast<uint32_t>(f);
+}
+
+// Layout pass over packed scratch: the chunk's words are read once into an
+// LDS tile of 64-bit words and all three arrays are written from it.  Tile
+// row r holds slot k0 + r (slot n - 1 - (k0 + r) for the reversed rows of a
+// walk laid out in several chunks), plus, for forward rows, slot k0 + kc:
+// the edge id of output slot i is in slot i + 1, the slot the edge reached;
+// reversed rows find it in the same word as their node.
+__global__ __launch_bounds__(256) void layout_packed_kernel(LayoutArgs a) {
+    constexpr int P = kLayoutWalks + 1;
+    extern __shared__ uint64_t layout_lds64[];
+    uint64_t* tile = layout_lds64;
+    int* cnt = reinterpret_cast<int*>(tile + (a.C + 1) * P);
+    uint32_t* row = reinterpret_cast<uint32_t*>(cnt + kLayoutWalks);
+    const uint64_t w0 = a.q0 + static_cast<uint64_t>(blockIdx.x) * kLayoutWalks;
+    const int k0 = blockIdx.y * a.C;
+    layout_columns(a, w0, cnt, row);
+    const int kc = min(a.C, a.L - k0);
+    const bool whole = k0 == 0 && kc == a.L;
+    const bool rev_in = a.reverse && !whole;
+    const int rows = min(kc + 1, a.L - k0);
+    const int wl = threadIdx.x & 63, srow = threadIdx.x >> 6;
+    const int c = cnt[wl];
+    const bool live = w0 + wl < a.q_end;
+    const uint64_t* in = a.sp + w0 * static_cast<uint64_t>(a.L);  // w0 % kScratchTile == 0
+    for (int j0 = 0; j0 < rows; j0 += 32) {
+        uint64_t v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int r = j0 + srow + 4 * j;
+            const int k = k0 + r;
+            uint64_t x = 0;
+            if (r < rows && live && k < c)
+                x = __builtin_nontemporal_load(in + static_cast<uint64_t>(rev_in ? c - 1 - k : k) * kScratchTile + wl);
+            v[j] = x;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int r = j0 + srow + 4 * j;
+            if (r < rows) tile[r * P + wl] = v[j];
+        }
+    }
+    __syncthreads();
+    const bool rev_out = a.reverse && whole;
+    // node and timestamp of output slot i: tile row i (reversed whole rows: n - 1 - i)
+    auto node_row = [&](int n, int cw, int i) { return rev_out && i < cw ? n - 1 - i : i; };
+    layout_rows<0>(a, cnt, row, w0, k0, [&](int wl2, int n, int cw, int i) {
+        return packed_field<0>(a, tile[node_row(n, cw, i) * P + wl2]);
+    });
+    layout_rows<1>(a, cnt, row, w0, k0, [&](int wl2, int n, int cw, int i) {
+        return packed_field<1>(a, tile[node_row(n, cw, i) * P + wl2]);
+    });
+    layout_rows<2>(a, cnt, row, w0, k0, [&](int wl2, int n, int cw, int i) {
+        const int r = a.reverse ? node_row(n, cw, i) : i + 1;
+        return packed_field<2>(a, tile[r * P + wl2]);
+    });
 }
 
 // ---- start arrays ----------------------------------------------------------
@@ -1331,9 +1473,25 @@ void Engine::sample(const trw_sample_params& p) {
     const uint64_t eslots = nw * static_cast<uint64_t>(L > 0 ? L - 1 : 0);
     // scratch: whole tiles of kScratchTile walks
     const uint64_t padded = (nw + kScratchTile - 1) / kScratchTile * kScratchTile;
-    sw_nodes.resize(padded * L);
-    sw_rank.resize(padded * L);
-    sw_eids.resize(padded * (L > 0 ? L - 1 : 0));
+    // packed scratch when a node id (in [0, max_node_id], as the node index
+    // requires), a rank below T with the all-ones value free for the start
+    // sentinel, and an edge id below E fit in one 64-bit word
+    auto bit_length = [](uint64_t v) { return v ? 64 - __builtin_clzll(v) : 0; };
+    const int pk_nb = std::max(1, bit_length(static_cast<uint64_t>(std::max(max_node_id, 0))));
+    const int pk_rb = bit_length(T);
+    const int pk_eb = E ? bit_length(E - 1) : 0;
+    const bool packed = E > 0 && max_node_id >= 0 && pk_nb + pk_rb + pk_eb <= 64 && pk_nb + pk_rb < 64;
+    if (packed) {
+        sw_packed.resize(padded * L);
+        sw_nodes.release();
+        sw_rank.release();
+        sw_eids.release();
+    } else {
+        sw_packed.release();
+        sw_nodes.resize(padded * L);
+        sw_rank.resize(padded * L);
+        sw_eids.resize(padded * (L > 0 ? L - 1 : 0));
+    }
     w_nodes.resize(slots);
     w_ts.resize(slots);
     w_eids.resize(eslots);
@@ -1403,6 +1561,9 @@ void Engine::sample(const trw_sample_params& p) {
     a.ranks = sw_rank.p;
     a.lens = w_lens.p;
     a.eids = sw_eids.p;
+    a.packed = packed ? sw_packed.p : nullptr;
+    a.pk_nb = pk_nb;
+    a.pk_rb = pk_rb;
 
     if (nw && E == 0) {
         // empty graph: every start fails; the kernel still writes the padding
@@ -1475,12 +1636,16 @@ void Engine::sample(const trw_sample_params& p) {
         la.sn = sw_nodes.p;
         la.sr = sw_rank.p;
         la.se = sw_eids.p;
+        la.sp = a.packed;
+        la.pk_nb = pk_nb;
+        la.pk_rb = pk_rb;
         la.on = w_nodes.p;
         la.ot = w_ts.p;
         la.oe = w_eids.p;
         la.lens = w_lens.p;
         la.L = L;
-        const int slot_chunks = (L + kLayoutMaxSlots - 1) / kLayoutMaxSlots;
+        const int max_slots = a.packed ? kLayoutPackedMaxSlots : kLayoutMaxSlots;
+        const int slot_chunks = (L + max_slots - 1) / max_slots;
         la.C = (L + slot_chunks - 1) / slot_chunks;
         la.reverse = forward ? 0 : 1;
         la.pad = static_cast<int32_t>(cfg.walk_padding_value);
@@ -1498,10 +1663,14 @@ void Engine::sample(const trw_sample_params& p) {
             la.of = w_feat.p;
             la.fv = static_cast<uint32_t>(feat_dim / 4);
         }
-        const size_t lds = static_cast<size_t>(la.C) * (kLayoutWalks + 1) * sizeof(uint32_t) +
-                           kLayoutWalks * (sizeof(int) + sizeof(uint32_t));
+        const size_t tile = a.packed ? static_cast<size_t>(la.C + 1) * (kLayoutWalks + 1) * sizeof(uint64_t)
+                                     : static_cast<size_t>(la.C) * (kLayoutWalks + 1) * sizeof(uint32_t);
+        const size_t lds = tile + kLayoutWalks * (sizeof(int) + sizeof(uint32_t));
         const unsigned gx = static_cast<unsigned>((nw + kLayoutWalks - 1) / kLayoutWalks);
-        hipLaunchKernelGGL(layout_walks_kernel, dim3(gx, slot_chunks), dim3(256), lds, s, la);
+        if (a.packed)
+            hipLaunchKernelGGL(layout_packed_kernel, dim3(gx, slot_chunks), dim3(256), lds, s, la);
+        else
+            hipLaunchKernelGGL(layout_walks_kernel, dim3(gx, slot_chunks), dim3(256), lds, s, la);
         check_hip(hipGetLastError(), "layout launch");
     }
 

@@ -398,6 +398,28 @@ def test_replay_walks_hub_with_more_groups_than_the_header_holds():
             _walk_case(og, eng, picker, "Uniform", forward, "total", 12, 3_000, seed=93)
 
 
+@pytest.mark.parametrize("forward", [True, False])
+def test_replay_walks_wide_ids_use_three_scratch_arrays(forward):
+    """Node ids up to 2^22 - 1, 2^21 + 60,000 distinct timestamps and as many
+    edges: a node id, a timestamp rank and an edge id need 22 + 22 + 22 bits,
+    more than one 64-bit scratch word holds, so the walks go through the
+    three 32-bit scratch arrays (every smaller graph here packs them)."""
+    rng = np.random.default_rng(95)
+    e = (1 << 21) + 60_000
+    ids = np.concatenate([[0, (1 << 22) - 1],
+                          rng.choice(np.arange(1, (1 << 22) - 1), 6_000, replace=False)])
+    perm = rng.permutation(ids.size)
+    s = ids[graphs.zipf_ids(rng, e, ids.size, 1.5, perm)].astype(np.int32)
+    d = ids[graphs.zipf_ids(rng, e, ids.size, 1.5, perm)].astype(np.int32)
+    t = rng.permutation(e).astype(np.int64)
+    og, eng = _pair(True, [(s, d, t)])
+    assert int(eng.array("active_node_ids").size) == 1 << 22
+    assert int(eng.array("unique_timestamps").size) == e
+    _walk_case(og, eng, "ExponentialIndex", "Uniform", forward, "total", 20, 20_000, seed=96)
+    _walk_case(og, eng, "Uniform", "Linear", forward, "nodes", 20, 4,
+               seed_nodes=ids[:500].astype(np.int32), seed=97)
+
+
 # ---- normal mode: the in-kernel Philox stream -----------------------------
 
 GLOBAL_SEED = 1234  # the seed _pair gives the engine
