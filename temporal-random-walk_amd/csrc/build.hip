@@ -892,25 +892,27 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
     int64_t* hs = reinterpret_cast<int64_t*>(host_scalars);
     check_hip(hipEventRecord(ev[0], s), "event");
 
-    if (E == 0) feat_dim = dim;
     const size_t e_old = E, etot = E + n;
 
+    // ---- 1. key range, latest timestamp, and the batch's smallest node id:
+    // the node index is keyed by ids in [0, max_node_id], so a negative id
+    // is rejected here, before the store changes
+    red64.ensure(minmax_scratch_elems());
+    minmax_ts_min_id(d_ts, d_src, d_dst, n, red64.p, s);
+    check_hip(hipMemcpyAsync(hs, red64.p, 24, hipMemcpyDeviceToHost, s), "read minmax");
+    sync();
+    if (hs[2] < 0) throw InvalidArgument("node ids must be non-negative");
+    if (E == 0) feat_dim = dim;
+    int64_t tmin = hs[0], tmax = hs[1];
+
     // the batch's endpoints, for ..._for_last_batch: copied on the side
-    // stream beside the build (the batch is ready when the call is made); the
-    // build's end waits for them
+    // stream beside the build; the build's end waits for them
     last_src.resize(n);
     last_dst.resize(n);
     check_hip(hipMemcpyAsync(last_src.p, d_src, n * 4, hipMemcpyDeviceToDevice, side), "last src");
     check_hip(hipMemcpyAsync(last_dst.p, d_dst, n * 4, hipMemcpyDeviceToDevice, side), "last dst");
     check_hip(hipEventRecord(side_done, side), "event");
     last_n = n;
-
-    // ---- 1. key range and latest timestamp
-    red64.ensure(2 + 2 * 1024);
-    minmax_i64(d_ts, n, red64.p, s);
-    check_hip(hipMemcpyAsync(hs, red64.p, 16, hipMemcpyDeviceToHost, s), "read minmax");
-    sync();
-    int64_t tmin = hs[0], tmax = hs[1];
     if (e_old) {
         tmin = std::min(tmin, store_tmin);
         tmax = std::max(tmax, store_tmax);

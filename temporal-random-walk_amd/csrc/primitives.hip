@@ -524,55 +524,66 @@ int radix_sort_impl(K* keys0, V* vals0, K* keys1, V* vals1, size_t n,
 // ---------------------------------------------------------------------------
 constexpr int kReduceBlocks = 1024;
 
-__global__ __launch_bounds__(kBlock) void minmax_partial_kernel(const int64_t* __restrict__ v,
-                                                                size_t n, int64_t* part) {
-    __shared__ int64_t s_min[kBlock], s_max[kBlock];
-    int64_t mn = INT64_MAX, mx = INT64_MIN;
-    for (size_t i = blockIdx.x * static_cast<size_t>(kBlock) + threadIdx.x; i < n;
-         i += static_cast<size_t>(gridDim.x) * kBlock) {
-        const int64_t x = v[i];
-        mn = x < mn ? x : mn;
-        mx = x > mx ? x : mx;
-    }
-    s_min[threadIdx.x] = mn;
-    s_max[threadIdx.x] = mx;
+// min and max of v, and the smallest of the ids a[i], b[i] (INT64_MAX for
+// n == 0): one pass over a batch's timestamps and endpoints
+struct MinMaxId {
+    int64_t mn, mx, id;
+};
+
+__device__ __forceinline__ MinMaxId minmax_id_join(MinMaxId x, MinMaxId y) {
+    return {y.mn < x.mn ? y.mn : x.mn, y.mx > x.mx ? y.mx : x.mx, y.id < x.id ? y.id : x.id};
+}
+
+__device__ __forceinline__ MinMaxId block_minmax_id(MinMaxId v, int64_t* sm) {
+    sm[3 * threadIdx.x] = v.mn;
+    sm[3 * threadIdx.x + 1] = v.mx;
+    sm[3 * threadIdx.x + 2] = v.id;
     __syncthreads();
     for (int st = kBlock / 2; st > 0; st >>= 1) {
         if (static_cast<int>(threadIdx.x) < st) {
-            const int64_t a = s_min[threadIdx.x + st], b = s_max[threadIdx.x + st];
-            if (a < s_min[threadIdx.x]) s_min[threadIdx.x] = a;
-            if (b > s_max[threadIdx.x]) s_max[threadIdx.x] = b;
+            const int o = 3 * (threadIdx.x + st);
+            const MinMaxId r = minmax_id_join({sm[3 * threadIdx.x], sm[3 * threadIdx.x + 1], sm[3 * threadIdx.x + 2]},
+                                              {sm[o], sm[o + 1], sm[o + 2]});
+            sm[3 * threadIdx.x] = r.mn;
+            sm[3 * threadIdx.x + 1] = r.mx;
+            sm[3 * threadIdx.x + 2] = r.id;
         }
         __syncthreads();
     }
+    return {sm[0], sm[1], sm[2]};
+}
+
+__global__ __launch_bounds__(kBlock) void minmax_partial_kernel(const int64_t* __restrict__ v,
+                                                                const int32_t* __restrict__ a,
+                                                                const int32_t* __restrict__ b,
+                                                                size_t n, int64_t* part) {
+    __shared__ int64_t sm[3 * kBlock];
+    MinMaxId acc{INT64_MAX, INT64_MIN, INT64_MAX};
+    for (size_t i = blockIdx.x * static_cast<size_t>(kBlock) + threadIdx.x; i < n;
+         i += static_cast<size_t>(gridDim.x) * kBlock) {
+        const int64_t x = v[i];
+        const int64_t id = min(a[i], b[i]);
+        acc = minmax_id_join(acc, {x, x, id});
+    }
+    const MinMaxId r = block_minmax_id(acc, sm);
     if (threadIdx.x == 0) {
-        part[2 * blockIdx.x] = s_min[0];
-        part[2 * blockIdx.x + 1] = s_max[0];
+        part[3 * blockIdx.x] = r.mn;
+        part[3 * blockIdx.x + 1] = r.mx;
+        part[3 * blockIdx.x + 2] = r.id;
     }
 }
 
 __global__ __launch_bounds__(kBlock) void minmax_final_kernel(const int64_t* part, int np,
                                                               int64_t* out) {
-    __shared__ int64_t s_min[kBlock], s_max[kBlock];
-    int64_t mn = INT64_MAX, mx = INT64_MIN;
-    for (int i = threadIdx.x; i < np; i += kBlock) {
-        mn = part[2 * i] < mn ? part[2 * i] : mn;
-        mx = part[2 * i + 1] > mx ? part[2 * i + 1] : mx;
-    }
-    s_min[threadIdx.x] = mn;
-    s_max[threadIdx.x] = mx;
-    __syncthreads();
-    for (int st = kBlock / 2; st > 0; st >>= 1) {
-        if (static_cast<int>(threadIdx.x) < st) {
-            const int64_t a = s_min[threadIdx.x + st], b = s_max[threadIdx.x + st];
-            if (a < s_min[threadIdx.x]) s_min[threadIdx.x] = a;
-            if (b > s_max[threadIdx.x]) s_max[threadIdx.x] = b;
-        }
-        __syncthreads();
-    }
+    __shared__ int64_t sm[3 * kBlock];
+    MinMaxId acc{INT64_MAX, INT64_MIN, INT64_MAX};
+    for (int i = threadIdx.x; i < np; i += kBlock)
+        acc = minmax_id_join(acc, {part[3 * i], part[3 * i + 1], part[3 * i + 2]});
+    const MinMaxId r = block_minmax_id(acc, sm);
     if (threadIdx.x == 0) {
-        out[0] = s_min[0];
-        out[1] = s_max[0];
+        out[0] = r.mn;
+        out[1] = r.mx;
+        out[2] = r.id;
     }
 }
 
@@ -679,10 +690,11 @@ int radix_passes(int begin_bit, int end_bit) {
 // Scratch for the reductions lives in a small per-call static device buffer
 // provided by the caller through `out` (2 * kReduceBlocks int64 / doubles
 // beyond out[0..1]).
-void minmax_i64(const int64_t* v, size_t n, int64_t* out, hipStream_t s) {
+void minmax_ts_min_id(const int64_t* v, const int32_t* a, const int32_t* b, size_t n, int64_t* out,
+                      hipStream_t s) {
     const int nb = reduce_blocks(n);
-    int64_t* part = out + 2;
-    hipLaunchKernelGGL(minmax_partial_kernel, dim3(nb), dim3(kBlock), 0, s, v, n, part);
+    int64_t* part = out + 4;
+    hipLaunchKernelGGL(minmax_partial_kernel, dim3(nb), dim3(kBlock), 0, s, v, a, b, n, part);
     hipLaunchKernelGGL(minmax_final_kernel, dim3(1), dim3(kBlock), 0, s, part, nb, out);
     check_hip(hipGetLastError(), "minmax launch");
 }

@@ -66,6 +66,27 @@ def test_feature_validation_errors():
                               np.array([40], np.int64))
 
 
+def test_negative_node_ids_are_rejected_before_the_store_changes():
+    """The node index is keyed by ids in [0, max_node_id]: a batch holding a
+    negative id raises ValueError and leaves the store and the last batch as
+    they were."""
+    tw = _trw(is_directed=True, global_seed=5)
+    tw.add_multiple_edges(np.array([0, 1, 2], np.int32), np.array([1, 2, 3], np.int32),
+                          np.array([10, 20, 30], np.int64))
+    for s, d in (([4, -1], [5, 6]), ([4, 5], [6, -7]), ([-2**31], [0])):
+        with pytest.raises(ValueError, match="non-negative"):
+            tw.add_multiple_edges(np.array(s, np.int32), np.array(d, np.int32),
+                                  np.arange(40, 40 + len(s), dtype=np.int64))
+    assert tw.get_edge_count() == 3
+    assert np.array_equal(tw.get_node_ids(), [0, 1, 2, 3])
+    nodes, _, lens, _ = tw.get_random_walks_and_times_for_last_batch(
+        max_walk_len=4, walk_bias="Uniform", num_walks_per_node=2)
+    assert nodes.shape == (3 * 2, 4) and set(int(x) for x in nodes[:, 0]) <= {0, 1, 2}
+    tw.add_multiple_edges(np.array([3], np.int32), np.array([4], np.int32),
+                          np.array([40], np.int64))
+    assert tw.get_edge_count() == 4
+
+
 def test_invalid_strings_raise_value_error():
     tw = _trw(is_directed=True)
     tw.add_multiple_edges(np.array([0], np.int32), np.array([1], np.int32),

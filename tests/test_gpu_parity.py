@@ -420,6 +420,23 @@ def test_replay_walks_wide_ids_use_three_scratch_arrays(forward):
                seed_nodes=ids[:500].astype(np.int32), seed=97)
 
 
+@pytest.mark.parametrize("forward", [True, False])
+def test_replay_walks_from_seeds_outside_the_graph(forward):
+    """Seeds that are no node of the graph (negative other than -1, past the
+    largest id, or an id without edges) start no walk; -1 is an unconstrained
+    start; the other seeds walk as usual."""
+    s, d, t = graphs.cfg1(n_nodes=300, n_edges=10_000, seed=61)
+    s = np.where(s == 7, 8, s).astype(np.int32)
+    d = np.where(d == 7, 8, d).astype(np.int32)
+    og, eng = _pair(True, [(s, d, t)])
+    seeds = np.array([-3, 3, 10**7, -1, 7, 299, -2**31, 2**31 - 1, 0], np.int32)
+    got = _walk_case(og, eng, "ExponentialIndex", "Uniform", forward, "nodes", 12, 3,
+                     seed_nodes=seeds, seed=62)
+    lens = got.lens.reshape(seeds.size, 3)
+    assert np.all(lens[[0, 2, 4, 6, 7]] == 0)
+    assert np.all(lens[[1, 3, 8]] >= 1)
+
+
 # ---- normal mode: the in-kernel Philox stream -----------------------------
 
 GLOBAL_SEED = 1234  # the seed _pair gives the engine
