@@ -189,7 +189,9 @@ int32_t trw_abi_version(void);
  * (timestamp, insertion position), window eviction, full index rebuild,
  * optional weights, last-batch uniques.  Host pointers; features are
  * [n, feature_dim] row-major or NULL.  Validation messages follow
- * graph/edge_data.cu:71-89. */
+ * graph/edge_data.cu:71-89.  A batch holding a negative node id is rejected
+ * with TRW_ERR_INVALID_ARGUMENT before the store changes (the reference
+ * indexes its dense node arrays by id and has no such check). */
 trw_status trw_add_edges(void* handle, const int32_t* sources, const int32_t* targets,
                          const int64_t* timestamps, uint64_t n, const float* edge_features,
                          uint64_t feature_dim);
