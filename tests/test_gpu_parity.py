@@ -399,22 +399,25 @@ def test_replay_walks_hub_with_more_groups_than_the_header_holds():
 
 
 @pytest.mark.parametrize("forward", [True, False])
-def test_replay_walks_wide_ids_use_three_scratch_arrays(forward):
-    """Node ids up to 2^22 - 1, 2^21 + 60,000 distinct timestamps and as many
-    edges: a node id, a timestamp rank and an edge id need 22 + 22 + 22 bits,
-    more than one 64-bit scratch word holds, so the walks go through the
-    three 32-bit scratch arrays (every smaller graph here packs them)."""
+@pytest.mark.parametrize("e,n_ts", [((1 << 21) + 60_000, (1 << 21) + 60_000), (1 << 21, (1 << 21) - 1)],
+                         ids=["66_bits", "64_bits"])
+def test_replay_walks_at_the_scratch_packing_limit(forward, e, n_ts):
+    """Node ids up to 2^22 - 1 with E edges and n_ts distinct timestamps.
+    66 bits: a node id, a rank and an edge id need 22 + 22 + 22 bits, more than
+    one 64-bit scratch word holds, so the walks go through the three 32-bit
+    scratch arrays (every smaller graph here packs them).  64 bits: 22 + 21 +
+    21 bits exactly fill the packed word -- the edge id in its top bits and
+    the largest rank one below the all-ones start sentinel."""
     rng = np.random.default_rng(95)
-    e = (1 << 21) + 60_000
     ids = np.concatenate([[0, (1 << 22) - 1],
                           rng.choice(np.arange(1, (1 << 22) - 1), 6_000, replace=False)])
     perm = rng.permutation(ids.size)
     s = ids[graphs.zipf_ids(rng, e, ids.size, 1.5, perm)].astype(np.int32)
     d = ids[graphs.zipf_ids(rng, e, ids.size, 1.5, perm)].astype(np.int32)
-    t = rng.permutation(e).astype(np.int64)
+    t = np.concatenate([rng.permutation(n_ts), rng.integers(0, n_ts, e - n_ts)]).astype(np.int64)
     og, eng = _pair(True, [(s, d, t)])
     assert int(eng.array("active_node_ids").size) == 1 << 22
-    assert int(eng.array("unique_timestamps").size) == e
+    assert int(eng.array("unique_timestamps").size) == n_ts
     _walk_case(og, eng, "ExponentialIndex", "Uniform", forward, "total", 20, 20_000, seed=96)
     _walk_case(og, eng, "Uniform", "Linear", forward, "nodes", 20, 4,
                seed_nodes=ids[:500].astype(np.int32), seed=97)
