@@ -873,11 +873,13 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
 // 50-80).
 //
 // A workgroup owns 64 consecutive scratch columns and a chunk of slots -- the
-// whole row when L <= kLayoutMaxSlots.  Per array it reads 64-column runs of
-// one slot (256 B, coalesced) into an LDS tile of the 32-bit scratch values,
-// then each wave writes whole row runs, converting as it writes (a walk's
-// ranks increase along its row, so the timestamp lookups of one run are close
-// together).  One tile is reused by the three arrays.  Column q holds walk
+// whole row when L <= kLayoutPackedMaxSlots (packed scratch) or
+// kLayoutMaxSlots (three arrays).  Packed scratch is read once, in 64-column
+// runs of one slot (512 B, coalesced), into an LDS tile of 64-bit words from
+// which the three arrays are written; three-array scratch is read per array
+// (256-byte runs) into a 32-bit tile reused by the arrays.  Each wave then
+// writes whole rows, converting as it writes (a walk's ranks increase along
+// its row, so the timestamp lookups of one row are close together).  Column q holds walk
 // order[q] when the walks ran in another order than their ids; its row goes to
 // that walk's place.  In walk-id order the 64 rows are one contiguous span of
 // the output, so no cache line is shared with another workgroup.  Scratch is
