@@ -170,9 +170,43 @@ def run_other_config(k, args):
         res["index_build_edges_per_s"] = edges / (sum(builds) * 1e-3)
         res["value"] = steps / (sum(samples) * 1e-3)
         eng.close()
+        if args.host_ingest:
+            res["host_ingest"] = cfg5_host_ingest(capi, configs)
     else:
         raise SystemExit("--config takes 1, 3, 4 or 5 (2 is the default bench line)")
     print(json.dumps(res))
+
+
+def cfg5_host_ingest(capi, configs):
+    """cfg5's streaming loop from host arrays, wall clock per batch: each batch
+    ingested with trw_add_edges before its sample (the reference's order), or
+    the next batch prefetched (trw_prefetch_edges) while the current batch is
+    sampled.  Walks stay on the device; the first batch is a warm-up."""
+    batches = list(configs.cfg5_batches())
+    out = {}
+    for mode in ("sequential", "prefetched"):
+        eng = capi.Engine(is_directed=True, global_seed=42, shuffle_walk_order=False,
+                          max_time_capacity=3_000_000, enable_temporal_node2vec=True,
+                          node2vec_p=0.5, node2vec_q=2.0)
+        times = []
+        if mode == "prefetched":
+            eng.prefetch_edges(*batches[0])
+        for b in range(len(batches)):
+            t0 = time.perf_counter()
+            if mode == "sequential":
+                eng.add_edges(*batches[b])
+            else:
+                eng.add_prefetched_edges()
+                if b + 1 < len(batches):
+                    eng.prefetch_edges(*batches[b + 1])
+            eng.sample_device("total", 40, "TemporalNode2Vec", 5_000_000,
+                              initial_edge_bias="Uniform", direction="Forward_In_Time")
+            times.append((time.perf_counter() - t0) * 1e3)
+        eng.close()
+        out[mode + "_ms_per_batch"] = sum(times[1:]) / (len(times) - 1)
+        log(f"host ingest, {mode}: {out[mode + '_ms_per_batch']:.2f} ms per batch")
+    out["batch_bytes"] = int(sum(x.nbytes for x in batches[0]))
+    return out
 
 
 def main():
@@ -197,6 +231,10 @@ def main():
                     help="also time the reference's host boundary once through the drop-in "
                          "Python class: numpy edges in (host->device copy included) and "
                          "numpy walks out (device->host copy included)")
+    ap.add_argument("--host-ingest", action="store_true",
+                    help="with --config 5: also time the streaming loop from host arrays, "
+                         "ingesting each batch before its sample or prefetching the next "
+                         "batch while the current one is sampled")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run one plain device copy of this many MiB (torch copy_ "
                          "kernel): the reference point that scales the HBM byte counters of "

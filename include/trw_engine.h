@@ -201,6 +201,22 @@ trw_status trw_add_edges_device(void* handle, const int32_t* d_sources,
                                 uint64_t n, const float* d_edge_features,
                                 uint64_t feature_dim);
 
+/* Ingestion front-end: the host -> device copy of the next batch overlapped
+ * with other calls.  trw_prefetch_edges starts copying a host batch into
+ * engine-owned device buffers on a thread and lanes of its own, and returns;
+ * the caller may then sample (or make any other call) while it copies, and
+ * must keep the arrays alive and unchanged until trw_add_prefetched_edges
+ * returns.  trw_add_prefetched_edges waits for the copy and ingests the batch
+ * exactly as trw_add_edges would have at that point (same validation, same
+ * store and index).  One batch may be pending at a time; trw_destroy waits
+ * for a pending copy.  The reference has no such call: its ingest copies each
+ * batch array with one blocking cudaMemcpy inside add_multiple_edges
+ * (data/buffer.cuh:135-149, core/temporal_random_walk.cu:276-329). */
+trw_status trw_prefetch_edges(void* handle, const int32_t* sources, const int32_t* targets,
+                              const int64_t* timestamps, uint64_t n, const float* edge_features,
+                              uint64_t feature_dim);
+trw_status trw_add_prefetched_edges(void* handle);
+
 /* ---- sampling ------------------------------------------------------------ */
 
 /* Replaces the four get_random_walks_and_times*_cuda samplers

@@ -7,8 +7,9 @@
 #include <stdlib.h>
 
 #include <new>
-#include <type_traits>
 #include <string>
+#include <thread>
+#include <type_traits>
 #include <vector>
 
 #include "engine.h"
@@ -24,6 +25,7 @@ Engine::Engine(const trw_config& c) : cfg(c), device(c.device_id) {
 }
 
 Engine::~Engine() {
+    (void)join_prefetch();  // no copy may outlive the engine
     if (stream) (void)hipStreamSynchronize(stream);
     if (side) (void)hipStreamSynchronize(side);
     for (auto& e : ev)
@@ -200,6 +202,56 @@ trw_status trw_add_edges(void* handle, const int32_t* sources, const int32_t* ta
         }
         e.copy_staged(segs.data(), segs.size(), true);
         e.build(e.stage_src.p, e.stage_dst.p, e.stage_ts.p, df, n, feature_dim);
+    });
+}
+
+trw_status trw_prefetch_edges(void* handle, const int32_t* sources, const int32_t* targets,
+                              const int64_t* timestamps, uint64_t n, const float* edge_features,
+                              uint64_t feature_dim) {
+    return guarded(handle, [&](Engine& e) {
+        if (e.pf_pending)
+            throw trw::InvalidArgument("a prefetched batch is pending: call trw_add_prefetched_edges first");
+        if (n && (!sources || !targets || !timestamps)) throw trw::InvalidArgument("null edge arrays");
+        if (edge_features != nullptr && feature_dim == 0)
+            throw std::runtime_error("edge_features provided but feature_dim is 0");
+        if (edge_features == nullptr && feature_dim != 0)
+            throw std::runtime_error("feature_dim must be 0 when edge_features is not provided");
+        const bool has_feat = edge_features && feature_dim;
+        e.pf_src.resize(n);
+        e.pf_dst.resize(n);
+        e.pf_ts.resize(n);
+        e.pf_feat.resize(has_feat ? n * feature_dim : 0);
+        e.pf_n = n;
+        e.pf_dim = feature_dim;
+        e.pf_has_feat = has_feat;
+        std::vector<trw::HostCopy> segs = {{e.pf_src.p, sources, n * 4},
+                                           {e.pf_dst.p, targets, n * 4},
+                                           {e.pf_ts.p, timestamps, n * 8}};
+        if (has_feat) segs.push_back({e.pf_feat.p, edge_features, n * feature_dim * 4});
+        e.pf_error.clear();
+        e.pf_pending = true;
+        Engine* ep = &e;
+        e.pf_thread = std::thread([ep, segs]() {
+            try {
+                trw::check_hip(hipSetDevice(ep->device), "hipSetDevice");
+                ep->copy_on_lanes(ep->pf_lanes, segs.data(), segs.size(), true, false);
+            } catch (const std::exception& ex) {
+                ep->pf_error = std::string("prefetch: ") + ex.what();
+            }
+        });
+    });
+}
+
+trw_status trw_add_prefetched_edges(void* handle) {
+    return guarded(handle, [&](Engine& e) {
+        if (!e.pf_pending) throw trw::InvalidArgument("no prefetched batch is pending");
+        const std::string err = e.join_prefetch();
+        if (!err.empty()) throw std::runtime_error(err);
+        const size_t n = e.pf_n;
+        if (n == 0) return;  // core/temporal_random_walk.cu:285
+        const float* df = e.pf_has_feat ? e.pf_feat.p : nullptr;
+        trw::validate_batch(e, df, n, e.pf_dim);
+        e.build(e.pf_src.p, e.pf_dst.p, e.pf_ts.p, df, n, e.pf_dim);
     });
 }
 

@@ -56,6 +56,7 @@
 #include <new>
 #include <stdexcept>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/trw_engine.h"
@@ -329,6 +330,18 @@ struct Engine {
     // host handoff lanes
     std::vector<std::unique_ptr<HostLane>> lanes;
 
+    // a host batch being staged into HBM beside other calls (trw_prefetch_edges):
+    // its own lanes and device buffers, and the thread that copies
+    std::vector<std::unique_ptr<HostLane>> pf_lanes;
+    std::thread pf_thread;
+    bool pf_pending = false;
+    std::string pf_error;  // set by the copying thread on failure
+    DBuf<int32_t> pf_src, pf_dst;
+    DBuf<int64_t> pf_ts;
+    DBuf<float> pf_feat;
+    size_t pf_n = 0, pf_dim = 0;
+    bool pf_has_feat = false;
+
     // timings
     hipEvent_t ev[8] = {};
     trw_timings timings{};
@@ -352,6 +365,13 @@ struct Engine {
     // device (pinned staging, several threads); a device -> host copy records
     // timings.handoff_*.  Returns when every byte has landed.
     void copy_staged(const HostCopy* segs, size_t nseg, bool to_device);
+    // The same copy on the lanes ls, without waiting for the engine stream
+    // (small copies go through the first lane's stream): safe beside other
+    // work on the engine as long as no other call uses ls or the spans.
+    void copy_on_lanes(std::vector<std::unique_ptr<HostLane>>& ls, const HostCopy* segs, size_t nseg,
+                       bool to_device, bool engine_order);
+    // Joins a pending prefetch; returns its error text ("" on success).
+    std::string join_prefetch();
 };
 
 // ---- launchers implemented in build.hip / walk.hip -------------------------

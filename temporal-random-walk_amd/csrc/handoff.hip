@@ -80,19 +80,38 @@ void HostLane::init() {
 }
 
 void Engine::copy_staged(const HostCopy* segs, size_t nseg, bool to_device) {
+    copy_on_lanes(lanes, segs, nseg, to_device, true);
+}
+
+std::string Engine::join_prefetch() {
+    if (!pf_pending) return "";
+    if (pf_thread.joinable()) pf_thread.join();
+    pf_pending = false;
+    std::string err;
+    err.swap(pf_error);
+    return err;
+}
+
+void Engine::copy_on_lanes(std::vector<std::unique_ptr<HostLane>>& ls, const HostCopy* segs,
+                           size_t nseg, bool to_device, bool engine_order) {
     size_t total = 0;
     for (size_t i = 0; i < nseg; ++i) total += segs[i].bytes;
     // earlier work on the engine stream may still read or write these buffers
-    sync();
+    if (engine_order) sync();
     const auto t0 = std::chrono::steady_clock::now();
     const hipMemcpyKind kind = to_device ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost;
 
     if (total < kDirectBelow) {
+        hipStream_t st = stream;
+        if (!engine_order) {
+            if (ls.empty()) ls.push_back(std::make_unique<HostLane>());
+            ls[0]->init();
+            st = ls[0]->stream;
+        }
         for (size_t i = 0; i < nseg; ++i)
             if (segs[i].bytes)
-                check_hip(hipMemcpyAsync(segs[i].dst, segs[i].src, segs[i].bytes, kind, stream),
-                          "copy");
-        sync();
+                check_hip(hipMemcpyAsync(segs[i].dst, segs[i].src, segs[i].bytes, kind, st), "copy");
+        check_hip(hipStreamSynchronize(st), "hipStreamSynchronize");
     } else {
         // chunk c of the whole transfer: segment seg_of[c], offset off_of[c]
         std::vector<size_t> seg_of, off_of;
@@ -103,8 +122,8 @@ void Engine::copy_staged(const HostCopy* segs, size_t nseg, bool to_device) {
             }
         const size_t nchunks = seg_of.size();
         const int nt = static_cast<int>(std::min<size_t>(copy_threads(), nchunks));
-        while (lanes.size() < static_cast<size_t>(nt)) lanes.push_back(std::make_unique<HostLane>());
-        for (int t = 0; t < nt; ++t) lanes[t]->init();
+        while (ls.size() < static_cast<size_t>(nt)) ls.push_back(std::make_unique<HostLane>());
+        for (int t = 0; t < nt; ++t) ls[t]->init();
 
         std::atomic<size_t> next{0};
         std::atomic<bool> failed{false};
@@ -165,7 +184,7 @@ void Engine::copy_staged(const HostCopy* segs, size_t nseg, bool to_device) {
             check_hip(hipStreamSynchronize(ln.stream), "hipStreamSynchronize");
         };
         auto worker = [&](int t) {
-            HostLane& ln = *lanes[t];
+            HostLane& ln = *ls[t];
             try {
                 check_hip(hipSetDevice(device), "hipSetDevice");
                 if (to_device) to_dev(ln);
@@ -186,7 +205,7 @@ void Engine::copy_staged(const HostCopy* segs, size_t nseg, bool to_device) {
     }
     const double ms =
         std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
-    if (!to_device) {
+    if (!to_device && engine_order) {
         timings.handoff_ms = ms;
         timings.handoff_bytes = total;
     }

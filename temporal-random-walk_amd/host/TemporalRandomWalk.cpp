@@ -146,6 +146,15 @@ void TemporalRandomWalk::add_multiple_edges(const int* sources, const int* targe
                         feature_dim));
 }
 
+void TemporalRandomWalk::prefetch_edges(const int* sources, const int* targets,
+                                        const int64_t* timestamps, size_t edges_size,
+                                        const float* edge_features, size_t feature_dim) const {
+    check(trw_prefetch_edges(handle_, sources, targets, timestamps, edges_size, edge_features,
+                             feature_dim));
+}
+
+void TemporalRandomWalk::add_prefetched_edges() const { check(trw_add_prefetched_edges(handle_)); }
+
 void TemporalRandomWalk::add_multiple_edges(
     const std::vector<std::tuple<int, int, int64_t>>& edges, const float* edge_features,
     size_t feature_dim, size_t block_dim) const {

@@ -133,6 +133,12 @@ public:
     void add_multiple_edges(const std::vector<std::tuple<int, int, int64_t>>& edges,
                             const float* edge_features = nullptr, size_t feature_dim = 0,
                             size_t block_dim = BLOCK_DIM) const;
+    // The next batch's host -> device copy beside other calls (trw_prefetch_edges);
+    // the arrays must stay alive until add_prefetched_edges returns.
+    void prefetch_edges(const int* sources, const int* targets, const int64_t* timestamps,
+                        size_t edges_size, const float* edge_features = nullptr,
+                        size_t feature_dim = 0) const;
+    void add_prefetched_edges() const;
 
     WalksWithEdgeFeaturesHost get_random_walks_and_times_for_all_nodes(
         int max_walk_len, const RandomPickerType* walk_bias, int num_walks_per_node,

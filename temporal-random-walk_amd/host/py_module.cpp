@@ -112,7 +112,7 @@ void bind_index_picker(py::module& m, const char* name, const char* what) {
 PYBIND11_MODULE(_temporal_random_walk, m) {
     m.doc() = "MI355X temporal random walk engine (drop-in for temporal_random_walk)";
 
-    py::class_<TemporalRandomWalk>(m, "TemporalRandomWalk")
+    py::class_<TemporalRandomWalk>(m, "TemporalRandomWalk", py::dynamic_attr())
         .def(py::init([](bool is_directed, bool use_gpu, std::optional<int64_t> max_time_capacity,
                          std::optional<bool> enable_weight_computation,
                          std::optional<bool> enable_temporal_node2vec,
@@ -183,6 +183,61 @@ PYBIND11_MODULE(_temporal_random_walk, m) {
             },
             "Add multiple edges to the temporal graph.", py::arg("sources"), py::arg("targets"),
             py::arg("timestamps"), py::arg("edge_features") = py::none())
+
+        .def(
+            "prefetch_edges",
+            [](py::object self, const py::array_t<int, py::array::c_style | py::array::forcecast>& sources,
+               const py::array_t<int, py::array::c_style | py::array::forcecast>& targets,
+               const py::array_t<int64_t, py::array::c_style | py::array::forcecast>& timestamps,
+               const py::object& edge_features_obj) {
+                auto& tw = self.cast<TemporalRandomWalk&>();
+                const auto si = sources.request();
+                const auto ti = targets.request();
+                const auto tsi = timestamps.request();
+                if (si.ndim != 1 || ti.ndim != 1 || tsi.ndim != 1)
+                    throw std::runtime_error("Arrays must be 1-dimensional");
+                const size_t n = static_cast<size_t>(si.shape[0]);
+                if (static_cast<size_t>(ti.shape[0]) != n || static_cast<size_t>(tsi.shape[0]) != n)
+                    throw std::runtime_error("All arrays must have the same length");
+                const float* fptr = nullptr;
+                size_t dim = 0;
+                py::object keep_f = py::none();
+                if (!edge_features_obj.is_none()) {
+                    auto f = edge_features_obj
+                                 .cast<py::array_t<float, py::array::c_style | py::array::forcecast>>();
+                    const auto fi = f.request();
+                    if (fi.ndim != 1 && fi.ndim != 2)
+                        throw std::runtime_error("edge_features must be a 1D or 2D NumPy array");
+                    const auto nv = static_cast<size_t>(fi.size);
+                    if (n > 0 && nv % n != 0)
+                        throw std::runtime_error("edge_features size must be num_edges * feature_dim");
+                    dim = n == 0 ? 0 : nv / n;
+                    fptr = static_cast<const float*>(fi.ptr);
+                    keep_f = f;
+                }
+                tw.prefetch_edges(static_cast<const int*>(si.ptr), static_cast<const int*>(ti.ptr),
+                                  static_cast<const int64_t*>(tsi.ptr), n, fptr, dim);
+                // the copy reads these arrays until add_prefetched_edges returns
+                self.attr("_prefetched_arrays") = py::make_tuple(sources, targets, timestamps, keep_f);
+            },
+            "Start copying the next batch to the GPU while other calls (such as sampling) run; "
+            "add_prefetched_edges() then ingests it as add_multiple_edges would.",
+            py::arg("sources"), py::arg("targets"), py::arg("timestamps"),
+            py::arg("edge_features") = py::none())
+
+        .def(
+            "add_prefetched_edges",
+            [](py::object self) {
+                auto& tw = self.cast<TemporalRandomWalk&>();
+                try {
+                    tw.add_prefetched_edges();
+                } catch (...) {
+                    self.attr("_prefetched_arrays") = py::none();
+                    throw;
+                }
+                self.attr("_prefetched_arrays") = py::none();
+            },
+            "Ingest the batch started by prefetch_edges().")
 
         .def(
             "set_node_features",

@@ -61,7 +61,7 @@ ARRAYS = {
 # every symbol include/trw_engine.h declares
 EXPORTS = [
     "trw_create", "trw_destroy", "trw_last_error", "trw_abi_version", "trw_add_edges",
-    "trw_add_edges_device", "trw_sample", "trw_sample_device", "trw_walks_free",
+    "trw_add_edges_device", "trw_prefetch_edges", "trw_add_prefetched_edges", "trw_sample", "trw_sample_device", "trw_walks_free",
     "trw_get_node_count", "trw_get_edge_count", "trw_get_node_ids", "trw_get_node_degrees",
     "trw_get_edges", "trw_get_is_directed", "trw_get_memory_used", "trw_get_feature_dim",
     "trw_get_latest_timestamp", "trw_clear", "trw_get_array", "trw_get_timings",
@@ -164,6 +164,8 @@ def lib():
         L.trw_abi_version.restype = C.c_int32
         L.trw_add_edges.argtypes = [P, P, P, P, C.c_uint64, P, C.c_uint64]
         L.trw_add_edges_device.argtypes = [P, P, P, P, C.c_uint64, P, C.c_uint64]
+        L.trw_prefetch_edges.argtypes = [P, P, P, P, C.c_uint64, P, C.c_uint64]
+        L.trw_add_prefetched_edges.argtypes = [P]
         L.trw_sample.argtypes = [P, C.POINTER(TrwSampleParams), C.POINTER(TrwWalks)]
         L.trw_sample_device.argtypes = [P, C.POINTER(TrwSampleParams), C.POINTER(TrwWalks)]
         L.trw_walks_free.argtypes = [C.POINTER(TrwWalks)]
@@ -350,8 +352,9 @@ class Engine:
 
     def close(self):
         if getattr(self, "h", None):
-            self._L.trw_destroy(self.h)
+            self._L.trw_destroy(self.h)  # waits for a pending prefetch
             self.h = None
+        self._prefetch_keep = None
 
     def __del__(self):
         self.close()
@@ -368,6 +371,29 @@ class Engine:
             dim = f.size // max(len(src), 1)
         _check(self._L.trw_add_edges(self.h, _ptr(src), _ptr(dst), _ptr(ts), len(src), _ptr(f),
                                      dim))
+
+    def prefetch_edges(self, src, dst, ts, features=None):
+        """Starts copying a host batch to the device beside later calls; the
+        arrays are held until add_prefetched_edges."""
+        src = np.ascontiguousarray(src, dtype=np.int32)
+        dst = np.ascontiguousarray(dst, dtype=np.int32)
+        ts = np.ascontiguousarray(ts, dtype=np.int64)
+        dim = 0
+        f = None
+        if features is not None:
+            f = np.ascontiguousarray(features, dtype=np.float32)
+            dim = f.size // max(len(src), 1)
+        _check(self._L.trw_prefetch_edges(self.h, _ptr(src), _ptr(dst), _ptr(ts), len(src),
+                                          _ptr(f), dim))
+        self._prefetch_keep = (src, dst, ts, f)
+
+    def add_prefetched_edges(self):
+        # the call joins the copy (or finds none pending) before it returns,
+        # so the held arrays may go either way
+        try:
+            _check(self._L.trw_add_prefetched_edges(self.h))
+        finally:
+            self._prefetch_keep = None
 
     def add_edges_device(self, src_ptr, dst_ptr, ts_ptr, n, feat_ptr=None, dim=0):
         _check(self._L.trw_add_edges_device(self.h, src_ptr, dst_ptr, ts_ptr, int(n), feat_ptr,

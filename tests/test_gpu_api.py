@@ -221,3 +221,94 @@ def test_networkx_round_trip():
     tw.add_edges_from_networkx(g)
     h = tw.to_networkx()
     assert sorted(h.edges(data="timestamp")) == [(1, 2, 5), (2, 3, 7)]
+
+
+def _stream_batches(n_batches, n_edges, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    for k in range(n_batches):
+        s = graphs.zipf_ids(rng, n_edges, 200_000, 1.8)
+        d = graphs.zipf_ids(rng, n_edges, 200_000, 1.8)
+        t = rng.integers(k * 1_000_000, (k + 1) * 1_000_000, n_edges).astype(np.int64)
+        out.append((s, d, t))
+    return out
+
+
+def test_prefetched_batches_overlap_sampling_and_match_direct_ingest():
+    """trw_prefetch_edges copies the next host batch while a sample runs;
+    trw_add_prefetched_edges then ingests it.  Store, index and walks equal
+    those of plain trw_add_edges of the same batches, through the staged lanes
+    (batches above 32 MiB) and the direct copy (a small batch), with a rolling
+    window evicting old edges."""
+    from temporal_random_walk import capi
+    from tests.test_gpu_parity import INDEX_ARRAYS
+
+    batches = _stream_batches(3, 3_000_000, 41) + _stream_batches(1, 50_000, 42)
+    kw = dict(is_directed=True, global_seed=9, shuffle_walk_order=False,
+              max_time_capacity=2_000_000)
+    a, b = capi.Engine(**kw), capi.Engine(**kw)
+    a.add_edges(*batches[0])
+    b.add_edges(*batches[0])
+    for s, d, t in batches[1:]:
+        a.prefetch_edges(s, d, t)
+        # the copy runs beside this sample; the store is not yet touched
+        a.sample_device("total", 20, "ExponentialIndex", 500_000, initial_edge_bias="Uniform")
+        a.add_prefetched_edges()
+        b.add_edges(s, d, t)
+        for name in ("sources", "targets", "timestamps", *INDEX_ARRAYS):
+            assert np.array_equal(a.array(name), b.array(name)), name
+    dr = graphs.draws(20_000, 16, seed=43)
+    wa = a.sample("total", 16, "ExponentialIndex", 20_000, replay=dr, shuffle=False)
+    wb = b.sample("total", 16, "ExponentialIndex", 20_000, replay=dr, shuffle=False)
+    for k in ("nodes", "timestamps", "lens", "edge_ids"):
+        assert np.array_equal(getattr(wa, k), getattr(wb, k)), k
+    a.close()
+    b.close()
+
+
+def test_prefetch_errors_and_validation():
+    from temporal_random_walk import capi
+
+    e = capi.Engine(is_directed=True, global_seed=1)
+    e.add_edges(np.array([0, 1], np.int32), np.array([1, 2], np.int32), np.array([1, 2], np.int64))
+    with pytest.raises(ValueError, match="no prefetched batch"):
+        e.add_prefetched_edges()
+    e.prefetch_edges(np.array([2], np.int32), np.array([3], np.int32), np.array([3], np.int64))
+    with pytest.raises(ValueError, match="pending"):
+        e.prefetch_edges(np.array([3], np.int32), np.array([4], np.int32), np.array([4], np.int64))
+    e.add_prefetched_edges()
+    assert e.edge_count() == 3
+    # validated when ingested, against the store as it is then
+    e.prefetch_edges(np.array([4, -1], np.int32), np.array([5, 6], np.int32),
+                     np.array([5, 6], np.int64))
+    with pytest.raises(ValueError, match="non-negative"):
+        e.add_prefetched_edges()
+    assert e.edge_count() == 3
+    e.prefetch_edges(np.array([4], np.int32), np.array([5], np.int32), np.array([5], np.int64),
+                     np.array([[1.0, 2.0]], np.float32))
+    with pytest.raises(Exception, match="feature_dim mismatch"):
+        e.add_prefetched_edges()
+    # a pending copy is waited for when the engine goes away
+    big = _stream_batches(1, 3_000_000, 44)[0]
+    e.prefetch_edges(*big)
+    e.close()
+
+
+def test_python_class_prefetch_matches_add_multiple_edges():
+    batches = _stream_batches(2, 3_000_000, 45)
+    tw_a = _trw(is_directed=True, global_seed=17, shuffle_walk_order=False)
+    tw_b = _trw(is_directed=True, global_seed=17, shuffle_walk_order=False)
+    tw_a.add_multiple_edges(*batches[0])
+    tw_b.add_multiple_edges(*batches[0])
+    # int64 ids are converted for the copy; the converted arrays are held
+    s, d, t = batches[1]
+    tw_a.prefetch_edges(s.astype(np.int64), d, t)
+    tw_a.get_random_walks_and_times(max_walk_len=10, walk_bias="Uniform", num_walks_total=100_000)
+    tw_a.add_prefetched_edges()
+    tw_b.add_multiple_edges(s, d, t)
+    assert tw_a.get_edge_count() == tw_b.get_edge_count()
+    out = [tw.get_random_walks_and_times_for_last_batch(max_walk_len=12, walk_bias="Linear",
+                                                         num_walks_per_node=1)
+           for tw in (tw_a, tw_b)]
+    for x, y in zip(out[0][:3], out[1][:3]):
+        assert np.array_equal(x, y)
