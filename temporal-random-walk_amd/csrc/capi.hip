@@ -229,7 +229,6 @@ trw_status trw_prefetch_edges(void* handle, const int32_t* sources, const int32_
                                            {e.pf_ts.p, timestamps, n * 8}};
         if (has_feat) segs.push_back({e.pf_feat.p, edge_features, n * feature_dim * 4});
         e.pf_error.clear();
-        e.pf_pending = true;
         Engine* ep = &e;
         e.pf_thread = std::thread([ep, segs]() {
             try {
@@ -239,6 +238,7 @@ trw_status trw_prefetch_edges(void* handle, const int32_t* sources, const int32_
                 ep->pf_error = std::string("prefetch: ") + ex.what();
             }
         });
+        e.pf_pending = true;  // only once the copy is under way
     });
 }
 
