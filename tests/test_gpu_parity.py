@@ -257,6 +257,35 @@ def test_normal_mode_invariants_and_features():
         assert np.all(w.edge_features[i, n - 1:] == 0)
 
 
+@pytest.mark.parametrize("dim", [8, 6])
+@pytest.mark.parametrize("forward", [True, False])
+def test_walk_features_through_every_layout_path(dim, forward):
+    """Edge features of every walk slot: dims that are multiples of 4 are
+    written by the layout pass from the edge ids it holds (packed scratch
+    here), others by a gather over the laid-out edge ids.  Rows of one chunk
+    (L = 20) and of several (L = 150), reversed for backward walks, in both
+    processing orders: each row's features are the store's rows of its edge
+    ids, zeros past its length."""
+    s, d, t = graphs.cfg1(n_nodes=200, n_edges=100_000, seed=18)
+    rng = np.random.default_rng(18)
+    feat = rng.standard_normal((len(s), dim)).astype(np.float32)
+    og, eng = _pair(True, [(s, d, t)], features=[feat])
+    store_f = eng.array("edge_features").reshape(-1, dim)
+    direction = "Forward_In_Time" if forward else "Backward_In_Time"
+    for L in (20, 150):
+        for order in ("walk_id", "start_time"):
+            w = eng.sample("total", L, "ExponentialIndex", 3_000, initial_edge_bias="Uniform",
+                           direction=direction, walk_order=order)
+            lens = w.lens.astype(np.int64)
+            assert w.edge_features.shape == (3_000, L - 1, dim)
+            assert lens.max() > 100 or L == 20
+            for i in range(0, 3_000, 5):
+                n = int(lens[i])
+                e = w.edge_ids[i, :max(n - 1, 0)]
+                np.testing.assert_array_equal(w.edge_features[i, :len(e)], store_f[e])
+                assert np.all(w.edge_features[i, len(e):] == 0)
+
+
 def test_host_handoff_matches_device_buffers():
     """trw_sample's staged, multi-threaded host delivery (used above 32 MiB)
     returns exactly the bytes trw_sample_device leaves in HBM; a fixed
