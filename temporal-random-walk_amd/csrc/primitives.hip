@@ -280,8 +280,7 @@ __global__ __launch_bounds__(kBlock) void radix_upsweep_kernel(const K* __restri
                                                                size_t n, int bit, int db,
                                                                uint32_t dmask,
                                                                uint32_t* __restrict__ hist,
-                                                               size_t nb,
-                                                               uint32_t* __restrict__ digit_tot) {
+                                                               size_t nb) {
     extern __shared__ uint32_t s_cnt[];  // [kWaves][R]
     const int R = 1 << db;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -312,8 +311,20 @@ __global__ __launch_bounds__(kBlock) void radix_upsweep_kernel(const K* __restri
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) tot += s_cnt[w * R + d];
         hist[static_cast<size_t>(d) * nb + blockIdx.x] = tot;
-        if (tot) atomicAdd(digit_tot + d, tot);
     }
+}
+
+// One workgroup per digit d: the digit's total over the workgroups' counts
+// (its contiguous histogram row).
+__global__ __launch_bounds__(kBlock) void radix_digit_totals_kernel(const uint32_t* __restrict__ hist,
+                                                                    size_t nb,
+                                                                    uint32_t* __restrict__ digit_tot) {
+    __shared__ uint32_t s_wave[kWaves];
+    const uint32_t* row = hist + static_cast<size_t>(blockIdx.x) * nb;
+    uint32_t acc = 0;
+    for (size_t i = threadIdx.x; i < nb; i += kBlock) acc += row[i];
+    const uint32_t tot = block_sum<uint32_t, OpSum>(acc, s_wave);
+    if (threadIdx.x == 0) digit_tot[blockIdx.x] = tot;
 }
 
 // One workgroup per digit d: the exclusive scan of the workgroups' counts of
@@ -494,8 +505,6 @@ int radix_sort_impl(K* keys0, V* vals0, K* keys1, V* vals1, size_t n,
     const int db = sort_digit_bits(end_bit - begin_bit);
     const int R = 1 << db;
     uint32_t* totals = hist + nb * kMaxRadix;
-    hipLaunchKernelGGL(fill_u32_kernel, dim3((passes * R + kBlock - 1) / kBlock), dim3(kBlock), 0,
-                       s, totals, static_cast<size_t>(passes * R), 0u);
     const size_t lds_up = static_cast<size_t>(kWaves) * R * sizeof(uint32_t);
     const size_t lds_sc = radix_scatter_lds<K, V>(R);
     int cur = 0;
@@ -508,7 +517,8 @@ int radix_sort_impl(K* keys0, V* vals0, K* keys1, V* vals1, size_t n,
         const uint32_t dmask = (1u << w) - 1u;
         uint32_t* tot = totals + pass * R;
         hipLaunchKernelGGL((radix_upsweep_kernel<K>), dim3(nb), dim3(kBlock), lds_up, s, kb[cur],
-                           n, bit, db, dmask, hist, nb, tot);
+                           n, bit, db, dmask, hist, nb);
+        hipLaunchKernelGGL(radix_digit_totals_kernel, dim3(R), dim3(kBlock), 0, s, hist, nb, tot);
         hipLaunchKernelGGL(radix_offsets_kernel, dim3(R), dim3(kBlock), 0, s, hist, nb, tot);
         hipLaunchKernelGGL((radix_scatter_kernel<K, V>), dim3(nb), dim3(kBlock), lds_sc, s,
                            kb[cur], vb[cur], kb[cur ^ 1], vb[cur ^ 1], n, bit, db, dmask, hist,
