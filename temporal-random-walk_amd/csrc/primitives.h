@@ -1,9 +1,10 @@
 // primitives.h -- device-wide scan and stable radix sort for the index build.
 //
 // Hand-written for CDNA4 (wave64): no rocPRIM / hipCUB.  The radix sort is a
-// classic LSD sort with three launches per digit pass (tile histograms plus
-// digit totals, one workgroup per digit scanning its histogram row, stable
-// scatter); a sort of B key bits takes the fewest passes of at most 10-bit
+// classic LSD sort with four launches per digit pass (tile histograms; the
+// digit totals, one workgroup per digit summing its histogram row; one
+// workgroup per digit scanning that row; stable scatter); a sort of B key
+// bits takes the fewest passes of at most 10-bit
 // digits, the bits split evenly.  Stable ranking inside a tile uses wave-level
 // multisplit: one 64-lane ballot per digit bit gives every lane the mask of
 // lanes holding the same digit, so the in-row rank is a popcount and a single

@@ -363,11 +363,6 @@ __global__ __launch_bounds__(kBlock) void radix_offsets_kernel(uint32_t* __restr
     }
 }
 
-__global__ void fill_u32_kernel(uint32_t* __restrict__ p, size_t n, uint32_t v) {
-    const size_t i = blockIdx.x * static_cast<size_t>(kBlock) + threadIdx.x;
-    if (i < n) p[i] = v;
-}
-
 // Stable scatter of one digit pass.  A tile's keys are first placed in LDS in
 // their sorted order within the tile (digit, then wave, then rank), then
 // written out by consecutive threads: the keys of one digit leave as one
