@@ -13,12 +13,27 @@ walks stay in HBM (device-resident boundary).
 Prints ONE JSON line.  `value` = walk steps/s (sum of walk lengths, the
 reference's definition, test_run/walk_sampling_speed_test.cpp:39-50) over the
 wall time of the sampling calls; index-build edges/s is reported beside it.
+`roofline` is the walk kernel's compulsory HBM bytes per launch over its
+launch time (HIP events), against the 8 TB/s peak; `traffic` is the HBM
+traffic one launch measured with rocprofv3 counters, read from
+profiles/walk_kernel_cfg2_pmc.json only while the kernel sources still hash to
+what that profile measured.  `host_boundary` times the reference's own
+boundary once (numpy in, numpy out), and `cpu_baseline` the oracle on the
+host cores, in a child process.
+
+`--summarize-pmc` turns rocprofv3 counter runs into the profiles/*_pmc.json
+summaries this line reads (see its help).
 """
 from __future__ import annotations
 
 import argparse
+import glob
+import hashlib
 import json
 import os
+import platform
+import statistics
+import subprocess
 import sys
 import time
 
@@ -31,6 +46,21 @@ for _p in (ROOT, PKG):
 METRIC = "sampled walk steps/s + index-build edges/s, 20M-edge power-law graph, 1 GPU"
 HBM_PEAK_GBS = 8000.0
 PMC_FILE = os.path.join(ROOT, "profiles", "walk_kernel_cfg2_pmc.json")
+CSRC = os.path.join(PKG, "csrc")
+# the sources each profiled kernel family is compiled from: a counter profile
+# describes the code only while these hash to what it measured
+KERNEL_SOURCES = {
+    "walk": ["walk.hip", "trw_device.h", "engine.h"],
+    "build": ["build.hip", "primitives.hip", "primitives.h", "engine.h"],
+}
+
+
+def sources_sha256(family):
+    h = hashlib.sha256()
+    for name in KERNEL_SOURCES[family]:
+        with open(os.path.join(CSRC, name), "rb") as f:
+            h.update(name.encode() + b"\0" + f.read() + b"\0")
+    return h.hexdigest()
 
 
 def log(*a):
@@ -50,37 +80,157 @@ def index_algorithmic_bytes(E, Vc, T, g_o, g_i):
     return 16 * E + 16 * E + 8 * E + 8 * E + 8 * (g_o + g_i) + 32 * Vc + 4 * (Vc - 1) + 16 * T + 8
 
 
-def cpu_baseline(src, dst, ts, n_walks, L, threads):
-    """The oracle (C restatement of the reference CPU path) on the host cores:
-    full ingest of the graph (single-threaded, as written) and a bounded
-    sample of walks (OpenMP over walks), draw generation included as in the
-    reference's CPU sampler."""
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline_child(args):
+    """Runs in a child process started by cpu_baseline() (no GPU is touched):
+    the oracle -- the C restatement of the reference CPU path -- on the host
+    cores with OpenMP, on the cfg2 graph.  One untimed warm-up, then the
+    median of `reps` timed rounds of each leg: the full ingest of all 20M
+    edges, and a bounded sample of walks (draw generation included, as in the
+    reference's CPU sampler, core/temporal_random_walk.cu:568-569).  Prints one
+    JSON object."""
     import numpy as np
     from oracle import pyoracle as po
 
-    og = po.OracleGraph(True)
-    t0 = time.perf_counter()
-    og.add_edges(src, dst, ts)
-    t_build = time.perf_counter() - t0
-    t0 = time.perf_counter()
-    draws = np.random.default_rng(1).random(n_walks * (1 + 2 * L))
-    starts = -np.ones(n_walks, dtype=np.int32)
-    w = og.walks(L, "ExponentialIndex", "Uniform", True, starts, draws, num_threads=threads)
-    t_walk = time.perf_counter() - t0
-    steps = int(w.lens.sum())
+    src, dst, ts = make_cfg2(args.nodes, args.edges, args.timestamps)
+    threads = args.cpu_threads
+    L, n_walks = args.walk_len, args.cpu_walks
+    builds, walks = [], []
+    og = None
+    for r in range(1 + args.cpu_reps):
+        og = po.OracleGraph(True)
+        t0 = time.perf_counter()
+        og.add_edges(src, dst, ts, num_threads=threads)
+        tb = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        draws = np.random.default_rng(1 + r).random(n_walks * (1 + 2 * L))
+        starts = -np.ones(n_walks, dtype=np.int32)
+        w = og.walks(L, "ExponentialIndex", "Uniform", True, starts, draws, num_threads=threads)
+        tw = time.perf_counter() - t0
+        steps = int(w.lens.sum())
+        del w, draws
+        if r:  # round 0 warms up
+            builds.append(tb)
+            walks.append(steps / tw)
+        print(f"[bench cpu] round {r}: build {tb:.2f} s, {steps} walk steps in {tw:.2f} s",
+              file=sys.stderr, flush=True)
+    print(json.dumps({"walk_steps_per_s": statistics.median(walks),
+                      "build_s": statistics.median(builds),
+                      "walk_steps_per_s_all": walks, "build_s_all": builds,
+                      "edges": int(len(src))}))
+
+
+def cpu_baseline(args):
+    """The oracle on the host cores, timed in a child process whose OpenMP
+    runtime starts with OMP_PROC_BIND=spread and OMP_PLACES=cores (this
+    process has already loaded torch's).  Threads: OMP_NUM_THREADS when set
+    (the GPU box sets it to its CPU share per GPU), else every core."""
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    env = dict(os.environ, OMP_NUM_THREADS=str(threads), OMP_PROC_BIND="spread",
+               OMP_PLACES="cores")
+    cmd = [sys.executable, os.path.abspath(__file__), "--cpu-baseline-child",
+           "--cpu-threads", str(threads), "--cpu-walks", str(args.cpu_walks),
+           "--cpu-reps", str(args.cpu_reps), "--edges", str(args.edges),
+           "--nodes", str(args.nodes), "--timestamps", str(args.timestamps),
+           "--walk-len", str(args.walk_len)]
+    log(f"cpu baseline: {threads} threads, {args.cpu_walks} walks, median of {args.cpu_reps}")
+    r = subprocess.run(cmd, env=env, stdout=subprocess.PIPE, text=True, check=True)
+    res = json.loads(r.stdout.strip().splitlines()[-1])
     return {
-        "value": steps / t_walk,
+        "value": res["walk_steps_per_s"],
         "unit": "walk steps/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"oracle/trw_oracle.c: {n_walks} walks (L={L}, ExponentialIndex/Uniform, fwd) "
-                   f"on the full cfg2 graph with {threads} OpenMP threads, draw generation "
-                   f"included; index build of all {len(src)} edges single-threaded"),
-        "index_build_edges_per_s": len(src) / t_build,
-        "index_build_cores": 1,
-        "walk_s": t_walk,
-        "build_s": t_build,
+        "sample": (f"oracle/trw_oracle.c on the GPU box's host: {args.cpu_walks} walks "
+                   f"(L={args.walk_len}, ExponentialIndex/Uniform, fwd) on the full cfg2 graph, "
+                   f"draw generation included, and the ingest of all {res['edges']} edges; "
+                   f"{threads} OpenMP threads (OMP_PROC_BIND=spread, OMP_PLACES=cores), "
+                   f"median of {args.cpu_reps} rounds after a warm-up"),
+        "index_build_edges_per_s": res["edges"] / res["build_s"],
+        "index_build_cores": threads,
+        "walk_steps_per_s_rounds": res["walk_steps_per_s_all"],
+        "build_s_rounds": res["build_s_all"],
+        "nproc": os.cpu_count(),
+        "affinity_cpus": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None,
+        "cpu_model": cpu_model(),
     }
+
+
+def summarize_pmc(args):
+    """Summarises rocprofv3 counter runs of one kernel into a JSON profile.
+
+    Each --pmc-dir holds one `rocprofv3 --pmc ... -f csv -d DIR -o pmc -- python3
+    bench.py ...` run.  Counter values are summed over a dispatch's rows
+    (instances), then averaged over the dispatches whose kernel name contains
+    --kernel.  FETCH_SIZE and WRITE_SIZE (KiB per dispatch) are scaled by what
+    the same counter read for the plain device copy of --copy-calibration-mib
+    MiB that the run made first (the largest __amd_rocclr_copyBuffer
+    dispatch), so bytes = KiB * (copy bytes / copy KiB).  The profile is
+    stamped with the sha256 of the kernel family's sources."""
+    per = {}  # counter -> list of per-dispatch values of the kernel
+    copy = {}
+    for d in args.pmc_dir:
+        files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+        if not files:
+            raise SystemExit(f"no counter_collection.csv under {d}")
+        import csv
+        rows = {}
+        for fn in files:
+            with open(fn) as f:
+                for r in csv.DictReader(f):
+                    key = (fn, r["Dispatch_Id"], r["Kernel_Name"], r["Counter_Name"])
+                    rows[key] = rows.get(key, 0.0) + float(r["Counter_Value"])
+        for (fn, disp, kname, cname), v in rows.items():
+            if args.kernel in kname:
+                per.setdefault(cname, []).append(v)
+            elif "copyBuffer" in kname:
+                copy[cname] = max(copy.get(cname, 0.0), v)
+    if not per:
+        raise SystemExit(f"no dispatch of a kernel named like {args.kernel!r}")
+    avg = {c: sum(v) / len(v) for c, v in per.items()}
+    out = {"kernel": args.kernel, "workload": args.workload, "command": args.command,
+           "dispatches": max(len(v) for v in per.values()),
+           "sources_sha256": sources_sha256(args.family), "source_family": args.family,
+           "counters": avg}
+    cal = args.copy_calibration_mib * (1 << 20)
+    for c, key in (("FETCH_SIZE", "hbm_read_bytes_per_launch"),
+                   ("WRITE_SIZE", "hbm_write_bytes_per_launch")):
+        if c in avg and copy.get(c):
+            scale = cal / (copy[c] * 1024)
+            out[c.lower() + "_scale"] = scale
+            out[key] = avg[c] * 1024 * scale
+    if "hbm_read_bytes_per_launch" in out and "hbm_write_bytes_per_launch" in out:
+        out["hbm_bytes_per_launch"] = out["hbm_read_bytes_per_launch"] + out["hbm_write_bytes_per_launch"]
+    if "TCC_HIT_sum" in avg and "TCC_MISS_sum" in avg:
+        out["l2_hit_rate"] = avg["TCC_HIT_sum"] / (avg["TCC_HIT_sum"] + avg["TCC_MISS_sum"])
+    if os.path.exists(args.summarize_pmc):
+        with open(args.summarize_pmc) as f:
+            old = json.load(f)
+        if old.get("sources_sha256") == out["sources_sha256"] and old.get("kernel") == args.kernel:
+            # a profile built up over several counter runs of the same sources
+            merged = dict(old)
+            merged.update({k: v for k, v in out.items() if k != "counters"})
+            merged["counters"] = dict(old.get("counters", {}), **avg)
+            for k in ("hbm_read_bytes_per_launch", "hbm_write_bytes_per_launch"):
+                if k not in out and k in old:
+                    merged[k] = old[k]
+            if "hbm_read_bytes_per_launch" in merged and "hbm_write_bytes_per_launch" in merged:
+                merged["hbm_bytes_per_launch"] = (merged["hbm_read_bytes_per_launch"] +
+                                                  merged["hbm_write_bytes_per_launch"])
+            out = merged
+    with open(args.summarize_pmc, "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps(out, indent=1))
 
 
 def run_other_config(k, args):
@@ -225,12 +375,25 @@ def main():
                     help="2 (default): the cfg2 bench line; 1, 3, 4 or 5: time that BASELINE "
                          "workload instead (device timings, one JSON line)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-walks", type=int, default=2_500_000,
-                    help="walks of the bounded CPU-baseline sample (about 10 s on 16 threads)")
-    ap.add_argument("--host-boundary", action="store_true",
-                    help="also time the reference's host boundary once through the drop-in "
-                         "Python class: numpy edges in (host->device copy included) and "
-                         "numpy walks out (device->host copy included)")
+    ap.add_argument("--cpu-walks", type=int, default=1_500_000,
+                    help="walks of the bounded CPU-baseline sample (about 5 s per round on "
+                         "16 threads)")
+    ap.add_argument("--cpu-reps", type=int, default=3,
+                    help="timed CPU-baseline rounds (the median is reported)")
+    ap.add_argument("--cpu-threads", type=int, default=0, help=argparse.SUPPRESS)
+    ap.add_argument("--cpu-baseline-child", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--no-host-boundary", action="store_true",
+                    help="skip timing the reference's host boundary (numpy edges in through "
+                         "the drop-in Python class, host->device copy included, and numpy "
+                         "walks out, device->host copy included)")
+    ap.add_argument("--summarize-pmc", metavar="OUT_JSON", default=None,
+                    help="summarise rocprofv3 counter runs (--pmc-dir) of one kernel "
+                         "(--kernel) into OUT_JSON, then exit; touches no GPU")
+    ap.add_argument("--pmc-dir", action="append", default=[])
+    ap.add_argument("--kernel", default="walk_kernel<")
+    ap.add_argument("--family", default="walk", choices=sorted(KERNEL_SOURCES))
+    ap.add_argument("--workload", default="")
+    ap.add_argument("--command", default="")
     ap.add_argument("--host-ingest", action="store_true",
                     help="with --config 5: also time the streaming loop from host arrays, "
                          "ingesting each batch before its sample or prefetching the next "
@@ -240,6 +403,13 @@ def main():
                          "kernel): the reference point that scales the HBM byte counters of "
                          "a --pmc profile")
     args = ap.parse_args()
+
+    if args.summarize_pmc:
+        summarize_pmc(args)
+        return
+    if args.cpu_baseline_child:
+        cpu_baseline_child(args)
+        return
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -313,13 +483,15 @@ def main():
     build_eps = E * args.steps / sum(builds)
     walk_kernel_ms = sum(t["walk_kernel_ms"] for t in tims) / len(tims)
     build_dev_ms = sum(t["build_ms"] for t in tims) / len(tims)
-    # roofline.achieved: the per-unit algorithmic bytes with the reference's
-    # element types (per hop 72 + 8*ceil(log2(G_u+1)) B, per walk 8 B + the start
-    # + the first two slots' output), summed over this launch's walks on the
-    # device; the same sum restated for this engine's 4-byte positions and ranks
-    # is reported beside it.
-    achieved = stats["reference_bytes"] / (walk_kernel_ms * 1e-3) / 1e9
-    achieved_engine = stats["algorithmic_bytes"] / (walk_kernel_ms * 1e-3) / 1e9
+    # roofline: the walk kernel's compulsory bytes -- inputs and the sampled
+    # direction's index read once, scratch slots and lengths written once
+    # (trw_get_walk_stats) -- over its launch time (HIP events on the engine's
+    # stream).  The per-hop demand bytes (every walk's reads, 72 + 8*probes B
+    # with the reference's types) are reported beside it: walks running side
+    # by side share most of those lines in L1/L2.
+    wk_s = walk_kernel_ms * 1e-3
+    compulsory = stats["compulsory_read_bytes"] + stats["compulsory_write_bytes"]
+    achieved = compulsory / wk_s / 1e9
 
     g_o = len(eng.array("node_ts_group_outbound_offsets"))
     g_i = len(eng.array("node_ts_group_inbound_offsets"))
@@ -327,12 +499,18 @@ def main():
     T = len(eng.array("unique_timestamps"))
     idx_bytes = index_algorithmic_bytes(E, Vc, T, g_o, g_i)
 
-    traffic = l2_hit = None
-    if os.path.exists(PMC_FILE):
-        with open(PMC_FILE) as f:
-            pmc = json.load(f)
-        traffic = pmc.get("hbm_bytes_per_launch")
-        l2_hit = pmc.get("l2_hit_rate")
+    def pmc_profile(path, family):
+        """(profile, current): current is False when the kernel sources no
+        longer hash to what the profile measured."""
+        if not os.path.exists(path):
+            return None, False
+        with open(path) as f:
+            prof = json.load(f)
+        return prof, prof.get("sources_sha256") == sources_sha256(family)
+
+    pmc, pmc_current = pmc_profile(PMC_FILE, "walk")
+    traffic = pmc.get("hbm_bytes_per_launch") if pmc and pmc_current else None
+    l2_hit = pmc.get("l2_hit_rate") if pmc and pmc_current else None
 
     result = {
         "metric": METRIC,
@@ -375,20 +553,36 @@ def main():
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": traffic,
             "kernel": "walk_kernel<true,true,0>",
-            "algorithmic_bytes_per_launch": stats["reference_bytes"],
-            "engine_types_bytes_per_launch": stats["algorithmic_bytes"],
-            "engine_types_achieved": achieved_engine,
-            "traffic_GB_per_s": (traffic / (walk_kernel_ms * 1e-3) / 1e9) if traffic else None,
+            "algorithmic_bytes_per_launch": compulsory,
+            "compulsory_read_bytes": stats["compulsory_read_bytes"],
+            "compulsory_write_bytes": stats["compulsory_write_bytes"],
+            "demand_bytes_per_launch": stats["reference_bytes"],
+            "demand_engine_types_bytes_per_launch": stats["algorithmic_bytes"],
+            "demand_GB_per_s": stats["reference_bytes"] / wk_s / 1e9,
+            "traffic_GB_per_s": (traffic / wk_s / 1e9) if traffic else None,
+            "traffic_frac": (traffic / wk_s / 1e9 / HBM_PEAK_GBS) if traffic else None,
             "l2_hit_rate": l2_hit,
-            "note": "algorithmic bytes count every walk's per-hop index reads (72 + 8*probes B "
-                    "with the reference's types); walks run in start-time order share those "
-                    "lines, so most are L2 hits and frac can exceed 1. traffic (PMC, L2 <-> "
-                    "fabric bytes of one launch) over the launch time is the HBM-side rate.",
+            "pmc_profile": os.path.relpath(PMC_FILE, ROOT) if pmc else None,
+            "pmc_current": pmc_current,
+            "note": "algorithmic bytes = compulsory bytes of one launch (start states, "
+                    "processing order and the sampled direction's index arrays read once; "
+                    "packed scratch and walk lengths written once). demand bytes count every "
+                    "walk's per-hop reads (72 + 8*ceil(log2(G+1)) B in the reference's types) "
+                    "and exceed the HBM rate because walks in start-time order share lines "
+                    "in L1/L2. traffic = FETCH_SIZE + WRITE_SIZE of one launch from the "
+                    "rocprofv3 profile, null when the walk sources changed since it was "
+                    "measured.",
         },
     }
+    bpmc, bpmc_current = pmc_profile(os.path.join(ROOT, "profiles", "index_build_cfg2_pmc.json"),
+                                     "build")
+    if bpmc and bpmc_current:
+        result["index_roofline"]["traffic"] = bpmc.get("hbm_bytes_per_launch")
+        result["index_roofline"]["l2_hit_rate"] = bpmc.get("l2_hit_rate")
+        result["index_roofline"]["pmc_profile"] = "profiles/index_build_cfg2_pmc.json"
 
     eng.close()
-    if args.host_boundary:
+    if not args.no_host_boundary:
         from temporal_random_walk import TemporalRandomWalk
 
         log("host boundary (PCIe-inclusive) run")
@@ -439,10 +633,8 @@ def main():
         }
 
     if not args.no_cpu_baseline:
-        threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
-        log(f"cpu baseline ({threads} threads)")
-        result["cpu_baseline"] = cpu_baseline(src, dst, ts, args.cpu_walks, args.walk_len,
-                                              threads)
+        del d_src, d_dst, d_ts
+        result["cpu_baseline"] = cpu_baseline(args)
     else:
         result["cpu_baseline"] = None
 

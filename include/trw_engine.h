@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TRW_ABI_VERSION 3
+#define TRW_ABI_VERSION 4
 
 typedef enum trw_status {
     TRW_OK = 0,
@@ -187,7 +187,9 @@ int32_t trw_abi_version(void);
 /* Replaces temporal_random_walk::add_multiple_edges
  * (core/temporal_random_walk.cu:276-329): append, stable sort by
  * (timestamp, insertion position), window eviction, full index rebuild,
- * optional weights, last-batch uniques.  Host pointers; features are
+ * optional weights, last-batch uniques.  A failure after the batch passed its
+ * checks (device out of memory, a HIP error) leaves the handle empty, as after
+ * trw_clear.  Host pointers; features are
  * [n, feature_dim] row-major or NULL.  Validation messages follow
  * graph/edge_data.cu:71-89.  A batch holding a negative node id is rejected
  * with TRW_ERR_INVALID_ARGUMENT before the store changes (the reference
@@ -283,15 +285,38 @@ trw_status trw_get_stream(void* handle, void** out_stream);
  * 32-bit edge id); per hop 36 + 4 p_u B (the node's group range 8 B, one 4 B
  * rank per probe, the picked group's range 8 B, the edge record 8 B and that
  * hop's 12 B of output).  Padding and the int64 widening are the layout
- * pass's, not the walk kernel's. */
+ * pass's, not the walk kernel's.  Both are demand bytes: every walk's reads
+ * count, also where walks running side by side read the same lines.
+ *
+ * compulsory_read_bytes / compulsory_write_bytes are the bytes one launch of
+ * the walk kernel must move at least once between HBM and the chip: every
+ * input read once -- per walk its 16 B start state, 4 B of processing order
+ * when the walks ran sorted by start time, 8 B of cutoff; the sampled
+ * direction's index arrays the launched kernel reads (node headers, bucket
+ * tables, panel, edge records; per-node weights and their search index for
+ * weight pickers; the adjacency pair set for TemporalNode2Vec), each counted
+ * whole; injected draws at 16 B per selection -- and every output written
+ * once: the walk scratch (8 B per written slot packed, else 4 B node + 4 B
+ * rank per slot and 4 B per edge id) and 8 B of length per walk. */
 typedef struct trw_walk_stats {
     uint64_t total_len;         /* sum of walk_lens: walk steps (reference metric) */
     uint64_t transitions;       /* sum of max(len - 1, 0) */
     uint64_t nonempty_walks;
     uint64_t algorithmic_bytes;
     uint64_t reference_bytes;
+    uint64_t compulsory_read_bytes;
+    uint64_t compulsory_write_bytes;
 } trw_walk_stats;
 trw_status trw_get_walk_stats(void* handle, trw_walk_stats* out);
+
+/* ---- test hooks ---------------------------------------------------------- */
+
+/* After this call, the next n device allocations of any handle succeed and the
+ * one after them fails as out of memory (TRW_ERR_OUT_OF_MEMORY); n < 0
+ * disarms.  For tests of the failure paths: an ingest that fails after its
+ * batch was accepted leaves the handle empty, as after trw_clear.  No
+ * counterpart in the reference. */
+void trw_debug_fail_allocation(int64_t n);
 
 /* ---- standalone pickers (proxies/RandomPicker.cu:11-313) --------------------- */
 

@@ -103,6 +103,8 @@ def lib():
         L.orc_create.argtypes = [C.c_int, C.c_int64, C.c_int, C.c_int, C.c_double,
                                  C.c_double, C.c_double]
         L.orc_destroy.argtypes = [_P]
+        L.orc_set_threads.restype = None
+        L.orc_set_threads.argtypes = [_P, C.c_int]
         L.orc_add_edges.restype = C.c_int
         L.orc_add_edges.argtypes = [_P, _P, _P, _P, C.c_size_t, _P, C.c_size_t]
         L.orc_last_error.restype = C.c_char_p
@@ -242,7 +244,10 @@ class OracleGraph:
             self._L.orc_destroy(self.h)
             self.h = None
 
-    def add_edges(self, src, dst, ts, features=None):
+    def add_edges(self, src, dst, ts, features=None, num_threads=1):
+        """Ingest one batch; num_threads OpenMP threads (same result for any
+        count)."""
+        self._L.orc_set_threads(self.h, int(num_threads))
         src = np.ascontiguousarray(src, dtype=np.int32)
         dst = np.ascontiguousarray(dst, dtype=np.int32)
         ts = np.ascontiguousarray(ts, dtype=np.int64)

@@ -80,6 +80,8 @@ struct orc_graph {
     double* out_fwd_w;
     double* out_bwd_w;
     double* in_bwd_w;
+
+    int threads; /* OpenMP threads of the ingest (orc_set_threads; 1 = serial) */
 };
 
 static void* xmalloc(size_t n) {
@@ -110,8 +112,11 @@ orc_graph* orc_create(int is_directed, int64_t max_time_capacity,
     g->inv_q = 1.0 / node2vec_q;
     g->latest_timestamp = 0;
     g->max_node_id = -1;
+    g->threads = 1;
     return g;
 }
+
+void orc_set_threads(orc_graph* g, int threads) { g->threads = threads > 0 ? threads : 1; }
 
 void orc_destroy(orc_graph* g) {
     if (!g) return;
@@ -125,24 +130,148 @@ void orc_destroy(orc_graph* g) {
 }
 
 /* ------------------------------------------------------------------ */
-/* Stable merge sort of int32 positions by a key array (int64).        */
+/* Parallel building blocks of the ingest.  Every one gives the same     */
+/* result for any thread count: the sorts are stable and the scans and   */
+/* scatters write each output once.                                      */
 /* ------------------------------------------------------------------ */
-static void merge_sort_by_ts(uint32_t* a, uint32_t* tmp, size_t n, const int64_t* key) {
-    /* bottom-up, stable: ties keep the left run first */
+typedef struct {
+    int64_t k;  /* timestamp */
+    uint32_t p; /* position in the store */
+} orc_kp;
+
+/* [lo, hi) of chunk t of n items split into nt chunks. */
+static void chunk_of(size_t n, int nt, int t, size_t* lo, size_t* hi) {
+    *lo = n * (size_t)t / (size_t)nt;
+    *hi = n * (size_t)(t + 1) / (size_t)nt;
+}
+
+/* Bottom-up stable merge sort of (key, position) pairs by key. */
+static void sort_kp(orc_kp* a, orc_kp* tmp, size_t n) {
     for (size_t width = 1; width < n; width *= 2) {
         for (size_t lo = 0; lo < n; lo += 2 * width) {
             size_t mid = lo + width < n ? lo + width : n;
             size_t hi = lo + 2 * width < n ? lo + 2 * width : n;
             size_t i = lo, j = mid, k = lo;
             while (i < mid && j < hi) {
-                if (key[a[j]] < key[a[i]]) tmp[k++] = a[j++];
+                if (a[j].k < a[i].k) tmp[k++] = a[j++];
                 else tmp[k++] = a[i++];
             }
             while (i < mid) tmp[k++] = a[i++];
             while (j < hi) tmp[k++] = a[j++];
         }
-        memcpy(a, tmp, n * sizeof(uint32_t));
+        memcpy(a, tmp, n * sizeof(orc_kp));
     }
+}
+
+/* Number of A's items among the first d outputs of the stable merge of A
+ * and B (on equal keys A's item comes first): the merge-path co-rank. */
+static size_t merge_corank(const orc_kp* A, size_t na, const orc_kp* B, size_t nb, size_t d) {
+    size_t lo = d > nb ? d - nb : 0, hi = d < na ? d : na;
+    while (lo < hi) {
+        size_t mid = lo + (hi - lo) / 2;
+        /* A[mid] precedes B[d - mid - 1]: more than mid items come from A */
+        if (A[mid].k <= B[d - mid - 1].k) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+/* Stable merge of A and B into out (std::merge: B's item is taken only when
+ * strictly less), cut into nt equal output spans by co-rank. */
+static void par_merge(const orc_kp* A, size_t na, const orc_kp* B, size_t nb, orc_kp* out,
+                      int nt) {
+    size_t n = na + nb;
+    if (n < 65536) nt = 1;
+#pragma omp parallel for schedule(static, 1) num_threads(nt)
+    for (int t = 0; t < nt; t++) {
+        size_t d0, d1;
+        chunk_of(n, nt, t, &d0, &d1);
+        size_t i = merge_corank(A, na, B, nb, d0), i1 = merge_corank(A, na, B, nb, d1);
+        size_t j = d0 - i, j1 = d1 - i1, k = d0;
+        while (i < i1 && j < j1) {
+            if (B[j].k < A[i].k) out[k++] = B[j++];
+            else out[k++] = A[i++];
+        }
+        while (i < i1) out[k++] = A[i++];
+        while (j < j1) out[k++] = B[j++];
+    }
+}
+
+/* Stable LSD radix sort of (key, position) pairs by key - kmin (all keys in
+ * [kmin, kmax]), 11-bit digits over the range's bits, per-thread chunk
+ * histograms: equal keys keep their input order.  Result in a. */
+static void par_radix_kp(orc_kp* a, size_t n, int64_t kmin, int64_t kmax, int nt) {
+    enum { RB = 11, RD = 1 << RB };
+    if (n < 65536) nt = 1;
+    const uint64_t range = (uint64_t)kmax - (uint64_t)kmin;
+    int bits = 0;
+    while (bits < 64 && (range >> bits) != 0) bits++;
+    orc_kp* b = (orc_kp*)xmalloc((n ? n : 1) * sizeof(orc_kp));
+    size_t* hist = (size_t*)xmalloc((size_t)nt * RD * sizeof(size_t));
+    orc_kp *src = a, *dst = b;
+    for (int shift = 0; shift < bits; shift += RB) {
+#pragma omp parallel for schedule(static, 1) num_threads(nt)
+        for (int t = 0; t < nt; t++) {
+            size_t lo, hi;
+            chunk_of(n, nt, t, &lo, &hi);
+            size_t* h = hist + (size_t)t * RD;
+            memset(h, 0, RD * sizeof(size_t));
+            for (size_t i = lo; i < hi; i++)
+                h[(((uint64_t)src[i].k - (uint64_t)kmin) >> shift) & (RD - 1)]++;
+        }
+        size_t run = 0;
+        for (int d = 0; d < RD; d++) {
+            for (int t = 0; t < nt; t++) {
+                size_t c = hist[(size_t)t * RD + d];
+                hist[(size_t)t * RD + d] = run;
+                run += c;
+            }
+        }
+#pragma omp parallel for schedule(static, 1) num_threads(nt)
+        for (int t = 0; t < nt; t++) {
+            size_t lo, hi;
+            chunk_of(n, nt, t, &lo, &hi);
+            size_t* h = hist + (size_t)t * RD;
+            for (size_t i = lo; i < hi; i++)
+                dst[h[(((uint64_t)src[i].k - (uint64_t)kmin) >> shift) & (RD - 1)]++] = src[i];
+        }
+        orc_kp* t0 = src;
+        src = dst;
+        dst = t0;
+    }
+    if (src != a) memcpy(a, src, n * sizeof(orc_kp));
+    free(b);
+    free(hist);
+}
+
+/* Stable sort of n pairs by key: chunks sorted side by side, then merged
+ * pairwise, each merge spread over every thread.  Result in a. */
+static void par_sort_kp(orc_kp* a, size_t n, int nt) {
+    orc_kp* tmp = (orc_kp*)xmalloc(n * sizeof(orc_kp));
+    int chunks = 1;
+    while (chunks < nt && n / (size_t)(2 * chunks) >= 65536) chunks *= 2;
+#pragma omp parallel for schedule(static, 1) num_threads(nt)
+    for (int c = 0; c < chunks; c++) {
+        size_t lo, hi;
+        chunk_of(n, chunks, c, &lo, &hi);
+        sort_kp(a + lo, tmp + lo, hi - lo);
+    }
+    orc_kp* src = a;
+    orc_kp* dst = tmp;
+    for (int run = 1; run < chunks; run *= 2) {
+        for (int c = 0; c < chunks; c += 2 * run) {
+            size_t lo, mid, hi, x;
+            chunk_of(n, chunks, c, &lo, &x);
+            chunk_of(n, chunks, c + run, &mid, &x);
+            chunk_of(n, chunks, c + 2 * run - 1, &x, &hi);
+            par_merge(src + lo, mid - lo, src + mid, hi - mid, dst + lo, nt);
+        }
+        orc_kp* t = src;
+        src = dst;
+        dst = t;
+    }
+    if (src != a) memcpy(a, src, n * sizeof(orc_kp));
+    free(tmp);
 }
 
 /* temporal_graph.cu:67-134: sort the new batch positions by timestamp,
@@ -150,28 +279,39 @@ static void merge_sort_by_ts(uint32_t* a, uint32_t* tmp, size_t n, const int64_t
 static void sort_and_merge(orc_graph* g, size_t start_idx) {
     size_t total = g->E, n_new = total - start_idx;
     if (n_new == 0) return;
-    uint32_t* nw = (uint32_t*)xmalloc(n_new * sizeof(uint32_t));
-    uint32_t* tmp = (uint32_t*)xmalloc(n_new * sizeof(uint32_t));
-    for (size_t i = 0; i < n_new; i++) nw[i] = (uint32_t)(start_idx + i);
-    merge_sort_by_ts(nw, tmp, n_new, g->ts);
-    free(tmp);
-    /* std::merge: takes from the second range only when strictly less */
-    uint32_t* merged = (uint32_t*)xmalloc(total * sizeof(uint32_t));
-    size_t i = 0, j = 0, k = 0;
-    while (i < start_idx && j < n_new) {
-        if (g->ts[nw[j]] < g->ts[i]) merged[k++] = nw[j++];
-        else merged[k++] = (uint32_t)(i++);
+    const int nt = g->threads;
+    orc_kp* nw = (orc_kp*)xmalloc(n_new * sizeof(orc_kp));
+    orc_kp* old = (orc_kp*)xmalloc((start_idx ? start_idx : 1) * sizeof(orc_kp));
+    int64_t kmin = g->ts[start_idx], kmax = g->ts[start_idx];
+#pragma omp parallel for schedule(static) reduction(min : kmin) reduction(max : kmax) num_threads(nt)
+    for (size_t i = 0; i < n_new; i++) {
+        nw[i].k = g->ts[start_idx + i];
+        nw[i].p = (uint32_t)(start_idx + i);
+        if (nw[i].k < kmin) kmin = nw[i].k;
+        if (nw[i].k > kmax) kmax = nw[i].k;
     }
-    while (i < start_idx) merged[k++] = (uint32_t)(i++);
-    while (j < n_new) merged[k++] = nw[j++];
+#pragma omp parallel for schedule(static) num_threads(nt)
+    for (size_t i = 0; i < start_idx; i++) {
+        old[i].k = g->ts[i];
+        old[i].p = (uint32_t)i;
+    }
+    /* a stable sort: the batch's tie order is the reference's input order
+     * (its std::sort is not stable; the canonical order is) */
+    if (nt > 1) par_radix_kp(nw, n_new, kmin, kmax, nt);
+    else par_sort_kp(nw, n_new, 1);
+    /* std::merge of the old positions with the sorted batch */
+    orc_kp* merged = (orc_kp*)xmalloc(total * sizeof(orc_kp));
+    par_merge(old, start_idx, nw, n_new, merged, nt);
     free(nw);
+    free(old);
 
     int32_t* s2 = (int32_t*)xmalloc(total * sizeof(int32_t));
     int32_t* d2 = (int32_t*)xmalloc(total * sizeof(int32_t));
     int64_t* t2 = (int64_t*)xmalloc(total * sizeof(int64_t));
     float* f2 = g->feat_dim ? (float*)xmalloc(total * g->feat_dim * sizeof(float)) : NULL;
+#pragma omp parallel for schedule(static) num_threads(nt)
     for (size_t p = 0; p < total; p++) {
-        uint32_t id = merged[p];
+        uint32_t id = merged[p].p;
         s2[p] = g->src[id];
         d2[p] = g->dst[id];
         t2[p] = g->ts[id];
@@ -214,6 +354,8 @@ static void populate_active_nodes(orc_graph* g) {
         return;
     }
     int32_t mx = -1;
+    const int nt = g->threads;
+#pragma omp parallel for schedule(static) reduction(max : mx) num_threads(nt)
     for (size_t i = 0; i < g->E; i++) {
         if (g->src[i] > mx) mx = g->src[i];
         if (g->dst[i] > mx) mx = g->dst[i];
@@ -221,9 +363,22 @@ static void populate_active_nodes(orc_graph* g) {
     g->max_node_id = mx;
     g->active_size = (size_t)mx + 1;
     int32_t* act = (int32_t*)calloc(g->active_size, sizeof(int32_t));
+#pragma omp parallel for schedule(static) num_threads(nt)
     for (size_t i = 0; i < g->E; i++) {
-        act[g->src[i]] = 1;
-        act[g->dst[i]] = 1;
+        /* a flag already set is left alone (a hub's line is then only read) */
+        int32_t a, b;
+#pragma omp atomic read
+        a = act[g->src[i]];
+        if (!a) {
+#pragma omp atomic write
+            act[g->src[i]] = 1;
+        }
+#pragma omp atomic read
+        b = act[g->dst[i]];
+        if (!b) {
+#pragma omp atomic write
+            act[g->dst[i]] = 1;
+        }
     }
     set_array((void**)&g->active, act);
 }
@@ -237,18 +392,33 @@ static void update_timestamp_groups(orc_graph* g) {
         set_array((void**)&g->unique_ts, NULL);
         return;
     }
-    size_t T = 1;
-    for (size_t i = 1; i < n; i++) T += g->ts[i] != g->ts[i - 1];
+    /* group starts counted per chunk, chunk bases scanned, then written */
+    const int nt = n < 65536 ? 1 : g->threads;
+    size_t* base = (size_t*)calloc((size_t)nt + 1, sizeof(size_t));
+#pragma omp parallel for schedule(static, 1) num_threads(nt)
+    for (int t = 0; t < nt; t++) {
+        size_t lo, hi, c = 0;
+        chunk_of(n, nt, t, &lo, &hi);
+        for (size_t i = lo; i < hi; i++) c += i == 0 || g->ts[i] != g->ts[i - 1];
+        base[t + 1] = c;
+    }
+    for (int t = 0; t < nt; t++) base[t + 1] += base[t];
+    size_t T = base[nt];
     uint64_t* off = (uint64_t*)xmalloc((T + 1) * sizeof(uint64_t));
     int64_t* uq = (int64_t*)xmalloc(T * sizeof(int64_t));
-    size_t k = 0;
-    for (size_t i = 0; i < n; i++) {
-        if (i == 0 || g->ts[i] != g->ts[i - 1]) {
-            off[k] = i;
-            uq[k] = g->ts[i];
-            k++;
+#pragma omp parallel for schedule(static, 1) num_threads(nt)
+    for (int t = 0; t < nt; t++) {
+        size_t lo, hi, k = base[t];
+        chunk_of(n, nt, t, &lo, &hi);
+        for (size_t i = lo; i < hi; i++) {
+            if (i == 0 || g->ts[i] != g->ts[i - 1]) {
+                off[k] = i;
+                uq[k] = g->ts[i];
+                k++;
+            }
         }
     }
+    free(base);
     off[T] = n;
     g->T = T;
     set_array((void**)&g->ts_group_offsets, off);
@@ -292,8 +462,76 @@ static void build_adjacency(orc_graph* g) {
     g->adj_nbr_size = 2 * m;
 }
 
+/* Stable LSD radix sort of (key, value) pairs by key (keys < 2^bits), 11-bit
+ * digits, per-thread chunk histograms: equal keys keep their input order. */
+static void par_radix_kv(uint32_t* key, uint32_t* val, size_t n, int bits, int nt) {
+    enum { RB = 11, RD = 1 << RB };
+    if (n < 65536) nt = 1;
+    uint32_t* k2 = (uint32_t*)xmalloc((n ? n : 1) * sizeof(uint32_t));
+    uint32_t* v2 = (uint32_t*)xmalloc((n ? n : 1) * sizeof(uint32_t));
+    size_t* hist = (size_t*)xmalloc((size_t)nt * RD * sizeof(size_t));
+    uint32_t *ks = key, *vs = val, *kd = k2, *vd = v2;
+    for (int shift = 0; shift < bits; shift += RB) {
+#pragma omp parallel for schedule(static, 1) num_threads(nt)
+        for (int t = 0; t < nt; t++) {
+            size_t lo, hi;
+            chunk_of(n, nt, t, &lo, &hi);
+            size_t* h = hist + (size_t)t * RD;
+            memset(h, 0, RD * sizeof(size_t));
+            for (size_t i = lo; i < hi; i++) h[(ks[i] >> shift) & (RD - 1)]++;
+        }
+        /* digit-major, thread-minor exclusive scan */
+        size_t run = 0;
+        for (int d = 0; d < RD; d++) {
+            for (int t = 0; t < nt; t++) {
+                size_t c = hist[(size_t)t * RD + d];
+                hist[(size_t)t * RD + d] = run;
+                run += c;
+            }
+        }
+#pragma omp parallel for schedule(static, 1) num_threads(nt)
+        for (int t = 0; t < nt; t++) {
+            size_t lo, hi;
+            chunk_of(n, nt, t, &lo, &hi);
+            size_t* h = hist + (size_t)t * RD;
+            for (size_t i = lo; i < hi; i++) {
+                size_t p = h[(ks[i] >> shift) & (RD - 1)]++;
+                kd[p] = ks[i];
+                vd[p] = vs[i];
+            }
+        }
+        uint32_t* t0 = ks; ks = kd; kd = t0;
+        uint32_t* t1 = vs; vs = vd; vd = t1;
+    }
+    if (ks != key) {
+        memcpy(key, ks, n * sizeof(uint32_t));
+        memcpy(val, vs, n * sizeof(uint32_t));
+    }
+    free(k2);
+    free(v2);
+    free(hist);
+}
+
+/* out[u] for u in [0, V]: the first position of a sorted array of n node ids
+ * whose id is >= u (a lower_bound, i.e. the CSR offsets).  Each out[u] is
+ * written once, by the position where the ids reach u. */
+static void lower_bound_offsets(const uint32_t* sorted, size_t n, size_t V, uint64_t* out,
+                                int nt) {
+    if (n == 0) {
+        for (size_t u = 0; u <= V; u++) out[u] = 0;
+        return;
+    }
+    if (n < 65536) nt = 1;
+    for (size_t u = 0; u <= sorted[0] && u <= V; u++) out[u] = 0;
+#pragma omp parallel for schedule(static) num_threads(nt)
+    for (size_t i = 1; i < n; i++) {
+        for (size_t u = (size_t)sorted[i - 1] + 1; u <= sorted[i] && u <= V; u++) out[u] = i;
+    }
+    for (size_t u = (size_t)sorted[n - 1] + 1; u <= V; u++) out[u] = n;
+}
+
 /* node_edge_index.cu:294-494 for one direction: stable order of entries by
- * node (counting sort keeps input order within a node), CSR offsets
+ * node (the radix sort keeps input order within a node), CSR offsets
  * (node_edge_index.cu:254-292), node-timestamp group starts and per-node
  * exclusive group counts. */
 static void build_direction(const orc_graph* g, const int32_t* keys, size_t n_entries,
@@ -301,40 +539,57 @@ static void build_direction(const orc_graph* g, const int32_t* keys, size_t n_en
                             uint64_t** idx_out, uint64_t** cnt_out,
                             uint64_t** grp_out, size_t* n_grp_out) {
     size_t V = g->active_size; /* node_count */
-    uint64_t* off = (uint64_t*)calloc(V + 1, sizeof(uint64_t));
-    for (size_t k = 0; k < n_entries; k++) off[(size_t)keys[k] + 1]++;
-    for (size_t u = 0; u < V; u++) off[u + 1] += off[u];
-    uint64_t* idx = (uint64_t*)xmalloc(n_entries * sizeof(uint64_t));
-    int32_t* sorted_node = (int32_t*)xmalloc(n_entries * sizeof(int32_t));
-    uint64_t* cur = (uint64_t*)xmalloc((V + 1) * sizeof(uint64_t));
-    memcpy(cur, off, (V + 1) * sizeof(uint64_t));
+    const int nt = g->threads;
+    uint32_t* node = (uint32_t*)xmalloc((n_entries ? n_entries : 1) * sizeof(uint32_t));
+    uint32_t* ent = (uint32_t*)xmalloc((n_entries ? n_entries : 1) * sizeof(uint32_t));
+#pragma omp parallel for schedule(static) num_threads(nt)
     for (size_t k = 0; k < n_entries; k++) {
-        uint64_t p = cur[keys[k]]++;
-        idx[p] = undirected_pairs ? (uint64_t)(k / 2) : (uint64_t)k;
-        sorted_node[p] = keys[k];
+        node[k] = (uint32_t)keys[k];
+        ent[k] = (uint32_t)k;
     }
-    free(cur);
-    size_t ng = 0;
-    for (size_t i = 0; i < n_entries; i++) {
-        if (i == 0 || sorted_node[i] != sorted_node[i - 1] ||
-            g->ts[idx[i]] != g->ts[idx[i - 1]])
-            ng++;
+    int bits = 1;
+    while (bits < 32 && ((size_t)1 << bits) < V) bits++;
+    par_radix_kv(node, ent, n_entries, bits, nt);
+    uint64_t* off = (uint64_t*)xmalloc((V + 1) * sizeof(uint64_t));
+    lower_bound_offsets(node, n_entries, V, off, nt);
+    uint64_t* idx = (uint64_t*)xmalloc((n_entries ? n_entries : 1) * sizeof(uint64_t));
+#pragma omp parallel for schedule(static) num_threads(nt)
+    for (size_t i = 0; i < n_entries; i++)
+        idx[i] = undirected_pairs ? (uint64_t)(ent[i] / 2) : (uint64_t)ent[i];
+    free(ent);
+    /* group starts: a new node or a new timestamp within the node */
+    const int gt = n_entries < 65536 ? 1 : nt;
+    size_t* base = (size_t*)calloc((size_t)gt + 1, sizeof(size_t));
+#pragma omp parallel for schedule(static, 1) num_threads(gt)
+    for (int t = 0; t < gt; t++) {
+        size_t lo, hi, c = 0;
+        chunk_of(n_entries, gt, t, &lo, &hi);
+        for (size_t i = lo; i < hi; i++)
+            c += i == 0 || node[i] != node[i - 1] || g->ts[idx[i]] != g->ts[idx[i - 1]];
+        base[t + 1] = c;
     }
-    uint64_t* grp = (uint64_t*)xmalloc(ng * sizeof(uint64_t));
-    uint64_t* counts = (uint64_t*)calloc(V, sizeof(uint64_t));
-    size_t k = 0;
-    for (size_t i = 0; i < n_entries; i++) {
-        if (i == 0 || sorted_node[i] != sorted_node[i - 1] ||
-            g->ts[idx[i]] != g->ts[idx[i - 1]]) {
-            grp[k++] = i;
-            counts[sorted_node[i]]++;
+    for (int t = 0; t < gt; t++) base[t + 1] += base[t];
+    size_t ng = base[gt];
+    uint64_t* grp = (uint64_t*)xmalloc((ng ? ng : 1) * sizeof(uint64_t));
+    uint32_t* gnode = (uint32_t*)xmalloc((ng ? ng : 1) * sizeof(uint32_t));
+#pragma omp parallel for schedule(static, 1) num_threads(gt)
+    for (int t = 0; t < gt; t++) {
+        size_t lo, hi, k = base[t];
+        chunk_of(n_entries, gt, t, &lo, &hi);
+        for (size_t i = lo; i < hi; i++) {
+            if (i == 0 || node[i] != node[i - 1] || g->ts[idx[i]] != g->ts[idx[i - 1]]) {
+                grp[k] = i;
+                gnode[k] = node[i];
+                k++;
+            }
         }
     }
+    free(base);
+    /* cnt[u] = number of groups of nodes below u */
     uint64_t* cnt = (uint64_t*)xmalloc((V + 1) * sizeof(uint64_t));
-    cnt[0] = 0;
-    for (size_t u = 0; u < V; u++) cnt[u + 1] = cnt[u] + counts[u];
-    free(counts);
-    free(sorted_node);
+    lower_bound_offsets(gnode, ng, V, cnt, nt);
+    free(gnode);
+    free(node);
     *off_out = off;
     *idx_out = idx;
     *cnt_out = cnt;

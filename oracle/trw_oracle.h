@@ -46,6 +46,9 @@ void orc_destroy(orc_graph* g);
 
 /* Returns 0 on success, nonzero on a validation error (message in
  * orc_last_error()).  temporal_graph.cu:158-220 */
+/* OpenMP threads of later ingests (1 = serial, the default); the result is
+ * the same for every count. */
+void orc_set_threads(orc_graph* g, int threads);
 int orc_add_edges(orc_graph* g, const int32_t* src, const int32_t* dst,
                   const int64_t* ts, size_t n, const float* features,
                   size_t feature_dim);

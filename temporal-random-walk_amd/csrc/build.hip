@@ -892,8 +892,6 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
     int64_t* hs = reinterpret_cast<int64_t*>(host_scalars);
     check_hip(hipEventRecord(ev[0], s), "event");
 
-    const size_t e_old = E, etot = E + n;
-
     // ---- 1. key range, latest timestamp, and the batch's smallest node id:
     // the node index is keyed by ids in [0, max_node_id], so a negative id
     // is rejected here, before the store changes
@@ -902,8 +900,25 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
     check_hip(hipMemcpyAsync(hs, red64.p, 24, hipMemcpyDeviceToHost, s), "read minmax");
     sync();
     if (hs[2] < 0) throw InvalidArgument("node ids must be non-negative");
+    try {
+        build_accepted(d_src, d_dst, d_ts, d_feat, n, dim, hs[0], hs[1]);
+    } catch (...) {
+        // the store, its index and the last batch may disagree: start empty
+        (void)hipStreamSynchronize(stream);
+        (void)hipStreamSynchronize(side);
+        clear();
+        throw;
+    }
+}
+
+void Engine::build_accepted(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_ts,
+                            const float* d_feat, size_t n, size_t dim, int64_t tmin,
+                            int64_t tmax) {
+    hipStream_t s = stream;
+    int64_t* hs = reinterpret_cast<int64_t*>(host_scalars);
+    const size_t e_old = E, etot = E + n;
+    const int64_t batch_tmax = tmax;
     if (E == 0) feat_dim = dim;
-    int64_t tmin = hs[0], tmax = hs[1];
 
     // the batch's endpoints, for ..._for_last_batch: copied on the side
     // stream beside the build; the build's end waits for them
@@ -917,7 +932,7 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
         tmin = std::min(tmin, store_tmin);
         tmax = std::max(tmax, store_tmax);
     }
-    latest_ts = std::max(latest_ts, hs[1]);
+    latest_ts = std::max(latest_ts, batch_tmax);
 
     // ---- 2. stable radix sort by (ts, position); 32-bit keys when the key
     // range fits (4-byte key traffic per pass instead of 8).  Without edge

@@ -476,6 +476,10 @@ trw_status trw_get_walk_stats(void* handle, trw_walk_stats* out) {
     return guarded(handle, [&](Engine& e) { trw::walk_stats(e, out); });
 }
 
+void trw_debug_fail_allocation(int64_t n) {
+    trw::g_alloc_fail_after.store(n < 0 ? -1 : n, std::memory_order_relaxed);
+}
+
 trw_status trw_pick_index(int32_t device_id, int32_t picker, const int32_t* start,
                           const int32_t* end, uint64_t n, int32_t prioritize_end,
                           const double* draws, uint64_t seed, int32_t* out) {

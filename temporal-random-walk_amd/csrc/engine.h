@@ -51,6 +51,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <cstring>
 #include <memory>
 #include <new>
@@ -67,6 +68,10 @@ namespace trw {
 struct InvalidArgument : std::invalid_argument {
     using std::invalid_argument::invalid_argument;
 };
+
+// Test hook (trw_debug_fail_allocation): when >= 0, the number of device
+// allocations that still succeed before one fails as out of memory.
+inline std::atomic<long long> g_alloc_fail_after{-1};
 
 // Grow-only device buffer; growth discards the contents.
 template <typename T>
@@ -89,6 +94,9 @@ struct DBuf {
         if (k > cap) {
             release();
             const size_t c = k + k / 4 + 64;
+            if (g_alloc_fail_after.load(std::memory_order_relaxed) >= 0 &&
+                g_alloc_fail_after.fetch_sub(1, std::memory_order_relaxed) == 0)
+                throw std::bad_alloc();
             const hipError_t e = hipMalloc(&p, c * sizeof(T));
             if (e == hipErrorOutOfMemory) {
                 (void)hipGetLastError();  // clear the sticky error
@@ -323,6 +331,12 @@ struct Engine {
     int w_len = 0;
     int w_dir_forward = 1;
     int w_constrained = 0;  // the last sample started from given nodes
+    // what the last sample's walk kernel reads once and how it writes its
+    // scratch (the compulsory bytes of trw_get_walk_stats)
+    uint64_t w_in_bytes_per_walk = 0;  // start state, processing order, cutoff
+    uint64_t w_index_bytes = 0;        // index arrays the launched kernel reads
+    int w_packed = 0;
+    int w_replay = 0;
 
     // pinned host scalars for the few readbacks that size allocations
     void* host_scalars = nullptr;
@@ -351,10 +365,15 @@ struct Engine {
 
     void sync() { check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize"); }
 
-    // ingest: batch arrays in device memory
+    // ingest: batch arrays in device memory.  A failure after the batch is
+    // accepted (device out of memory, a HIP error) leaves the engine empty, as
+    // after clear(), rather than holding a store its index does not describe.
     void build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_ts,
                const float* d_feat, size_t n, size_t dim);
     void clear();
+    // the pipeline of build() after the batch's checks
+    void build_accepted(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_ts,
+                        const float* d_feat, size_t n, size_t dim, int64_t tmin, int64_t tmax);
 
     // sampling into w_* buffers
     void sample(const trw_sample_params& p);

@@ -1221,38 +1221,48 @@ inline unsigned grid_capped(uint64_t n) {
     return static_cast<unsigned>(g == 0 ? 1 : (g > (1u << 20) ? (1u << 20) : g));
 }
 
-// Walk statistics and algorithmic bytes of the walk path (trw_get_walk_stats):
+// Walk statistics and demand bytes of the walk path (trw_get_walk_stats):
 // acc[3] with this engine's 4-byte positions and ranks, acc[4] with the
-// reference's element types.
-__global__ void walk_stats_kernel(const int32_t* __restrict__ nodes,
-                                  const uint64_t* __restrict__ lens, uint64_t n, int L,
-                                  const uint32_t* __restrict__ cnt, int32_t active_size,
-                                  int constrained, unsigned long long* acc) {
-    const uint64_t w = blockIdx.x * static_cast<uint64_t>(kB) + threadIdx.x;
+// reference's element types.  One wave per walk row (grid-stride over
+// walks): the wave reads the row's nodes together, 256 B per access, and
+// each lane adds the hops of the slots it holds.
+__global__ __launch_bounds__(kB) void walk_stats_kernel(const int32_t* __restrict__ nodes,
+                                                        const uint64_t* __restrict__ lens,
+                                                        uint64_t n, int L,
+                                                        const uint32_t* __restrict__ cnt,
+                                                        int32_t active_size, int constrained,
+                                                        unsigned long long* acc) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t waves = static_cast<uint64_t>(gridDim.x) * (kB / 64);
     unsigned long long bytes = 0, ref = 0, trans = 0, total = 0, nonempty = 0;
-    if (w < n && L > 0) {
+    for (uint64_t w = blockIdx.x * static_cast<uint64_t>(kB / 64) + threadIdx.x / 64; w < n;
+         w += waves) {
         const int len = static_cast<int>(lens[w]);
-        bytes = 24;
-        ref = 8 + (constrained ? 52 : 32);
-        if (len >= 1) {
-            bytes += 8;
-            ref += 12;
+        if (lane == 0) {
+            bytes += 24;
+            ref += 8 + (constrained ? 52 : 32);
+            if (len >= 1) {
+                bytes += 8;
+                ref += 12;
+            }
+            if (len >= 2) {
+                bytes += 12;
+                ref += 20;
+            }
+            trans += len > 0 ? len - 1 : 0;
+            total += len;
+            nonempty += len > 0;
         }
-        if (len >= 2) {
-            bytes += 12;
-            ref += 20;
-        }
-        for (int k = 1; k + 1 < len; ++k) {
-            const int u = nodes[w * L + k];
+        // hops are selected at slots 1 .. len - 2
+        const int32_t* row = nodes + w * static_cast<uint64_t>(L);
+        for (int k = 1 + lane; k + 1 < len; k += 64) {
+            const int u = row[k];
             uint32_t G = 0;
             if (u >= 0 && u < active_size) G = cnt[u + 1] - cnt[u];
             const int probes = G ? 32 - __clz(G) : 0;  // ceil(log2(G + 1))
             bytes += 36 + 4 * probes;
             ref += 72 + 8 * probes;
         }
-        trans = len > 0 ? len - 1 : 0;
-        total = len;
-        nonempty = len > 0;
     }
     // wave reduction then one atomic per wave
     for (int off = 32; off > 0; off >>= 1) {
@@ -1262,7 +1272,7 @@ __global__ void walk_stats_kernel(const int32_t* __restrict__ nodes,
         total += __shfl_down(total, off, 64);
         nonempty += __shfl_down(nonempty, off, 64);
     }
-    if ((threadIdx.x & 63) == 0) {
+    if (lane == 0) {
         atomicAdd(acc + 0, total);
         atomicAdd(acc + 1, trans);
         atomicAdd(acc + 2, nonempty);
@@ -1483,6 +1493,11 @@ void Engine::sample(const trw_sample_params& p) {
     const int pk_rb = bit_length(T);
     const int pk_eb = E ? bit_length(E - 1) : 0;
     const bool packed = E > 0 && max_node_id >= 0 && pk_nb + pk_rb + pk_eb <= 64 && pk_nb + pk_rb < 64;
+    // no walks until every output buffer is sized: a failed allocation
+    // below leaves an empty walk set, not a count over released buffers
+    w_num = 0;
+    w_len = 0;
+    w_feat.n = 0;
     if (packed) {
         sw_packed.resize(padded * L);
         sw_nodes.release();
@@ -1502,6 +1517,8 @@ void Engine::sample(const trw_sample_params& p) {
     w_len = L;
     w_dir_forward = forward ? 1 : 0;
     w_constrained = have_starts ? 1 : 0;
+    w_packed = packed ? 1 : 0;
+    w_replay = p.replay_draws ? 1 : 0;
 
     // ---- graph view of the sampled direction
     const bool use_in = !forward && cfg.is_directed;
@@ -1574,6 +1591,17 @@ void Engine::sample(const trw_sample_params& p) {
     }
     const bool index_only = is_index_picker(walk_bias) && is_index_picker(start_bias);
     const bool no_node2vec = walk_bias != kTemporalNode2Vec;  // start_bias never is (above)
+    // the index arrays the launched walk kernel reads (each counted whole):
+    // headers, bucket tables, panel and records of the sampled direction;
+    // per-node weights and their search index for a weight picker on the
+    // hops; the adjacency pair set for node2vec
+    w_index_bytes = d.hdr.bytes() + d.tab.bytes() + d.pan.bytes() + d.rec.bytes();
+    if (!is_index_picker(walk_bias) && weights_ready) {
+        const DirIndex& wd = (!forward && cfg.is_directed) ? in : out;
+        w_index_bytes += (forward ? wd.w_fwd : wd.w_bwd).bytes() +
+                         (forward ? wd.wx_fwd : wd.wx_bwd).bytes() + wd.wx_off.bytes();
+    }
+    if (walk_bias == kTemporalNode2Vec && adj_ready) w_index_bytes += adj_hash.bytes();
 #define TRW_LAUNCH_FAMILY(K, F, D, G, ...)                                                     \
     do {                                                                                       \
         if (index_only)                                                                        \
@@ -1618,6 +1646,8 @@ void Engine::sample(const trw_sample_params& p) {
         }
         check_hip(hipGetLastError(), "walk start launch");
     }
+
+    w_in_bytes_per_walk = sizeof(StartState) + (a.order ? 4 : 0) + (have_cutoffs ? 8 : 0);
 
     // ---- walk kernel, then the layout pass.  (Running the layout of finished
     // grid chunks on a second stream beside the remaining walks was measured
@@ -1706,10 +1736,12 @@ void walk_stats(Engine& e, trw_walk_stats* out) {
     const bool use_in = !e.w_dir_forward && e.cfg.is_directed;
     const DirIndex& d = use_in ? e.in : e.out;
     if (e.w_num && e.w_len > 0) {
-        hipLaunchKernelGGL(walk_stats_kernel, dim3(grid_for(e.w_num)), dim3(kB), 0, s, e.w_nodes.p,
-                           e.w_lens.p, e.w_num, e.w_len, d.cnt.p,
+        const uint64_t blocks = std::min<uint64_t>((e.w_num + 3) / 4, 1u << 16);
+        hipLaunchKernelGGL(walk_stats_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kB), 0, s,
+                           e.w_nodes.p, e.w_lens.p, e.w_num, e.w_len, d.cnt.p,
                            static_cast<int32_t>(e.active.n), e.w_constrained,
                            reinterpret_cast<unsigned long long*>(e.acc64.p));
+        check_hip(hipGetLastError(), "walk stats launch");
     }
     uint64_t h[5];
     check_hip(hipMemcpyAsync(h, e.acc64.p, 40, hipMemcpyDeviceToHost, s), "read stats");
@@ -1719,6 +1751,15 @@ void walk_stats(Engine& e, trw_walk_stats* out) {
     out->nonempty_walks = h[2];
     out->algorithmic_bytes = h[3];
     out->reference_bytes = h[4];
+    // compulsory bytes of the walk kernel's launch: inputs and the index read
+    // once, the scratch slots and lengths written once
+    const uint64_t nw = e.w_num;
+    out->compulsory_read_bytes =
+        nw && e.w_len > 0 ? nw * e.w_in_bytes_per_walk + e.w_index_bytes +
+                                (e.w_replay ? 16 * out->transitions : 0)
+                          : 0;
+    const uint64_t scratch = e.w_packed ? 8 * out->total_len : 8 * out->total_len + 4 * out->transitions;
+    out->compulsory_write_bytes = nw ? 8 * nw + (e.w_len > 0 ? scratch : 0) : 0;
 }
 
 }  // namespace trw

@@ -65,7 +65,8 @@ EXPORTS = [
     "trw_get_node_count", "trw_get_edge_count", "trw_get_node_ids", "trw_get_node_degrees",
     "trw_get_edges", "trw_get_is_directed", "trw_get_memory_used", "trw_get_feature_dim",
     "trw_get_latest_timestamp", "trw_clear", "trw_get_array", "trw_get_timings",
-    "trw_get_stream", "trw_get_walk_stats", "trw_pick_index", "trw_pick_weights",
+    "trw_get_stream", "trw_get_walk_stats", "trw_debug_fail_allocation", "trw_pick_index",
+    "trw_pick_weights",
 ]
 
 
@@ -137,10 +138,12 @@ class TrwWalkStats(C.Structure):
         ("nonempty_walks", C.c_uint64),
         ("algorithmic_bytes", C.c_uint64),
         ("reference_bytes", C.c_uint64),
+        ("compulsory_read_bytes", C.c_uint64),
+        ("compulsory_write_bytes", C.c_uint64),
     ]
 
 
-ABI_VERSION = 3  # TRW_ABI_VERSION of include/trw_engine.h
+ABI_VERSION = 4  # TRW_ABI_VERSION of include/trw_engine.h
 _lib = None
 
 
@@ -185,6 +188,8 @@ def lib():
         L.trw_get_timings.argtypes = [P, C.POINTER(TrwTimings)]
         L.trw_get_stream.argtypes = [P, C.POINTER(C.c_void_p)]
         L.trw_get_walk_stats.argtypes = [P, C.POINTER(TrwWalkStats)]
+        L.trw_debug_fail_allocation.argtypes = [C.c_int64]
+        L.trw_debug_fail_allocation.restype = None
         L.trw_pick_index.argtypes = [C.c_int32, C.c_int32, P, P, C.c_uint64, C.c_int32, P,
                                      C.c_uint64, P]
         L.trw_pick_weights.argtypes = [C.c_int32, P, C.c_uint64, P, P, C.c_uint64, P,
@@ -313,6 +318,12 @@ def _check(rc):
 
 def _ptr(a):
     return None if a is None else a.ctypes.data
+
+
+def debug_fail_allocation(n):
+    """Test hook: the next n device allocations succeed, the one after them
+    fails as out of memory (MemoryError); n < 0 disarms."""
+    lib().trw_debug_fail_allocation(int(n))
 
 
 class Walks:

@@ -312,3 +312,200 @@ def test_python_class_prefetch_matches_add_multiple_edges():
            for tw in (tw_a, tw_b)]
     for x, y in zip(out[0][:3], out[1][:3]):
         assert np.array_equal(x, y)
+
+
+def _last_batch_graph(seed):
+    """Two undirected batches; the second batch's targets (ids 50..79) are
+    nodes the first batch never had."""
+    rng = np.random.default_rng(seed)
+    s1 = rng.integers(0, 50, 400).astype(np.int32)
+    d1 = ((s1 + rng.integers(1, 50, 400)) % 50).astype(np.int32)  # no self-loops
+    t1 = rng.integers(0, 1_000, 400).astype(np.int64)
+    s2 = rng.integers(0, 50, 300).astype(np.int32)
+    d2 = rng.integers(50, 80, 300).astype(np.int32)
+    t2 = rng.integers(500, 2_000, 300).astype(np.int64)
+    return (s1, d1, t1), (s2, d2, t2)
+
+
+@pytest.mark.parametrize("forward", [True, False])
+def test_last_batch_undirected_starts_are_the_batch_endpoints(forward):
+    """..._for_last_batch on an undirected graph starts from the sorted unique
+    union of the last batch's sources and targets, each repeated
+    num_walks_per_node times (core/temporal_random_walk.cu:248-272; pinned by
+    test/test_temporal_random_walk.cpp:669-685).  With shuffling off and
+    injected draws the walks equal the oracle's walks from exactly those
+    starts, row for row."""
+    from oracle import pyoracle as po
+    from temporal_random_walk import capi
+    b1, b2 = _last_batch_graph(11)
+    og = po.OracleGraph(False)
+    eng = capi.Engine(is_directed=False, shuffle_walk_order=False, global_seed=5)
+    for b in (b1, b2):
+        og.add_edges(*b)
+        eng.add_edges(*b)
+    wpn, L = 3, 12
+    uniq = np.unique(np.concatenate([b2[0], b2[1]])).astype(np.int32)
+    assert uniq.size > np.unique(b2[0]).size  # the targets add starts
+    starts = np.repeat(uniq, wpn)
+    direction = "Forward_In_Time" if forward else "Backward_In_Time"
+    for picker in ("Linear", "ExponentialIndex"):
+        dr = graphs.draws(len(starts), L, seed=21)
+        ref = og.walks(L, picker, "Uniform", forward, starts, dr)
+        got = eng.sample("last_batch", L, picker, wpn, initial_edge_bias="Uniform",
+                         direction=direction, replay=dr, shuffle=False)
+        for k in ("nodes", "timestamps", "lens", "edge_ids"):
+            assert np.array_equal(getattr(ref, k), getattr(got, k)), (picker, k)
+        # every walk that found a start edge begins at its start node
+        lens = got.lens.astype(np.int64)
+        rows = np.nonzero(lens > 0)[0]
+        assert rows.size > len(starts) // 2
+        origin = got.nodes[rows, 0] if forward else got.nodes[rows, lens[rows] - 1]
+        assert np.array_equal(origin, starts[rows])
+    eng.close()
+
+
+def test_last_batch_undirected_through_the_class():
+    """The drop-in class: unshuffled last-batch walks of an undirected graph
+    come in the order of the batch's sorted unique endpoints."""
+    b1, b2 = _last_batch_graph(12)
+    tw = _trw(is_directed=False, global_seed=8, shuffle_walk_order=False)
+    tw.add_multiple_edges(*b1)
+    tw.add_multiple_edges(*b2)
+    wpn = 2
+    nodes, _, lens, _ = tw.get_random_walks_and_times_for_last_batch(
+        max_walk_len=6, walk_bias="Uniform", num_walks_per_node=wpn)
+    starts = np.repeat(np.unique(np.concatenate([b2[0], b2[1]])), wpn)
+    assert nodes.shape == (starts.size, 6)
+    rows = np.nonzero(lens > 0)[0]
+    assert np.array_equal(nodes[rows, 0], starts[rows])
+
+
+def test_node_features_grow_and_keep_old_rows():
+    """graph/node_features.cu:7-66, restating test/test_node_features.cpp:32-75:
+    setting features sizes the dense store to max_node_id + 1 rows (zeros
+    where unset), a later call after the graph grows keeps the old rows, and
+    rows can be set through arbitrary id lists."""
+    tw = _trw(is_directed=True)
+    tw.add_multiple_edges(np.array([0, 2], np.int32), np.array([1, 3], np.int32),
+                          np.array([1, 2], np.int64))  # max_node_id 3
+    tw.set_node_features(np.array([1, 3], np.int32),
+                         np.array([[1.0, 2.0], [3.0, 4.0]], np.float32))
+    f = tw.get_node_features()
+    assert f.shape == (4, 2)
+    np.testing.assert_array_equal(f[1], [1.0, 2.0])
+    np.testing.assert_array_equal(f[3], [3.0, 4.0])
+    np.testing.assert_array_equal(f[[0, 2]], 0.0)
+    tw.add_multiple_edges(np.array([4], np.int32), np.array([5], np.int32),
+                          np.array([3], np.int64))  # max_node_id 5
+    tw.set_node_features(np.array([5], np.int32), np.array([[9.0, 10.0]], np.float32))
+    f = tw.get_node_features()
+    assert f.shape == (6, 2)
+    np.testing.assert_array_equal(f[1], [1.0, 2.0])  # kept on grow
+    np.testing.assert_array_equal(f[3], [3.0, 4.0])
+    np.testing.assert_array_equal(f[5], [9.0, 10.0])
+    np.testing.assert_array_equal(f[[0, 2, 4]], 0.0)
+    with pytest.raises(RuntimeError, match="feature_dim mismatch"):
+        tw.set_node_features(np.array([1], np.int32), np.array([[1.0, 2.0, 3.0]], np.float32))
+
+    # SetNodeFeaturesWithPointers: ids {0, 2}, dim 3
+    tw2 = _trw(is_directed=True)
+    tw2.add_multiple_edges(np.array([0], np.int32), np.array([2], np.int32),
+                           np.array([5], np.int64))  # max_node_id 2
+    tw2.set_node_features(np.array([0, 2], np.int32),
+                          np.array([[7.0, 8.0, 9.0], [1.0, 2.0, 3.0]], np.float32))
+    flat = tw2.get_node_features().ravel()
+    assert flat[2] == 9.0 and flat[2 * 3] == 1.0
+    assert tw2.get_node_features().shape == (3, 3)
+    with pytest.raises(RuntimeError, match="row count"):
+        tw2.set_node_features(np.array([0, 1], np.int32), np.array([[1.0, 2.0, 3.0]], np.float32))
+
+
+def test_failed_ingest_leaves_an_empty_usable_engine():
+    """A device allocation failing at any point of an ingest (forced by the
+    test hook) raises MemoryError and leaves the engine empty, as after
+    clear(); the engine then samples (no walks start) and a new ingest gives
+    the oracle's index and replay walks."""
+    from oracle import pyoracle as po
+    from temporal_random_walk import capi
+    s1, d1, t1 = graphs.cfg1(n_nodes=300, n_edges=2_000, seed=3)
+    s2, d2, t2 = graphs.cfg1(n_nodes=3_000, n_edges=40_000, seed=4)
+    og1 = po.OracleGraph(True, enable_weight_computation=True, enable_temporal_node2vec=True)
+    og1.add_edges(s1, d1, t1)
+    og = po.OracleGraph(True, enable_weight_computation=True, enable_temporal_node2vec=True)
+    og.add_edges(s2, d2, t2)
+    L = 8
+    starts = -np.ones(500, np.int32)
+    dr = graphs.draws(500, L, seed=2)
+    ref = og.walks(L, "ExponentialIndex", "Uniform", True, starts, dr)
+    failures = 0
+    for k in range(200):
+        eng = capi.Engine(is_directed=True, enable_weight_computation=True,
+                          enable_temporal_node2vec=True, shuffle_walk_order=False, global_seed=1)
+        eng.add_edges(s1, d1, t1)
+        capi.debug_fail_allocation(k)
+        try:
+            eng.add_edges(s2, d2, t2)  # larger: grows the buffers
+            done = True
+        except MemoryError:
+            done = False
+        finally:
+            capi.debug_fail_allocation(-1)
+        if done:
+            eng.close()
+            break
+        failures += 1
+        # a failure before the batch was accepted (staging) keeps the store;
+        # one after it leaves the engine empty
+        if eng.edge_count() == len(s1):
+            for name in ("timestamps", "node_ts_sorted_outbound_indices"):
+                assert np.array_equal(og1.array(name), eng.array(name)), (k, name)
+        else:
+            assert eng.edge_count() == 0
+            w = eng.sample("total", L, "Uniform", 50, shuffle=False)
+            assert int(w.lens.sum()) == 0 and np.all(w.nodes == -1)
+        eng.clear()
+        eng.add_edges(s2, d2, t2)
+        for name in ("timestamps", "node_ts_sorted_outbound_indices",
+                     "node_ts_group_inbound_offsets", "node_adj_neighbors"):
+            assert np.array_equal(og.array(name), eng.array(name)), (k, name)
+        got = eng.sample("total", L, "ExponentialIndex", 500, initial_edge_bias="Uniform",
+                         replay=dr, shuffle=False)
+        for name in ("nodes", "timestamps", "lens", "edge_ids"):
+            assert np.array_equal(getattr(ref, name), getattr(got, name)), (k, name)
+        eng.close()
+    assert failures >= 10  # the ingest allocates at many points
+
+
+def test_walk_stats_byte_accounting():
+    """trw_get_walk_stats against numpy: steps, the per-hop demand bytes
+    (72 + 8 ceil(log2(G_u + 1)) B with the reference's types) and the
+    compulsory bytes of the walk kernel (start states, processing order and
+    the sampled direction's index read once; packed scratch and lengths
+    written once)."""
+    from temporal_random_walk import capi
+    s, d, t = graphs.powerlaw(5_000, 60_000, n_ts=2_000, seed=9)
+    eng = capi.Engine(is_directed=True, shuffle_walk_order=False, global_seed=3)
+    eng.add_edges(s, d, t)
+    L, n = 16, 70_000  # >= 2^16 walks: start-time order
+    w = eng.sample("total", L, "ExponentialIndex", n, initial_edge_bias="Uniform")
+    st = eng.walk_stats()
+    lens = w.lens.astype(np.int64)
+    assert st["total_len"] == lens.sum()
+    assert st["transitions"] == np.maximum(lens - 1, 0).sum()
+    assert st["nonempty_walks"] == (lens > 0).sum()
+    cnt = eng.array("count_ts_group_per_node_outbound").astype(np.int64)
+    G = np.diff(cnt)
+    ref = 40 * n + 12 * (lens >= 1).sum() + 20 * (lens >= 2).sum()
+    for k in range(1, L - 1):
+        rows = lens > k + 1
+        g = G[w.nodes[rows, k]]
+        probes = np.where(g > 0, np.ceil(np.log2(g + 1)), 0).astype(np.int64)
+        ref += int((72 + 8 * probes).sum())
+    assert st["reference_bytes"] == ref
+    vc = eng.array("node_group_outbound_offsets").size
+    g_o = eng.array("node_ts_group_outbound_offsets").size
+    n_ent = eng.array("node_ts_sorted_outbound_indices").size
+    index = 16 * vc + 4 * 2 * (g_o + vc) + 8 * (g_o + 1) + 8 * n_ent
+    assert st["compulsory_read_bytes"] == (16 + 4) * n + index
+    assert st["compulsory_write_bytes"] == 8 * n + 8 * lens.sum()
+    eng.close()

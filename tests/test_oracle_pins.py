@@ -378,3 +378,30 @@ def test_philox_shuffle_order_is_a_permutation():
     assert np.array_equal(np.sort(order), np.arange(10_000))
     assert not np.array_equal(order, np.arange(10_000))
     assert np.array_equal(order, po.philox_shuffle_order(99, 10_000))
+
+
+@pytest.mark.parametrize("directed", [True, False])
+def test_parallel_oracle_ingest_equals_serial(directed):
+    """The oracle's OpenMP ingest (parallel stable sort and merge, radix node
+    sort, chunked group scans) gives the serial ingest's arrays for any
+    thread count: multi-batch, ties, eviction and weights included."""
+    rng = np.random.default_rng(17)
+    batches = []
+    for k in range(3):
+        n = 150_000
+        s = graphs.zipf_ids(rng, n, 40_000, 1.6)
+        d = rng.integers(0, 40_000, n).astype(np.int32)
+        t = rng.integers(k * 300, k * 300 + 1_000, n).astype(np.int64)  # heavy ties
+        batches.append((s, d, t))
+    names = list(po.ARRAY_DTYPES)
+    names.remove("edge_features")
+    results = []
+    for threads in (1, 3, 8):
+        og = po.OracleGraph(directed, max_time_capacity=1_500, enable_weight_computation=True,
+                            enable_temporal_node2vec=True, timescale_bound=20.0)
+        for b in batches:
+            og.add_edges(*b, num_threads=threads)
+        results.append({n: og.array(n) for n in names})
+    for r in results[1:]:
+        for n in names:
+            assert np.array_equal(results[0][n], r[n]), n
