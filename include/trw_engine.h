@@ -227,6 +227,25 @@ trw_status trw_add_prefetched_edges(void* handle);
 trw_status trw_sample(void* handle, const trw_sample_params* params, trw_walks* out);
 /* Same, leaving the walks in device memory owned by the handle. */
 trw_status trw_sample_device(void* handle, const trw_sample_params* params, trw_walks* out);
+/* Same as trw_sample_device, into caller-owned device buffers, allocating
+ * nothing: no hipMalloc, hipFree or allocating library call.  No counterpart
+ * in the reference; it is for callers that cannot allocate (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid allocation).
+ *
+ * On entry out->nodes, ->timestamps, ->walk_lens, ->edge_ids and, when the
+ * store has edge features, ->edge_features point to device buffers with room
+ * for capacity_walks walks (rows of max_walk_len, max_walk_len - 1 and
+ * (max_walk_len - 1) * feature_dim values); on return num_walks, max_walk_len
+ * and feature_dim are set.  Every per-call buffer (start arrays, draws,
+ * processing order, walk scratch) comes from a fixed device array of
+ * 128 MiB per device, held until the process ends: a sample needing more
+ * (about 640 B per walk at max_walk_len 80, plus 50 B) or more walks than
+ * capacity_walks is rejected with TRW_ERR_INVALID_ARGUMENT.  Calls on one
+ * device share that array, so calls that overlap on one device race; the
+ * array keeps the last call's contents.  trw_get_walk_stats does not describe
+ * these walks. */
+trw_status trw_sample_device_noalloc(void* handle, const trw_sample_params* params,
+                                     uint64_t capacity_walks, trw_walks* out);
 /* free() of the host buffers of a trw_walks returned by trw_sample. */
 void trw_walks_free(trw_walks* walks);
 

@@ -1192,8 +1192,12 @@ void Engine::clear() {
 
 void update_neg1_rank(Engine& e) {
     e.neg1_rank.resize(1);
+    launch_neg1_rank(e, e.neg1_rank.p);
+}
+
+void launch_neg1_rank(Engine& e, int32_t* out) {
     hipLaunchKernelGGL(neg1_rank_kernel, dim3(1), dim3(1), 0, e.stream, e.uniq_ts.p,
-                       static_cast<uint32_t>(e.E ? e.T : 0), e.neg1_rank.p);
+                       static_cast<uint32_t>(e.E ? e.T : 0), out);
     check_hip(hipGetLastError(), "neg1 rank launch");
 }
 

@@ -17,6 +17,7 @@
 namespace trw {
 
 Engine::Engine(const trw_config& c) : cfg(c), device(c.device_id) {
+    init_noalloc_scratch(device);  // the device is current (trw_create)
     check_hip(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
     check_hip(hipStreamCreateWithFlags(&side, hipStreamNonBlocking), "hipStreamCreate");
     check_hip(hipEventCreateWithFlags(&side_done, hipEventDisableTiming), "hipEventCreate");
@@ -278,6 +279,31 @@ trw_status trw_sample_device(void* handle, const trw_sample_params* params, trw_
         out->walk_lens = e.w_lens.p;
         out->edge_ids = e.w_eids.p;
         out->edge_features = e.w_feat.n ? e.w_feat.p : nullptr;
+    });
+}
+
+trw_status trw_sample_device_noalloc(void* handle, const trw_sample_params* params,
+                                     uint64_t capacity_walks, trw_walks* out) {
+    return guarded(handle, [&](Engine& e) {
+        if (!params || !out) throw trw::InvalidArgument("null argument");
+        trw::SampleTarget t{};
+        t.space.base = static_cast<unsigned char*>(trw::noalloc_scratch(e.device));
+        t.space.cap = trw::kNoAllocScratchBytes;
+        t.capacity_walks = capacity_walks;
+        t.nodes = out->nodes;
+        t.ts = out->timestamps;
+        t.lens = out->walk_lens;
+        t.eids = out->edge_ids;
+        t.feat = out->edge_features;
+        const bool want_feat = e.feat_dim > 0 && params->max_walk_len > 1;
+        if (capacity_walks && (!t.nodes || !t.ts || !t.lens ||
+                               (params->max_walk_len > 1 && !t.eids) || (want_feat && !t.feat)))
+            throw trw::InvalidArgument("null output buffer");
+        e.sample(*params, &t);
+        out->num_walks = e.w_last_num;
+        out->max_walk_len = params->max_walk_len;
+        out->feature_dim = static_cast<int32_t>(want_feat ? e.feat_dim : 0);
+        if (!want_feat) out->edge_features = nullptr;
     });
 }
 

@@ -51,6 +51,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cstring>
 #include <memory>
@@ -117,6 +118,48 @@ struct DBuf {
         std::swap(cap, o.cap);
     }
     size_t bytes() const { return n * sizeof(T); }
+};
+
+// Where one sample call's per-call device buffers come from: the engine's
+// grow-only buffers, or -- for trw_sample_device_noalloc -- a fixed device
+// region handed out front to back (no allocation; a call needing more than
+// the region is rejected before any work is queued).
+struct SampleSpace {
+    unsigned char* base = nullptr;  // nullptr: the engine's buffers
+    size_t cap = 0, used = 0;
+
+    // n elements: the engine buffer `own` (grown if needed) or the next
+    // 256-byte aligned piece of the region
+    template <typename T>
+    T* take(DBuf<T>& own, size_t n) {
+        if (!base) {
+            own.resize(n);
+            return own.p;
+        }
+        const size_t off = (used + 255) & ~static_cast<size_t>(255);
+        if (n > (cap - std::min(cap, off)) / sizeof(T))
+            throw InvalidArgument("sample needs more device scratch than the " +
+                                  std::to_string(cap >> 20) +
+                                  " MiB of the no-allocation entry point");
+        used = off + n * sizeof(T);
+        return reinterpret_cast<T*>(base + off);
+    }
+};
+
+// Size of the device array trw_sample_device_noalloc takes its per-call
+// buffers from (one per device, held for the life of the process).
+constexpr size_t kNoAllocScratchBytes = size_t{128} << 20;
+
+// Caller-owned device outputs of trw_sample_device_noalloc, and the fixed
+// scratch region its per-call buffers come from.
+struct SampleTarget {
+    SampleSpace space;
+    uint64_t capacity_walks;
+    int32_t* nodes;
+    int64_t* ts;
+    uint64_t* lens;
+    int64_t* eids;
+    float* feat;
 };
 
 // One entry of a node's edge list in walk order: the node reached over the
@@ -315,6 +358,10 @@ struct Engine {
     DBuf<int32_t> starts;
     DBuf<int64_t> cutoffs;
     DBuf<double> replay;
+    // start-array temporaries of a sample (kept between calls: no per-call
+    // allocation once they are large enough)
+    DBuf<int32_t> s_ids, s_seeds, s_tmp32;
+    DBuf<int64_t> s_cuts, s_tmp64;
     DBuf<uint64_t> acc64;
 
     // walks (device): slot-major scratch written by the walk kernel (node,
@@ -328,6 +375,7 @@ struct Engine {
     DBuf<uint64_t> w_lens;
     DBuf<float> w_feat;
     uint64_t w_num = 0;
+    uint64_t w_last_num = 0;  // walks of the last sample, wherever they went
     int w_len = 0;
     int w_dir_forward = 1;
     int w_constrained = 0;  // the last sample started from given nodes
@@ -376,7 +424,10 @@ struct Engine {
                         const float* d_feat, size_t n, size_t dim, int64_t tmin, int64_t tmax);
 
     // sampling into w_* buffers
-    void sample(const trw_sample_params& p);
+    // sampling: into the engine's w_* buffers, or -- with `into` -- into
+    // caller-owned device outputs with every per-call buffer taken from
+    // into->space (trw_sample_device_noalloc: no allocation)
+    void sample(const trw_sample_params& p, const SampleTarget* into = nullptr);
 
     size_t memory_used() const;
 
@@ -404,7 +455,13 @@ void pick_weights_batch(const double* cumulative, uint64_t size, const uint64_t*
                         const uint64_t* group_end, uint64_t n, const double* draws, uint64_t seed,
                         int32_t* out);
 // Rank of timestamp -1 among the stored unique timestamps (-2 if absent) into
-// e.neg1_rank, on the engine stream.
+// e.neg1_rank (update_neg1_rank) or into out, on the engine stream.
 void update_neg1_rank(Engine& e);
+void launch_neg1_rank(Engine& e, int32_t* out);
+// The no-allocation scratch array of a device: its address is looked up once
+// per device, with the device current (init_noalloc_scratch, at the first
+// handle's creation); noalloc_scratch returns it.
+void init_noalloc_scratch(int device);
+void* noalloc_scratch(int device);
 
 }  // namespace trw

@@ -25,7 +25,9 @@
 #include <math.h>
 
 #include <algorithm>
+#include <mutex>
 #include <random>
+#include <vector>
 
 #include "engine.h"
 #include "trw_device.h"
@@ -1283,8 +1285,46 @@ __global__ __launch_bounds__(kB) void walk_stats_kernel(const int32_t* __restric
 
 }  // namespace
 
-void Engine::sample(const trw_sample_params& p) {
+// ---- fixed scratch of the no-allocation entry point -------------------------
+// trw_sample_device_noalloc takes every per-call buffer of a sample from this
+// array instead of allocating.  Each device the library runs on holds its own
+// copy for the life of the process.  In host code the array's name is only a
+// stand-in: its device address comes from hipGetSymbolAddress, looked up once
+// per device (with that device current) when the first handle on it is
+// created, and only that address is handed to kernels and copies.  Calls on
+// one device share the array, so overlapping calls race.
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+std::vector<void*> g_scratch_ptr;  // per device; nullptr: not looked up yet
+}  // namespace
+
+void init_noalloc_scratch(int device) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (device < 0) throw InvalidArgument("device id out of range");
+    if (g_scratch_ptr.size() <= static_cast<size_t>(device)) g_scratch_ptr.resize(device + 1, nullptr);
+    if (g_scratch_ptr[device]) return;
+    int cur = -1;
+    check_hip(hipGetDevice(&cur), "hipGetDevice");
+    if (cur != device) throw std::runtime_error("no-allocation scratch: device is not current");
+    void* ptr = nullptr;
+    check_hip(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    if (!ptr) throw std::runtime_error("no-allocation scratch: null symbol address");
+    g_scratch_ptr[device] = ptr;
+}
+
+void* noalloc_scratch(int device) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (device < 0 || static_cast<size_t>(device) >= g_scratch_ptr.size() || !g_scratch_ptr[device])
+        throw std::runtime_error("no-allocation scratch was not set up on this device");
+    return g_scratch_ptr[device];
+}
+
+void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
     hipStream_t s = stream;
+    // per-call buffers: the engine's, or the caller's fixed region
+    SampleSpace sp = into ? into->space : SampleSpace{};
     int64_t* hs = reinterpret_cast<int64_t*>(host_scalars);
     const int L = p.max_walk_len;
     if (L < 0) throw InvalidArgument("max_walk_len must be >= 0");
@@ -1308,6 +1348,8 @@ void Engine::sample(const trw_sample_params& p) {
     // ---- start array (core/temporal_random_walk.cu:394-588)
     uint64_t nw = 0;
     bool have_starts = false, have_cutoffs = false;
+    int32_t* a_starts = nullptr;
+    int64_t* a_cutoffs = nullptr;
     if (p.num_walks_per_node < 0 && p.mode != TRW_START_TOTAL)
         throw InvalidArgument("num_walks_per_node must be >= 0");
     const int wpn = p.num_walks_per_node;
@@ -1315,75 +1357,78 @@ void Engine::sample(const trw_sample_params& p) {
         case TRW_START_TOTAL: {
             if (p.num_walks_total < 0) throw InvalidArgument("num_walks_total must be >= 0");
             nw = static_cast<uint64_t>(p.num_walks_total);
+            if (into && nw > into->capacity_walks)
+                throw InvalidArgument("the sample has more walks than the outputs' capacity");
             break;
         }
         case TRW_START_ALL_NODES:
         case TRW_START_LAST_BATCH: {
             size_t count = 0;
-            DBuf<int32_t> ids;
+            int32_t* ids = nullptr;
             if (p.mode == TRW_START_ALL_NODES) {
                 const size_t v = active.n;
-                flags.ensure(v + 1);
-                scan.ensure(v + 1);
-                scan_scratch.ensure(scan_scratch_elems(v + 1));
+                uint32_t* fl = sp.take(flags, v + 1);
+                uint32_t* sc = sp.take(scan, v + 1);
+                uint32_t* ss = sp.take(scan_scratch, scan_scratch_elems(v + 1));
                 if (v) {
                     hipLaunchKernelGGL(flags_from_u8_kernel, dim3(grid_for(v)), dim3(kB), 0, s,
-                                       active.p, v, flags.p);
+                                       active.p, v, fl);
                 }
-                exclusive_scan_u32(flags.p, scan.p, v, scan_scratch.p, s);
-                check_hip(hipMemcpyAsync(hs, scan.p + v, 4, hipMemcpyDeviceToHost, s), "count");
+                exclusive_scan_u32(fl, sc, v, ss, s);
+                check_hip(hipMemcpyAsync(hs, sc + v, 4, hipMemcpyDeviceToHost, s), "count");
                 sync();
                 uint32_t c;
                 std::memcpy(&c, hs, 4);
                 count = c;
-                ids.resize(count);
+                ids = sp.take(s_ids, count);
                 if (v) {
                     hipLaunchKernelGGL(compact_ids_kernel, dim3(grid_for(v)), dim3(kB), 0, s,
-                                       flags.p, scan.p, v, ids.p);
+                                       fl, sc, v, ids);
                 }
             } else {
                 // unique sources (directed) or unique endpoints (undirected) of the
                 // last batch, ascending (core/temporal_random_walk.cu:157-272)
                 const size_t m = cfg.is_directed ? last_n : 2 * last_n;
-                k32a.ensure(m);
-                k32b.ensure(m);
-                hist.ensure(radix_hist_elems(m));
-                flags.ensure(m + 1);
-                scan.ensure(m + 1);
-                scan_scratch.ensure(scan_scratch_elems(m + 1));
+                uint32_t* ka = sp.take(k32a, m);
+                uint32_t* kb = sp.take(k32b, m);
+                uint32_t* hi = sp.take(hist, radix_hist_elems(m));
+                uint32_t* fl = sp.take(flags, m + 1);
+                uint32_t* sc = sp.take(scan, m + 1);
+                uint32_t* ss = sp.take(scan_scratch, scan_scratch_elems(m + 1));
                 if (last_n) {
                     hipLaunchKernelGGL(u32_from_i32_kernel, dim3(grid_for(last_n)), dim3(kB), 0, s,
-                                       last_src.p, last_n, k32a.p);
+                                       last_src.p, last_n, ka);
                     if (!cfg.is_directed) {
                         hipLaunchKernelGGL(u32_from_i32_kernel, dim3(grid_for(last_n)), dim3(kB),
-                                           0, s, last_dst.p, last_n, k32a.p + last_n);
+                                           0, s, last_dst.p, last_n, ka + last_n);
                     }
                 }
-                const int w = radix_sort_u32(k32a.p, nullptr, k32b.p, nullptr, m, 0, 32, hist.p, s);
-                uint32_t* keys = w ? k32b.p : k32a.p;
+                const int w = radix_sort_u32(ka, nullptr, kb, nullptr, m, 0, 32, hi, s);
+                uint32_t* keys = w ? kb : ka;
                 if (m) {
                     hipLaunchKernelGGL(unique_flags_kernel, dim3(grid_for(m)), dim3(kB), 0, s,
-                                       keys, m, flags.p);
+                                       keys, m, fl);
                 }
-                exclusive_scan_u32(flags.p, scan.p, m, scan_scratch.p, s);
-                check_hip(hipMemcpyAsync(hs, scan.p + m, 4, hipMemcpyDeviceToHost, s), "count");
+                exclusive_scan_u32(fl, sc, m, ss, s);
+                check_hip(hipMemcpyAsync(hs, sc + m, 4, hipMemcpyDeviceToHost, s), "count");
                 sync();
                 uint32_t c;
                 std::memcpy(&c, hs, 4);
                 count = c;
-                ids.resize(count);
+                ids = sp.take(s_ids, count);
                 if (m) {
                     hipLaunchKernelGGL(compact_keys_kernel, dim3(grid_for(m)), dim3(kB), 0, s,
-                                       keys, flags.p, scan.p, m, ids.p);
+                                       keys, fl, sc, m, ids);
                 }
             }
             nw = static_cast<uint64_t>(count) * static_cast<uint64_t>(wpn);
-            starts.resize(nw);
+            if (into && nw > into->capacity_walks)
+                throw InvalidArgument("the sample has more walks than the outputs' capacity");
+            a_starts = sp.take(starts, nw);
             if (nw) {
                 hipLaunchKernelGGL((repeat_kernel<int32_t>), dim3(grid_for(nw)), dim3(kB), 0, s,
-                                   ids.p, nw, wpn, starts.p);
+                                   ids, nw, wpn, a_starts);
             }
-            sync();  // `ids` is released at scope exit
             have_starts = true;
             break;
         }
@@ -1391,32 +1436,33 @@ void Engine::sample(const trw_sample_params& p) {
             const size_t ns = p.num_seed_nodes;
             if (ns && !p.seed_nodes) throw InvalidArgument("seed_nodes is null");
             nw = static_cast<uint64_t>(ns) * static_cast<uint64_t>(wpn);
-            DBuf<int32_t> seeds;
-            DBuf<int64_t> cuts;
-            seeds.resize(ns);
+            if (into && nw > into->capacity_walks)
+                throw InvalidArgument("the sample has more walks than the outputs' capacity");
+            int32_t* seeds = sp.take(s_seeds, ns);
             if (ns) {
-                check_hip(hipMemcpyAsync(seeds.p, p.seed_nodes, ns * 4, hipMemcpyHostToDevice, s),
+                check_hip(hipMemcpyAsync(seeds, p.seed_nodes, ns * 4, hipMemcpyHostToDevice, s),
                           "seeds H2D");
             }
-            starts.resize(nw);
+            a_starts = sp.take(starts, nw);
             if (nw) {
                 hipLaunchKernelGGL((repeat_kernel<int32_t>), dim3(grid_for(nw)), dim3(kB), 0, s,
-                                   seeds.p, nw, wpn, starts.p);
+                                   seeds, nw, wpn, a_starts);
             }
             if (p.cutoff_times) {
-                cuts.resize(ns);
+                int64_t* cuts = sp.take(s_cuts, ns);
                 if (ns) {
-                    check_hip(hipMemcpyAsync(cuts.p, p.cutoff_times, ns * 8,
+                    check_hip(hipMemcpyAsync(cuts, p.cutoff_times, ns * 8,
                                              hipMemcpyHostToDevice, s),
                               "cutoffs H2D");
                 }
-                cutoffs.resize(nw);
+                a_cutoffs = sp.take(cutoffs, nw);
                 if (nw) {
                     hipLaunchKernelGGL((repeat_kernel<int64_t>), dim3(grid_for(nw)), dim3(kB), 0,
-                                       s, cuts.p, nw, wpn, cutoffs.p);
+                                       s, cuts, nw, wpn, a_cutoffs);
                 }
                 have_cutoffs = true;
             }
+            // the host arrays may be released once the copies have run
             sync();
             have_starts = true;
             break;
@@ -1430,30 +1476,24 @@ void Engine::sample(const trw_sample_params& p) {
     // ---- optional shuffle of the walk order (same permutation for cutoffs)
     if (have_starts && shuffle && nw > 1) {
         if (nw > 0xffffffffull) throw InvalidArgument("shuffle supports < 2^32 walks");
-        k32a.ensure(nw);
-        k32b.ensure(nw);
-        v32a.ensure(nw);
-        v32b.ensure(nw);
-        hist.ensure(radix_hist_elems(nw));
+        uint32_t* ka = sp.take(k32a, nw);
+        uint32_t* kb = sp.take(k32b, nw);
+        uint32_t* va = sp.take(v32a, nw);
+        uint32_t* vb = sp.take(v32b, nw);
+        uint32_t* hi = sp.take(hist, radix_hist_elems(nw));
         hipLaunchKernelGGL(random_keys_kernel, dim3(grid_for(nw)), dim3(kB), 0, s, nw,
-                           static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32), k32a.p,
-                           v32a.p);
-        const int w = radix_sort_u32(k32a.p, v32a.p, k32b.p, v32b.p, nw, 0, 32, hist.p, s);
-        const uint32_t* perm = w ? v32b.p : v32a.p;
-        DBuf<int32_t> tmp;
-        tmp.resize(nw);
+                           static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32), ka, va);
+        const int w = radix_sort_u32(ka, va, kb, vb, nw, 0, 32, hi, s);
+        const uint32_t* perm = w ? vb : va;
+        int32_t* ps = sp.take(s_tmp32, nw);
         hipLaunchKernelGGL((permute_kernel<int32_t>), dim3(grid_for(nw)), dim3(kB), 0, s,
-                           starts.p, perm, nw, tmp.p);
-        starts.swap(tmp);
+                           a_starts, perm, nw, ps);
+        a_starts = ps;
         if (have_cutoffs) {
-            DBuf<int64_t> tmpc;
-            tmpc.resize(nw);
+            int64_t* pc = sp.take(s_tmp64, nw);
             hipLaunchKernelGGL((permute_kernel<int64_t>), dim3(grid_for(nw)), dim3(kB), 0, s,
-                               cutoffs.p, perm, nw, tmpc.p);
-            cutoffs.swap(tmpc);
-            sync();
-        } else {
-            sync();
+                               a_cutoffs, perm, nw, pc);
+            a_cutoffs = pc;
         }
     }
 
@@ -1472,12 +1512,12 @@ void Engine::sample(const trw_sample_params& p) {
             const double r = p.replay_draws[i];
             if (!(r >= 0.0 && r < 1.0)) throw InvalidArgument("replay_draws must lie in [0, 1)");
         }
-        replay.resize(need);
+        double* rp = sp.take(replay, need);
         if (need) {
-            check_hip(hipMemcpyAsync(replay.p, p.replay_draws, need * 8, hipMemcpyHostToDevice, s),
+            check_hip(hipMemcpyAsync(rp, p.replay_draws, need * 8, hipMemcpyHostToDevice, s),
                       "replay H2D");
         }
-        ds.replay = replay.p;
+        ds.replay = rp;
     }
 
     // ---- outputs
@@ -1498,22 +1538,43 @@ void Engine::sample(const trw_sample_params& p) {
     w_num = 0;
     w_len = 0;
     w_feat.n = 0;
+    uint64_t* sc_packed = nullptr;
+    int32_t* sc_nodes = nullptr;
+    uint32_t *sc_rank = nullptr, *sc_eids = nullptr;
     if (packed) {
-        sw_packed.resize(padded * L);
-        sw_nodes.release();
-        sw_rank.release();
-        sw_eids.release();
+        if (!into) {
+            sw_nodes.release();
+            sw_rank.release();
+            sw_eids.release();
+        }
+        sc_packed = sp.take(sw_packed, padded * L);
     } else {
-        sw_packed.release();
-        sw_nodes.resize(padded * L);
-        sw_rank.resize(padded * L);
-        sw_eids.resize(padded * (L > 0 ? L - 1 : 0));
+        if (!into) sw_packed.release();
+        sc_nodes = sp.take(sw_nodes, padded * L);
+        sc_rank = sp.take(sw_rank, padded * L);
+        sc_eids = sp.take(sw_eids, padded * (L > 0 ? L - 1 : 0));
     }
-    w_nodes.resize(slots);
-    w_ts.resize(slots);
-    w_eids.resize(eslots);
-    w_lens.resize(nw);
-    w_num = nw;
+    // outputs: the engine's buffers, or the caller's
+    int32_t* o_nodes;
+    int64_t *o_ts, *o_eids;
+    uint64_t* o_lens;
+    if (into) {
+        o_nodes = into->nodes;
+        o_ts = into->ts;
+        o_eids = into->eids;
+        o_lens = into->lens;
+    } else {
+        w_nodes.resize(slots);
+        w_ts.resize(slots);
+        w_eids.resize(eslots);
+        w_lens.resize(nw);
+        o_nodes = w_nodes.p;
+        o_ts = w_ts.p;
+        o_eids = w_eids.p;
+        o_lens = w_lens.p;
+    }
+    w_num = into ? 0 : nw;  // the walk statistics describe the engine's buffers
+    w_last_num = nw;
     w_len = L;
     w_dir_forward = forward ? 1 : 0;
     w_constrained = have_starts ? 1 : 0;
@@ -1530,8 +1591,13 @@ void Engine::sample(const trw_sample_params& p) {
     g.E = static_cast<uint32_t>(E);
     g.tsg_off = tsg_off.p;
     g.uniq_ts = uniq_ts.p;
-    if (neg1_rank.n == 0) update_neg1_rank(*this);  // no build since the last clear
-    g.neg1_rank = neg1_rank.p;
+    if (neg1_rank.n == 0) {  // no build since the last clear
+        int32_t* nr = sp.take(neg1_rank, 1);
+        launch_neg1_rank(*this, nr);
+        g.neg1_rank = nr;
+    } else {
+        g.neg1_rank = neg1_rank.p;
+    }
     g.T = static_cast<uint32_t>(T);
     g.gw = forward ? fwd_cum.p : bwd_cum.p;
     g.gw_size = weights_ready ? T : 0;
@@ -1572,15 +1638,15 @@ void Engine::sample(const trw_sample_params& p) {
     a.walk_bias = walk_bias;
     a.start_bias = start_bias;
     a.pad = cfg.walk_padding_value;
-    a.starts = have_starts ? starts.p : nullptr;
-    a.cutoffs = have_cutoffs ? cutoffs.p : nullptr;
+    a.starts = have_starts ? a_starts : nullptr;
+    a.cutoffs = have_cutoffs ? a_cutoffs : nullptr;
     a.n = nw;
     a.ds = ds;
-    a.nodes = sw_nodes.p;
-    a.ranks = sw_rank.p;
-    a.lens = w_lens.p;
-    a.eids = sw_eids.p;
-    a.packed = packed ? sw_packed.p : nullptr;
+    a.nodes = sc_nodes;
+    a.ranks = sc_rank;
+    a.lens = o_lens;
+    a.eids = sc_eids;
+    a.packed = packed ? sc_packed : nullptr;
     a.pk_nb = pk_nb;
     a.pk_rb = pk_rb;
 
@@ -1628,20 +1694,19 @@ void Engine::sample(const trw_sample_params& p) {
     if (order_mode != TRW_ORDER_WALK_ID && order_mode != TRW_ORDER_START_TIME)
         throw InvalidArgument("Invalid walk order");
     if (nw && L > 0) {
-        walk_st.ensure(4 * nw);
-        k32a.ensure(nw);
-        v32a.ensure(nw);
-        StartState* st = reinterpret_cast<StartState*>(walk_st.p);
+        StartState* st = reinterpret_cast<StartState*>(sp.take(walk_st, 4 * nw));
+        uint32_t* ka = sp.take(k32a, nw);
+        uint32_t* va = sp.take(v32a, nw);
         const uint32_t none = g.T;  // past every rank: walks without a start run last
-        TRW_LAUNCH(walk_start_kernel, dim3(grid_for(nw)), g, a, st, k32a.p, v32a.p, none);
+        TRW_LAUNCH(walk_start_kernel, dim3(grid_for(nw)), g, a, st, ka, va, none);
         a.st = st;
         if (order_mode == TRW_ORDER_START_TIME && nw > 1 && L > 1) {
-            k32b.ensure(nw);
-            v32b.ensure(nw);
-            hist.ensure(radix_hist_elems(nw));
+            uint32_t* kb = sp.take(k32b, nw);
+            uint32_t* vb = sp.take(v32b, nw);
+            uint32_t* hi = sp.take(hist, radix_hist_elems(nw));
             const int bits = std::max(1, 32 - __builtin_clz(none | 1u));
-            const int wsort = radix_sort_u32(k32a.p, v32a.p, k32b.p, v32b.p, nw, 0, bits, hist.p, s);
-            a.order = wsort ? v32b.p : v32a.p;
+            const int wsort = radix_sort_u32(ka, va, kb, vb, nw, 0, bits, hi, s);
+            a.order = wsort ? vb : va;
             a.xcd_remap = 1;
         }
         check_hip(hipGetLastError(), "walk start launch");
@@ -1665,16 +1730,16 @@ void Engine::sample(const trw_sample_params& p) {
     check_hip(hipEventRecord(ev[6], s), "event");
     if (nw && L > 0) {
         LayoutArgs la{};
-        la.sn = sw_nodes.p;
-        la.sr = sw_rank.p;
-        la.se = sw_eids.p;
+        la.sn = sc_nodes;
+        la.sr = sc_rank;
+        la.se = sc_eids;
         la.sp = a.packed;
         la.pk_nb = pk_nb;
         la.pk_rb = pk_rb;
-        la.on = w_nodes.p;
-        la.ot = w_ts.p;
-        la.oe = w_eids.p;
-        la.lens = w_lens.p;
+        la.on = o_nodes;
+        la.ot = o_ts;
+        la.oe = o_eids;
+        la.lens = o_lens;
         la.L = L;
         const int max_slots = a.packed ? kLayoutPackedMaxSlots : kLayoutMaxSlots;
         const int slot_chunks = (L + max_slots - 1) / max_slots;
@@ -1690,9 +1755,9 @@ void Engine::sample(const trw_sample_params& p) {
         // the edge ids it holds in LDS (device buffers are 256-byte aligned)
         const bool fused_feat = feat_dim > 0 && eslots && feat_dim % 4 == 0;
         if (fused_feat) {
-            w_feat.resize(eslots * feat_dim);
+            if (!into) w_feat.resize(eslots * feat_dim);
             la.feat = feat.p;
-            la.of = w_feat.p;
+            la.of = into ? into->feat : w_feat.p;
             la.fv = static_cast<uint32_t>(feat_dim / 4);
         }
         const size_t tile = a.packed ? static_cast<size_t>(la.C + 1) * (kLayoutWalks + 1) * sizeof(uint64_t)
@@ -1710,10 +1775,10 @@ void Engine::sample(const trw_sample_params& p) {
     // other dims than multiples of 4 gather from the laid-out edge ids
     if (feat_dim > 0 && eslots) {
         if (feat_dim % 4 != 0) {
-            w_feat.resize(eslots * feat_dim);
+            if (!into) w_feat.resize(eslots * feat_dim);
             hipLaunchKernelGGL(gather_walk_features_kernel, dim3(grid_capped(eslots * feat_dim)),
-                               dim3(kB), 0, s, w_eids.p, eslots, static_cast<uint32_t>(feat_dim),
-                               feat.p, w_feat.p);
+                               dim3(kB), 0, s, o_eids, eslots, static_cast<uint32_t>(feat_dim),
+                               feat.p, into ? into->feat : w_feat.p);
             check_hip(hipGetLastError(), "feature gather launch");
         }
     } else {

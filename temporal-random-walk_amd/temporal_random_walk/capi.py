@@ -61,7 +61,8 @@ ARRAYS = {
 # every symbol include/trw_engine.h declares
 EXPORTS = [
     "trw_create", "trw_destroy", "trw_last_error", "trw_abi_version", "trw_add_edges",
-    "trw_add_edges_device", "trw_prefetch_edges", "trw_add_prefetched_edges", "trw_sample", "trw_sample_device", "trw_walks_free",
+    "trw_add_edges_device", "trw_prefetch_edges", "trw_add_prefetched_edges", "trw_sample",
+    "trw_sample_device", "trw_sample_device_noalloc", "trw_walks_free",
     "trw_get_node_count", "trw_get_edge_count", "trw_get_node_ids", "trw_get_node_degrees",
     "trw_get_edges", "trw_get_is_directed", "trw_get_memory_used", "trw_get_feature_dim",
     "trw_get_latest_timestamp", "trw_clear", "trw_get_array", "trw_get_timings",
@@ -171,6 +172,8 @@ def lib():
         L.trw_add_prefetched_edges.argtypes = [P]
         L.trw_sample.argtypes = [P, C.POINTER(TrwSampleParams), C.POINTER(TrwWalks)]
         L.trw_sample_device.argtypes = [P, C.POINTER(TrwSampleParams), C.POINTER(TrwWalks)]
+        L.trw_sample_device_noalloc.argtypes = [P, C.POINTER(TrwSampleParams), C.c_uint64,
+                                                C.POINTER(TrwWalks)]
         L.trw_walks_free.argtypes = [C.POINTER(TrwWalks)]
         L.trw_walks_free.restype = None
         L.trw_get_node_count.argtypes = [P, C.POINTER(C.c_uint64)]
@@ -464,6 +467,23 @@ class Engine:
         p, keep = self._params(mode, max_walk_len, walk_bias, num_walks, **kw)
         w = TrwWalks()
         _check(self._L.trw_sample_device(self.h, C.byref(p), C.byref(w)))
+        return w
+
+    def sample_device_noalloc(self, mode, max_walk_len, walk_bias, num_walks=0, *,
+                              capacity_walks, nodes_ptr, timestamps_ptr, lens_ptr,
+                              edge_ids_ptr, features_ptr=None, **kw):
+        """trw_sample_device_noalloc: walks into the caller's device buffers
+        (room for capacity_walks walks), nothing allocated.  Returns the
+        TrwWalks filled in by the call."""
+        p, keep = self._params(mode, max_walk_len, walk_bias, num_walks, **kw)
+        w = TrwWalks()
+        w.nodes = nodes_ptr
+        w.timestamps = timestamps_ptr
+        w.walk_lens = lens_ptr
+        w.edge_ids = edge_ids_ptr
+        w.edge_features = features_ptr
+        _check(self._L.trw_sample_device_noalloc(self.h, C.byref(p), int(capacity_walks),
+                                                 C.byref(w)))
         return w
 
     # ---- queries
