@@ -204,13 +204,15 @@ __device__ __forceinline__ uint64_t pack_rec(int32_t nbr, uint32_t eid) {
     return static_cast<uint64_t>(static_cast<uint32_t>(nbr)) | (static_cast<uint64_t>(eid) << 32);
 }
 
+// The edges are src/dst[0, e); their edge ids (store positions) start at id0.
 __global__ void node_entries_kernel(const int32_t* __restrict__ src,
                                     const int32_t* __restrict__ dst, size_t e, int mode,
-                                    uint32_t* __restrict__ keys, uint64_t* __restrict__ vals) {
+                                    uint32_t id0, uint32_t* __restrict__ keys,
+                                    uint64_t* __restrict__ vals) {
     const size_t i = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
     if (i >= e) return;
     const int32_t a = src[i], b = dst[i];
-    const uint32_t id = static_cast<uint32_t>(i);
+    const uint32_t id = id0 + static_cast<uint32_t>(i);
     if (mode == 0) {
         keys[i] = static_cast<uint32_t>(a);
         vals[i] = pack_rec(b, id);
@@ -237,6 +239,119 @@ __global__ void lower_bound_offsets_kernel(const uint32_t* __restrict__ keys, si
         else hi = mid;
     }
     off[u] = static_cast<uint32_t>(lo);
+}
+
+// ---- append path: a batch whose timestamps are all >= the store's ----------
+// The stable order by (timestamp, position) then puts the batch, sorted, after
+// the store's kept edges, and every node's list keeps its old entries first:
+// the store and the node index are updated by copies and scatters instead of
+// sorts of the whole window.
+
+// Eviction over the store old[0, e_old) followed by the sorted batch (keys +
+// tmin): out[0] = evicted store edges, out[1] = evicted batch edges, out[2] /
+// out[3] = the first / last kept timestamp.  cutoff: drop ts <= cutoff.
+template <typename K>
+__global__ void append_evict_kernel(const int64_t* __restrict__ old_ts, size_t e_old,
+                                    const K* __restrict__ keys, size_t n, int64_t tmin,
+                                    int64_t cutoff, int has_cutoff, int64_t* __restrict__ out) {
+    size_t del_old = 0, del_new = 0;
+    if (has_cutoff) {
+        size_t lo = 0, hi = e_old;  // upper_bound
+        while (lo < hi) {
+            const size_t mid = lo + ((hi - lo) >> 1);
+            if (cutoff < old_ts[mid]) hi = mid;
+            else lo = mid + 1;
+        }
+        del_old = lo;
+        if (del_old == e_old && cutoff >= tmin) {
+            const uint64_t t = static_cast<uint64_t>(cutoff) - static_cast<uint64_t>(tmin);
+            lo = 0;
+            hi = n;
+            while (lo < hi) {
+                const size_t mid = lo + ((hi - lo) >> 1);
+                if (t < static_cast<uint64_t>(keys[mid])) hi = mid;
+                else lo = mid + 1;
+            }
+            del_new = lo;
+        }
+    }
+    out[0] = static_cast<int64_t>(del_old);
+    out[1] = static_cast<int64_t>(del_new);
+    const int64_t last_new = static_cast<int64_t>(static_cast<uint64_t>(keys[n - 1]) +
+                                                  static_cast<uint64_t>(tmin));
+    // the cut can empty the batch too (a window ending before every timestamp)
+    out[2] = del_old < e_old ? old_ts[del_old]
+             : del_new < n   ? static_cast<int64_t>(static_cast<uint64_t>(keys[del_new]) +
+                                                    static_cast<uint64_t>(tmin))
+                             : 0;
+    out[3] = del_new < n ? last_new : 0;
+}
+
+// ev[u] = entries of node u in the old index whose edge was evicted (edge id
+// < del).  A node's list is ordered by edge id, so they are a prefix of it, and
+// the prefix's last entry writes the count (nodes without one keep the 0 of
+// the fill; no atomics, so a hub costs one write).
+__global__ void evicted_prefix_kernel(const uint32_t* __restrict__ keys,
+                                      const EdgeRec* __restrict__ rec, size_t n, uint32_t del,
+                                      const uint32_t* __restrict__ off, uint32_t* __restrict__ ev) {
+    const size_t k = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (k >= n || rec[k].eid >= del) return;
+    const uint32_t u = keys[k];
+    if (k + 1 == n || keys[k + 1] != u || rec[k + 1].eid >= del)
+        ev[u] = static_cast<uint32_t>(k + 1) - off[u];
+}
+
+// Kept old entries of node u (0 past the old index's nodes).
+__device__ __forceinline__ uint32_t kept_old(const uint32_t* off_old, size_t v_old,
+                                             const uint32_t* ev, size_t u) {
+    return u < v_old ? off_old[u + 1] - off_old[u] - ev[u] : 0u;
+}
+
+// Entries of node u in the updated index, u in [0, v): its kept old entries
+// plus its batch entries (bstart: the batch's sorted-key offsets).
+__global__ void append_counts_kernel(const uint32_t* __restrict__ off_old, size_t v_old,
+                                     const uint32_t* __restrict__ ev,
+                                     const uint32_t* __restrict__ bstart, size_t v,
+                                     uint32_t* __restrict__ cnt) {
+    const size_t u = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (u >= v) return;
+    cnt[u] = kept_old(off_old, v_old, ev, u) + bstart[u + 1] - bstart[u];
+}
+
+// Old entry k of node u, if its edge is kept, moves to
+// off[u] + (k - off_old[u] - ev[u]) with its edge id lowered by del.
+__global__ void append_old_entries_kernel(const uint32_t* __restrict__ keys_old,
+                                          const EdgeRec* __restrict__ rec_old, size_t n_old,
+                                          uint32_t del, const uint32_t* __restrict__ off_old,
+                                          const uint32_t* __restrict__ ev,
+                                          const uint32_t* __restrict__ off,
+                                          uint32_t* __restrict__ keys, EdgeRec* __restrict__ rec) {
+    const size_t k = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (k >= n_old) return;
+    const EdgeRec r = rec_old[k];
+    if (r.eid < del) return;
+    const uint32_t u = keys_old[k];
+    const uint32_t d = off[u] + (static_cast<uint32_t>(k) - off_old[u] - ev[u]);
+    keys[d] = u;
+    rec[d] = EdgeRec{r.nbr, r.eid - del};
+}
+
+// Batch entry j (sorted stably by node) of node u follows u's kept old
+// entries: off[u] + kept_old(u) + (j - bstart[u]).
+__global__ void append_new_entries_kernel(const uint32_t* __restrict__ bkeys,
+                                          const uint64_t* __restrict__ brec, size_t m,
+                                          const uint32_t* __restrict__ bstart,
+                                          const uint32_t* __restrict__ off_old, size_t v_old,
+                                          const uint32_t* __restrict__ ev,
+                                          const uint32_t* __restrict__ off,
+                                          uint32_t* __restrict__ keys, EdgeRec* __restrict__ rec) {
+    const size_t j = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (j >= m) return;
+    const uint32_t u = bkeys[j];
+    const uint32_t d = off[u] + kept_old(off_old, v_old, ev, u) + (static_cast<uint32_t>(j) - bstart[u]);
+    keys[d] = u;
+    const uint64_t b = brec[j];
+    rec[d] = EdgeRec{static_cast<int32_t>(static_cast<uint32_t>(b)), static_cast<uint32_t>(b >> 32)};
 }
 
 // Group-start flags of the sorted entries (a new node, or a new timestamp
@@ -434,19 +549,74 @@ __global__ void adj_offsets_kernel(const uint64_t* __restrict__ keys, size_t n, 
     off[u] = static_cast<uint32_t>(lo);
 }
 
-// One slot of the adjacency pair set per distinct sorted key (linear probing;
-// the set is at most half full, so every probe sequence reaches a free slot).
+// The adjacency pair set (open addressing, linear probing, Fibonacci hash; at
+// most half full, so every probe sequence reaches a free slot), filled from
+// the pair keys sorted with their duplicates adjacent: one insertion per
+// distinct pair.  (Inserting every edge's two pairs straight from the store
+// touched the table 2E times at random -- 1.4 ms at cfg5's 9M edges, against
+// 42 us for the distinct pairs.)  Keys of active-id ranks (ranked != nullptr:
+// ids[] maps a rank back to its node) or of node ids.
+__device__ __forceinline__ void adj_set_insert(uint64_t k, int shift, uint64_t mask,
+                                               uint64_t* tab) {
+    uint64_t h = (k * kAdjHashMul) >> shift;
+    while (atomicCAS(reinterpret_cast<unsigned long long*>(tab + h),
+                     static_cast<unsigned long long>(kAdjEmpty),
+                     static_cast<unsigned long long>(k)) != kAdjEmpty)
+        h = (h + 1) & mask;
+}
+
+__global__ void adj_hash_insert_ranked_kernel(const uint32_t* __restrict__ keys, size_t n, int rb,
+                                              const uint32_t* __restrict__ ids, int b, int shift,
+                                              uint64_t mask, uint64_t* __restrict__ tab) {
+    const size_t i = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (i >= n) return;
+    const uint32_t k = keys[i];
+    if (i > 0 && keys[i - 1] == k) return;  // a repeated pair
+    const uint64_t u = ids[k >> rb], v = ids[k & ((1u << rb) - 1u)];
+    adj_set_insert((u << b) | v, shift, mask, tab);
+}
+
 __global__ void adj_hash_insert_kernel(const uint64_t* __restrict__ keys, size_t n, int shift,
                                        uint64_t mask, uint64_t* __restrict__ tab) {
     const size_t i = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
     if (i >= n) return;
     const uint64_t k = keys[i];
     if (i > 0 && keys[i - 1] == k) return;  // a repeated pair
-    uint64_t h = (k * kAdjHashMul) >> shift;
-    while (atomicCAS(reinterpret_cast<unsigned long long*>(tab + h),
-                     static_cast<unsigned long long>(kAdjEmpty),
-                     static_cast<unsigned long long>(k)) != kAdjEmpty)
-        h = (h + 1) & mask;
+    adj_set_insert(k, shift, mask, tab);
+}
+
+// Ranks of the active node ids (the exclusive scan of these flags) and the
+// ids by rank.
+__global__ void active_u32_kernel(const uint8_t* __restrict__ active, size_t v,
+                                  uint32_t* __restrict__ f) {
+    const size_t u = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (u < v) f[u] = active[u];
+}
+
+__global__ void active_ids_kernel(const uint8_t* __restrict__ active,
+                                  const uint32_t* __restrict__ rank, size_t v,
+                                  uint32_t* __restrict__ ids) {
+    const size_t u = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (u < v && active[u]) ids[rank[u]] = static_cast<uint32_t>(u);
+}
+
+// Both pairs of every edge as keys of active-id ranks: rank(owner) << rb |
+// rank(neighbour), ordered as (owner, neighbour) because ranks keep the ids'
+// order.
+__global__ void adj_rank_keys_kernel(const int32_t* __restrict__ s, const int32_t* __restrict__ d,
+                                     size_t e, const uint32_t* __restrict__ rank, int rb,
+                                     uint32_t* __restrict__ keys) {
+    const size_t i = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (i >= e) return;
+    const uint32_t ru = rank[s[i]], rv = rank[d[i]];
+    keys[2 * i] = (ru << rb) | rv;
+    keys[2 * i + 1] = (rv << rb) | ru;
+}
+
+__global__ void distinct_flags_kernel(const uint32_t* __restrict__ keys, size_t n,
+                                      uint32_t* __restrict__ flags) {
+    const size_t i = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (i < n) flags[i] = (i == 0 || keys[i] != keys[i - 1]) ? 1u : 0u;
 }
 
 // Global per-timestamp-group weights before normalisation
@@ -506,8 +676,10 @@ __device__ __forceinline__ void raw_node_weights(const NodeWeightParams& q, cons
 
 // Nodes with at most kHeavyGroups groups: one thread per node; the normalised
 // weights are accumulated sequentially in group order, exactly as the
-// reference does (node_edge_index.cu:617-639).
-constexpr uint32_t kHeavyGroups = 512;
+// reference does (node_edge_index.cu:617-639).  A wave of such threads waits
+// for its largest node's two loops, so larger nodes take the tile path (one
+// workgroup per kHeavyTile groups).
+constexpr uint32_t kHeavyGroups = 32;
 
 __global__ void node_weights_light_kernel(const uint32_t* __restrict__ cnt,
                                           const uint32_t* __restrict__ grp,
@@ -731,6 +903,8 @@ void validate_batch(const Engine& e, const void* feat, size_t n, size_t dim) {
 
 namespace {
 
+void finish_direction(Engine& e, DirIndex& dir, size_t n, size_t vc, int64_t* host_scratch);
+
 // Stable per-direction node index of the store's n entries (mode: see
 // node_entries_kernel).
 void build_direction(Engine& e, DirIndex& dir, size_t n, int key_bits, size_t vc, int mode,
@@ -751,16 +925,94 @@ void build_direction(Engine& e, DirIndex& dir, size_t n, int key_bits, size_t vc
     const size_t edges = mode == 2 ? n / 2 : n;
     if (edges)
         hipLaunchKernelGGL(node_entries_kernel, dim3(grid_for(edges)), dim3(kB), 0, s, e.src.p,
-                           e.dst.p, edges, mode, e.k32a.p, v0);
+                           e.dst.p, edges, mode, 0u, e.k32a.p, v0);
     const int which = radix_sort_u32_v64(e.k32a.p, v0, e.k32b.p, v1, n, 0, key_bits, e.hist.p, s);
     // the sorted keys become the direction's (the scratch takes the old
     // buffer, which every user sizes again before writing)
     dir.key.swap(which ? e.k32b : e.k32a);
     dir.key.n = n;
-    dir.idx.resize(n);
     dir.off.resize(vc);
     hipLaunchKernelGGL(lower_bound_offsets_kernel, dim3(grid_for(vc)), dim3(kB), 0, s, dir.key.p,
                        n, vc, dir.off.p);
+    finish_direction(e, dir, n, vc, host_scratch);
+}
+
+// The node index of one direction after an append (Engine::append_store):
+// every node's list is its old entries whose edges were kept (edge ids
+// lowered by the evicted count), then its batch entries in batch order -- the
+// stable (node, position) order of the new store, because the kept old edges
+// precede the batch.  Only the batch's entries are sorted; the old entries
+// move by one scatter.  mode as node_entries_kernel.
+void append_direction(Engine& e, DirIndex& dir, int mode, int key_bits, size_t vc,
+                      int64_t* host_scratch) {
+    hipStream_t s = e.stream;
+    const size_t per = mode == 2 ? 2 : 1;
+    const size_t n_old = dir.n_entries;
+    const size_t v_old = dir.off.n ? dir.off.n - 1 : 0;
+    const size_t v = vc - 1;
+    const size_t m = per * e.append_kept_new;
+    const size_t n = per * e.E;
+    const uint32_t del = static_cast<uint32_t>(e.append_del);
+    dir.present = true;
+    dir.n_entries = n;
+    // the batch's entries (the store's tail), sorted stably by node
+    e.k32a.ensure(m);
+    e.k32b.ensure(m);
+    e.k64a.ensure(m);
+    e.k64b.ensure(m);
+    e.hist.ensure(radix_hist_elems(m));
+    const uint32_t id0 = static_cast<uint32_t>(e.append_kept_old);
+    if (e.append_kept_new)
+        hipLaunchKernelGGL(node_entries_kernel, dim3(grid_for(e.append_kept_new)), dim3(kB), 0, s,
+                           e.src.p + id0, e.dst.p + id0, e.append_kept_new, mode, id0, e.k32a.p,
+                           e.k64a.p);
+    const int w = radix_sort_u32_v64(e.k32a.p, e.k64a.p, e.k32b.p, e.k64b.p, m, 0, key_bits,
+                                     e.hist.p, s);
+    const uint32_t* bkeys = w ? e.k32b.p : e.k32a.p;
+    const uint64_t* brec = w ? e.k64b.p : e.k64a.p;
+    e.inc_bstart.resize(vc);
+    uint32_t* bstart = e.inc_bstart.p;
+    hipLaunchKernelGGL(lower_bound_offsets_kernel, dim3(grid_for(vc)), dim3(kB), 0, s, bkeys, m,
+                       vc, bstart);
+    // evicted prefix of every old node, then the new offsets
+    e.inc_ev.resize(std::max<size_t>(v_old, 1));
+    check_hip(hipMemsetAsync(e.inc_ev.p, 0, e.inc_ev.n * 4, s), "evicted counts clear");
+    if (del && n_old)
+        hipLaunchKernelGGL(evicted_prefix_kernel, dim3(grid_for(n_old)), dim3(kB), 0, s, dir.key.p,
+                           dir.rec.p, n_old, del, dir.off.p, e.inc_ev.p);
+    e.inc_cnt.resize(vc);
+    hipLaunchKernelGGL(append_counts_kernel, dim3(grid_for(v)), dim3(kB), 0, s, dir.off.p, v_old,
+                       e.inc_ev.p, bstart, v, e.inc_cnt.p);
+    e.off_next.resize(vc);
+    e.scan_scratch.ensure(scan_scratch_elems(vc));
+    exclusive_scan_u32(e.inc_cnt.p, e.off_next.p, v, e.scan_scratch.p, s);
+    // the entries at their new places
+    e.key_next.resize(n);
+    e.rec_next.resize(n);
+    if (n_old)
+        hipLaunchKernelGGL(append_old_entries_kernel, dim3(grid_for(n_old)), dim3(kB), 0, s,
+                           dir.key.p, dir.rec.p, n_old, del, dir.off.p, e.inc_ev.p, e.off_next.p,
+                           e.key_next.p, e.rec_next.p);
+    if (m)
+        hipLaunchKernelGGL(append_new_entries_kernel, dim3(grid_for(m)), dim3(kB), 0, s, bkeys,
+                           brec, m, bstart, dir.off.p, v_old, e.inc_ev.p, e.off_next.p,
+                           e.key_next.p, e.rec_next.p);
+    check_hip(hipGetLastError(), "append index launch");
+    dir.key.swap(e.key_next);
+    dir.rec.swap(e.rec_next);
+    dir.off.swap(e.off_next);
+    dir.key.n = n;
+    dir.rec.n = n;
+    dir.off.n = vc;
+    finish_direction(e, dir, n, vc, host_scratch);
+}
+
+// The rest of a direction's index from its sorted entries (dir.key, dir.rec)
+// and CSR offsets (dir.off): edge ids, node-timestamp groups, per-node group
+// counts, walk headers and bucket tables.
+void finish_direction(Engine& e, DirIndex& dir, size_t n, size_t vc, int64_t* host_scratch) {
+    hipStream_t s = e.stream;
+    dir.idx.resize(n);
     e.v32a.ensure(n);  // the entries' timestamp ranks
     hipLaunchKernelGGL(node_group_flags_kernel, dim3(grid_for(n)), dim3(kB), 0, s, dir.key.p,
                        dir.rec.p, e.erank.p, n, e.flags.p, dir.idx.p, e.v32a.p);
@@ -911,29 +1163,18 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
     }
 }
 
-void Engine::build_accepted(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_ts,
-                            const float* d_feat, size_t n, size_t dim, int64_t tmin,
-                            int64_t tmax) {
+// Steps 2-4 of an ingest, general case: one stable LSD radix sort of
+// (ts - tmin, position) over the old store followed by the batch -- identical
+// to the reference's "sort the batch, stable-merge it after the old store"
+// (temporal_graph.cu:67-134) because the old store is already sorted and
+// precedes the batch -- then the window eviction as an upper_bound on the
+// sorted keys (temporal_graph.cu:136-156) and the gather of the kept suffix.
+// tmin / tmax span the store and the batch.
+void Engine::sort_store(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_ts,
+                        const float* d_feat, size_t n, int64_t tmin, int64_t tmax) {
     hipStream_t s = stream;
     int64_t* hs = reinterpret_cast<int64_t*>(host_scalars);
     const size_t e_old = E, etot = E + n;
-    const int64_t batch_tmax = tmax;
-    if (E == 0) feat_dim = dim;
-
-    // the batch's endpoints, for ..._for_last_batch: copied on the side
-    // stream beside the build; the build's end waits for them
-    last_src.resize(n);
-    last_dst.resize(n);
-    check_hip(hipMemcpyAsync(last_src.p, d_src, n * 4, hipMemcpyDeviceToDevice, side), "last src");
-    check_hip(hipMemcpyAsync(last_dst.p, d_dst, n * 4, hipMemcpyDeviceToDevice, side), "last dst");
-    check_hip(hipEventRecord(side_done, side), "event");
-    last_n = n;
-    if (e_old) {
-        tmin = std::min(tmin, store_tmin);
-        tmax = std::max(tmax, store_tmax);
-    }
-    latest_ts = std::max(latest_ts, batch_tmax);
-
     // ---- 2. stable radix sort by (ts, position); 32-bit keys when the key
     // range fits (4-byte key traffic per pass instead of 8).  Without edge
     // features the sort's values are the packed endpoints themselves, so the
@@ -1043,6 +1284,169 @@ void Engine::build_accepted(const int32_t* d_src, const int32_t* d_dst, const in
     ts.swap(ts2);
     E = kept;
     check_hip(hipGetLastError(), "gather launch");
+
+}
+
+// Steps 2-4 of an ingest whose batch timestamps are all >= the store's last
+// (btmin >= store_tmax): in the stable (ts, position) order the batch then
+// follows the store's edges, ties included (old before new), so the new
+// store is the old store's kept suffix followed by the batch sorted alone --
+// no pass over the old store but one copy.  The eviction cut can fall in the
+// old store or, when it empties it, in the batch.
+void Engine::append_store(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_ts,
+                          const float* d_feat, size_t n, int64_t btmin, int64_t btmax) {
+    hipStream_t s = stream;
+    int64_t* hs = reinterpret_cast<int64_t*>(host_scalars);
+    const size_t e_old = E;
+    const int bits = bit_length_u64(static_cast<uint64_t>(btmax) - static_cast<uint64_t>(btmin));
+    const bool keys32 = bits <= 32;
+    const bool carry_ends = feat_dim == 0;
+    k64a.ensure(n);
+    k64b.ensure(n);
+    ends64.ensure(n);
+    if (carry_ends) ends64b.ensure(n);
+    v32a.ensure(n);
+    v32b.ensure(n);
+    hist.ensure(radix_hist_elems(n));
+    uint32_t* k32s[2] = {reinterpret_cast<uint32_t*>(k64a.p), reinterpret_cast<uint32_t*>(k64b.p)};
+    uint32_t* pos0 = carry_ends ? nullptr : v32a.p;
+    int which;
+    if (keys32) {
+        hipLaunchKernelGGL((make_ts_keys_kernel<uint32_t>), dim3(grid_for(n)), dim3(kB), 0, s,
+                           ts.p, src.p, dst.p, size_t{0}, d_ts, d_src, d_dst, n, btmin, k32s[0],
+                           pos0, ends64.p);
+        which = carry_ends
+                    ? radix_sort_u32_v64(k32s[0], ends64.p, k32s[1], ends64b.p, n, 0, bits, hist.p, s)
+                    : radix_sort_u32(k32s[0], v32a.p, k32s[1], v32b.p, n, 0, bits, hist.p, s);
+    } else {
+        hipLaunchKernelGGL((make_ts_keys_kernel<uint64_t>), dim3(grid_for(n)), dim3(kB), 0, s,
+                           ts.p, src.p, dst.p, size_t{0}, d_ts, d_src, d_dst, n, btmin, k64a.p,
+                           pos0, ends64.p);
+        which = carry_ends
+                    ? radix_sort_u64_v64(k64a.p, ends64.p, k64b.p, ends64b.p, n, 0, bits, hist.p, s)
+                    : radix_sort_u64(k64a.p, v32a.p, k64b.p, v32b.p, n, 0, bits, hist.p, s);
+    }
+    const uint32_t* perm = which ? v32b.p : v32a.p;
+    const uint64_t* sorted_ends = which ? ends64b.p : ends64.p;
+    const uint32_t* sk32 = k32s[which];
+    const uint64_t* sk64 = which ? k64b.p : k64a.p;
+
+    // eviction: drop ts <= latest - capacity, from the store first
+    size_t del_old = 0, del_new = 0;
+    const int64_t cutoff = latest_ts - cfg.max_time_capacity;
+    if (cfg.max_time_capacity > 0 && cutoff >= store_tmin) {
+        if (keys32)
+            hipLaunchKernelGGL((append_evict_kernel<uint32_t>), dim3(1), dim3(1), 0, s, ts.p,
+                               e_old, sk32, n, btmin, cutoff, 1, red64.p);
+        else
+            hipLaunchKernelGGL((append_evict_kernel<uint64_t>), dim3(1), dim3(1), 0, s, ts.p,
+                               e_old, sk64, n, btmin, cutoff, 1, red64.p);
+        check_hip(hipMemcpyAsync(hs, red64.p, 32, hipMemcpyDeviceToHost, s), "read evict");
+        sync();
+        del_old = static_cast<size_t>(hs[0]);
+        del_new = static_cast<size_t>(hs[1]);
+        store_tmin = hs[2];
+        store_tmax = hs[3];
+    } else {
+        store_tmax = btmax;  // store_tmin stays
+    }
+    const size_t kept_old = e_old - del_old, kept_new = n - del_new, kept = kept_old + kept_new;
+    append_del = del_old;
+    append_kept_old = kept_old;
+    append_kept_new = kept_new;
+
+    src2.resize(kept);
+    dst2.resize(kept);
+    ts2.resize(kept);
+    if (kept_old) {
+        check_hip(hipMemcpyAsync(src2.p, src.p + del_old, kept_old * 4, hipMemcpyDeviceToDevice, s),
+                  "store copy");
+        check_hip(hipMemcpyAsync(dst2.p, dst.p + del_old, kept_old * 4, hipMemcpyDeviceToDevice, s),
+                  "store copy");
+        check_hip(hipMemcpyAsync(ts2.p, ts.p + del_old, kept_old * 8, hipMemcpyDeviceToDevice, s),
+                  "store copy");
+    }
+    if (kept_new && carry_ends) {
+        if (keys32)
+            hipLaunchKernelGGL((store_from_sorted_kernel<uint32_t>), dim3(grid_for(kept_new)),
+                               dim3(kB), 0, s, sk32, sorted_ends, del_new, kept_new, btmin,
+                               src2.p + kept_old, dst2.p + kept_old, ts2.p + kept_old);
+        else
+            hipLaunchKernelGGL((store_from_sorted_kernel<uint64_t>), dim3(grid_for(kept_new)),
+                               dim3(kB), 0, s, sk64, sorted_ends, del_new, kept_new, btmin,
+                               src2.p + kept_old, dst2.p + kept_old, ts2.p + kept_old);
+    } else if (kept_new) {
+        if (keys32)
+            hipLaunchKernelGGL((gather_store_kernel<uint32_t>), dim3(grid_for(kept_new)), dim3(kB),
+                               0, s, sk32, perm, ends64.p, del_new, kept_new, btmin,
+                               src2.p + kept_old, dst2.p + kept_old, ts2.p + kept_old);
+        else
+            hipLaunchKernelGGL((gather_store_kernel<uint64_t>), dim3(grid_for(kept_new)), dim3(kB),
+                               0, s, sk64, perm, ends64.p, del_new, kept_new, btmin,
+                               src2.p + kept_old, dst2.p + kept_old, ts2.p + kept_old);
+    }
+    if (feat_dim > 0) {
+        feat2.resize(kept * feat_dim);
+        if (kept_old)
+            check_hip(hipMemcpyAsync(feat2.p, feat.p + del_old * feat_dim,
+                                     kept_old * feat_dim * sizeof(float), hipMemcpyDeviceToDevice,
+                                     s),
+                      "feature copy");
+        float* fdst = feat2.p + kept_old * feat_dim;
+        const uint32_t V = static_cast<uint32_t>(feat_dim / 4);
+        if (kept_new && feat_dim % 4 == 0 && V <= 256 && aligned16(d_feat) && aligned16(fdst)) {
+            const uint32_t R = 256 / V;
+            const size_t blocks = std::min<size_t>((kept_new + R - 1) / R, 65536);
+            hipLaunchKernelGGL(gather_feat_vec_kernel, dim3(blocks ? blocks : 1), dim3(V * R), 0, s,
+                               perm, del_new, kept_new, V, nullptr, size_t{0},
+                               reinterpret_cast<const f32x4*>(d_feat),
+                               reinterpret_cast<f32x4*>(fdst));
+        } else if (kept_new) {
+            hipLaunchKernelGGL(gather_feat_kernel, dim3(grid_capped(kept_new * feat_dim)), dim3(kB),
+                               0, s, perm, del_new, kept_new, feat_dim, nullptr, size_t{0}, d_feat,
+                               fdst);
+        }
+        feat.swap(feat2);
+    }
+    src.swap(src2);
+    dst.swap(dst2);
+    ts.swap(ts2);
+    E = kept;
+    check_hip(hipGetLastError(), "append launch");
+}
+
+void Engine::build_accepted(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_ts,
+                            const float* d_feat, size_t n, size_t dim, int64_t tmin,
+                            int64_t tmax) {
+    hipStream_t s = stream;
+    int64_t* hs = reinterpret_cast<int64_t*>(host_scalars);
+    const size_t e_old = E;
+    const int64_t batch_tmin = tmin, batch_tmax = tmax;
+    if (E == 0) feat_dim = dim;
+
+    // the batch's endpoints, for ..._for_last_batch: copied on the side
+    // stream beside the build; the build's end waits for them
+    last_src.resize(n);
+    last_dst.resize(n);
+    check_hip(hipMemcpyAsync(last_src.p, d_src, n * 4, hipMemcpyDeviceToDevice, side), "last src");
+    check_hip(hipMemcpyAsync(last_dst.p, d_dst, n * 4, hipMemcpyDeviceToDevice, side), "last dst");
+    check_hip(hipEventRecord(side_done, side), "event");
+    last_n = n;
+    if (e_old) {
+        tmin = std::min(tmin, store_tmin);
+        tmax = std::max(tmax, store_tmax);
+    }
+    latest_ts = std::max(latest_ts, batch_tmax);
+
+    // ---- 2-4. the new store: sorted stable by (ts, position), the window's
+    // old edges evicted.  A batch whose timestamps are all >= the store's
+    // (streaming) goes after the store's kept edges as it is, sorted alone;
+    // any other batch is sorted together with the store.
+    append_mode = e_old > 0 && batch_tmin >= store_tmax;
+    if (append_mode)
+        append_store(d_src, d_dst, d_ts, d_feat, n, batch_tmin, batch_tmax);
+    else
+        sort_store(d_src, d_dst, d_ts, d_feat, n, tmin, tmax);
     check_hip(hipEventRecord(ev[1], s), "event");
 
     // ---- 5. max node id, timestamp groups
@@ -1073,7 +1477,11 @@ void Engine::build_accepted(const int32_t* d_src, const int32_t* d_dst, const in
     const size_t v = static_cast<size_t>(max_node_id) + 1;  // active_node_ids size
     const size_t vc = v + 1;                                // node_index_capacity
     const int key_bits = std::max(1, bit_length_u64(static_cast<uint64_t>(max_node_id)));
-    if (cfg.is_directed) {
+    if (append_mode) {
+        append_direction(*this, out, cfg.is_directed ? 0 : 2, key_bits, vc, hs);
+        if (cfg.is_directed) append_direction(*this, in, 1, key_bits, vc, hs);
+        else in.clear();
+    } else if (cfg.is_directed) {
         build_direction(*this, out, E, key_bits, vc, 0, hs);
         build_direction(*this, in, E, key_bits, vc, 1, hs);
     } else {
@@ -1086,35 +1494,88 @@ void Engine::build_accepted(const int32_t* d_src, const int32_t* d_dst, const in
     check_hip(hipGetLastError(), "index launch");
     check_hip(hipEventRecord(ev[2], s), "event");
 
-    // ---- 7. node2vec adjacency
-    adj_ready = false;
+    // ---- 7. node2vec adjacency (edge_data.cu:298-392).  The walks' test "is
+    // a candidate adjacent to the previous node?" probes a hash set of the
+    // (owner, neighbour) pairs -- about one line -- instead of binary-searching
+    // a hub's list of millions of neighbours.  The sorted neighbour lists
+    // themselves are only read through trw_get_array, which builds them on
+    // first request after an ingest (build_adjacency_lists).
+    adj_ready = adj_lists_ready = false;
     if (cfg.enable_temporal_node2vec) {
         const int b = key_bits;
         const size_t m2 = 2 * E;
-        k64a.ensure(m2);
-        k64b.ensure(m2);
-        hipLaunchKernelGGL(adj_keys_kernel, dim3(grid_for(E)), dim3(kB), 0, s, src.p, dst.p, E, b,
-                           k64a.p);
-        const int w = radix_sort_u64(k64a.p, nullptr, k64b.p, nullptr, m2, 0, 2 * b, hist.p, s);
-        uint64_t* ak = w ? k64b.p : k64a.p;
-        adj_nbr.resize(m2);
-        hipLaunchKernelGGL(adj_finish_kernel, dim3(grid_for(m2)), dim3(kB), 0, s, ak, m2,
-                           (1ull << b) - 1, adj_nbr.p);
-        adj_off.resize(v + 1);
-        hipLaunchKernelGGL(adj_offsets_kernel, dim3(grid_for(v + 1)), dim3(kB), 0, s, ak, m2, b,
-                           v + 1, adj_off.p);
-        // the walks' membership tests (is a candidate adjacent to the previous
-        // node?) probe a hash set of the pairs instead of binary-searching a
-        // hub's list of millions of neighbours
+        // the pairs sorted with duplicates adjacent: as 32-bit keys of the
+        // active ids' ranks when two ranks fit (a streaming window of a
+        // power-law graph touches few of its ids: cfg5's 15k of 1M ids make
+        // 28-bit keys, three passes of 4-byte keys instead of four of
+        // 8-byte ones), else as 64-bit keys of the ids
+        flags.ensure(v + 1);
+        scan.ensure(v + 1);
+        scan_scratch.ensure(scan_scratch_elems(std::max(v + 1, m2 + 1)));
+        hipLaunchKernelGGL(active_u32_kernel, dim3(grid_for(v)), dim3(kB), 0, s, active.p, v,
+                           flags.p);
+        exclusive_scan_u32(flags.p, scan.p, v, scan_scratch.p, s);
+        check_hip(hipMemcpyAsync(hs, scan.p + v, 4, hipMemcpyDeviceToHost, s), "read active count");
+        sync();
+        uint32_t n_active;
+        std::memcpy(&n_active, hs, 4);
+        const int rb = std::max(1, bit_length_u64(n_active ? n_active - 1 : 0));
+        const bool ranked = 2 * rb <= 32;
+        hist.ensure(radix_hist_elems(m2));
+        const uint32_t* rkeys = nullptr;
+        const uint64_t* fkeys = nullptr;
+        if (ranked) {
+            adj_rank.resize(v + 1);
+            check_hip(hipMemcpyAsync(adj_rank.p, scan.p, (v + 1) * 4, hipMemcpyDeviceToDevice, s),
+                      "rank copy");
+            adj_ids.resize(std::max<size_t>(n_active, 1));
+            hipLaunchKernelGGL(active_ids_kernel, dim3(grid_for(v)), dim3(kB), 0, s, active.p,
+                               adj_rank.p, v, adj_ids.p);
+            k32a.ensure(m2);
+            k32b.ensure(m2);
+            if (E)
+                hipLaunchKernelGGL(adj_rank_keys_kernel, dim3(grid_for(E)), dim3(kB), 0, s, src.p,
+                                   dst.p, E, adj_rank.p, rb, k32a.p);
+            const int w = radix_sort_u32(k32a.p, nullptr, k32b.p, nullptr, m2, 0, 2 * rb, hist.p, s);
+            rkeys = w ? k32b.p : k32a.p;
+        } else {
+            k64a.ensure(m2);
+            k64b.ensure(m2);
+            if (E)
+                hipLaunchKernelGGL(adj_keys_kernel, dim3(grid_for(E)), dim3(kB), 0, s, src.p,
+                                   dst.p, E, b, k64a.p);
+            const int w = radix_sort_u64(k64a.p, nullptr, k64b.p, nullptr, m2, 0, 2 * b, hist.p, s);
+            fkeys = w ? k64b.p : k64a.p;
+        }
+        // a set at most half full of the distinct pairs
+        size_t distinct = m2;
+        if (ranked && m2) {
+            flags.ensure(m2 + 1);
+            scan.ensure(m2 + 1);
+            hipLaunchKernelGGL(distinct_flags_kernel, dim3(grid_for(m2)), dim3(kB), 0, s, rkeys, m2,
+                               flags.p);
+            exclusive_scan_u32(flags.p, scan.p, m2, scan_scratch.p, s);
+            check_hip(hipMemcpyAsync(hs, scan.p + m2, 4, hipMemcpyDeviceToHost, s), "read pairs");
+            sync();
+            uint32_t dcount;
+            std::memcpy(&dcount, hs, 4);
+            distinct = dcount;
+        }
         int lg = 10;
-        while ((size_t{1} << lg) < 2 * m2) ++lg;
+        while ((size_t{1} << lg) < 2 * distinct) ++lg;
         adj_hash.resize(size_t{1} << lg);
         check_hip(hipMemsetAsync(adj_hash.p, 0xff, (size_t{1} << lg) * sizeof(uint64_t), s),
                   "adjacency set clear");
-        hipLaunchKernelGGL(adj_hash_insert_kernel, dim3(grid_for(m2)), dim3(kB), 0, s, ak, m2,
-                           64 - lg, (uint64_t{1} << lg) - 1, adj_hash.p);
+        if (m2 && ranked)
+            hipLaunchKernelGGL(adj_hash_insert_ranked_kernel, dim3(grid_for(m2)), dim3(kB), 0, s,
+                               rkeys, m2, rb, adj_ids.p, b, 64 - lg, (uint64_t{1} << lg) - 1,
+                               adj_hash.p);
+        else if (m2)
+            hipLaunchKernelGGL(adj_hash_insert_kernel, dim3(grid_for(m2)), dim3(kB), 0, s, fkeys,
+                               m2, 64 - lg, (uint64_t{1} << lg) - 1, adj_hash.p);
         adj_hash_log = lg;
         adj_bits = b;
+        adj_nodes = v;
         check_hip(hipGetLastError(), "adjacency launch");
         adj_ready = true;
     }
@@ -1173,6 +1634,34 @@ void Engine::build_accepted(const int32_t* d_src, const int32_t* d_dst, const in
     timings.index_ms = ms;
 }
 
+void Engine::build_adjacency_lists() {
+    // edge_data.cu:298-392: every edge adds v to N(u) and u to N(v),
+    // duplicates kept, each list ascending -- one radix sort of the 2E keys
+    // owner << b | neighbour
+    if (!adj_ready || adj_lists_ready) return;
+    hipStream_t s = stream;
+    const int b = adj_bits;
+    const size_t m2 = 2 * E, v = adj_nodes;
+    k64a.ensure(m2);
+    k64b.ensure(m2);
+    hist.ensure(radix_hist_elems(m2));
+    if (E)
+        hipLaunchKernelGGL(adj_keys_kernel, dim3(grid_for(E)), dim3(kB), 0, s, src.p, dst.p, E, b,
+                           k64a.p);
+    const int w = radix_sort_u64(k64a.p, nullptr, k64b.p, nullptr, m2, 0, 2 * b, hist.p, s);
+    uint64_t* ak = w ? k64b.p : k64a.p;
+    adj_nbr.resize(m2);
+    if (m2)
+        hipLaunchKernelGGL(adj_finish_kernel, dim3(grid_for(m2)), dim3(kB), 0, s, ak, m2,
+                           (1ull << b) - 1, adj_nbr.p);
+    adj_off.resize(v + 1);
+    hipLaunchKernelGGL(adj_offsets_kernel, dim3(grid_for(v + 1)), dim3(kB), 0, s, ak, m2, b,
+                       v + 1, adj_off.p);
+    check_hip(hipGetLastError(), "adjacency lists launch");
+    sync();
+    adj_lists_ready = true;
+}
+
 void Engine::clear() {
     // core/temporal_random_walk.cu:358-373: a fresh store with the same config
     E = 0;
@@ -1183,7 +1672,8 @@ void Engine::clear() {
     store_tmin = store_tmax = 0;
     src.n = dst.n = ts.n = feat.n = tsg_off.n = uniq_ts.n = erank.n = neg1_rank.n = active.n = 0;
     fwd_cum.n = bwd_cum.n = gwx_fwd.n = gwx_bwd.n = adj_off.n = adj_nbr.n = adj_hash.n = 0;
-    weights_ready = adj_ready = false;
+    weights_ready = adj_ready = adj_lists_ready = false;
+    adj_nodes = 0;
     out.clear();
     in.clear();
     last_n = 0;

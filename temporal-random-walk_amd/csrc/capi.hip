@@ -29,6 +29,7 @@ Engine::~Engine() {
     (void)join_prefetch();  // no copy may outlive the engine
     if (stream) (void)hipStreamSynchronize(stream);
     if (side) (void)hipStreamSynchronize(side);
+    free_retired();
     for (auto& e : ev)
         if (e) (void)hipEventDestroy(e);
     if (side_done) (void)hipEventDestroy(side_done);
@@ -68,12 +69,20 @@ struct DeviceGuard {
     }
 };
 
+// Points trw::g_retired at an engine's retired-block list for one call.
+struct RetireInto {
+    trw::RetiredBlocks* prev;
+    explicit RetireInto(trw::RetiredBlocks* r) : prev(trw::g_retired) { trw::g_retired = r; }
+    ~RetireInto() { trw::g_retired = prev; }
+};
+
 template <typename F>
 trw_status guarded(void* h, F&& f) {
     try {
         if (!h) throw trw::InvalidArgument("null handle");
         Engine* e = static_cast<Engine*>(h);
         DeviceGuard g(e->device);
+        RetireInto r(&e->retired);
         f(*e);
         return TRW_OK;
     } catch (const trw::InvalidArgument& ex) {
@@ -436,6 +445,7 @@ trw_status trw_clear(void* handle) {
     return guarded(handle, [&](Engine& e) {
         e.sync();
         e.clear();
+        e.free_retired();
     });
 }
 
@@ -470,8 +480,18 @@ trw_status trw_get_array(void* handle, int32_t id, void* dst, uint64_t cap, uint
             case TRW_ARR_OUTBOUND_FORWARD_CUMULATIVE_WEIGHTS: p = e.out.w_fwd.p; n = w ? e.out.n_groups : 0; kind = 3; break;
             case TRW_ARR_OUTBOUND_BACKWARD_CUMULATIVE_WEIGHTS: p = e.out.w_bwd.p; n = w ? e.out.n_groups : 0; kind = 3; break;
             case TRW_ARR_INBOUND_BACKWARD_CUMULATIVE_WEIGHTS: p = e.in.w_bwd.p; n = (w && dir) ? e.in.n_groups : 0; kind = 3; break;
-            case TRW_ARR_NODE_ADJ_OFFSETS: p = e.adj_off.p; n = e.adj_ready ? e.adj_off.n : 0; break;
-            case TRW_ARR_NODE_ADJ_NEIGHBORS: p = e.adj_nbr.p; n = e.adj_ready ? e.adj_nbr.n : 0; kind = 1; es = 4; break;
+            case TRW_ARR_NODE_ADJ_OFFSETS:
+                e.build_adjacency_lists();
+                p = e.adj_off.p;
+                n = e.adj_lists_ready ? e.adj_off.n : 0;
+                break;
+            case TRW_ARR_NODE_ADJ_NEIGHBORS:
+                e.build_adjacency_lists();
+                p = e.adj_nbr.p;
+                n = e.adj_lists_ready ? e.adj_nbr.n : 0;
+                kind = 1;
+                es = 4;
+                break;
             case TRW_ARR_EDGE_FEATURES: p = e.feat.p; n = e.E * e.feat_dim; kind = 4; es = 4; break;
             default: throw trw::InvalidArgument("unknown array id");
         }

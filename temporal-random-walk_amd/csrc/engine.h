@@ -43,8 +43,9 @@
 //                                  blocks; top level first
 //   global weights  fwd_cum, bwd_cum fp64[T] (+ gwx_fwd, gwx_bwd: their
 //                   search index, one segment of T)
-//   node2vec        adj_off uint32[max_id+2], adj_nbr int32[2E],
-//                   adj_hash uint64[2^k >= 4E] (pair membership set)
+//   node2vec        adj_hash uint64[2^k >= 4E] (pair membership set, built
+//                   with the index); adj_off uint32[max_id+2], adj_nbr
+//                   int32[2E] (sorted lists, built when first requested)
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -74,7 +75,24 @@ struct InvalidArgument : std::invalid_argument {
 // allocations that still succeed before one fails as out of memory.
 inline std::atomic<long long> g_alloc_fail_after{-1};
 
-// Grow-only device buffer; growth discards the contents.
+// Device blocks whose buffers grew during an engine call (set by the C ABI's
+// call guard to the engine's list): they are freed at the engine's next
+// clear() or destruction instead of at once.  hipFree synchronises the device
+// and unmaps (about 0.3-0.5 ms per block of 100 MB or more), and an ingest
+// whose store grows regrows some 40 buffers: freeing them inside the call
+// made the ingests where a streaming window fills up 2-3x slower.  nullptr
+// (outside engine calls): blocks are freed at once.
+struct RetiredBlocks {
+    std::vector<void*> blocks;
+    size_t bytes = 0;
+};
+inline thread_local RetiredBlocks* g_retired = nullptr;
+// Past this many retired bytes a growing buffer frees its old block at once.
+constexpr size_t kMaxRetiredBytes = size_t{32} << 30;
+
+// Grow-only device buffer; growth discards the contents.  A buffer that grows
+// again takes twice its capacity, so a store filling a streaming window
+// regrows its buffers once or twice rather than at every batch.
 template <typename T>
 struct DBuf {
     T* p = nullptr;
@@ -93,8 +111,16 @@ struct DBuf {
     }
     void ensure(size_t k) {
         if (k > cap) {
-            release();
-            const size_t c = k + k / 4 + 64;
+            const size_t old_cap = cap;
+            if (p && g_retired && g_retired->bytes + cap * sizeof(T) <= kMaxRetiredBytes) {
+                g_retired->blocks.push_back(p);
+                g_retired->bytes += cap * sizeof(T);
+                p = nullptr;
+                n = cap = 0;
+            } else {
+                release();
+            }
+            const size_t c = std::max(k + k / 4, 2 * old_cap) + 64;
             if (g_alloc_fail_after.load(std::memory_order_relaxed) >= 0 &&
                 g_alloc_fail_after.fetch_sub(1, std::memory_order_relaxed) == 0)
                 throw std::bad_alloc();
@@ -334,9 +360,23 @@ struct Engine {
     DBuf<uint64_t> adj_hash;
     int adj_hash_log = 0;
     int adj_bits = 0;
-    bool adj_ready = false;
+    size_t adj_nodes = 0;  // node ids the adjacency covers (max_node_id + 1)
+    DBuf<uint32_t> adj_rank, adj_ids;  // active ids' ranks and the ids by rank
+    bool adj_ready = false;        // the pair set describes the store
+    bool adj_lists_ready = false;  // adj_off / adj_nbr do too (built on request)
 
     DirIndex out, in;
+
+    // the last ingest appended its batch after the store (append_store): the
+    // store edges it evicted and the old and batch edges it kept, which the
+    // node index update takes its entries from
+    bool append_mode = false;
+    size_t append_del = 0, append_kept_old = 0, append_kept_new = 0;
+    // node index update of an append: evicted prefix and batch offsets per
+    // node, entry counts, and the next index arrays (swapped in)
+    DBuf<uint32_t> inc_ev, inc_bstart, inc_cnt;
+    DBuf<uint32_t> key_next, off_next;
+    DBuf<EdgeRec> rec_next;
 
     // last ingested batch (for ..._for_last_batch)
     DBuf<int32_t> last_src, last_dst;
@@ -404,6 +444,14 @@ struct Engine {
     size_t pf_n = 0, pf_dim = 0;
     bool pf_has_feat = false;
 
+    // device blocks retired by buffer growth, freed at clear() / destruction
+    RetiredBlocks retired;
+    void free_retired() {
+        for (void* q : retired.blocks) (void)hipFree(q);
+        retired.blocks.clear();
+        retired.bytes = 0;
+    }
+
     // timings
     hipEvent_t ev[8] = {};
     trw_timings timings{};
@@ -419,9 +467,18 @@ struct Engine {
     void build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_ts,
                const float* d_feat, size_t n, size_t dim);
     void clear();
+    // the sorted adjacency lists adj_off / adj_nbr of the store (for
+    // trw_get_array; the walks use the pair set)
+    void build_adjacency_lists();
     // the pipeline of build() after the batch's checks
     void build_accepted(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_ts,
                         const float* d_feat, size_t n, size_t dim, int64_t tmin, int64_t tmax);
+    // its store update: the general sort of store + batch, or the append of a
+    // batch at or after the store's last timestamp (sets append_*)
+    void sort_store(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_ts,
+                    const float* d_feat, size_t n, int64_t tmin, int64_t tmax);
+    void append_store(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_ts,
+                      const float* d_feat, size_t n, int64_t btmin, int64_t btmax);
 
     // sampling into w_* buffers
     // sampling: into the engine's w_* buffers, or -- with `into` -- into

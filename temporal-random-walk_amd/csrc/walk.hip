@@ -83,9 +83,9 @@ struct WalkGraph {
     const uint8_t* active;
     int32_t active_size;
     DirView d;
-    const uint32_t* adj_off;
+    const uint32_t* adj_off;   // sorted lists (nullptr: not built)
     const int32_t* adj_nbr;
-    uint32_t adj_off_size;
+    uint32_t adj_nodes;        // node ids the adjacency covers (0: none)
     const uint64_t* adj_hash;  // pair set (nullptr: search the lists)
     uint64_t adj_mask;
     int adj_shift, adj_bits;
@@ -360,8 +360,8 @@ __device__ Sel start_edge(const WalkGraph& g, int picker, double rg, double re) 
 }
 
 __device__ __forceinline__ bool adjacent(const WalkGraph& g, int prev, int cand) {
-    if (!g.tn2v || g.adj_off == nullptr) return false;
-    if (prev < 0 || static_cast<uint32_t>(prev) + 1 >= g.adj_off_size) return false;
+    if (!g.tn2v || g.adj_nodes == 0) return false;
+    if (prev < 0 || static_cast<uint32_t>(prev) >= g.adj_nodes) return false;
     if (g.adj_hash) {
         // cand is a stored node id (a record's neighbour), below 2^adj_bits
         if (cand < 0) return false;
@@ -372,6 +372,7 @@ __device__ __forceinline__ bool adjacent(const WalkGraph& g, int prev, int cand)
             if (v == kAdjEmpty) return false;
         }
     }
+    if (g.adj_off == nullptr) return false;
     uint32_t lo = g.adj_off[prev];
     const uint32_t end = g.adj_off[prev + 1];
     uint32_t hi = end;
@@ -1225,61 +1226,58 @@ inline unsigned grid_capped(uint64_t n) {
 
 // Walk statistics and demand bytes of the walk path (trw_get_walk_stats):
 // acc[3] with this engine's 4-byte positions and ranks, acc[4] with the
-// reference's element types.  One wave per walk row (grid-stride over
-// walks): the wave reads the row's nodes together, 256 B per access, and
-// each lane adds the hops of the slots it holds.
+// reference's element types.  Workgroup b covers the walks [b * wpb,
+// (b + 1) * wpb) and its threads take their slots in row order (coalesced
+// node loads, independent from one slot to the next); the workgroup's sums
+// meet in LDS and leave with one atomic per counter (one per wave contended
+// for the same five addresses across all waves and ran the kernel slower than
+// the walks themselves).
 __global__ __launch_bounds__(kB) void walk_stats_kernel(const int32_t* __restrict__ nodes,
                                                         const uint64_t* __restrict__ lens,
-                                                        uint64_t n, int L,
+                                                        uint64_t n, int L, uint64_t wpb,
                                                         const uint32_t* __restrict__ cnt,
                                                         int32_t active_size, int constrained,
                                                         unsigned long long* acc) {
-    const int lane = threadIdx.x & 63;
-    const uint64_t waves = static_cast<uint64_t>(gridDim.x) * (kB / 64);
-    unsigned long long bytes = 0, ref = 0, trans = 0, total = 0, nonempty = 0;
-    for (uint64_t w = blockIdx.x * static_cast<uint64_t>(kB / 64) + threadIdx.x / 64; w < n;
-         w += waves) {
-        const int len = static_cast<int>(lens[w]);
-        if (lane == 0) {
-            bytes += 24;
-            ref += 8 + (constrained ? 52 : 32);
-            if (len >= 1) {
-                bytes += 8;
-                ref += 12;
+    __shared__ unsigned long long red[5][kB / 64];
+    unsigned long long v[5] = {0, 0, 0, 0, 0};  // total, trans, nonempty, bytes, ref
+    const uint64_t w0 = blockIdx.x * wpb;
+    const uint64_t w1 = w0 + wpb < n ? w0 + wpb : n;
+    if (w0 < w1) {
+        const uint32_t Lu = static_cast<uint32_t>(L);
+        const uint32_t slots = static_cast<uint32_t>(w1 - w0) * Lu;  // < 2^32 (host)
+        for (uint32_t off = threadIdx.x; off < slots; off += kB) {
+            const uint32_t dw = off / Lu, k = off - dw * Lu;
+            const uint64_t w = w0 + dw;
+            const int len = static_cast<int>(lens[w]);
+            if (k == 0) {
+                v[0] += len;
+                v[1] += len > 0 ? len - 1 : 0;
+                v[2] += len > 0;
+                v[3] += 24 + (len >= 1 ? 8 : 0) + (len >= 2 ? 12 : 0);
+                v[4] += 8 + (constrained ? 52 : 32) + (len >= 1 ? 12 : 0) + (len >= 2 ? 20 : 0);
             }
-            if (len >= 2) {
-                bytes += 12;
-                ref += 20;
+            // hops are selected at slots 1 .. len - 2
+            if (k >= 1 && static_cast<int>(k) + 1 < len) {
+                const int u = nodes[w * L + k];
+                uint32_t G = 0;
+                if (u >= 0 && u < active_size) G = cnt[u + 1] - cnt[u];
+                const int probes = G ? 32 - __clz(G) : 0;  // ceil(log2(G + 1))
+                v[3] += 36 + 4 * probes;
+                v[4] += 72 + 8 * probes;
             }
-            trans += len > 0 ? len - 1 : 0;
-            total += len;
-            nonempty += len > 0;
-        }
-        // hops are selected at slots 1 .. len - 2
-        const int32_t* row = nodes + w * static_cast<uint64_t>(L);
-        for (int k = 1 + lane; k + 1 < len; k += 64) {
-            const int u = row[k];
-            uint32_t G = 0;
-            if (u >= 0 && u < active_size) G = cnt[u + 1] - cnt[u];
-            const int probes = G ? 32 - __clz(G) : 0;  // ceil(log2(G + 1))
-            bytes += 36 + 4 * probes;
-            ref += 72 + 8 * probes;
         }
     }
-    // wave reduction then one atomic per wave
-    for (int off = 32; off > 0; off >>= 1) {
-        bytes += __shfl_down(bytes, off, 64);
-        ref += __shfl_down(ref, off, 64);
-        trans += __shfl_down(trans, off, 64);
-        total += __shfl_down(total, off, 64);
-        nonempty += __shfl_down(nonempty, off, 64);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int c = 0; c < 5; ++c) {
+        for (int o = 32; o > 0; o >>= 1) v[c] += __shfl_down(v[c], o, 64);
+        if (lane == 0) red[c][wave] = v[c];
     }
-    if (lane == 0) {
-        atomicAdd(acc + 0, total);
-        atomicAdd(acc + 1, trans);
-        atomicAdd(acc + 2, nonempty);
-        atomicAdd(acc + 3, bytes);
-        atomicAdd(acc + 4, ref);
+    __syncthreads();
+    if (threadIdx.x < 5) {
+        unsigned long long t = 0;
+        for (int q = 0; q < kB / 64; ++q) t += red[threadIdx.x][q];
+        atomicAdd(acc + threadIdx.x, t);
     }
 }
 
@@ -1622,9 +1620,9 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
         g.d.wx_off = wd.wx_off.p;
         g.d.wx = weights_ready && wx.n ? wx.p : nullptr;
     }
-    g.adj_off = adj_ready ? adj_off.p : nullptr;
+    g.adj_off = adj_lists_ready ? adj_off.p : nullptr;
     g.adj_nbr = adj_nbr.p;
-    g.adj_off_size = adj_ready ? static_cast<uint32_t>(adj_off.n) : 0;
+    g.adj_nodes = adj_ready ? static_cast<uint32_t>(adj_nodes) : 0;
     g.adj_hash = adj_ready && adj_hash.n ? adj_hash.p : nullptr;
     g.adj_mask = adj_hash.n ? adj_hash.n - 1 : 0;
     g.adj_shift = 64 - adj_hash_log;
@@ -1801,9 +1799,13 @@ void walk_stats(Engine& e, trw_walk_stats* out) {
     const bool use_in = !e.w_dir_forward && e.cfg.is_directed;
     const DirIndex& d = use_in ? e.in : e.out;
     if (e.w_num && e.w_len > 0) {
-        const uint64_t blocks = std::min<uint64_t>((e.w_num + 3) / 4, 1u << 16);
+        // about 4096 workgroups, each over a run of walks whose slots number
+        // below 2^32
+        uint64_t wpb = (e.w_num + 4095) / 4096;
+        wpb = std::min<uint64_t>(wpb, 0xffffffffull / static_cast<uint64_t>(e.w_len));
+        const uint64_t blocks = (e.w_num + wpb - 1) / wpb;
         hipLaunchKernelGGL(walk_stats_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kB), 0, s,
-                           e.w_nodes.p, e.w_lens.p, e.w_num, e.w_len, d.cnt.p,
+                           e.w_nodes.p, e.w_lens.p, e.w_num, e.w_len, wpb, d.cnt.p,
                            static_cast<int32_t>(e.active.n), e.w_constrained,
                            reinterpret_cast<unsigned long long*>(e.acc64.p));
         check_hip(hipGetLastError(), "walk stats launch");

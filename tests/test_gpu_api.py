@@ -420,15 +420,18 @@ def test_node_features_grow_and_keep_old_rows():
         tw2.set_node_features(np.array([0, 1], np.int32), np.array([[1.0, 2.0, 3.0]], np.float32))
 
 
-def test_failed_ingest_leaves_an_empty_usable_engine():
+@pytest.mark.parametrize("shift", [0, 2_000_000])
+def test_failed_ingest_leaves_an_empty_usable_engine(shift):
     """A device allocation failing at any point of an ingest (forced by the
     test hook) raises MemoryError and leaves the engine empty, as after
     clear(); the engine then samples (no walks start) and a new ingest gives
-    the oracle's index and replay walks."""
+    the oracle's index and replay walks.  shift puts the second batch after
+    the first in time (the append path) or among it (the general sort)."""
     from oracle import pyoracle as po
     from temporal_random_walk import capi
     s1, d1, t1 = graphs.cfg1(n_nodes=300, n_edges=2_000, seed=3)
     s2, d2, t2 = graphs.cfg1(n_nodes=3_000, n_edges=40_000, seed=4)
+    t2 = t2 + shift
     og1 = po.OracleGraph(True, enable_weight_computation=True, enable_temporal_node2vec=True)
     og1.add_edges(s1, d1, t1)
     og = po.OracleGraph(True, enable_weight_computation=True, enable_temporal_node2vec=True)

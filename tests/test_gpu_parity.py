@@ -107,6 +107,91 @@ def test_index_streaming_window_eviction():
     assert eng.latest_timestamp() == og.latest_timestamp
 
 
+def _append_batches(seed, n_batches, n, span, overlap=0, n_ids=5_000, dims=0):
+    """Batches whose timestamps start where the previous batch's end (ties at
+    the boundary: a batch's first timestamp equals the previous one's last),
+    each shifted back by `overlap` to make batches that interleave with the
+    store instead."""
+    rng = np.random.default_rng(seed)
+    out, feats = [], []
+    t0 = 0
+    for k in range(n_batches):
+        s = graphs.zipf_ids(rng, n, n_ids, 1.6)
+        d = graphs.zipf_ids(rng, n, n_ids, 1.6)
+        t = rng.integers(t0, t0 + span, n).astype(np.int64)
+        t[rng.integers(0, n)] = t0  # the boundary tie
+        t0 = int(t.max()) - overlap
+        out.append((s, d, t))
+        feats.append(rng.standard_normal((n, dims)).astype(np.float32) if dims else None)
+    return out, (feats if dims else None)
+
+
+@pytest.mark.parametrize("directed", [True, False])
+@pytest.mark.parametrize("cap", [-1, 2_500, 700, 150])
+def test_index_append_batches(directed, cap):
+    """Streaming batches whose timestamps start at the store's last one take
+    the append path (the batch sorted alone, old entries moved by a scatter);
+    the window cuts inside the store (2500), empties it and cuts into the
+    batch (700, 150: narrower than a batch), or not at all.  Every index array
+    equals the oracle's after every batch; weights, the adjacency and replay
+    walks after the last."""
+    batches, _ = _append_batches(21, 6, 20_000, 1_000)
+    og = po.OracleGraph(directed, cap, True, True, 30.0, 0.5, 2.0)
+    eng = _engine(is_directed=directed, max_time_capacity=cap, enable_weight_computation=True,
+                  enable_temporal_node2vec=True, timescale_bound=30.0, node2vec_p=0.5,
+                  node2vec_q=2.0, shuffle_walk_order=False, global_seed=77)
+    for b in batches:
+        og.add_edges(*b)
+        eng.add_edges(*b)
+        _assert_index_equal(og, eng)
+    _assert_index_equal(og, eng, weights=True, tn2v=True)
+    assert eng.edge_count() == len(og.array("timestamps"))
+    for forward in (True, False):
+        _walk_case(og, eng, "Linear", "Uniform", forward, "total", 16, 3_000, seed=31)
+
+
+def test_index_cfg5_shaped_stream():
+    """configs[4]'s stream at a tenth of its batch size: the same 1M-id
+    Zipf(1.8) graph, 10 batches of 300k edges in consecutive time ranges,
+    window 3e6, node2vec p=0.5 q=2.  Every batch takes the append path; after
+    each one every index array equals the oracle's, after the last also the
+    weights and the adjacency, and node2vec replay walks (on the engine's
+    weights) are bit-exact."""
+    from tests import configs
+    cap = 3_000_000
+    og = po.OracleGraph(True, cap, False, True, -1.0, 0.5, 2.0)
+    eng = _engine(is_directed=True, max_time_capacity=cap, enable_temporal_node2vec=True,
+                  node2vec_p=0.5, node2vec_q=2.0, shuffle_walk_order=False, global_seed=3)
+    for b in configs.cfg5_batches(batch=300_000):
+        og.add_edges(*b, num_threads=8)
+        eng.add_edges(*b)
+        _assert_index_equal(og, eng)
+    assert eng.edge_count() == 900_000
+    _assert_index_equal(og, eng, weights=True, tn2v=True)
+    for name in WEIGHT_ARRAYS:
+        w = eng.array(name)
+        if w.size:
+            og.set_weights(name, w)
+    _walk_case(og, eng, "TemporalNode2Vec", "Uniform", True, "total", 20, 20_000, seed=6)
+
+
+def test_index_append_then_interleaved_batches():
+    """Append batches, then batches reaching back before the store's last
+    timestamp (the general sort of store and batch), then append again, with
+    edge features carried along: identical to the oracle throughout."""
+    a, fa = _append_batches(22, 3, 15_000, 1_000, dims=4)
+    b, fb = _append_batches(23, 2, 15_000, 1_000, overlap=600, dims=4)
+    b = [(s, d, t + int(a[-1][2].max()) - 300) for s, d, t in b]  # reach into the store
+    c, fc = _append_batches(24, 2, 15_000, 1_000, dims=4)
+    c = [(s, d, t + int(b[-1][2].max())) for s, d, t in c]
+    og, eng = _pair(True, [], max_time_capacity=2_000)
+    for (s, d, t), f in zip(a + b + c, fa + fb + fc):
+        og.add_edges(s, d, t, f)
+        eng.add_edges(s, d, t, f)
+        _assert_index_equal(og, eng)
+        assert np.array_equal(og.array("edge_features"), eng.array("edge_features"))
+
+
 def test_index_weights_and_adjacency():
     s, d, t = graphs.powerlaw(5_000, 60_000, s=1.6, seed=5, ts_hi=10_000_000)
     for directed in (True, False):
