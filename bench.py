@@ -55,6 +55,11 @@ KERNEL_SOURCES = {
 }
 
 
+# kernels of the walk path; every other kernel belongs to the index build
+WALK_PATH_KERNELS = ("walk_kernel", "walk_start_kernel", "layout_", "walk_stats",
+                     "node_group_init", "node_group_segment", "gather_walk_features")
+
+
 def sources_sha256(family):
     h = hashlib.sha256()
     for name in KERNEL_SOURCES[family]:
@@ -177,29 +182,44 @@ def summarize_pmc(args):
     MiB that the run made first (the largest __amd_rocclr_copyBuffer
     dispatch), so bytes = KiB * (copy bytes / copy KiB).  The profile is
     stamped with the sha256 of the kernel family's sources."""
-    per = {}  # counter -> list of per-dispatch values of the kernel
+    import csv
+
+    def selected(kname):
+        if args.kernel == "@build":  # every kernel of the index build
+            return not any(k in kname for k in WALK_PATH_KERNELS)
+        return any(k in kname for k in args.kernel.split("|"))
+
+    per = {}  # counter -> list of per-dispatch values of the selected kernels
     copy = {}
     for d in args.pmc_dir:
         files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
         if not files:
             raise SystemExit(f"no counter_collection.csv under {d}")
-        import csv
         rows = {}
         for fn in files:
             with open(fn) as f:
                 for r in csv.DictReader(f):
                     key = (fn, r["Dispatch_Id"], r["Kernel_Name"], r["Counter_Name"])
                     rows[key] = rows.get(key, 0.0) + float(r["Counter_Value"])
+        # the calibration copy: the largest copyBuffer dispatch of the run
+        cal = {}
         for (fn, disp, kname, cname), v in rows.items():
-            if args.kernel in kname:
+            if "copyBuffer" in kname and v > cal.get(cname, (None, -1.0))[1]:
+                cal[cname] = (disp, v)
+        for cname, (disp, v) in cal.items():
+            copy[cname] = max(copy.get(cname, 0.0), v)
+        for (fn, disp, kname, cname), v in rows.items():
+            if cname in cal and cal[cname][0] == disp and "copyBuffer" in kname:
+                continue  # not part of the measured work
+            if selected(kname):
                 per.setdefault(cname, []).append(v)
-            elif "copyBuffer" in kname:
-                copy[cname] = max(copy.get(cname, 0.0), v)
     if not per:
         raise SystemExit(f"no dispatch of a kernel named like {args.kernel!r}")
-    avg = {c: sum(v) / len(v) for c, v in per.items()}
+    # per launch: the mean over the selected dispatches, or their sum over
+    # --per launches (a kernel set: one ingest is many dispatches)
+    avg = {c: (sum(v) / args.per if args.per else sum(v) / len(v)) for c, v in per.items()}
     out = {"kernel": args.kernel, "workload": args.workload, "command": args.command,
-           "dispatches": max(len(v) for v in per.values()),
+           "dispatches": max(len(v) for v in per.values()), "per": args.per or None,
            "sources_sha256": sources_sha256(args.family), "source_family": args.family,
            "counters": avg}
     cal = args.copy_calibration_mib * (1 << 20)
@@ -233,6 +253,21 @@ def summarize_pmc(args):
     print(json.dumps(out, indent=1))
 
 
+def copy_calibration(dev, mib):
+    """One plain device copy of `mib` MiB (torch copy_, dispatched as
+    __amd_rocclr_copyBuffer): the reference that scales the HBM byte counters
+    of a --pmc profile (--summarize-pmc)."""
+    import torch
+    n = mib * (1 << 20) // 4
+    a = torch.ones(n, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    b.copy_(a)
+    torch.cuda.synchronize()
+    log(f"copy calibration: {mib} MiB read + written")
+    del a, b
+
+
 def run_other_config(k, args):
     """One of BASELINE.json's other workloads (configs[k-1]), timed on the
     device (HIP events of the engine): index build and sampling.  These are
@@ -249,6 +284,8 @@ def run_other_config(k, args):
         return out
 
     res = {"config": f"cfg{k}", "unit": "walk steps/s"}
+    if args.copy_calibration_mib > 0:
+        copy_calibration(dev, args.copy_calibration_mib)
     log(f"generating cfg{k} inputs")
     if k in (1, 3, 4):
         if k == 1:
@@ -369,7 +406,8 @@ def main():
     ap.add_argument("--timestamps", type=int, default=100_000)
     ap.add_argument("--walks", type=int, default=10_000_000)
     ap.add_argument("--walk-len", type=int, default=80)
-    ap.add_argument("--walk-order", default="auto", choices=["auto", "walk_id", "start_time"],
+    ap.add_argument("--walk-order", default="auto",
+                    choices=["auto", "walk_id", "start_time", "node_grouped"],
                     help="order the walks run in on the device (the output is the same)")
     ap.add_argument("--config", type=int, default=2,
                     help="2 (default): the cfg2 bench line; 1, 3, 4 or 5: time that BASELINE "
@@ -390,7 +428,12 @@ def main():
                     help="summarise rocprofv3 counter runs (--pmc-dir) of one kernel "
                          "(--kernel) into OUT_JSON, then exit; touches no GPU")
     ap.add_argument("--pmc-dir", action="append", default=[])
-    ap.add_argument("--kernel", default="walk_kernel<")
+    ap.add_argument("--kernel", default="walk_kernel<",
+                    help="kernel name substrings joined by |, or @build for every kernel "
+                         "of the index build")
+    ap.add_argument("--per", type=int, default=0,
+                    help="sum the selected dispatches over this many launches (0: mean "
+                         "per dispatch)")
     ap.add_argument("--family", default="walk", choices=sorted(KERNEL_SOURCES))
     ap.add_argument("--workload", default="")
     ap.add_argument("--command", default="")
@@ -433,14 +476,7 @@ def main():
 
     dev = torch.device("cuda:0")
     if args.copy_calibration_mib > 0:
-        n = args.copy_calibration_mib * (1 << 20) // 4
-        a = torch.ones(n, dtype=torch.float32, device=dev)
-        b = torch.empty_like(a)
-        torch.cuda.synchronize()
-        b.copy_(a)
-        torch.cuda.synchronize()
-        log(f"copy calibration: {args.copy_calibration_mib} MiB read + written")
-        del a, b
+        copy_calibration(dev, args.copy_calibration_mib)
     d_src = torch.from_numpy(src).to(dev)
     d_dst = torch.from_numpy(dst).to(dev)
     d_ts = torch.from_numpy(ts).to(dev)

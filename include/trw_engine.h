@@ -102,14 +102,17 @@ typedef struct trw_sample_params {
      * order (each walk depends only on the graph and its own draws).
      * 0 = automatic (TRW_ORDER_START_TIME from 2^16 walks on), 1 = walk id
      * order, 2 = sorted by the time of the start edge, so that walks running
-     * side by side read the same parts of the index. */
+     * side by side read the same parts of the index, 3 = node-grouped: every
+     * 8 hops the live walks are regrouped by their current node on the device
+     * (measured slower than 2; kept for comparison). */
     int32_t walk_order;
 } trw_sample_params;
 
 typedef enum trw_walk_order {
     TRW_ORDER_AUTO = 0,
     TRW_ORDER_WALK_ID = 1,
-    TRW_ORDER_START_TIME = 2
+    TRW_ORDER_START_TIME = 2,
+    TRW_ORDER_NODE_GROUPED = 3
 } trw_walk_order;
 
 /* Walk output.  nodes/timestamps: [num_walks, max_walk_len]; edge_ids:

@@ -205,25 +205,40 @@ __device__ __forceinline__ uint64_t pack_rec(int32_t nbr, uint32_t eid) {
 }
 
 // The edges are src/dst[0, e); their edge ids (store positions) start at id0.
+// With erank given, a value packs the neighbour, the edge id and the edge's
+// timestamp rank into one word (nbr | eid << nb | rank << (nb + eb); the caller
+// checks that they fit), so that the entries leave the node sort with their
+// ranks and the group flags need no gather of erank in node order.
 __global__ void node_entries_kernel(const int32_t* __restrict__ src,
                                     const int32_t* __restrict__ dst, size_t e, int mode,
-                                    uint32_t id0, uint32_t* __restrict__ keys,
+                                    uint32_t id0, const uint32_t* __restrict__ erank, int nb,
+                                    int eb, uint32_t* __restrict__ keys,
                                     uint64_t* __restrict__ vals) {
     const size_t i = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
     if (i >= e) return;
     const int32_t a = src[i], b = dst[i];
     const uint32_t id = id0 + static_cast<uint32_t>(i);
+    uint64_t va, vb;
+    if (erank) {
+        const uint64_t hi = (static_cast<uint64_t>(id) << nb) |
+                            (static_cast<uint64_t>(erank[id]) << (nb + eb));
+        va = hi | static_cast<uint32_t>(b);  // entry of a (out / first), neighbour b
+        vb = hi | static_cast<uint32_t>(a);
+    } else {
+        va = pack_rec(b, id);
+        vb = pack_rec(a, id);
+    }
     if (mode == 0) {
         keys[i] = static_cast<uint32_t>(a);
-        vals[i] = pack_rec(b, id);
+        vals[i] = va;
     } else if (mode == 1) {
         keys[i] = static_cast<uint32_t>(b);
-        vals[i] = pack_rec(a, id);
+        vals[i] = vb;
     } else {
         keys[2 * i] = static_cast<uint32_t>(a);
-        vals[2 * i] = pack_rec(b, id);
+        vals[2 * i] = va;
         keys[2 * i + 1] = static_cast<uint32_t>(b);
-        vals[2 * i + 1] = pack_rec(a, id);
+        vals[2 * i + 1] = vb;
     }
 }
 
@@ -375,6 +390,29 @@ __global__ __launch_bounds__(kB) void node_group_flags_kernel(const uint32_t* __
     if ((threadIdx.x & 63) == 0 && k > 0) {
         kp = keys[k - 1];
         rp = erank[rec[k - 1].eid];
+    }
+    flags[k] = (k == 0 || key != kp || r != rp) ? 1u : 0u;
+}
+
+// node_group_flags_kernel for entries whose sorted values carry their ranks
+// (node_entries_kernel with erank): also unpacks the walk records.
+__global__ __launch_bounds__(kB) void node_group_flags_packed_kernel(
+    const uint32_t* __restrict__ keys, const uint64_t* __restrict__ packed, size_t n, int nb,
+    int eb, uint32_t* __restrict__ flags, uint32_t* __restrict__ idx,
+    uint32_t* __restrict__ rank, EdgeRec* __restrict__ rec) {
+    const size_t k = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (k >= n) return;  // the active lanes of a wave are a prefix
+    const uint32_t key = keys[k];
+    const uint64_t v = packed[k];
+    const uint32_t e = static_cast<uint32_t>((v >> nb) & ((1ull << eb) - 1ull));
+    const uint32_t r = static_cast<uint32_t>(v >> (nb + eb));
+    rec[k] = EdgeRec{static_cast<int32_t>(static_cast<uint32_t>(v & ((1ull << nb) - 1ull))), e};
+    idx[k] = e;
+    rank[k] = r;
+    uint32_t kp = __shfl_up(key, 1, 64), rp = __shfl_up(r, 1, 64);
+    if ((threadIdx.x & 63) == 0 && k > 0) {
+        kp = keys[k - 1];
+        rp = static_cast<uint32_t>(packed[k - 1] >> (nb + eb));
     }
     flags[k] = (k == 0 || key != kp || r != rp) ? 1u : 0u;
 }
@@ -903,7 +941,16 @@ void validate_batch(const Engine& e, const void* feat, size_t n, size_t dim) {
 
 namespace {
 
-void finish_direction(Engine& e, DirIndex& dir, size_t n, size_t vc, int64_t* host_scratch);
+// Sorted node-index entries whose values carry their timestamp ranks
+// (node_entries_kernel with erank), or none (vals == nullptr: dir.rec holds
+// the records and the ranks are gathered from erank).
+struct PackedEntries {
+    const uint64_t* vals;
+    int nb, eb;
+};
+
+void finish_direction(Engine& e, DirIndex& dir, size_t n, size_t vc, int64_t* host_scratch,
+                      const PackedEntries& pe);
 
 // Stable per-direction node index of the store's n entries (mode: see
 // node_entries_kernel).
@@ -912,20 +959,28 @@ void build_direction(Engine& e, DirIndex& dir, size_t n, int key_bits, size_t vc
     hipStream_t s = e.stream;
     dir.present = true;
     dir.n_entries = n;
-    // the sorted records land in dir.rec: start in the buffer set the last
-    // digit pass does not write into
+    // values carry the timestamp rank when neighbour, edge id and rank fit
+    // in 64 bits (cfg2: 20 + 25 + 17)
+    const int nb = key_bits;
+    const int eb = std::max(1, bit_length_u64(e.E ? e.E - 1 : 0));
+    const int rb = std::max(1, bit_length_u64(e.T ? e.T - 1 : 0));
+    const bool packed = nb + eb + rb <= 64;
     dir.rec.resize(n);
     e.k32a.ensure(n);
     e.k32b.ensure(n);
     e.k64a.ensure(n);
+    if (packed) e.k64b.ensure(n);
     const int passes = n > 1 ? radix_passes(0, key_bits) : 0;
+    // unpacked, the sorted records land in dir.rec: start in the buffer set
+    // the last digit pass does not write into
     uint64_t* recs = reinterpret_cast<uint64_t*>(dir.rec.p);
-    uint64_t* v0 = passes % 2 == 0 ? recs : e.k64a.p;
-    uint64_t* v1 = passes % 2 == 0 ? e.k64a.p : recs;
+    uint64_t* v0 = packed ? e.k64a.p : (passes % 2 == 0 ? recs : e.k64a.p);
+    uint64_t* v1 = packed ? e.k64b.p : (passes % 2 == 0 ? e.k64a.p : recs);
     const size_t edges = mode == 2 ? n / 2 : n;
     if (edges)
         hipLaunchKernelGGL(node_entries_kernel, dim3(grid_for(edges)), dim3(kB), 0, s, e.src.p,
-                           e.dst.p, edges, mode, 0u, e.k32a.p, v0);
+                           e.dst.p, edges, mode, 0u, packed ? e.erank.p : nullptr, nb, eb,
+                           e.k32a.p, v0);
     const int which = radix_sort_u32_v64(e.k32a.p, v0, e.k32b.p, v1, n, 0, key_bits, e.hist.p, s);
     // the sorted keys become the direction's (the scratch takes the old
     // buffer, which every user sizes again before writing)
@@ -934,7 +989,8 @@ void build_direction(Engine& e, DirIndex& dir, size_t n, int key_bits, size_t vc
     dir.off.resize(vc);
     hipLaunchKernelGGL(lower_bound_offsets_kernel, dim3(grid_for(vc)), dim3(kB), 0, s, dir.key.p,
                        n, vc, dir.off.p);
-    finish_direction(e, dir, n, vc, host_scratch);
+    PackedEntries pe{packed ? (which ? v1 : v0) : nullptr, nb, eb};
+    finish_direction(e, dir, n, vc, host_scratch, pe);
 }
 
 // The node index of one direction after an append (Engine::append_store):
@@ -964,8 +1020,8 @@ void append_direction(Engine& e, DirIndex& dir, int mode, int key_bits, size_t v
     const uint32_t id0 = static_cast<uint32_t>(e.append_kept_old);
     if (e.append_kept_new)
         hipLaunchKernelGGL(node_entries_kernel, dim3(grid_for(e.append_kept_new)), dim3(kB), 0, s,
-                           e.src.p + id0, e.dst.p + id0, e.append_kept_new, mode, id0, e.k32a.p,
-                           e.k64a.p);
+                           e.src.p + id0, e.dst.p + id0, e.append_kept_new, mode, id0, nullptr, 0,
+                           0, e.k32a.p, e.k64a.p);
     const int w = radix_sort_u32_v64(e.k32a.p, e.k64a.p, e.k32b.p, e.k64b.p, m, 0, key_bits,
                                      e.hist.p, s);
     const uint32_t* bkeys = w ? e.k32b.p : e.k32a.p;
@@ -1004,18 +1060,25 @@ void append_direction(Engine& e, DirIndex& dir, int mode, int key_bits, size_t v
     dir.key.n = n;
     dir.rec.n = n;
     dir.off.n = vc;
-    finish_direction(e, dir, n, vc, host_scratch);
+    // the old entries' ranks changed with the eviction: gathered from erank
+    finish_direction(e, dir, n, vc, host_scratch, PackedEntries{nullptr, 0, 0});
 }
 
 // The rest of a direction's index from its sorted entries (dir.key, dir.rec)
 // and CSR offsets (dir.off): edge ids, node-timestamp groups, per-node group
 // counts, walk headers and bucket tables.
-void finish_direction(Engine& e, DirIndex& dir, size_t n, size_t vc, int64_t* host_scratch) {
+void finish_direction(Engine& e, DirIndex& dir, size_t n, size_t vc, int64_t* host_scratch,
+                      const PackedEntries& pe) {
     hipStream_t s = e.stream;
     dir.idx.resize(n);
     e.v32a.ensure(n);  // the entries' timestamp ranks
-    hipLaunchKernelGGL(node_group_flags_kernel, dim3(grid_for(n)), dim3(kB), 0, s, dir.key.p,
-                       dir.rec.p, e.erank.p, n, e.flags.p, dir.idx.p, e.v32a.p);
+    if (pe.vals)
+        hipLaunchKernelGGL(node_group_flags_packed_kernel, dim3(grid_for(n)), dim3(kB), 0, s,
+                           dir.key.p, pe.vals, n, pe.nb, pe.eb, e.flags.p, dir.idx.p, e.v32a.p,
+                           dir.rec.p);
+    else
+        hipLaunchKernelGGL(node_group_flags_kernel, dim3(grid_for(n)), dim3(kB), 0, s, dir.key.p,
+                           dir.rec.p, e.erank.p, n, e.flags.p, dir.idx.p, e.v32a.p);
     exclusive_scan_u32(e.flags.p, e.scan.p, n, e.scan_scratch.p, s);
     uint32_t g = 0;
     check_hip(hipMemcpyAsync(host_scratch, e.scan.p + n, 4, hipMemcpyDeviceToHost, s), "read g");

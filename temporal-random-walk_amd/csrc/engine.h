@@ -402,6 +402,9 @@ struct Engine {
     // allocation once they are large enough)
     DBuf<int32_t> s_ids, s_seeds, s_tmp32;
     DBuf<int64_t> s_cuts, s_tmp64;
+    // node-grouped processing: walk states between segments, the (node, walk)
+    // lists and the live count
+    DBuf<uint32_t> ng_carry, ng_keys0, ng_keys1, ng_vals0, ng_vals1, ng_count;
     DBuf<uint64_t> acc64;
 
     // walks (device): slot-major scratch written by the walk kernel (node,

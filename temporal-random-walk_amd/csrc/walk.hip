@@ -865,6 +865,147 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
     a.lens[w] = static_cast<uint64_t>(len);
 }
 
+// ---- node-grouped processing (TRW_ORDER_NODE_GROUPED) ----------------------
+// The north star's cooperative alternative to start-time order: every
+// kNodeGroupHops hops the live walks are regrouped by their current node (a
+// device radix sort of (node, walk)), so the lanes of a wave -- and the
+// waves of an XCD -- select their next hops at the same nodes and share the
+// header, bucket-table and panel lines.  A walk's state lives in HBM between
+// segments; its scratch column is its walk id (its place changes from one
+// segment to the next).  Each walk runs exactly the hops of walk_kernel's
+// loop with the same draws, so the walks are the same.
+constexpr int kNodeGroupHops = 8;
+
+// A walk between segments: at the top of walk_kernel's loop with c slots
+// written (c == the loop's walk_len == len).
+struct WalkCarry {
+    int32_t cur, r, e, prev;
+    int32_t c, cut, pad0, pad1;
+};
+static_assert(sizeof(WalkCarry) == 32, "WalkCarry must be 32 bytes");
+
+// Appends the workgroup's live walks (keep) as (current node, walk) to the
+// next segment's list: one atomic per workgroup.  (Keys of node and time rank,
+// so that the walks at one node also ran in time order, cut the L1 -> L2
+// reads per step from 2.07 to 1.58 but took the walk phase from 44 to 48 ms
+// at cfg2: four sort passes per segment instead of two.)
+__device__ __forceinline__ void emit_live(bool keep, uint32_t node, uint32_t w,
+                                          uint32_t* __restrict__ keys,
+                                          uint32_t* __restrict__ vals,
+                                          uint32_t* __restrict__ count) {
+    __shared__ uint32_t s_wave[kB / 64];
+    __shared__ uint32_t s_base;
+    const uint64_t m = __ballot(keep);
+    const int lane = __lane_id(), wave = threadIdx.x >> 6;
+    const uint32_t below = static_cast<uint32_t>(__popcll(m & ((1ull << lane) - 1ull)));
+    if (lane == 0) s_wave[wave] = static_cast<uint32_t>(__popcll(m));
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t t = 0;
+        for (int q = 0; q < kB / 64; ++q) {
+            const uint32_t c = s_wave[q];
+            s_wave[q] = t;
+            t += c;
+        }
+        s_base = t ? atomicAdd(count, t) : 0u;
+    }
+    __syncthreads();
+    if (keep) {
+        const uint32_t pos = s_base + s_wave[wave] + below;
+        keys[pos] = node;
+        vals[pos] = w;
+    }
+}
+
+// Segment 0: every walk's first slot from its start state; the walks that go
+// on enter the first list.
+template <bool Fwd, bool Dir, int Fam>
+__global__ __launch_bounds__(kB) void node_group_init_kernel(WalkGraph g, WalkArgs a,
+                                                             WalkCarry* __restrict__ carry,
+                                                             uint32_t* __restrict__ keys,
+                                                             uint32_t* __restrict__ vals,
+                                                             uint32_t* __restrict__ count) {
+    const uint64_t w = blockIdx.x * static_cast<uint64_t>(kB) + threadIdx.x;
+    bool keep = false;
+    int32_t cur = 0;
+    if (w < a.n) {
+        const StartState s0 = a.st[w];
+        if (s0.e == -1) {
+            a.lens[w] = 0;
+        } else {
+            SlotWriter out(a, w);
+            out.first(s0.first);
+            keep = 1 < a.L && s0.cur != a.pad;
+            if (keep) {
+                cur = s0.cur;
+                carry[w] = WalkCarry{s0.cur, s0.r, s0.e, -1, 1, cutoff_rank(g, a, w), 0, 0};
+            } else {
+                a.lens[w] = 1;
+            }
+        }
+    }
+    emit_live(keep, static_cast<uint32_t>(cur), static_cast<uint32_t>(w), keys, vals, count);
+}
+
+// One segment: the walks of the list (sorted by current node), up to
+// kNodeGroupHops iterations of walk_kernel's loop each; the walks that go on
+// enter the next list.  n: the list's length.
+template <bool Fwd, bool Dir, int Fam>
+__global__ __launch_bounds__(kB) void node_group_segment_kernel(
+    WalkGraph g, WalkArgs a, const uint32_t* __restrict__ list, uint32_t n,
+    WalkCarry* __restrict__ carry, uint32_t* __restrict__ keys, uint32_t* __restrict__ vals,
+    uint32_t* __restrict__ count) {
+    __shared__ double s_xt[kExpTables];
+    const bool use_xt = a.walk_bias == kExponentialIndex;
+    if (use_xt) {
+        fill_exp_tables(s_xt, threadIdx.x, kB);
+        __syncthreads();
+    }
+    const double* em1 = use_xt ? s_xt : nullptr;
+    const uint32_t i = blockIdx.x * kB + threadIdx.x;
+    bool keep = false;
+    uint32_t w = 0;
+    WalkCarry s{};
+    if (i < n) {
+        w = list[i];
+        s = carry[w];
+        const int L = a.L;
+        const int32_t neg1 = *g.neg1_rank;
+        SlotWriter out(a, w);
+        keep = true;
+        for (int it = 0; it < kNodeGroupHops; ++it) {
+            out.slot(s.c, s.cur, static_cast<uint32_t>(s.r), static_cast<uint32_t>(s.e));
+            ++s.c;
+            if (s.c == L) {  // the last slot: the reference's final selection is unused
+                keep = false;
+                break;
+            }
+            const bool ok = s.cur >= 0 && s.cur < g.active_size;
+            const uint32_t u = ok ? static_cast<uint32_t>(s.cur) : 0u;
+            const NodeHdr hd = g.d.hdr[u];
+            const DrawPair r = draw_pair(a.ds, w, static_cast<uint32_t>(s.c));
+            const Hop h = node_edge_from<Fwd, Fam>(g, a.walk_bias, u, ok, hd,
+                                                   s.r == neg1 ? -1 : s.r, s.cut, s.prev, r.a,
+                                                   r.b, em1);
+            if (h.e == -1 || h.r == neg1) {
+                keep = false;
+                break;
+            }
+            s.prev = s.cur;
+            s.cur = h.nbr;
+            s.r = h.r;
+            s.e = h.e;
+            if (s.cur == a.pad) {
+                keep = false;
+                break;
+            }
+        }
+        if (keep) carry[w] = s;
+        else a.lens[w] = static_cast<uint64_t>(s.c);
+    }
+    emit_live(keep, static_cast<uint32_t>(s.cur), w, keys, vals, count);
+}
+
 // Layout pass: slot-major scratch [K][n] -> the row-major output [n][K] the
 // reference returns, for all three walk arrays in one pass.  Values become the
 // reference's types on the way: nodes are copied, a timestamp rank becomes the
@@ -1689,8 +1830,10 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
     const int order_mode = p.walk_order == TRW_ORDER_AUTO
                                ? (nw >= kTimeOrderMinWalks ? TRW_ORDER_START_TIME : TRW_ORDER_WALK_ID)
                                : p.walk_order;
-    if (order_mode != TRW_ORDER_WALK_ID && order_mode != TRW_ORDER_START_TIME)
+    if (order_mode != TRW_ORDER_WALK_ID && order_mode != TRW_ORDER_START_TIME &&
+        order_mode != TRW_ORDER_NODE_GROUPED)
         throw InvalidArgument("Invalid walk order");
+    const bool node_grouped = order_mode == TRW_ORDER_NODE_GROUPED && nw > 1 && L > 1;
     if (nw && L > 0) {
         StartState* st = reinterpret_cast<StartState*>(sp.take(walk_st, 4 * nw));
         uint32_t* ka = sp.take(k32a, nw);
@@ -1698,7 +1841,7 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
         const uint32_t none = g.T;  // past every rank: walks without a start run last
         TRW_LAUNCH(walk_start_kernel, dim3(grid_for(nw)), g, a, st, ka, va, none);
         a.st = st;
-        if (order_mode == TRW_ORDER_START_TIME && nw > 1 && L > 1) {
+        if (order_mode == TRW_ORDER_START_TIME && nw > 1 && L > 1 && !node_grouped) {
             uint32_t* kb = sp.take(k32b, nw);
             uint32_t* vb = sp.take(v32b, nw);
             uint32_t* hi = sp.take(hist, radix_hist_elems(nw));
@@ -1717,7 +1860,41 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
     // slower: the layout's streaming traffic evicts the hub lines the walks
     // hit in L2.)
     check_hip(hipEventRecord(ev[5], s), "event");
-    if (nw) {
+    uint64_t launches = nw ? 1 : 0;
+    if (node_grouped) {
+        // segments of kNodeGroupHops hops, the live walks regrouped by their
+        // current node in between (the count of live walks is read back to
+        // size the next sort and launch)
+        if (nw > 0xffffffffull) throw InvalidArgument("node-grouped order supports < 2^32 walks");
+        WalkCarry* carry = reinterpret_cast<WalkCarry*>(sp.take(ng_carry, 8 * nw));
+        uint32_t* kb[2] = {sp.take(ng_keys0, nw), sp.take(ng_keys1, nw)};
+        uint32_t* vb[2] = {sp.take(ng_vals0, nw), sp.take(ng_vals1, nw)};
+        uint32_t* hi = sp.take(hist, radix_hist_elems(nw));
+        uint32_t* cnt = sp.take(ng_count, 1);
+        const int nbits = std::max(1, bit_length(static_cast<uint64_t>(std::max(max_node_id, 0))));
+        check_hip(hipMemsetAsync(cnt, 0, 4, s), "live count clear");
+        int in = 0;  // the pair the next list is emitted into
+        TRW_LAUNCH(node_group_init_kernel, dim3(grid_for(nw)), g, a, carry, kb[in], vb[in], cnt);
+        check_hip(hipGetLastError(), "node-grouped init launch");
+        launches = 1;
+        for (;;) {
+            check_hip(hipMemcpyAsync(hs, cnt, 4, hipMemcpyDeviceToHost, s), "live count");
+            sync();
+            uint32_t live;
+            std::memcpy(&live, hs, 4);
+            if (live == 0) break;
+            const int w = radix_sort_u32(kb[in], vb[in], kb[in ^ 1], vb[in ^ 1], live, 0, nbits,
+                                         hi, s);
+            const int sorted = w ? in ^ 1 : in;  // the pair holding the sorted list
+            const uint32_t* list = vb[sorted];
+            in = sorted ^ 1;
+            check_hip(hipMemsetAsync(cnt, 0, 4, s), "live count clear");
+            TRW_LAUNCH(node_group_segment_kernel, dim3(grid_for(live)), g, a, list, live, carry,
+                       kb[in], vb[in], cnt);
+            check_hip(hipGetLastError(), "node-grouped segment launch");
+            ++launches;
+        }
+    } else if (nw) {
         a.q0 = 0;
         a.q_end = nw;
         TRW_LAUNCH(walk_kernel, dim3(grid_for(nw)), g, a);
@@ -1789,7 +1966,7 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
     timings.sample_ms = ms;
     check_hip(hipEventElapsedTime(&ms, ev[5], ev[6]), "elapsed");
     timings.walk_kernel_ms = ms;
-    timings.walk_kernel_launches = nw ? 1 : 0;
+    timings.walk_kernel_launches = launches;
 }
 
 void walk_stats(Engine& e, trw_walk_stats* out) {

@@ -29,7 +29,7 @@ PICKERS = {
 }
 DIRECTIONS = {"Forward_In_Time": 0, "Backward_In_Time": 1}
 # trw_walk_order: the order walks run in on the device (the output is the same)
-WALK_ORDERS = {"auto": 0, "walk_id": 1, "start_time": 2}
+WALK_ORDERS = {"auto": 0, "walk_id": 1, "start_time": 2, "node_grouped": 3}
 MODES = {"total": 0, "all_nodes": 1, "last_batch": 2, "nodes": 3}
 
 # (id, numpy dtype) in the order of trw_array_id

@@ -199,7 +199,13 @@ def test_cfg2_full_parity():
     by_time = _device_arrays(w, L)
     for name, x, y in zip(("nodes", "timestamps", "lens", "edge_ids"), by_id, by_time):
         assert torch.equal(x, y), name
-    del by_id, by_time
+    del by_time
+    w = eng.sample_device("total", L, "ExponentialIndex", 10_000_000,
+                          initial_edge_bias="Uniform", walk_order="node_grouped")
+    by_node = _device_arrays(w, L)
+    for name, x, y in zip(("nodes", "timestamps", "lens", "edge_ids"), by_id, by_node):
+        assert torch.equal(x, y), name
+    del by_id, by_node
     st = eng.walk_stats()
     assert st["total_len"] > 70 * 10_000_000  # mean walk length ~76
     s, d, t = eng.array("sources"), eng.array("targets"), eng.array("timestamps")
