@@ -184,9 +184,9 @@ def summarize_pmc(args):
     stamped with the sha256 of the kernel family's sources."""
     import csv
 
-    def selected(kname):
-        if args.kernel == "@build":  # every kernel of the index build
-            return not any(k in kname for k in WALK_PATH_KERNELS)
+    def selected(kname, in_build):
+        if args.kernel == "@build":  # every dispatch of an ingest
+            return in_build
         return any(k in kname for k in args.kernel.split("|"))
 
     per = {}  # counter -> list of per-dispatch values of the selected kernels
@@ -208,10 +208,20 @@ def summarize_pmc(args):
                 cal[cname] = (disp, v)
         for cname, (disp, v) in cal.items():
             copy[cname] = max(copy.get(cname, 0.0), v)
+        # the dispatches of an ingest: from its first kernel (the batch's
+        # min/max reduction) to the first kernel of the next sample
+        in_build, build_of = False, {}
+        for fn, disp, kname in sorted({(k[0], k[1], k[2]) for k in rows},
+                                      key=lambda x: (x[0], int(x[1]))):
+            if "minmax_partial_kernel" in kname:
+                in_build = True
+            elif any(k in kname for k in WALK_PATH_KERNELS):
+                in_build = False
+            build_of[(fn, disp)] = in_build
         for (fn, disp, kname, cname), v in rows.items():
             if cname in cal and cal[cname][0] == disp and "copyBuffer" in kname:
                 continue  # not part of the measured work
-            if selected(kname):
+            if selected(kname, build_of[(fn, disp)]):
                 per.setdefault(cname, []).append(v)
     if not per:
         raise SystemExit(f"no dispatch of a kernel named like {args.kernel!r}")
@@ -429,8 +439,8 @@ def main():
                          "(--kernel) into OUT_JSON, then exit; touches no GPU")
     ap.add_argument("--pmc-dir", action="append", default=[])
     ap.add_argument("--kernel", default="walk_kernel<",
-                    help="kernel name substrings joined by |, or @build for every kernel "
-                         "of the index build")
+                    help="kernel name substrings joined by |, or @build for every "
+                         "dispatch of an ingest (from its first kernel to the next sample's)")
     ap.add_argument("--per", type=int, default=0,
                     help="sum the selected dispatches over this many launches (0: mean "
                          "per dispatch)")
