@@ -50,8 +50,8 @@ CSRC = os.path.join(PKG, "csrc")
 # the sources each profiled kernel family is compiled from: a counter profile
 # describes the code only while these hash to what it measured
 KERNEL_SOURCES = {
-    "walk": ["walk.hip", "trw_device.h", "engine.h"],
-    "build": ["build.hip", "primitives.hip", "primitives.h", "engine.h"],
+    "walk": ["walk.hip", "trw_device.h", "index_layout.h"],
+    "build": ["build.hip", "primitives.hip", "primitives.h", "index_layout.h"],
 }
 
 

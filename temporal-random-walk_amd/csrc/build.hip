@@ -1212,10 +1212,11 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
     // is rejected here, before the store changes
     red64.ensure(minmax_scratch_elems());
     minmax_ts_min_id(d_ts, d_src, d_dst, n, red64.p, s);
-    check_hip(hipMemcpyAsync(hs, red64.p, 24, hipMemcpyDeviceToHost, s), "read minmax");
+    check_hip(hipMemcpyAsync(hs, red64.p, 32, hipMemcpyDeviceToHost, s), "read minmax");
     sync();
     if (hs[2] < 0) throw InvalidArgument("node ids must be non-negative");
     try {
+        batch_max_id = static_cast<int32_t>(hs[3]);
         build_accepted(d_src, d_dst, d_ts, d_feat, n, dim, hs[0], hs[1]);
     } catch (...) {
         // the store, its index and the last batch may disagree: start empty
@@ -1512,20 +1513,25 @@ void Engine::build_accepted(const int32_t* d_src, const int32_t* d_dst, const in
         sort_store(d_src, d_dst, d_ts, d_feat, n, tmin, tmax);
     check_hip(hipEventRecord(ev[1], s), "event");
 
-    // ---- 5. max node id, timestamp groups
-    red32.ensure(4);
-    max_i32_pair(src.p, dst.p, E, red32.p, s);
+    // ---- 5. max node id, timestamp groups.  Without an eviction the store
+    // is the old store plus the batch, whose largest id the batch's reduction
+    // found; an eviction can remove the largest id, so the store is reduced
+    const bool evicted = E != e_old + n;
+    if (evicted) {
+        red32.ensure(4);
+        max_i32_pair(src.p, dst.p, E, red32.p, s);
+    }
     flags.ensure(2 * E + 1);
     scan.ensure(2 * E + 1);
     scan_scratch.ensure(scan_scratch_elems(2 * E + 1));
     hipLaunchKernelGGL(ts_group_flags_kernel, dim3(grid_for(E)), dim3(kB), 0, s, ts.p, E, flags.p);
     exclusive_scan_u32(flags.p, scan.p, E, scan_scratch.p, s);
-    check_hip(hipMemcpyAsync(hs, red32.p, 4, hipMemcpyDeviceToHost, s), "read max id");
+    if (evicted) check_hip(hipMemcpyAsync(hs, red32.p, 4, hipMemcpyDeviceToHost, s), "read max id");
     check_hip(hipMemcpyAsync(hs + 1, scan.p + E, 4, hipMemcpyDeviceToHost, s), "read T");
     sync();
-    int32_t mx;
+    int32_t mx = std::max(max_node_id, batch_max_id);
     uint32_t tg;
-    std::memcpy(&mx, hs, 4);
+    if (evicted) std::memcpy(&mx, hs, 4);
     std::memcpy(&tg, hs + 1, 4);
     max_node_id = mx;
     T = tg;

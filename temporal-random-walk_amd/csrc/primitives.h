@@ -60,11 +60,12 @@ int radix_sort_u32_v64(uint32_t* keys0, uint64_t* vals0, uint32_t* keys1, uint64
 int radix_passes(int begin_bit, int end_bit);
 
 // ---- reductions ---------------------------------------------------------------
-// out[0], out[1] = min and max of v[0..n); out[2] = the smallest of a[i], b[i]
-// (INT64_MAX when n == 0); out must hold minmax_scratch_elems() values
+// out[0], out[1] = min and max of v[0..n); out[2], out[3] = the smallest and
+// the largest of a[i], b[i] (INT64_MAX / INT64_MIN when n == 0); out must hold
+// minmax_scratch_elems() values
 void minmax_ts_min_id(const int64_t* v, const int32_t* a, const int32_t* b, size_t n, int64_t* out,
                       hipStream_t s);
-inline size_t minmax_scratch_elems() { return 4 + 3 * 1024; }
+inline size_t minmax_scratch_elems() { return 4 + 4 * 1024; }
 // max of two int32 arrays -> *out (device memory); -1 when n == 0.
 void max_i32_pair(const int32_t* a, const int32_t* b, size_t n, int32_t* out, hipStream_t s);
 // sum of doubles -> *out (device memory).

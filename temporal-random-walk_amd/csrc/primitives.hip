@@ -532,63 +532,71 @@ constexpr int kReduceBlocks = 1024;
 // min and max of v, and the smallest of the ids a[i], b[i] (INT64_MAX for
 // n == 0): one pass over a batch's timestamps and endpoints
 struct MinMaxId {
-    int64_t mn, mx, id;
+    int64_t mn, mx, id, idmax;
 };
 
 __device__ __forceinline__ MinMaxId minmax_id_join(MinMaxId x, MinMaxId y) {
-    return {y.mn < x.mn ? y.mn : x.mn, y.mx > x.mx ? y.mx : x.mx, y.id < x.id ? y.id : x.id};
+    return {y.mn < x.mn ? y.mn : x.mn, y.mx > x.mx ? y.mx : x.mx, y.id < x.id ? y.id : x.id,
+            y.idmax > x.idmax ? y.idmax : x.idmax};
 }
 
 __device__ __forceinline__ MinMaxId block_minmax_id(MinMaxId v, int64_t* sm) {
-    sm[3 * threadIdx.x] = v.mn;
-    sm[3 * threadIdx.x + 1] = v.mx;
-    sm[3 * threadIdx.x + 2] = v.id;
+    int64_t* m = sm + 4 * threadIdx.x;
+    m[0] = v.mn;
+    m[1] = v.mx;
+    m[2] = v.id;
+    m[3] = v.idmax;
     __syncthreads();
     for (int st = kBlock / 2; st > 0; st >>= 1) {
         if (static_cast<int>(threadIdx.x) < st) {
-            const int o = 3 * (threadIdx.x + st);
-            const MinMaxId r = minmax_id_join({sm[3 * threadIdx.x], sm[3 * threadIdx.x + 1], sm[3 * threadIdx.x + 2]},
-                                              {sm[o], sm[o + 1], sm[o + 2]});
-            sm[3 * threadIdx.x] = r.mn;
-            sm[3 * threadIdx.x + 1] = r.mx;
-            sm[3 * threadIdx.x + 2] = r.id;
+            const int64_t* o = sm + 4 * (threadIdx.x + st);
+            const MinMaxId r = minmax_id_join({m[0], m[1], m[2], m[3]}, {o[0], o[1], o[2], o[3]});
+            m[0] = r.mn;
+            m[1] = r.mx;
+            m[2] = r.id;
+            m[3] = r.idmax;
         }
         __syncthreads();
     }
-    return {sm[0], sm[1], sm[2]};
+    return {sm[0], sm[1], sm[2], sm[3]};
 }
 
 __global__ __launch_bounds__(kBlock) void minmax_partial_kernel(const int64_t* __restrict__ v,
                                                                 const int32_t* __restrict__ a,
                                                                 const int32_t* __restrict__ b,
                                                                 size_t n, int64_t* part) {
-    __shared__ int64_t sm[3 * kBlock];
-    MinMaxId acc{INT64_MAX, INT64_MIN, INT64_MAX};
+    __shared__ int64_t sm[4 * kBlock];
+    MinMaxId acc{INT64_MAX, INT64_MIN, INT64_MAX, INT64_MIN};
     for (size_t i = blockIdx.x * static_cast<size_t>(kBlock) + threadIdx.x; i < n;
          i += static_cast<size_t>(gridDim.x) * kBlock) {
         const int64_t x = v[i];
-        const int64_t id = min(a[i], b[i]);
-        acc = minmax_id_join(acc, {x, x, id});
+        const int32_t p = a[i], q = b[i];
+        acc = minmax_id_join(acc, {x, x, min(p, q), max(p, q)});
     }
     const MinMaxId r = block_minmax_id(acc, sm);
     if (threadIdx.x == 0) {
-        part[3 * blockIdx.x] = r.mn;
-        part[3 * blockIdx.x + 1] = r.mx;
-        part[3 * blockIdx.x + 2] = r.id;
+        int64_t* o = part + 4 * blockIdx.x;
+        o[0] = r.mn;
+        o[1] = r.mx;
+        o[2] = r.id;
+        o[3] = r.idmax;
     }
 }
 
 __global__ __launch_bounds__(kBlock) void minmax_final_kernel(const int64_t* part, int np,
                                                               int64_t* out) {
-    __shared__ int64_t sm[3 * kBlock];
-    MinMaxId acc{INT64_MAX, INT64_MIN, INT64_MAX};
-    for (int i = threadIdx.x; i < np; i += kBlock)
-        acc = minmax_id_join(acc, {part[3 * i], part[3 * i + 1], part[3 * i + 2]});
+    __shared__ int64_t sm[4 * kBlock];
+    MinMaxId acc{INT64_MAX, INT64_MIN, INT64_MAX, INT64_MIN};
+    for (int i = threadIdx.x; i < np; i += kBlock) {
+        const int64_t* p = part + 4 * i;
+        acc = minmax_id_join(acc, {p[0], p[1], p[2], p[3]});
+    }
     const MinMaxId r = block_minmax_id(acc, sm);
     if (threadIdx.x == 0) {
         out[0] = r.mn;
         out[1] = r.mx;
         out[2] = r.id;
+        out[3] = r.idmax;
     }
 }
 
