@@ -321,6 +321,11 @@ __device__ __forceinline__ int pick_weights(const double* w, uint64_t wsize, uin
     const double end_sum = w[ge - 1];
     if (end_sum < start_sum) return -1;
     const double target = start_sum + r * (end_sum - start_sum);
+    // w[gs - 1] = start_sum >= target puts the lower_bound before gs (or at
+    // seg = gs with start_sum = 0), which the clamp turns into gs: no search.
+    // Forward weights saturate at their final sum over the late part of a
+    // node's span, where start_sum == end_sum makes this the common case.
+    if (target <= start_sum) return static_cast<int>(gs);
     const uint64_t x = seg + weight_lower_bound(w + seg, G, lv, target);
     return static_cast<int>(x < gs ? gs : (x > ge ? ge : x));
 }
@@ -577,33 +582,67 @@ __device__ __forceinline__ uint64_t grid_position(int remap) {
 // need not be aligned -- and a wave of such lanes touches 64 lines per
 // access.  Shared by the wave, a block costs one access: in round j the 16
 // lanes of each quarter of the wave read one entry each of the block of the
-// quarter's lane j, and one ballot counts the four blocks of the round.
+// quarter's lane j, and one ballot counts the four blocks of the round.  A
+// quarter is a DPP row, so lane j's request reaches its quarter by a row
+// broadcast (row_newbcast:j, a VALU move) rather than through the LDS.
+
+// Lane J's value in every lane of its 16-lane row.
+template <int J>
+__device__ __forceinline__ uint32_t row_bcast(uint32_t v) {
+    return static_cast<uint32_t>(
+        __builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x150 + J, 0xf, 0xf, false));
+}
+
+// Round J of wave_count_below16: the quarters count the blocks of their lanes
+// J, and lane J of each quarter keeps its count in mine.
+template <int J>
+__device__ __forceinline__ void count_round16(uint32_t& mine, int sub, int qbase, uint32_t p_lo,
+                                              uint32_t p_hi, uint32_t t_lo, uint32_t t_hi,
+                                              uint32_t ln) {
+    const uint64_t bp = (static_cast<uint64_t>(row_bcast<J>(p_hi)) << 32) | row_bcast<J>(p_lo);
+    const double t = __hiloint2double(static_cast<int>(row_bcast<J>(t_hi)),
+                                      static_cast<int>(row_bcast<J>(t_lo)));
+    const int l = static_cast<int>(row_bcast<J>(ln));
+    // every lane loads (entry 0 past the limit) so the rounds' loads need no
+    // branch and can all be in flight together
+    const double v = reinterpret_cast<const double*>(bp)[sub < l ? sub : 0];
+    const uint64_t m = __ballot(sub < l && v < t);
+    const uint32_t c = static_cast<uint32_t>(__popcll((m >> qbase) & 0xffffull));
+    mine = sub == J ? c : mine;
+}
 
 // Number of the first lim (<= 16) entries of blk below target, for every lane
-// with need (0 for the others).  All lanes of the wave call it together;
-// safe is a readable address for lanes without a request.
+// with need (0 for the others).  All lanes of the wave call it together (the
+// row broadcasts read every lane); safe is a readable address for lanes
+// without a request.
 __device__ __forceinline__ uint32_t wave_count_below16(bool need, const double* blk,
                                                        uint32_t lim, double target,
                                                        const double* safe) {
     if (__ballot(need) == 0) return 0;  // uniform: no request in the wave
     const int lane = __lane_id();
     const int sub = lane & 15, qbase = lane & 48;
-    const long long bp = reinterpret_cast<long long>(need ? blk : safe);
-    const int ln = need ? static_cast<int>(lim) : 0;
+    const uint64_t bp = reinterpret_cast<uint64_t>(need ? blk : safe);
+    const uint32_t p_lo = static_cast<uint32_t>(bp), p_hi = static_cast<uint32_t>(bp >> 32);
+    const uint32_t t_lo = static_cast<uint32_t>(__double2loint(target));
+    const uint32_t t_hi = static_cast<uint32_t>(__double2hiint(target));
+    const uint32_t ln = need ? lim : 0u;
     uint32_t mine = 0;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const int src = qbase | j;
-        const double* b = reinterpret_cast<const double*>(__shfl(bp, src));
-        const double t = __shfl(target, src);
-        const int l = __shfl(ln, src);
-        // every lane loads (entry 0 past the limit) so the rounds' loads need
-        // no branch and can all be in flight together
-        const double v = b[sub < l ? sub : 0];
-        const uint64_t m = __ballot(sub < l && v < t);
-        const uint32_t c = static_cast<uint32_t>(__popcll((m >> qbase) & 0xffffull));
-        mine = sub == j ? c : mine;
-    }
+    count_round16<0>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
+    count_round16<1>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
+    count_round16<2>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
+    count_round16<3>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
+    count_round16<4>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
+    count_round16<5>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
+    count_round16<6>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
+    count_round16<7>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
+    count_round16<8>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
+    count_round16<9>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
+    count_round16<10>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
+    count_round16<11>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
+    count_round16<12>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
+    count_round16<13>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
+    count_round16<14>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
+    count_round16<15>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
     return mine;
 }
 
@@ -712,6 +751,11 @@ __device__ __forceinline__ WeightHop weight_hop_begin(const WalkGraph& g, int pi
     const double end_sum = g.d.w[gse - 1];
     if (end_sum < start_sum) return s;
     s.target = start_sum + rg * (end_sum - start_sum);
+    if (s.target <= start_sum) {  // pick_weights' case without a search
+        s.gpos = static_cast<uint32_t>(gs);
+        s.fail = false;
+        return s;
+    }
     s.lv = (g.d.wx && G > static_cast<int>(kWIdxMin)) ? g.d.wx + g.d.wx_off[u] : nullptr;
     s.gb = gb;
     s.G = Gu;
