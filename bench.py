@@ -56,7 +56,8 @@ KERNEL_SOURCES = {
 
 
 # kernels of the walk path; every other kernel belongs to the index build
-WALK_PATH_KERNELS = ("walk_kernel", "walk_start_kernel", "layout_", "walk_stats",
+WALK_PATH_KERNELS = ("walk_kernel", "walk_weights_kernel", "walk_start_kernel", "layout_",
+                     "walk_stats",
                      "node_group_init", "node_group_segment", "gather_walk_features")
 
 

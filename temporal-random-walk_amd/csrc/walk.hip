@@ -586,6 +586,11 @@ __device__ __forceinline__ uint64_t grid_position(int remap) {
 // quarter is a DPP row, so lane j's request reaches its quarter by a row
 // broadcast (row_newbcast:j, a VALU move) rather than through the LDS.
 
+// A device-memory double.  Loads through it are global loads, whose results
+// return in order, so a wave waits for each round's load alone (vmcnt(n))
+// rather than for all of them (flat loads, which may also reach the LDS).
+typedef __attribute__((address_space(1))) const double GlobalF64;
+
 // Lane J's value in every lane of its 16-lane row.
 template <int J>
 __device__ __forceinline__ uint32_t row_bcast(uint32_t v) {
@@ -593,19 +598,25 @@ __device__ __forceinline__ uint32_t row_bcast(uint32_t v) {
         __builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x150 + J, 0xf, 0xf, false));
 }
 
-// Round J of wave_count_below16: the quarters count the blocks of their lanes
-// J, and lane J of each quarter keeps its count in mine.
+// Round J of wave_count_below16, in two halves: count_load16<J> issues the
+// read of the quarters' lanes J blocks and count_below16_round<J> counts them,
+// lane J of each quarter keeping its count in mine.  A request is the block's
+// address with its limit in bits 48-52 (device addresses have 48 bits, which
+// the host checks) and the target.  Every lane loads (entry 0 past the limit:
+// a select of the index, not of the load, so the loads need no branch).
 template <int J>
-__device__ __forceinline__ void count_round16(uint32_t& mine, int sub, int qbase, uint32_t p_lo,
-                                              uint32_t p_hi, uint32_t t_lo, uint32_t t_hi,
-                                              uint32_t ln) {
-    const uint64_t bp = (static_cast<uint64_t>(row_bcast<J>(p_hi)) << 32) | row_bcast<J>(p_lo);
+__device__ __forceinline__ double count_load16(int sub, uint32_t p_lo, uint32_t p_hi) {
+    const uint32_t hi = row_bcast<J>(p_hi);
+    const uint64_t bp = (static_cast<uint64_t>(hi & 0xffffu) << 32) | row_bcast<J>(p_lo);
+    const int l = static_cast<int>(hi >> 16);
+    return reinterpret_cast<const GlobalF64*>(bp)[sub < l ? sub : 0];
+}
+template <int J>
+__device__ __forceinline__ void count_below16_round(uint32_t& mine, int sub, int qbase, double v,
+                                                    uint32_t p_hi, uint32_t t_lo, uint32_t t_hi) {
+    const int l = static_cast<int>(row_bcast<J>(p_hi) >> 16);
     const double t = __hiloint2double(static_cast<int>(row_bcast<J>(t_hi)),
                                       static_cast<int>(row_bcast<J>(t_lo)));
-    const int l = static_cast<int>(row_bcast<J>(ln));
-    // every lane loads (entry 0 past the limit) so the rounds' loads need no
-    // branch and can all be in flight together
-    const double v = reinterpret_cast<const double*>(bp)[sub < l ? sub : 0];
     const uint64_t m = __ballot(sub < l && v < t);
     const uint32_t c = static_cast<uint32_t>(__popcll((m >> qbase) & 0xffffull));
     mine = sub == J ? c : mine;
@@ -614,7 +625,8 @@ __device__ __forceinline__ void count_round16(uint32_t& mine, int sub, int qbase
 // Number of the first lim (<= 16) entries of blk below target, for every lane
 // with need (0 for the others).  All lanes of the wave call it together (the
 // row broadcasts read every lane); safe is a readable address for lanes
-// without a request.
+// without a request.  The sixteen rounds' loads are issued before the first
+// count, so they are in flight together.
 __device__ __forceinline__ uint32_t wave_count_below16(bool need, const double* blk,
                                                        uint32_t lim, double target,
                                                        const double* safe) {
@@ -622,27 +634,22 @@ __device__ __forceinline__ uint32_t wave_count_below16(bool need, const double* 
     const int lane = __lane_id();
     const int sub = lane & 15, qbase = lane & 48;
     const uint64_t bp = reinterpret_cast<uint64_t>(need ? blk : safe);
-    const uint32_t p_lo = static_cast<uint32_t>(bp), p_hi = static_cast<uint32_t>(bp >> 32);
+    const uint32_t p_lo = static_cast<uint32_t>(bp);
+    const uint32_t p_hi = static_cast<uint32_t>(bp >> 32) | ((need ? lim : 0u) << 16);
     const uint32_t t_lo = static_cast<uint32_t>(__double2loint(target));
     const uint32_t t_hi = static_cast<uint32_t>(__double2hiint(target));
-    const uint32_t ln = need ? lim : 0u;
+    double v[16];
+#define TRW_LOAD(J) v[J] = count_load16<J>(sub, p_lo, p_hi)
+    TRW_LOAD(0); TRW_LOAD(1); TRW_LOAD(2); TRW_LOAD(3); TRW_LOAD(4); TRW_LOAD(5);
+    TRW_LOAD(6); TRW_LOAD(7); TRW_LOAD(8); TRW_LOAD(9); TRW_LOAD(10); TRW_LOAD(11);
+    TRW_LOAD(12); TRW_LOAD(13); TRW_LOAD(14); TRW_LOAD(15);
+#undef TRW_LOAD
     uint32_t mine = 0;
-    count_round16<0>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
-    count_round16<1>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
-    count_round16<2>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
-    count_round16<3>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
-    count_round16<4>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
-    count_round16<5>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
-    count_round16<6>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
-    count_round16<7>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
-    count_round16<8>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
-    count_round16<9>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
-    count_round16<10>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
-    count_round16<11>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
-    count_round16<12>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
-    count_round16<13>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
-    count_round16<14>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
-    count_round16<15>(mine, sub, qbase, p_lo, p_hi, t_lo, t_hi, ln);
+#define TRW_COUNT(J) count_below16_round<J>(mine, sub, qbase, v[J], p_hi, t_lo, t_hi)
+    TRW_COUNT(0); TRW_COUNT(1); TRW_COUNT(2); TRW_COUNT(3); TRW_COUNT(4); TRW_COUNT(5);
+    TRW_COUNT(6); TRW_COUNT(7); TRW_COUNT(8); TRW_COUNT(9); TRW_COUNT(10); TRW_COUNT(11);
+    TRW_COUNT(12); TRW_COUNT(13); TRW_COUNT(14); TRW_COUNT(15);
+#undef TRW_COUNT
     return mine;
 }
 
@@ -832,6 +839,27 @@ __device__ __forceinline__ void walk_wave_weights(const WalkGraph& g, const Walk
     if (in_range) a.lens[w] = static_cast<uint64_t>(len);
 }
 
+// walk_kernel of the weight family: the walks of a wave share its weight
+// searches (walk_wave_weights).  Its registers (the search keeps sixteen loads
+// in flight) allow four waves per SIMD; a cap at five makes the compiler
+// issue the loads one at a time, which is slower.
+template <bool Fwd, bool Dir, int Fam>
+__global__ __launch_bounds__(kB) void walk_weights_kernel(WalkGraph g, WalkArgs a) {
+    static_assert(Fam == kFamWeight, "the weight family's kernel");
+    __shared__ double s_xt[kExpTables];
+    const bool use_xt = a.walk_bias == kExponentialIndex;
+    if (use_xt) {
+        fill_exp_tables(s_xt, threadIdx.x, kB);
+        __syncthreads();
+    }
+    if (a.L > 0) {  // uniform
+        walk_wave_weights<Fwd>(g, a, use_xt ? s_xt : nullptr);
+        return;
+    }
+    const uint64_t q = a.q0 + grid_position(a.xcd_remap);
+    if (q < a.q_end) a.lens[a.order ? a.order[q] : q] = 0;
+}
+
 template <bool Fwd, bool Dir, int Fam>
 __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
     // the exponential index picker's thresholds (expm1 of every length it
@@ -843,12 +871,6 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
         __syncthreads();
     }
     const double* em1 = use_xt ? s_xt : nullptr;
-    if constexpr (Fam == kFamWeight) {
-        if (a.L > 0) {  // uniform
-            walk_wave_weights<Fwd>(g, a, em1);
-            return;
-        }
-    }
     const uint64_t q = a.q0 + grid_position(a.xcd_remap);
     if (q >= a.q_end) return;
     const uint64_t w = a.order ? a.order[q] : q;
@@ -1804,6 +1826,11 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
         g.d.w_size = weights_ready ? wd.n_groups : 0;
         g.d.wx_off = wd.wx_off.p;
         g.d.wx = weights_ready && wx.n ? wx.p : nullptr;
+        // the wave-shared weight search carries a block's limit above bit 47
+        // of its address
+        for (const void* ptr : {static_cast<const void*>(w.p), static_cast<const void*>(wx.p)})
+            if (reinterpret_cast<uintptr_t>(ptr) >> 48)
+                throw std::runtime_error("weight arrays above the 48-bit address range");
     }
     g.adj_off = adj_lists_ready ? adj_off.p : nullptr;
     g.adj_nbr = adj_nbr.p;
@@ -1851,22 +1878,24 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
                          (forward ? wd.wx_fwd : wd.wx_bwd).bytes() + wd.wx_off.bytes();
     }
     if (walk_bias == kTemporalNode2Vec && adj_ready) w_index_bytes += adj_hash.bytes();
-#define TRW_LAUNCH_FAMILY(K, F, D, G, ...)                                                     \
+#define TRW_LAUNCH_FAMILY(K, KW, F, D, G, ...)                                                 \
     do {                                                                                       \
         if (index_only)                                                                        \
             hipLaunchKernelGGL((K<F, D, kFamIndex>), G, dim3(kB), 0, s, __VA_ARGS__);           \
         else if (no_node2vec)                                                                  \
-            hipLaunchKernelGGL((K<F, D, kFamWeight>), G, dim3(kB), 0, s, __VA_ARGS__);          \
+            hipLaunchKernelGGL((KW<F, D, kFamWeight>), G, dim3(kB), 0, s, __VA_ARGS__);         \
         else                                                                                   \
             hipLaunchKernelGGL((K<F, D, kFamAny>), G, dim3(kB), 0, s, __VA_ARGS__);             \
     } while (0)
-#define TRW_LAUNCH(K, G, ...)                                                                  \
+// K for every family, or KW in K's place for the weight family
+#define TRW_LAUNCH2(K, KW, G, ...)                                                             \
     do {                                                                                       \
-        if (forward && cfg.is_directed) TRW_LAUNCH_FAMILY(K, true, true, G, __VA_ARGS__);      \
-        else if (forward) TRW_LAUNCH_FAMILY(K, true, false, G, __VA_ARGS__);                   \
-        else if (cfg.is_directed) TRW_LAUNCH_FAMILY(K, false, true, G, __VA_ARGS__);           \
-        else TRW_LAUNCH_FAMILY(K, false, false, G, __VA_ARGS__);                               \
+        if (forward && cfg.is_directed) TRW_LAUNCH_FAMILY(K, KW, true, true, G, __VA_ARGS__);  \
+        else if (forward) TRW_LAUNCH_FAMILY(K, KW, true, false, G, __VA_ARGS__);               \
+        else if (cfg.is_directed) TRW_LAUNCH_FAMILY(K, KW, false, true, G, __VA_ARGS__);       \
+        else TRW_LAUNCH_FAMILY(K, KW, false, false, G, __VA_ARGS__);                           \
     } while (0)
+#define TRW_LAUNCH(K, G, ...) TRW_LAUNCH2(K, K, G, __VA_ARGS__)
 
     // ---- processing order: walks sorted by the time rank of their start
     // edge, so the walks of one wave -- and of one XCD -- search the same
@@ -1941,10 +1970,11 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
     } else if (nw) {
         a.q0 = 0;
         a.q_end = nw;
-        TRW_LAUNCH(walk_kernel, dim3(grid_for(nw)), g, a);
+        TRW_LAUNCH2(walk_kernel, walk_weights_kernel, dim3(grid_for(nw)), g, a);
         check_hip(hipGetLastError(), "walk kernel launch");
     }
 #undef TRW_LAUNCH
+#undef TRW_LAUNCH2
 #undef TRW_LAUNCH_FAMILY
     check_hip(hipEventRecord(ev[6], s), "event");
     if (nw && L > 0) {
