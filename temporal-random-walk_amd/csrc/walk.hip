@@ -400,6 +400,12 @@ __device__ Hop tn2v_pick(const WalkGraph& g, int prev, uint32_t vb, uint32_t ve,
     if (g.inv_p > bmax) bmax = g.inv_p;
     if (g.inv_q > bmax) bmax = g.inv_q;
     const double inv_bmax = 1.0 / bmax;
+    // acceptance thresholds beta * inv_bmax of a neighbour of prev (beta = 1)
+    // and of another node (beta = 1/q); a draw below both or at or above both
+    // is decided without the adjacency lookup
+    const double acc_adj = 1.0 * inv_bmax, acc_far = g.inv_q * inv_bmax;
+    const double acc_lo = acc_adj < acc_far ? acc_adj : acc_far;
+    const double acc_hi = acc_adj < acc_far ? acc_far : acc_adj;
     Hop last = no_hop();
     for (int retry = 0; retry < kNode2VecMaxRetries; ++retry) {
         const double gr = derive_uniform(rg, re, retry * 3 + 0);
@@ -417,9 +423,13 @@ __device__ Hop tn2v_pick(const WalkGraph& g, int prev, uint32_t vb, uint32_t ve,
         const uint32_t pick = es + static_cast<uint32_t>(local < ee - es ? local : ee - es - 1);
         const EdgeRec r = load_rec(g.d.rec + pick);
         const int cand = r.nbr;
-        const double beta = (cand == prev) ? g.inv_p : (adjacent(g, prev, cand) ? 1.0 : g.inv_q);
         last = hop_of(r, pr.rank);
-        if (ar < beta * inv_bmax) return last;
+        bool accept;
+        if (cand == prev) accept = ar < g.inv_p * inv_bmax;
+        else if (ar < acc_lo) accept = true;
+        else if (ar >= acc_hi) accept = false;
+        else accept = ar < (adjacent(g, prev, cand) ? acc_adj : acc_far);
+        if (accept) return last;
     }
     return last;
 }

@@ -251,6 +251,24 @@ def test_replay_walks_index_pickers(directed, forward, picker):
                seed=3)
 
 
+@pytest.mark.parametrize("p,q", [(2.0, 0.5), (1.0, 1.0), (0.25, 4.0), (4.0, 1.0)])
+def test_replay_walks_node2vec_return_in_out(p, q):
+    """TemporalNode2Vec's acceptance (temporal_node2vec_helpers.cuh:127-199)
+    with the in-out bias on either side of 1 and a return bias above and
+    below the others: a draw below both non-return thresholds, at or above
+    both, or between them (the only case that asks whether the candidate
+    neighbours the previous node) decides as the reference does."""
+    s, d, t = graphs.powerlaw(2_000, 40_000, s=1.4, seed=19, ts_hi=500_000)
+    og, eng = _pair(True, [(s, d, t)], weights=True, tn2v=True, timescale_bound=20.0, p=p, q=q)
+    for name in WEIGHT_ARRAYS:
+        w = eng.array(name)
+        if w.size:
+            og.set_weights(name, w)
+    _walk_case(og, eng, "TemporalNode2Vec", "Uniform", True, "total", 24, 3_000, seed=8)
+    _walk_case(og, eng, "TemporalNode2Vec", "ExponentialWeight", False, "total", 16, 2_000,
+               seed=9)
+
+
 @pytest.mark.parametrize("directed", [True, False])
 @pytest.mark.parametrize("forward", [True, False])
 @pytest.mark.parametrize("picker", ["ExponentialWeight", "TemporalNode2Vec"])
