@@ -56,7 +56,8 @@ KERNEL_SOURCES = {
 
 
 # kernels of the walk path; every other kernel belongs to the index build
-WALK_PATH_KERNELS = ("walk_kernel", "walk_weights_kernel", "walk_start_kernel", "layout_",
+WALK_PATH_KERNELS = ("walk_kernel", "walk_rows_kernel", "walk_weights_kernel",
+                     "walk_start_kernel", "layout_",
                      "walk_stats",
                      "node_group_init", "node_group_segment", "gather_walk_features")
 
@@ -326,7 +327,8 @@ def run_other_config(k, args):
             tb = eng.timings()["build_ms"]
             mode, L, bias, n, start, direction = call
             eng.sample_device(mode, L, bias, n, initial_edge_bias=start, direction=direction,
-                              walk_order=args.walk_order)
+                              walk_order=args.walk_order,
+                              walk_layout=args.walk_layout)
             tm = eng.timings()
             if i:  # the first round warms up
                 builds.append(tb)
@@ -353,7 +355,8 @@ def run_other_config(k, args):
             tb = eng.timings()["build_ms"]
             eng.sample_device("total", 40, "TemporalNode2Vec", 5_000_000,
                               initial_edge_bias="Uniform", direction="Forward_In_Time",
-                              walk_order=args.walk_order)
+                              walk_order=args.walk_order,
+                              walk_layout=args.walk_layout)
             tm = eng.timings()
             builds.append(tb)
             samples.append(tm["sample_ms"])
@@ -420,6 +423,10 @@ def main():
     ap.add_argument("--walk-order", default="auto",
                     choices=["auto", "walk_id", "start_time", "node_grouped"],
                     help="order the walks run in on the device (the output is the same)")
+    ap.add_argument("--walk-layout", default="auto", choices=["auto", "scratch"],
+                    help="auto: forward walks that pack are written as output rows by the walk "
+                         "kernel; scratch: always walk scratch and the layout pass (the output "
+                         "is the same)")
     ap.add_argument("--config", type=int, default=2,
                     help="2 (default): the cfg2 bench line; 1, 3, 4 or 5: time that BASELINE "
                          "workload instead (device timings, one JSON line)")
@@ -439,7 +446,7 @@ def main():
                     help="summarise rocprofv3 counter runs (--pmc-dir) of one kernel "
                          "(--kernel) into OUT_JSON, then exit; touches no GPU")
     ap.add_argument("--pmc-dir", action="append", default=[])
-    ap.add_argument("--kernel", default="walk_kernel<",
+    ap.add_argument("--kernel", default="walk_rows_kernel<|walk_kernel<",
                     help="kernel name substrings joined by |, or @build for every "
                          "dispatch of an ingest (from its first kernel to the next sample's)")
     ap.add_argument("--per", type=int, default=0,
@@ -503,7 +510,8 @@ def main():
         t1 = time.perf_counter()
         eng.sample_device("total", args.walk_len, "ExponentialIndex", args.walks,
                           initial_edge_bias="Uniform", direction="Forward_In_Time",
-                          walk_order=args.walk_order)
+                          walk_order=args.walk_order,
+                              walk_layout=args.walk_layout)
         t2 = time.perf_counter()
         return t1 - t0, t2 - t1, eng.timings()
 
@@ -531,7 +539,8 @@ def main():
     walk_kernel_ms = sum(t["walk_kernel_ms"] for t in tims) / len(tims)
     build_dev_ms = sum(t["build_ms"] for t in tims) / len(tims)
     # roofline: the walk kernel's compulsory bytes -- inputs and the sampled
-    # direction's index read once, scratch slots and lengths written once
+    # direction's index read once, the output rows it writes (or its scratch
+    # slots) and lengths written once
     # (trw_get_walk_stats) -- over its launch time (HIP events on the engine's
     # stream).  The per-hop demand bytes (every walk's reads, 72 + 8*probes B
     # with the reference's types) are reported beside it: walks running side
@@ -580,6 +589,7 @@ def main():
             "max_walk_len": args.walk_len,
             "parallelism": "1 GPU",
             "walk_order": args.walk_order,
+            "walk_layout": args.walk_layout,
         },
         "index_build_edges_per_s": build_eps,
         "index_build_ms": sum(builds) * 1e3 / args.steps,
@@ -599,7 +609,8 @@ def main():
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": traffic,
-            "kernel": "walk_kernel<true,true,0>",
+            "kernel": ("walk_rows_kernel<true,true,0,16>" if stats["rows_by_walk_kernel"]
+                       else "walk_kernel<true,true,0>"),
             "algorithmic_bytes_per_launch": compulsory,
             "compulsory_read_bytes": stats["compulsory_read_bytes"],
             "compulsory_write_bytes": stats["compulsory_write_bytes"],
@@ -613,7 +624,8 @@ def main():
             "pmc_current": pmc_current,
             "note": "algorithmic bytes = compulsory bytes of one launch (start states, "
                     "processing order and the sampled direction's index arrays read once; "
-                    "packed scratch and walk lengths written once). demand bytes count every "
+                    "the output rows -- or packed scratch, when a layout pass writes the rows -- "
+                    "and walk lengths written once). demand bytes count every "
                     "walk's per-hop reads (72 + 8*ceil(log2(G+1)) B in the reference's types) "
                     "and exceed the HBM rate because walks in start-time order share lines "
                     "in L1/L2. traffic = FETCH_SIZE + WRITE_SIZE of one launch from the "

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TRW_ABI_VERSION 4
+#define TRW_ABI_VERSION 5
 
 typedef enum trw_status {
     TRW_OK = 0,
@@ -106,7 +106,19 @@ typedef struct trw_sample_params {
      * 8 hops the live walks are regrouped by their current node on the device
      * (measured slower than 2; kept for comparison). */
     int32_t walk_order;
+    /* How walks become the row-major output arrays (the output is the same
+     * either way).  0 = automatic: forward walks of the index pickers or
+     * TemporalNode2Vec whose node id, timestamp rank and edge id pack into
+     * 64 bits are written as rows by the walk kernel itself, which buffers
+     * each wave's next 16 slots in LDS; other samples go through walk scratch
+     * and a layout pass.  1 = always scratch and the layout pass. */
+    int32_t walk_layout;
 } trw_sample_params;
+
+typedef enum trw_walk_layout {
+    TRW_LAYOUT_AUTO = 0,
+    TRW_LAYOUT_SCRATCH = 1
+} trw_walk_layout;
 
 typedef enum trw_walk_order {
     TRW_ORDER_AUTO = 0,
@@ -328,6 +340,9 @@ typedef struct trw_walk_stats {
     uint64_t reference_bytes;
     uint64_t compulsory_read_bytes;
     uint64_t compulsory_write_bytes;
+    uint64_t rows_by_walk_kernel; /* 1: the walk kernel wrote the output rows
+                                   * (no scratch, no layout pass); 0: scratch
+                                   * and the layout pass */
 } trw_walk_stats;
 trw_status trw_get_walk_stats(void* handle, trw_walk_stats* out);
 

@@ -125,6 +125,14 @@ struct WalkArgs {
     const StartState* st;  // start state of every walk (walk_start_kernel)
     int xcd_remap;                // spread the order over the XCDs in contiguous slices
     uint64_t q0, q_end;           // grid positions [q0, q_end) of this launch
+    // Row-major outputs written by the walk kernel itself (walk_rows_kernel):
+    // nodes [n][L], timestamps [n][L], edge ids [n][L - 1], in the reference's
+    // types, with the first slot's timestamp start_ts and the padding.
+    int32_t* on;
+    int64_t* ot;
+    int64_t* oe;
+    const int64_t* uniq_ts;
+    int64_t start_ts;
 };
 
 // Scratch rank of a walk's first slot, whose timestamp is the direction's
@@ -224,6 +232,9 @@ __device__ __forceinline__ void store_out(T* p, T v) {
 }
 
 typedef uint32_t u32x2_a4 __attribute__((ext_vector_type(2), aligned(4)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int64_t i64x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // First local index i in [0, G) whose group rank is >= x, G if none: a
 // lower_bound over the node's sorted panel, so the answer is unique and the
@@ -941,6 +952,214 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
     a.lens[w] = static_cast<uint64_t>(len);
 }
 
+// ---- walks written as output rows by the walk kernel -----------------------
+// Forward walks whose slots pack into 64 bits need no scratch and no layout
+// pass: each wave keeps the packed words of its 64 walks' next kRowSlots
+// slots in LDS and, every kRowSlots slots, writes them out as segments of the
+// walks' output rows in the reference's types (int32 nodes, int64 timestamps
+// via uniq_ts, int64 edge ids, padding past a walk's length).  The wave's
+// lanes cut those row segments into store units (16 bytes where the rows
+// allow), so a store covers whole segments of several rows.  Sixteen slots
+// make a timestamp segment one 128-byte line and a node segment half of one
+// when L is a multiple of 16; the 8 KB per wave this takes in LDS holds the
+// kernel to 4 waves per SIMD.  (8 or 12 slots, with 5 waves per SIMD, left
+// partial lines behind every flush and measured slower.)
+constexpr int kRowSlots = 16;
+
+// A row of the wave's flush: the walk (its output row) and its length, -1
+// for a lane without a walk.
+struct RowInfo {
+    uint32_t w;
+    int32_t len;
+};
+
+// Output elements [e0, e0 + ne) of one array (0: nodes, 1: timestamps,
+// 2: edge ids) for the 64 rows of the wave, from its slot buffer buf ([C][64]
+// packed words, entry j of lane l holding slot c0 + j of l's walk) and row
+// table info.  NE > 0 fixes ne at compile time.  Element i of the edge-id row
+// is the edge into slot i + 1.  Store units: 16 bytes (4 nodes, 2 timestamps
+// or edge ids) when every row's segment is 16-byte aligned, else one element.
+// (Aligned 16-byte pairs over the odd-stride edge-id rows, with single
+// elements at the ends, measured slower: the pair and single stores of one
+// round are separate store instructions.)
+template <int Arr, int NE>
+__device__ __forceinline__ void rows_out(const WalkArgs& a, const uint64_t* buf,
+                                         const RowInfo* info, int c0, int e0, int ne_rt,
+                                         int lane) {
+    const int ne = NE > 0 ? NE : ne_rt;
+    if (ne <= 0) return;  // uniform
+    const int K = Arr == 2 ? a.L - 1 : a.L;
+    constexpr int V = Arr == 0 ? 4 : 2;
+    const bool vec = K % V == 0 && e0 % V == 0 && ne % V == 0;
+    const int S = vec ? V : 1;
+    const int U = ne / S;  // store units per row
+    const int total = 64 * U;
+    const int nb = a.pk_nb, rb = a.pk_rb;
+    const uint64_t nmask = (1ull << nb) - 1, rmask = (1ull << rb) - 1;
+    const int soff = (Arr == 2 ? 1 : 0) - c0;  // buffer entry of element i: i + soff
+    // one round at a time: unrolled rounds hold more registers than the 4
+    // waves per SIMD the LDS allows (and were not faster unrolled 2, 4 or 8
+    // times over the timestamp rounds)
+#pragma unroll 1
+    for (int t0 = 0; t0 < total; t0 += 64) {
+        const int t = t0 + lane;
+        const int j = t / U;  // the row: lane j's walk
+        const RowInfo ri = info[j];
+        if (ri.len < 0) continue;
+        const int lj = ri.len;
+        const int i0 = e0 + (t - j * U) * S;
+        const uint64_t at = static_cast<uint64_t>(ri.w) * static_cast<uint64_t>(K) + i0;
+        auto value = [&](int i) -> int64_t {
+            const int slot = i + (Arr == 2 ? 1 : 0);
+            const uint64_t word = buf[(i + soff) * 64 + j];
+            if (Arr == 0) return slot < lj ? static_cast<int32_t>(word & nmask) : a.pad;
+            if (Arr == 2) return slot < lj ? static_cast<int64_t>(word >> (nb + rb)) : -1;
+            if (slot >= lj) return -1;
+            const uint64_t r = (word >> nb) & rmask;
+            return r == rmask ? a.start_ts : a.uniq_ts[r];
+        };
+        if (vec) {
+            if (Arr == 0) {
+                const i32x4 o = {static_cast<int32_t>(value(i0)), static_cast<int32_t>(value(i0 + 1)),
+                                 static_cast<int32_t>(value(i0 + 2)),
+                                 static_cast<int32_t>(value(i0 + 3))};
+                __builtin_nontemporal_store(o, reinterpret_cast<i32x4*>(a.on + at));
+            } else {
+                const i64x2 o = {value(i0), value(i0 + 1)};
+                __builtin_nontemporal_store(o, reinterpret_cast<i64x2*>((Arr == 1 ? a.ot : a.oe) + at));
+            }
+        } else {
+            const int64_t y = value(i0);
+            if (Arr == 0) __builtin_nontemporal_store(static_cast<int32_t>(y), a.on + at);
+            else if (Arr == 1) __builtin_nontemporal_store(y, a.ot + at);
+            else __builtin_nontemporal_store(y, a.oe + at);
+        }
+    }
+}
+
+// Every lane's LDS stores are complete and visible to the whole wave.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Writes slots [c0, c0 + n) of the wave's walks from its slot buffer; n == C
+// but for a row's last chunk.
+template <int C>
+__device__ __forceinline__ void rows_flush(const WalkArgs& a, const uint64_t* buf, RowInfo* info,
+                                           int c0, int n, uint32_t w, int len, bool live,
+                                           int lane) {
+    info[lane] = RowInfo{w, live ? len : -1};
+    wave_lds_sync();
+    const int e0 = c0 > 0 ? c0 - 1 : 0;
+    if (n == C) {
+        rows_out<0, C>(a, buf, info, c0, c0, C, lane);
+        rows_out<1, C>(a, buf, info, c0, c0, C, lane);
+        if (c0 > 0) rows_out<2, C>(a, buf, info, c0, e0, C, lane);
+        else rows_out<2, C - 1>(a, buf, info, c0, e0, C - 1, lane);
+    } else {
+        rows_out<0, 0>(a, buf, info, c0, c0, n, lane);
+        rows_out<1, 0>(a, buf, info, c0, c0, n, lane);
+        rows_out<2, 0>(a, buf, info, c0, e0, c0 + n - 1 - e0, lane);
+    }
+    // every lane's reads of the buffer precede the next chunk's stores
+    wave_lds_sync();
+}
+
+// walk_kernel's walks, forward, written as output rows (above) instead of
+// scratch.  The loop runs in chunks of C slots over the whole row for every
+// lane (wave-uniform), so every row is written to its end, the padding
+// included; a lane whose walk has ended (or that has no walk) only fills.
+template <bool Fwd, bool Dir, int Fam, int C>
+__global__ __launch_bounds__(kB) void walk_rows_kernel(WalkGraph g, WalkArgs a) {
+    static_assert(Fwd, "backward walks are reversed by the layout pass");
+    __shared__ double s_xt[kExpTables];
+    __shared__ uint64_t s_slots[(kB / 64) * C * 64];
+    __shared__ RowInfo s_rows[kB];
+    const bool use_xt = a.walk_bias == kExponentialIndex;
+    if (use_xt) {
+        fill_exp_tables(s_xt, threadIdx.x, kB);
+        __syncthreads();
+    }
+    const double* em1 = use_xt ? s_xt : nullptr;
+    const int lane = __lane_id();
+    uint64_t* buf = s_slots + (threadIdx.x >> 6) * C * 64;
+    RowInfo* info = s_rows + (threadIdx.x & ~63);
+    const uint64_t q = a.q0 + grid_position(a.xcd_remap);
+    const bool live = q < a.q_end;
+    const uint64_t w = live ? (a.order ? a.order[q] : q) : 0;
+    const int L = a.L;  // >= 1 (the host launches it only then)
+    const int32_t cut = live ? cutoff_rank(g, a, w) : -1;
+    const int32_t neg1 = *g.neg1_rank;
+    const StartState s0 = live ? a.st[w] : StartState{-1, -1, -1, -1};
+    int cur = s0.cur, prev = -1;
+    int32_t cur_r = s0.r, cur_e = s0.e;
+    bool alive = live && s0.e != -1;  // the walk writes its next slot
+    int len = 0;
+    const int nb = a.pk_nb, rb = a.pk_rb;
+    for (int c0 = 0; c0 < L; c0 += C) {
+        const int n = min(C, L - c0);
+        for (int j = 0; j < n; ++j) {
+            if (!alive) continue;
+            const int k = c0 + j;
+            uint64_t word;
+            if (k == 0) {
+                word = static_cast<uint64_t>(static_cast<uint32_t>(s0.first)) |
+                       (((1ull << rb) - 1) << nb);
+                len = 1;
+                alive = L > 1 && cur != a.pad;
+            } else {
+                word = static_cast<uint64_t>(static_cast<uint32_t>(cur)) |
+                       (static_cast<uint64_t>(static_cast<uint32_t>(cur_r)) << nb) |
+                       (static_cast<uint64_t>(static_cast<uint32_t>(cur_e)) << (nb + rb));
+                len = k + 1;
+                if (k == L - 1) {
+                    alive = false;  // the reference's last selection cannot change the output
+                } else {
+                    // as in walk_kernel: the header load goes out before the
+                    // hop's Philox rounds
+                    const bool ok = cur >= 0 && cur < g.active_size;
+                    const uint32_t u = ok ? static_cast<uint32_t>(cur) : 0u;
+                    const NodeHdr hd = g.d.hdr[u];
+                    const uint32_t p = static_cast<uint32_t>(k) + 1;
+                    DrawPair r = philox_pair(a.ds, w, p);
+                    asm volatile("" : "+v"(r.a), "+v"(r.b));
+                    if (a.ds.replay) r = replay_pair(a.ds, w, p);
+                    const Hop h = node_edge_from<Fwd, Fam>(g, a.walk_bias, u, ok, hd,
+                                                           cur_r == neg1 ? -1 : cur_r, cut, prev,
+                                                           r.a, r.b, em1);
+                    if (h.e == -1 || h.r == neg1) {
+                        alive = false;
+                    } else {
+                        prev = cur;
+                        cur = h.nbr;
+                        cur_r = h.r;
+                        cur_e = h.e;
+                        alive = cur != a.pad;
+                    }
+                }
+            }
+            buf[j * 64 + lane] = word;
+        }
+        rows_flush<C>(a, buf, info, c0, n, static_cast<uint32_t>(w), len, live, lane);
+    }
+    if (live) a.lens[w] = static_cast<uint64_t>(len);
+}
+
+void launch_rows(bool directed, bool index_only, dim3 grid, hipStream_t s, const WalkGraph& g,
+                 const WalkArgs& a) {
+    constexpr int C = kRowSlots;
+    if (directed && index_only)
+        hipLaunchKernelGGL((walk_rows_kernel<true, true, kFamIndex, C>), grid, dim3(kB), 0, s, g, a);
+    else if (directed)
+        hipLaunchKernelGGL((walk_rows_kernel<true, true, kFamAny, C>), grid, dim3(kB), 0, s, g, a);
+    else if (index_only)
+        hipLaunchKernelGGL((walk_rows_kernel<true, false, kFamIndex, C>), grid, dim3(kB), 0, s, g, a);
+    else
+        hipLaunchKernelGGL((walk_rows_kernel<true, false, kFamAny, C>), grid, dim3(kB), 0, s, g, a);
+}
+
 // ---- node-grouped processing (TRW_ORDER_NODE_GROUPED) ----------------------
 // The north star's cooperative alternative to start-time order: every
 // kNodeGroupHops hops the live walks are regrouped by their current node (a
@@ -1137,9 +1356,6 @@ struct LayoutArgs {
     uint32_t fv;
 };
 
-typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-typedef int64_t i64x2 __attribute__((ext_vector_type(2)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // Value of output slot i of a row whose first `cw` slots were written (x: the
 // scratch value).  Arr 0: nodes, 1: timestamps, 2: edge ids.
@@ -1548,6 +1764,8 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
     if (walk_bias < 0 || walk_bias > kTestLast || start_bias > kTestLast)
         throw InvalidArgument("Invalid picker type");
     if (p.direction != 0 && p.direction != 1) throw InvalidArgument("Invalid walk direction");
+    if (p.walk_layout != TRW_LAYOUT_AUTO && p.walk_layout != TRW_LAYOUT_SCRATCH)
+        throw InvalidArgument("Invalid walk layout");
     // core/temporal_random_walk_cpu.cuh:168-171
     if (start_bias == kTemporalNode2Vec) start_bias = kExponentialWeight;
     const bool forward = p.direction == 0;
@@ -1756,7 +1974,21 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
     uint64_t* sc_packed = nullptr;
     int32_t* sc_nodes = nullptr;
     uint32_t *sc_rank = nullptr, *sc_eids = nullptr;
-    if (packed) {
+    // forward walks of the index pickers or node2vec whose slots pack: the
+    // walk kernel writes the output rows itself (walk_rows_kernel)
+    const bool weight_family = !(is_index_picker(walk_bias) && is_index_picker(start_bias)) &&
+                               walk_bias != kTemporalNode2Vec;
+    const bool rows_direct = p.walk_layout == TRW_LAYOUT_AUTO && packed && forward &&
+                             !weight_family && L > 0 && nw <= 0xffffffffull &&
+                             p.walk_order != TRW_ORDER_NODE_GROUPED;
+    if (rows_direct) {
+        if (!into) {
+            sw_nodes.release();
+            sw_rank.release();
+            sw_eids.release();
+            sw_packed.release();
+        }
+    } else if (packed) {
         if (!into) {
             sw_nodes.release();
             sw_rank.release();
@@ -1794,6 +2026,7 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
     w_dir_forward = forward ? 1 : 0;
     w_constrained = have_starts ? 1 : 0;
     w_packed = packed ? 1 : 0;
+    w_rows = rows_direct ? 1 : 0;
     w_replay = p.replay_draws ? 1 : 0;
 
     // ---- graph view of the sampled direction
@@ -1977,6 +2210,17 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
             check_hip(hipGetLastError(), "node-grouped segment launch");
             ++launches;
         }
+    } else if (nw && rows_direct) {
+        a.q0 = 0;
+        a.q_end = nw;
+        a.on = o_nodes;
+        a.ot = o_ts;
+        a.oe = o_eids;
+        a.uniq_ts = uniq_ts.p;
+        a.start_ts = INT64_MIN;
+        const dim3 grid(grid_for(nw));
+        launch_rows(cfg.is_directed, index_only, grid, s, g, a);
+        check_hip(hipGetLastError(), "walk kernel launch");
     } else if (nw) {
         a.q0 = 0;
         a.q_end = nw;
@@ -1987,7 +2231,7 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
 #undef TRW_LAUNCH2
 #undef TRW_LAUNCH_FAMILY
     check_hip(hipEventRecord(ev[6], s), "event");
-    if (nw && L > 0) {
+    if (nw && L > 0 && !rows_direct) {
         LayoutArgs la{};
         la.sn = sc_nodes;
         la.sr = sc_rank;
@@ -2033,7 +2277,7 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
     // ---- edge features of every walk slot (finalize_host_walks, on device):
     // other dims than multiples of 4 gather from the laid-out edge ids
     if (feat_dim > 0 && eslots) {
-        if (feat_dim % 4 != 0) {
+        if (feat_dim % 4 != 0 || rows_direct) {
             if (!into) w_feat.resize(eslots * feat_dim);
             hipLaunchKernelGGL(gather_walk_features_kernel, dim3(grid_capped(eslots * feat_dim)),
                                dim3(kB), 0, s, o_eids, eslots, static_cast<uint32_t>(feat_dim),
@@ -2086,8 +2330,14 @@ void walk_stats(Engine& e, trw_walk_stats* out) {
         nw && e.w_len > 0 ? nw * e.w_in_bytes_per_walk + e.w_index_bytes +
                                 (e.w_replay ? 16 * out->transitions : 0)
                           : 0;
-    const uint64_t scratch = e.w_packed ? 8 * out->total_len : 8 * out->total_len + 4 * out->transitions;
+    // the kernel's slot writes: packed scratch words, three scratch arrays, or
+    // (rows written by the walk kernel) every output row in full
+    const uint64_t L = static_cast<uint64_t>(e.w_len);
+    const uint64_t scratch =
+        e.w_rows ? nw * (4 * L + 8 * L + 8 * (L > 0 ? L - 1 : 0))
+                 : (e.w_packed ? 8 * out->total_len : 8 * out->total_len + 4 * out->transitions);
     out->compulsory_write_bytes = nw ? 8 * nw + (e.w_len > 0 ? scratch : 0) : 0;
+    out->rows_by_walk_kernel = static_cast<uint64_t>(e.w_rows);
 }
 
 }  // namespace trw

@@ -30,6 +30,9 @@ PICKERS = {
 DIRECTIONS = {"Forward_In_Time": 0, "Backward_In_Time": 1}
 # trw_walk_order: the order walks run in on the device (the output is the same)
 WALK_ORDERS = {"auto": 0, "walk_id": 1, "start_time": 2, "node_grouped": 3}
+# trw_walk_layout: rows written by the walk kernel where it applies, or always
+# scratch and the layout pass (the output is the same)
+WALK_LAYOUTS = {"auto": 0, "scratch": 1}
 MODES = {"total": 0, "all_nodes": 1, "last_batch": 2, "nodes": 3}
 
 # (id, numpy dtype) in the order of trw_array_id
@@ -103,6 +106,7 @@ class TrwSampleParams(C.Structure):
         ("replay_draws_len", C.c_uint64),
         ("shuffle", C.c_int32),
         ("walk_order", C.c_int32),
+        ("walk_layout", C.c_int32),
     ]
 
 
@@ -141,10 +145,11 @@ class TrwWalkStats(C.Structure):
         ("reference_bytes", C.c_uint64),
         ("compulsory_read_bytes", C.c_uint64),
         ("compulsory_write_bytes", C.c_uint64),
+        ("rows_by_walk_kernel", C.c_uint64),
     ]
 
 
-ABI_VERSION = 4  # TRW_ABI_VERSION of include/trw_engine.h
+ABI_VERSION = 5  # TRW_ABI_VERSION of include/trw_engine.h
 _lib = None
 
 
@@ -416,7 +421,7 @@ class Engine:
     # ---- sampling
     def _params(self, mode, max_walk_len, walk_bias, num_walks=0, initial_edge_bias=None,
                 direction="Forward_In_Time", seed_nodes=None, cutoff_times=None, replay=None,
-                shuffle=None, walk_order="auto"):
+                shuffle=None, walk_order="auto", walk_layout="auto"):
         keep = []
         p = TrwSampleParams()
         p.mode = MODES[mode]
@@ -444,6 +449,7 @@ class Engine:
             p.replay_draws_len = r.size
         p.shuffle = -1 if shuffle is None else int(bool(shuffle))
         p.walk_order = WALK_ORDERS[walk_order]
+        p.walk_layout = WALK_LAYOUTS[walk_layout]
         return p, keep
 
     def sample(self, mode, max_walk_len, walk_bias, num_walks=0, **kw):

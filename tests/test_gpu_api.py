@@ -483,14 +483,16 @@ def test_walk_stats_byte_accounting():
     """trw_get_walk_stats against numpy: steps, the per-hop demand bytes
     (72 + 8 ceil(log2(G_u + 1)) B with the reference's types) and the
     compulsory bytes of the walk kernel (start states, processing order and
-    the sampled direction's index read once; packed scratch and lengths
-    written once)."""
+    the sampled direction's index read once; lengths written once, and either
+    packed scratch or -- rows written by the walk kernel -- every output row
+    in full)."""
     from temporal_random_walk import capi
     s, d, t = graphs.powerlaw(5_000, 60_000, n_ts=2_000, seed=9)
     eng = capi.Engine(is_directed=True, shuffle_walk_order=False, global_seed=3)
     eng.add_edges(s, d, t)
     L, n = 16, 70_000  # >= 2^16 walks: start-time order
-    w = eng.sample("total", L, "ExponentialIndex", n, initial_edge_bias="Uniform")
+    w = eng.sample("total", L, "ExponentialIndex", n, initial_edge_bias="Uniform",
+                   walk_layout="scratch")
     st = eng.walk_stats()
     lens = w.lens.astype(np.int64)
     assert st["total_len"] == lens.sum()
@@ -511,4 +513,11 @@ def test_walk_stats_byte_accounting():
     index = 16 * vc + 4 * 2 * (g_o + vc) + 8 * (g_o + 1) + 8 * n_ent
     assert st["compulsory_read_bytes"] == (16 + 4) * n + index
     assert st["compulsory_write_bytes"] == 8 * n + 8 * lens.sum()
+    # the same sample with the rows written by the walk kernel
+    w2 = eng.sample("total", L, "ExponentialIndex", n, initial_edge_bias="Uniform")
+    np.testing.assert_array_equal(w2.nodes, w.nodes)
+    st2 = eng.walk_stats()
+    assert st2["compulsory_read_bytes"] == st["compulsory_read_bytes"]
+    assert st2["compulsory_write_bytes"] == 8 * n + n * (4 * L + 8 * L + 8 * (L - 1))
+    assert st2["reference_bytes"] == st["reference_bytes"]
     eng.close()

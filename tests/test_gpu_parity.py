@@ -219,19 +219,22 @@ def _walk_case(og, eng, picker, start_picker, forward, mode, L, n_or_wpn, seed_n
         cut = None if cutoffs is None else np.repeat(np.asarray(cutoffs, dtype=np.int64), n_or_wpn)
     dr = graphs.draws(len(starts), L, seed=seed)
     ref = og.walks(L, picker, start_picker, forward, starts, dr, cutoffs=cut)
-    # every device processing order gives the reference's walks, row for row
-    for order in ("walk_id", "start_time", "node_grouped"):
+    # every device processing order gives the reference's walks, row for row,
+    # and so do both ways to the output rows (written by the walk kernel, or
+    # scratch and the layout pass)
+    for order, layout in (("walk_id", "auto"), ("start_time", "auto"),
+                          ("start_time", "scratch"), ("node_grouped", "auto")):
         got = eng.sample(mode, L, picker, n_or_wpn, initial_edge_bias=start_picker,
                          direction=direction, seed_nodes=seed_nodes, cutoff_times=cutoffs,
-                         replay=dr, shuffle=False, walk_order=order)
+                         replay=dr, shuffle=False, walk_order=order, walk_layout=layout)
         for k in ("nodes", "timestamps", "lens", "edge_ids"):
             a = getattr(ref, k)
             b = getattr(got, k)
             assert a.shape == b.shape, k
             bad = np.nonzero((a != b).reshape(len(starts), -1).any(axis=1))[0] if a.ndim > 1 \
                 else np.nonzero(a != b)[0]
-            assert bad.size == 0, (f"{picker}/{start_picker} fwd={forward} {mode} {order}: {k} "
-                                   f"differs in {bad.size} walks, first {bad[:5]}")
+            assert bad.size == 0, (f"{picker}/{start_picker} fwd={forward} {mode} {order} "
+                                   f"{layout}: {k} differs in {bad.size} walks, first {bad[:5]}")
     return got
 
 
@@ -370,10 +373,11 @@ def test_normal_mode_invariants_and_features():
 def test_walk_features_through_every_layout_path(dim, forward):
     """Edge features of every walk slot: dims that are multiples of 4 are
     written by the layout pass from the edge ids it holds (packed scratch
-    here), others by a gather over the laid-out edge ids.  Rows of one chunk
-    (L = 20) and of several (L = 150), reversed for backward walks, in both
-    processing orders: each row's features are the store's rows of its edge
-    ids, zeros past its length."""
+    here), others -- and those of rows the walk kernel wrote itself -- by a
+    gather over the laid-out edge ids.  Rows of one chunk (L = 20) and of
+    several (L = 150), reversed for backward walks, in both processing orders
+    and both ways to the rows: each row's features are the store's rows of
+    its edge ids, zeros past its length."""
     s, d, t = graphs.cfg1(n_nodes=200, n_edges=100_000, seed=18)
     rng = np.random.default_rng(18)
     feat = rng.standard_normal((len(s), dim)).astype(np.float32)
@@ -381,9 +385,10 @@ def test_walk_features_through_every_layout_path(dim, forward):
     store_f = eng.array("edge_features").reshape(-1, dim)
     direction = "Forward_In_Time" if forward else "Backward_In_Time"
     for L in (20, 150):
-        for order in ("walk_id", "start_time"):
+        for order, layout in (("walk_id", "auto"), ("start_time", "auto"),
+                              ("start_time", "scratch")):
             w = eng.sample("total", L, "ExponentialIndex", 3_000, initial_edge_bias="Uniform",
-                           direction=direction, walk_order=order)
+                           direction=direction, walk_order=order, walk_layout=layout)
             lens = w.lens.astype(np.int64)
             assert w.edge_features.shape == (3_000, L - 1, dim)
             assert lens.max() > 100 or L == 20

@@ -94,6 +94,9 @@ def test_noalloc_sample_equals_sample_device(dim):
     assert _same(eng, cap, L, dim, "total", "ExponentialIndex", 80_000,
                  initial_edge_bias="Uniform") == 80_000
     assert _same(eng, cap, L, dim, "total", "Linear", 5_000) == 5_000
+    # the scratch and layout pass, in place of rows written by the walk kernel
+    _same(eng, cap, L, dim, "total", "ExponentialIndex", 60_000, initial_edge_bias="Uniform",
+          walk_layout="scratch")
     # start arrays built in the scratch: all nodes (shuffled), seeds with
     # cutoffs (shuffled together), replay draws, backward walks
     nodes = eng.node_count()
@@ -115,9 +118,12 @@ def test_noalloc_sample_rejects_what_does_not_fit():
     # more walks than the outputs hold
     with pytest.raises(ValueError, match="capacity"):
         _noalloc(eng, 1_000, L, 0, "total", "Uniform", 2_000)
-    # more scratch than the fixed array holds (640 B per walk at L = 80)
+    # more scratch than the fixed array holds (walk scratch of 640 B per walk
+    # at L = 80)
     with pytest.raises(ValueError, match="no-allocation"):
-        _noalloc(eng, 400_000, L, 0, "total", "Uniform", 400_000)
+        _noalloc(eng, 400_000, L, 0, "total", "Uniform", 400_000, walk_layout="scratch")
     # the handle and the array stay usable
     _same(eng, 20_000, L, 0, "total", "ExponentialIndex", 20_000)
+    # rows written by the walk kernel need no walk scratch: the same sample fits
+    _same(eng, 400_000, L, 0, "total", "Uniform", 400_000)
     eng.close()
