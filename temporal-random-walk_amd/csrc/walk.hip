@@ -966,26 +966,39 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
 // partial lines behind every flush and measured slower.)
 constexpr int kRowSlots = 16;
 
+// The wave's slot buffer: slot j of lane l at word j * kRowStride + l.  The
+// flush reads 4, 8 or 16 consecutive slots of 16, 8 or 4 rows per
+// instruction; with a stride of 64 words all slots of a row share a bank (4-,
+// 8- and 16-way conflicts), with 68 the 64 lanes' words cover every bank
+// twice, the least a 64-bit access needs.  The 4 pad words of each slot row
+// hold the row table (RowInfo of lane l at word (l / 4) * kRowStride + 64 +
+// l % 4), so the padding costs no LDS.
+constexpr int kRowStride = 68;
+
 // A row of the wave's flush: the walk (its output row) and its length, -1
 // for a lane without a walk.
 struct RowInfo {
     uint32_t w;
     int32_t len;
 };
+static_assert(sizeof(RowInfo) == sizeof(uint64_t), "a row-table entry is one buffer word");
+
+__device__ __forceinline__ RowInfo* row_info(uint64_t* buf, int l) {
+    return reinterpret_cast<RowInfo*>(buf + (l >> 2) * kRowStride + 64 + (l & 3));
+}
 
 // Output elements [e0, e0 + ne) of one array (0: nodes, 1: timestamps,
-// 2: edge ids) for the 64 rows of the wave, from its slot buffer buf ([C][64]
-// packed words, entry j of lane l holding slot c0 + j of l's walk) and row
-// table info.  NE > 0 fixes ne at compile time.  Element i of the edge-id row
+// 2: edge ids) for the 64 rows of the wave, from its slot buffer buf (packed
+// words, entry j of lane l holding slot c0 + j of l's walk) and the row table
+// in its pad words.  NE > 0 fixes ne at compile time.  Element i of the edge-id row
 // is the edge into slot i + 1.  Store units: 16 bytes (4 nodes, 2 timestamps
 // or edge ids) when every row's segment is 16-byte aligned, else one element.
 // (Aligned 16-byte pairs over the odd-stride edge-id rows, with single
 // elements at the ends, measured slower: the pair and single stores of one
 // round are separate store instructions.)
 template <int Arr, int NE>
-__device__ __forceinline__ void rows_out(const WalkArgs& a, const uint64_t* buf,
-                                         const RowInfo* info, int c0, int e0, int ne_rt,
-                                         int lane) {
+__device__ __forceinline__ void rows_out(const WalkArgs& a, uint64_t* buf, int c0, int e0,
+                                         int ne_rt, int lane) {
     const int ne = NE > 0 ? NE : ne_rt;
     if (ne <= 0) return;  // uniform
     const int K = Arr == 2 ? a.L - 1 : a.L;
@@ -1004,14 +1017,14 @@ __device__ __forceinline__ void rows_out(const WalkArgs& a, const uint64_t* buf,
     for (int t0 = 0; t0 < total; t0 += 64) {
         const int t = t0 + lane;
         const int j = t / U;  // the row: lane j's walk
-        const RowInfo ri = info[j];
+        const RowInfo ri = *row_info(buf, j);
         if (ri.len < 0) continue;
         const int lj = ri.len;
         const int i0 = e0 + (t - j * U) * S;
         const uint64_t at = static_cast<uint64_t>(ri.w) * static_cast<uint64_t>(K) + i0;
         auto value = [&](int i) -> int64_t {
             const int slot = i + (Arr == 2 ? 1 : 0);
-            const uint64_t word = buf[(i + soff) * 64 + j];
+            const uint64_t word = buf[(i + soff) * kRowStride + j];
             if (Arr == 0) return slot < lj ? static_cast<int32_t>(word & nmask) : a.pad;
             if (Arr == 2) return slot < lj ? static_cast<int64_t>(word >> (nb + rb)) : -1;
             if (slot >= lj) return -1;
@@ -1047,21 +1060,20 @@ __device__ __forceinline__ void wave_lds_sync() {
 // Writes slots [c0, c0 + n) of the wave's walks from its slot buffer; n == C
 // but for a row's last chunk.
 template <int C>
-__device__ __forceinline__ void rows_flush(const WalkArgs& a, const uint64_t* buf, RowInfo* info,
-                                           int c0, int n, uint32_t w, int len, bool live,
-                                           int lane) {
-    info[lane] = RowInfo{w, live ? len : -1};
+__device__ __forceinline__ void rows_flush(const WalkArgs& a, uint64_t* buf, int c0, int n,
+                                           uint32_t w, int len, bool live, int lane) {
+    *row_info(buf, lane) = RowInfo{w, live ? len : -1};
     wave_lds_sync();
     const int e0 = c0 > 0 ? c0 - 1 : 0;
     if (n == C) {
-        rows_out<0, C>(a, buf, info, c0, c0, C, lane);
-        rows_out<1, C>(a, buf, info, c0, c0, C, lane);
-        if (c0 > 0) rows_out<2, C>(a, buf, info, c0, e0, C, lane);
-        else rows_out<2, C - 1>(a, buf, info, c0, e0, C - 1, lane);
+        rows_out<0, C>(a, buf, c0, c0, C, lane);
+        rows_out<1, C>(a, buf, c0, c0, C, lane);
+        if (c0 > 0) rows_out<2, C>(a, buf, c0, e0, C, lane);
+        else rows_out<2, C - 1>(a, buf, c0, e0, C - 1, lane);
     } else {
-        rows_out<0, 0>(a, buf, info, c0, c0, n, lane);
-        rows_out<1, 0>(a, buf, info, c0, c0, n, lane);
-        rows_out<2, 0>(a, buf, info, c0, e0, c0 + n - 1 - e0, lane);
+        rows_out<0, 0>(a, buf, c0, c0, n, lane);
+        rows_out<1, 0>(a, buf, c0, c0, n, lane);
+        rows_out<2, 0>(a, buf, c0, e0, c0 + n - 1 - e0, lane);
     }
     // every lane's reads of the buffer precede the next chunk's stores
     wave_lds_sync();
@@ -1075,8 +1087,8 @@ template <bool Fwd, bool Dir, int Fam, int C>
 __global__ __launch_bounds__(kB) void walk_rows_kernel(WalkGraph g, WalkArgs a) {
     static_assert(Fwd, "backward walks are reversed by the layout pass");
     __shared__ double s_xt[kExpTables];
-    __shared__ uint64_t s_slots[(kB / 64) * C * 64];
-    __shared__ RowInfo s_rows[kB];
+    __shared__ uint64_t s_slots[(kB / 64) * C * kRowStride];
+    static_assert(C >= 16, "the row table lives in the pad words of 16 slot rows");
     const bool use_xt = a.walk_bias == kExponentialIndex;
     if (use_xt) {
         fill_exp_tables(s_xt, threadIdx.x, kB);
@@ -1084,8 +1096,7 @@ __global__ __launch_bounds__(kB) void walk_rows_kernel(WalkGraph g, WalkArgs a) 
     }
     const double* em1 = use_xt ? s_xt : nullptr;
     const int lane = __lane_id();
-    uint64_t* buf = s_slots + (threadIdx.x >> 6) * C * 64;
-    RowInfo* info = s_rows + (threadIdx.x & ~63);
+    uint64_t* buf = s_slots + (threadIdx.x >> 6) * C * kRowStride;
     const uint64_t q = a.q0 + grid_position(a.xcd_remap);
     const bool live = q < a.q_end;
     const uint64_t w = live ? (a.order ? a.order[q] : q) : 0;
@@ -1140,24 +1151,122 @@ __global__ __launch_bounds__(kB) void walk_rows_kernel(WalkGraph g, WalkArgs a) 
                     }
                 }
             }
-            buf[j * 64 + lane] = word;
+            buf[j * kRowStride + lane] = word;
         }
-        rows_flush<C>(a, buf, info, c0, n, static_cast<uint32_t>(w), len, live, lane);
+        rows_flush<C>(a, buf, c0, n, static_cast<uint32_t>(w), len, live, lane);
     }
     if (live) a.lens[w] = static_cast<uint64_t>(len);
 }
 
-void launch_rows(bool directed, bool index_only, dim3 grid, hipStream_t s, const WalkGraph& g,
+// walk_wave_weights' walks (the weight family, the wave sharing its weight
+// searches), forward, written as output rows: the same chunked loop as
+// walk_rows_kernel, every lane taking part in every slot's shared search.
+template <bool Fwd, int C>
+__device__ __forceinline__ void walk_wave_weights_rows(const WalkGraph& g, const WalkArgs& a,
+                                                       const double* em1, uint64_t* buf) {
+    const int lane = __lane_id();
+    const uint64_t q = a.q0 + grid_position(a.xcd_remap);
+    const bool live = q < a.q_end;
+    const uint64_t w = live ? (a.order ? a.order[q] : q) : 0;
+    const int L = a.L;  // >= 1 (the host launches it only then)
+    const int32_t cut = live ? cutoff_rank(g, a, w) : -1;
+    const int32_t neg1 = *g.neg1_rank;
+    const StartState s0 = live ? a.st[w] : StartState{-1, -1, -1, -1};
+    int cur = s0.cur;
+    int32_t cur_r = s0.r, cur_e = s0.e;
+    bool alive = live && s0.e != -1;  // the walk writes its next slot
+    int len = 0;
+    const int nb = a.pk_nb, rb = a.pk_rb;
+    for (int c0 = 0; c0 < L; c0 += C) {
+        const int n = min(C, L - c0);
+        for (int j = 0; j < n; ++j) {
+            const int k = c0 + j;
+            WeightHop hs{true, false, 0, 0, 0, 0, 0, 0, nullptr, 0.0};
+            double re = 0.0;
+            bool hop = false;  // the lane selects a hop after slot k
+            if (alive) {
+                uint64_t word;
+                if (k == 0) {
+                    word = static_cast<uint64_t>(static_cast<uint32_t>(s0.first)) |
+                           (((1ull << rb) - 1) << nb);
+                    len = 1;
+                    alive = L > 1 && cur != a.pad;
+                } else {
+                    word = static_cast<uint64_t>(static_cast<uint32_t>(cur)) |
+                           (static_cast<uint64_t>(static_cast<uint32_t>(cur_r)) << nb) |
+                           (static_cast<uint64_t>(static_cast<uint32_t>(cur_e)) << (nb + rb));
+                    len = k + 1;
+                    if (k == L - 1) {
+                        alive = false;  // the reference's last selection cannot change the output
+                    } else {
+                        const bool ok = cur >= 0 && cur < g.active_size;
+                        const uint32_t u = ok ? static_cast<uint32_t>(cur) : 0u;
+                        const NodeHdr hd = g.d.hdr[u];
+                        const DrawPair r = draw_pair(a.ds, w, static_cast<uint32_t>(k) + 1);
+                        hs = weight_hop_begin<Fwd>(g, a.walk_bias, u, ok, hd,
+                                                   cur_r == neg1 ? -1 : cur_r, cut, r.a, em1);
+                        re = r.b;
+                        if (hs.fail) alive = false;
+                        else hop = true;
+                    }
+                }
+                buf[j * kRowStride + lane] = word;
+            }
+            const uint32_t kk = wave_weight_lower_bound(hs.need, g.d.w + hs.gb, hs.G, hs.lv,
+                                                        hs.target, g.d.w);
+            if (hop) {
+                uint32_t gpos = hs.gpos;
+                if (hs.need) {
+                    const uint32_t x = hs.gb + kk;
+                    gpos = x < hs.gs ? hs.gs : (x > hs.gse ? hs.gse : x);
+                }
+                const Hop h = hop_from_group(g, gpos, hs.ge, re);
+                if (h.e == -1 || h.r == neg1) {
+                    alive = false;
+                } else {
+                    cur = h.nbr;
+                    cur_r = h.r;
+                    cur_e = h.e;
+                    alive = cur != a.pad;
+                }
+            }
+        }
+        rows_flush<C>(a, buf, c0, n, static_cast<uint32_t>(w), len, live, lane);
+    }
+    if (live) a.lens[w] = static_cast<uint64_t>(len);
+}
+
+template <bool Fwd, bool Dir, int Fam, int C>
+__global__ __launch_bounds__(kB) void walk_weights_rows_kernel(WalkGraph g, WalkArgs a) {
+    static_assert(Fam == kFamWeight && Fwd, "the weight family's forward row writer");
+    __shared__ double s_xt[kExpTables];
+    __shared__ uint64_t s_slots[(kB / 64) * C * kRowStride];
+    const bool use_xt = a.walk_bias == kExponentialIndex;
+    if (use_xt) {
+        fill_exp_tables(s_xt, threadIdx.x, kB);
+        __syncthreads();
+    }
+    walk_wave_weights_rows<Fwd, C>(g, a, use_xt ? s_xt : nullptr,
+                                   s_slots + (threadIdx.x >> 6) * C * kRowStride);
+}
+
+// The row-writing walk kernel of a picker family (kFamIndex, kFamWeight or
+// kFamAny), forward.
+void launch_rows(bool directed, int family, dim3 grid, hipStream_t s, const WalkGraph& g,
                  const WalkArgs& a) {
     constexpr int C = kRowSlots;
-    if (directed && index_only)
-        hipLaunchKernelGGL((walk_rows_kernel<true, true, kFamIndex, C>), grid, dim3(kB), 0, s, g, a);
-    else if (directed)
-        hipLaunchKernelGGL((walk_rows_kernel<true, true, kFamAny, C>), grid, dim3(kB), 0, s, g, a);
-    else if (index_only)
-        hipLaunchKernelGGL((walk_rows_kernel<true, false, kFamIndex, C>), grid, dim3(kB), 0, s, g, a);
-    else
-        hipLaunchKernelGGL((walk_rows_kernel<true, false, kFamAny, C>), grid, dim3(kB), 0, s, g, a);
+#define TRW_ROWS(K, D, F) hipLaunchKernelGGL((K<true, D, F, C>), grid, dim3(kB), 0, s, g, a)
+    if (family == kFamIndex) {
+        if (directed) TRW_ROWS(walk_rows_kernel, true, kFamIndex);
+        else TRW_ROWS(walk_rows_kernel, false, kFamIndex);
+    } else if (family == kFamWeight) {
+        if (directed) TRW_ROWS(walk_weights_rows_kernel, true, kFamWeight);
+        else TRW_ROWS(walk_weights_rows_kernel, false, kFamWeight);
+    } else {
+        if (directed) TRW_ROWS(walk_rows_kernel, true, kFamAny);
+        else TRW_ROWS(walk_rows_kernel, false, kFamAny);
+    }
+#undef TRW_ROWS
 }
 
 // ---- node-grouped processing (TRW_ORDER_NODE_GROUPED) ----------------------
@@ -1974,13 +2083,10 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
     uint64_t* sc_packed = nullptr;
     int32_t* sc_nodes = nullptr;
     uint32_t *sc_rank = nullptr, *sc_eids = nullptr;
-    // forward walks of the index pickers or node2vec whose slots pack: the
-    // walk kernel writes the output rows itself (walk_rows_kernel)
-    const bool weight_family = !(is_index_picker(walk_bias) && is_index_picker(start_bias)) &&
-                               walk_bias != kTemporalNode2Vec;
-    const bool rows_direct = p.walk_layout == TRW_LAYOUT_AUTO && packed && forward &&
-                             !weight_family && L > 0 && nw <= 0xffffffffull &&
-                             p.walk_order != TRW_ORDER_NODE_GROUPED;
+    // forward walks whose slots pack: the walk kernel writes the output rows
+    // itself (walk_rows_kernel, walk_weights_rows_kernel)
+    const bool rows_direct = p.walk_layout == TRW_LAYOUT_AUTO && packed && forward && L > 0 &&
+                             nw <= 0xffffffffull && p.walk_order != TRW_ORDER_NODE_GROUPED;
     if (rows_direct) {
         if (!into) {
             sw_nodes.release();
@@ -2219,7 +2325,8 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
         a.uniq_ts = uniq_ts.p;
         a.start_ts = INT64_MIN;
         const dim3 grid(grid_for(nw));
-        launch_rows(cfg.is_directed, index_only, grid, s, g, a);
+        launch_rows(cfg.is_directed,
+                    index_only ? kFamIndex : (no_node2vec ? kFamWeight : kFamAny), grid, s, g, a);
         check_hip(hipGetLastError(), "walk kernel launch");
     } else if (nw) {
         a.q0 = 0;
