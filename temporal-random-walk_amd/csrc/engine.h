@@ -283,11 +283,10 @@ struct Engine {
     DBuf<uint32_t> ng_carry, ng_keys0, ng_keys1, ng_vals0, ng_vals1, ng_count;
     DBuf<uint64_t> acc64;
 
-    // walks (device): slot-major scratch written by the walk kernel (node,
-    // timestamp rank, 32-bit edge id), then the row-major output
-    // [num_walks, L] in the reference's types
-    DBuf<int32_t> sw_nodes;
-    DBuf<uint32_t> sw_rank, sw_eids;
+    // walks (device): slot-major scratch of 64-bit slot words (node, rank of
+    // the slot's time when it fits, 32-bit edge id) where a layout pass writes
+    // the rows, then the row-major output [num_walks, L] in the reference's
+    // types
     DBuf<uint64_t> sw_packed;
     DBuf<int32_t> w_nodes;
     DBuf<int64_t> w_ts, w_eids;
@@ -302,7 +301,6 @@ struct Engine {
     // scratch (the compulsory bytes of trw_get_walk_stats)
     uint64_t w_in_bytes_per_walk = 0;  // start state, processing order, cutoff
     uint64_t w_index_bytes = 0;        // index arrays the launched kernel reads
-    int w_packed = 0;
     int w_rows = 0;  // the walk kernel wrote the output rows itself (no scratch)
     int w_replay = 0;
 

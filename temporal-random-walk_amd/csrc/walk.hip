@@ -110,12 +110,8 @@ struct WalkArgs {
     const int64_t* cutoffs;  // nullptr => none
     uint64_t n;
     DrawSource ds;
-    int32_t* nodes;
-    uint32_t* ranks;
     uint64_t* lens;
-    uint32_t* eids;
-    // packed scratch (nullptr: the three arrays above): one 64-bit word per
-    // slot, node | rank << pk_nb | (edge id into the slot) << (pk_nb + pk_rb)
+    // walk scratch, one 64-bit slot word per slot (slot_word below)
     uint64_t* packed;
     int pk_nb, pk_rb;
     // Processing order (nullptr: walk id order).  Position q of the grid runs
@@ -132,61 +128,64 @@ struct WalkArgs {
     int64_t* ot;
     int64_t* oe;
     const int64_t* uniq_ts;
+    const int64_t* edge_ts;  // the store's timestamps (slot words without a rank field)
     int64_t start_ts;
 };
 
-// Scratch rank of a walk's first slot, whose timestamp is the direction's
-// sentinel (INT64_MIN forward, INT64_MAX backward) rather than an edge time.
-constexpr uint32_t kStartRank = 0xffffffffu;
+// A slot of a walk as one 64-bit word: the slot's node in the low nb bits,
+// then -- when node id, timestamp rank and edge id fit in 64 bits together
+// (rb > 0) -- the rank of the slot's time in rb bits, then the id of the edge
+// into the slot.  Otherwise (rb == 0) the word holds node and edge id only,
+// which always fit (both below 2^31), and the time is the edge's timestamp in
+// the store.  The first slot, which no edge reaches and whose time is the
+// direction's sentinel, has every bit above the node set: a rank field of all
+// ones (no rank is), or an edge field of all ones (no edge id is).
+__device__ __forceinline__ uint64_t first_word(int nb, int32_t node) {
+    return static_cast<uint64_t>(static_cast<uint32_t>(node)) | (~0ull << nb);
+}
+__device__ __forceinline__ uint64_t slot_word(int nb, int rb, int32_t node, uint32_t rank,
+                                              uint32_t eid) {
+    uint64_t v = static_cast<uint64_t>(static_cast<uint32_t>(node)) |
+                 (static_cast<uint64_t>(eid) << (nb + rb));
+    if (rb) v |= static_cast<uint64_t>(rank) << nb;
+    return v;
+}
+__device__ __forceinline__ int32_t word_node(uint64_t v, int nb) {
+    return static_cast<int32_t>(v & ((1ull << nb) - 1));
+}
+__device__ __forceinline__ int64_t word_eid(uint64_t v, int nb, int rb) {
+    return static_cast<int64_t>(v >> (nb + rb));
+}
+// The slot's timestamp: the sentinel of the first slot, else uniq_ts of its
+// rank or the store's timestamp of its edge.
+__device__ __forceinline__ int64_t word_ts(uint64_t v, int nb, int rb, const int64_t* uniq_ts,
+                                           const int64_t* edge_ts, int64_t start_ts) {
+    if ((v >> nb) == (~0ull >> nb)) return start_ts;
+    return rb ? uniq_ts[(v >> nb) & ((1ull << rb) - 1)] : edge_ts[v >> nb];
+}
 
 // The walk scratch of one grid position.  Tile-major: grid positions come in
 // tiles of 64 (one wave), and slot k of position q lives at
-// [(q / 64) * 64 * K + k * 64 + q % 64] (K slots per row), so the wave stores
-// 256 B per slot and array contiguously and a tile's whole scratch is one
-// contiguous run for the layout pass.  Either three 32-bit arrays (node,
-// timestamp rank, edge id; K = L, L, L - 1), or -- when a node id, a rank and
-// an edge id fit in 64 bits together -- one 64-bit word per slot holding the
-// slot's node and rank and the id of the edge into the slot (K = L; rank
-// field all ones for the first slot): one store per hop instead of three, and
-// 8 instead of 12 scratch bytes per slot for the layout pass to read.
+// [(q / 64) * 64 * L + k * 64 + q % 64], so the wave stores 512 B per slot
+// contiguously and a tile's whole scratch is one contiguous run for the
+// layout pass.
 struct SlotWriter {
-    int32_t* wn;
-    uint32_t* wt;
-    uint32_t* we;
     uint64_t* wp;
     int nb, rb;
     __device__ __forceinline__ SlotWriter(const WalkArgs& a, uint64_t q) {
         const uint64_t tile = q / 64, lane = q % 64, L = static_cast<uint64_t>(a.L);
-        wp = a.packed ? a.packed + tile * 64 * L + lane : nullptr;
-        wn = a.nodes + tile * 64 * L + lane;
-        wt = a.ranks + tile * 64 * L + lane;
-        we = a.eids + tile * 64 * (L - 1) + lane;
+        wp = a.packed + tile * 64 * L + lane;
         nb = a.pk_nb;
         rb = a.pk_rb;
     }
     // slot 0: the walk's origin at the direction's sentinel time
     __device__ __forceinline__ void first(int32_t node) {
-        if (wp) {
-            __builtin_nontemporal_store(static_cast<uint64_t>(static_cast<uint32_t>(node)) |
-                                            (((1ull << rb) - 1) << nb),
-                                        wp);
-        } else {
-            __builtin_nontemporal_store(node, wn);
-            __builtin_nontemporal_store(kStartRank, wt);
-        }
+        __builtin_nontemporal_store(first_word(nb, node), wp);
     }
     // slot k >= 1: its node and rank and the edge that reached it
     __device__ __forceinline__ void slot(int k, int32_t node, uint32_t rank, uint32_t eid) {
-        if (wp) {
-            __builtin_nontemporal_store(static_cast<uint64_t>(static_cast<uint32_t>(node)) |
-                                            (static_cast<uint64_t>(rank) << nb) |
-                                            (static_cast<uint64_t>(eid) << (nb + rb)),
-                                        wp + static_cast<uint64_t>(k) * 64);
-        } else {
-            __builtin_nontemporal_store(node, wn + static_cast<uint64_t>(k) * 64);
-            __builtin_nontemporal_store(rank, wt + static_cast<uint64_t>(k) * 64);
-            __builtin_nontemporal_store(eid, we + static_cast<uint64_t>(k - 1) * 64);
-        }
+        __builtin_nontemporal_store(slot_word(nb, rb, node, rank, eid),
+                                    wp + static_cast<uint64_t>(k) * 64);
     }
 };
 
@@ -1008,7 +1007,6 @@ __device__ __forceinline__ void rows_out(const WalkArgs& a, uint64_t* buf, int c
     const int U = ne / S;  // store units per row
     const int total = 64 * U;
     const int nb = a.pk_nb, rb = a.pk_rb;
-    const uint64_t nmask = (1ull << nb) - 1, rmask = (1ull << rb) - 1;
     const int soff = (Arr == 2 ? 1 : 0) - c0;  // buffer entry of element i: i + soff
     // one round at a time: unrolled rounds hold more registers than the 4
     // waves per SIMD the LDS allows (and were not faster unrolled 2, 4 or 8
@@ -1025,11 +1023,9 @@ __device__ __forceinline__ void rows_out(const WalkArgs& a, uint64_t* buf, int c
         auto value = [&](int i) -> int64_t {
             const int slot = i + (Arr == 2 ? 1 : 0);
             const uint64_t word = buf[(i + soff) * kRowStride + j];
-            if (Arr == 0) return slot < lj ? static_cast<int32_t>(word & nmask) : a.pad;
-            if (Arr == 2) return slot < lj ? static_cast<int64_t>(word >> (nb + rb)) : -1;
-            if (slot >= lj) return -1;
-            const uint64_t r = (word >> nb) & rmask;
-            return r == rmask ? a.start_ts : a.uniq_ts[r];
+            if (Arr == 0) return slot < lj ? word_node(word, nb) : a.pad;
+            if (Arr == 2) return slot < lj ? word_eid(word, nb, rb) : -1;
+            return slot < lj ? word_ts(word, nb, rb, a.uniq_ts, a.edge_ts, a.start_ts) : -1;
         };
         if (vec) {
             if (Arr == 0) {
@@ -1116,14 +1112,12 @@ __global__ __launch_bounds__(kB) void walk_rows_kernel(WalkGraph g, WalkArgs a) 
             const int k = c0 + j;
             uint64_t word;
             if (k == 0) {
-                word = static_cast<uint64_t>(static_cast<uint32_t>(s0.first)) |
-                       (((1ull << rb) - 1) << nb);
+                word = first_word(nb, s0.first);
                 len = 1;
                 alive = L > 1 && cur != a.pad;
             } else {
-                word = static_cast<uint64_t>(static_cast<uint32_t>(cur)) |
-                       (static_cast<uint64_t>(static_cast<uint32_t>(cur_r)) << nb) |
-                       (static_cast<uint64_t>(static_cast<uint32_t>(cur_e)) << (nb + rb));
+                word = slot_word(nb, rb, cur, static_cast<uint32_t>(cur_r),
+                                 static_cast<uint32_t>(cur_e));
                 len = k + 1;
                 if (k == L - 1) {
                     alive = false;  // the reference's last selection cannot change the output
@@ -1158,114 +1152,19 @@ __global__ __launch_bounds__(kB) void walk_rows_kernel(WalkGraph g, WalkArgs a) 
     if (live) a.lens[w] = static_cast<uint64_t>(len);
 }
 
-// walk_wave_weights' walks (the weight family, the wave sharing its weight
-// searches), forward, written as output rows: the same chunked loop as
-// walk_rows_kernel, every lane taking part in every slot's shared search.
-template <bool Fwd, int C>
-__device__ __forceinline__ void walk_wave_weights_rows(const WalkGraph& g, const WalkArgs& a,
-                                                       const double* em1, uint64_t* buf) {
-    const int lane = __lane_id();
-    const uint64_t q = a.q0 + grid_position(a.xcd_remap);
-    const bool live = q < a.q_end;
-    const uint64_t w = live ? (a.order ? a.order[q] : q) : 0;
-    const int L = a.L;  // >= 1 (the host launches it only then)
-    const int32_t cut = live ? cutoff_rank(g, a, w) : -1;
-    const int32_t neg1 = *g.neg1_rank;
-    const StartState s0 = live ? a.st[w] : StartState{-1, -1, -1, -1};
-    int cur = s0.cur;
-    int32_t cur_r = s0.r, cur_e = s0.e;
-    bool alive = live && s0.e != -1;  // the walk writes its next slot
-    int len = 0;
-    const int nb = a.pk_nb, rb = a.pk_rb;
-    for (int c0 = 0; c0 < L; c0 += C) {
-        const int n = min(C, L - c0);
-        for (int j = 0; j < n; ++j) {
-            const int k = c0 + j;
-            WeightHop hs{true, false, 0, 0, 0, 0, 0, 0, nullptr, 0.0};
-            double re = 0.0;
-            bool hop = false;  // the lane selects a hop after slot k
-            if (alive) {
-                uint64_t word;
-                if (k == 0) {
-                    word = static_cast<uint64_t>(static_cast<uint32_t>(s0.first)) |
-                           (((1ull << rb) - 1) << nb);
-                    len = 1;
-                    alive = L > 1 && cur != a.pad;
-                } else {
-                    word = static_cast<uint64_t>(static_cast<uint32_t>(cur)) |
-                           (static_cast<uint64_t>(static_cast<uint32_t>(cur_r)) << nb) |
-                           (static_cast<uint64_t>(static_cast<uint32_t>(cur_e)) << (nb + rb));
-                    len = k + 1;
-                    if (k == L - 1) {
-                        alive = false;  // the reference's last selection cannot change the output
-                    } else {
-                        const bool ok = cur >= 0 && cur < g.active_size;
-                        const uint32_t u = ok ? static_cast<uint32_t>(cur) : 0u;
-                        const NodeHdr hd = g.d.hdr[u];
-                        const DrawPair r = draw_pair(a.ds, w, static_cast<uint32_t>(k) + 1);
-                        hs = weight_hop_begin<Fwd>(g, a.walk_bias, u, ok, hd,
-                                                   cur_r == neg1 ? -1 : cur_r, cut, r.a, em1);
-                        re = r.b;
-                        if (hs.fail) alive = false;
-                        else hop = true;
-                    }
-                }
-                buf[j * kRowStride + lane] = word;
-            }
-            const uint32_t kk = wave_weight_lower_bound(hs.need, g.d.w + hs.gb, hs.G, hs.lv,
-                                                        hs.target, g.d.w);
-            if (hop) {
-                uint32_t gpos = hs.gpos;
-                if (hs.need) {
-                    const uint32_t x = hs.gb + kk;
-                    gpos = x < hs.gs ? hs.gs : (x > hs.gse ? hs.gse : x);
-                }
-                const Hop h = hop_from_group(g, gpos, hs.ge, re);
-                if (h.e == -1 || h.r == neg1) {
-                    alive = false;
-                } else {
-                    cur = h.nbr;
-                    cur_r = h.r;
-                    cur_e = h.e;
-                    alive = cur != a.pad;
-                }
-            }
-        }
-        rows_flush<C>(a, buf, c0, n, static_cast<uint32_t>(w), len, live, lane);
-    }
-    if (live) a.lens[w] = static_cast<uint64_t>(len);
-}
-
-template <bool Fwd, bool Dir, int Fam, int C>
-__global__ __launch_bounds__(kB) void walk_weights_rows_kernel(WalkGraph g, WalkArgs a) {
-    static_assert(Fam == kFamWeight && Fwd, "the weight family's forward row writer");
-    __shared__ double s_xt[kExpTables];
-    __shared__ uint64_t s_slots[(kB / 64) * C * kRowStride];
-    const bool use_xt = a.walk_bias == kExponentialIndex;
-    if (use_xt) {
-        fill_exp_tables(s_xt, threadIdx.x, kB);
-        __syncthreads();
-    }
-    walk_wave_weights_rows<Fwd, C>(g, a, use_xt ? s_xt : nullptr,
-                                   s_slots + (threadIdx.x >> 6) * C * kRowStride);
-}
-
-// The row-writing walk kernel of a picker family (kFamIndex, kFamWeight or
-// kFamAny), forward.
-void launch_rows(bool directed, int family, dim3 grid, hipStream_t s, const WalkGraph& g,
+// The row-writing walk kernel of the index family (index_only) or of any
+// picker, forward.  (A row writer for the ExponentialWeight family, its wave
+// sharing the weight searches, measured slower than scratch and the layout
+// pass at cfg4: walk kernel 161.0 ms against 138.8 + 19.8 ms.  That kernel is
+// bound by its searches' loads, and the flush's stores queue behind them.)
+void launch_rows(bool directed, bool index_only, dim3 grid, hipStream_t s, const WalkGraph& g,
                  const WalkArgs& a) {
     constexpr int C = kRowSlots;
-#define TRW_ROWS(K, D, F) hipLaunchKernelGGL((K<true, D, F, C>), grid, dim3(kB), 0, s, g, a)
-    if (family == kFamIndex) {
-        if (directed) TRW_ROWS(walk_rows_kernel, true, kFamIndex);
-        else TRW_ROWS(walk_rows_kernel, false, kFamIndex);
-    } else if (family == kFamWeight) {
-        if (directed) TRW_ROWS(walk_weights_rows_kernel, true, kFamWeight);
-        else TRW_ROWS(walk_weights_rows_kernel, false, kFamWeight);
-    } else {
-        if (directed) TRW_ROWS(walk_rows_kernel, true, kFamAny);
-        else TRW_ROWS(walk_rows_kernel, false, kFamAny);
-    }
+#define TRW_ROWS(D, F) hipLaunchKernelGGL((walk_rows_kernel<true, D, F, C>), grid, dim3(kB), 0, s, g, a)
+    if (directed && index_only) TRW_ROWS(true, kFamIndex);
+    else if (directed) TRW_ROWS(true, kFamAny);
+    else if (index_only) TRW_ROWS(false, kFamIndex);
+    else TRW_ROWS(false, kFamAny);
 #undef TRW_ROWS
 }
 
@@ -1410,42 +1309,35 @@ __global__ __launch_bounds__(kB) void node_group_segment_kernel(
     emit_live(keep, static_cast<uint32_t>(s.cur), w, keys, vals, count);
 }
 
-// Layout pass: slot-major scratch [K][n] -> the row-major output [n][K] the
-// reference returns, for all three walk arrays in one pass.  Values become the
-// reference's types on the way: nodes are copied, a timestamp rank becomes the
-// timestamp (uniq_ts; kStartRank becomes the first slot's sentinel), a 32-bit
-// edge id is widened.  `count` of walk w is its number of written slots (len
-// for nodes and timestamps, len - 1 for edge ids); slots at or beyond it get
-// the padding (data/walk_set/walk_set_host.cu:25-29).  Backward walks come
-// out reversed into chronological order (data/walk_set/walk_set_view.cuh:
-// 50-80).
+// Layout pass: slot-major scratch [L][n] -> the row-major output arrays the
+// reference returns ([n][L] nodes and timestamps, [n][L - 1] edge ids), in
+// one pass.  Values become the reference's types on the way: nodes are
+// copied, a slot's time becomes its timestamp (word_ts), a 32-bit edge id is
+// widened.  `count` of walk w is its number of written slots (len for nodes
+// and timestamps, len - 1 for edge ids); slots at or beyond it get the
+// padding (data/walk_set/walk_set_host.cu:25-29).  Backward walks come out
+// reversed into chronological order (data/walk_set/walk_set_view.cuh:50-80).
 //
 // A workgroup owns 64 consecutive scratch columns and a chunk of slots -- the
-// whole row when L <= kLayoutPackedMaxSlots (packed scratch) or
-// kLayoutMaxSlots (three arrays).  Packed scratch is read once, in 64-column
-// runs of one slot (512 B, coalesced), into an LDS tile of 64-bit words from
-// which the three arrays are written; three-array scratch is read per array
-// (256-byte runs) into a 32-bit tile reused by the arrays.  Each wave then
-// writes whole rows, converting as it writes (a walk's ranks increase along
-// its row, so the timestamp lookups of one row are close together).  Column q holds walk
-// order[q] when the walks ran in another order than their ids; its row goes to
-// that walk's place.  In walk-id order the 64 rows are one contiguous span of
-// the output, so no cache line is shared with another workgroup.  Scratch is
-// read and output written once, with non-temporal hints.
+// whole row when L <= kLayoutPackedMaxSlots.  The scratch is read once, in
+// 64-column runs of one slot (512 B, coalesced), into an LDS tile of 64-bit
+// words from which the three arrays are written.  Each wave then writes whole
+// rows, converting as it writes (a walk's ranks increase along its row, so
+// the timestamp lookups of one row are close together).  Column q holds walk
+// order[q] when the walks ran in another order than their ids; its row goes
+// to that walk's place.  In walk-id order the 64 rows are one contiguous span
+// of the output, so no cache line is shared with another workgroup.  Scratch
+// is read and output written once, with non-temporal hints.
 constexpr int kLayoutWalks = 64;
 static_assert(kLayoutWalks == kScratchTile, "a layout workgroup owns one scratch tile");
-constexpr int kLayoutMaxSlots = 128;  // tile <= 33 KB of LDS
 // 64-bit tile <= 64 KB of LDS.  A row split into chunks costs more than the
 // occupancy a smaller tile buys: 80-slot rows in two chunks of 40 were
 // measured 1.3 ms slower over 10M walks than in one.
 constexpr int kLayoutPackedMaxSlots = 120;
 
 struct LayoutArgs {
-    const int32_t* sn;   // scratch nodes
-    const uint32_t* sr;  // scratch timestamp ranks
-    const uint32_t* se;  // scratch edge ids
-    const uint64_t* sp;  // packed scratch (replaces the three above when set)
-    int pk_nb, pk_rb;    // its node and rank field widths
+    const uint64_t* sp;  // scratch slot words
+    int pk_nb, pk_rb;    // their node and rank field widths
     int32_t* on;
     int64_t* ot;
     int64_t* oe;
@@ -1455,6 +1347,7 @@ struct LayoutArgs {
     int reverse;
     int32_t pad;
     const int64_t* uniq_ts;
+    const int64_t* edge_ts;
     int64_t start_ts;
     const uint32_t* order;  // walk of each scratch column (nullptr: the column index)
     uint64_t q0, q_end;     // scratch columns [q0, q_end) of this launch (q0 % 64 == 0)
@@ -1465,23 +1358,24 @@ struct LayoutArgs {
     uint32_t fv;
 };
 
-
-// Value of output slot i of a row whose first `cw` slots were written (x: the
-// scratch value).  Arr 0: nodes, 1: timestamps, 2: edge ids.
+// Value of output slot i of a row whose first `cw` slots were written (v: the
+// slot word of the slot the value comes from).  Arr 0: nodes, 1: timestamps,
+// 2: edge ids.
 template <int Arr>
-__device__ __forceinline__ int64_t layout_value(const LayoutArgs& a, uint32_t x, int i, int cw) {
-    if (Arr == 0) return i < cw ? static_cast<int32_t>(x) : a.pad;
-    if (Arr == 1) return i >= cw ? -1 : (x == kStartRank ? a.start_ts : a.uniq_ts[x]);
-    return i < cw ? static_cast<int64_t>(x) : -1;
+__device__ __forceinline__ int64_t layout_value(const LayoutArgs& a, uint64_t v, int i, int cw) {
+    if (Arr == 0) return i < cw ? word_node(v, a.pk_nb) : a.pad;
+    if (Arr == 1)
+        return i < cw ? word_ts(v, a.pk_nb, a.pk_rb, a.uniq_ts, a.edge_ts, a.start_ts) : -1;
+    return i < cw ? word_eid(v, a.pk_nb, a.pk_rb) : -1;
 }
 
 // Writes the chunk's output rows of one array: each wave owns whole rows and
-// converts values as it writes them.  src_at(wl2, n, cw, i) is the 32-bit
-// scratch value of output slot i of tile column wl2, whose walk wrote n node
-// slots and has cw slots of this array's chunk below its count.
+// converts values as it writes them.  word_at(wl2, n, cw, i) is the slot word
+// output slot i of tile column wl2 comes from, whose walk wrote n node slots
+// and has cw slots of this array's chunk below its count.
 template <int Arr, class Src>
 __device__ __forceinline__ void layout_rows(const LayoutArgs& a, const int* cnt, const uint32_t* row,
-                                            uint64_t w0, int k0, Src src_at) {
+                                            uint64_t w0, int k0, Src word_at) {
     const int K = Arr == 2 ? a.L - 1 : a.L;
     const int kc = min(a.C, K - k0);
     if (kc <= 0) return;  // uniform over the workgroup
@@ -1505,22 +1399,19 @@ __device__ __forceinline__ void layout_rows(const LayoutArgs& a, const int* cnt,
         const uint64_t base = static_cast<uint64_t>(row[wl2]) * static_cast<uint64_t>(K) + k0;
         const int n = cnt[wl2];
         const int cw = n - (Arr == 2 ? 1 : 0) - k0;  // slots of the row below the count
-        auto src = [&](int x) { return src_at(wl2, n, cw, x); };
+        auto val = [&](int x) { return layout_value<Arr>(a, word_at(wl2, n, cw, x), x, cw); };
         if (vec) {
             if (Arr == 0) {
-                const i32x4 o = {static_cast<int32_t>(layout_value<0>(a, src(i), i, cw)),
-                                 static_cast<int32_t>(layout_value<0>(a, src(i + 1), i + 1, cw)),
-                                 static_cast<int32_t>(layout_value<0>(a, src(i + 2), i + 2, cw)),
-                                 static_cast<int32_t>(layout_value<0>(a, src(i + 3), i + 3, cw))};
+                const i32x4 o = {static_cast<int32_t>(val(i)), static_cast<int32_t>(val(i + 1)),
+                                 static_cast<int32_t>(val(i + 2)), static_cast<int32_t>(val(i + 3))};
                 __builtin_nontemporal_store(o, reinterpret_cast<i32x4*>(a.on + base + i));
             } else {
-                const i64x2 o = {layout_value<Arr>(a, src(i), i, cw),
-                                 layout_value<Arr>(a, src(i + 1), i + 1, cw)};
+                const i64x2 o = {val(i), val(i + 1)};
                 int64_t* out = Arr == 1 ? a.ot : a.oe;
                 __builtin_nontemporal_store(o, reinterpret_cast<i64x2*>(out + base + i));
             }
         } else {
-            const int64_t y = layout_value<Arr>(a, src(i), i, cw);
+            const int64_t y = val(i);
             if (Arr == 0) __builtin_nontemporal_store(static_cast<int32_t>(y), a.on + base + i);
             else if (Arr == 1) __builtin_nontemporal_store(y, a.ot + base + i);
             else __builtin_nontemporal_store(y, a.oe + base + i);
@@ -1532,7 +1423,6 @@ __device__ __forceinline__ void layout_rows(const LayoutArgs& a, const int* cnt,
         const uint64_t base = static_cast<uint64_t>(row[wl2]) * static_cast<uint64_t>(K) + k0;
         const int n = cnt[wl2];
         const int cw = n - 1 - k0;
-        auto src = [&](int x) { return src_at(wl2, n, cw, x); };
         // the slots' edge features (finalize_host_walks,
         // walks_with_edge_features_host.cuh:44-62), from the edge ids in
         // the tile: row [slot][dim] of the walk, zeros past the count
@@ -1544,56 +1434,13 @@ __device__ __forceinline__ void layout_rows(const LayoutArgs& a, const int* cnt,
             const int i = static_cast<int>(t / fv);
             const uint32_t c = t - static_cast<uint32_t>(i) * fv;
             f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (i < cw) v = __builtin_nontemporal_load(feat + static_cast<uint64_t>(src(i)) * fv + c);
+            if (i < cw) {
+                const uint64_t e = static_cast<uint64_t>(word_eid(word_at(wl2, n, cw, i), a.pk_nb, a.pk_rb));
+                v = __builtin_nontemporal_load(feat + e * fv + c);
+            }
             __builtin_nontemporal_store(v, of + t);
         }
     }
-}
-
-template <int Arr>
-__device__ __forceinline__ void layout_array(const LayoutArgs& a, uint32_t* tile, const int* cnt,
-                                             const uint32_t* row, uint64_t w0, int k0) {
-    const int K = Arr == 2 ? a.L - 1 : a.L;
-    const int kc = min(a.C, K - k0);
-    if (kc <= 0) return;  // uniform over the workgroup
-    constexpr int P = kLayoutWalks + 1;
-    const int tid = threadIdx.x;
-    const int wl = tid & 63, srow = tid >> 6;
-    const uint64_t w = w0 + wl;
-    int c = cnt[wl] - (Arr == 2 ? 1 : 0);
-    c = c > 0 ? c : 0;
-    // A reversed row held whole by the tile (one chunk) is read in slot order
-    // -- every load a 256-byte run -- and reversed on its way out of LDS; rows
-    // laid out in several chunks read their reversed slots directly.
-    const bool whole = k0 == 0 && kc == K;
-    const bool rev_in = a.reverse && !whole;
-    // slots at or past the count are not read; the writer pads them
-    const uint32_t* in = Arr == 0 ? reinterpret_cast<const uint32_t*>(a.sn) : (Arr == 1 ? a.sr : a.se);
-    in += w0 * static_cast<uint64_t>(K);  // w0 % kScratchTile == 0
-    for (int j0 = 0; j0 < kc; j0 += 32) {
-        uint32_t v[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int r = j0 + srow + 4 * j;
-            const int k = k0 + r;
-            uint32_t x = 0;
-            if (r < kc && w < a.q_end && k < c)
-                x = __builtin_nontemporal_load(in + static_cast<uint64_t>(rev_in ? c - 1 - k : k) * kScratchTile + wl);
-            v[j] = x;
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int r = j0 + srow + 4 * j;
-            if (r < kc) tile[r * P + wl] = v[j];
-        }
-    }
-    __syncthreads();
-    const bool rev_out = a.reverse && whole;
-    // tile slot of output slot i (reversed rows: slot cw - 1 - i)
-    layout_rows<Arr>(a, cnt, row, w0, k0, [&](int wl2, int, int cw, int i) {
-        return tile[(rev_out && i < cw ? cw - 1 - i : i) * P + wl2];
-    });
-    __syncthreads();
 }
 
 // Loads the walk count and destination row of the workgroup's 64 columns.
@@ -1607,36 +1454,12 @@ __device__ __forceinline__ void layout_columns(const LayoutArgs& a, uint64_t w0,
     __syncthreads();
 }
 
-__global__ __launch_bounds__(256) void layout_walks_kernel(LayoutArgs a) {
-    extern __shared__ uint32_t layout_lds[];
-    uint32_t* tile = layout_lds;
-    int* cnt = reinterpret_cast<int*>(layout_lds + a.C * (kLayoutWalks + 1));
-    uint32_t* row = reinterpret_cast<uint32_t*>(cnt + kLayoutWalks);
-    const uint64_t w0 = a.q0 + static_cast<uint64_t>(blockIdx.x) * kLayoutWalks;
-    const int k0 = blockIdx.y * a.C;
-    layout_columns(a, w0, cnt, row);
-    layout_array<0>(a, tile, cnt, row, w0, k0);
-    layout_array<1>(a, tile, cnt, row, w0, k0);
-    layout_array<2>(a, tile, cnt, row, w0, k0);
-}
-
-// Field of a packed scratch word: the node, the rank (all ones: the first
-// slot's sentinel, kStartRank) or the id of the edge into the slot.
-template <int Arr>
-__device__ __forceinline__ uint32_t packed_field(const LayoutArgs& a, uint64_t word) {
-    if (Arr == 2) return static_cast<uint32_t>(word >> (a.pk_nb + a.pk_rb));
-    const int sh = Arr == 0 ? 0 : a.pk_nb;
-    const uint64_t m = (1ull << (Arr == 0 ? a.pk_nb : a.pk_rb)) - 1;
-    const uint64_t f = (word >> sh) & m;
-    return Arr == 1 && f == m ? kStartRank : static_cast<uint32_t>(f);
-}
-
-// Layout pass over packed scratch: the chunk's words are read once into an
-// LDS tile of 64-bit words and all three arrays are written from it.  Tile
-// row r holds slot k0 + r (slot n - 1 - (k0 + r) for the reversed rows of a
-// walk laid out in several chunks), plus, for forward rows, slot k0 + kc:
-// the edge id of output slot i is in slot i + 1, the slot the edge reached;
-// reversed rows find it in the same word as their node.
+// The chunk's words are read once into an LDS tile of 64-bit words and all
+// three arrays are written from it.  Tile row r holds slot k0 + r (slot
+// n - 1 - (k0 + r) for the reversed rows of a walk laid out in several
+// chunks), plus, for forward rows, slot k0 + kc: the edge id of output slot i
+// is in slot i + 1, the slot the edge reached; reversed rows find it in the
+// same word as their node.
 __global__ __launch_bounds__(256) void layout_packed_kernel(LayoutArgs a) {
     constexpr int P = kLayoutWalks + 1;
     extern __shared__ uint64_t layout_lds64[];
@@ -1676,14 +1499,14 @@ __global__ __launch_bounds__(256) void layout_packed_kernel(LayoutArgs a) {
     // node and timestamp of output slot i: tile row i (reversed whole rows: n - 1 - i)
     auto node_row = [&](int n, int cw, int i) { return rev_out && i < cw ? n - 1 - i : i; };
     layout_rows<0>(a, cnt, row, w0, k0, [&](int wl2, int n, int cw, int i) {
-        return packed_field<0>(a, tile[node_row(n, cw, i) * P + wl2]);
+        return tile[node_row(n, cw, i) * P + wl2];
     });
     layout_rows<1>(a, cnt, row, w0, k0, [&](int wl2, int n, int cw, int i) {
-        return packed_field<1>(a, tile[node_row(n, cw, i) * P + wl2]);
+        return tile[node_row(n, cw, i) * P + wl2];
     });
     layout_rows<2>(a, cnt, row, w0, k0, [&](int wl2, int n, int cw, int i) {
         const int r = a.reverse ? node_row(n, cw, i) : i + 1;
-        return packed_field<2>(a, tile[r * P + wl2]);
+        return tile[r * P + wl2];
     });
 }
 
@@ -2067,45 +1890,36 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
     const uint64_t eslots = nw * static_cast<uint64_t>(L > 0 ? L - 1 : 0);
     // scratch: whole tiles of kScratchTile walks
     const uint64_t padded = (nw + kScratchTile - 1) / kScratchTile * kScratchTile;
-    // packed scratch when a node id (in [0, max_node_id], as the node index
-    // requires), a rank below T with the all-ones value free for the start
-    // sentinel, and an edge id below E fit in one 64-bit word
+    // slot words (slot_word): node id (in [0, max_node_id], as the node index
+    // requires), the rank of the slot's time (below T, the all-ones value free
+    // for the first slot) and the id of the edge into the slot (below E), or,
+    // when the three do not fit in 64 bits, node and edge id alone (rank
+    // field width 0; the edge field's all-ones value marks the first slot)
     auto bit_length = [](uint64_t v) { return v ? 64 - __builtin_clzll(v) : 0; };
     const int pk_nb = std::max(1, bit_length(static_cast<uint64_t>(std::max(max_node_id, 0))));
-    const int pk_rb = bit_length(T);
-    const int pk_eb = E ? bit_length(E - 1) : 0;
-    const bool packed = E > 0 && max_node_id >= 0 && pk_nb + pk_rb + pk_eb <= 64 && pk_nb + pk_rb < 64;
+    const int rank_bits = bit_length(T);
+    const bool with_rank = T > 0 && pk_nb + rank_bits + (E ? bit_length(E - 1) : 0) <= 64;
+    const int pk_rb = with_rank ? rank_bits : 0;
+    if (!with_rank && pk_nb + bit_length(E) >= 64)
+        throw std::runtime_error("node ids and edge ids do not fit a slot word");
     // no walks until every output buffer is sized: a failed allocation
     // below leaves an empty walk set, not a count over released buffers
     w_num = 0;
     w_len = 0;
     w_feat.n = 0;
     uint64_t* sc_packed = nullptr;
-    int32_t* sc_nodes = nullptr;
-    uint32_t *sc_rank = nullptr, *sc_eids = nullptr;
-    // forward walks whose slots pack: the walk kernel writes the output rows
-    // itself (walk_rows_kernel, walk_weights_rows_kernel)
-    const bool rows_direct = p.walk_layout == TRW_LAYOUT_AUTO && packed && forward && L > 0 &&
-                             nw <= 0xffffffffull && p.walk_order != TRW_ORDER_NODE_GROUPED;
+    // forward walks of the index pickers or node2vec: the walk kernel writes
+    // the output rows itself (walk_rows_kernel); the others go through
+    // scratch and the layout pass
+    const bool weight_family = !(is_index_picker(walk_bias) && is_index_picker(start_bias)) &&
+                               walk_bias != kTemporalNode2Vec;
+    const bool rows_direct = p.walk_layout == TRW_LAYOUT_AUTO && forward && !weight_family &&
+                             L > 0 && nw <= 0xffffffffull &&
+                             p.walk_order != TRW_ORDER_NODE_GROUPED;
     if (rows_direct) {
-        if (!into) {
-            sw_nodes.release();
-            sw_rank.release();
-            sw_eids.release();
-            sw_packed.release();
-        }
-    } else if (packed) {
-        if (!into) {
-            sw_nodes.release();
-            sw_rank.release();
-            sw_eids.release();
-        }
-        sc_packed = sp.take(sw_packed, padded * L);
-    } else {
         if (!into) sw_packed.release();
-        sc_nodes = sp.take(sw_nodes, padded * L);
-        sc_rank = sp.take(sw_rank, padded * L);
-        sc_eids = sp.take(sw_eids, padded * (L > 0 ? L - 1 : 0));
+    } else {
+        sc_packed = sp.take(sw_packed, padded * L);
     }
     // outputs: the engine's buffers, or the caller's
     int32_t* o_nodes;
@@ -2131,7 +1945,6 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
     w_len = L;
     w_dir_forward = forward ? 1 : 0;
     w_constrained = have_starts ? 1 : 0;
-    w_packed = packed ? 1 : 0;
     w_rows = rows_direct ? 1 : 0;
     w_replay = p.replay_draws ? 1 : 0;
 
@@ -2201,11 +2014,8 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
     a.cutoffs = have_cutoffs ? a_cutoffs : nullptr;
     a.n = nw;
     a.ds = ds;
-    a.nodes = sc_nodes;
-    a.ranks = sc_rank;
     a.lens = o_lens;
-    a.eids = sc_eids;
-    a.packed = packed ? sc_packed : nullptr;
+    a.packed = sc_packed;
     a.pk_nb = pk_nb;
     a.pk_rb = pk_rb;
 
@@ -2323,10 +2133,10 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
         a.ot = o_ts;
         a.oe = o_eids;
         a.uniq_ts = uniq_ts.p;
+        a.edge_ts = ts.p;
         a.start_ts = INT64_MIN;
         const dim3 grid(grid_for(nw));
-        launch_rows(cfg.is_directed,
-                    index_only ? kFamIndex : (no_node2vec ? kFamWeight : kFamAny), grid, s, g, a);
+        launch_rows(cfg.is_directed, index_only, grid, s, g, a);
         check_hip(hipGetLastError(), "walk kernel launch");
     } else if (nw) {
         a.q0 = 0;
@@ -2340,9 +2150,6 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
     check_hip(hipEventRecord(ev[6], s), "event");
     if (nw && L > 0 && !rows_direct) {
         LayoutArgs la{};
-        la.sn = sc_nodes;
-        la.sr = sc_rank;
-        la.se = sc_eids;
         la.sp = a.packed;
         la.pk_nb = pk_nb;
         la.pk_rb = pk_rb;
@@ -2351,12 +2158,12 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
         la.oe = o_eids;
         la.lens = o_lens;
         la.L = L;
-        const int max_slots = a.packed ? kLayoutPackedMaxSlots : kLayoutMaxSlots;
-        const int slot_chunks = (L + max_slots - 1) / max_slots;
+        const int slot_chunks = (L + kLayoutPackedMaxSlots - 1) / kLayoutPackedMaxSlots;
         la.C = (L + slot_chunks - 1) / slot_chunks;
         la.reverse = forward ? 0 : 1;
         la.pad = static_cast<int32_t>(cfg.walk_padding_value);
         la.uniq_ts = uniq_ts.p;
+        la.edge_ts = ts.p;
         la.start_ts = forward ? INT64_MIN : INT64_MAX;
         la.order = a.order;
         la.q0 = 0;
@@ -2370,14 +2177,10 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
             la.of = into ? into->feat : w_feat.p;
             la.fv = static_cast<uint32_t>(feat_dim / 4);
         }
-        const size_t tile = a.packed ? static_cast<size_t>(la.C + 1) * (kLayoutWalks + 1) * sizeof(uint64_t)
-                                     : static_cast<size_t>(la.C) * (kLayoutWalks + 1) * sizeof(uint32_t);
+        const size_t tile = static_cast<size_t>(la.C + 1) * (kLayoutWalks + 1) * sizeof(uint64_t);
         const size_t lds = tile + kLayoutWalks * (sizeof(int) + sizeof(uint32_t));
         const unsigned gx = static_cast<unsigned>((nw + kLayoutWalks - 1) / kLayoutWalks);
-        if (a.packed)
-            hipLaunchKernelGGL(layout_packed_kernel, dim3(gx, slot_chunks), dim3(256), lds, s, la);
-        else
-            hipLaunchKernelGGL(layout_walks_kernel, dim3(gx, slot_chunks), dim3(256), lds, s, la);
+        hipLaunchKernelGGL(layout_packed_kernel, dim3(gx, slot_chunks), dim3(256), lds, s, la);
         check_hip(hipGetLastError(), "layout launch");
     }
 
@@ -2437,12 +2240,11 @@ void walk_stats(Engine& e, trw_walk_stats* out) {
         nw && e.w_len > 0 ? nw * e.w_in_bytes_per_walk + e.w_index_bytes +
                                 (e.w_replay ? 16 * out->transitions : 0)
                           : 0;
-    // the kernel's slot writes: packed scratch words, three scratch arrays, or
-    // (rows written by the walk kernel) every output row in full
+    // the kernel's slot writes: scratch slot words, or (rows written by the
+    // walk kernel) every output row in full
     const uint64_t L = static_cast<uint64_t>(e.w_len);
     const uint64_t scratch =
-        e.w_rows ? nw * (4 * L + 8 * L + 8 * (L > 0 ? L - 1 : 0))
-                 : (e.w_packed ? 8 * out->total_len : 8 * out->total_len + 4 * out->transitions);
+        e.w_rows ? nw * (4 * L + 8 * L + 8 * (L > 0 ? L - 1 : 0)) : 8 * out->total_len;
     out->compulsory_write_bytes = nw ? 8 * nw + (e.w_len > 0 ? scratch : 0) : 0;
     out->rows_by_walk_kernel = static_cast<uint64_t>(e.w_rows);
 }

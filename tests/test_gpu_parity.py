@@ -546,10 +546,12 @@ def test_replay_walks_hub_with_more_groups_than_the_header_holds():
 def test_replay_walks_at_the_scratch_packing_limit(forward, e, n_ts):
     """Node ids up to 2^22 - 1 with E edges and n_ts distinct timestamps.
     66 bits: a node id, a rank and an edge id need 22 + 22 + 22 bits, more than
-    one 64-bit scratch word holds, so the walks go through the three 32-bit
-    scratch arrays (every smaller graph here packs them).  64 bits: 22 + 21 +
-    21 bits exactly fill the packed word -- the edge id in its top bits and
-    the largest rank one below the all-ones start sentinel."""
+    one 64-bit slot word holds, so the slot words hold node and edge id only
+    and a slot's timestamp is its edge's (every smaller graph here fits the
+    rank).  64 bits: 22 + 21 + 21 bits exactly fill the slot word -- the edge
+    id in its top bits and the largest rank one below the all-ones start
+    sentinel.  Both through rows written by the walk kernel (forward) and
+    through scratch and the layout pass."""
     rng = np.random.default_rng(95)
     ids = np.concatenate([[0, (1 << 22) - 1],
                           rng.choice(np.arange(1, (1 << 22) - 1), 6_000, replace=False)])
