@@ -581,6 +581,26 @@ __global__ __launch_bounds__(kB) void walk_start_kernel(WalkGraph g, WalkArgs a,
     vals[w] = static_cast<uint32_t>(w);
 }
 
+// The same keys for unconstrained starts of an index picker, without the
+// start states: start_edge picks timestamp group idx from the walk's first
+// draw alone, a group is never empty, and the start edge's time has rank idx.
+// The walk kernel then finds the start edge itself (walk_start).
+template <bool Fwd>
+__global__ __launch_bounds__(kB) void walk_start_keys_kernel(WalkGraph g, WalkArgs a,
+                                                             uint32_t* __restrict__ keys,
+                                                             uint32_t* __restrict__ vals,
+                                                             uint32_t none) {
+    const uint64_t w = blockIdx.x * static_cast<uint64_t>(kB) + threadIdx.x;
+    if (w >= a.n) return;
+    uint32_t key = none;
+    if (g.E != 0 && g.T != 0) {
+        const int idx = pick_index(a.start_bias, 0, static_cast<int>(g.T), !Fwd, draw_slot0(a.ds, w));
+        if (idx != -1 && static_cast<uint32_t>(idx) < g.T) key = static_cast<uint32_t>(idx);
+    }
+    keys[w] = key;
+    vals[w] = static_cast<uint32_t>(w);
+}
+
 // Workgroup b runs on XCD b % 8 (round-robin dispatch).  With the remap, XCD
 // x runs the x-th contiguous slice of the grid's positions, so the walks
 // resident on one XCD -- and sharing its L2 -- are neighbours in the order.
@@ -797,7 +817,7 @@ __device__ __forceinline__ WeightHop weight_hop_begin(const WalkGraph& g, int pi
 // shared by the wave: a lane whose walk has ended (or that has no walk) keeps
 // taking part until every walk of its wave has, so the loop's control is
 // wave-uniform around the shared search.  Same walks as walk_kernel's loop.
-template <bool Fwd>
+template <bool Fwd, bool Dir>
 __device__ __forceinline__ void walk_wave_weights(const WalkGraph& g, const WalkArgs& a,
                                                   const double* em1) {
     const uint64_t q = a.q0 + grid_position(a.xcd_remap);
@@ -807,7 +827,9 @@ __device__ __forceinline__ void walk_wave_weights(const WalkGraph& g, const Walk
     SlotWriter out(a, q);
     const int32_t cut = in_range ? cutoff_rank(g, a, w) : -1;
     const int32_t neg1 = *g.neg1_rank;
-    const StartState s0 = in_range ? a.st[w] : StartState{-1, -1, -1, -1};
+    // the start state from the pre-pass, or found here
+    const StartState s0 = !in_range ? StartState{-1, -1, -1, -1}
+                                    : (a.st ? a.st[w] : walk_start<Fwd, Dir, kFamWeight>(g, a, w, cut));
     int cur = s0.cur;
     int32_t cur_r = s0.r, cur_e = s0.e;
     int len = 0, walk_len = 1;
@@ -873,7 +895,7 @@ __global__ __launch_bounds__(kB) void walk_weights_kernel(WalkGraph g, WalkArgs 
         __syncthreads();
     }
     if (a.L > 0) {  // uniform
-        walk_wave_weights<Fwd>(g, a, use_xt ? s_xt : nullptr);
+        walk_wave_weights<Fwd, Dir>(g, a, use_xt ? s_xt : nullptr);
         return;
     }
     const uint64_t q = a.q0 + grid_position(a.xcd_remap);
@@ -907,7 +929,8 @@ __global__ __launch_bounds__(kB) void walk_kernel(WalkGraph g, WalkArgs a) {
     // the reference's tests of a current time of -1, on ranks
     const int32_t neg1 = *g.neg1_rank;
 
-    const StartState s0 = a.st[w];
+    // the start state from the pre-pass, or found here
+    const StartState s0 = a.st ? a.st[w] : walk_start<Fwd, Dir, Fam>(g, a, w, cut);
     const int first = s0.first;
     int cur = s0.cur;
     int32_t cur_r = s0.r, cur_e = s0.e;
@@ -1099,7 +1122,9 @@ __global__ __launch_bounds__(kB) void walk_rows_kernel(WalkGraph g, WalkArgs a) 
     const int L = a.L;  // >= 1 (the host launches it only then)
     const int32_t cut = live ? cutoff_rank(g, a, w) : -1;
     const int32_t neg1 = *g.neg1_rank;
-    const StartState s0 = live ? a.st[w] : StartState{-1, -1, -1, -1};
+    // the start state from the pre-pass, or found here
+    const StartState s0 = !live ? StartState{-1, -1, -1, -1}
+                                : (a.st ? a.st[w] : walk_start<Fwd, Dir, Fam>(g, a, w, cut));
     int cur = s0.cur, prev = -1;
     int32_t cur_r = s0.r, cur_e = s0.e;
     bool alive = live && s0.e != -1;  // the walk writes its next slot
@@ -2067,13 +2092,32 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
         throw InvalidArgument("Invalid walk order");
     const bool node_grouped = order_mode == TRW_ORDER_NODE_GROUPED && nw > 1 && L > 1;
     if (nw && L > 0) {
-        StartState* st = reinterpret_cast<StartState*>(sp.take(walk_st, 4 * nw));
-        uint32_t* ka = sp.take(k32a, nw);
-        uint32_t* va = sp.take(v32a, nw);
         const uint32_t none = g.T;  // past every rank: walks without a start run last
-        TRW_LAUNCH(walk_start_kernel, dim3(grid_for(nw)), g, a, st, ka, va, none);
-        a.st = st;
-        if (order_mode == TRW_ORDER_START_TIME && nw > 1 && L > 1 && !node_grouped) {
+        const bool sorted = order_mode == TRW_ORDER_START_TIME && nw > 1 && L > 1 && !node_grouped;
+        // The start states come from a pre-pass where the order needs them (or
+        // its keys need the index); unconstrained starts of an index picker
+        // need only keys, and walks in walk-id order no pre-pass: the walk
+        // kernel finds their start edges itself.
+        const bool keys_only = !have_starts && is_index_picker(start_bias);
+        uint32_t* ka = nullptr;
+        uint32_t* va = nullptr;
+        if (node_grouped || (sorted && !keys_only)) {
+            StartState* st = reinterpret_cast<StartState*>(sp.take(walk_st, 4 * nw));
+            ka = sp.take(k32a, nw);
+            va = sp.take(v32a, nw);
+            TRW_LAUNCH(walk_start_kernel, dim3(grid_for(nw)), g, a, st, ka, va, none);
+            a.st = st;
+        } else if (sorted) {
+            ka = sp.take(k32a, nw);
+            va = sp.take(v32a, nw);
+            if (forward)
+                hipLaunchKernelGGL(walk_start_keys_kernel<true>, dim3(grid_for(nw)), dim3(kB), 0, s,
+                                   g, a, ka, va, none);
+            else
+                hipLaunchKernelGGL(walk_start_keys_kernel<false>, dim3(grid_for(nw)), dim3(kB), 0, s,
+                                   g, a, ka, va, none);
+        }
+        if (sorted) {
             uint32_t* kb = sp.take(k32b, nw);
             uint32_t* vb = sp.take(v32b, nw);
             uint32_t* hi = sp.take(hist, radix_hist_elems(nw));
@@ -2085,7 +2129,12 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
         check_hip(hipGetLastError(), "walk start launch");
     }
 
-    w_in_bytes_per_walk = sizeof(StartState) + (a.order ? 4 : 0) + (have_cutoffs ? 8 : 0);
+    // a start state read per walk, or (starts found by the walk kernel) the
+    // walk's seed node, or the start edge's endpoints and the timestamp
+    // groups' offsets
+    w_in_bytes_per_walk = (a.st ? sizeof(StartState) : (have_starts ? 4 : 8)) +
+                          (a.order ? 4 : 0) + (have_cutoffs ? 8 : 0);
+    if (!a.st && !have_starts && nw && L > 0) w_index_bytes += tsg_off.bytes();
 
     // ---- walk kernel, then the layout pass.  (Running the layout of finished
     // grid chunks on a second stream beside the remaining walks was measured

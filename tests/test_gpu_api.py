@@ -482,10 +482,12 @@ def test_failed_ingest_leaves_an_empty_usable_engine(shift):
 def test_walk_stats_byte_accounting():
     """trw_get_walk_stats against numpy: steps, the per-hop demand bytes
     (72 + 8 ceil(log2(G_u + 1)) B with the reference's types) and the
-    compulsory bytes of the walk kernel (start states, processing order and
-    the sampled direction's index read once; lengths written once, and either
-    packed scratch or -- rows written by the walk kernel -- every output row
-    in full)."""
+    compulsory bytes of the walk kernel (processing order and the sampled
+    direction's index read once, and per walk its start edge's endpoints --
+    the kernel finds unconstrained starts of an index picker itself -- with
+    the timestamp groups' offsets, or the start state a pre-pass found;
+    lengths written once, and either scratch slot words or -- rows written by
+    the walk kernel -- every output row in full)."""
     from temporal_random_walk import capi
     s, d, t = graphs.powerlaw(5_000, 60_000, n_ts=2_000, seed=9)
     eng = capi.Engine(is_directed=True, shuffle_walk_order=False, global_seed=3)
@@ -511,7 +513,8 @@ def test_walk_stats_byte_accounting():
     g_o = eng.array("node_ts_group_outbound_offsets").size
     n_ent = eng.array("node_ts_sorted_outbound_indices").size
     index = 16 * vc + 4 * 2 * (g_o + vc) + 8 * (g_o + 1) + 8 * n_ent
-    assert st["compulsory_read_bytes"] == (16 + 4) * n + index
+    tsg = 4 * eng.array("timestamp_group_offsets").size
+    assert st["compulsory_read_bytes"] == (8 + 4) * n + index + tsg
     assert st["compulsory_write_bytes"] == 8 * n + 8 * lens.sum()
     # the same sample with the rows written by the walk kernel
     w2 = eng.sample("total", L, "ExponentialIndex", n, initial_edge_bias="Uniform")
