@@ -507,6 +507,39 @@ def test_replay_long_walks_span_layout_chunks(forward):
     assert lens.max() == 150 and (lens > 96).mean() > 0.5
 
 
+@pytest.mark.parametrize("forward", [True, False])
+def test_replay_walks_stop_at_the_padding_node(forward):
+    """The reference's walk loop runs while the current node differs from the
+    padding value (temporal_random_walk_cpu.cuh:93): a walk that reaches a
+    node whose id is the padding value ends there, without writing it.  Here
+    the padding value is the id of the node with the sixth most in-edges: it
+    cuts about 40 % of the walks short (against the same walks with padding
+    -1), and about a third still run to L; every order and both ways to the
+    rows."""
+    s, d, t = graphs.powerlaw(3_000, 60_000, s=1.7, n_ts=4_000, seed=61)
+    hub = int(np.argsort(-np.bincount(d), kind="stable")[5])
+    og = po.OracleGraph(True)
+    og.add_edges(s, d, t)
+    eng = _engine(is_directed=True, shuffle_walk_order=False, global_seed=1234,
+                  walk_padding_value=hub)
+    eng.add_edges(s, d, t)
+    L, n = 24, 70_000  # >= 2^16 walks: start-time order in the automatic choice
+    dr = graphs.draws(n, L, seed=62)
+    direction = "Forward_In_Time" if forward else "Backward_In_Time"
+    ref = og.walks(L, "ExponentialIndex", "Uniform", forward, -np.ones(n, np.int32), dr, pad=hub)
+    unpadded = og.walks(L, "ExponentialIndex", "Uniform", forward, -np.ones(n, np.int32), dr)
+    lens = ref.lens.astype(np.int64)
+    assert (lens < unpadded.lens.astype(np.int64)).mean() > 0.3 and (lens == L).mean() > 0.2
+    for order, layout in (("walk_id", "auto"), ("start_time", "auto"), ("start_time", "scratch"),
+                          ("node_grouped", "auto")):
+        got = eng.sample("total", L, "ExponentialIndex", n, initial_edge_bias="Uniform",
+                         direction=direction, replay=dr, shuffle=False, walk_order=order,
+                         walk_layout=layout)
+        for k in ("nodes", "timestamps", "lens", "edge_ids"):
+            np.testing.assert_array_equal(getattr(got, k), getattr(ref, k), err_msg=f"{order} {layout} {k}")
+    eng.close()
+
+
 def test_replay_walks_million_scale():
     """2^20 + a ragged remainder of walks (time-ordered by default at this
     size) against the oracle, forward and backward."""
