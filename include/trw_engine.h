@@ -248,14 +248,16 @@ trw_status trw_sample_device(void* handle, const trw_sample_params* params, trw_
  * graph capture, tight serving loops, harnesses that forbid allocation).
  *
  * On entry out->nodes, ->timestamps, ->walk_lens, ->edge_ids and, when the
- * store has edge features, ->edge_features point to device buffers with room
- * for capacity_walks walks (rows of max_walk_len, max_walk_len - 1 and
- * (max_walk_len - 1) * feature_dim values); on return num_walks, max_walk_len
- * and feature_dim are set.  Every per-call buffer (start arrays, draws,
- * processing order, walk scratch) comes from a fixed device array of
- * 128 MiB per device, held until the process ends: a sample needing more
- * (about 640 B per walk at max_walk_len 80, plus 50 B) or more walks than
- * capacity_walks is rejected with TRW_ERR_INVALID_ARGUMENT.  Calls on one
+ * store has edge features, ->edge_features point to 16-byte aligned device
+ * buffers with room for capacity_walks walks (rows of max_walk_len,
+ * max_walk_len - 1 and (max_walk_len - 1) * feature_dim values); on return
+ * num_walks, max_walk_len and feature_dim are set.  Every per-call buffer
+ * (start keys and states, draws, processing order, walk scratch) comes from a
+ * fixed device array of 128 MiB per device, held until the process ends: a
+ * sample needing more (about 40 B per walk, plus 8 B per slot of walk scratch
+ * -- 640 B per walk at max_walk_len 80 -- where a layout pass writes the
+ * rows), more walks than capacity_walks, or misaligned buffers, is rejected
+ * with TRW_ERR_INVALID_ARGUMENT.  Calls on one
  * device share that array, so calls that overlap on one device race; the
  * array keeps the last call's contents.  trw_get_walk_stats does not describe
  * these walks. */

@@ -308,6 +308,12 @@ trw_status trw_sample_device_noalloc(void* handle, const trw_sample_params* para
         if (capacity_walks && (!t.nodes || !t.ts || !t.lens ||
                                (params->max_walk_len > 1 && !t.eids) || (want_feat && !t.feat)))
             throw trw::InvalidArgument("null output buffer");
+        // the row writers store 16-byte vectors
+        for (const void* p : {static_cast<const void*>(t.nodes), static_cast<const void*>(t.ts),
+                              static_cast<const void*>(t.lens), static_cast<const void*>(t.eids),
+                              static_cast<const void*>(t.feat)})
+            if (reinterpret_cast<uintptr_t>(p) % 16 != 0)
+                throw trw::InvalidArgument("output buffers must be 16-byte aligned");
         e.sample(*params, &t);
         out->num_walks = e.w_last_num;
         out->max_walk_len = params->max_walk_len;

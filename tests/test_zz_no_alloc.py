@@ -122,6 +122,18 @@ def test_noalloc_sample_rejects_what_does_not_fit():
     # at L = 80)
     with pytest.raises(ValueError, match="no-allocation"):
         _noalloc(eng, 400_000, L, 0, "total", "Uniform", 400_000, walk_layout="scratch")
+    # outputs the 16-byte row stores cannot take
+    import torch
+    ts = torch.empty(1_000 * L + 1, dtype=torch.int64, device="cuda")
+    with pytest.raises(ValueError, match="aligned"):
+        eng.sample_device_noalloc("total", L, "Uniform", 1_000, capacity_walks=1_000,
+                                  nodes_ptr=torch.empty(1_000 * L, dtype=torch.int32,
+                                                        device="cuda").data_ptr(),
+                                  timestamps_ptr=ts.data_ptr() + 8,
+                                  lens_ptr=torch.empty(1_000, dtype=torch.int64,
+                                                       device="cuda").data_ptr(),
+                                  edge_ids_ptr=torch.empty(1_000 * (L - 1), dtype=torch.int64,
+                                                           device="cuda").data_ptr())
     # the handle and the array stay usable
     _same(eng, 20_000, L, 0, "total", "ExponentialIndex", 20_000)
     # rows written by the walk kernel need no walk scratch: the same sample fits
