@@ -280,6 +280,32 @@ def copy_calibration(dev, mib):
     del a, b
 
 
+def pmc_profile(path, family):
+    """(profile, current): current is False when the kernel sources no longer
+    hash to what the profile measured."""
+    if not os.path.exists(path):
+        return None, False
+    with open(path) as f:
+        prof = json.load(f)
+    return prof, prof.get("sources_sha256") == sources_sha256(family)
+
+
+def other_roofline(k, compulsory, kernel_ms, kernel):
+    """The walk kernel's compulsory bytes per launch over its mean launch
+    time, with the measured traffic and L2 hit rate of the config's counter
+    profile while it is current."""
+    path = os.path.join(ROOT, "profiles", f"walk_kernel_cfg{k}_pmc.json")
+    pmc, current = pmc_profile(path, "walk")
+    achieved = compulsory / (kernel_ms * 1e-3) / 1e9
+    traffic = pmc.get("hbm_bytes_per_launch") if pmc and current else None
+    return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "kernel": kernel,
+            "algorithmic_bytes_per_launch": compulsory,
+            "traffic_GB_per_s": (traffic / (kernel_ms * 1e-3) / 1e9) if traffic else None,
+            "l2_hit_rate": pmc.get("l2_hit_rate") if pmc and current else None,
+            "pmc_profile": os.path.relpath(path, ROOT) if pmc else None, "pmc_current": current}
+
+
 def run_other_config(k, args):
     """One of BASELINE.json's other workloads (configs[k-1]), timed on the
     device (HIP events of the engine): index build and sampling.  These are
@@ -342,12 +368,17 @@ def run_other_config(k, args):
                    walk_kernel_ms=sum(kernels) / len(kernels))
         res["index_build_edges_per_s"] = E / (res["build_ms"] * 1e-3)
         res["value"] = st["total_len"] / (res["sample_ms"] * 1e-3)
+        kname = ("walk_rows_kernel" if st["rows_by_walk_kernel"]
+                 else ("walk_weights_kernel" if k == 4 else "walk_kernel"))
+        res["roofline"] = other_roofline(
+            k, st["compulsory_read_bytes"] + st["compulsory_write_bytes"], res["walk_kernel_ms"],
+            kname)
         eng.close()
     elif k == 5:
         eng = capi.Engine(is_directed=True, global_seed=42, shuffle_walk_order=False,
                           max_time_capacity=3_000_000, enable_temporal_node2vec=True,
                           node2vec_p=0.5, node2vec_q=2.0)
-        builds, samples, kernels, steps, edges = [], [], [], 0, 0
+        builds, samples, kernels, steps, edges, comp = [], [], [], 0, 0, 0
         for b, (src, dst, ts) in enumerate(configs.cfg5_batches()):
             arrs = resident(src, dst, ts)
             eng.add_edges_device(arrs[0].data_ptr(), arrs[1].data_ptr(), arrs[2].data_ptr(),
@@ -361,7 +392,10 @@ def run_other_config(k, args):
             builds.append(tb)
             samples.append(tm["sample_ms"])
             kernels.append(tm["walk_kernel_ms"])
-            steps += int(eng.walk_stats()["total_len"])
+            st = eng.walk_stats()
+            steps += int(st["total_len"])
+            comp += st["compulsory_read_bytes"] + st["compulsory_write_bytes"]
+            kname = "walk_rows_kernel" if st["rows_by_walk_kernel"] else "walk_kernel"
             edges += len(src)
             log(f"batch {b}: store {eng.edge_count()} edges, build {tb:.2f} ms, sample "
                 f"{tm['sample_ms']:.2f} ms, walk kernel {tm['walk_kernel_ms']:.2f} ms")
@@ -370,6 +404,7 @@ def run_other_config(k, args):
                    walk_kernel_ms=sum(kernels) / len(kernels))
         res["index_build_edges_per_s"] = edges / (sum(builds) * 1e-3)
         res["value"] = steps / (sum(samples) * 1e-3)
+        res["roofline"] = other_roofline(5, comp / len(builds), res["walk_kernel_ms"], kname)
         eng.close()
         if args.host_ingest:
             res["host_ingest"] = cfg5_host_ingest(capi, configs)
@@ -554,15 +589,6 @@ def main():
     Vc = len(eng.array("node_group_outbound_offsets"))
     T = len(eng.array("unique_timestamps"))
     idx_bytes = index_algorithmic_bytes(E, Vc, T, g_o, g_i)
-
-    def pmc_profile(path, family):
-        """(profile, current): current is False when the kernel sources no
-        longer hash to what the profile measured."""
-        if not os.path.exists(path):
-            return None, False
-        with open(path) as f:
-            prof = json.load(f)
-        return prof, prof.get("sources_sha256") == sources_sha256(family)
 
     pmc, pmc_current = pmc_profile(PMC_FILE, "walk")
     traffic = pmc.get("hbm_bytes_per_launch") if pmc and pmc_current else None
