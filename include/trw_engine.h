@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TRW_ABI_VERSION 5
+#define TRW_ABI_VERSION 6
 
 typedef enum trw_status {
     TRW_OK = 0,
@@ -345,6 +345,9 @@ typedef struct trw_walk_stats {
     uint64_t rows_by_walk_kernel; /* 1: the walk kernel wrote the output rows
                                    * (no scratch, no layout pass); 0: scratch
                                    * and the layout pass */
+    uint64_t slot_word_format;    /* what a walk slot's 64-bit word held: 0 node,
+                                   * timestamp rank and edge id; 1 node and edge
+                                   * id (the three do not fit in 64 bits) */
 } trw_walk_stats;
 trw_status trw_get_walk_stats(void* handle, trw_walk_stats* out);
 

@@ -302,6 +302,7 @@ struct Engine {
     uint64_t w_in_bytes_per_walk = 0;  // start state, processing order, cutoff
     uint64_t w_index_bytes = 0;        // index arrays the launched kernel reads
     int w_rows = 0;  // the walk kernel wrote the output rows itself (no scratch)
+    int w_slot_format = 0;  // trw_walk_stats.slot_word_format of the last sample
     int w_replay = 0;
 
     // pinned host scalars for the few readbacks that size allocations

@@ -1971,6 +1971,7 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
     w_dir_forward = forward ? 1 : 0;
     w_constrained = have_starts ? 1 : 0;
     w_rows = rows_direct ? 1 : 0;
+    w_slot_format = with_rank ? 0 : 1;
     w_replay = p.replay_draws ? 1 : 0;
 
     // ---- graph view of the sampled direction
@@ -2296,6 +2297,7 @@ void walk_stats(Engine& e, trw_walk_stats* out) {
         e.w_rows ? nw * (4 * L + 8 * L + 8 * (L > 0 ? L - 1 : 0)) : 8 * out->total_len;
     out->compulsory_write_bytes = nw ? 8 * nw + (e.w_len > 0 ? scratch : 0) : 0;
     out->rows_by_walk_kernel = static_cast<uint64_t>(e.w_rows);
+    out->slot_word_format = static_cast<uint64_t>(e.w_slot_format);
 }
 
 }  // namespace trw

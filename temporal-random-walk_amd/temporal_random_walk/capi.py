@@ -146,10 +146,11 @@ class TrwWalkStats(C.Structure):
         ("compulsory_read_bytes", C.c_uint64),
         ("compulsory_write_bytes", C.c_uint64),
         ("rows_by_walk_kernel", C.c_uint64),
+        ("slot_word_format", C.c_uint64),
     ]
 
 
-ABI_VERSION = 5  # TRW_ABI_VERSION of include/trw_engine.h
+ABI_VERSION = 6  # TRW_ABI_VERSION of include/trw_engine.h
 _lib = None
 
 

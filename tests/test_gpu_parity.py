@@ -574,9 +574,10 @@ def test_replay_walks_hub_with_more_groups_than_the_header_holds():
 
 
 @pytest.mark.parametrize("forward", [True, False])
-@pytest.mark.parametrize("e,n_ts", [((1 << 21) + 60_000, (1 << 21) + 60_000), (1 << 21, (1 << 21) - 1)],
+@pytest.mark.parametrize("e,n_ts,fmt", [((1 << 21) + 60_000, (1 << 21) + 60_000, 1),
+                                        (1 << 21, (1 << 21) - 1, 0)],
                          ids=["66_bits", "64_bits"])
-def test_replay_walks_at_the_scratch_packing_limit(forward, e, n_ts):
+def test_replay_walks_at_the_scratch_packing_limit(forward, e, n_ts, fmt):
     """Node ids up to 2^22 - 1 with E edges and n_ts distinct timestamps.
     66 bits: a node id, a rank and an edge id need 22 + 22 + 22 bits, more than
     one 64-bit slot word holds, so the slot words hold node and edge id only
@@ -596,6 +597,7 @@ def test_replay_walks_at_the_scratch_packing_limit(forward, e, n_ts):
     assert int(eng.array("active_node_ids").size) == 1 << 22
     assert int(eng.array("unique_timestamps").size) == n_ts
     _walk_case(og, eng, "ExponentialIndex", "Uniform", forward, "total", 20, 20_000, seed=96)
+    assert eng.walk_stats()["slot_word_format"] == fmt
     _walk_case(og, eng, "Uniform", "Linear", forward, "nodes", 20, 4,
                seed_nodes=ids[:500].astype(np.int32), seed=97)
 
