@@ -188,8 +188,9 @@ def test_cfg2_full_parity():
                      replay=dr, shuffle=False)
     for k in ("nodes", "timestamps", "lens", "edge_ids"):
         assert np.array_equal(getattr(ref, k), getattr(got, k)), k
-    # the full sample, run in walk-id order and sorted by start time: the
-    # outputs are the same bytes
+    # the full sample, run in walk-id order and sorted by start time, with the
+    # rows written by the walk kernel or by the layout pass: the outputs are
+    # the same bytes
     import torch
     w = eng.sample_device("total", L, "ExponentialIndex", 10_000_000,
                           initial_edge_bias="Uniform", walk_order="walk_id")
@@ -200,6 +201,14 @@ def test_cfg2_full_parity():
     for name, x, y in zip(("nodes", "timestamps", "lens", "edge_ids"), by_id, by_time):
         assert torch.equal(x, y), name
     del by_time
+    w = eng.sample_device("total", L, "ExponentialIndex", 10_000_000,
+                          initial_edge_bias="Uniform", walk_order="start_time",
+                          walk_layout="scratch")
+    assert eng.walk_stats()["rows_by_walk_kernel"] == 0
+    by_layout = _device_arrays(w, L)
+    for name, x, y in zip(("nodes", "timestamps", "lens", "edge_ids"), by_id, by_layout):
+        assert torch.equal(x, y), name
+    del by_layout
     w = eng.sample_device("total", L, "ExponentialIndex", 10_000_000,
                           initial_edge_bias="Uniform", walk_order="node_grouped")
     by_node = _device_arrays(w, L)
@@ -317,6 +326,19 @@ def test_cfg5_streaming_node2vec():
         all_t.append(t_b)
         w = eng.sample_device("total", L, "TemporalNode2Vec", 5_000_000,
                               initial_edge_bias="Uniform")
+        if k == 9:
+            # the same walks with the rows written by the layout pass
+            import torch
+            rows = _device_arrays(w, L)
+            assert eng.walk_stats()["rows_by_walk_kernel"] == 1
+            w2 = eng.sample_device("total", L, "TemporalNode2Vec", 5_000_000,
+                                   initial_edge_bias="Uniform", walk_layout="scratch")
+            for name, x, y in zip(("nodes", "timestamps", "lens", "edge_ids"), rows,
+                                  _device_arrays(w2, L)):
+                assert torch.equal(x, y), name
+            del rows
+            w = eng.sample_device("total", L, "TemporalNode2Vec", 5_000_000,
+                                  initial_edge_bias="Uniform")
         if k in (0, 9):
             s, d, t = eng.array("sources"), eng.array("targets"), eng.array("timestamps")
             nodes, wts, lens, eids, _ = _fetch_rows(w, range(1_000_000, 1_001_000), L)
