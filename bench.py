@@ -306,6 +306,51 @@ def other_roofline(k, compulsory, kernel_ms, kernel):
             "pmc_profile": os.path.relpath(path, ROOT) if pmc else None, "pmc_current": current}
 
 
+GATHER_TABLES = (("l2_2MiB", 2 << 20), ("mall_128MiB", 128 << 20), ("hbm_4GiB", 4 << 30))
+
+
+def gather_ceiling(capi, pmc, pmc_current, walk_kernel_ms):
+    """Random 8-byte gather rates of this GPU (trw_probe_gather: 512K lanes x
+    256 gathers per launch, mean of 5 launches after a warm-up) from tables
+    that fit L2, the Infinity Cache and neither, as independent loads and as
+    dependent chains; beside them the walk kernel's L1 -> L2 read rate from
+    its counter profile (every one of its per-lane record, panel and header
+    loads that misses L1 is one such read)."""
+    out = {"unit": "gathers/s", "independent": {}, "chained": {}}
+    for name, size in GATHER_TABLES:
+        for mode in ("independent", "chained"):
+            r = capi.probe_gather(size, lanes=256 * 2048, rounds=256,
+                                  chained=(mode == "chained"), reps=5)
+            out[mode][name] = r["gathers_per_s"]
+    c = (pmc or {}).get("counters", {}) if pmc_current else {}
+    reads = c.get("TCP_TCC_READ_REQ_sum")
+    out["walk_l1_l2_reads_per_s"] = None
+    out["walk_read_l2_hit_rate"] = None
+    out["walk_mixed_ceiling"] = None
+    out["walk_frac_of_mixed_ceiling"] = None
+    if reads:
+        rate = reads / (walk_kernel_ms * 1e-3)
+        out["walk_l1_l2_reads_per_s"] = rate
+        hit, miss = c.get("TCC_HIT_sum"), c.get("TCC_MISS_sum")
+        if hit is not None and miss:
+            # the L2 hit rate of the walk's reads lies between the hit rate
+            # of all its L2 requests (writes included, nearly all misses) and
+            # the one with every hit counted as a read
+            h = (hit / (hit + miss), min(1.0, hit / reads))
+            l2, mall = out["independent"]["l2_2MiB"], out["independent"]["mall_128MiB"]
+            ceil = [1.0 / (x / l2 + (1.0 - x) / mall) for x in h]
+            out["walk_read_l2_hit_rate"] = list(h)
+            out["walk_mixed_ceiling"] = ceil
+            out["walk_frac_of_mixed_ceiling"] = [rate / x for x in ceil]
+    out["note"] = ("probe: 512K lanes gather 8-byte words at random places of a table of the "
+                   "named size, one L1 miss each; chained = each address follows from the "
+                   "previous load's value (one load in flight per lane, as in a walk). "
+                   "walk_l1_l2_reads_per_s = TCP_TCC_READ_REQ of one walk-kernel launch "
+                   "(profile) / its time here; walk_mixed_ceiling = the independent L2 and "
+                   "Infinity-Cache rates mixed at the walk's read hit rate (both bounds).")
+    return out
+
+
 def run_other_config(k, args):
     """One of BASELINE.json's other workloads (configs[k-1]), timed on the
     device (HIP events of the engine): index build and sampling.  These are
@@ -494,6 +539,10 @@ def main():
                     help="with --config 5: also time the streaming loop from host arrays, "
                          "ingesting each batch before its sample or prefetching the next "
                          "batch while the current one is sampled")
+    ap.add_argument("--no-gather-ceiling", action="store_true",
+                    help="skip the random-gather rate probe (trw_probe_gather)")
+    ap.add_argument("--gather-ceiling-only", action="store_true",
+                    help="run only the random-gather probe and print its rates")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run one plain device copy of this many MiB (torch copy_ "
                          "kernel): the reference point that scales the HBM byte counters of "
@@ -515,6 +564,10 @@ def main():
 
     if args.config != 2:
         run_other_config(args.config, args)
+        return
+    if args.gather_ceiling_only:
+        from temporal_random_walk import capi
+        print(json.dumps(gather_ceiling(capi, None, False, 1.0)))
         return
 
     import numpy as np
@@ -667,6 +720,9 @@ def main():
         result["index_roofline"]["pmc_profile"] = "profiles/index_build_cfg2_pmc.json"
 
     eng.close()
+    if not args.no_gather_ceiling:
+        log("random-gather probe")
+        result["gather_ceiling"] = gather_ceiling(capi, pmc, pmc_current, walk_kernel_ms)
     if not args.no_host_boundary:
         from temporal_random_walk import TemporalRandomWalk
 

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TRW_ABI_VERSION 6
+#define TRW_ABI_VERSION 7
 
 typedef enum trw_status {
     TRW_OK = 0,
@@ -359,6 +359,26 @@ trw_status trw_get_walk_stats(void* handle, trw_walk_stats* out);
  * batch was accepted leaves the handle empty, as after trw_clear.  No
  * counterpart in the reference. */
 void trw_debug_fail_allocation(int64_t n);
+
+/* ---- measurement aid ------------------------------------------------------ */
+
+/* The rate at which the device serves random 8-byte gathers from a table of
+ * table_bytes (a power of two, 4 KiB - 64 GiB, filled with random words):
+ * lanes (a multiple of 256) each make `rounds` gathers, as independent loads
+ * (chained 0) or as a chain whose next address is the loaded value (chained
+ * 1, one load in flight per lane, as a walk has).  One warm-up launch, then
+ * reps timed launches on the null stream; out gets the mean time per launch.
+ * Every gather is one L1 miss, so the rate bounds the walk kernels' L1 -> L2
+ * read rate.  It allocates the table for the call.  No counterpart in the
+ * reference: the reference has no such measurement. */
+typedef struct trw_probe_result {
+    double ms;            /* per launch */
+    double gathers_per_s;
+    uint64_t gathers;     /* per launch: lanes * rounds */
+} trw_probe_result;
+trw_status trw_probe_gather(int32_t device_id, uint64_t table_bytes, uint32_t lanes,
+                            uint32_t rounds, int32_t chained, int32_t reps,
+                            trw_probe_result* out);
 
 /* ---- standalone pickers (proxies/RandomPicker.cu:11-313) --------------------- */
 

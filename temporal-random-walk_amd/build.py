@@ -43,7 +43,7 @@ HIP_FLAGS = [
     f"-I{INCLUDE}",
 ]
 
-HIP_SOURCES = ["primitives.hip", "build.hip", "walk.hip", "handoff.hip", "pickers.hip", "capi.hip"]
+HIP_SOURCES = ["primitives.hip", "build.hip", "walk.hip", "handoff.hip", "pickers.hip", "probe.hip", "capi.hip"]
 
 
 def _run(cmd):

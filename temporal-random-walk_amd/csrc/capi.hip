@@ -532,6 +532,14 @@ void trw_debug_fail_allocation(int64_t n) {
     trw::g_alloc_fail_after.store(n < 0 ? -1 : n, std::memory_order_relaxed);
 }
 
+trw_status trw_probe_gather(int32_t device_id, uint64_t table_bytes, uint32_t lanes,
+                            uint32_t rounds, int32_t chained, int32_t reps,
+                            trw_probe_result* out) {
+    return guarded_device(device_id, [&] {
+        trw::probe_gather(table_bytes, lanes, rounds, chained, reps, out);
+    });
+}
+
 trw_status trw_pick_index(int32_t device_id, int32_t picker, const int32_t* start,
                           const int32_t* end, uint64_t n, int32_t prioritize_end,
                           const double* draws, uint64_t seed, int32_t* out) {

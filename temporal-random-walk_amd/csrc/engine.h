@@ -390,6 +390,9 @@ void pick_index_batch(int picker, const int32_t* start, const int32_t* end, uint
 void pick_weights_batch(const double* cumulative, uint64_t size, const uint64_t* group_start,
                         const uint64_t* group_end, uint64_t n, const double* draws, uint64_t seed,
                         int32_t* out);
+// Random-gather rate of the device (probe.hip), a measurement aid.
+void probe_gather(uint64_t table_bytes, uint32_t lanes, uint32_t rounds, int chained, int reps,
+                  trw_probe_result* out);
 // Rank of timestamp -1 among the stored unique timestamps (-2 if absent) into
 // e.neg1_rank (update_neg1_rank) or into out, on the engine stream.
 void update_neg1_rank(Engine& e);

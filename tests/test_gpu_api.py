@@ -524,3 +524,20 @@ def test_walk_stats_byte_accounting():
     assert st2["compulsory_write_bytes"] == 8 * n + n * (4 * L + 8 * L + 8 * (L - 1))
     assert st2["reference_bytes"] == st["reference_bytes"]
     eng.close()
+
+
+def test_gather_probe_counts_its_gathers_and_checks_arguments():
+    """trw_probe_gather, the measurement aid bench.py compares the walk
+    kernel's L1 -> L2 read rate with: lanes * rounds gathers per launch, a
+    positive rate in both modes, and its argument checks."""
+    from temporal_random_walk import capi
+    for chained in (False, True):
+        r = capi.probe_gather(1 << 20, lanes=512, rounds=16, chained=chained, reps=2)
+        assert r["gathers"] == 512 * 16
+        assert r["ms"] > 0 and r["gathers_per_s"] > 0
+    for bad in (dict(table_bytes=3 << 20), dict(table_bytes=1024), dict(lanes=100),
+                dict(rounds=0), dict(reps=0)):
+        kw = dict(table_bytes=1 << 20, lanes=256, rounds=4, reps=1)
+        kw.update(bad)
+        with pytest.raises(ValueError):
+            capi.probe_gather(**kw)
