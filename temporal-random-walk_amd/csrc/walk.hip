@@ -1102,8 +1102,13 @@ __device__ __forceinline__ void rows_flush(const WalkArgs& a, uint64_t* buf, int
 // scratch.  The loop runs in chunks of C slots over the whole row for every
 // lane (wave-uniform), so every row is written to its end, the padding
 // included; a lane whose walk has ended (or that has no walk) only fills.
+//
+// At least 4 waves per SIMD, as many as the slot buffers' LDS allows: the
+// index family needs 97 VGPRs, but the any-picker instance (node2vec's retry
+// loop) took 155 and ran at 3 waves; held to 128 (28 bytes of spills) its
+// cfg5 walks run in 12.7 instead of 15.4 ms per batch.
 template <bool Fwd, bool Dir, int Fam, int C>
-__global__ __launch_bounds__(kB) void walk_rows_kernel(WalkGraph g, WalkArgs a) {
+__global__ __launch_bounds__(kB) __attribute__((amdgpu_waves_per_eu(4))) void walk_rows_kernel(WalkGraph g, WalkArgs a) {
     static_assert(Fwd, "backward walks are reversed by the layout pass");
     __shared__ double s_xt[kExpTables];
     __shared__ uint64_t s_slots[(kB / 64) * C * kRowStride];
