@@ -355,6 +355,7 @@ def run_other_config(k, args):
     """One of BASELINE.json's other workloads (configs[k-1]), timed on the
     device (HIP events of the engine): index build and sampling.  These are
     parity-test configs; the bench line proper is cfg2."""
+    import numpy as np
     import torch
     from temporal_random_walk import capi
     from tests import configs
@@ -367,6 +368,8 @@ def run_other_config(k, args):
         return out
 
     res = {"config": f"cfg{k}", "unit": "walk steps/s"}
+    if k == 5 and args.late_frac > 0:
+        res["late_frac"] = args.late_frac
     if args.copy_calibration_mib > 0:
         copy_calibration(dev, args.copy_calibration_mib)
     log(f"generating cfg{k} inputs")
@@ -424,7 +427,15 @@ def run_other_config(k, args):
                           max_time_capacity=3_000_000, enable_temporal_node2vec=True,
                           node2vec_p=0.5, node2vec_q=2.0)
         builds, samples, kernels, steps, edges, comp = [], [], [], 0, 0, 0
+        late_rng = np.random.default_rng(48)
         for b, (src, dst, ts) in enumerate(configs.cfg5_batches()):
+            if args.late_frac > 0 and b > 0:
+                # late arrivals: a share of the batch carries timestamps of the
+                # previous batch's range, so the batch reaches back into the
+                # store (the merge path instead of the append path)
+                late = late_rng.random(len(ts)) < args.late_frac
+                ts = ts.copy()
+                ts[late] = late_rng.integers((b - 1) * 1_000_000, b * 1_000_000, int(late.sum()))
             arrs = resident(src, dst, ts)
             eng.add_edges_device(arrs[0].data_ptr(), arrs[1].data_ptr(), arrs[2].data_ptr(),
                                  len(src))
@@ -539,6 +550,9 @@ def main():
                     help="with --config 5: also time the streaming loop from host arrays, "
                          "ingesting each batch before its sample or prefetching the next "
                          "batch while the current one is sampled")
+    ap.add_argument("--late-frac", type=float, default=0.0,
+                    help="--config 5: this share of every batch after the first gets "
+                         "timestamps of the previous batch's range (late arrivals)")
     ap.add_argument("--no-gather-ceiling", action="store_true",
                     help="skip the random-gather rate probe (trw_probe_gather)")
     ap.add_argument("--gather-ceiling-only", action="store_true",

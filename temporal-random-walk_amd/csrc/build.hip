@@ -369,6 +369,112 @@ __global__ void append_new_entries_kernel(const uint32_t* __restrict__ bkeys,
     rec[d] = EdgeRec{static_cast<int32_t>(static_cast<uint32_t>(b)), static_cast<uint32_t>(b >> 32)};
 }
 
+// ---- merge path: a batch reaching back before the store's last timestamp ----
+// The stable (timestamp, position) order of store + batch interleaves the two
+// sorted runs -- the store's and the batch's, sorted alone -- with a store edge
+// first on equal timestamps.  Each kept edge finds its place by counting the
+// other run's kept edges before it (one binary search), so the store moves by
+// one scatter instead of a sort of the whole window.  (The node index is
+// rebuilt: the same co-rank merge of every node's old and batch entries took
+// longer than the node sort it replaces.)
+
+// Number of sorted batch keys k[lo, hi) (timestamp - btmin) whose timestamp is
+// below t (strict: lower_bound) or at most t (upper_bound).
+template <typename K>
+__device__ __forceinline__ size_t batch_rank(const K* __restrict__ k, size_t lo, size_t hi,
+                                             int64_t btmin, int64_t t, bool strict) {
+    if (t < btmin || (strict && t == btmin)) return lo;
+    const uint64_t x = static_cast<uint64_t>(t) - static_cast<uint64_t>(btmin);
+    while (lo < hi) {
+        const size_t mid = lo + ((hi - lo) >> 1);
+        const uint64_t y = static_cast<uint64_t>(k[mid]);
+        if (strict ? y < x : y <= x) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// Upper_bound of t over the store's timestamps ts[lo, hi).
+__device__ __forceinline__ size_t store_rank(const int64_t* __restrict__ ts, size_t lo, size_t hi,
+                                             int64_t t) {
+    while (lo < hi) {
+        const size_t mid = lo + ((hi - lo) >> 1);
+        if (ts[mid] <= t) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// Eviction of the merge: out[0] / out[1] = evicted store / batch edges (those
+// with ts <= cutoff: a prefix of each run), out[2] / out[3] = first / last kept
+// timestamp (0 when nothing is kept).
+template <typename K>
+__global__ void merge_evict_kernel(const int64_t* __restrict__ old_ts, size_t e_old,
+                                   const K* __restrict__ keys, size_t n, int64_t btmin,
+                                   int64_t cutoff, int64_t* __restrict__ out) {
+    const size_t del_old = store_rank(old_ts, 0, e_old, cutoff);
+    const size_t del_new = batch_rank(keys, 0, n, btmin, cutoff, false);
+    const auto bts = [&](size_t j) {
+        return static_cast<int64_t>(static_cast<uint64_t>(keys[j]) + static_cast<uint64_t>(btmin));
+    };
+    int64_t first = 0, last = 0;
+    if (del_old < e_old && del_new < n) {
+        first = old_ts[del_old] <= bts(del_new) ? old_ts[del_old] : bts(del_new);
+        last = old_ts[e_old - 1] >= bts(n - 1) ? old_ts[e_old - 1] : bts(n - 1);
+    } else if (del_old < e_old) {
+        first = old_ts[del_old];
+        last = old_ts[e_old - 1];
+    } else if (del_new < n) {
+        first = bts(del_new);
+        last = bts(n - 1);
+    }
+    out[0] = static_cast<int64_t>(del_old);
+    out[1] = static_cast<int64_t>(del_new);
+    out[2] = first;
+    out[3] = last;
+}
+
+// Kept store edge i goes to (i - del_old) + (kept batch edges with a smaller
+// timestamp).  perm (the feature gather's source, store ids first) is written
+// when given.
+template <typename K>
+__global__ void merge_old_kernel(const int64_t* __restrict__ old_ts,
+                                 const int32_t* __restrict__ old_src,
+                                 const int32_t* __restrict__ old_dst, size_t del_old, size_t e_old,
+                                 const K* __restrict__ keys, size_t del_new, size_t n,
+                                 int64_t btmin, int32_t* __restrict__ s, int32_t* __restrict__ d,
+                                 int64_t* __restrict__ t, uint32_t* __restrict__ perm) {
+    const size_t i = del_old + blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (i >= e_old) return;
+    const int64_t ti = old_ts[i];
+    const size_t p = (i - del_old) + (batch_rank(keys, del_new, n, btmin, ti, true) - del_new);
+    s[p] = old_src[i];
+    d[p] = old_dst[i];
+    t[p] = ti;
+    if (perm) perm[p] = static_cast<uint32_t>(i);
+}
+
+// Kept batch edge j (sorted position) goes to (j - del_new) + (kept store
+// edges with a timestamp <= its own).  Its endpoints come packed: sorted with
+// the keys (bpos == nullptr), or by batch position bpos[j].
+template <typename K>
+__global__ void merge_new_kernel(const int64_t* __restrict__ old_ts, size_t del_old, size_t e_old,
+                                 const K* __restrict__ keys, const uint64_t* __restrict__ ends,
+                                 const uint32_t* __restrict__ bpos, size_t del_new, size_t n,
+                                 int64_t btmin, int32_t* __restrict__ s, int32_t* __restrict__ d,
+                                 int64_t* __restrict__ t, uint32_t* __restrict__ perm) {
+    const size_t j = del_new + blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (j >= n) return;
+    const int64_t tj =
+        static_cast<int64_t>(static_cast<uint64_t>(keys[j]) + static_cast<uint64_t>(btmin));
+    const size_t p = (j - del_new) + (store_rank(old_ts, del_old, e_old, tj) - del_old);
+    const uint64_t sd = bpos ? ends[bpos[j]] : ends[j];
+    s[p] = static_cast<int32_t>(static_cast<uint32_t>(sd));
+    d[p] = static_cast<int32_t>(static_cast<uint32_t>(sd >> 32));
+    t[p] = tj;
+    if (perm) perm[p] = static_cast<uint32_t>(e_old) + bpos[j];
+}
+
 // Group-start flags of the sorted entries (a new node, or a new timestamp
 // rank within a node) and the sorted edge ids (node_ts_sorted_*_indices).  The
 // previous entry's node and rank come from the lane below.
@@ -1198,6 +1304,60 @@ void build_global_weight_index(Engine& e, const DBuf<double>& w, size_t n, DBuf<
     check_hip(hipGetLastError(), "global weight index launch");
 }
 
+// The batch alone, sorted stably by timestamp: keys ts - btmin (32-bit when the
+// batch's range fits).  Without edge features the packed endpoints travel as
+// the sort's values (ends sorted, bpos null); with them the batch positions do
+// (bpos), the endpoints staying in batch order (ends).
+struct SortedBatch {
+    bool keys32;
+    const uint32_t* k32;
+    const uint64_t* k64;
+    const uint64_t* ends;
+    const uint32_t* bpos;
+};
+
+SortedBatch sort_batch(Engine& e, const int32_t* d_src, const int32_t* d_dst, const int64_t* d_ts,
+                       size_t n, int64_t btmin, int64_t btmax) {
+    hipStream_t s = e.stream;
+    const int bits = bit_length_u64(static_cast<uint64_t>(btmax) - static_cast<uint64_t>(btmin));
+    const bool keys32 = bits <= 32;
+    const bool carry_ends = e.feat_dim == 0;
+    e.k64a.ensure(n);
+    e.k64b.ensure(n);
+    e.ends64.ensure(n);
+    if (carry_ends) e.ends64b.ensure(n);
+    e.v32a.ensure(n);
+    e.v32b.ensure(n);
+    e.hist.ensure(radix_hist_elems(n));
+    uint32_t* k32s[2] = {reinterpret_cast<uint32_t*>(e.k64a.p), reinterpret_cast<uint32_t*>(e.k64b.p)};
+    uint32_t* pos0 = carry_ends ? nullptr : e.v32a.p;
+    int which;
+    if (keys32) {
+        hipLaunchKernelGGL((make_ts_keys_kernel<uint32_t>), dim3(grid_for(n)), dim3(kB), 0, s,
+                           e.ts.p, e.src.p, e.dst.p, size_t{0}, d_ts, d_src, d_dst, n, btmin,
+                           k32s[0], pos0, e.ends64.p);
+        which = carry_ends ? radix_sort_u32_v64(k32s[0], e.ends64.p, k32s[1], e.ends64b.p, n, 0,
+                                                bits, e.hist.p, s)
+                           : radix_sort_u32(k32s[0], e.v32a.p, k32s[1], e.v32b.p, n, 0, bits,
+                                            e.hist.p, s);
+    } else {
+        hipLaunchKernelGGL((make_ts_keys_kernel<uint64_t>), dim3(grid_for(n)), dim3(kB), 0, s,
+                           e.ts.p, e.src.p, e.dst.p, size_t{0}, d_ts, d_src, d_dst, n, btmin,
+                           e.k64a.p, pos0, e.ends64.p);
+        which = carry_ends ? radix_sort_u64_v64(e.k64a.p, e.ends64.p, e.k64b.p, e.ends64b.p, n, 0,
+                                                bits, e.hist.p, s)
+                           : radix_sort_u64(e.k64a.p, e.v32a.p, e.k64b.p, e.v32b.p, n, 0, bits,
+                                            e.hist.p, s);
+    }
+    SortedBatch b;
+    b.keys32 = keys32;
+    b.k32 = k32s[which];
+    b.k64 = which ? e.k64b.p : e.k64a.p;
+    b.ends = carry_ends ? (which ? e.ends64b.p : e.ends64.p) : e.ends64.p;
+    b.bpos = carry_ends ? nullptr : (which ? e.v32b.p : e.v32a.p);
+    return b;
+}
+
 }  // namespace
 
 void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_ts,
@@ -1362,38 +1522,13 @@ void Engine::append_store(const int32_t* d_src, const int32_t* d_dst, const int6
     hipStream_t s = stream;
     int64_t* hs = reinterpret_cast<int64_t*>(host_scalars);
     const size_t e_old = E;
-    const int bits = bit_length_u64(static_cast<uint64_t>(btmax) - static_cast<uint64_t>(btmin));
-    const bool keys32 = bits <= 32;
     const bool carry_ends = feat_dim == 0;
-    k64a.ensure(n);
-    k64b.ensure(n);
-    ends64.ensure(n);
-    if (carry_ends) ends64b.ensure(n);
-    v32a.ensure(n);
-    v32b.ensure(n);
-    hist.ensure(radix_hist_elems(n));
-    uint32_t* k32s[2] = {reinterpret_cast<uint32_t*>(k64a.p), reinterpret_cast<uint32_t*>(k64b.p)};
-    uint32_t* pos0 = carry_ends ? nullptr : v32a.p;
-    int which;
-    if (keys32) {
-        hipLaunchKernelGGL((make_ts_keys_kernel<uint32_t>), dim3(grid_for(n)), dim3(kB), 0, s,
-                           ts.p, src.p, dst.p, size_t{0}, d_ts, d_src, d_dst, n, btmin, k32s[0],
-                           pos0, ends64.p);
-        which = carry_ends
-                    ? radix_sort_u32_v64(k32s[0], ends64.p, k32s[1], ends64b.p, n, 0, bits, hist.p, s)
-                    : radix_sort_u32(k32s[0], v32a.p, k32s[1], v32b.p, n, 0, bits, hist.p, s);
-    } else {
-        hipLaunchKernelGGL((make_ts_keys_kernel<uint64_t>), dim3(grid_for(n)), dim3(kB), 0, s,
-                           ts.p, src.p, dst.p, size_t{0}, d_ts, d_src, d_dst, n, btmin, k64a.p,
-                           pos0, ends64.p);
-        which = carry_ends
-                    ? radix_sort_u64_v64(k64a.p, ends64.p, k64b.p, ends64b.p, n, 0, bits, hist.p, s)
-                    : radix_sort_u64(k64a.p, v32a.p, k64b.p, v32b.p, n, 0, bits, hist.p, s);
-    }
-    const uint32_t* perm = which ? v32b.p : v32a.p;
-    const uint64_t* sorted_ends = which ? ends64b.p : ends64.p;
-    const uint32_t* sk32 = k32s[which];
-    const uint64_t* sk64 = which ? k64b.p : k64a.p;
+    const SortedBatch sb = sort_batch(*this, d_src, d_dst, d_ts, n, btmin, btmax);
+    const bool keys32 = sb.keys32;
+    const uint32_t* perm = sb.bpos;
+    const uint64_t* sorted_ends = sb.ends;
+    const uint32_t* sk32 = sb.k32;
+    const uint64_t* sk64 = sb.k64;
 
     // eviction: drop ts <= latest - capacity, from the store first
     size_t del_old = 0, del_new = 0;
@@ -1479,6 +1614,88 @@ void Engine::append_store(const int32_t* d_src, const int32_t* d_dst, const int6
     check_hip(hipGetLastError(), "append launch");
 }
 
+// Steps 2-4 of an ingest of a batch that reaches back before the store's last
+// timestamp: the batch is sorted alone and merged with the store (the merge
+// kernels above), which gives the same order as the reference's "sort the
+// batch, stable-merge it after the old store" (temporal_graph.cu:67-134);
+// the window's cut (temporal_graph.cu:136-156) drops a prefix of each run.
+void Engine::merge_store(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_ts,
+                         const float* d_feat, size_t n, int64_t btmin, int64_t btmax) {
+    hipStream_t s = stream;
+    int64_t* hs = reinterpret_cast<int64_t*>(host_scalars);
+    const size_t e_old = E;
+    const SortedBatch sb = sort_batch(*this, d_src, d_dst, d_ts, n, btmin, btmax);
+    size_t del_old = 0, del_new = 0;
+    if (cfg.max_time_capacity > 0) {
+        const int64_t cutoff = latest_ts - cfg.max_time_capacity;
+        if (sb.keys32)
+            hipLaunchKernelGGL((merge_evict_kernel<uint32_t>), dim3(1), dim3(1), 0, s, ts.p, e_old,
+                               sb.k32, n, btmin, cutoff, red64.p);
+        else
+            hipLaunchKernelGGL((merge_evict_kernel<uint64_t>), dim3(1), dim3(1), 0, s, ts.p, e_old,
+                               sb.k64, n, btmin, cutoff, red64.p);
+        check_hip(hipMemcpyAsync(hs, red64.p, 32, hipMemcpyDeviceToHost, s), "read evict");
+        sync();
+        del_old = static_cast<size_t>(hs[0]);
+        del_new = static_cast<size_t>(hs[1]);
+        store_tmin = hs[2];
+        store_tmax = hs[3];
+    } else {
+        store_tmin = std::min(store_tmin, btmin);
+        store_tmax = std::max(store_tmax, btmax);
+    }
+    const size_t kept_old = e_old - del_old, kept_new = n - del_new, kept = kept_old + kept_new;
+    src2.resize(kept);
+    dst2.resize(kept);
+    ts2.resize(kept);
+    uint32_t* perm = nullptr;
+    if (feat_dim > 0) {
+        merge_perm.resize(std::max<size_t>(kept, 1));
+        perm = merge_perm.p;
+    }
+    if (kept_old) {
+        if (sb.keys32)
+            hipLaunchKernelGGL((merge_old_kernel<uint32_t>), dim3(grid_for(kept_old)), dim3(kB), 0, s,
+                               ts.p, src.p, dst.p, del_old, e_old, sb.k32, del_new, n, btmin,
+                               src2.p, dst2.p, ts2.p, perm);
+        else
+            hipLaunchKernelGGL((merge_old_kernel<uint64_t>), dim3(grid_for(kept_old)), dim3(kB), 0, s,
+                               ts.p, src.p, dst.p, del_old, e_old, sb.k64, del_new, n, btmin,
+                               src2.p, dst2.p, ts2.p, perm);
+    }
+    if (kept_new) {
+        if (sb.keys32)
+            hipLaunchKernelGGL((merge_new_kernel<uint32_t>), dim3(grid_for(kept_new)), dim3(kB), 0, s,
+                               ts.p, del_old, e_old, sb.k32, sb.ends, sb.bpos, del_new, n, btmin,
+                               src2.p, dst2.p, ts2.p, perm);
+        else
+            hipLaunchKernelGGL((merge_new_kernel<uint64_t>), dim3(grid_for(kept_new)), dim3(kB), 0, s,
+                               ts.p, del_old, e_old, sb.k64, sb.ends, sb.bpos, del_new, n, btmin,
+                               src2.p, dst2.p, ts2.p, perm);
+    }
+    if (feat_dim > 0) {
+        feat2.resize(kept * feat_dim);
+        const uint32_t V = static_cast<uint32_t>(feat_dim / 4);
+        if (kept && feat_dim % 4 == 0 && V <= 256 && aligned16(d_feat)) {
+            const uint32_t R = 256 / V;
+            const size_t blocks = std::min<size_t>((kept + R - 1) / R, 65536);
+            hipLaunchKernelGGL(gather_feat_vec_kernel, dim3(blocks), dim3(V * R), 0, s, perm,
+                               size_t{0}, kept, V, reinterpret_cast<const f32x4*>(feat.p), e_old,
+                               reinterpret_cast<const f32x4*>(d_feat),
+                               reinterpret_cast<f32x4*>(feat2.p));
+        } else if (kept) {
+            hipLaunchKernelGGL(gather_feat_kernel, dim3(grid_capped(kept * feat_dim)), dim3(kB), 0,
+                               s, perm, size_t{0}, kept, feat_dim, feat.p, e_old, d_feat, feat2.p);
+        }
+        feat.swap(feat2);
+    }
+    src.swap(src2);
+    dst.swap(dst2);
+    ts.swap(ts2);
+    E = kept;
+    check_hip(hipGetLastError(), "merge launch");
+}
+
 void Engine::build_accepted(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_ts,
                             const float* d_feat, size_t n, size_t dim, int64_t tmin,
                             int64_t tmax) {
@@ -1507,8 +1724,11 @@ void Engine::build_accepted(const int32_t* d_src, const int32_t* d_dst, const in
     // (streaming) goes after the store's kept edges as it is, sorted alone;
     // any other batch is sorted together with the store.
     append_mode = e_old > 0 && batch_tmin >= store_tmax;
+    merge_mode = e_old > 0 && !append_mode;
     if (append_mode)
         append_store(d_src, d_dst, d_ts, d_feat, n, batch_tmin, batch_tmax);
+    else if (merge_mode)
+        merge_store(d_src, d_dst, d_ts, d_feat, n, batch_tmin, batch_tmax);
     else
         sort_store(d_src, d_dst, d_ts, d_feat, n, tmin, tmax);
     check_hip(hipEventRecord(ev[1], s), "event");

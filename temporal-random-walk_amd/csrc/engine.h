@@ -254,6 +254,11 @@ struct Engine {
     DBuf<uint32_t> key_next, off_next;
     DBuf<EdgeRec> rec_next;
 
+    // the last ingest merged its batch into the store (merge_store), and the
+    // merged store's feature rows' sources (store ids, then e_old + batch row)
+    bool merge_mode = false;
+    DBuf<uint32_t> merge_perm;
+
     // last ingested batch (for ..._for_last_batch)
     DBuf<int32_t> last_src, last_dst;
     size_t last_n = 0;
@@ -352,12 +357,17 @@ struct Engine {
     // the pipeline of build() after the batch's checks
     void build_accepted(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_ts,
                         const float* d_feat, size_t n, size_t dim, int64_t tmin, int64_t tmax);
-    // its store update: the general sort of store + batch, or the append of a
-    // batch at or after the store's last timestamp (sets append_*)
+    // its store update: the sort of the first batch into an empty store, the
+    // append of a batch at or after the store's last timestamp (sets
+    // append_*), or the merge of any other batch (below)
     void sort_store(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_ts,
                     const float* d_feat, size_t n, int64_t tmin, int64_t tmax);
     void append_store(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_ts,
                       const float* d_feat, size_t n, int64_t btmin, int64_t btmax);
+    // any other batch into a non-empty store: the batch sorted alone, then
+    // merged with the store (sets merge_*)
+    void merge_store(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_ts,
+                     const float* d_feat, size_t n, int64_t btmin, int64_t btmax);
 
     // sampling into w_* buffers
     // sampling: into the engine's w_* buffers, or -- with `into` -- into

@@ -154,6 +154,41 @@ def test_index_append_batches(directed, cap):
         _walk_case(og, eng, "Linear", "Uniform", forward, "total", 16, 3_000, seed=31)
 
 
+@pytest.mark.parametrize("directed", [True, False])
+@pytest.mark.parametrize("cap", [-1, 2_500, 700, 150])
+def test_index_merge_batches(directed, cap):
+    """Batches reaching back before the store's last timestamp take the merge
+    path (the batch sorted alone, then merged into the store by binary search;
+    the node index rebuilt): batches overlapping the store's end, one lying
+    wholly before the store, one spanning all of it, ties at equal timestamps
+    throughout, edge features carried along.  The window cuts inside the store
+    (2500), into the batch (700, 150) or not at all.  Every index array and the
+    features equal the oracle's after every batch; weights, the adjacency and
+    replay walks after the last."""
+    batches, feats = _append_batches(25, 5, 20_000, 1_000, overlap=400, dims=4)
+    rng = np.random.default_rng(26)
+    t_hi = int(batches[-1][2].max())
+    s = graphs.zipf_ids(rng, 20_000, 5_000, 1.6)
+    d = graphs.zipf_ids(rng, 20_000, 5_000, 1.6)
+    batches.append((s, d, rng.integers(0, t_hi + 1, 20_000).astype(np.int64)))  # spans all
+    feats.append(rng.standard_normal((20_000, 4)).astype(np.float32))
+    batches.append((d, s, rng.integers(t_hi - 3_000, t_hi - 2_000, 20_000).astype(np.int64)))
+    feats.append(rng.standard_normal((20_000, 4)).astype(np.float32))
+    og = po.OracleGraph(directed, cap, True, True, 30.0, 0.5, 2.0)
+    eng = _engine(is_directed=directed, max_time_capacity=cap, enable_weight_computation=True,
+                  enable_temporal_node2vec=True, timescale_bound=30.0, node2vec_p=0.5,
+                  node2vec_q=2.0, shuffle_walk_order=False, global_seed=78)
+    for b, f in zip(batches, feats):
+        og.add_edges(*b, f)
+        eng.add_edges(*b, f)
+        _assert_index_equal(og, eng)
+        assert np.array_equal(og.array("edge_features"), eng.array("edge_features"))
+    _assert_index_equal(og, eng, weights=True, tn2v=True)
+    assert eng.edge_count() == len(og.array("timestamps"))
+    for forward in (True, False):
+        _walk_case(og, eng, "Linear", "Uniform", forward, "total", 16, 3_000, seed=32)
+
+
 def test_index_cfg5_shaped_stream():
     """configs[4]'s stream at a tenth of its batch size: the same 1M-id
     Zipf(1.8) graph, 10 batches of 300k edges in consecutive time ranges,
