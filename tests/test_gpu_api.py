@@ -426,7 +426,7 @@ def test_failed_ingest_leaves_an_empty_usable_engine(shift):
     test hook) raises MemoryError and leaves the engine empty, as after
     clear(); the engine then samples (no walks start) and a new ingest gives
     the oracle's index and replay walks.  shift puts the second batch after
-    the first in time (the append path) or among it (the general sort)."""
+    the first in time (the append path) or among it (the merge path)."""
     from oracle import pyoracle as po
     from temporal_random_walk import capi
     s1, d1, t1 = graphs.cfg1(n_nodes=300, n_edges=2_000, seed=3)
