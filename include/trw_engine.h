@@ -364,9 +364,10 @@ void trw_debug_fail_allocation(int64_t n);
 
 /* The rate at which the device serves random 8-byte gathers from a table of
  * table_bytes (a power of two, 4 KiB - 64 GiB, filled with random words):
- * lanes (a multiple of 256) each make `rounds` gathers, as independent loads
- * (chained 0) or as a chain whose next address is the loaded value (chained
- * 1, one load in flight per lane, as a walk has).  One warm-up launch, then
+ * lanes (a multiple of 256) each make `rounds` gathers (at most 2^36 in all),
+ * as independent loads (chained 0) or as a chain whose next address follows
+ * from the loaded value (chained 1, one load in flight per lane, as a walk
+ * has).  One warm-up launch, then
  * reps timed launches on the null stream; out gets the mean time per launch.
  * Every gather is one L1 miss, so the rate bounds the walk kernels' L1 -> L2
  * read rate.  It allocates the table for the call.  No counterpart in the

@@ -67,6 +67,9 @@ void probe_gather(uint64_t table_bytes, uint32_t lanes, uint32_t rounds, int cha
         throw InvalidArgument("table_bytes must be a power of two in [4 KiB, 64 GiB]");
     if (lanes == 0 || lanes % kPB != 0) throw InvalidArgument("lanes must be a positive multiple of 256");
     if (rounds == 0 || reps <= 0) throw InvalidArgument("rounds and reps must be positive");
+    // a launch of at most 2^36 gathers: about a second at the slowest rate
+    if (static_cast<uint64_t>(lanes) * rounds > (uint64_t{1} << 36))
+        throw InvalidArgument("lanes * rounds must not exceed 2^36 gathers per launch");
     const uint64_t n = table_bytes / 8;
     DBuf<uint64_t> table, sink;
     table.resize(n);
