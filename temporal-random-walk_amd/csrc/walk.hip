@@ -902,12 +902,13 @@ __global__ __launch_bounds__(kB) void walk_weights_kernel(WalkGraph g, WalkArgs 
     if (q < a.q_end) a.lens[a.order ? a.order[q] : q] = 0;
 }
 
-// At least 5 waves per SIMD: the index family needs 86 VGPRs, the any-picker
-// instance (node2vec's retry loop) 146-150, which left it at 3 waves; held to
-// 102 its cfg5 walks (scratch path) run in 11.1 instead of 13.0 ms per batch
-// (4 waves: 11.7 ms; 6 waves: 14.0 ms).
+// Waves per SIMD: the any-picker instance (node2vec's retry loop) needs
+// 146-150 VGPRs, which left it at 3 waves; held to 5 (102 VGPRs) its cfg5
+// walks (scratch path) run in 11.1 instead of 13.0 ms per batch (4 waves:
+// 11.7 ms; 6: 14.0 ms).  The index family needs 86 (5 waves); held to 6 (80
+// VGPRs, 12 bytes of spills) its cfg2 walks run in 9.75 instead of 9.98 ms.
 template <bool Fwd, bool Dir, int Fam>
-__global__ __launch_bounds__(kB) __attribute__((amdgpu_waves_per_eu(5))) void walk_kernel(WalkGraph g, WalkArgs a) {
+__global__ __launch_bounds__(kB) __attribute__((amdgpu_waves_per_eu(Fam == kFamIndex ? 6 : 5))) void walk_kernel(WalkGraph g, WalkArgs a) {
     // the exponential index picker's thresholds (expm1 of every length it
     // evaluates, exp(-j)), once per workgroup instead of a logarithm per hop
     __shared__ double s_xt[kExpTables];
