@@ -335,19 +335,25 @@ def gather_ceiling(capi, pmc, pmc_current, walk_kernel_ms):
         if hit is not None and miss:
             # the L2 hit rate of the walk's reads lies between the hit rate
             # of all its L2 requests (writes included, nearly all misses) and
-            # the one with every hit counted as a read
+            # the one with every hit counted as a read; its misses are served
+            # by the Infinity Cache or by HBM
             h = (hit / (hit + miss), min(1.0, hit / reads))
-            l2, mall = out["independent"]["l2_2MiB"], out["independent"]["mall_128MiB"]
-            ceil = [1.0 / (x / l2 + (1.0 - x) / mall) for x in h]
+            l2 = out["independent"]["l2_2MiB"]
             out["walk_read_l2_hit_rate"] = list(h)
-            out["walk_mixed_ceiling"] = ceil
-            out["walk_frac_of_mixed_ceiling"] = [rate / x for x in ceil]
+            out["walk_mixed_ceiling"] = {}
+            out["walk_frac_of_mixed_ceiling"] = {}
+            for name, far in (("misses_in_infinity_cache", out["independent"]["mall_128MiB"]),
+                              ("misses_in_hbm", out["independent"]["hbm_4GiB"])):
+                ceil = [1.0 / (x / l2 + (1.0 - x) / far) for x in h]
+                out["walk_mixed_ceiling"][name] = ceil
+                out["walk_frac_of_mixed_ceiling"][name] = [rate / x for x in ceil]
     out["note"] = ("probe: 512K lanes gather 8-byte words at random places of a table of the "
                    "named size, one L1 miss each; chained = each address follows from the "
                    "previous load's value (one load in flight per lane, as in a walk). "
                    "walk_l1_l2_reads_per_s = TCP_TCC_READ_REQ of one walk-kernel launch "
-                   "(profile) / its time here; walk_mixed_ceiling = the independent L2 and "
-                   "Infinity-Cache rates mixed at the walk's read hit rate (both bounds).")
+                   "(profile) / its time here; walk_mixed_ceiling = the independent L2 rate "
+                   "mixed with the Infinity-Cache or the HBM rate at the walk's read hit rate "
+                   "(both bounds of it).")
     return out
 
 
@@ -422,6 +428,10 @@ def run_other_config(k, args):
             k, st["compulsory_read_bytes"] + st["compulsory_write_bytes"], res["walk_kernel_ms"],
             kname)
         eng.close()
+        if not args.no_gather_ceiling:
+            pmc, current = pmc_profile(os.path.join(ROOT, "profiles", f"walk_kernel_cfg{k}_pmc.json"),
+                                       "walk")
+            res["gather_ceiling"] = gather_ceiling(capi, pmc, current, res["walk_kernel_ms"])
     elif k == 5:
         eng = capi.Engine(is_directed=True, global_seed=42, shuffle_walk_order=False,
                           max_time_capacity=3_000_000, enable_temporal_node2vec=True,
@@ -462,6 +472,10 @@ def run_other_config(k, args):
         res["value"] = steps / (sum(samples) * 1e-3)
         res["roofline"] = other_roofline(5, comp / len(builds), res["walk_kernel_ms"], kname)
         eng.close()
+        if not args.no_gather_ceiling:
+            pmc, current = pmc_profile(os.path.join(ROOT, "profiles", "walk_kernel_cfg5_pmc.json"),
+                                       "walk")
+            res["gather_ceiling"] = gather_ceiling(capi, pmc, current, res["walk_kernel_ms"])
         if args.host_ingest:
             res["host_ingest"] = cfg5_host_ingest(capi, configs)
     else:
