@@ -319,6 +319,17 @@ __device__ __forceinline__ uint32_t weight_lower_bound(const double* w, uint32_t
     return b + k;
 }
 
+// pick_weights after its range checks, with the slice's start_sum and end_sum
+// already loaded (end_sum >= start_sum): the same result.
+__device__ __forceinline__ int pick_weights_sums(const double* w, uint64_t gs, uint64_t ge,
+                                                 double r, double start_sum, double end_sum,
+                                                 uint64_t seg, uint32_t G, const double* lv) {
+    const double target = start_sum + r * (end_sum - start_sum);
+    if (target <= start_sum) return static_cast<int>(gs);
+    const uint64_t x = seg + weight_lower_bound(w + seg, G, lv, target);
+    return static_cast<int>(x < gs ? gs : (x > ge ? ge : x));
+}
+
 // pick_exponential_weights (random/pickers.cuh:84-126) over the slice
 // [gs, ge) of the segment [seg, seg + G) that holds it: the lower_bound over
 // the whole segment, clamped to the slice, is the slice's lower_bound because
@@ -416,13 +427,18 @@ __device__ Hop tn2v_pick(const WalkGraph& g, int prev, uint32_t vb, uint32_t ve,
     const double acc_adj = 1.0 * inv_bmax, acc_far = g.inv_q * inv_bmax;
     const double acc_lo = acc_adj < acc_far ? acc_adj : acc_far;
     const double acc_hi = acc_adj < acc_far ? acc_far : acc_adj;
+    // every retry's weight pick (pick_weights over the slice [vb, ve) of the
+    // segment [gb, ge)) reads the same two sums: loaded once, outside the loop
+    if (ve > g.d.w_size) return no_hop();
+    const double start_sum = vb > gb ? g.d.w[vb - 1] : 0.0;
+    const double end_sum = g.d.w[ve - 1];
+    if (end_sum < start_sum) return no_hop();
     Hop last = no_hop();
     for (int retry = 0; retry < kNode2VecMaxRetries; ++retry) {
         const double gr = derive_uniform(rg, re, retry * 3 + 0);
         const double er = derive_uniform(rg, re, retry * 3 + 1);
         const double ar = derive_uniform(rg, re, retry * 3 + 2);
-        const int gp = pick_weights(g.d.w, g.d.w_size, vb, ve, gr, gb, gb, ge - gb, lv);
-        if (gp == -1) return no_hop();
+        const int gp = pick_weights_sums(g.d.w, vb, ve, gr, start_sum, end_sum, gb, ge - gb, lv);
         // a pick one past the node's last group is an empty range in the
         // reference (get_node_group_edge_end, walk_step_helpers.cuh:19-38)
         if (static_cast<uint32_t>(gp) >= ge) continue;
