@@ -475,6 +475,15 @@ __device__ __forceinline__ Hop hop_from_group(const WalkGraph& g, uint32_t gpos,
                   pp.rank);
 }
 
+// Node u's base in the weight search index, loaded beside its header (the
+// pick that reads it comes after the group search): 0 for the index family.
+// (Loaded so in the ExponentialWeight kernel's shared-search loop it ran cfg4
+// 0.7 % slower; that loop reads it after the group search.)
+template <int Fam>
+__device__ __forceinline__ uint32_t wx_base(const WalkGraph& g, uint32_t u) {
+    return (Fam != kFamIndex && g.d.wx) ? g.d.wx_off[u] : 0u;
+}
+
 // Per-hop selector (edge_selectors.cuh:277-443).  The reference first checks
 // the dense active flag; an inactive node has no entries in either direction,
 // so the empty group range below rejects it identically without that load.
@@ -487,7 +496,8 @@ __device__ __forceinline__ Hop hop_from_group(const WalkGraph& g, uint32_t gpos,
 template <bool Fwd, int Fam>
 __device__ __forceinline__ Hop node_edge_from(const WalkGraph& g, int picker, uint32_t u, bool ok,
                                               const NodeHdr& h, int32_t t, int32_t cut, int prev,
-                                              double rg, double re, const double* em1) {
+                                              double rg, double re, const double* em1,
+                                              uint32_t wxo) {
     uint32_t Gu = ok ? (h.meta & kHdrGMask) : 0u;
     if (Gu == kHdrGMask) Gu = g.d.hdr[u + 1].gb - h.gb;  // more groups than 24 bits hold
     if (Gu == 0) return no_hop();
@@ -514,8 +524,7 @@ __device__ __forceinline__ Hop node_edge_from(const WalkGraph& g, int picker, ui
         if (index == -1 || index >= avail) return no_hop();
         gpos = gb + static_cast<uint32_t>(vb + index);
     } else {
-        const double* lv =
-            (g.d.wx && G > static_cast<int>(kWIdxMin)) ? g.d.wx + g.d.wx_off[u] : nullptr;
+        const double* lv = (g.d.wx && G > static_cast<int>(kWIdxMin)) ? g.d.wx + wxo : nullptr;
         if (Fam != kFamWeight && picker == kTemporalNode2Vec && prev != -1)
             return tn2v_pick(g, prev, gb + vb, gb + ve, gb, ge, lv, rg, re);
         // ExponentialWeight, or node2vec's first hop (no previous node)
@@ -533,7 +542,8 @@ __device__ Hop node_edge_at(const WalkGraph& g, int picker, int node, int32_t t,
                             int prev, double rg, double re, const double* em1 = nullptr) {
     if (!(node >= 0 && node < g.active_size)) return no_hop();
     const uint32_t u = static_cast<uint32_t>(node);
-    return node_edge_from<Fwd, Fam>(g, picker, u, true, g.d.hdr[u], t, cut, prev, rg, re, em1);
+    return node_edge_from<Fwd, Fam>(g, picker, u, true, g.d.hdr[u], t, cut, prev, rg, re, em1,
+                                    wx_base<Fam>(g, u));
 }
 
 // Rank bound of a walk's cutoff time: groups at or past it are excluded
@@ -976,13 +986,14 @@ __global__ __launch_bounds__(kB) __attribute__((amdgpu_waves_per_eu(Fam == kFamI
             const bool ok = cur >= 0 && cur < g.active_size;
             const uint32_t u = ok ? static_cast<uint32_t>(cur) : 0u;
             const NodeHdr hd = g.d.hdr[u];
+            const uint32_t wxo = wx_base<Fam>(g, u);
             const uint32_t p = static_cast<uint32_t>(walk_len) + 1;
             DrawPair r = philox_pair(a.ds, w, p);
             asm volatile("" : "+v"(r.a), "+v"(r.b));
             if (a.ds.replay) r = replay_pair(a.ds, w, p);
             const Hop h = node_edge_from<Fwd, Fam>(g, a.walk_bias, u, ok, hd,
                                                    cur_r == neg1 ? -1 : cur_r, cut, prev, r.a,
-                                                   r.b, em1);
+                                                   r.b, em1, wxo);
             // the reference's failure test is ts == -1: no edge, or an edge at -1
             if (h.e == -1 || h.r == neg1) break;
             prev = cur;
@@ -1178,13 +1189,14 @@ __global__ __launch_bounds__(kB) __attribute__((amdgpu_waves_per_eu(4))) void wa
                     const bool ok = cur >= 0 && cur < g.active_size;
                     const uint32_t u = ok ? static_cast<uint32_t>(cur) : 0u;
                     const NodeHdr hd = g.d.hdr[u];
+                    const uint32_t wxo = wx_base<Fam>(g, u);
                     const uint32_t p = static_cast<uint32_t>(k) + 1;
                     DrawPair r = philox_pair(a.ds, w, p);
                     asm volatile("" : "+v"(r.a), "+v"(r.b));
                     if (a.ds.replay) r = replay_pair(a.ds, w, p);
                     const Hop h = node_edge_from<Fwd, Fam>(g, a.walk_bias, u, ok, hd,
                                                            cur_r == neg1 ? -1 : cur_r, cut, prev,
-                                                           r.a, r.b, em1);
+                                                           r.a, r.b, em1, wxo);
                     if (h.e == -1 || h.r == neg1) {
                         alive = false;
                     } else {
@@ -1337,10 +1349,11 @@ __global__ __launch_bounds__(kB) void node_group_segment_kernel(
             const bool ok = s.cur >= 0 && s.cur < g.active_size;
             const uint32_t u = ok ? static_cast<uint32_t>(s.cur) : 0u;
             const NodeHdr hd = g.d.hdr[u];
+            const uint32_t wxo = wx_base<Fam>(g, u);
             const DrawPair r = draw_pair(a.ds, w, static_cast<uint32_t>(s.c));
             const Hop h = node_edge_from<Fwd, Fam>(g, a.walk_bias, u, ok, hd,
                                                    s.r == neg1 ? -1 : s.r, s.cut, s.prev, r.a,
-                                                   r.b, em1);
+                                                   r.b, em1, wxo);
             if (h.e == -1 || h.r == neg1) {
                 keep = false;
                 break;
