@@ -1101,6 +1101,56 @@ __device__ __forceinline__ void rows_out(const WalkArgs& a, uint64_t* buf, int c
     }
 }
 
+// The timestamp rows of a full chunk (NE slots per row, an even row length,
+// 16-byte units of two values) in two phases: rows_ts_fetch looks every value
+// up (uniq_ts or edge_ts loads) into tv before the flush stores anything, and
+// rows_ts_store writes them last.  One vector-memory counter covers loads and
+// stores here, so a lookup issued after a store waits for that store to be
+// acknowledged: looked up round by round between the stores, the lookups
+// serialised the flush on its stores' acknowledgements.
+template <int NE>
+__device__ __forceinline__ void rows_ts_fetch(const WalkArgs& a, uint64_t* buf, int c0, int lane,
+                                              int64_t (&tv)[NE]) {
+    constexpr int U = NE / 2;  // units per row; NE / 2 rounds of 64 units
+    const int nb = a.pk_nb, rb = a.pk_rb;
+    asm volatile("" : "+v"(lane));
+#pragma unroll
+    for (int r = 0; r < U; ++r) {
+        const int t = r * 64 + lane;
+        const int j = t / U;
+        const int lj = row_info(buf, j)->len;
+        const int s0 = (t - j * U) * 2;  // chunk slot of the unit's first value
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const uint64_t word = buf[(s0 + q) * kRowStride + j];
+            tv[2 * r + q] = c0 + s0 + q < lj
+                                ? word_ts(word, nb, rb, a.uniq_ts, a.edge_ts, a.start_ts)
+                                : -1;
+        }
+        // round by round: only the values stay live, not every round's words
+        // and addresses
+        asm volatile("" ::: "memory");
+    }
+}
+
+template <int NE>
+__device__ __forceinline__ void rows_ts_store(const WalkArgs& a, uint64_t* buf, int c0, int lane,
+                                              const int64_t (&tv)[NE]) {
+    constexpr int U = NE / 2;
+    asm volatile("" : "+v"(lane));
+#pragma unroll
+    for (int r = 0; r < U; ++r) {
+        const int t = r * 64 + lane;
+        const int j = t / U;
+        const RowInfo ri = *row_info(buf, j);
+        if (ri.len < 0) continue;
+        const uint64_t at = static_cast<uint64_t>(ri.w) * static_cast<uint64_t>(a.L) + c0 +
+                            (t - j * U) * 2;
+        const i64x2 o = {tv[2 * r], tv[2 * r + 1]};
+        __builtin_nontemporal_store(o, reinterpret_cast<i64x2*>(a.ot + at));
+    }
+}
+
 // Every lane's LDS stores are complete and visible to the whole wave.
 __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -1116,7 +1166,14 @@ __device__ __forceinline__ void rows_flush(const WalkArgs& a, uint64_t* buf, int
     *row_info(buf, lane) = RowInfo{w, live ? len : -1};
     wave_lds_sync();
     const int e0 = c0 > 0 ? c0 - 1 : 0;
-    if (n == C) {
+    if (n == C && a.L % 2 == 0) {
+        int64_t tv[C];
+        rows_ts_fetch<C>(a, buf, c0, lane, tv);
+        rows_out<0, C>(a, buf, c0, c0, C, lane);
+        if (c0 > 0) rows_out<2, C>(a, buf, c0, e0, C, lane);
+        else rows_out<2, C - 1>(a, buf, c0, e0, C - 1, lane);
+        rows_ts_store<C>(a, buf, c0, lane, tv);
+    } else if (n == C) {
         rows_out<0, C>(a, buf, c0, c0, C, lane);
         rows_out<1, C>(a, buf, c0, c0, C, lane);
         if (c0 > 0) rows_out<2, C>(a, buf, c0, e0, C, lane);
