@@ -323,6 +323,13 @@ def test_replay_walks_weight_pickers(directed, forward, picker):
             og.set_weights(name, w)
     _walk_case(og, eng, picker, picker, forward, "total", 24, 4_000, seed=4)
     _walk_case(og, eng, picker, picker, forward, "all_nodes", 12, 1, seed=5)
+    # per-walk cutoffs: the slice's cutoff end moves off the time search's
+    # bound (the hubs' tables hold several groups in some buckets)
+    seeds = np.unique(s[:600]).astype(np.int32)
+    cuts = np.where(np.arange(seeds.size) % 3 == 0, -1,
+                    np.random.default_rng(6).integers(0, 1_000_000, seeds.size)).astype(np.int64)
+    _walk_case(og, eng, picker, picker, forward, "nodes", 16, 3, seed_nodes=seeds, cutoffs=cuts,
+               seed=6)
 
 
 @pytest.mark.parametrize("directed,g", [(True, 300_000), (False, 300_000), (True, 1_200_000)])
@@ -369,6 +376,11 @@ def test_replay_walks_exponential_weight_deep_search_index(directed, g):
         _walk_case(og, eng, "ExponentialWeight", "Uniform", forward, "nodes", 20, 400,
                    seed_nodes=np.array([0, 7, 11], np.int32), seed=73)
         _walk_case(og, eng, "Linear", "ExponentialWeight", forward, "total", 12, 3_000, seed=74)
+        # the hub's single-rank buckets give the time bound and its weight
+        # sum; cutoffs inside its span move the slice's other end
+        _walk_case(og, eng, "ExponentialWeight", "ExponentialWeight", forward, "nodes", 20, 300,
+                   seed_nodes=np.array([0, 0, 0, 7], np.int32),
+                   cutoffs=np.array([g, 2 * g, -1, 3 * g // 2], np.int64), seed=75)
 
 
 def test_replay_walks_powerlaw_exponential_index():
