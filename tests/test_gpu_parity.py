@@ -239,6 +239,76 @@ def test_index_weights_and_adjacency():
         _assert_index_equal(og, eng, weights=True, tn2v=True)
 
 
+def _node_segments(cnt):
+    """(start, end) of every node's groups from count_ts_group_per_node_*."""
+    return [(int(cnt[u]), int(cnt[u + 1])) for u in range(cnt.size - 1) if cnt[u] < cnt[u + 1]]
+
+
+@pytest.mark.parametrize("bound", [-1.0, 0.0, 10.0, 50.0])
+def test_reference_weight_edge_cases(bound):
+    """The reference's small weight cases (test/test_edge_data_weights.cpp:
+    TimescaleBoundZero, SingleTimestampWithBounds, TimescaleBoundPositive;
+    test/test_node_edge_index_weights.cpp: EmptyGraph,
+    SingleTimestampGroupPerNode, TimescaleBoundZero,
+    TimescaleBoundWithSingleTimestamp, WeightBiasPerNode) on the device
+    engine: the same arrays as the oracle, and the reference's own assertions
+    (cumulative arrays non-decreasing to 1 within 1e-6 per segment, one group
+    of weight 1 for a single timestamp, forward weights falling and backward
+    rising in time when the bound scales them)."""
+    def arr(*x):
+        return np.array(x, np.int32)
+
+    # an engine without edges has empty weight arrays
+    og, eng = _pair(True, [], weights=True, timescale_bound=bound)
+    for name in WEIGHT_ARRAYS:
+        assert eng.array(name).size == 0, name
+    eng.close()
+
+    cases = [
+        (arr(1, 1, 2, 2, 3, 4), arr(2, 3, 3, 4, 4, 1), np.array([10, 10, 20, 20, 30, 40])),
+        (arr(1, 2, 3), arr(2, 3, 4), np.array([100, 100, 100])),  # one timestamp
+        (arr(1, 1, 2), arr(2, 3, 3), np.array([10, 10, 10])),     # one group per node
+        (arr(1, 1, 1), arr(2, 3, 4), np.array([10, 20, 30])),     # one node, three groups
+    ]
+    for k, (s, d, t) in enumerate(cases):
+        og, eng = _pair(True, [(s, d, t.astype(np.int64))], weights=True, timescale_bound=bound)
+        _assert_index_equal(og, eng, weights=True)
+        T = np.unique(t).size
+        for name in ("forward_cumulative_weights_exponential",
+                     "backward_cumulative_weights_exponential"):
+            w = eng.array(name)
+            assert w.size == T and np.all(w >= 0) and np.all(np.diff(w) >= 0), name
+            assert abs(w[-1] - 1.0) <= 1e-6, name
+        for name, cnt_name in (
+                ("outbound_forward_cumulative_weights_exponential", "count_ts_group_per_node_outbound"),
+                ("outbound_backward_cumulative_weights_exponential", "count_ts_group_per_node_outbound"),
+                ("inbound_backward_cumulative_weights_exponential", "count_ts_group_per_node_inbound")):
+            w = eng.array(name)
+            for a, b in _node_segments(eng.array(cnt_name)):
+                seg = w[a:b]
+                assert np.all(seg >= 0) and np.all(np.diff(seg) >= 0), name
+                assert abs(seg[-1] - 1.0) <= 1e-6, name
+                if T == 1 or k == 2:
+                    assert b - a == 1, name
+        if k == 0 and bound > 0:
+            # scaled by the bound: earlier groups weigh more forward, later
+            # ones backward (TimescaleBoundPositive)
+            f = np.diff(eng.array("forward_cumulative_weights_exponential"), prepend=0.0)
+            b_ = np.diff(eng.array("backward_cumulative_weights_exponential"), prepend=0.0)
+            assert np.all(np.diff(f) < 0) and np.all(np.diff(b_) > 0)
+        if k == 3:
+            # node 1 with groups at 10, 20, 30 (WeightBiasPerNode): forward
+            # weights fall in time, backward ones rise
+            cnt = eng.array("count_ts_group_per_node_outbound")
+            a, b = int(cnt[1]), int(cnt[2])
+            fw = np.diff(eng.array("outbound_forward_cumulative_weights_exponential")[a:b],
+                         prepend=0.0)
+            bw = np.diff(eng.array("outbound_backward_cumulative_weights_exponential")[a:b],
+                         prepend=0.0)
+            assert np.all(np.diff(fw) < 0) and np.all(np.diff(bw) > 0)
+        eng.close()
+
+
 def _walk_case(og, eng, picker, start_picker, forward, mode, L, n_or_wpn, seed_nodes=None,
                cutoffs=None, seed=0):
     direction = "Forward_In_Time" if forward else "Backward_In_Time"
