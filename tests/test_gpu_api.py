@@ -186,6 +186,73 @@ def test_cutoff_times_bound_every_hop():
         assert bounded_hops > 0 and late_hops_unbounded > 0
 
 
+def _every_edge_before_cutoff(ts, lens, cutoffs, wpn):
+    """expect_every_edge_before_cutoff of test/test_walk_cutoff_times.cpp:63-83:
+    every real edge time of walk w is below its seed slot's cutoff (-1: none)."""
+    sentinel = (np.iinfo(np.int64).min, np.iinfo(np.int64).max)
+    for w, n in enumerate(lens):
+        c = int(cutoffs[w // wpn])
+        if c == -1:
+            continue
+        row = ts[w, :int(n)]
+        row = row[(row != sentinel[0]) & (row != sentinel[1])]
+        assert np.all(row < c), (w, row, c)
+
+
+def test_cutoff_reference_cases():
+    """test/test_walk_cutoff_times.cpp:301-415 on the reference's
+    sample_data.csv (walks of up to 20 slots, 8 per seed, seed-major): a
+    cutoff at the earliest timestamp admits no hop; one past the latest leaves
+    every walk as it is without a cutoff (same engine, same global seed);
+    cutoffs at the midpoint bound every edge, forward and backward; per-seed
+    cutoffs over repeated seeds with one unbounded position bound backward
+    ExponentialWeight walks, directed and undirected."""
+    s, d, t = graphs.sample_data()
+    lo, hi = int(t.min()), int(t.max())
+    L, wpn = 20, 8
+
+    def walks(tw, seeds, bias, direction, cut):
+        return tw.get_random_walks_and_times_for_nodes(
+            np.asarray(seeds, np.int32), max_walk_len=L, walk_bias=bias,
+            num_walks_per_node=wpn, walk_direction=direction,
+            cutoff_times=None if cut is None else np.asarray(cut, np.int64))
+
+    tw = _trw(is_directed=True, global_seed=0xC0FFEE, shuffle_walk_order=False,
+              enable_weight_computation=True)
+    tw.add_multiple_edges(s, d, t)
+    # CutoffBelowAllProducesEmptyWalks
+    _, _, lens, _ = walks(tw, [109, 41, 15], "Uniform", "Backward_In_Time", [lo] * 3)
+    assert int(lens.sum()) == 0
+    # CutoffAboveAllEqualsUnbounded
+    for direction in ("Backward_In_Time", "Forward_In_Time"):
+        bounded = walks(tw, [109, 41, 15, 7], "ExponentialIndex", direction, [hi + 1] * 4)
+        unbounded = walks(tw, [109, 41, 15, 7], "ExponentialIndex", direction, None)
+        for a, b in zip(bounded[:3], unbounded[:3]):
+            np.testing.assert_array_equal(a, b)
+        assert int(bounded[2].sum()) > 4
+    # Backward/ForwardEveryEdgeBeforeCutoff
+    mid = lo + (hi - lo) // 2
+    seeds = [109, 41, 15, 7, 88]
+    for direction in ("Backward_In_Time", "Forward_In_Time"):
+        _, ts, lens, _ = walks(tw, seeds, "ExponentialIndex", direction, [mid] * 5)
+        _every_edge_before_cutoff(ts, lens, [mid] * 5, wpn)
+        if direction == "Backward_In_Time":
+            assert int(lens.sum()) > len(seeds)
+    # HeterogeneousPerSeedCutoffs
+    q1, q2, q3 = lo + (hi - lo) // 4, mid, lo + 3 * (hi - lo) // 4
+    cuts = [q1, q2, -1, q3, q2]
+    _, ts, lens, _ = walks(tw, [109, 109, 109, 41, 15], "ExponentialWeight", "Backward_In_Time",
+                           cuts)
+    _every_edge_before_cutoff(ts, lens, cuts, wpn)
+    # UndirectedBackwardRespectsCutoff
+    tu = _trw(is_directed=False, global_seed=0xC0FFEE, shuffle_walk_order=False,
+              enable_weight_computation=True)
+    tu.add_multiple_edges(s, d, t)
+    _, ts, lens, _ = walks(tu, [109, 41, 15], "ExponentialWeight", "Backward_In_Time", [mid] * 3)
+    _every_edge_before_cutoff(ts, lens, [mid] * 3, wpn)
+    assert int(lens.sum()) > 3
+
+
 def test_last_batch_starts_only_from_batch_sources():
     tw = _trw(is_directed=True, global_seed=3)
     tw.add_multiple_edges(np.array([1, 2], np.int32), np.array([2, 3], np.int32),
