@@ -253,6 +253,59 @@ def test_cutoff_reference_cases():
     assert int(lens.sum()) > 3
 
 
+@pytest.mark.parametrize("picker,wpn", [("Linear", 10), ("ExponentialWeight", 100)])
+def test_walks_end_only_where_no_edge_continues(picker, wpn):
+    """test/test_temporal_random_walk.cpp:246-570 (WalkCountAndLens,
+    WalkIncreasingTimestamp, WalkValidEdges, WalkTerminalEdges and their
+    ExponentialWeight forms) on the reference's sample_data.csv, directed,
+    walks of up to 20 slots from every node: lengths are 0 or in [2, 20];
+    every step is an edge of the graph at the step's time, times rise along
+    the walk; a forward walk shorter than 20 ends at a node with no edge after
+    its last time, a backward one starts at a node with no edge into it
+    before its first time."""
+    s, d, t = graphs.sample_data()
+    L = 20
+    tw = _trw(is_directed=True, enable_weight_computation=True, global_seed=17)
+    tw.add_multiple_edges(s, d, t)
+    n_id = int(max(s.max(), d.max())) + 1
+    uniq = np.unique(t)
+    edge_keys = np.unique((s.astype(np.int64) * n_id + d) * (uniq.size + 1) +
+                          np.searchsorted(uniq, t))
+    max_out = np.full(n_id, np.iinfo(np.int64).min)
+    np.maximum.at(max_out, s, t)
+    min_in = np.full(n_id, np.iinfo(np.int64).max)
+    np.minimum.at(min_in, d, t)
+
+    def are_edges(a, b, ts):
+        r = np.searchsorted(uniq, ts)
+        ok = (r < uniq.size) & (uniq[np.minimum(r, uniq.size - 1)] == ts)
+        keys = (a.astype(np.int64) * n_id + b) * (uniq.size + 1) + r
+        return ok & np.isin(keys, edge_keys)
+
+    for direction in ("Forward_In_Time", "Backward_In_Time"):
+        nodes, ts, lens, _ = tw.get_random_walks_and_times_for_all_nodes(
+            max_walk_len=L, walk_bias=picker, num_walks_per_node=wpn, walk_direction=direction)
+        lens = lens.astype(np.int64)
+        assert np.all((lens == 0) | ((lens >= 2) & (lens <= L)))
+        assert lens[lens > 0].mean() > 2
+        fwd = direction == "Forward_In_Time"
+        for n in range(2, L + 1):
+            rows = np.nonzero(lens == n)[0]
+            if rows.size == 0:
+                continue
+            nd, tt = nodes[rows, :n], ts[rows, :n]
+            # edge times: slots 1.. forward, slots ..n-2 backward (the other
+            # end holds the direction's sentinel)
+            et = tt[:, 1:] if fwd else tt[:, :-1]
+            assert np.all(np.diff(et, axis=1) > 0)
+            assert np.all(are_edges(nd[:, :-1], nd[:, 1:], et)), (direction, n)
+            if n < L:
+                if fwd:
+                    assert np.all(max_out[nd[:, -1]] <= et[:, -1]), (direction, n)
+                else:
+                    assert np.all(min_in[nd[:, 0]] >= et[:, 0]), (direction, n)
+
+
 def test_last_batch_starts_only_from_batch_sources():
     tw = _trw(is_directed=True, global_seed=3)
     tw.add_multiple_edges(np.array([1, 2], np.int32), np.array([2, 3], np.int32),
