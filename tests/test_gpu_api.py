@@ -253,8 +253,9 @@ def test_cutoff_reference_cases():
     assert int(lens.sum()) > 3
 
 
-@pytest.mark.parametrize("picker,wpn", [("Linear", 10), ("ExponentialWeight", 100)])
-def test_walks_end_only_where_no_edge_continues(picker, wpn):
+@pytest.mark.parametrize("picker,wpn,bound", [("Linear", 10, -1.0), ("ExponentialWeight", 100, -1.0),
+                                               ("ExponentialWeight", 20, 10.0)])
+def test_walks_end_only_where_no_edge_continues(picker, wpn, bound):
     """test/test_temporal_random_walk.cpp:246-570 (WalkCountAndLens,
     WalkIncreasingTimestamp, WalkValidEdges, WalkTerminalEdges and their
     ExponentialWeight forms) on the reference's sample_data.csv, directed,
@@ -262,10 +263,12 @@ def test_walks_end_only_where_no_edge_continues(picker, wpn):
     every step is an edge of the graph at the step's time, times rise along
     the walk; a forward walk shorter than 20 ends at a node with no edge after
     its last time, a backward one starts at a node with no edge into it
-    before its first time."""
+    before its first time.  Timescale bound 10: TimescaleBoundedTemporalRandomWalkTest
+    (ValidEdgesWithScaling, TerminalEdgeValidation)."""
     s, d, t = graphs.sample_data()
     L = 20
-    tw = _trw(is_directed=True, enable_weight_computation=True, global_seed=17)
+    tw = _trw(is_directed=True, enable_weight_computation=True, global_seed=17,
+              timescale_bound=bound)
     tw.add_multiple_edges(s, d, t)
     n_id = int(max(s.max(), d.max())) + 1
     uniq = np.unique(t)
