@@ -309,6 +309,54 @@ def test_reference_weight_edge_cases(bound):
         eng.close()
 
 
+def test_reference_cutoff_selector_cases():
+    """test/test_walk_cutoff_times.cpp:163-252 (ForwardCutoffUpperBound,
+    BackwardCutoffUpperBound, CutoffBoundaryIsExclusive): get_node_edge_at
+    with the TEST_FIRST / TEST_LAST pickers, no time bound and a cutoff, read
+    as the start edge of a two-slot walk from the node (its start selection is
+    that call); an invalid edge is a walk of length 0."""
+    I64 = np.int64
+
+    def start_edge(eng, node, picker, forward, cutoff):
+        got = eng.sample("nodes", 2, picker, 1, initial_edge_bias=picker,
+                         direction="Forward_In_Time" if forward else "Backward_In_Time",
+                         seed_nodes=np.array([node], np.int32),
+                         cutoff_times=np.array([cutoff], I64), shuffle=False)
+        n = int(got.lens[0])
+        if n == 0:
+            return None
+        assert n == 2
+        nd, ts = got.nodes[0], got.timestamps[0]
+        return (int(nd[0]), int(nd[1]), int(ts[1] if forward else ts[0]))
+
+    def engine(edges):
+        e = _engine(is_directed=True, global_seed=5, shuffle_walk_order=False)
+        s, d, t = (np.array(x) for x in zip(*edges))
+        e.add_edges(s.astype(np.int32), d.astype(np.int32), t.astype(I64))
+        return e
+
+    F, L_, NONE = "TEST_FIRST", "TEST_LAST", -1
+    fwd = engine([(10, 20, 100), (10, 30, 101), (10, 40, 102), (10, 50, 103), (10, 60, 104)])
+    for picker, cut, want in [(F, NONE, (10, 20, 100)), (L_, NONE, (10, 60, 104)),
+                              (L_, 104, (10, 50, 103)), (L_, 103, (10, 40, 102)),
+                              (F, 101, (10, 20, 100)), (F, 100, None), (F, 50, None),
+                              (L_, 1000, (10, 60, 104))]:
+        assert start_edge(fwd, 10, picker, True, cut) == want, (picker, cut)
+    fwd.close()
+    bwd = engine([(20, 10, 100), (30, 10, 101), (40, 10, 102), (50, 10, 103), (60, 10, 104)])
+    for picker, cut, want in [(F, NONE, (20, 10, 100)), (L_, NONE, (60, 10, 104)),
+                              (L_, 104, (50, 10, 103)), (L_, 102, (30, 10, 101)),
+                              (F, 101, (20, 10, 100)), (F, 100, None),
+                              (L_, 1000, (60, 10, 104))]:
+        assert start_edge(bwd, 10, picker, False, cut) == want, (picker, cut)
+    bwd.close()
+    both = engine([(10, 20, 100), (10, 30, 110), (10, 40, 120),
+                   (50, 70, 100), (60, 70, 110), (80, 70, 120)])
+    assert start_edge(both, 10, L_, True, 110) == (10, 20, 100)
+    assert start_edge(both, 70, L_, False, 110) == (50, 70, 100)
+    both.close()
+
+
 def _walk_case(og, eng, picker, start_picker, forward, mode, L, n_or_wpn, seed_nodes=None,
                cutoffs=None, seed=0):
     direction = "Forward_In_Time" if forward else "Backward_In_Time"
