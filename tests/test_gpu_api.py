@@ -309,6 +309,33 @@ def test_walks_end_only_where_no_edge_continues(picker, wpn, bound):
                     assert np.all(min_in[nd[:, 0]] >= et[:, 0]), (direction, n)
 
 
+def test_reference_node_and_edge_counts():
+    """test/test_temporal_random_walk.cpp:116-168 (ConstructorTest,
+    AddEdgeTest, WhenMaxTimeCapacityExceedsEdgesAreDeletedAutomatically with
+    max_time_capacity 5): node and edge counts of the engine, through the
+    window's evictions."""
+    def add(tw, edges):
+        s, d, t = (np.array(x) for x in zip(*edges))
+        tw.add_multiple_edges(s.astype(np.int32), d.astype(np.int32), t.astype(np.int64))
+
+    tw = _trw(is_directed=True)
+    assert tw.get_node_count() == 0
+    add(tw, [(1, 2, 100), (2, 3, 101), (7, 8, 102), (1, 7, 103), (3, 2, 103), (10, 11, 104)])
+    assert tw.get_edge_count() == 6 and tw.get_node_count() == 7
+
+    tw = _trw(is_directed=True, max_time_capacity=5, enable_weight_computation=True,
+              timescale_bound=-1.0)
+    steps = [
+        ([(0, 2, 1), (2, 3, 3), (1, 9, 2), (2, 4, 3), (2, 4, 1), (1, 5, 4)], 7, 6),
+        ([(5, 6, 4), (2, 5, 4), (4, 3, 5)], 8, 9),
+        ([(1, 7, 6)], 8, 8),
+        ([(1, 5, 7), (4, 7, 8)], 7, 7),
+    ]
+    for edges, nodes, n_edges in steps:
+        add(tw, edges)
+        assert tw.get_node_count() == nodes and tw.get_edge_count() == n_edges, edges
+
+
 def test_last_batch_starts_only_from_batch_sources():
     tw = _trw(is_directed=True, global_seed=3)
     tw.add_multiple_edges(np.array([1, 2], np.int32), np.array([2, 3], np.int32),
