@@ -357,6 +357,45 @@ def test_reference_cutoff_selector_cases():
     both.close()
 
 
+@pytest.mark.parametrize("forward", [True, False])
+def test_reference_node2vec_rejection_cases(forward):
+    """test/test_temporal_node2vec_rejection.cpp:171-260 on the device's
+    in-kernel draws: at V with previous node P, the candidates P (beta 1/p),
+    N (a neighbour of P, beta 1) and F (beta 1/q) are taken in the analytic
+    proportions within 0.025 over 10,000 hops, across the reference's (p, q)
+    sweep, and under the degenerate p = 0.1, q = 10 every hop still returns
+    one of them.  The previous node is set only after a walk's first loop hop
+    (temporal_random_walk_cpu.cuh:65, 116-120), so the hop is the last of a
+    four-slot walk seeded at S: S -> P (start edge), P -> V (the only edge
+    on), then V's pick with P behind it (forward: S->P at 5, P->V at 10, P->N
+    at 2; backward: P->S at 300, V->P at 200, P->N at 50)."""
+    V, P, N, F, S = 0, 1, 2, 3, 4
+    if forward:
+        edges = [(V, P, 100), (V, N, 100), (V, F, 100), (P, N, 2), (S, P, 5), (P, V, 10)]
+    else:
+        edges = [(P, V, 100), (N, V, 100), (F, V, 100), (P, N, 50), (V, P, 200), (P, S, 300)]
+    s, d, t = (np.array(x) for x in zip(*edges))
+    n = 10_000
+    for p, q in [(1.0, 1.0), (1.0, 2.0), (0.5, 2.0), (2.0, 0.5), (0.25, 4.0), (0.1, 10.0)]:
+        eng = _engine(is_directed=True, enable_weight_computation=True,
+                      enable_temporal_node2vec=True, timescale_bound=-1.0, node2vec_p=p,
+                      node2vec_q=q, global_seed=31, shuffle_walk_order=False)
+        eng.add_edges(s.astype(np.int32), d.astype(np.int32), t.astype(np.int64))
+        w = eng.sample("nodes", 4, "TemporalNode2Vec", n, initial_edge_bias="TEST_FIRST",
+                       direction="Forward_In_Time" if forward else "Backward_In_Time",
+                       seed_nodes=np.array([S], np.int32), shuffle=False)
+        assert np.all(w.lens == 4), (p, q)
+        path = w.nodes[:, :3] if forward else w.nodes[:, 1:][:, ::-1]
+        assert np.all(path == [S, P, V])
+        cand = w.nodes[:, 3] if forward else w.nodes[:, 0]
+        assert np.all(np.isin(cand, [P, N, F])), (p, q)
+        wts = np.array([1.0 / p, 1.0, 1.0 / q])
+        want = wts / wts.sum()
+        got = np.array([(cand == c).mean() for c in (P, N, F)])
+        assert np.all(np.abs(got - want) <= 0.025), (p, q, got, want)
+        eng.close()
+
+
 def _walk_case(og, eng, picker, start_picker, forward, mode, L, n_or_wpn, seed_nodes=None,
                cutoffs=None, seed=0):
     direction = "Forward_In_Time" if forward else "Backward_In_Time"
