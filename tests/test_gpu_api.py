@@ -253,9 +253,10 @@ def test_cutoff_reference_cases():
     assert int(lens.sum()) > 3
 
 
-@pytest.mark.parametrize("picker,wpn,bound", [("Linear", 10, -1.0), ("ExponentialWeight", 100, -1.0),
-                                               ("ExponentialWeight", 20, 10.0)])
-def test_walks_end_only_where_no_edge_continues(picker, wpn, bound):
+@pytest.mark.parametrize("picker,wpn,bound,directed", [
+    ("Linear", 10, -1.0, True), ("ExponentialWeight", 100, -1.0, True),
+    ("ExponentialWeight", 20, 10.0, True), ("Linear", 10, -1.0, False)])
+def test_walks_end_only_where_no_edge_continues(picker, wpn, bound, directed):
     """test/test_temporal_random_walk.cpp:246-570 (WalkCountAndLens,
     WalkIncreasingTimestamp, WalkValidEdges, WalkTerminalEdges and their
     ExponentialWeight forms) on the reference's sample_data.csv, directed,
@@ -264,12 +265,15 @@ def test_walks_end_only_where_no_edge_continues(picker, wpn, bound):
     the walk; a forward walk shorter than 20 ends at a node with no edge after
     its last time, a backward one starts at a node with no edge into it
     before its first time.  Timescale bound 10: TimescaleBoundedTemporalRandomWalkTest
-    (ValidEdgesWithScaling, TerminalEdgeValidation)."""
+    (ValidEdgesWithScaling, TerminalEdgeValidation).  Undirected
+    (FilledUndirectedTemporalRandomWalkTest): an edge serves both ways."""
     s, d, t = graphs.sample_data()
     L = 20
-    tw = _trw(is_directed=True, enable_weight_computation=True, global_seed=17,
+    tw = _trw(is_directed=directed, enable_weight_computation=True, global_seed=17,
               timescale_bound=bound)
     tw.add_multiple_edges(s, d, t)
+    if not directed:
+        s, d, t = np.concatenate([s, d]), np.concatenate([d, s]), np.concatenate([t, t])
     n_id = int(max(s.max(), d.max())) + 1
     uniq = np.unique(t)
     edge_keys = np.unique((s.astype(np.int64) * n_id + d) * (uniq.size + 1) +
