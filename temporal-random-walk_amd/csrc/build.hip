@@ -614,40 +614,112 @@ __global__ void node_table_fill_kernel(const uint32_t* __restrict__ key,
     if (i == G - 1) t[bi + 1] = G;
 }
 
-// Weight search index (see engine.h): entries per node, then one thread per
-// group writes its cumulative weight into every level whose stride divides
-// its local index; the segment's last group writes the +inf padding.  With
-// key == nullptr the whole array [0, ng) is one segment (global weights).
-__global__ void wx_sizes_kernel(const uint32_t* __restrict__ cnt, size_t v,
-                                uint32_t* __restrict__ sizes) {
-    const size_t u = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
-    if (u >= v) return;
-    sizes[u] = wx_size(cnt[u + 1] - cnt[u]);
+// Guide parameters (index_layout.h) of the segment c[0, G): the smallest
+// bucket shift (at least 4, so the first bucket's key fits 58 bits) that gives
+// at most kWgBucketsPerGroup * G buckets over the segment's keys.
+__device__ __forceinline__ WGuide make_guide(const double* c, uint32_t G, bool decaying) {
+    WGuide gd{0, G ? c[G - 1] : 0.0};
+    if (G > kWGuideMin) {
+        const int64_t kf = wg_key(c[0], decaying), kl = wg_key(c[G - 1], decaying);
+        const int64_t lim = std::min<int64_t>(static_cast<int64_t>(G) * kWgBucketsPerGroup,
+                                              0xfffffffeLL);
+        int sh = 4;
+        while ((kl >> sh) - (kf >> sh) + 1 > lim) ++sh;
+        gd.bs = (static_cast<uint64_t>(kf >> sh) << 6) | static_cast<uint64_t>(sh);
+    }
+    return gd;
 }
 
-__global__ void wx_fill_kernel(const double* __restrict__ w, const uint32_t* __restrict__ key,
-                               const uint32_t* __restrict__ grp, const uint32_t* __restrict__ cnt,
-                               const uint32_t* __restrict__ off, size_t ng,
-                               double* __restrict__ wx) {
+// The weight pickers' node headers: the walk header of every node and the
+// guide of its cumulative weights (the terminator entry V_c - 1 has none).
+__global__ void whdr_kernel(const double* __restrict__ w, const uint32_t* __restrict__ cnt,
+                            const NodeHdr* __restrict__ hdr, size_t vc, int decaying,
+                            WNodeHdr* __restrict__ out) {
+    const size_t u = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (u >= vc) return;
+    const uint32_t gb = cnt[u];
+    const uint32_t G = u + 1 < vc ? cnt[u + 1] - gb : 0u;
+    out[u] = WNodeHdr{hdr[u], make_guide(w + gb, G, decaying != 0)};
+}
+
+// The guide of a global cumulative array (one segment).
+__global__ void global_guide_kernel(const double* __restrict__ w, size_t n, int decaying,
+                                    WGuide* __restrict__ out) {
+    out[0] = make_guide(w, static_cast<uint32_t>(n), decaying != 0);
+}
+
+// The weighted panel: every group's panel record with its cumulative weight,
+// plus the panel's terminator.
+__global__ void wpan_kernel(const PanelRec* __restrict__ pan, const double* __restrict__ w,
+                            size_t ng, WPanelRec* __restrict__ out) {
     const size_t g = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
-    if (g >= ng) return;
-    uint32_t gb = 0, G = static_cast<uint32_t>(ng), base = 0;
+    if (g > ng) return;
+    const PanelRec p = pan[g];
+    out[g] = WPanelRec{p.rank, p.start, g < ng ? w[g] : 0.0};
+}
+
+// The buckets [from, to] of group g (local index i of a segment of G): those
+// after its predecessor's bucket up to its own, all of which first reach group
+// i.  Segments are the nodes of a direction (key, grp, cnt, whdr) or, with
+// key == nullptr, the whole array under the guide gg.
+struct WgRun {
+    uint32_t* t;  // the segment's table (nullptr: none)
+    uint32_t i, from, to, G;
+};
+__device__ __forceinline__ WgRun wg_run(const double* w, const uint32_t* key, const uint32_t* grp,
+                                        const uint32_t* cnt, const WNodeHdr* whdr,
+                                        const WGuide* gg, size_t ng, int decaying, uint32_t* tab,
+                                        size_t g) {
+    uint32_t u = 0, gb = 0, G = static_cast<uint32_t>(ng);
+    uint64_t bs;
     if (key) {
-        const uint32_t u = key[grp[g]];
+        u = key[grp[g]];
         gb = cnt[u];
         G = cnt[u + 1] - gb;
-        base = off[u];
+        bs = whdr[u].g.bs;
+    } else {
+        bs = gg->bs;
     }
-    if (G <= kWIdxMin) return;
-    const uint32_t i = static_cast<uint32_t>(g) - gb;
-    uint32_t loff = 0;
-    for (uint64_t span = wx_top_span(G);; span >>= 4) {
-        const uint32_t n = wx_level_entries(G, span);
-        if (i % span == 0) wx[base + loff + static_cast<uint32_t>(i / span)] = w[g];
-        if (i == G - 1)
-            for (uint32_t p = n; p < wx_pad16(n); ++p) wx[base + loff + p] = __builtin_huge_val();
-        loff += wx_pad16(n);
-        if (span == 16) break;
+    WgRun r{nullptr, 0, 0, 0, G};
+    if (G <= kWGuideMin) return r;
+    r.t = tab + (key ? 2ull * (static_cast<uint64_t>(gb) + u) : 0ull);
+    r.i = static_cast<uint32_t>(g) - gb;
+    r.to = wg_bucket(bs, wg_key(w[g], decaying != 0));
+    r.from = r.i == 0 ? 0u : wg_bucket(bs, wg_key(w[g - 1], decaying != 0)) + 1;
+    return r;
+}
+
+// One thread per group writes its run of buckets, or -- for a run longer than
+// kWgRun -- lists the group for wg_long_kernel; the segment's last group also
+// writes the closing entry G after its own bucket, the last.
+__global__ void wg_fill_kernel(const double* __restrict__ w, const uint32_t* __restrict__ key,
+                               const uint32_t* __restrict__ grp, const uint32_t* __restrict__ cnt,
+                               const WNodeHdr* __restrict__ whdr, const WGuide* __restrict__ gg,
+                               size_t ng, int decaying, uint32_t* __restrict__ tab,
+                               uint32_t* __restrict__ longs) {
+    const size_t g = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (g >= ng) return;
+    const WgRun r = wg_run(w, key, grp, cnt, whdr, gg, ng, decaying, tab, g);
+    if (r.t == nullptr) return;
+    if (r.to + 1 > r.from + kWgRun) {
+        longs[1 + atomicAdd(longs, 1u)] = static_cast<uint32_t>(g);
+    } else {
+        for (uint32_t b = r.from; b <= r.to; ++b) r.t[b] = r.i;
+    }
+    if (r.i == r.G - 1) r.t[r.to + 1] = r.G;
+}
+
+// The listed long runs, one workgroup at a time (longs[0] holds the count).
+__global__ __launch_bounds__(256) void wg_long_kernel(
+    const double* __restrict__ w, const uint32_t* __restrict__ key, const uint32_t* __restrict__ grp,
+    const uint32_t* __restrict__ cnt, const WNodeHdr* __restrict__ whdr,
+    const WGuide* __restrict__ gg, size_t ng, int decaying, uint32_t* __restrict__ tab,
+    const uint32_t* __restrict__ longs) {
+    const uint32_t n = longs[0];
+    for (uint32_t k = blockIdx.x; k < n; k += gridDim.x) {
+        const WgRun r = wg_run(w, key, grp, cnt, whdr, gg, ng, decaying, tab, longs[1 + k]);
+        for (uint64_t b = static_cast<uint64_t>(r.from) + threadIdx.x; b <= r.to; b += blockDim.x)
+            r.t[b] = r.i;
     }
 }
 
@@ -1265,43 +1337,52 @@ void node_weights(Engine& e, DirIndex& dir, size_t v, double bound, bool compute
     check_hip(hipGetLastError(), "node weights launch");
 }
 
-// Weight search indexes of one direction's per-node cumulative weights.
-void build_weight_index(Engine& e, DirIndex& dir, size_t v, int64_t* host_scratch) {
+// Guide tables of one cumulative weight array (index_layout.h), its guides
+// already written: per node of a direction (key, grp, cnt, whdr) or, with
+// key == nullptr, the whole array under the guide gg.  Each bucket is written
+// once: by its group's thread, or for a run of more than kWgRun buckets (the
+// weights jumping by orders of magnitude) by a workgroup of wg_long_kernel.
+void fill_weight_guides(Engine& e, const double* w, size_t ng, const uint32_t* key,
+                        const uint32_t* grp, const uint32_t* cnt, const WNodeHdr* whdr,
+                        const WGuide* gg, bool decaying, uint32_t* tab, size_t tsize) {
+    if (ng == 0) return;
     hipStream_t s = e.stream;
-    const size_t vc = v + 1;
-    e.flags.ensure(vc);
-    e.scan.ensure(vc);
-    e.scan_scratch.ensure(scan_scratch_elems(vc));
-    hipLaunchKernelGGL(wx_sizes_kernel, dim3(grid_for(v)), dim3(kB), 0, s, dir.cnt.p, v, e.flags.p);
-    exclusive_scan_u32(e.flags.p, e.scan.p, v, e.scan_scratch.p, s);
-    dir.wx_off.resize(vc);
-    check_hip(hipMemcpyAsync(dir.wx_off.p, e.scan.p, vc * 4, hipMemcpyDeviceToDevice, s),
-              "copy wx offsets");
-    check_hip(hipMemcpyAsync(host_scratch, e.scan.p + v, 4, hipMemcpyDeviceToHost, s), "read wx");
-    e.sync();
-    uint32_t total = 0;
-    std::memcpy(&total, host_scratch, 4);
-    const size_t g = dir.n_groups;
-    DBuf<double>* dst[2] = {&dir.wx_fwd, &dir.wx_bwd};
-    const DBuf<double>* src[2] = {&dir.w_fwd, &dir.w_bwd};
-    for (int k = 0; k < 2; ++k) {
-        const bool have = src[k]->n == g && g > 0;
-        dst[k]->resize(have ? total : 0);
-        if (have && total)
-            hipLaunchKernelGGL(wx_fill_kernel, dim3(grid_for(g)), dim3(kB), 0, s, src[k]->p,
-                               dir.key.p, dir.grp.p, dir.cnt.p, dir.wx_off.p, g, dst[k]->p);
-    }
-    check_hip(hipGetLastError(), "weight index launch");
+    e.wg_long.ensure(tsize / kWgRun + 2);
+    check_hip(hipMemsetAsync(e.wg_long.p, 0, 4, s), "guide long-run count");
+    hipLaunchKernelGGL(wg_fill_kernel, dim3(grid_for(ng)), dim3(kB), 0, s, w, key, grp, cnt, whdr,
+                       gg, ng, decaying ? 1 : 0, tab, e.wg_long.p);
+    hipLaunchKernelGGL(wg_long_kernel, dim3(256), dim3(256), 0, s, w, key, grp, cnt, whdr, gg, ng,
+                       decaying ? 1 : 0, tab, e.wg_long.p);
 }
 
-// Weight search index of a global cumulative array (one segment of n).
-void build_global_weight_index(Engine& e, const DBuf<double>& w, size_t n, DBuf<double>& wx) {
-    const uint32_t total = wx_size(static_cast<uint32_t>(n));
-    wx.resize(total);
-    if (total)
-        hipLaunchKernelGGL(wx_fill_kernel, dim3(grid_for(n)), dim3(kB), 0, e.stream, w.p, nullptr,
-                           nullptr, nullptr, nullptr, n, wx.p);
-    check_hip(hipGetLastError(), "global weight index launch");
+// The weight pickers' view of one direction's cumulative weights w (forward
+// weights decay, backward weights grow: node_edge_index.cu:540-575).
+void build_walk_weights(Engine& e, DirIndex& dir, size_t v, const DBuf<double>& w, bool decaying,
+                        WalkWeights& ww) {
+    hipStream_t s = e.stream;
+    const size_t vc = v + 1, g = dir.n_groups;
+    ww.hdr.resize(vc);
+    ww.pan.resize(g + 1);
+    ww.tab.resize(2 * (g + v));
+    hipLaunchKernelGGL(whdr_kernel, dim3(grid_for(vc)), dim3(kB), 0, s, w.p, dir.cnt.p, dir.hdr.p,
+                       vc, decaying ? 1 : 0, ww.hdr.p);
+    hipLaunchKernelGGL(wpan_kernel, dim3(grid_for(g + 1)), dim3(kB), 0, s, dir.pan.p, w.p, g,
+                       ww.pan.p);
+    fill_weight_guides(e, w.p, g, dir.key.p, dir.grp.p, dir.cnt.p, ww.hdr.p, nullptr, decaying,
+                       ww.tab.p, ww.tab.n);
+    check_hip(hipGetLastError(), "walk weights launch");
+}
+
+// The guide of a global cumulative array (one segment of n).
+void build_global_guide(Engine& e, const DBuf<double>& w, size_t n, bool decaying,
+                        DBuf<WGuide>& gd, DBuf<uint32_t>& tab) {
+    gd.resize(1);
+    tab.resize(2 * n + 1);
+    hipLaunchKernelGGL(global_guide_kernel, dim3(1), dim3(1), 0, e.stream, w.p, n,
+                       decaying ? 1 : 0, gd.p);
+    fill_weight_guides(e, w.p, n, nullptr, nullptr, nullptr, nullptr, gd.p, decaying, tab.p,
+                       tab.n);
+    check_hip(hipGetLastError(), "global guide launch");
 }
 
 // The batch alone, sorted stably by timestamp: keys ts - btmin (32-bit when the
@@ -1894,8 +1975,8 @@ void Engine::build_accepted(const int32_t* d_src, const int32_t* d_dst, const in
         // lower_bound only on a non-decreasing array
         running_max_f64(fwd_cum.p, T, fscan_scratch.p, s);
         running_max_f64(bwd_cum.p, T, fscan_scratch.p, s);
-        build_global_weight_index(*this, fwd_cum, T, gwx_fwd);
-        build_global_weight_index(*this, bwd_cum, T, gwx_bwd);
+        build_global_guide(*this, fwd_cum, T, true, gwg_fwd, gwt_fwd);
+        build_global_guide(*this, bwd_cum, T, false, gwg_bwd, gwt_bwd);
         // per node (node_edge_index.cu:644-684): outbound forward + backward,
         // inbound backward (directed)
         out.w_fwd.resize(out.n_groups);
@@ -1905,8 +1986,11 @@ void Engine::build_accepted(const int32_t* d_src, const int32_t* d_dst, const in
             in.w_bwd.resize(in.n_groups);
             node_weights(*this, in, v, bound, false, hs);
         }
-        build_weight_index(*this, out, v, hs);
-        if (cfg.is_directed) build_weight_index(*this, in, v, hs);
+        // the weight pickers' views: forward walks read out's forward
+        // weights, backward walks in's backward weights (out's if undirected)
+        build_walk_weights(*this, out, v, out.w_fwd, true, out.wf);
+        if (cfg.is_directed) build_walk_weights(*this, in, v, in.w_bwd, false, in.wb);
+        else build_walk_weights(*this, out, v, out.w_bwd, false, out.wb);
         check_hip(hipGetLastError(), "weights launch");
         weights_ready = true;
     }
@@ -1960,7 +2044,8 @@ void Engine::clear() {
     max_node_id = -1;
     store_tmin = store_tmax = 0;
     src.n = dst.n = ts.n = feat.n = tsg_off.n = uniq_ts.n = erank.n = neg1_rank.n = active.n = 0;
-    fwd_cum.n = bwd_cum.n = gwx_fwd.n = gwx_bwd.n = adj_off.n = adj_nbr.n = adj_hash.n = 0;
+    fwd_cum.n = bwd_cum.n = adj_off.n = adj_nbr.n = adj_hash.n = 0;
+    gwg_fwd.n = gwg_bwd.n = gwt_fwd.n = gwt_bwd.n = 0;
     weights_ready = adj_ready = adj_lists_ready = false;
     adj_nodes = 0;
     out.clear();

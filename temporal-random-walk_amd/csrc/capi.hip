@@ -40,14 +40,16 @@ Engine::~Engine() {
 
 size_t Engine::memory_used() const {
     size_t b = src.bytes() + dst.bytes() + ts.bytes() + feat.bytes() + tsg_off.bytes() +
-               uniq_ts.bytes() + erank.bytes() + gwx_fwd.bytes() + gwx_bwd.bytes() + active.bytes() + fwd_cum.bytes() + bwd_cum.bytes() +
-               adj_off.bytes() + adj_nbr.bytes();
+               uniq_ts.bytes() + erank.bytes() + active.bytes() + fwd_cum.bytes() +
+               bwd_cum.bytes() + gwg_fwd.bytes() + gwg_bwd.bytes() + gwt_fwd.bytes() +
+               gwt_bwd.bytes() + adj_off.bytes() + adj_nbr.bytes() + adj_hash.bytes();
     for (const DirIndex* d : {&out, &in}) {
-        b += d->off.bytes() + d->idx.bytes() + d->cnt.bytes() + d->grp.bytes() +
+        b += d->off.bytes() + d->idx.bytes() + d->rec.bytes() + d->cnt.bytes() + d->grp.bytes() +
              d->first_ts.bytes() + d->pan.bytes() + d->hdr.bytes() + d->tab.bytes() +
-             d->wx_off.bytes() + d->wx_fwd.bytes() + d->wx_bwd.bytes() + d->w_fwd.bytes() + d->w_bwd.bytes();
+             d->w_fwd.bytes() + d->w_bwd.bytes() + d->wf.bytes() + d->wb.bytes();
     }
-    return b;
+    // blocks of grown buffers held until the next clear() (DBuf::ensure)
+    return b + retired.bytes;
 }
 
 }  // namespace trw

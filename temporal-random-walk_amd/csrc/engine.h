@@ -143,6 +143,17 @@ struct SampleTarget {
     float* feat;
 };
 
+// A walk direction's view of its cumulative weights for the weight pickers
+// (index_layout.h): node headers with guide parameters, the weighted panel and
+// the guide tables.
+struct WalkWeights {
+    DBuf<WNodeHdr> hdr;  // V_c
+    DBuf<WPanelRec> pan;  // g + 1
+    DBuf<uint32_t> tab;   // 2 (g + V_c - 1)
+    void clear() { hdr.n = pan.n = tab.n = 0; }
+    size_t bytes() const { return hdr.bytes() + pan.bytes() + tab.bytes(); }
+};
+
 struct DirIndex {
     DBuf<uint32_t> off;      // V_c
     DBuf<uint32_t> idx;      // n entries
@@ -156,15 +167,18 @@ struct DirIndex {
     DBuf<uint32_t> tab;      // bucket tables
     DBuf<double> w_fwd;      // g (outbound only)
     DBuf<double> w_bwd;      // g
-    DBuf<uint32_t> wx_off;   // V_c
-    DBuf<double> wx_fwd, wx_bwd;
+    // weight pickers' views: of w_fwd for forward walks (out), of w_bwd for
+    // backward walks (in; out if undirected)
+    WalkWeights wf, wb;
     size_t n_entries = 0;
     size_t n_groups = 0;
     bool present = false;
 
     void clear() {
         off.n = idx.n = rec.n = key.n = cnt.n = grp.n = first_ts.n = pan.n = hdr.n = tab.n = w_fwd.n =
-            w_bwd.n = wx_off.n = wx_fwd.n = wx_bwd.n = 0;
+            w_bwd.n = 0;
+        wf.clear();
+        wb.clear();
         n_entries = n_groups = 0;
         present = false;
     }
@@ -225,7 +239,9 @@ struct Engine {
 
     // global weights
     DBuf<double> fwd_cum, bwd_cum;
-    DBuf<double> gwx_fwd, gwx_bwd;
+    DBuf<WGuide> gwg_fwd, gwg_bwd;      // their guides (one segment each)
+    DBuf<uint32_t> gwt_fwd, gwt_bwd;
+    DBuf<uint32_t> wg_long;  // guide build: long-run count and list
     bool weights_ready = false;
 
     // node2vec adjacency

@@ -36,15 +36,15 @@
 //                                  picked group's range usually shares the
 //                                  line of the search's last probe
 //     w_fwd, w_bwd  fp64[g]        per-node cumulative exponential weights
-//     wx_off        uint32[V_c]    each node's base in the weight search index
-//     wx_fwd/wx_bwd fp64[..]       weight search index of nodes with > kWIdxMin
-//                                  groups: level k (k = 1..K) holds every
-//                                  16^k-th cumulative weight, K the first level
-//                                  of at most 16 entries; every level padded
-//                                  with +inf to whole 16-entry (128-byte)
-//                                  blocks; top level first
-//   global weights  fwd_cum, bwd_cum fp64[T] (+ gwx_fwd, gwx_bwd: their
-//                   search index, one segment of T)
+//   per walk direction with weights (forward walks: out with w_fwd; backward
+//   walks: in with w_bwd, or out with w_bwd if undirected)
+//     whdr          WNodeHdr[V_c]  node header + guide parameters and weight
+//                                  total of the node's cumulative weights
+//     wpan          WPanelRec[g+1] (ts rank, start, cumulative weight) of every
+//                                  group: pan and the weights in one record
+//     wgt           uint32[2(g+V_c)] guide tables of nodes with > kWGuideMin
+//                                  groups, node u's at 2 (gb + u) (below)
+//   global weights  fwd_cum, bwd_cum fp64[T] (+ their guides: one segment)
 //   node2vec        adj_hash uint64[2^k >= 4E] (pair membership set, built
 //                   with the index); adj_off uint32[max_id+2], adj_nbr
 //                   int32[2E] (sorted lists, built when first requested)
@@ -56,11 +56,8 @@
 
 namespace trw {
 
-// One entry of a node's edge list in walk order: the node reached over the
-// edge, the edge id and its timestamp -- everything a hop needs from the edge
-// in one aligned 16-byte load (instead of idx -> dst -> ts, three dependent
-// cache-line misses).
-// One entry of a node's list as the walk reads it.  Its timestamp is the
+// One entry of a node's list as the walk reads it: the node reached over the
+// edge and the edge id, one 8-byte load.  Its timestamp is the
 // group's (every entry of a node-timestamp group shares it), carried by the
 // walk as the group's rank.
 struct alignas(8) EdgeRec {
@@ -69,36 +66,73 @@ struct alignas(8) EdgeRec {
 };
 static_assert(sizeof(EdgeRec) == 8, "EdgeRec must be 8 bytes");
 
-// Cumulative-weight segments longer than this get a search index (levels of
-// every 16^k-th value); shorter ones are binary-searched directly.
-constexpr uint32_t kWIdxMin = 16;
+// Segments of more than this many cumulative weights get a guide table (below);
+// shorter ones are binary-searched directly (at most two lines of a weighted
+// panel).
+constexpr uint32_t kWGuideMin = 16;
 
 // Adjacency pair set: an empty slot, and the multiplier of its Fibonacci
 // hash (slot = key * kAdjHashMul >> (64 - log2 slots)).
 constexpr uint64_t kAdjEmpty = ~0ull;
 constexpr uint64_t kAdjHashMul = 0x9E3779B97F4A7C15ull;
 
-// Geometry of the weight search index of a segment of G cumulative weights:
-// level k has ceil(G / 16^k) entries; the top level K is the first with at
-// most 16; each level is padded to whole 16-entry blocks.
-__host__ __device__ inline uint32_t wx_level_entries(uint32_t G, uint64_t span) {
-    return static_cast<uint32_t>((G + span - 1) / span);
+// ---- weight guide tables ----------------------------------------------------
+// An inverse-CDF guide table (Chen & Asau, "On generating random variates
+// from an empirical distribution", AIIE Trans. 6, 1974) over each segment of
+// more than kWGuideMin cumulative weights, keyed not by the weight but by
+// wg_key(weight): an integer that never decreases as the weight grows and is
+// spaced about evenly in the logarithm of the weight's distance from the end
+// its picks crowd towards.  Bucket b of a segment holds the first local index
+// whose key bucket is >= b, followed by a closing entry G; since the key is
+// monotone, the lower_bound of any target (at most the segment's last weight)
+// whose key falls in bucket b lies in [tab[b], tab[b + 1]] -- exact, whatever
+// the weights look like.
+//
+// The key of a decaying segment (forward weights: most mass at its start, so
+// a late slice's sums sit within a few ulps of 1) is the bit pattern of
+// 1 - c, negated: 1 - c is monotone under round-to-nearest, and the bits of a
+// positive double order as its value, so the key is monotone and grows by
+// 2^52 per halving of 1 - c.  A growing segment (backward weights) keys on
+// the bits of c itself.  Either way an exponential weight profile maps to
+// keys that are close to linear in the group index.
+constexpr uint32_t kWgBucketsPerGroup = 2;
+// Runs of more buckets than this between two consecutive groups are filled by
+// a workgroup each rather than by the group's thread.
+constexpr uint32_t kWgRun = 64;
+
+__host__ __device__ inline uint64_t wg_double_bits(double x) {
+#ifdef __HIP_DEVICE_COMPILE__
+    return static_cast<uint64_t>(__double_as_longlong(x));
+#else
+    uint64_t b;
+    __builtin_memcpy(&b, &x, 8);
+    return b;
+#endif
 }
-__host__ __device__ inline uint32_t wx_pad16(uint32_t n) { return (n + 15u) & ~15u; }
-__host__ __device__ inline uint64_t wx_top_span(uint32_t G) {
-    uint64_t span = 16;
-    while ((G + span - 1) / span > 16) span <<= 4;
-    return span;
-}
-__host__ __device__ inline uint32_t wx_size(uint32_t G) {
-    if (G <= kWIdxMin) return 0;
-    uint32_t total = 0;
-    for (uint64_t span = 16;; span <<= 4) {
-        const uint32_t n = wx_level_entries(G, span);
-        total += wx_pad16(n);
-        if (n <= 16) break;
+// Monotone key of a cumulative weight c (see above); never negative for
+// c >= 0, negative only for a negative decaying target.
+__host__ __device__ inline int64_t wg_key(double c, bool decaying) {
+    if (decaying) {
+        double u = 1.0 - c;
+        if (!(u >= 0x1p-54)) u = 0x1p-54;  // c at or above 1 (and NaN)
+        return static_cast<int64_t>(wg_double_bits(1.0)) - static_cast<int64_t>(wg_double_bits(u));
     }
-    return total;
+    return c > 0.0 ? static_cast<int64_t>(wg_double_bits(c)) : 0;
+}
+
+// A segment's guide parameters and its last (largest) cumulative weight.
+struct alignas(16) WGuide {
+    uint64_t bs;   // bucket shift (bits 0-5) and the first bucket's key >> shift
+                   // (bits 6-63); unused for a segment of at most kWGuideMin
+    double total;  // the segment's last cumulative weight
+};
+static_assert(sizeof(WGuide) == 16, "WGuide must be 16 bytes");
+// Bucket of the key of a target no larger than the segment's total (so at
+// most the last bucket); keys below the first bucket go to bucket 0.
+__host__ __device__ inline uint32_t wg_bucket(uint64_t bs, int64_t key) {
+    const int sh = static_cast<int>(bs & 63u);
+    const int64_t kb = key >> sh, base = static_cast<int64_t>(bs >> 6);
+    return kb <= base ? 0u : static_cast<uint32_t>(kb - base);
 }
 
 // Nodes with more groups than this get a bucket table for the walk's search;
@@ -135,5 +169,23 @@ struct alignas(8) PanelRec {
                      // start ends the group
 };
 static_assert(sizeof(PanelRec) == 8, "PanelRec must be 8 bytes");
+
+// The weight pickers' view of a node: its header and the guide of its
+// cumulative weights, one 32-byte load.
+struct alignas(32) WNodeHdr {
+    NodeHdr h;
+    WGuide g;
+};
+static_assert(sizeof(WNodeHdr) == 32, "WNodeHdr must be 32 bytes");
+
+// One node-timestamp group in the weight pickers' panel: the panel record and
+// the group's cumulative weight, so the weight search, the slice's sums and
+// the picked group's range read the same lines.
+struct alignas(16) WPanelRec {
+    uint32_t rank;
+    uint32_t start;
+    double c;
+};
+static_assert(sizeof(WPanelRec) == 16, "WPanelRec must be 16 bytes");
 
 }  // namespace trw

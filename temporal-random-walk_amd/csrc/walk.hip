@@ -54,10 +54,12 @@ struct DirView {
     const PanelRec* pan;  // g + 1 group records (terminator)
     const EdgeRec* rec;   // walk-order edge records
     uint32_t idx_size;
-    const double* w;  // per-node cumulative weights of the sampled direction
-    uint64_t w_size;
-    const uint32_t* wx_off;  // their search index: per-node base ...
-    const double* wx;        // ... and levels (nullptr: none)
+    // the weight pickers' view of the sampled direction's cumulative weights
+    // (read by the weight families' kernels only; nullptr without weights)
+    const WNodeHdr* whdr;   // V_c node headers with guide parameters
+    const WPanelRec* wpan;  // g + 1 weighted panel records
+    const uint32_t* wgt;    // guide tables, node u's at 2 (gb + u)
+    uint64_t w_size;        // groups with weights (0: none)
 };
 
 // Picker families the walk kernel is specialised for: only index pickers
@@ -79,7 +81,8 @@ struct WalkGraph {
     uint32_t T;
     const double* gw;  // global cumulative weights of the sampled direction
     uint64_t gw_size;
-    const double* gwx;  // their search index (nullptr: none)
+    const WGuide* gwg;    // their guide (nullptr: none) and guide table
+    const uint32_t* gwt;
     const uint8_t* active;
     int32_t active_size;
     DirView d;
@@ -243,8 +246,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // single-rank bucket holds the answer itself; a wider one gives the bracket
 // [tab[b], tab[b + 1]] (about one group).  The rest is a binary search over
 // at most kTabMin groups.
+template <class Rec>
 __device__ __forceinline__ int first_ge(const uint32_t* tab, const NodeHdr& h, uint32_t u, int G,
-                                        const PanelRec* f, uint32_t x) {
+                                        const Rec* f, uint32_t x) {
     int lo = 0, hi = G;
     if (G > static_cast<int>(kTabMin)) {
         if (x <= h.r0) return 0;
@@ -270,85 +274,53 @@ __device__ __forceinline__ Sel edge_of(const WalkGraph& g, uint32_t e, long grou
     return Sel{g.src[e], g.dst[e], static_cast<int32_t>(e), static_cast<int32_t>(group)};
 }
 
-// Entries below `target` in an aligned block of 16 cumulative weights (one
-// 128-byte line; padding is +inf).
-__device__ __forceinline__ uint32_t count_below16(const double* p, double target) {
-    const double2* q = reinterpret_cast<const double2*>(p);
-    uint32_t c = 0;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const double2 v = q[j];
-        c += (v.x < target ? 1u : 0u) + (v.y < target ? 1u : 0u);
+// lower_bound over the non-decreasing cumulative weights c(0) .. c(G - 1) of
+// one segment, the number of weights below target -- the reference's binary
+// search (random/pickers.cuh:84-126) gives the same unique answer.  A
+// segment of more than kWGuideMin weights looks the target's key bucket up in
+// its guide table (index_layout.h): one 8-byte load brackets the answer in
+// [tab[b], tab[b + 1]], usually zero to two weights, which a binary search
+// settles.  A target above the segment's total (a rounded-up sum) is above
+// every weight.  Decaying: forward weights (the key of 1 - c).
+template <bool Decaying, class CAt>
+__device__ __forceinline__ uint32_t guided_lower_bound(CAt c, uint32_t G, const uint32_t* gt,
+                                                       const WGuide& gd, double target) {
+    if (!(target <= gd.total)) return G;
+    uint32_t lo = 0, hi = G;
+    if (G > kWGuideMin) {
+        const u32x2_a4 br =
+            *reinterpret_cast<const u32x2_a4*>(gt + wg_bucket(gd.bs, wg_key(target, Decaying)));
+        lo = br.x;
+        hi = br.y;
+        // a wide bracket is a run of equal keys (a weight repeated, as a
+        // saturated forward sum is): its first weight usually answers
+        if (hi - lo > 4 && !(c(lo) < target)) return lo;
     }
-    return c;
-}
-
-// lower_bound over one segment's non-decreasing cumulative weights w[0, G),
-// i.e. the number of entries below target -- the same answer as the
-// reference's binary search.  A segment with a search index `lv` descends it
-// from the top level: if c entries of level k are below target, the answer's
-// level-(k-1) entries below target end inside block c - 1 (all 16 entries of
-// which lie in one aligned line), and so on down to w itself.
-__device__ __forceinline__ uint32_t weight_lower_bound(const double* w, uint32_t G,
-                                                       const double* lv, double target) {
-    if (lv == nullptr || G <= kWIdxMin) {
-        uint32_t lo = 0, hi = G;
-        while (lo < hi) {
-            const uint32_t mid = lo + ((hi - lo) >> 1);
-            if (w[mid] < target) lo = mid + 1;
-            else hi = mid;
-        }
-        return lo;
+    while (lo < hi) {
+        const uint32_t mid = lo + ((hi - lo) >> 1);
+        if (c(mid) < target) lo = mid + 1;
+        else hi = mid;
     }
-    uint64_t span = wx_top_span(G);
-    uint32_t n = wx_level_entries(G, span);
-    const double* A = lv;
-    uint32_t c = count_below16(A, target);
-    if (c == 0) return 0;
-    while (span > 16) {
-        A += wx_pad16(n);
-        span >>= 4;
-        n = wx_level_entries(G, span);
-        const uint32_t b = (c - 1) * 16;
-        c = b + count_below16(A + b, target);
-    }
-    const uint32_t b = (c - 1) * 16;
-    const uint32_t m = G - b < 16 ? G - b : 16;
-    uint32_t k = 0;
-    for (uint32_t j = 0; j < m; ++j) k += w[b + j] < target ? 1u : 0u;
-    return b + k;
-}
-
-// pick_weights after its range checks, with the slice's start_sum and end_sum
-// already loaded (end_sum >= start_sum): the same result.
-__device__ __forceinline__ int pick_weights_sums(const double* w, uint64_t gs, uint64_t ge,
-                                                 double r, double start_sum, double end_sum,
-                                                 uint64_t seg, uint32_t G, const double* lv) {
-    const double target = start_sum + r * (end_sum - start_sum);
-    if (target <= start_sum) return static_cast<int>(gs);
-    const uint64_t x = seg + weight_lower_bound(w + seg, G, lv, target);
-    return static_cast<int>(x < gs ? gs : (x > ge ? ge : x));
+    return lo;
 }
 
 // pick_exponential_weights (random/pickers.cuh:84-126) over the slice
-// [gs, ge) of the segment [seg, seg + G) that holds it: the lower_bound over
-// the whole segment, clamped to the slice, is the slice's lower_bound because
-// the segment is non-decreasing.
-__device__ __forceinline__ int pick_weights(const double* w, uint64_t wsize, uint64_t gs,
-                                            uint64_t ge, double r, uint64_t slice_start,
-                                            uint64_t seg, uint32_t G, const double* lv) {
-    if (gs >= ge || ge > wsize) return -1;
-    const double start_sum = gs > slice_start ? w[gs - 1] : 0.0;
-    const double end_sum = w[ge - 1];
-    if (end_sum < start_sum) return -1;
+// [vb, ve) of a node's groups (local indexes; f is the node's weighted
+// panel), with the slice's sums loaded: the lower_bound over the node's whole
+// segment, clamped to the slice, is the slice's lower_bound because the
+// segment is non-decreasing.  start_sum >= target puts it before vb (or at
+// vb = 0 with start_sum = 0), which the clamp turns into vb: no search.
+// Forward weights saturate at their final sum over the late part of a node's
+// span, where start_sum == end_sum makes that the common case.
+template <bool Fwd>
+__device__ __forceinline__ uint32_t node_weight_pick(const WPanelRec* f, uint32_t G,
+                                                     const uint32_t* gt, const WGuide& gd,
+                                                     uint32_t vb, uint32_t ve, double r,
+                                                     double start_sum, double end_sum) {
     const double target = start_sum + r * (end_sum - start_sum);
-    // w[gs - 1] = start_sum >= target puts the lower_bound before gs (or at
-    // seg = gs with start_sum = 0), which the clamp turns into gs: no search.
-    // Forward weights saturate at their final sum over the late part of a
-    // node's span, where start_sum == end_sum makes this the common case.
-    if (target <= start_sum) return static_cast<int>(gs);
-    const uint64_t x = seg + weight_lower_bound(w + seg, G, lv, target);
-    return static_cast<int>(x < gs ? gs : (x > ge ? ge : x));
+    if (target <= start_sum) return vb;
+    const uint32_t x = guided_lower_bound<Fwd>([f](uint32_t i) { return f[i].c; }, G, gt, gd, target);
+    return x < vb ? vb : (x > ve ? ve : x);
 }
 
 // Number of unique timestamps below t: groups at or past this rank have
@@ -374,7 +346,16 @@ __device__ Sel start_edge(const WalkGraph& g, int picker, double rg, double re) 
         group = idx;
     } else {
         if (picker != kExponentialWeight && picker != kTemporalNode2Vec) return no_edge();
-        group = pick_weights(g.gw, g.gw_size, 0, g.T, rg, 0, 0, g.T, g.gwx);
+        // pick_exponential_weights over [0, T): start_sum 0, end_sum the total
+        if (g.T > g.gw_size || g.gwg == nullptr) return no_edge();
+        const WGuide gd = *g.gwg;
+        const double end_sum = gd.total;
+        if (end_sum < 0.0) return no_edge();
+        const double target = 0.0 + rg * (end_sum - 0.0);
+        const double* gw = g.gw;
+        group = target <= 0.0 ? 0
+                              : guided_lower_bound<Fwd>([gw](uint32_t i) { return gw[i]; }, g.T,
+                                                        g.gwt, gd, target);
         // an index past the last group reads as an empty range in the
         // reference (get_timestamp_group_range_host, edge_selectors.cuh:38-43)
         if (group == -1 || static_cast<uint32_t>(group) >= g.T) return no_edge();
@@ -411,11 +392,14 @@ __device__ __forceinline__ bool adjacent(const WalkGraph& g, int prev, int cand)
     return lo < end && g.adj_nbr[lo] == cand;
 }
 
-// graph/temporal_node2vec_helpers.cuh:127-199; vb/ve/gb/ge are global group
-// positions.  The candidate node of a proposal is its record's neighbour
+// graph/temporal_node2vec_helpers.cuh:127-199 over the slice [vb, ve) of a
+// node's G groups (local indexes; f is its weighted panel, gt its guide
+// table).  The candidate node of a proposal is its record's neighbour
 // (get_candidate_node, walk_step_helpers.cuh:40-54).
-__device__ Hop tn2v_pick(const WalkGraph& g, int prev, uint32_t vb, uint32_t ve, uint32_t gb,
-                         uint32_t ge, const double* lv, double rg, double re) {
+template <bool Fwd>
+__device__ Hop tn2v_pick(const WalkGraph& g, int prev, const WPanelRec* f, uint32_t G,
+                         const uint32_t* gt, const WGuide& gd, uint32_t vb, uint32_t ve, double rg,
+                         double re) {
     if (vb >= ve || prev == -1) return no_hop();
     double bmax = 1.0;
     if (g.inv_p > bmax) bmax = g.inv_p;
@@ -427,29 +411,28 @@ __device__ Hop tn2v_pick(const WalkGraph& g, int prev, uint32_t vb, uint32_t ve,
     const double acc_adj = 1.0 * inv_bmax, acc_far = g.inv_q * inv_bmax;
     const double acc_lo = acc_adj < acc_far ? acc_adj : acc_far;
     const double acc_hi = acc_adj < acc_far ? acc_far : acc_adj;
-    // every retry's weight pick (pick_weights over the slice [vb, ve) of the
-    // segment [gb, ge)) reads the same two sums: loaded once, outside the loop
-    if (ve > g.d.w_size) return no_hop();
-    const double start_sum = vb > gb ? g.d.w[vb - 1] : 0.0;
-    const double end_sum = g.d.w[ve - 1];
+    // every retry's weight pick (over the slice [vb, ve)) reads the same two
+    // sums: loaded once, outside the loop
+    const double start_sum = vb > 0 ? f[vb - 1].c : 0.0;
+    const double end_sum = ve == G ? gd.total : f[ve - 1].c;
     if (end_sum < start_sum) return no_hop();
     Hop last = no_hop();
     for (int retry = 0; retry < kNode2VecMaxRetries; ++retry) {
         const double gr = derive_uniform(rg, re, retry * 3 + 0);
         const double er = derive_uniform(rg, re, retry * 3 + 1);
         const double ar = derive_uniform(rg, re, retry * 3 + 2);
-        const int gp = pick_weights_sums(g.d.w, vb, ve, gr, start_sum, end_sum, gb, ge - gb, lv);
+        const uint32_t x = node_weight_pick<Fwd>(f, G, gt, gd, vb, ve, gr, start_sum, end_sum);
         // a pick one past the node's last group is an empty range in the
         // reference (get_node_group_edge_end, walk_step_helpers.cuh:19-38)
-        if (static_cast<uint32_t>(gp) >= ge) continue;
-        const PanelPair pr = load_pair(g.d.pan + gp);
-        const uint32_t es = pr.start, ee = pr.next_start;
+        if (x >= G) continue;
+        const u32x2_a4 rs = *reinterpret_cast<const u32x2_a4*>(f + x);  // rank, start
+        const uint32_t es = rs.y, ee = f[x + 1].start;
         if (es >= ee) continue;
         const uint64_t local = static_cast<uint64_t>(er * static_cast<double>(ee - es));
         const uint32_t pick = es + static_cast<uint32_t>(local < ee - es ? local : ee - es - 1);
         const EdgeRec r = load_rec(g.d.rec + pick);
         const int cand = r.nbr;
-        last = hop_of(r, pr.rank);
+        last = hop_of(r, rs.x);
         bool accept;
         if (cand == prev) accept = ar < g.inv_p * inv_bmax;
         else if (ar < acc_lo) accept = true;
@@ -475,13 +458,16 @@ __device__ __forceinline__ Hop hop_from_group(const WalkGraph& g, uint32_t gpos,
                   pp.rank);
 }
 
-// Node u's base in the weight search index, loaded beside its header (the
-// pick that reads it comes after the group search): 0 for the index family.
-// (Loaded so in the ExponentialWeight kernel's shared-search loop it ran cfg4
-// 0.7 % slower; that loop reads it after the group search.)
-template <int Fam>
-__device__ __forceinline__ uint32_t wx_base(const WalkGraph& g, uint32_t u) {
-    return (Fam != kFamIndex && g.d.wx) ? g.d.wx_off[u] : 0u;
+// The same over a weighted panel f of G groups, group x (local).
+__device__ __forceinline__ Hop whop_from_group(const WalkGraph& g, const WPanelRec* f, uint32_t x,
+                                               uint32_t G, double re) {
+    if (x >= G) return no_hop();
+    const u32x2_a4 rs = *reinterpret_cast<const u32x2_a4*>(f + x);  // rank, start
+    const uint32_t es = rs.y, ee = f[x + 1].start;
+    if (es >= ee || es >= g.d.idx_size || ee > g.d.idx_size) return no_hop();
+    return hop_of(load_rec(g.d.rec + es +
+                           static_cast<uint32_t>(static_cast<int>(re * static_cast<int>(ee - es)))),
+                  rs.x);
 }
 
 // Per-hop selector (edge_selectors.cuh:277-443).  The reference first checks
@@ -491,50 +477,114 @@ __device__ __forceinline__ uint32_t wx_base(const WalkGraph& g, uint32_t u) {
 // -1, which the reference also reads as unconstrained); cut: rank bound of
 // the walk's cutoff time (groups at or past it are excluded), -1 for none.
 //
-// The selection after the header load of node u: ok is false for a node
-// outside the index (then the value of h is ignored).
-template <bool Fwd, int Fam>
+// The valid slice [vb, ve) of node u's G groups (local indexes), searched in
+// its panel f (PanelRec or WPanelRec: the ranks are the same): filter_valid_
+// groups_by_timestamp_slice (edge_selectors.cuh:66-120) and the cutoff.
+template <bool Fwd, class Rec>
+__device__ __forceinline__ void valid_slice(const uint32_t* tab, const NodeHdr& h, uint32_t u,
+                                            int G, const Rec* f, int32_t t, int32_t cut, int& vb,
+                                            int& ve) {
+    vb = 0;
+    ve = G;
+    if (t != -1) {
+        const uint32_t x = static_cast<uint32_t>(t);
+        if (Fwd) vb = first_ge(tab, h, u, G, f, x + 1);  // upper_bound
+        else ve = first_ge(tab, h, u, G, f, x);         // lower_bound
+    }
+    if (cut != -1) {
+        // the first group at or past the cutoff, within [vb, ve]
+        const int c = first_ge(tab, h, u, G, f, static_cast<uint32_t>(cut));
+        ve = c < vb ? vb : (c < ve ? c : ve);
+    }
+}
+
+// The selection after the header load of node u for the index pickers (the
+// index family's kernels): ok is false for a node outside the index (then
+// the value of h is ignored).
+template <bool Fwd>
 __device__ __forceinline__ Hop node_edge_from(const WalkGraph& g, int picker, uint32_t u, bool ok,
-                                              const NodeHdr& h, int32_t t, int32_t cut, int prev,
-                                              double rg, double re, const double* em1,
-                                              uint32_t wxo) {
+                                              const NodeHdr& h, int32_t t, int32_t cut,
+                                              double rg, double re, const double* em1) {
     uint32_t Gu = ok ? (h.meta & kHdrGMask) : 0u;
     if (Gu == kHdrGMask) Gu = g.d.hdr[u + 1].gb - h.gb;  // more groups than 24 bits hold
     if (Gu == 0) return no_hop();
     const uint32_t gb = h.gb, ge = gb + Gu;
     const int G = static_cast<int>(Gu);
-    const PanelRec* fts = g.d.pan + gb;
-    // filter_valid_groups_by_timestamp_slice (edge_selectors.cuh:66-120)
-    int vb = 0, ve = G;
-    if (t != -1) {
-        const uint32_t x = static_cast<uint32_t>(t);
-        if (Fwd) vb = first_ge(g.d.tab, h, u, G, fts, x + 1);  // upper_bound
-        else ve = first_ge(g.d.tab, h, u, G, fts, x);         // lower_bound
-    }
-    if (cut != -1) {
-        // the first group at or past the cutoff, within [vb, ve]
-        const int c = first_ge(g.d.tab, h, u, G, fts, static_cast<uint32_t>(cut));
-        ve = c < vb ? vb : (c < ve ? c : ve);
-    }
+    int vb, ve;
+    valid_slice<Fwd>(g.d.tab, h, u, G, g.d.pan + gb, t, cut, vb, ve);
     if (vb >= ve) return no_hop();
-    uint32_t gpos;
-    if (Fam == kFamIndex || is_index_picker(picker)) {
+    const int avail = ve - vb;
+    const int index = pick_index(picker, 0, avail, !Fwd, rg, em1);
+    if (index == -1 || index >= avail) return no_hop();
+    return hop_from_group(g, gb + static_cast<uint32_t>(vb + index), ge, re);
+}
+
+// The same for any picker, over the weighted view (the weight families'
+// kernels): the time search, the slice's sums, the weight search and the
+// picked group's range all read the node's weighted panel.
+template <bool Fwd, int Fam>
+__device__ __forceinline__ Hop wnode_edge_from(const WalkGraph& g, int picker, uint32_t u, bool ok,
+                                               const WNodeHdr& wh, int32_t t, int32_t cut,
+                                               int prev, double rg, double re,
+                                               const double* em1) {
+    const NodeHdr& h = wh.h;
+    uint32_t Gu = ok ? (h.meta & kHdrGMask) : 0u;
+    if (Gu == kHdrGMask) Gu = g.d.whdr[u + 1].h.gb - h.gb;
+    if (Gu == 0) return no_hop();
+    const uint32_t gb = h.gb;
+    const int G = static_cast<int>(Gu);
+    const WPanelRec* f = g.d.wpan + gb;
+    int vb, ve;
+    valid_slice<Fwd>(g.d.tab, h, u, G, f, t, cut, vb, ve);
+    if (vb >= ve) return no_hop();
+    uint32_t x;
+    if (is_index_picker(picker)) {
         const int avail = ve - vb;
         const int index = pick_index(picker, 0, avail, !Fwd, rg, em1);
         if (index == -1 || index >= avail) return no_hop();
-        gpos = gb + static_cast<uint32_t>(vb + index);
+        x = static_cast<uint32_t>(vb + index);
     } else {
-        const double* lv = (g.d.wx && G > static_cast<int>(kWIdxMin)) ? g.d.wx + wxo : nullptr;
-        if (Fam != kFamWeight && picker == kTemporalNode2Vec && prev != -1)
-            return tn2v_pick(g, prev, gb + vb, gb + ve, gb, ge, lv, rg, re);
-        // ExponentialWeight, or node2vec's first hop (no previous node)
         if (picker != kExponentialWeight && picker != kTemporalNode2Vec) return no_hop();
-        const int p = pick_weights(g.d.w, g.d.w_size, gb + vb, gb + ve, rg, gb, gb,
-                                   static_cast<uint32_t>(G), lv);
-        if (p == -1) return no_hop();
-        gpos = static_cast<uint32_t>(p);
+        // the reference's range check: no weights, no pick
+        if (gb + Gu > g.d.w_size) return no_hop();
+        const uint32_t* gt = g.d.wgt + hdr_tab_base(h, u);
+        if (Fam != kFamWeight && picker == kTemporalNode2Vec && prev != -1)
+            return tn2v_pick<Fwd>(g, prev, f, Gu, gt, wh.g, vb, ve, rg, re);
+        // ExponentialWeight, or node2vec's first hop (no previous node)
+        const double start_sum = vb > 0 ? f[vb - 1].c : 0.0;
+        const double end_sum = ve == G ? wh.g.total : f[ve - 1].c;
+        if (end_sum < start_sum) return no_hop();
+        x = node_weight_pick<Fwd>(f, Gu, gt, wh.g, static_cast<uint32_t>(vb),
+                                  static_cast<uint32_t>(ve), rg, start_sum, end_sum);
     }
-    return hop_from_group(g, gpos, ge, re);
+    return whop_from_group(g, f, x, Gu, re);
+}
+
+// The node header a family's kernel loads per hop (issued before the hop's
+// draws), and the selection after it.
+template <int Fam>
+struct HopHdrOf {
+    using type = WNodeHdr;
+};
+template <>
+struct HopHdrOf<kFamIndex> {
+    using type = NodeHdr;
+};
+template <int Fam>
+using HopHdr = typename HopHdrOf<Fam>::type;
+
+template <int Fam>
+__device__ __forceinline__ HopHdr<Fam> load_hop_hdr(const WalkGraph& g, uint32_t u) {
+    if constexpr (Fam == kFamIndex) return g.d.hdr[u];
+    else return g.d.whdr[u];
+}
+
+template <bool Fwd, int Fam>
+__device__ __forceinline__ Hop hop_at(const WalkGraph& g, int picker, uint32_t u, bool ok,
+                                      const HopHdr<Fam>& hh, int32_t t, int32_t cut, int prev,
+                                      double rg, double re, const double* em1) {
+    if constexpr (Fam == kFamIndex) return node_edge_from<Fwd>(g, picker, u, ok, hh, t, cut, rg, re, em1);
+    else return wnode_edge_from<Fwd, Fam>(g, picker, u, ok, hh, t, cut, prev, rg, re, em1);
 }
 
 template <bool Fwd, int Fam>
@@ -542,8 +592,7 @@ __device__ Hop node_edge_at(const WalkGraph& g, int picker, int node, int32_t t,
                             int prev, double rg, double re, const double* em1 = nullptr) {
     if (!(node >= 0 && node < g.active_size)) return no_hop();
     const uint32_t u = static_cast<uint32_t>(node);
-    return node_edge_from<Fwd, Fam>(g, picker, u, true, g.d.hdr[u], t, cut, prev, rg, re, em1,
-                                    wx_base<Fam>(g, u));
+    return hop_at<Fwd, Fam>(g, picker, u, true, load_hop_hdr<Fam>(g, u), t, cut, prev, rg, re, em1);
 }
 
 // Rank bound of a walk's cutoff time: groups at or past it are excluded
@@ -641,293 +690,6 @@ __device__ __forceinline__ uint64_t grid_position(int remap) {
     return b * static_cast<uint64_t>(kB) + threadIdx.x;
 }
 
-// ---- wave-cooperative weight search ---------------------------------------
-// A weight pick descends a 16-ary search index, one 16-entry block per level
-// (weight_lower_bound).  Read by its own lane, a block costs that lane eight
-// 16-byte accesses -- or sixteen 8-byte ones at the bottom level, whose block
-// need not be aligned -- and a wave of such lanes touches 64 lines per
-// access.  Shared by the wave, a block costs one access: in round j the 16
-// lanes of each quarter of the wave read one entry each of the block of the
-// quarter's lane j, and one ballot counts the four blocks of the round.  A
-// quarter is a DPP row, so lane j's request reaches its quarter by a row
-// broadcast (row_newbcast:j, a VALU move) rather than through the LDS.
-
-// A device-memory double.  Loads through it are global loads, whose results
-// return in order, so a wave waits for each round's load alone (vmcnt(n))
-// rather than for all of them (flat loads, which may also reach the LDS).
-typedef __attribute__((address_space(1))) const double GlobalF64;
-
-// Lane J's value in every lane of its 16-lane row.
-template <int J>
-__device__ __forceinline__ uint32_t row_bcast(uint32_t v) {
-    return static_cast<uint32_t>(
-        __builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x150 + J, 0xf, 0xf, false));
-}
-
-// Round J of wave_count_below16, in two halves: count_load16<J> issues the
-// read of the quarters' lanes J blocks and count_below16_round<J> counts them,
-// lane J of each quarter keeping its count in mine.  A request is the block's
-// address with its limit in bits 48-52 (device addresses have 48 bits, which
-// the host checks) and the target.  Every lane loads (entry 0 past the limit:
-// a select of the index, not of the load, so the loads need no branch).
-template <int J>
-__device__ __forceinline__ double count_load16(int sub, uint32_t p_lo, uint32_t p_hi) {
-    const uint32_t hi = row_bcast<J>(p_hi);
-    const uint64_t bp = (static_cast<uint64_t>(hi & 0xffffu) << 32) | row_bcast<J>(p_lo);
-    const int l = static_cast<int>(hi >> 16);
-    return reinterpret_cast<const GlobalF64*>(bp)[sub < l ? sub : 0];
-}
-template <int J>
-__device__ __forceinline__ void count_below16_round(uint32_t& mine, int sub, int qbase, double v,
-                                                    uint32_t p_hi, uint32_t t_lo, uint32_t t_hi) {
-    const int l = static_cast<int>(row_bcast<J>(p_hi) >> 16);
-    const double t = __hiloint2double(static_cast<int>(row_bcast<J>(t_hi)),
-                                      static_cast<int>(row_bcast<J>(t_lo)));
-    const uint64_t m = __ballot(sub < l && v < t);
-    const uint32_t c = static_cast<uint32_t>(__popcll((m >> qbase) & 0xffffull));
-    mine = sub == J ? c : mine;
-}
-
-// Number of the first lim (<= 16) entries of blk below target, for every lane
-// with need (0 for the others).  All lanes of the wave call it together (the
-// row broadcasts read every lane); safe is a readable address for lanes
-// without a request.  The sixteen rounds' loads are issued before the first
-// count, so they are in flight together.
-__device__ __forceinline__ uint32_t wave_count_below16(bool need, const double* blk,
-                                                       uint32_t lim, double target,
-                                                       const double* safe) {
-    if (__ballot(need) == 0) return 0;  // uniform: no request in the wave
-    const int lane = __lane_id();
-    const int sub = lane & 15, qbase = lane & 48;
-    const uint64_t bp = reinterpret_cast<uint64_t>(need ? blk : safe);
-    const uint32_t p_lo = static_cast<uint32_t>(bp);
-    const uint32_t p_hi = static_cast<uint32_t>(bp >> 32) | ((need ? lim : 0u) << 16);
-    const uint32_t t_lo = static_cast<uint32_t>(__double2loint(target));
-    const uint32_t t_hi = static_cast<uint32_t>(__double2hiint(target));
-    double v[16];
-#define TRW_LOAD(J) v[J] = count_load16<J>(sub, p_lo, p_hi)
-    TRW_LOAD(0); TRW_LOAD(1); TRW_LOAD(2); TRW_LOAD(3); TRW_LOAD(4); TRW_LOAD(5);
-    TRW_LOAD(6); TRW_LOAD(7); TRW_LOAD(8); TRW_LOAD(9); TRW_LOAD(10); TRW_LOAD(11);
-    TRW_LOAD(12); TRW_LOAD(13); TRW_LOAD(14); TRW_LOAD(15);
-#undef TRW_LOAD
-    uint32_t mine = 0;
-#define TRW_COUNT(J) count_below16_round<J>(mine, sub, qbase, v[J], p_hi, t_lo, t_hi)
-    TRW_COUNT(0); TRW_COUNT(1); TRW_COUNT(2); TRW_COUNT(3); TRW_COUNT(4); TRW_COUNT(5);
-    TRW_COUNT(6); TRW_COUNT(7); TRW_COUNT(8); TRW_COUNT(9); TRW_COUNT(10); TRW_COUNT(11);
-    TRW_COUNT(12); TRW_COUNT(13); TRW_COUNT(14); TRW_COUNT(15);
-#undef TRW_COUNT
-    return mine;
-}
-
-// weight_lower_bound for every lane with need, the wave sharing each level's
-// block reads: the same descent, one wave_count_below16 per level.  A segment
-// of at most kWIdxMin weights is one block.  All lanes of the wave call it
-// together.
-__device__ __forceinline__ uint32_t wave_weight_lower_bound(bool need, const double* w, uint32_t G,
-                                                            const double* lv, double target,
-                                                            const double* safe) {
-    const bool indexed = need && G > kWIdxMin;
-    uint32_t res = 0;
-    bool pending = need;
-    if (indexed && lv == nullptr) {  // no index was built: the lane searches alone
-        res = weight_lower_bound(w, G, nullptr, target);
-        pending = false;
-    }
-    // state 0: the top level; 1: a lower index level; 2: the weights themselves
-    int state = indexed ? 0 : 2;
-    uint64_t span = indexed ? wx_top_span(G) : 0;
-    uint32_t n = indexed ? wx_level_entries(G, span) : 0;
-    const double* A = lv;
-    uint32_t b = 0;
-    while (__any(pending)) {
-        const double* blk = safe;
-        uint32_t lim = 0;
-        if (pending) {
-            blk = state == 2 ? w + b : A + b;
-            lim = state == 2 ? (G - b < 16u ? G - b : 16u) : 16u;
-        }
-        const uint32_t k = wave_count_below16(pending, blk, lim, target, safe);
-        if (pending) {
-            if (state == 2) {
-                res = b + k;
-                pending = false;
-            } else if (state == 0 && k == 0) {
-                res = 0;
-                pending = false;
-            } else {
-                const uint32_t c = b + k;  // entries of this level below target
-                if (span > 16) {
-                    A += wx_pad16(n);
-                    span >>= 4;
-                    n = wx_level_entries(G, span);
-                    state = 1;
-                } else {
-                    state = 2;
-                }
-                b = (c - 1) * 16;
-            }
-        }
-    }
-    return res;
-}
-
-// A weight-family hop up to its weight search.
-struct WeightHop {
-    bool fail;        // no hop
-    bool need;        // waits for the weight search over [gb, gb + G)
-    uint32_t gpos;    // the picked group (index pickers)
-    uint32_t gb, G;   // the node's groups
-    uint32_t gs, gse; // the valid slice [gs, gse)
-    uint32_t ge;      // the node's group end
-    const double* lv;
-    double target;
-};
-
-// node_edge_from's selection for the weight family (ExponentialWeight or an
-// index picker), stopping where pick_weights would search.
-template <bool Fwd>
-__device__ __forceinline__ WeightHop weight_hop_begin(const WalkGraph& g, int picker, uint32_t u,
-                                                      bool ok, const NodeHdr& h, int32_t t,
-                                                      int32_t cut, double rg, const double* em1) {
-    WeightHop s{true, false, 0, 0, 0, 0, 0, 0, nullptr, 0.0};
-    uint32_t Gu = ok ? (h.meta & kHdrGMask) : 0u;
-    if (Gu == kHdrGMask) Gu = g.d.hdr[u + 1].gb - h.gb;
-    if (Gu == 0) return s;
-    const uint32_t gb = h.gb, ge = gb + Gu;
-    const int G = static_cast<int>(Gu);
-    const PanelRec* fts = g.d.pan + gb;
-    int vb = 0, ve = G;
-    if (t != -1) {
-        const uint32_t x = static_cast<uint32_t>(t);
-        if (Fwd) vb = first_ge(g.d.tab, h, u, G, fts, x + 1);
-        else ve = first_ge(g.d.tab, h, u, G, fts, x);
-    }
-    if (cut != -1) {
-        const int c = first_ge(g.d.tab, h, u, G, fts, static_cast<uint32_t>(cut));
-        ve = c < vb ? vb : (c < ve ? c : ve);
-    }
-    if (vb >= ve) return s;
-    s.ge = ge;
-    if (is_index_picker(picker)) {
-        const int avail = ve - vb;
-        const int index = pick_index(picker, 0, avail, !Fwd, rg, em1);
-        if (index == -1 || index >= avail) return s;
-        s.gpos = gb + static_cast<uint32_t>(vb + index);
-        s.fail = false;
-        return s;
-    }
-    if (picker != kExponentialWeight) return s;
-    // pick_weights up to its search
-    const uint64_t gs = gb + vb, gse = gb + ve;
-    if (gs >= gse || gse > g.d.w_size) return s;
-    const double start_sum = gs > gb ? g.d.w[gs - 1] : 0.0;
-    const double end_sum = g.d.w[gse - 1];
-    if (end_sum < start_sum) return s;
-    s.target = start_sum + rg * (end_sum - start_sum);
-    if (s.target <= start_sum) {  // pick_weights' case without a search
-        s.gpos = static_cast<uint32_t>(gs);
-        s.fail = false;
-        return s;
-    }
-    s.lv = (g.d.wx && G > static_cast<int>(kWIdxMin)) ? g.d.wx + g.d.wx_off[u] : nullptr;
-    s.gb = gb;
-    s.G = Gu;
-    s.gs = static_cast<uint32_t>(gs);
-    s.gse = static_cast<uint32_t>(gse);
-    s.need = true;
-    s.fail = false;
-    return s;
-}
-
-// The walk loop of walk_kernel for the weight family, with the weight search
-// shared by the wave: a lane whose walk has ended (or that has no walk) keeps
-// taking part until every walk of its wave has, so the loop's control is
-// wave-uniform around the shared search.  Same walks as walk_kernel's loop.
-template <bool Fwd, bool Dir>
-__device__ __forceinline__ void walk_wave_weights(const WalkGraph& g, const WalkArgs& a,
-                                                  const double* em1) {
-    const uint64_t q = a.q0 + grid_position(a.xcd_remap);
-    const bool in_range = q < a.q_end;
-    const uint64_t w = in_range ? (a.order ? a.order[q] : q) : 0;
-    const int L = a.L;  // >= 1 (the caller returned for L == 0)
-    SlotWriter out(a, q);
-    const int32_t cut = in_range ? cutoff_rank(g, a, w) : -1;
-    const int32_t neg1 = *g.neg1_rank;
-    // the start state from the pre-pass, or found here
-    const StartState s0 = !in_range ? StartState{-1, -1, -1, -1}
-                                    : (a.st ? a.st[w] : walk_start<Fwd, Dir, kFamWeight>(g, a, w, cut));
-    int cur = s0.cur;
-    int32_t cur_r = s0.r, cur_e = s0.e;
-    int len = 0, walk_len = 1;
-    bool active = in_range && cur_e != -1;
-    if (active) {
-        out.first(s0.first);
-        len = 1;
-    }
-    active = active && walk_len < L && cur != a.pad;
-    while (__any(active)) {
-        WeightHop hs{true, false, 0, 0, 0, 0, 0, 0, nullptr, 0.0};
-        double re = 0.0;
-        if (active) {
-            out.slot(len, cur, static_cast<uint32_t>(cur_r), static_cast<uint32_t>(cur_e));
-            ++len;
-            if (walk_len == L - 1) {
-                active = false;  // the reference's last selection cannot change the output
-            } else {
-                const bool ok = cur >= 0 && cur < g.active_size;
-                const uint32_t u = ok ? static_cast<uint32_t>(cur) : 0u;
-                const NodeHdr hd = g.d.hdr[u];
-                const DrawPair r = draw_pair(a.ds, w, static_cast<uint32_t>(walk_len) + 1);
-                hs = weight_hop_begin<Fwd>(g, a.walk_bias, u, ok, hd, cur_r == neg1 ? -1 : cur_r,
-                                           cut, r.a, em1);
-                re = r.b;
-                if (hs.fail) active = false;
-            }
-        }
-        const uint32_t k = wave_weight_lower_bound(hs.need, g.d.w + hs.gb, hs.G, hs.lv, hs.target,
-                                                   g.d.w);
-        if (active) {
-            uint32_t gpos = hs.gpos;
-            if (hs.need) {
-                const uint32_t x = hs.gb + k;
-                gpos = x < hs.gs ? hs.gs : (x > hs.gse ? hs.gse : x);
-            }
-            const Hop h = hop_from_group(g, gpos, hs.ge, re);
-            if (h.e == -1 || h.r == neg1) {
-                active = false;
-            } else {
-                cur = h.nbr;
-                cur_r = h.r;
-                cur_e = h.e;
-                ++walk_len;
-                active = walk_len < L && cur != a.pad;
-            }
-        }
-    }
-    if (in_range) a.lens[w] = static_cast<uint64_t>(len);
-}
-
-// walk_kernel of the weight family: the walks of a wave share its weight
-// searches (walk_wave_weights).  Its registers (the search keeps sixteen loads
-// in flight) allow four waves per SIMD; a cap at five makes the compiler
-// issue the loads one at a time, which is slower.
-template <bool Fwd, bool Dir, int Fam>
-__global__ __launch_bounds__(kB) void walk_weights_kernel(WalkGraph g, WalkArgs a) {
-    static_assert(Fam == kFamWeight, "the weight family's kernel");
-    __shared__ double s_xt[kExpTables];
-    const bool use_xt = a.walk_bias == kExponentialIndex;
-    if (use_xt) {
-        fill_exp_tables(s_xt, threadIdx.x, kB);
-        __syncthreads();
-    }
-    if (a.L > 0) {  // uniform
-        walk_wave_weights<Fwd, Dir>(g, a, use_xt ? s_xt : nullptr);
-        return;
-    }
-    const uint64_t q = a.q0 + grid_position(a.xcd_remap);
-    if (q < a.q_end) a.lens[a.order ? a.order[q] : q] = 0;
-}
-
 // Waves per SIMD: the any-picker instance (node2vec's retry loop) needs
 // 146-150 VGPRs, which left it at 3 waves; held to 5 (102 VGPRs) its cfg5
 // walks (scratch path) run in 11.1 instead of 13.0 ms per batch (4 waves:
@@ -985,15 +747,14 @@ __global__ __launch_bounds__(kB) __attribute__((amdgpu_waves_per_eu(Fam == kFamI
             // empty and entry 0 is a valid address for a node outside it.
             const bool ok = cur >= 0 && cur < g.active_size;
             const uint32_t u = ok ? static_cast<uint32_t>(cur) : 0u;
-            const NodeHdr hd = g.d.hdr[u];
-            const uint32_t wxo = wx_base<Fam>(g, u);
+            const HopHdr<Fam> hd = load_hop_hdr<Fam>(g, u);
             const uint32_t p = static_cast<uint32_t>(walk_len) + 1;
             DrawPair r = philox_pair(a.ds, w, p);
             asm volatile("" : "+v"(r.a), "+v"(r.b));
             if (a.ds.replay) r = replay_pair(a.ds, w, p);
-            const Hop h = node_edge_from<Fwd, Fam>(g, a.walk_bias, u, ok, hd,
+            const Hop h = hop_at<Fwd, Fam>(g, a.walk_bias, u, ok, hd,
                                                    cur_r == neg1 ? -1 : cur_r, cut, prev, r.a,
-                                                   r.b, em1, wxo);
+                                                   r.b, em1);
             // the reference's failure test is ts == -1: no edge, or an edge at -1
             if (h.e == -1 || h.r == neg1) break;
             prev = cur;
@@ -1245,15 +1006,14 @@ __global__ __launch_bounds__(kB) __attribute__((amdgpu_waves_per_eu(4))) void wa
                     // hop's Philox rounds
                     const bool ok = cur >= 0 && cur < g.active_size;
                     const uint32_t u = ok ? static_cast<uint32_t>(cur) : 0u;
-                    const NodeHdr hd = g.d.hdr[u];
-                    const uint32_t wxo = wx_base<Fam>(g, u);
+                    const HopHdr<Fam> hd = load_hop_hdr<Fam>(g, u);
                     const uint32_t p = static_cast<uint32_t>(k) + 1;
                     DrawPair r = philox_pair(a.ds, w, p);
                     asm volatile("" : "+v"(r.a), "+v"(r.b));
                     if (a.ds.replay) r = replay_pair(a.ds, w, p);
-                    const Hop h = node_edge_from<Fwd, Fam>(g, a.walk_bias, u, ok, hd,
+                    const Hop h = hop_at<Fwd, Fam>(g, a.walk_bias, u, ok, hd,
                                                            cur_r == neg1 ? -1 : cur_r, cut, prev,
-                                                           r.a, r.b, em1, wxo);
+                                                           r.a, r.b, em1);
                     if (h.e == -1 || h.r == neg1) {
                         alive = false;
                     } else {
@@ -1272,19 +1032,20 @@ __global__ __launch_bounds__(kB) __attribute__((amdgpu_waves_per_eu(4))) void wa
     if (live) a.lens[w] = static_cast<uint64_t>(len);
 }
 
-// The row-writing walk kernel of the index family (index_only) or of any
-// picker, forward.  (A row writer for the ExponentialWeight family, its wave
-// sharing the weight searches, measured slower than scratch and the layout
-// pass at cfg4: walk kernel 161.0 ms against 138.8 + 19.8 ms.  That kernel is
-// bound by its searches' loads, and the flush's stores queue behind them.)
-void launch_rows(bool directed, bool index_only, dim3 grid, hipStream_t s, const WalkGraph& g,
+// The row-writing walk kernel of a picker family, forward.
+void launch_rows(bool directed, int fam, dim3 grid, hipStream_t s, const WalkGraph& g,
                  const WalkArgs& a) {
     constexpr int C = kRowSlots;
 #define TRW_ROWS(D, F) hipLaunchKernelGGL((walk_rows_kernel<true, D, F, C>), grid, dim3(kB), 0, s, g, a)
-    if (directed && index_only) TRW_ROWS(true, kFamIndex);
-    else if (directed) TRW_ROWS(true, kFamAny);
-    else if (index_only) TRW_ROWS(false, kFamIndex);
-    else TRW_ROWS(false, kFamAny);
+#define TRW_ROWS_FAM(D)                                      \
+    do {                                                     \
+        if (fam == kFamIndex) TRW_ROWS(D, kFamIndex);        \
+        else if (fam == kFamWeight) TRW_ROWS(D, kFamWeight); \
+        else TRW_ROWS(D, kFamAny);                           \
+    } while (0)
+    if (directed) TRW_ROWS_FAM(true);
+    else TRW_ROWS_FAM(false);
+#undef TRW_ROWS_FAM
 #undef TRW_ROWS
 }
 
@@ -1405,12 +1166,11 @@ __global__ __launch_bounds__(kB) void node_group_segment_kernel(
             }
             const bool ok = s.cur >= 0 && s.cur < g.active_size;
             const uint32_t u = ok ? static_cast<uint32_t>(s.cur) : 0u;
-            const NodeHdr hd = g.d.hdr[u];
-            const uint32_t wxo = wx_base<Fam>(g, u);
+            const HopHdr<Fam> hd = load_hop_hdr<Fam>(g, u);
             const DrawPair r = draw_pair(a.ds, w, static_cast<uint32_t>(s.c));
-            const Hop h = node_edge_from<Fwd, Fam>(g, a.walk_bias, u, ok, hd,
+            const Hop h = hop_at<Fwd, Fam>(g, a.walk_bias, u, ok, hd,
                                                    s.r == neg1 ? -1 : s.r, s.cut, s.prev, r.a,
-                                                   r.b, em1, wxo);
+                                                   r.b, em1);
             if (h.e == -1 || h.r == neg1) {
                 keep = false;
                 break;
@@ -2029,12 +1789,10 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
     w_len = 0;
     w_feat.n = 0;
     uint64_t* sc_packed = nullptr;
-    // forward walks of the index pickers or node2vec: the walk kernel writes
-    // the output rows itself (walk_rows_kernel); the others go through
-    // scratch and the layout pass
-    const bool weight_family = !(is_index_picker(walk_bias) && is_index_picker(start_bias)) &&
-                               walk_bias != kTemporalNode2Vec;
-    const bool rows_direct = p.walk_layout == TRW_LAYOUT_AUTO && forward && !weight_family &&
+    // forward walks: the walk kernel writes the output rows itself
+    // (walk_rows_kernel); backward walks go through scratch and the layout
+    // pass, which reverses them
+    const bool rows_direct = p.walk_layout == TRW_LAYOUT_AUTO && forward &&
                              L > 0 && nw <= 0xffffffffull &&
                              p.walk_order != TRW_ORDER_NODE_GROUPED;
     if (rows_direct) {
@@ -2091,8 +1849,9 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
     g.gw = forward ? fwd_cum.p : bwd_cum.p;
     g.gw_size = weights_ready ? T : 0;
     {
-        const DBuf<double>& gx = forward ? gwx_fwd : gwx_bwd;
-        g.gwx = weights_ready && gx.n ? gx.p : nullptr;
+        const DBuf<WGuide>& gd = forward ? gwg_fwd : gwg_bwd;
+        g.gwg = weights_ready && gd.n ? gd.p : nullptr;
+        g.gwt = (forward ? gwt_fwd : gwt_bwd).p;
     }
     g.active = active.p;
     g.active_size = static_cast<int32_t>(active.n);
@@ -2101,21 +1860,13 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
     g.d.pan = d.pan.p;
     g.d.rec = d.rec.p;
     g.d.idx_size = static_cast<uint32_t>(d.n_entries);
-    {
-        // per-node weights of the sampled direction and their search index
-        const DirIndex& wd = (!forward && cfg.is_directed) ? in : out;
-        const DBuf<double>& w = forward ? wd.w_fwd : wd.w_bwd;
-        const DBuf<double>& wx = forward ? wd.wx_fwd : wd.wx_bwd;
-        g.d.w = w.p;
-        g.d.w_size = weights_ready ? wd.n_groups : 0;
-        g.d.wx_off = wd.wx_off.p;
-        g.d.wx = weights_ready && wx.n ? wx.p : nullptr;
-        // the wave-shared weight search carries a block's limit above bit 47
-        // of its address
-        for (const void* ptr : {static_cast<const void*>(w.p), static_cast<const void*>(wx.p)})
-            if (reinterpret_cast<uintptr_t>(ptr) >> 48)
-                throw std::runtime_error("weight arrays above the 48-bit address range");
-    }
+    // the weight pickers' view of the sampled direction's per-node weights
+    const WalkWeights& ww = forward ? out.wf : d.wb;
+    const bool wview = weights_ready && ww.hdr.n == d.hdr.n && ww.pan.n == d.pan.n;
+    g.d.whdr = wview ? ww.hdr.p : nullptr;
+    g.d.wpan = wview ? ww.pan.p : nullptr;
+    g.d.wgt = wview ? ww.tab.p : nullptr;
+    g.d.w_size = wview ? d.n_groups : 0;
     g.adj_off = adj_lists_ready ? adj_off.p : nullptr;
     g.adj_nbr = adj_nbr.p;
     g.adj_nodes = adj_ready ? static_cast<uint32_t>(adj_nodes) : 0;
@@ -2146,37 +1897,35 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
         g.T = 0;
         g.active_size = 0;
     }
-    const bool index_only = is_index_picker(walk_bias) && is_index_picker(start_bias);
+    // The index family's kernels serve the index pickers; without weights a
+    // weight picker picks nothing there, as it does in the reference (its
+    // range check against an empty weight array).  The weight families read
+    // the weighted view instead of the plain headers and panel.
+    const bool index_only = (is_index_picker(walk_bias) && is_index_picker(start_bias)) || !wview;
     const bool no_node2vec = walk_bias != kTemporalNode2Vec;  // start_bias never is (above)
     // the index arrays the launched walk kernel reads (each counted whole):
-    // headers, bucket tables, panel and records of the sampled direction;
-    // per-node weights and their search index for a weight picker on the
-    // hops; the adjacency pair set for node2vec
-    w_index_bytes = d.hdr.bytes() + d.tab.bytes() + d.pan.bytes() + d.rec.bytes();
-    if (!is_index_picker(walk_bias) && weights_ready) {
-        const DirIndex& wd = (!forward && cfg.is_directed) ? in : out;
-        w_index_bytes += (forward ? wd.w_fwd : wd.w_bwd).bytes() +
-                         (forward ? wd.wx_fwd : wd.wx_bwd).bytes() + wd.wx_off.bytes();
-    }
+    // headers (plain or weighted), bucket tables, panel (plain or weighted)
+    // and records of the sampled direction, the guide tables for the weight
+    // families; the adjacency pair set for node2vec
+    w_index_bytes = d.tab.bytes() + d.rec.bytes() +
+                    (index_only ? d.hdr.bytes() + d.pan.bytes() : ww.bytes());
     if (walk_bias == kTemporalNode2Vec && adj_ready) w_index_bytes += adj_hash.bytes();
-#define TRW_LAUNCH_FAMILY(K, KW, F, D, G, ...)                                                 \
+#define TRW_LAUNCH_FAMILY(K, F, D, G, ...)                                                     \
     do {                                                                                       \
         if (index_only)                                                                        \
             hipLaunchKernelGGL((K<F, D, kFamIndex>), G, dim3(kB), 0, s, __VA_ARGS__);           \
         else if (no_node2vec)                                                                  \
-            hipLaunchKernelGGL((KW<F, D, kFamWeight>), G, dim3(kB), 0, s, __VA_ARGS__);         \
+            hipLaunchKernelGGL((K<F, D, kFamWeight>), G, dim3(kB), 0, s, __VA_ARGS__);          \
         else                                                                                   \
             hipLaunchKernelGGL((K<F, D, kFamAny>), G, dim3(kB), 0, s, __VA_ARGS__);             \
     } while (0)
-// K for every family, or KW in K's place for the weight family
-#define TRW_LAUNCH2(K, KW, G, ...)                                                             \
+#define TRW_LAUNCH(K, G, ...)                                                                  \
     do {                                                                                       \
-        if (forward && cfg.is_directed) TRW_LAUNCH_FAMILY(K, KW, true, true, G, __VA_ARGS__);  \
-        else if (forward) TRW_LAUNCH_FAMILY(K, KW, true, false, G, __VA_ARGS__);               \
-        else if (cfg.is_directed) TRW_LAUNCH_FAMILY(K, KW, false, true, G, __VA_ARGS__);       \
-        else TRW_LAUNCH_FAMILY(K, KW, false, false, G, __VA_ARGS__);                           \
+        if (forward && cfg.is_directed) TRW_LAUNCH_FAMILY(K, true, true, G, __VA_ARGS__);      \
+        else if (forward) TRW_LAUNCH_FAMILY(K, true, false, G, __VA_ARGS__);                   \
+        else if (cfg.is_directed) TRW_LAUNCH_FAMILY(K, false, true, G, __VA_ARGS__);           \
+        else TRW_LAUNCH_FAMILY(K, false, false, G, __VA_ARGS__);                               \
     } while (0)
-#define TRW_LAUNCH(K, G, ...) TRW_LAUNCH2(K, K, G, __VA_ARGS__)
 
     // ---- processing order: walks sorted by the time rank of their start
     // edge, so the walks of one wave -- and of one XCD -- search the same
@@ -2282,16 +2031,16 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
         a.edge_ts = ts.p;
         a.start_ts = INT64_MIN;
         const dim3 grid(grid_for(nw));
-        launch_rows(cfg.is_directed, index_only, grid, s, g, a);
+        launch_rows(cfg.is_directed, index_only ? kFamIndex : (no_node2vec ? kFamWeight : kFamAny),
+                    grid, s, g, a);
         check_hip(hipGetLastError(), "walk kernel launch");
     } else if (nw) {
         a.q0 = 0;
         a.q_end = nw;
-        TRW_LAUNCH2(walk_kernel, walk_weights_kernel, dim3(grid_for(nw)), g, a);
+        TRW_LAUNCH(walk_kernel, dim3(grid_for(nw)), g, a);
         check_hip(hipGetLastError(), "walk kernel launch");
     }
 #undef TRW_LAUNCH
-#undef TRW_LAUNCH2
 #undef TRW_LAUNCH_FAMILY
     check_hip(hipEventRecord(ev[6], s), "event");
     if (nw && L > 0 && !rows_direct) {

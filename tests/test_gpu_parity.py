@@ -491,11 +491,11 @@ def test_replay_walks_weight_pickers(directed, forward, picker):
 
 @pytest.mark.parametrize("directed,g", [(True, 300_000), (False, 300_000), (True, 1_200_000)])
 def test_replay_walks_exponential_weight_deep_search_index(directed, g):
-    """ExponentialWeight walks through a hub of 300k (1.2M) timestamp groups:
-    its weight search index has five (six) levels above the weights, searched
-    by the wave together.  Walks of every length end at different hops, so
-    waves keep lanes with ended walks in the shared search.  Walk-picker index
-    families mixed with weight starts go through the same loop."""
+    """ExponentialWeight walks through a hub of 300k (1.2M) timestamp groups,
+    whose picks go through its guide table (and, for a wide bracket, its
+    weight search index of five or six levels).  Walks of every length end
+    at different hops.  Walk-picker index families mixed with weight starts
+    go through the same kernels."""
     rng = np.random.default_rng(71)
     hub_t = rng.permutation(g).astype(np.int64) * 3
     hub_d = rng.integers(1, 3_000, g).astype(np.int32)
@@ -538,6 +538,53 @@ def test_replay_walks_exponential_weight_deep_search_index(directed, g):
         _walk_case(og, eng, "ExponentialWeight", "ExponentialWeight", forward, "nodes", 20, 300,
                    seed_nodes=np.array([0, 0, 0, 7], np.int32),
                    cutoffs=np.array([g, 2 * g, -1, 3 * g // 2], np.int64), seed=75)
+
+
+@pytest.mark.parametrize("bound", [-1.0, 1e-4, 5.0, 200.0])
+def test_replay_walks_weight_guide_profiles(bound):
+    """Weight picks look their group up in a per-node guide table keyed by
+    the bit pattern of the cumulative weight (1 - c for forward weights, c
+    for backward ones), then settle the bracket.  Profiles that stress it,
+    bit-exact against the oracle on the engine's weights: unscaled weights
+    (bound -1) over gaps of 1 to 10^6, which fall by hundreds of orders of
+    magnitude between groups (runs of thousands of empty buckets, filled by
+    workgroups) and sit at exactly 0 or 1 over long stretches; nearly flat
+    weights (bound 1e-4: many groups per bucket where the key is linear in
+    c); the cfg4-like exponential (bound 5); and a steep one (200, weights
+    exhausted within a few percent of the span).  The hubs are picked from
+    by walks in both directions, from weight-picked starts (the global
+    guides) and from seeds with cutoffs."""
+    rng = np.random.default_rng(401)
+    n_hub = 40_000
+    gaps = rng.choice(np.array([1, 2, 3, 40, 5_000, 1_000_000]), n_hub,
+                      p=[0.5, 0.2, 0.15, 0.1, 0.045, 0.005])
+    hub_t = np.cumsum(gaps).astype(np.int64)
+    span = int(hub_t[-1])
+    # hub 0: one edge per group; hub 1: the same times with 1-6 edges each
+    reps = rng.integers(1, 7, n_hub)
+    s = [np.zeros(n_hub, np.int32), np.ones(int(reps.sum()), np.int32)]
+    d = [rng.integers(2, 2_000, n_hub).astype(np.int32),
+         rng.integers(2, 2_000, int(reps.sum())).astype(np.int32)]
+    t = [hub_t, np.repeat(hub_t, reps)]
+    n_o = 60_000
+    s.append(rng.integers(2, 2_000, n_o).astype(np.int32))
+    d.append(np.where(rng.random(n_o) < 0.5, rng.integers(0, 2, n_o),
+                      rng.integers(2, 2_000, n_o)).astype(np.int32))
+    t.append(rng.integers(0, span, n_o).astype(np.int64))
+    s, d, t = np.concatenate(s), np.concatenate(d), np.concatenate(t)
+    og, eng = _pair(True, [(s, d, t)], weights=True, timescale_bound=bound)
+    for name in WEIGHT_ARRAYS:
+        w = eng.array(name)
+        if w.size:
+            og.set_weights(name, w)
+    seeds = np.array([0, 1, 0, 1, 5, 0, 1], np.int32)
+    cuts = np.array([-1, -1, span // 2, span // 3, -1, int(hub_t[100]), int(hub_t[-50])], np.int64)
+    for forward in (True, False):
+        _walk_case(og, eng, "ExponentialWeight", "ExponentialWeight", forward, "total", 24,
+                   8_000, seed=402)
+        _walk_case(og, eng, "ExponentialWeight", "Uniform", forward, "nodes", 16, 300,
+                   seed_nodes=seeds, cutoffs=cuts, seed=403)
+    eng.close()
 
 
 def test_replay_walks_powerlaw_exponential_index():
