@@ -648,14 +648,15 @@ __global__ void global_guide_kernel(const double* __restrict__ w, size_t n, int 
     out[0] = make_guide(w, static_cast<uint32_t>(n), decaying != 0);
 }
 
-// The weighted panel: every group's panel record with its cumulative weight,
-// plus the panel's terminator.
+// The weighted panel: every group's panel record with its end, cumulative
+// weight and first edge record.
 __global__ void wpan_kernel(const PanelRec* __restrict__ pan, const double* __restrict__ w,
-                            size_t ng, WPanelRec* __restrict__ out) {
+                            const EdgeRec* __restrict__ rec, size_t ng,
+                            WPanelRec* __restrict__ out) {
     const size_t g = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
-    if (g > ng) return;
+    if (g >= ng) return;
     const PanelRec p = pan[g];
-    out[g] = WPanelRec{p.rank, p.start, g < ng ? w[g] : 0.0};
+    out[g] = WPanelRec{p.rank, p.start, pan[g + 1].start, 0u, w[g], rec[p.start]};
 }
 
 // The buckets [from, to] of group g (local index i of a segment of G): those
@@ -1362,12 +1363,13 @@ void build_walk_weights(Engine& e, DirIndex& dir, size_t v, const DBuf<double>& 
     hipStream_t s = e.stream;
     const size_t vc = v + 1, g = dir.n_groups;
     ww.hdr.resize(vc);
-    ww.pan.resize(g + 1);
+    ww.pan.resize(g);
     ww.tab.resize(2 * (g + v));
     hipLaunchKernelGGL(whdr_kernel, dim3(grid_for(vc)), dim3(kB), 0, s, w.p, dir.cnt.p, dir.hdr.p,
                        vc, decaying ? 1 : 0, ww.hdr.p);
-    hipLaunchKernelGGL(wpan_kernel, dim3(grid_for(g + 1)), dim3(kB), 0, s, dir.pan.p, w.p, g,
-                       ww.pan.p);
+    if (g)
+        hipLaunchKernelGGL(wpan_kernel, dim3(grid_for(g)), dim3(kB), 0, s, dir.pan.p, w.p,
+                           dir.rec.p, g, ww.pan.p);
     fill_weight_guides(e, w.p, g, dir.key.p, dir.grp.p, dir.cnt.p, ww.hdr.p, nullptr, decaying,
                        ww.tab.p, ww.tab.n);
     check_hip(hipGetLastError(), "walk weights launch");

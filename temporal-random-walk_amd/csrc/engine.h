@@ -147,8 +147,8 @@ struct SampleTarget {
 // (index_layout.h): node headers with guide parameters, the weighted panel and
 // the guide tables.
 struct WalkWeights {
-    DBuf<WNodeHdr> hdr;  // V_c
-    DBuf<WPanelRec> pan;  // g + 1
+    DBuf<WNodeHdr> hdr;   // V_c
+    DBuf<WPanelRec> pan;  // g
     DBuf<uint32_t> tab;   // 2 (g + V_c - 1)
     void clear() { hdr.n = pan.n = tab.n = 0; }
     size_t bytes() const { return hdr.bytes() + pan.bytes() + tab.bytes(); }

@@ -40,8 +40,8 @@
 //   walks: in with w_bwd, or out with w_bwd if undirected)
 //     whdr          WNodeHdr[V_c]  node header + guide parameters and weight
 //                                  total of the node's cumulative weights
-//     wpan          WPanelRec[g+1] (ts rank, start, cumulative weight) of every
-//                                  group: pan and the weights in one record
+//     wpan          WPanelRec[g]   (ts rank, start, end, cumulative weight,
+//                                  first edge record) of every group
 //     wgt           uint32[2(g+V_c)] guide tables of nodes with > kWGuideMin
 //                                  groups, node u's at 2 (gb + u) (below)
 //   global weights  fwd_cum, bwd_cum fp64[T] (+ their guides: one segment)
@@ -96,6 +96,10 @@ constexpr uint64_t kAdjHashMul = 0x9E3779B97F4A7C15ull;
 // the bits of c itself.  Either way an exponential weight profile maps to
 // keys that are close to linear in the group index.
 constexpr uint32_t kWgBucketsPerGroup = 2;
+// A segment of G weights has at most kWgBucketsPerGroup * G buckets plus the
+// closing entry; node u's table at 2 (gb + u) has room for 2 G + 2 of them,
+// and a global segment's table holds 2 G + 1.
+static_assert(kWgBucketsPerGroup <= 2, "guide tables have room for 2 buckets per group");
 // Runs of more buckets than this between two consecutive groups are filled by
 // a workgroup each rather than by the group's thread.
 constexpr uint32_t kWgRun = 64;
@@ -178,14 +182,19 @@ struct alignas(32) WNodeHdr {
 };
 static_assert(sizeof(WNodeHdr) == 32, "WNodeHdr must be 32 bytes");
 
-// One node-timestamp group in the weight pickers' panel: the panel record and
-// the group's cumulative weight, so the weight search, the slice's sums and
-// the picked group's range read the same lines.
-struct alignas(16) WPanelRec {
+// One node-timestamp group in the weight pickers' panel: its panel record, its
+// end, its cumulative weight and its first edge record, so the weight search,
+// the slice's sums, the picked group's range and -- for a group of one edge
+// -- the edge itself read one aligned 32-byte record.
+struct alignas(32) WPanelRec {
     uint32_t rank;
     uint32_t start;
+    uint32_t end;  // the next group's start
+    uint32_t pad;
     double c;
+    EdgeRec rec0;  // rec[start]
 };
-static_assert(sizeof(WPanelRec) == 16, "WPanelRec must be 16 bytes");
+static_assert(sizeof(WPanelRec) == 32, "WPanelRec must be 32 bytes");
+
 
 }  // namespace trw

@@ -57,7 +57,7 @@ struct DirView {
     // the weight pickers' view of the sampled direction's cumulative weights
     // (read by the weight families' kernels only; nullptr without weights)
     const WNodeHdr* whdr;   // V_c node headers with guide parameters
-    const WPanelRec* wpan;  // g + 1 weighted panel records
+    const WPanelRec* wpan;  // g weighted panel records
     const uint32_t* wgt;    // guide tables, node u's at 2 (gb + u)
     uint64_t w_size;        // groups with weights (0: none)
 };
@@ -290,8 +290,10 @@ __device__ __forceinline__ uint32_t guided_lower_bound(CAt c, uint32_t G, const 
     if (G > kWGuideMin) {
         const u32x2_a4 br =
             *reinterpret_cast<const u32x2_a4*>(gt + wg_bucket(gd.bs, wg_key(target, Decaying)));
-        lo = br.x;
-        hi = br.y;
+        // (the table's entries are local indexes in [0, G]; the clamps keep
+        // every probe inside the segment whatever they hold)
+        hi = br.y < G ? br.y : G;
+        lo = br.x < hi ? br.x : hi;
         // a wide bracket is a run of equal keys (a weight repeated, as a
         // saturated forward sum is): its first weight usually answers
         if (hi - lo > 4 && !(c(lo) < target)) return lo;
@@ -392,14 +394,37 @@ __device__ __forceinline__ bool adjacent(const WalkGraph& g, int prev, int cand)
     return lo < end && g.adj_nbr[lo] == cand;
 }
 
+// The edge of group x of a node's weighted panel f (x < G): a uniform pick re
+// within the group's range -- (int)(re * size) as edge_selectors.cuh:420-443
+// takes it, or, for node2vec (Clamp), min((size_t)(re * size), size - 1) as
+// temporal_node2vec_helpers.cuh:169-182 does.  The group's record holds its
+// first edge record, so a pick of entry 0 (every pick in a group of one edge)
+// loads no record.
+template <bool Clamp>
+__device__ __forceinline__ Hop weighted_group_hop(const WalkGraph& g, const WPanelRec* f,
+                                                  uint32_t x, double re) {
+    const u32x4_a8 v = *reinterpret_cast<const u32x4_a8*>(f + x);  // rank, start, end
+    const uint32_t rank = v.x, es = v.y, ee = v.z;
+    const EdgeRec r0 = f[x].rec0;
+    if (es >= ee || es >= g.d.idx_size || ee > g.d.idx_size) return no_hop();
+    uint32_t k;
+    if (Clamp) {
+        const uint64_t local = static_cast<uint64_t>(re * static_cast<double>(ee - es));
+        k = static_cast<uint32_t>(local < ee - es ? local : ee - es - 1);
+    } else {
+        k = static_cast<uint32_t>(static_cast<int>(re * static_cast<int>(ee - es)));
+    }
+    return hop_of(k == 0 ? r0 : load_rec(g.d.rec + es + k), rank);
+}
+
 // graph/temporal_node2vec_helpers.cuh:127-199 over the slice [vb, ve) of a
 // node's G groups (local indexes; f is its weighted panel, gt its guide
-// table).  The candidate node of a proposal is its record's neighbour
-// (get_candidate_node, walk_step_helpers.cuh:40-54).
+// table), with the slice's sums loaded.  The candidate node of a proposal is
+// its record's neighbour (get_candidate_node, walk_step_helpers.cuh:40-54).
 template <bool Fwd>
 __device__ Hop tn2v_pick(const WalkGraph& g, int prev, const WPanelRec* f, uint32_t G,
-                         const uint32_t* gt, const WGuide& gd, uint32_t vb, uint32_t ve, double rg,
-                         double re) {
+                         const uint32_t* gt, const WGuide& gd, uint32_t vb, uint32_t ve,
+                         double start_sum, double end_sum, double rg, double re) {
     if (vb >= ve || prev == -1) return no_hop();
     double bmax = 1.0;
     if (g.inv_p > bmax) bmax = g.inv_p;
@@ -411,10 +436,6 @@ __device__ Hop tn2v_pick(const WalkGraph& g, int prev, const WPanelRec* f, uint3
     const double acc_adj = 1.0 * inv_bmax, acc_far = g.inv_q * inv_bmax;
     const double acc_lo = acc_adj < acc_far ? acc_adj : acc_far;
     const double acc_hi = acc_adj < acc_far ? acc_far : acc_adj;
-    // every retry's weight pick (over the slice [vb, ve)) reads the same two
-    // sums: loaded once, outside the loop
-    const double start_sum = vb > 0 ? f[vb - 1].c : 0.0;
-    const double end_sum = ve == G ? gd.total : f[ve - 1].c;
     if (end_sum < start_sum) return no_hop();
     Hop last = no_hop();
     for (int retry = 0; retry < kNode2VecMaxRetries; ++retry) {
@@ -425,14 +446,10 @@ __device__ Hop tn2v_pick(const WalkGraph& g, int prev, const WPanelRec* f, uint3
         // a pick one past the node's last group is an empty range in the
         // reference (get_node_group_edge_end, walk_step_helpers.cuh:19-38)
         if (x >= G) continue;
-        const u32x2_a4 rs = *reinterpret_cast<const u32x2_a4*>(f + x);  // rank, start
-        const uint32_t es = rs.y, ee = f[x + 1].start;
-        if (es >= ee) continue;
-        const uint64_t local = static_cast<uint64_t>(er * static_cast<double>(ee - es));
-        const uint32_t pick = es + static_cast<uint32_t>(local < ee - es ? local : ee - es - 1);
-        const EdgeRec r = load_rec(g.d.rec + pick);
-        const int cand = r.nbr;
-        last = hop_of(r, rs.x);
+        const Hop h = weighted_group_hop<true>(g, f, x, er);
+        if (h.e == -1) continue;
+        last = h;
+        const int cand = h.nbr;
         bool accept;
         if (cand == prev) accept = ar < g.inv_p * inv_bmax;
         else if (ar < acc_lo) accept = true;
@@ -456,18 +473,6 @@ __device__ __forceinline__ Hop hop_from_group(const WalkGraph& g, uint32_t gpos,
     return hop_of(load_rec(g.d.rec + es +
                            static_cast<uint32_t>(static_cast<int>(re * static_cast<int>(ee - es)))),
                   pp.rank);
-}
-
-// The same over a weighted panel f of G groups, group x (local).
-__device__ __forceinline__ Hop whop_from_group(const WalkGraph& g, const WPanelRec* f, uint32_t x,
-                                               uint32_t G, double re) {
-    if (x >= G) return no_hop();
-    const u32x2_a4 rs = *reinterpret_cast<const u32x2_a4*>(f + x);  // rank, start
-    const uint32_t es = rs.y, ee = f[x + 1].start;
-    if (es >= ee || es >= g.d.idx_size || ee > g.d.idx_size) return no_hop();
-    return hop_of(load_rec(g.d.rec + es +
-                           static_cast<uint32_t>(static_cast<int>(re * static_cast<int>(ee - es)))),
-                  rs.x);
 }
 
 // Per-hop selector (edge_selectors.cuh:277-443).  The reference first checks
@@ -521,7 +526,7 @@ __device__ __forceinline__ Hop node_edge_from(const WalkGraph& g, int picker, ui
 
 // The same for any picker, over the weighted view (the weight families'
 // kernels): the time search, the slice's sums, the weight search and the
-// picked group's range all read the node's weighted panel.
+// picked group's range and first edge read the node's weighted panel.
 template <bool Fwd, int Fam>
 __device__ __forceinline__ Hop wnode_edge_from(const WalkGraph& g, int picker, uint32_t u, bool ok,
                                                const WNodeHdr& wh, int32_t t, int32_t cut,
@@ -548,16 +553,18 @@ __device__ __forceinline__ Hop wnode_edge_from(const WalkGraph& g, int picker, u
         // the reference's range check: no weights, no pick
         if (gb + Gu > g.d.w_size) return no_hop();
         const uint32_t* gt = g.d.wgt + hdr_tab_base(h, u);
-        if (Fam != kFamWeight && picker == kTemporalNode2Vec && prev != -1)
-            return tn2v_pick<Fwd>(g, prev, f, Gu, gt, wh.g, vb, ve, rg, re);
-        // ExponentialWeight, or node2vec's first hop (no previous node)
+        // the slice's sums: the cumulative weight before vb and at ve - 1
         const double start_sum = vb > 0 ? f[vb - 1].c : 0.0;
         const double end_sum = ve == G ? wh.g.total : f[ve - 1].c;
+        if (Fam != kFamWeight && picker == kTemporalNode2Vec && prev != -1)
+            return tn2v_pick<Fwd>(g, prev, f, Gu, gt, wh.g, vb, ve, start_sum, end_sum, rg, re);
+        // ExponentialWeight, or node2vec's first hop (no previous node)
         if (end_sum < start_sum) return no_hop();
         x = node_weight_pick<Fwd>(f, Gu, gt, wh.g, static_cast<uint32_t>(vb),
                                   static_cast<uint32_t>(ve), rg, start_sum, end_sum);
+        if (x >= Gu) return no_hop();
     }
-    return whop_from_group(g, f, x, Gu, re);
+    return weighted_group_hop<false>(g, f, x, re);
 }
 
 // The node header a family's kernel loads per hop (issued before the hop's
@@ -1862,7 +1869,7 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
     g.d.idx_size = static_cast<uint32_t>(d.n_entries);
     // the weight pickers' view of the sampled direction's per-node weights
     const WalkWeights& ww = forward ? out.wf : d.wb;
-    const bool wview = weights_ready && ww.hdr.n == d.hdr.n && ww.pan.n == d.pan.n;
+    const bool wview = weights_ready && ww.hdr.n == d.hdr.n && ww.pan.n == d.n_groups;
     g.d.whdr = wview ? ww.hdr.p : nullptr;
     g.d.wpan = wview ? ww.pan.p : nullptr;
     g.d.wgt = wview ? ww.tab.p : nullptr;

@@ -551,9 +551,11 @@ def test_replay_walks_weight_guide_profiles(bound):
     workgroups) and sit at exactly 0 or 1 over long stretches; nearly flat
     weights (bound 1e-4: many groups per bucket where the key is linear in
     c); the cfg4-like exponential (bound 5); and a steep one (200, weights
-    exhausted within a few percent of the span).  The hubs are picked from
-    by walks in both directions, from weight-picked starts (the global
-    guides) and from seeds with cutoffs."""
+    exhausted within a few percent of the span).  Most other edges reuse the
+    hubs' timestamps, so the hubs hold most ranks of their span and take the
+    rank-table path (single-rank time buckets).  The hubs are picked from by
+    ExponentialWeight and TemporalNode2Vec walks in both directions, from
+    weight-picked starts (the global guides) and from seeds with cutoffs."""
     rng = np.random.default_rng(401)
     n_hub = 40_000
     gaps = rng.choice(np.array([1, 2, 3, 40, 5_000, 1_000_000]), n_hub,
@@ -570,9 +572,11 @@ def test_replay_walks_weight_guide_profiles(bound):
     s.append(rng.integers(2, 2_000, n_o).astype(np.int32))
     d.append(np.where(rng.random(n_o) < 0.5, rng.integers(0, 2, n_o),
                       rng.integers(2, 2_000, n_o)).astype(np.int32))
-    t.append(rng.integers(0, span, n_o).astype(np.int64))
+    t.append(np.where(rng.random(n_o) < 0.8, rng.choice(hub_t, n_o),
+                      rng.integers(0, span, n_o)).astype(np.int64))
     s, d, t = np.concatenate(s), np.concatenate(d), np.concatenate(t)
-    og, eng = _pair(True, [(s, d, t)], weights=True, timescale_bound=bound)
+    og, eng = _pair(True, [(s, d, t)], weights=True, tn2v=True, timescale_bound=bound, p=0.5,
+                    q=2.0)
     for name in WEIGHT_ARRAYS:
         w = eng.array(name)
         if w.size:
@@ -584,6 +588,10 @@ def test_replay_walks_weight_guide_profiles(bound):
                    8_000, seed=402)
         _walk_case(og, eng, "ExponentialWeight", "Uniform", forward, "nodes", 16, 300,
                    seed_nodes=seeds, cutoffs=cuts, seed=403)
+        _walk_case(og, eng, "TemporalNode2Vec", "ExponentialWeight", forward, "total", 16,
+                   4_000, seed=404)
+        _walk_case(og, eng, "TemporalNode2Vec", "Uniform", forward, "nodes", 12, 200,
+                   seed_nodes=seeds, cutoffs=cuts, seed=405)
     eng.close()
 
 
