@@ -309,18 +309,20 @@ def other_roofline(k, compulsory, kernel_ms, kernel):
 GATHER_TABLES = (("l2_2MiB", 2 << 20), ("mall_128MiB", 128 << 20), ("hbm_4GiB", 4 << 30))
 
 
-def gather_ceiling(capi, pmc, pmc_current, walk_kernel_ms):
-    """Random 8-byte gather rates of this GPU (trw_probe_gather: 512K lanes x
+def gather_ceiling(pmc, pmc_current, walk_kernel_ms):
+    """Random 8-byte gather rates of this GPU (the probe library, libtrw_probe.so: 512K lanes x
     256 gathers per launch, mean of 5 launches after a warm-up) from tables
     that fit L2, the Infinity Cache and neither, as independent loads and as
     dependent chains; beside them the walk kernel's L1 -> L2 read rate from
     its counter profile (every one of its per-lane record, panel and header
     loads that misses L1 is one such read)."""
+    import probe  # temporal-random-walk_amd/probe: the probe library's wrapper
+
     out = {"unit": "gathers/s", "independent": {}, "chained": {}}
     for name, size in GATHER_TABLES:
         for mode in ("independent", "chained"):
-            r = capi.probe_gather(size, lanes=256 * 2048, rounds=256,
-                                  chained=(mode == "chained"), reps=5)
+            r = probe.gather(size, lanes=256 * 2048, rounds=256, chained=(mode == "chained"),
+                             reps=5)
             out[mode][name] = r["gathers_per_s"]
     c = (pmc or {}).get("counters", {}) if pmc_current else {}
     reads = c.get("TCP_TCC_READ_REQ_sum")
@@ -431,7 +433,7 @@ def run_other_config(k, args):
         if not args.no_gather_ceiling:
             pmc, current = pmc_profile(os.path.join(ROOT, "profiles", f"walk_kernel_cfg{k}_pmc.json"),
                                        "walk")
-            res["gather_ceiling"] = gather_ceiling(capi, pmc, current, res["walk_kernel_ms"])
+            res["gather_ceiling"] = gather_ceiling(pmc, current, res["walk_kernel_ms"])
     elif k == 5:
         eng = capi.Engine(is_directed=True, global_seed=42, shuffle_walk_order=False,
                           max_time_capacity=3_000_000, enable_temporal_node2vec=True,
@@ -475,7 +477,7 @@ def run_other_config(k, args):
         if not args.no_gather_ceiling:
             pmc, current = pmc_profile(os.path.join(ROOT, "profiles", "walk_kernel_cfg5_pmc.json"),
                                        "walk")
-            res["gather_ceiling"] = gather_ceiling(capi, pmc, current, res["walk_kernel_ms"])
+            res["gather_ceiling"] = gather_ceiling(pmc, current, res["walk_kernel_ms"])
         if args.host_ingest:
             res["host_ingest"] = cfg5_host_ingest(capi, configs)
     else:
@@ -568,7 +570,7 @@ def main():
                     help="--config 5: this share of every batch after the first gets "
                          "timestamps of the previous batch's range (late arrivals)")
     ap.add_argument("--no-gather-ceiling", action="store_true",
-                    help="skip the random-gather rate probe (trw_probe_gather)")
+                    help="skip the random-gather rate probe (libtrw_probe.so)")
     ap.add_argument("--gather-ceiling-only", action="store_true",
                     help="run only the random-gather probe and print its rates")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -595,7 +597,7 @@ def main():
         return
     if args.gather_ceiling_only:
         from temporal_random_walk import capi
-        print(json.dumps(gather_ceiling(capi, None, False, 1.0)))
+        print(json.dumps(gather_ceiling(None, False, 1.0)))
         return
 
     import numpy as np
@@ -750,7 +752,7 @@ def main():
     eng.close()
     if not args.no_gather_ceiling:
         log("random-gather probe")
-        result["gather_ceiling"] = gather_ceiling(capi, pmc, pmc_current, walk_kernel_ms)
+        result["gather_ceiling"] = gather_ceiling(pmc, pmc_current, walk_kernel_ms)
     if not args.no_host_boundary:
         from temporal_random_walk import TemporalRandomWalk
 

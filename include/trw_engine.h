@@ -258,9 +258,10 @@ trw_status trw_sample_device(void* handle, const trw_sample_params* params, trw_
  * -- 640 B per walk at max_walk_len 80 -- where a layout pass writes the
  * rows), more walks than capacity_walks, or misaligned buffers, is rejected
  * with TRW_ERR_INVALID_ARGUMENT.  Calls on one
- * device share that array, so calls that overlap on one device race; the
- * array keeps the last call's contents.  trw_get_walk_stats does not describe
- * these walks. */
+ * device share that array: calls of any handles on one device run one at a
+ * time (a per-device lock held for the whole call; a call returns with its
+ * walks written), and the array keeps the last call's contents.
+ * trw_get_walk_stats does not describe these walks. */
 trw_status trw_sample_device_noalloc(void* handle, const trw_sample_params* params,
                                      uint64_t capacity_walks, trw_walks* out);
 /* free() of the host buffers of a trw_walks returned by trw_sample. */
@@ -354,32 +355,17 @@ trw_status trw_get_walk_stats(void* handle, trw_walk_stats* out);
 /* ---- test hooks ---------------------------------------------------------- */
 
 /* After this call, the next n device allocations of any handle succeed and the
- * one after them fails as out of memory (TRW_ERR_OUT_OF_MEMORY); n < 0
- * disarms.  For tests of the failure paths: an ingest that fails after its
- * batch was accepted leaves the handle empty, as after trw_clear.  No
- * counterpart in the reference. */
+ * one after them fails as out of memory (TRW_ERR_OUT_OF_MEMORY), its retry
+ * included; n < 0 disarms.  For tests of the failure paths: an ingest that
+ * fails after its batch was accepted leaves the handle empty, as after
+ * trw_clear.  No counterpart in the reference. */
 void trw_debug_fail_allocation(int64_t n);
-
-/* ---- measurement aid ------------------------------------------------------ */
-
-/* The rate at which the device serves random 8-byte gathers from a table of
- * table_bytes (a power of two, 4 KiB - 64 GiB, filled with random words):
- * lanes (a multiple of 256) each make `rounds` gathers (at most 2^36 in all),
- * as independent loads (chained 0) or as a chain whose next address follows
- * from the loaded value (chained 1, one load in flight per lane, as a walk
- * has).  One warm-up launch, then
- * reps timed launches on the null stream; out gets the mean time per launch.
- * Every gather is one L1 miss, so the rate bounds the walk kernels' L1 -> L2
- * read rate.  It allocates the table for the call.  No counterpart in the
- * reference: the reference has no such measurement. */
-typedef struct trw_probe_result {
-    double ms;            /* per launch */
-    double gathers_per_s;
-    uint64_t gathers;     /* per launch: lanes * rounds */
-} trw_probe_result;
-trw_status trw_probe_gather(int32_t device_id, uint64_t table_bytes, uint32_t lanes,
-                            uint32_t rounds, int32_t chained, int32_t reps,
-                            trw_probe_result* out);
+/* The same, but only the allocation's first attempt fails: an allocation that
+ * runs out of memory while blocks of grown buffers are held (they are kept
+ * until trw_clear, a failed ingest or destruction, and counted by
+ * trw_get_memory_used) releases them and tries once more, which then
+ * succeeds; with none held it fails.  No counterpart in the reference. */
+void trw_debug_fail_allocation_transient(int64_t n);
 
 /* ---- standalone pickers (proxies/RandomPicker.cu:11-313) --------------------- */
 

@@ -6,7 +6,10 @@ Produces, inside ``temporal-random-walk_amd/temporal_random_walk/``:
   C ABI of ``include/trw_engine.h``;
 * ``_temporal_random_walk*.so`` -- the pybind11 module that mirrors the
   reference's Python surface on top of the C++ ``TemporalRandomWalk`` class,
-  which calls the C ABI.
+  which calls the C ABI;
+
+and ``temporal-random-walk_amd/probe/libtrw_probe.so``, bench.py's
+random-gather probe (a measurement aid outside the engine).
 
 Run ``python temporal-random-walk_amd/build.py`` (or ``__graft_entry__.build()``).
 """
@@ -43,7 +46,8 @@ HIP_FLAGS = [
     f"-I{INCLUDE}",
 ]
 
-HIP_SOURCES = ["primitives.hip", "build.hip", "walk.hip", "handoff.hip", "pickers.hip", "probe.hip", "capi.hip"]
+HIP_SOURCES = ["primitives.hip", "build.hip", "walk.hip", "handoff.hip", "pickers.hip", "capi.hip"]
+PROBE_DIR = os.path.join(PKG_ROOT, "probe")
 
 
 def _run(cmd):
@@ -94,9 +98,20 @@ def build_python_module() -> str:
     return target
 
 
+def build_probe() -> str:
+    """bench.py's random-gather probe: its own library beside probe.hip, not
+    part of the engine."""
+    lib = os.path.join(PROBE_DIR, "libtrw_probe.so")
+    tmp = lib + ".tmp"
+    _run([HIPCC, *HIP_FLAGS, "-shared", os.path.join(PROBE_DIR, "probe.hip"), "-o", tmp])
+    os.replace(tmp, lib)
+    return lib
+
+
 def build_all() -> None:
     build_engine()
     build_python_module()
+    build_probe()
 
 
 if __name__ == "__main__":

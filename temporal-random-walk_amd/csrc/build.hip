@@ -1462,10 +1462,12 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
         batch_max_id = static_cast<int32_t>(hs[3]);
         build_accepted(d_src, d_dst, d_ts, d_feat, n, dim, hs[0], hs[1]);
     } catch (...) {
-        // the store, its index and the last batch may disagree: start empty
+        // the store, its index and the last batch may disagree: start empty,
+        // and hand back the blocks the failed ingest's growth retired
         (void)hipStreamSynchronize(stream);
         (void)hipStreamSynchronize(side);
         clear();
+        free_retired();
         throw;
     }
 }

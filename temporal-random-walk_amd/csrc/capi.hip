@@ -297,6 +297,9 @@ trw_status trw_sample_device_noalloc(void* handle, const trw_sample_params* para
                                      uint64_t capacity_walks, trw_walks* out) {
     return guarded(handle, [&](Engine& e) {
         if (!params || !out) throw trw::InvalidArgument("null argument");
+        // the device's scratch array is shared by every handle on it: one
+        // call at a time (the sample waits for its stream before returning)
+        std::lock_guard<std::mutex> scratch_lock(trw::noalloc_scratch_lock(e.device));
         trw::SampleTarget t{};
         t.space.base = static_cast<unsigned char*>(trw::noalloc_scratch(e.device));
         t.space.cap = trw::kNoAllocScratchBytes;
@@ -534,12 +537,8 @@ void trw_debug_fail_allocation(int64_t n) {
     trw::g_alloc_fail_after.store(n < 0 ? -1 : n, std::memory_order_relaxed);
 }
 
-trw_status trw_probe_gather(int32_t device_id, uint64_t table_bytes, uint32_t lanes,
-                            uint32_t rounds, int32_t chained, int32_t reps,
-                            trw_probe_result* out) {
-    return guarded_device(device_id, [&] {
-        trw::probe_gather(table_bytes, lanes, rounds, chained, reps, out);
-    });
+void trw_debug_fail_allocation_transient(int64_t n) {
+    trw::g_alloc_fail_transient.store(n < 0 ? -1 : n, std::memory_order_relaxed);
 }
 
 trw_status trw_pick_index(int32_t device_id, int32_t picker, const int32_t* start,

@@ -10,6 +10,7 @@
 #include <atomic>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <new>
 #include <stdexcept>
 #include <string>
@@ -26,9 +27,16 @@ struct InvalidArgument : std::invalid_argument {
     using std::invalid_argument::invalid_argument;
 };
 
-// Test hook (trw_debug_fail_allocation): when >= 0, the number of device
-// allocations that still succeed before one fails as out of memory.
+// Test hooks: when >= 0, the number of device allocations that still succeed
+// before one fails as out of memory -- for good (trw_debug_fail_allocation:
+// its retry fails too), or only at its first attempt
+// (trw_debug_fail_allocation_transient: the retry after releasing the retired
+// blocks succeeds).
 inline std::atomic<long long> g_alloc_fail_after{-1};
+inline std::atomic<long long> g_alloc_fail_transient{-1};
+inline bool alloc_hook_fires(std::atomic<long long>& c) {
+    return c.load(std::memory_order_relaxed) >= 0 && c.fetch_sub(1, std::memory_order_relaxed) == 0;
+}
 
 // Device blocks whose buffers grew during an engine call (set by the C ABI's
 // call guard to the engine's list): they are freed at the engine's next
@@ -40,6 +48,12 @@ inline std::atomic<long long> g_alloc_fail_after{-1};
 struct RetiredBlocks {
     std::vector<void*> blocks;
     size_t bytes = 0;
+    // hipFree waits for the device, so no queued kernel still reads a block
+    void release() {
+        for (void* q : blocks) (void)hipFree(q);
+        blocks.clear();
+        bytes = 0;
+    }
 };
 inline thread_local RetiredBlocks* g_retired = nullptr;
 // Past this many retired bytes a growing buffer frees its old block at once.
@@ -76,10 +90,17 @@ struct DBuf {
                 release();
             }
             const size_t c = std::max(k + k / 4, 2 * old_cap) + 64;
-            if (g_alloc_fail_after.load(std::memory_order_relaxed) >= 0 &&
-                g_alloc_fail_after.fetch_sub(1, std::memory_order_relaxed) == 0)
-                throw std::bad_alloc();
-            const hipError_t e = hipMalloc(&p, c * sizeof(T));
+            if (alloc_hook_fires(g_alloc_fail_after)) throw std::bad_alloc();
+            hipError_t e = alloc_hook_fires(g_alloc_fail_transient) ? hipErrorOutOfMemory
+                                                                     : hipMalloc(&p, c * sizeof(T));
+            if (e == hipErrorOutOfMemory && g_retired && !g_retired->blocks.empty()) {
+                // out of memory while blocks of grown buffers are held: release
+                // them and try once more
+                (void)hipGetLastError();
+                p = nullptr;
+                g_retired->release();
+                e = hipMalloc(&p, c * sizeof(T));
+            }
             if (e == hipErrorOutOfMemory) {
                 (void)hipGetLastError();  // clear the sticky error
                 p = nullptr;
@@ -344,13 +365,10 @@ struct Engine {
     size_t pf_n = 0, pf_dim = 0;
     bool pf_has_feat = false;
 
-    // device blocks retired by buffer growth, freed at clear() / destruction
+    // device blocks retired by buffer growth, freed at clear(), after a failed
+    // ingest, at destruction, or when an allocation runs out of memory
     RetiredBlocks retired;
-    void free_retired() {
-        for (void* q : retired.blocks) (void)hipFree(q);
-        retired.blocks.clear();
-        retired.bytes = 0;
-    }
+    void free_retired() { retired.release(); }
 
     // timings
     hipEvent_t ev[8] = {};
@@ -416,9 +434,6 @@ void pick_index_batch(int picker, const int32_t* start, const int32_t* end, uint
 void pick_weights_batch(const double* cumulative, uint64_t size, const uint64_t* group_start,
                         const uint64_t* group_end, uint64_t n, const double* draws, uint64_t seed,
                         int32_t* out);
-// Random-gather rate of the device (probe.hip), a measurement aid.
-void probe_gather(uint64_t table_bytes, uint32_t lanes, uint32_t rounds, int chained, int reps,
-                  trw_probe_result* out);
 // Rank of timestamp -1 among the stored unique timestamps (-2 if absent) into
 // e.neg1_rank (update_neg1_rank) or into out, on the engine stream.
 void update_neg1_rank(Engine& e);
@@ -428,5 +443,8 @@ void launch_neg1_rank(Engine& e, int32_t* out);
 // handle's creation); noalloc_scratch returns it.
 void init_noalloc_scratch(int device);
 void* noalloc_scratch(int device);
+// Held for the whole of a no-allocation call: calls on one device (of any
+// handles, from any threads) use its scratch array one at a time.
+std::mutex& noalloc_scratch_lock(int device);
 
 }  // namespace trw

@@ -1549,12 +1549,17 @@ static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 namespace {
 std::mutex g_scratch_mu;
 std::vector<void*> g_scratch_ptr;  // per device; nullptr: not looked up yet
+// per device: held by a no-allocation call for its whole length, so calls of
+// any handles on one device take the device's array in turn
+std::vector<std::unique_ptr<std::mutex>> g_scratch_call_mu;
 }  // namespace
 
 void init_noalloc_scratch(int device) {
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (device < 0) throw InvalidArgument("device id out of range");
     if (g_scratch_ptr.size() <= static_cast<size_t>(device)) g_scratch_ptr.resize(device + 1, nullptr);
+    while (g_scratch_call_mu.size() <= static_cast<size_t>(device))
+        g_scratch_call_mu.push_back(std::make_unique<std::mutex>());
     if (g_scratch_ptr[device]) return;
     int cur = -1;
     check_hip(hipGetDevice(&cur), "hipGetDevice");
@@ -1570,6 +1575,13 @@ void* noalloc_scratch(int device) {
     if (device < 0 || static_cast<size_t>(device) >= g_scratch_ptr.size() || !g_scratch_ptr[device])
         throw std::runtime_error("no-allocation scratch was not set up on this device");
     return g_scratch_ptr[device];
+}
+
+std::mutex& noalloc_scratch_lock(int device) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (device < 0 || static_cast<size_t>(device) >= g_scratch_call_mu.size())
+        throw std::runtime_error("no-allocation scratch was not set up on this device");
+    return *g_scratch_call_mu[device];
 }
 
 void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {

@@ -69,8 +69,8 @@ EXPORTS = [
     "trw_get_node_count", "trw_get_edge_count", "trw_get_node_ids", "trw_get_node_degrees",
     "trw_get_edges", "trw_get_is_directed", "trw_get_memory_used", "trw_get_feature_dim",
     "trw_get_latest_timestamp", "trw_clear", "trw_get_array", "trw_get_timings",
-    "trw_get_stream", "trw_get_walk_stats", "trw_debug_fail_allocation", "trw_probe_gather",
-    "trw_pick_index", "trw_pick_weights",
+    "trw_get_stream", "trw_get_walk_stats", "trw_debug_fail_allocation",
+    "trw_debug_fail_allocation_transient", "trw_pick_index", "trw_pick_weights",
 ]
 
 
@@ -150,14 +150,6 @@ class TrwWalkStats(C.Structure):
     ]
 
 
-class TrwProbeResult(C.Structure):
-    _fields_ = [
-        ("ms", C.c_double),
-        ("gathers_per_s", C.c_double),
-        ("gathers", C.c_uint64),
-    ]
-
-
 ABI_VERSION = 7  # TRW_ABI_VERSION of include/trw_engine.h
 _lib = None
 
@@ -207,8 +199,8 @@ def lib():
         L.trw_get_walk_stats.argtypes = [P, C.POINTER(TrwWalkStats)]
         L.trw_debug_fail_allocation.argtypes = [C.c_int64]
         L.trw_debug_fail_allocation.restype = None
-        L.trw_probe_gather.argtypes = [C.c_int32, C.c_uint64, C.c_uint32, C.c_uint32, C.c_int32,
-                                       C.c_int32, C.POINTER(TrwProbeResult)]
+        L.trw_debug_fail_allocation_transient.argtypes = [C.c_int64]
+        L.trw_debug_fail_allocation_transient.restype = None
         L.trw_pick_index.argtypes = [C.c_int32, C.c_int32, P, P, C.c_uint64, C.c_int32, P,
                                      C.c_uint64, P]
         L.trw_pick_weights.argtypes = [C.c_int32, P, C.c_uint64, P, P, C.c_uint64, P,
@@ -341,21 +333,16 @@ def _ptr(a):
 
 def debug_fail_allocation(n):
     """Test hook: the next n device allocations succeed, the one after them
-    fails as out of memory (MemoryError); n < 0 disarms."""
+    fails as out of memory (MemoryError), its retry included; n < 0 disarms."""
     lib().trw_debug_fail_allocation(int(n))
 
 
-def probe_gather(table_bytes, lanes=256 * 2048, rounds=256, chained=False, reps=3,
-                 device_id=-1):
-    """Random 8-byte gathers from a table of table_bytes (a power of two) on
-    the device: lanes * rounds per launch, independent or chained (each address
-    the previous load's value).  Returns {"ms", "gathers_per_s", "gathers"} of
-    one launch (mean over reps after a warm-up).  A measurement aid: the rate
-    bounds the walk kernels' L1 -> L2 read rate."""
-    r = TrwProbeResult()
-    _check(lib().trw_probe_gather(int(device_id), int(table_bytes), int(lanes), int(rounds),
-                                  1 if chained else 0, int(reps), C.byref(r)))
-    return {"ms": r.ms, "gathers_per_s": r.gathers_per_s, "gathers": r.gathers}
+def debug_fail_allocation_transient(n):
+    """Test hook: the next n device allocations succeed and the first attempt
+    of the one after them fails as out of memory; the retry after releasing
+    the blocks of grown buffers the engine holds succeeds (with none held the
+    allocation fails: MemoryError).  n < 0 disarms."""
+    lib().trw_debug_fail_allocation_transient(int(n))
 
 
 class Walks:

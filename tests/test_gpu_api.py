@@ -633,6 +633,53 @@ def test_failed_ingest_leaves_an_empty_usable_engine(shift):
     assert failures >= 10  # the ingest allocates at many points
 
 
+def test_out_of_memory_with_held_blocks_releases_them_and_retries():
+    """A device allocation that runs out of memory while the engine holds the
+    blocks of buffers that grew (kept until clear(), a failed ingest or
+    destruction, and counted by get_memory_used) releases them and tries once
+    more (the transient test hook fails only the first attempt): the ingest
+    completes with the oracle's index.  A fresh engine holds no such blocks,
+    so the same failure ends its first ingest with MemoryError and leaves it
+    empty and usable."""
+    from oracle import pyoracle as po
+    from temporal_random_walk import capi
+    s1, d1, t1 = graphs.cfg1(n_nodes=300, n_edges=2_000, seed=3)
+    s2, d2, t2 = graphs.cfg1(n_nodes=3_000, n_edges=40_000, seed=4)
+    t2 = t2 + 4_000_000
+    og = po.OracleGraph(True, enable_weight_computation=True)
+    for b in ((s1, d1, t1), (s1, d1, t1 + 2_000_000), (s2, d2, t2)):
+        og.add_edges(*b)
+    # a fresh engine: nothing held, the failure stands
+    eng = capi.Engine(is_directed=True, enable_weight_computation=True, global_seed=1)
+    capi.debug_fail_allocation_transient(0)
+    try:
+        with pytest.raises(MemoryError):
+            eng.add_edges(s1, d1, t1)
+    finally:
+        capi.debug_fail_allocation_transient(-1)
+    assert eng.edge_count() == 0
+    eng.close()
+    retried = 0
+    for k in (0, 1, 5, 20, 60):
+        eng = capi.Engine(is_directed=True, enable_weight_computation=True, global_seed=1)
+        eng.add_edges(s1, d1, t1)
+        eng.add_edges(s1, d1, t1 + 2_000_000)  # the store doubles: blocks are held
+        capi.debug_fail_allocation_transient(k)
+        try:
+            eng.add_edges(s2, d2, t2)  # larger: grows the buffers, retiring their blocks
+        finally:
+            capi.debug_fail_allocation_transient(-1)
+        for name in ("timestamps", "node_ts_sorted_outbound_indices",
+                     "node_ts_group_inbound_offsets", "count_ts_group_per_node_outbound"):
+            assert np.array_equal(og.array(name), eng.array(name)), (k, name)
+        np.testing.assert_allclose(eng.array("outbound_forward_cumulative_weights_exponential"),
+                                   og.array("outbound_forward_cumulative_weights_exponential"),
+                                   rtol=1e-12, atol=1e-300)
+        retried += 1
+        eng.close()
+    assert retried == 5
+
+
 def test_walk_stats_byte_accounting():
     """trw_get_walk_stats against numpy: steps, the per-hop demand bytes
     (72 + 8 ceil(log2(G_u + 1)) B with the reference's types) and the
@@ -679,19 +726,3 @@ def test_walk_stats_byte_accounting():
     assert st2["reference_bytes"] == st["reference_bytes"]
     eng.close()
 
-
-def test_gather_probe_counts_its_gathers_and_checks_arguments():
-    """trw_probe_gather, the measurement aid bench.py compares the walk
-    kernel's L1 -> L2 read rate with: lanes * rounds gathers per launch, a
-    positive rate in both modes, and its argument checks."""
-    from temporal_random_walk import capi
-    for chained in (False, True):
-        r = capi.probe_gather(1 << 20, lanes=512, rounds=16, chained=chained, reps=2)
-        assert r["gathers"] == 512 * 16
-        assert r["ms"] > 0 and r["gathers_per_s"] > 0
-    for bad in (dict(table_bytes=3 << 20), dict(table_bytes=1024), dict(lanes=100),
-                dict(rounds=0), dict(reps=0), dict(lanes=1 << 20, rounds=1 << 17)):
-        kw = dict(table_bytes=1 << 20, lanes=256, rounds=4, reps=1)
-        kw.update(bad)
-        with pytest.raises(ValueError):
-            capi.probe_gather(**kw)

@@ -3,7 +3,10 @@ walks, written into caller-owned device buffers with every per-call buffer
 taken from the library's fixed per-device scratch array, equal those of
 trw_sample_device for the same call -- on consecutive calls, the second
 smaller than the first, across start modes, processing orders, shuffles,
-cutoffs, replay draws and edge features.  Through the C ABI."""
+cutoffs, replay draws, edge features and the weight pickers -- and every
+call runs with the engine's allocation hook armed, so any device allocation
+inside it would fail the call.  Calls of two handles from two threads take
+the device's array in turn.  Through the C ABI."""
 import numpy as np
 import pytest
 
@@ -22,11 +25,13 @@ def _torch_device_first():
     torch.cuda.synchronize()
 
 
-def _engine(dim, seed=9):
+def _engine(dim, seed=9, weights=False):
     from temporal_random_walk import capi
     s, d, t = graphs.powerlaw(20_000, 300_000, n_ts=5_000, seed=5)
     f = np.random.default_rng(2).standard_normal((len(s), dim)).astype(np.float32) if dim else None
-    eng = capi.Engine(is_directed=True, global_seed=seed, shuffle_walk_order=True)
+    eng = capi.Engine(is_directed=True, global_seed=seed, shuffle_walk_order=True,
+                      enable_weight_computation=weights, enable_temporal_node2vec=weights,
+                      timescale_bound=20.0 if weights else -1.0, node2vec_p=0.5, node2vec_q=2.0)
     eng.add_edges(s, d, t, f)
     return eng
 
@@ -61,14 +66,26 @@ def _noalloc(eng, cap, L, dim, mode, bias, n, **kw):
                            device="cuda"),
     }
     torch.cuda.synchronize()
-    w = eng.sample_device_noalloc(mode, L, bias, n, capacity_walks=cap,
-                                  nodes_ptr=bufs["nodes"].data_ptr(),
-                                  timestamps_ptr=bufs["ts"].data_ptr(),
-                                  lens_ptr=bufs["lens"].data_ptr(),
-                                  edge_ids_ptr=bufs["eids"].data_ptr(),
-                                  features_ptr=bufs["feat"].data_ptr() if dim else None, **kw)
+    w = _call_noalloc(eng, cap, L, dim, mode, bias, n, bufs, **kw)
     assert w.max_walk_len == L and w.feature_dim == dim
     return w, bufs
+
+
+def _call_noalloc(eng, cap, L, dim, mode, bias, n, bufs, **kw):
+    """The call with the engine's allocation hook armed: the first device
+    allocation of any handle would fail it (MemoryError)."""
+    from temporal_random_walk import capi
+    capi.debug_fail_allocation(0)
+    try:
+        return eng.sample_device_noalloc(mode, L, bias, n, capacity_walks=cap,
+                                         nodes_ptr=bufs["nodes"].data_ptr(),
+                                         timestamps_ptr=bufs["ts"].data_ptr(),
+                                         lens_ptr=bufs["lens"].data_ptr(),
+                                         edge_ids_ptr=bufs["eids"].data_ptr(),
+                                         features_ptr=bufs["feat"].data_ptr() if dim else None,
+                                         **kw)
+    finally:
+        capi.debug_fail_allocation(-1)
 
 
 def _same(eng, cap, L, dim, mode, bias, n, **kw):
@@ -139,3 +156,71 @@ def test_noalloc_sample_rejects_what_does_not_fit():
     # rows written by the walk kernel need no walk scratch: the same sample fits
     _same(eng, 400_000, L, 0, "total", "Uniform", 400_000)
     eng.close()
+
+
+def test_noalloc_sample_weight_pickers():
+    """The weight families' kernels (guide tables, weighted panel) through the
+    entry point that allocates nothing: ExponentialWeight walks from weight-
+    picked starts, then a smaller node2vec sample, then backward walks."""
+    eng = _engine(0, weights=True)
+    cap = 70_000
+    L = 20
+    _same(eng, cap, L, 0, "total", "ExponentialWeight", 70_000,
+          initial_edge_bias="ExponentialWeight")
+    _same(eng, cap, L, 0, "total", "TemporalNode2Vec", 30_000, initial_edge_bias="Uniform")
+    _same(eng, cap, L, 0, "total", "ExponentialWeight", 20_000, initial_edge_bias="Uniform",
+          direction="Backward_In_Time")
+    eng.close()
+
+
+def test_noalloc_calls_of_two_handles_from_two_threads():
+    """Two handles on one device, each sampling from its own thread: the
+    device's scratch array is taken in turn, so both threads' walks equal
+    their handles' trw_sample_device walks on every round."""
+    import threading
+
+    import torch
+    L, n = 24, 70_000
+    engs = [_engine(0, seed=11), _engine(0, seed=12)]
+    kw = dict(initial_edge_bias="Uniform")
+    refs = [_rows(e.sample_device("total", L, "ExponentialIndex", n, **kw), L, 0) for e in engs]
+    bufs = []
+    for _ in engs:
+        bufs.append({
+            "nodes": torch.empty(n * L, dtype=torch.int32, device="cuda"),
+            "ts": torch.empty(n * L, dtype=torch.int64, device="cuda"),
+            "lens": torch.empty(n, dtype=torch.int64, device="cuda"),
+            "eids": torch.empty(n * (L - 1), dtype=torch.int64, device="cuda"),
+            "feat": torch.empty(1, dtype=torch.float32, device="cuda"),
+        })
+    torch.cuda.synchronize()
+    from temporal_random_walk import capi
+    for rnd in range(3):
+        errors, walks = [], [None, None]
+        start = threading.Barrier(2)
+
+        def run(k):
+            try:
+                start.wait()
+                walks[k] = engs[k].sample_device_noalloc(
+                    "total", L, "ExponentialIndex", n, capacity_walks=n,
+                    nodes_ptr=bufs[k]["nodes"].data_ptr(),
+                    timestamps_ptr=bufs[k]["ts"].data_ptr(),
+                    lens_ptr=bufs[k]["lens"].data_ptr(),
+                    edge_ids_ptr=bufs[k]["eids"].data_ptr(), **kw)
+            except Exception as ex:  # reported on the main thread
+                errors.append(ex)
+
+        threads = [threading.Thread(target=run, args=(k,)) for k in range(2)]
+        for t in threads:
+            t.start()
+        for t in threads:
+            t.join()
+        assert not errors, errors
+        for k in range(2):
+            got = _rows(walks[k], L, 0)
+            for name, x, y in zip(("nodes", "timestamps", "lens", "edge_ids"), refs[k], got):
+                assert torch.equal(x, y), (rnd, k, name)
+    capi.debug_fail_allocation(-1)
+    for e in engs:
+        e.close()
