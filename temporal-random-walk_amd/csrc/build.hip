@@ -710,17 +710,20 @@ __global__ void wg_fill_kernel(const double* __restrict__ w, const uint32_t* __r
     if (r.i == r.G - 1) r.t[r.to + 1] = r.G;
 }
 
-// The listed long runs, one workgroup at a time (longs[0] holds the count).
+// The listed long runs, one wave each (longs[0] holds the count): the wave's
+// lanes write consecutive buckets.
+constexpr unsigned kWgLongBlocks = 1024;
 __global__ __launch_bounds__(256) void wg_long_kernel(
     const double* __restrict__ w, const uint32_t* __restrict__ key, const uint32_t* __restrict__ grp,
     const uint32_t* __restrict__ cnt, const WNodeHdr* __restrict__ whdr,
     const WGuide* __restrict__ gg, size_t ng, int decaying, uint32_t* __restrict__ tab,
     const uint32_t* __restrict__ longs) {
     const uint32_t n = longs[0];
-    for (uint32_t k = blockIdx.x; k < n; k += gridDim.x) {
+    const uint32_t waves = gridDim.x * (blockDim.x / 64);
+    const uint32_t lane = threadIdx.x & 63;
+    for (uint32_t k = blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6); k < n; k += waves) {
         const WgRun r = wg_run(w, key, grp, cnt, whdr, gg, ng, decaying, tab, longs[1 + k]);
-        for (uint64_t b = static_cast<uint64_t>(r.from) + threadIdx.x; b <= r.to; b += blockDim.x)
-            r.t[b] = r.i;
+        for (uint64_t b = static_cast<uint64_t>(r.from) + lane; b <= r.to; b += 64) r.t[b] = r.i;
     }
 }
 
@@ -1342,7 +1345,7 @@ void node_weights(Engine& e, DirIndex& dir, size_t v, double bound, bool compute
 // already written: per node of a direction (key, grp, cnt, whdr) or, with
 // key == nullptr, the whole array under the guide gg.  Each bucket is written
 // once: by its group's thread, or for a run of more than kWgRun buckets (the
-// weights jumping by orders of magnitude) by a workgroup of wg_long_kernel.
+// weights jumping by orders of magnitude) by a wave of wg_long_kernel.
 void fill_weight_guides(Engine& e, const double* w, size_t ng, const uint32_t* key,
                         const uint32_t* grp, const uint32_t* cnt, const WNodeHdr* whdr,
                         const WGuide* gg, bool decaying, uint32_t* tab, size_t tsize) {
@@ -1352,8 +1355,8 @@ void fill_weight_guides(Engine& e, const double* w, size_t ng, const uint32_t* k
     check_hip(hipMemsetAsync(e.wg_long.p, 0, 4, s), "guide long-run count");
     hipLaunchKernelGGL(wg_fill_kernel, dim3(grid_for(ng)), dim3(kB), 0, s, w, key, grp, cnt, whdr,
                        gg, ng, decaying ? 1 : 0, tab, e.wg_long.p);
-    hipLaunchKernelGGL(wg_long_kernel, dim3(256), dim3(256), 0, s, w, key, grp, cnt, whdr, gg, ng,
-                       decaying ? 1 : 0, tab, e.wg_long.p);
+    hipLaunchKernelGGL(wg_long_kernel, dim3(kWgLongBlocks), dim3(256), 0, s, w, key, grp, cnt,
+                       whdr, gg, ng, decaying ? 1 : 0, tab, e.wg_long.p);
 }
 
 // The weight pickers' view of one direction's cumulative weights w (forward
@@ -1458,6 +1461,21 @@ void Engine::build(const int32_t* d_src, const int32_t* d_dst, const int64_t* d_
     check_hip(hipMemcpyAsync(hs, red64.p, 32, hipMemcpyDeviceToHost, s), "read minmax");
     sync();
     if (hs[2] < 0) throw InvalidArgument("node ids must be non-negative");
+    // A windowed store settles at about the edges one window of time holds:
+    // this batch's rate times the window.  Buffers that grow while it fills
+    // are sized for that at once (at most kMaxGrowthHint times what the
+    // store after this batch asks).
+    struct HintScope {
+        double prev = g_growth_hint;
+        ~HintScope() { g_growth_hint = prev; }
+    } hint_scope;
+    if (cfg.max_time_capacity > 0) {
+        const double span = static_cast<double>(hs[1] - hs[0]) + 1.0;
+        const double window = static_cast<double>(cfg.max_time_capacity) + 1.0;
+        const double settled = static_cast<double>(n) * std::max(1.0, window / span);
+        const double after = static_cast<double>(E + n);
+        g_growth_hint = std::min(kMaxGrowthHint, std::max(1.0, settled / after));
+    }
     try {
         batch_max_id = static_cast<int32_t>(hs[3]);
         build_accepted(d_src, d_dst, d_ts, d_feat, n, dim, hs[0], hs[1]);

@@ -59,9 +59,17 @@ inline thread_local RetiredBlocks* g_retired = nullptr;
 // Past this many retired bytes a growing buffer frees its old block at once.
 constexpr size_t kMaxRetiredBytes = size_t{32} << 30;
 
+// Growth hint of the current engine call (set by an ingest into a windowed
+// store, 1 otherwise): a buffer that grows takes at least this many times
+// the size asked for, so a store filling its window is sized for the whole
+// window at once instead of regrowing batch after batch.
+inline thread_local double g_growth_hint = 1.0;
+constexpr double kMaxGrowthHint = 4.0;
+
 // Grow-only device buffer; growth discards the contents.  A buffer that grows
-// again takes twice its capacity, so a store filling a streaming window
-// regrows its buffers once or twice rather than at every batch.
+// again takes twice its capacity (and at least g_growth_hint times what is
+// asked), so a store filling a streaming window regrows its buffers once at
+// most rather than at every batch.
 template <typename T>
 struct DBuf {
     T* p = nullptr;
@@ -89,7 +97,8 @@ struct DBuf {
             } else {
                 release();
             }
-            const size_t c = std::max(k + k / 4, 2 * old_cap) + 64;
+            const size_t hinted = static_cast<size_t>(static_cast<double>(k) * g_growth_hint);
+            const size_t c = std::max({k + k / 4, 2 * old_cap, hinted + hinted / 4}) + 64;
             if (alloc_hook_fires(g_alloc_fail_after)) throw std::bad_alloc();
             hipError_t e = alloc_hook_fires(g_alloc_fail_transient) ? hipErrorOutOfMemory
                                                                      : hipMalloc(&p, c * sizeof(T));

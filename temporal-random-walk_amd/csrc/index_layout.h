@@ -101,8 +101,8 @@ constexpr uint32_t kWgBucketsPerGroup = 2;
 // and a global segment's table holds 2 G + 1.
 static_assert(kWgBucketsPerGroup <= 2, "guide tables have room for 2 buckets per group");
 // Runs of more buckets than this between two consecutive groups are filled by
-// a workgroup each rather than by the group's thread.
-constexpr uint32_t kWgRun = 64;
+// a wave each rather than by the group's thread.
+constexpr uint32_t kWgRun = 16;
 
 __host__ __device__ inline uint64_t wg_double_bits(double x) {
 #ifdef __HIP_DEVICE_COMPILE__
