@@ -395,25 +395,16 @@ __device__ __forceinline__ bool adjacent(const WalkGraph& g, int prev, int cand)
 }
 
 // The edge of group x of a node's weighted panel f (x < G): a uniform pick re
-// within the group's range -- (int)(re * size) as edge_selectors.cuh:420-443
-// takes it, or, for node2vec (Clamp), min((size_t)(re * size), size - 1) as
-// temporal_node2vec_helpers.cuh:169-182 does.  The group's record holds its
-// first edge record, so a pick of entry 0 (every pick in a group of one edge)
-// loads no record.
-template <bool Clamp>
+// within the group's range, (int)(re * size) as edge_selectors.cuh:420-443
+// takes it.  The group's record holds its first edge record, so a pick of
+// entry 0 (every pick in a group of one edge) loads no record.
 __device__ __forceinline__ Hop weighted_group_hop(const WalkGraph& g, const WPanelRec* f,
                                                   uint32_t x, double re) {
     const u32x4_a8 v = *reinterpret_cast<const u32x4_a8*>(f + x);  // rank, start, end
     const uint32_t rank = v.x, es = v.y, ee = v.z;
     const EdgeRec r0 = f[x].rec0;
     if (es >= ee || es >= g.d.idx_size || ee > g.d.idx_size) return no_hop();
-    uint32_t k;
-    if (Clamp) {
-        const uint64_t local = static_cast<uint64_t>(re * static_cast<double>(ee - es));
-        k = static_cast<uint32_t>(local < ee - es ? local : ee - es - 1);
-    } else {
-        k = static_cast<uint32_t>(static_cast<int>(re * static_cast<int>(ee - es)));
-    }
+    const uint32_t k = static_cast<uint32_t>(static_cast<int>(re * static_cast<int>(ee - es)));
     return hop_of(k == 0 ? r0 : load_rec(g.d.rec + es + k), rank);
 }
 
@@ -438,6 +429,15 @@ __device__ Hop tn2v_pick(const WalkGraph& g, int prev, const WPanelRec* f, uint3
     const double acc_hi = acc_adj < acc_far ? acc_far : acc_adj;
     if (end_sum < start_sum) return no_hop();
     Hop last = no_hop();
+    // Retries often repeat the previous one's pick -- a saturated slice
+    // (start_sum == end_sum) picks its first group every time -- so the
+    // last group's record, edge record and adjacency answer are kept and
+    // reused while they still apply: the same values, no reload.
+    uint32_t gx = ~0u, g_rank = 0, g_es = 0, g_ee = 0;
+    EdgeRec g_r0{0, 0}, e_rec{0, 0};
+    uint32_t e_pick = ~0u;
+    int adj_cand = -1;
+    bool adj_val = false, adj_known = false;
     for (int retry = 0; retry < kNode2VecMaxRetries; ++retry) {
         const double gr = derive_uniform(rg, re, retry * 3 + 0);
         const double er = derive_uniform(rg, re, retry * 3 + 1);
@@ -446,15 +446,40 @@ __device__ Hop tn2v_pick(const WalkGraph& g, int prev, const WPanelRec* f, uint3
         // a pick one past the node's last group is an empty range in the
         // reference (get_node_group_edge_end, walk_step_helpers.cuh:19-38)
         if (x >= G) continue;
-        const Hop h = weighted_group_hop<true>(g, f, x, er);
-        if (h.e == -1) continue;
-        last = h;
-        const int cand = h.nbr;
+        if (x != gx) {
+            const u32x4_a8 v = *reinterpret_cast<const u32x4_a8*>(f + x);  // rank, start, end
+            g_rank = v.x;
+            g_es = v.y;
+            g_ee = v.z;
+            g_r0 = f[x].rec0;
+            gx = x;
+        }
+        if (g_es >= g_ee || g_es >= g.d.idx_size || g_ee > g.d.idx_size) continue;
+        // min((size_t)(er * size), size - 1): temporal_node2vec_helpers.cuh:169-182
+        const uint64_t local = static_cast<uint64_t>(er * static_cast<double>(g_ee - g_es));
+        const uint32_t pick =
+            g_es + static_cast<uint32_t>(local < g_ee - g_es ? local : g_ee - g_es - 1);
+        if (pick != e_pick) {
+            e_rec = pick == g_es ? g_r0 : load_rec(g.d.rec + pick);
+            e_pick = pick;
+        }
+        last = hop_of(e_rec, g_rank);
+        const int cand = e_rec.nbr;
         bool accept;
-        if (cand == prev) accept = ar < g.inv_p * inv_bmax;
-        else if (ar < acc_lo) accept = true;
-        else if (ar >= acc_hi) accept = false;
-        else accept = ar < (adjacent(g, prev, cand) ? acc_adj : acc_far);
+        if (cand == prev) {
+            accept = ar < g.inv_p * inv_bmax;
+        } else if (ar < acc_lo) {
+            accept = true;
+        } else if (ar >= acc_hi) {
+            accept = false;
+        } else {
+            if (!adj_known || cand != adj_cand) {
+                adj_val = adjacent(g, prev, cand);
+                adj_cand = cand;
+                adj_known = true;
+            }
+            accept = ar < (adj_val ? acc_adj : acc_far);
+        }
         if (accept) return last;
     }
     return last;
@@ -462,8 +487,6 @@ __device__ Hop tn2v_pick(const WalkGraph& g, int prev, const WPanelRec* f, uint3
 
 // The edge of the picked group gpos of a node whose groups end at ge
 // (edge_selectors.cuh:420-443): a uniform pick re within the group's range.
-// A weight pick one past the node's last group reads, in the reference, the
-// next node's first group start for both ends: an empty range.
 __device__ __forceinline__ Hop hop_from_group(const WalkGraph& g, uint32_t gpos, uint32_t ge,
                                               double re) {
     if (gpos >= ge) return no_hop();
@@ -564,7 +587,7 @@ __device__ __forceinline__ Hop wnode_edge_from(const WalkGraph& g, int picker, u
                                   static_cast<uint32_t>(ve), rg, start_sum, end_sum);
         if (x >= Gu) return no_hop();
     }
-    return weighted_group_hop<false>(g, f, x, re);
+    return weighted_group_hop(g, f, x, re);
 }
 
 // The node header a family's kernel loads per hop (issued before the hop's
