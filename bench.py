@@ -56,8 +56,7 @@ KERNEL_SOURCES = {
 
 
 # kernels of the walk path; every other kernel belongs to the index build
-WALK_PATH_KERNELS = ("walk_kernel", "walk_rows_kernel", "walk_weights_kernel",
-                     "walk_start_kernel", "layout_",
+WALK_PATH_KERNELS = ("walk_kernel", "walk_rows_kernel", "walk_start_kernel", "layout_",
                      "walk_stats",
                      "node_group_init", "node_group_segment", "gather_walk_features")
 
@@ -424,8 +423,7 @@ def run_other_config(k, args):
                    walk_kernel_ms=sum(kernels) / len(kernels))
         res["index_build_edges_per_s"] = E / (res["build_ms"] * 1e-3)
         res["value"] = st["total_len"] / (res["sample_ms"] * 1e-3)
-        kname = ("walk_rows_kernel" if st["rows_by_walk_kernel"]
-                 else ("walk_weights_kernel" if k == 4 else "walk_kernel"))
+        kname = "walk_rows_kernel" if st["rows_by_walk_kernel"] else "walk_kernel"
         res["roofline"] = other_roofline(
             k, st["compulsory_read_bytes"] + st["compulsory_write_bytes"], res["walk_kernel_ms"],
             kname)
