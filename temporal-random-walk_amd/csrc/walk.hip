@@ -485,6 +485,165 @@ __device__ Hop tn2v_pick(const WalkGraph& g, int prev, const WPanelRec* f, uint3
     return last;
 }
 
+// ---- node2vec retries decided by the whole wave ------------------------------
+// A lane's retries end at its first accepted proposal, 1.7 per hop on average
+// at cfg5, but a wave that runs them in step runs as many as its slowest lane
+// needs (about 7).  The row-writing kernel instead hands the retries of its
+// undecided hops to the whole wave: each round, the lanes whose hops are still
+// open are the owners; while more than 32 are, each tries its own next retry;
+// with m <= 32 of them, each owner's hop gets 64 / P lanes (P the power of two
+// at or above m) that evaluate its next 64 / P retries side by side, and the
+// owner takes the first accepted one (or, after the last retry, the last valid
+// one) -- the answer of tn2v_pick's loop, which tries the same proposals in
+// order.
+
+// What any lane needs to evaluate any retry of one hop (tn2v_pick's state).
+struct Tn2vHop {
+    const WPanelRec* f;  // the node's weighted panel
+    const uint32_t* gt;  // its guide table
+    WGuide gd;
+    uint32_t G, vb, ve;
+    int prev;
+    double start_sum, end_sum, rg, re;
+};
+
+// Retry `retry` of hop s (tn2v_pick's loop body): 0 for a proposal that is no
+// edge (the loop's `continue`), 1 for an edge it rejects, 2 for an edge it
+// accepts; out holds the edge's hop for 1 and 2.
+template <bool Fwd>
+__device__ __forceinline__ int tn2v_try(const WalkGraph& g, const Tn2vHop& s, int retry,
+                                        Hop& out) {
+    double bmax = 1.0;
+    if (g.inv_p > bmax) bmax = g.inv_p;
+    if (g.inv_q > bmax) bmax = g.inv_q;
+    const double inv_bmax = 1.0 / bmax;
+    const double acc_adj = 1.0 * inv_bmax, acc_far = g.inv_q * inv_bmax;
+    const double acc_lo = acc_adj < acc_far ? acc_adj : acc_far;
+    const double acc_hi = acc_adj < acc_far ? acc_far : acc_adj;
+    const double gr = derive_uniform(s.rg, s.re, retry * 3 + 0);
+    const double er = derive_uniform(s.rg, s.re, retry * 3 + 1);
+    const double ar = derive_uniform(s.rg, s.re, retry * 3 + 2);
+    const uint32_t x = node_weight_pick<Fwd>(s.f, s.G, s.gt, s.gd, s.vb, s.ve, gr, s.start_sum,
+                                             s.end_sum);
+    if (x >= s.G) return 0;
+    const u32x4_a8 v = *reinterpret_cast<const u32x4_a8*>(s.f + x);  // rank, start, end
+    const uint32_t es = v.y, ee = v.z;
+    if (es >= ee || es >= g.d.idx_size || ee > g.d.idx_size) return 0;
+    const uint64_t local = static_cast<uint64_t>(er * static_cast<double>(ee - es));
+    const uint32_t pick = es + static_cast<uint32_t>(local < ee - es ? local : ee - es - 1);
+    const EdgeRec rec = pick == es ? s.f[x].rec0 : load_rec(g.d.rec + pick);
+    out = hop_of(rec, v.x);
+    const int cand = rec.nbr;
+    bool accept;
+    if (cand == s.prev) accept = ar < g.inv_p * inv_bmax;
+    else if (ar < acc_lo) accept = true;
+    else if (ar >= acc_hi) accept = false;
+    else accept = ar < (adjacent(g, s.prev, cand) ? acc_adj : acc_far);
+    return accept ? 2 : 1;
+}
+
+template <class T>
+__device__ __forceinline__ T lane_read(T v, int src) {
+    return __shfl(v, src, 64);
+}
+template <class T>
+__device__ __forceinline__ const T* lane_read(const T* v, int src) {
+    return reinterpret_cast<const T*>(
+        __shfl(static_cast<unsigned long long>(reinterpret_cast<uintptr_t>(v)), src, 64));
+}
+__device__ __forceinline__ Tn2vHop lane_read(const Tn2vHop& s, int src) {
+    Tn2vHop o;
+    o.f = lane_read(s.f, src);
+    o.gt = lane_read(s.gt, src);
+    o.gd.bs = lane_read(static_cast<unsigned long long>(s.gd.bs), src);
+    o.gd.total = lane_read(s.gd.total, src);
+    o.G = lane_read(s.G, src);
+    o.vb = lane_read(s.vb, src);
+    o.ve = lane_read(s.ve, src);
+    o.prev = lane_read(s.prev, src);
+    o.start_sum = lane_read(s.start_sum, src);
+    o.end_sum = lane_read(s.end_sum, src);
+    o.rg = lane_read(s.rg, src);
+    o.re = lane_read(s.re, src);
+    return o;
+}
+__device__ __forceinline__ Hop lane_read(const Hop& h, int src) {
+    return Hop{lane_read(h.nbr, src), lane_read(h.r, src), lane_read(h.e, src)};
+}
+
+// The hops of the lanes with `want` (state s) decided by the whole wave (see
+// above); every lane of the (full) wave must call it.  Returns the lane's hop.
+template <bool Fwd>
+__device__ Hop tn2v_wave(const WalkGraph& g, bool want, const Tn2vHop& s) {
+    const int lane = __lane_id();
+    Hop res = no_hop(), last = no_hop();
+    int base = 0;  // the owner's next retry
+    bool open = want;
+    for (;;) {
+        const uint64_t owners = __ballot(open);
+        if (owners == 0) break;
+        const int m = __popcll(owners);
+        Hop hh = no_hop();
+        int st = 0;
+        if (m > 32) {
+            // as many open hops as lanes to spare: each owner tries its own
+            if (open) {
+                st = tn2v_try<Fwd>(g, s, base, hh);
+                if (st >= 1) last = hh;
+                if (st == 2) {
+                    res = hh;
+                    open = false;
+                } else if (++base >= kNode2VecMaxRetries) {
+                    res = last;
+                    open = false;
+                }
+            }
+            continue;
+        }
+        // owner i (its rank among the owners) gets the lanes l with
+        // l % P == i, P the power of two at or above m: lane l tries its
+        // retry base + l / P.  map: lane i holds owner i's lane (each lane
+        // pushes its own id, owners to their rank, the rest past m).
+        const int lg = 64 - __builtin_clzll(static_cast<unsigned long long>(m - 1) | 1ull) -
+                       (m == 1 ? 1 : 0);  // log2 P
+        const int h = 64 >> lg;              // lanes per open hop
+        const int rank = __popcll(owners & (lane ? ~0ull >> (64 - lane) : 0ull));
+        const int map = __builtin_amdgcn_ds_permute((open ? rank : m + lane - rank) << 2, lane);
+        const int i = lane & ((1 << lg) - 1), t = lane >> lg;
+        const int o = __builtin_amdgcn_ds_bpermute(i << 2, map);
+        const Tn2vHop hs = lane_read(s, o);
+        const int r = lane_read(base, o) + t;
+        if (i < m && r < kNode2VecMaxRetries) st = tn2v_try<Fwd>(g, hs, r, hh);
+        const uint64_t acc = __ballot(st == 2), val = __ballot(st >= 1);
+        // the owner of rank i reads its tries at lanes i, i + P, ...: the
+        // first accepted, else the last valid one
+        int src_acc = -1, src_val = -1;
+        if (open) {
+            for (int k = h - 1; k >= 0; --k) {
+                const int b = rank + (k << lg);
+                if ((acc >> b) & 1ull) src_acc = b;
+                if (src_val < 0 && ((val >> b) & 1ull)) src_val = b;
+            }
+        }
+        const Hop ha = lane_read(hh, src_acc < 0 ? lane : src_acc);
+        const Hop hv = lane_read(hh, src_val < 0 ? lane : src_val);
+        if (open) {
+            if (src_acc >= 0) {
+                res = ha;
+                open = false;
+            } else {
+                if (src_val >= 0) last = hv;
+                base += h;
+                if (base >= kNode2VecMaxRetries) {
+                    res = last;
+                    open = false;
+                }
+            }
+        }
+    }
+    return res;
+}
+
 // The edge of the picked group gpos of a node whose groups end at ge
 // (edge_selectors.cuh:420-443): a uniform pick re within the group's range.
 __device__ __forceinline__ Hop hop_from_group(const WalkGraph& g, uint32_t gpos, uint32_t ge,
@@ -588,6 +747,38 @@ __device__ __forceinline__ Hop wnode_edge_from(const WalkGraph& g, int picker, u
         if (x >= Gu) return no_hop();
     }
     return weighted_group_hop(g, f, x, re);
+}
+
+// wnode_edge_from in the any-picker row-writing kernel, whose node2vec
+// retries the wave decides (tn2v_wave): a node2vec hop from a previous node
+// with a non-empty slice returns with `want` set and its retry state in s
+// (the checks before tn2v_pick's loop done); any other hop is decided here.
+template <bool Fwd>
+__device__ __forceinline__ Hop wnode_edge_from_wave(const WalkGraph& g, int picker, uint32_t u,
+                                                    bool ok, const WNodeHdr& wh, int32_t t,
+                                                    int32_t cut, int prev, double rg, double re,
+                                                    const double* em1, bool& want, Tn2vHop& s) {
+    want = false;
+    if (picker != kTemporalNode2Vec || prev == -1)
+        return wnode_edge_from<Fwd, kFamAny>(g, picker, u, ok, wh, t, cut, prev, rg, re, em1);
+    const NodeHdr& h = wh.h;
+    uint32_t Gu = ok ? (h.meta & kHdrGMask) : 0u;
+    if (Gu == kHdrGMask) Gu = g.d.whdr[u + 1].h.gb - h.gb;
+    if (Gu == 0) return no_hop();
+    const uint32_t gb = h.gb;
+    const int G = static_cast<int>(Gu);
+    const WPanelRec* f = g.d.wpan + gb;
+    int vb, ve;
+    valid_slice<Fwd>(g.d.tab, h, u, G, f, t, cut, vb, ve);
+    if (vb >= ve) return no_hop();
+    if (gb + Gu > g.d.w_size) return no_hop();
+    const double start_sum = vb > 0 ? f[vb - 1].c : 0.0;
+    const double end_sum = ve == G ? wh.g.total : f[ve - 1].c;
+    if (end_sum < start_sum) return no_hop();
+    s = Tn2vHop{f, g.d.wgt + hdr_tab_base(h, u), wh.g, Gu, static_cast<uint32_t>(vb),
+                static_cast<uint32_t>(ve), prev, start_sum, end_sum, rg, re};
+    want = true;
+    return no_hop();
 }
 
 // The node header a family's kernel loads per hop (issued before the hop's
@@ -984,9 +1175,10 @@ __device__ __forceinline__ void rows_flush(const WalkArgs& a, uint64_t* buf, int
 // included; a lane whose walk has ended (or that has no walk) only fills.
 //
 // At least 4 waves per SIMD, as many as the slot buffers' LDS allows: the
-// index family needs 97 VGPRs, but the any-picker instance (node2vec's retry
-// loop) took 155 and ran at 3 waves; held to 128 (28 bytes of spills) its
-// cfg5 walks run in 12.7 instead of 15.4 ms per batch.
+// index family needs 109 VGPRs, but the any-picker instance (node2vec's
+// retries) took 155 and ran at 3 waves; held to 128 its cfg5 walks ran in
+// 12.7 instead of 15.4 ms per batch.  That instance hands node2vec's retries
+// to the whole wave (tn2v_wave; 128 VGPRs, 44 bytes of spills).
 template <bool Fwd, bool Dir, int Fam, int C>
 __global__ __launch_bounds__(kB) __attribute__((amdgpu_waves_per_eu(4))) void walk_rows_kernel(WalkGraph g, WalkArgs a) {
     static_assert(Fwd, "backward walks are reversed by the layout pass");
@@ -1017,6 +1209,61 @@ __global__ __launch_bounds__(kB) __attribute__((amdgpu_waves_per_eu(4))) void wa
     const int nb = a.pk_nb, rb = a.pk_rb;
     for (int c0 = 0; c0 < L; c0 += C) {
         const int n = min(C, L - c0);
+        if constexpr (Fam == kFamAny) {
+            // the same slots; node2vec's retries are decided by the whole
+            // wave after every lane has prepared its hop
+            for (int j = 0; j < n; ++j) {
+                const int k = c0 + j;
+                bool stepping = false, want = false;
+                Hop h = no_hop();
+                Tn2vHop ts{};
+                if (alive) {
+                    uint64_t word;
+                    if (k == 0) {
+                        word = first_word(nb, s0.first);
+                        len = 1;
+                        alive = L > 1 && cur != a.pad;
+                    } else {
+                        word = slot_word(nb, rb, cur, static_cast<uint32_t>(cur_r),
+                                         static_cast<uint32_t>(cur_e));
+                        len = k + 1;
+                        if (k == L - 1) {
+                            alive = false;
+                        } else {
+                            const bool ok = cur >= 0 && cur < g.active_size;
+                            const uint32_t u = ok ? static_cast<uint32_t>(cur) : 0u;
+                            const WNodeHdr hd = load_hop_hdr<Fam>(g, u);
+                            const uint32_t p = static_cast<uint32_t>(k) + 1;
+                            DrawPair r = philox_pair(a.ds, w, p);
+                            asm volatile("" : "+v"(r.a), "+v"(r.b));
+                            if (a.ds.replay) r = replay_pair(a.ds, w, p);
+                            h = wnode_edge_from_wave<Fwd>(g, a.walk_bias, u, ok, hd,
+                                                          cur_r == neg1 ? -1 : cur_r, cut, prev,
+                                                          r.a, r.b, em1, want, ts);
+                            stepping = true;
+                        }
+                    }
+                    buf[j * kRowStride + lane] = word;
+                }
+                if (__ballot(want)) {
+                    const Hop hw = tn2v_wave<Fwd>(g, want, ts);
+                    if (want) h = hw;
+                }
+                if (stepping) {
+                    if (h.e == -1 || h.r == neg1) {
+                        alive = false;
+                    } else {
+                        prev = cur;
+                        cur = h.nbr;
+                        cur_r = h.r;
+                        cur_e = h.e;
+                        alive = cur != a.pad;
+                    }
+                }
+            }
+            rows_flush<C>(a, buf, c0, n, static_cast<uint32_t>(w), len, live, lane);
+            continue;
+        }
         for (int j = 0; j < n; ++j) {
             if (!alive) continue;
             const int k = c0 + j;
