@@ -446,13 +446,16 @@ def test_replay_walks_index_pickers(directed, forward, picker):
                seed=3)
 
 
-@pytest.mark.parametrize("p,q", [(2.0, 0.5), (1.0, 1.0), (0.25, 4.0), (4.0, 1.0)])
+@pytest.mark.parametrize("p,q", [(2.0, 0.5), (1.0, 1.0), (0.25, 4.0), (4.0, 1.0), (0.5, 50.0)])
 def test_replay_walks_node2vec_return_in_out(p, q):
     """TemporalNode2Vec's acceptance (temporal_node2vec_helpers.cuh:127-199)
     with the in-out bias on either side of 1 and a return bias above and
     below the others: a draw below both non-return thresholds, at or above
     both, or between them (the only case that asks whether the candidate
-    neighbours the previous node) decides as the reference does."""
+    neighbours the previous node) decides as the reference does.  q = 50
+    accepts a far candidate with probability 0.01, so most hops run all 64
+    retries and take the last valid proposal (the row-writing kernel's
+    wave-decided retries, with few open hops and many lanes each)."""
     s, d, t = graphs.powerlaw(2_000, 40_000, s=1.4, seed=19, ts_hi=500_000)
     og, eng = _pair(True, [(s, d, t)], weights=True, tn2v=True, timescale_bound=20.0, p=p, q=q)
     for name in WEIGHT_ARRAYS:
