@@ -297,12 +297,22 @@ __global__ __launch_bounds__(kBlock) void radix_upsweep_kernel(const K* __restri
             key[r] = i < n ? keys[i] : K(0);
         }
         // counts only (no ranks): an LDS atomic per key, which a wave's
-        // same-digit lanes serialise only among themselves
+        // same-digit lanes serialise among themselves -- the row's lanes with
+        // its first lane's digit add their count in one atomic (a hub's
+        // node id fills half the rows of a power-law graph's node sort, and
+        // their serialised atomics slowed that pass's histogram by 60 %)
 #pragma unroll
         for (int r = 0; r < kRows; ++r) {
             const size_t i = wave_base + static_cast<size_t>(r) * 64 + lane;
             const uint32_t d = static_cast<uint32_t>(key[r] >> bit) & dmask;
-            if (i < n) atomicAdd(&s_cnt[wave * R + d], 1u);
+            const bool valid = i < n;
+            const uint64_t vm = __ballot(valid);
+            if (vm == 0) continue;
+            const int first = __ffsll(static_cast<long long>(vm)) - 1;
+            const uint32_t d0 = __shfl(d, first, 64);
+            const uint64_t m0 = __ballot(valid && d == d0);
+            if (lane == first) atomicAdd(&s_cnt[wave * R + d0], static_cast<uint32_t>(__popcll(m0)));
+            if (valid && d != d0) atomicAdd(&s_cnt[wave * R + d], 1u);
         }
     }
     __syncthreads();
