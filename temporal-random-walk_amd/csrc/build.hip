@@ -702,16 +702,27 @@ __global__ void wg_fill_kernel(const double* __restrict__ w, const uint32_t* __r
     if (g >= ng) return;
     const WgRun r = wg_run(w, key, grp, cnt, whdr, gg, ng, decaying, tab, g);
     if (r.t == nullptr) return;
-    if (r.to + 1 > r.from + kWgRun) {
-        longs[1 + atomicAdd(longs, 1u)] = static_cast<uint32_t>(g);
-    } else {
-        for (uint32_t b = r.from; b <= r.to; ++b) r.t[b] = r.i;
+    // the wave's long runs join the list with one atomic (a device-scope
+    // atomic per run on one counter serialises beyond the XCDs' L2s)
+    const bool is_long = r.to + 1 > r.from + kWgRun;
+    const uint64_t lm = __ballot(is_long);
+    if (lm != 0) {
+        const int lane = __lane_id(), leader = __ffsll(static_cast<long long>(lm)) - 1;
+        uint32_t base = 0;
+        if (lane == leader) base = atomicAdd(longs, static_cast<uint32_t>(__popcll(lm)));
+        base = __shfl(base, leader, 64);
+        const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+        if (is_long) longs[1 + base + __popcll(lm & below)] = static_cast<uint32_t>(g);
     }
+    if (!is_long)
+        for (uint32_t b = r.from; b <= r.to; ++b) r.t[b] = r.i;
     if (r.i == r.G - 1) r.t[r.to + 1] = r.G;
 }
 
-// The listed long runs, one wave each (longs[0] holds the count): the wave's
-// lanes write consecutive buckets.
+// The listed long runs (longs[0] holds the count): with fewer runs than
+// waves, each run is cut into equal parts, one wave each, so that a run of
+// millions of buckets does not hold one wave for the whole launch; the
+// wave's lanes write consecutive buckets.
 constexpr unsigned kWgLongBlocks = 1024;
 __global__ __launch_bounds__(256) void wg_long_kernel(
     const double* __restrict__ w, const uint32_t* __restrict__ key, const uint32_t* __restrict__ grp,
@@ -719,11 +730,18 @@ __global__ __launch_bounds__(256) void wg_long_kernel(
     const WGuide* __restrict__ gg, size_t ng, int decaying, uint32_t* __restrict__ tab,
     const uint32_t* __restrict__ longs) {
     const uint32_t n = longs[0];
+    if (n == 0) return;
     const uint32_t waves = gridDim.x * (blockDim.x / 64);
+    const uint32_t parts = n < waves ? waves / n : 1u;
+    const uint64_t items = static_cast<uint64_t>(n) * parts;
     const uint32_t lane = threadIdx.x & 63;
-    for (uint32_t k = blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6); k < n; k += waves) {
+    for (uint64_t it = blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6); it < items;
+         it += waves) {
+        const uint32_t k = static_cast<uint32_t>(it / parts), part = static_cast<uint32_t>(it % parts);
         const WgRun r = wg_run(w, key, grp, cnt, whdr, gg, ng, decaying, tab, longs[1 + k]);
-        for (uint64_t b = static_cast<uint64_t>(r.from) + lane; b <= r.to; b += 64) r.t[b] = r.i;
+        const uint64_t len = static_cast<uint64_t>(r.to) - r.from + 1;
+        const uint64_t lo = r.from + len * part / parts, hi = r.from + len * (part + 1) / parts;
+        for (uint64_t b = lo + lane; b < hi; b += 64) r.t[b] = r.i;
     }
 }
 
