@@ -838,17 +838,25 @@ __global__ void active_ids_kernel(const uint8_t* __restrict__ active,
     if (u < v && active[u]) ids[rank[u]] = static_cast<uint32_t>(u);
 }
 
-// Both pairs of every edge as keys of active-id ranks: rank(owner) << rb |
-// rank(neighbour), ordered as (owner, neighbour) because ranks keep the ids'
-// order.
+// The pair set holds every edge once, as its endpoints in increasing order
+// (the walks ask about both orders, and adjacency is symmetric): keys of
+// active-id ranks, rank(smaller) << rb | rank(larger) -- ranks keep the ids'
+// order -- or of the ids themselves.
 __global__ void adj_rank_keys_kernel(const int32_t* __restrict__ s, const int32_t* __restrict__ d,
                                      size_t e, const uint32_t* __restrict__ rank, int rb,
                                      uint32_t* __restrict__ keys) {
     const size_t i = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
     if (i >= e) return;
     const uint32_t ru = rank[s[i]], rv = rank[d[i]];
-    keys[2 * i] = (ru << rb) | rv;
-    keys[2 * i + 1] = (rv << rb) | ru;
+    keys[i] = (min(ru, rv) << rb) | max(ru, rv);
+}
+
+__global__ void adj_pair_keys_kernel(const int32_t* __restrict__ s, const int32_t* __restrict__ d,
+                                     size_t e, int b, uint64_t* __restrict__ keys) {
+    const size_t i = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (i >= e) return;
+    const uint64_t u = static_cast<uint32_t>(s[i]), v = static_cast<uint32_t>(d[i]);
+    keys[i] = (min(u, v) << b) | max(u, v);
 }
 
 __global__ void distinct_flags_kernel(const uint32_t* __restrict__ keys, size_t n,
@@ -1906,14 +1914,15 @@ void Engine::build_accepted(const int32_t* d_src, const int32_t* d_dst, const in
 
     // ---- 7. node2vec adjacency (edge_data.cu:298-392).  The walks' test "is
     // a candidate adjacent to the previous node?" probes a hash set of the
-    // (owner, neighbour) pairs -- about one line -- instead of binary-searching
-    // a hub's list of millions of neighbours.  The sorted neighbour lists
-    // themselves are only read through trw_get_array, which builds them on
-    // first request after an ingest (build_adjacency_lists).
+    // node pairs joined by an edge, each once in increasing order -- about
+    // one line -- instead of binary-searching a hub's list of millions of
+    // neighbours.  The sorted neighbour lists themselves are only read
+    // through trw_get_array, which builds them on first request after an
+    // ingest (build_adjacency_lists).
     adj_ready = adj_lists_ready = false;
     if (cfg.enable_temporal_node2vec) {
         const int b = key_bits;
-        const size_t m2 = 2 * E;
+        const size_t m2 = E;  // one pair key per edge
         // the pairs sorted with duplicates adjacent: as 32-bit keys of the
         // active ids' ranks when two ranks fit (a streaming window of a
         // power-law graph touches few of its ids: cfg5's 15k of 1M ids make
@@ -1952,7 +1961,7 @@ void Engine::build_accepted(const int32_t* d_src, const int32_t* d_dst, const in
             k64a.ensure(m2);
             k64b.ensure(m2);
             if (E)
-                hipLaunchKernelGGL(adj_keys_kernel, dim3(grid_for(E)), dim3(kB), 0, s, src.p,
+                hipLaunchKernelGGL(adj_pair_keys_kernel, dim3(grid_for(E)), dim3(kB), 0, s, src.p,
                                    dst.p, E, b, k64a.p);
             const int w = radix_sort_u64(k64a.p, nullptr, k64b.p, nullptr, m2, 0, 2 * b, hist.p, s);
             fkeys = w ? k64b.p : k64a.p;

@@ -45,8 +45,9 @@
 //     wgt           uint32[2(g+V_c)] guide tables of nodes with > kWGuideMin
 //                                  groups, node u's at 2 (gb + u) (below)
 //   global weights  fwd_cum, bwd_cum fp64[T] (+ their guides: one segment)
-//   node2vec        adj_hash uint64[2^k >= 4E] (pair membership set, built
-//                   with the index); adj_off uint32[max_id+2], adj_nbr
+//   node2vec        adj_hash uint64[2^k >= 2 x distinct edge pairs] (the
+//                   endpoints of every edge, smaller first: a membership set,
+//                   built with the index); adj_off uint32[max_id+2], adj_nbr
 //                   int32[2E] (sorted lists, built when first requested)
 #pragma once
 

@@ -372,9 +372,12 @@ __device__ __forceinline__ bool adjacent(const WalkGraph& g, int prev, int cand)
     if (!g.tn2v || g.adj_nodes == 0) return false;
     if (prev < 0 || static_cast<uint32_t>(prev) >= g.adj_nodes) return false;
     if (g.adj_hash) {
-        // cand is a stored node id (a record's neighbour), below 2^adj_bits
+        // cand is a stored node id (a record's neighbour), below 2^adj_bits;
+        // the set holds each edge's endpoints in increasing order
         if (cand < 0) return false;
-        const uint64_t key = (static_cast<uint64_t>(prev) << g.adj_bits) | static_cast<uint32_t>(cand);
+        const uint64_t lo = static_cast<uint32_t>(min(prev, cand)),
+                       hi = static_cast<uint32_t>(max(prev, cand));
+        const uint64_t key = (lo << g.adj_bits) | hi;
         for (uint64_t h = (key * kAdjHashMul) >> g.adj_shift;; h = (h + 1) & g.adj_mask) {
             const uint64_t v = g.adj_hash[h];
             if (v == key) return true;
