@@ -1178,6 +1178,7 @@ void build_direction(Engine& e, DirIndex& dir, size_t n, int key_bits, size_t vc
     e.k32b.ensure(n);
     e.k64a.ensure(n);
     if (packed) e.k64b.ensure(n);
+    e.hist.ensure(radix_hist_elems(n));
     const int passes = n > 1 ? radix_passes(0, key_bits) : 0;
     // unpacked, the sorted records land in dir.rec: start in the buffer set
     // the last digit pass does not write into

@@ -226,13 +226,6 @@ __device__ __forceinline__ PanelPair load_pair(const PanelRec* p) {
     return PanelPair{v.x, v.y, v.z, v.w};
 }
 
-// The slot-major walk scratch is written once and read once by the layout
-// pass: non-temporal stores keep it from evicting the node panels from L2.
-template <typename T>
-__device__ __forceinline__ void store_out(T* p, T v) {
-    __builtin_nontemporal_store(v, p);
-}
-
 typedef uint32_t u32x2_a4 __attribute__((ext_vector_type(2), aligned(4)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef int64_t i64x2 __attribute__((ext_vector_type(2)));
