@@ -969,6 +969,13 @@ __global__ void heavy_node_flags_kernel(const uint32_t* __restrict__ cnt, size_t
 // i-th heavy node (in id order) owns tiles [tile_base[i], tile_base[i + 1]).
 constexpr int kHeavyItems = 16;
 constexpr uint32_t kHeavyTile = 256 * kHeavyItems;
+// Workgroups of the tile kernels, each taking tiles in turn.
+constexpr size_t kHeavyGrid = 2048;
+
+__global__ void fill_u32_kernel(uint32_t* __restrict__ p, size_t n, uint32_t v) {
+    const size_t i = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (i < n) p[i] = v;
+}
 
 __global__ void compact_heavy_kernel(const uint32_t* __restrict__ flags,
                                      const uint32_t* __restrict__ scan,
@@ -1023,63 +1030,68 @@ __device__ __forceinline__ int heavy_tile_node(const uint32_t* tile_base, uint32
 // tile's values are non-decreasing -- written in place; the tile's last
 // value goes to tsum.  Both directions (f is skipped when wf is null).
 __global__ __launch_bounds__(256) void heavy_tile_scan_kernel(
-    const uint32_t* __restrict__ heavy, const uint32_t* __restrict__ tile_base, uint32_t nh,
-    const uint32_t* __restrict__ cnt, const uint32_t* __restrict__ grp,
-    const int64_t* __restrict__ first_ts, double bound, double* __restrict__ wf,
-    double* __restrict__ wb, double* __restrict__ tsum_f, double* __restrict__ tsum_b) {
+    const uint32_t* __restrict__ heavy, const uint32_t* __restrict__ tile_base,
+    const uint32_t* __restrict__ nh_dev, const uint32_t* __restrict__ cnt,
+    const uint32_t* __restrict__ grp, const int64_t* __restrict__ first_ts, double bound,
+    double* __restrict__ wf, double* __restrict__ wb, double* __restrict__ tsum_f,
+    double* __restrict__ tsum_b) {
     __shared__ double s4[4];
-    const int i = heavy_tile_node(tile_base, nh, blockIdx.x);
-    if (i < 0) return;  // uniform over the workgroup
-    const uint32_t u = heavy[i];
-    const uint32_t s = cnt[u], e = cnt[u + 1];
-    const NodeWeightParams q = node_weight_params(first_ts, s, e, bound);
-    const uint32_t t0 = s + (blockIdx.x - tile_base[i]) * kHeavyTile;
-    const uint32_t p0 = t0 + threadIdx.x * kHeavyItems;
-    double vf[kHeavyItems], vb[kHeavyItems];
-    double rf = 0.0, rb = 0.0;
-#pragma unroll
-    for (int j = 0; j < kHeavyItems; ++j) {
-        const uint32_t p = p0 + j;
-        double f = 0.0, b = 0.0;
-        if (p < e) raw_node_weights(q, grp, first_ts, p, bound, &f, &b);
-        rf += f;
-        rb += b;
-        vf[j] = rf;
-        vb[j] = rb;
-    }
-    for (int dir = 0; dir < (wf ? 2 : 1); ++dir) {
-        double* v = dir == 0 ? vb : vf;
-        double* w = dir == 0 ? wb : wf;
-        double tot;
-        const double before = block_excl_scan_f64<false>(dir == 0 ? rb : rf, s4, &tot);
-        double mx = 0.0;
-#pragma unroll
-        for (int j = 0; j < kHeavyItems; ++j) {
-            v[j] = before + v[j];
-            mx = fmax(mx, v[j]);
-        }
-        double mtot;
-        double m = block_excl_scan_f64<true>(mx, s4, &mtot);
-        m = fmax(m, 0.0);
+    const uint32_t nh = *nh_dev;
+    for (uint32_t t = blockIdx.x;; t += gridDim.x) {
+        const int i = heavy_tile_node(tile_base, nh, t);
+        if (i < 0) return;  // uniform over the workgroup
+        const uint32_t u = heavy[i];
+        const uint32_t s = cnt[u], e = cnt[u + 1];
+        const NodeWeightParams q = node_weight_params(first_ts, s, e, bound);
+        const uint32_t t0 = s + (t - tile_base[i]) * kHeavyTile;
+        const uint32_t p0 = t0 + threadIdx.x * kHeavyItems;
+        double vf[kHeavyItems], vb[kHeavyItems];
+        double rf = 0.0, rb = 0.0;
 #pragma unroll
         for (int j = 0; j < kHeavyItems; ++j) {
             const uint32_t p = p0 + j;
-            m = fmax(m, v[j]);
-            if (p < e) w[p] = m;
+            double f = 0.0, b = 0.0;
+            if (p < e) raw_node_weights(q, grp, first_ts, p, bound, &f, &b);
+            rf += f;
+            rb += b;
+            vf[j] = rf;
+            vb[j] = rb;
         }
-        if (threadIdx.x == 0) (dir == 0 ? tsum_b : tsum_f)[blockIdx.x] = mtot;
+        for (int dir = 0; dir < (wf ? 2 : 1); ++dir) {
+            double* v = dir == 0 ? vb : vf;
+            double* w = dir == 0 ? wb : wf;
+            double tot;
+            const double before = block_excl_scan_f64<false>(dir == 0 ? rb : rf, s4, &tot);
+            double mx = 0.0;
+#pragma unroll
+            for (int j = 0; j < kHeavyItems; ++j) {
+                v[j] = before + v[j];
+                mx = fmax(mx, v[j]);
+            }
+            double mtot;
+            double m = block_excl_scan_f64<true>(mx, s4, &mtot);
+            m = fmax(m, 0.0);
+#pragma unroll
+            for (int j = 0; j < kHeavyItems; ++j) {
+                const uint32_t p = p0 + j;
+                m = fmax(m, v[j]);
+                if (p < e) w[p] = m;
+            }
+            if (threadIdx.x == 0) (dir == 0 ? tsum_b : tsum_f)[t] = mtot;
+        }
     }
 }
 
 // Pass 2, one thread per heavy node: its tiles' exclusive prefixes, each the
 // previous prefix plus the previous tile's last value, so consecutive tiles
 // stay non-decreasing across their boundary; the node's total follows.
-__global__ void heavy_tile_prefix_kernel(const uint32_t* __restrict__ tile_base, uint32_t nh,
+__global__ void heavy_tile_prefix_kernel(const uint32_t* __restrict__ tile_base,
+                                         const uint32_t* __restrict__ nh_dev,
                                          double* __restrict__ tsum_f, double* __restrict__ tsum_b,
                                          double* __restrict__ total_f,
                                          double* __restrict__ total_b, int compute_forward) {
     const uint32_t i = blockIdx.x * kB + threadIdx.x;
-    if (i >= nh) return;
+    if (i >= *nh_dev) return;
     for (int dir = 0; dir < (compute_forward ? 2 : 1); ++dir) {
         double* ts = dir == 0 ? tsum_b : tsum_f;
         double run = 0.0;
@@ -1111,21 +1123,25 @@ __global__ void heavy_tile_prefix_kernel(const uint32_t* __restrict__ tile_base,
 // node total, the normalisation of node_edge_index.cu:617-639 applied to the
 // prefix sums (non-decreasing, the node's last value exactly 1).
 __global__ __launch_bounds__(256) void heavy_tile_finish_kernel(
-    const uint32_t* __restrict__ heavy, const uint32_t* __restrict__ tile_base, uint32_t nh,
-    const uint32_t* __restrict__ cnt, const double* __restrict__ tsum_f,
-    const double* __restrict__ tsum_b, const double* __restrict__ total_f,
-    const double* __restrict__ total_b, double* __restrict__ wf, double* __restrict__ wb) {
-    const int i = heavy_tile_node(tile_base, nh, blockIdx.x);
-    if (i < 0) return;
-    const uint32_t u = heavy[i];
-    const uint32_t s = cnt[u], e = cnt[u + 1];
-    const uint32_t t0 = s + (blockIdx.x - tile_base[i]) * kHeavyTile;
-    for (int dir = 0; dir < (wf ? 2 : 1); ++dir) {
-        double* w = dir == 0 ? wb : wf;
-        const double pre = (dir == 0 ? tsum_b : tsum_f)[blockIdx.x];
-        const double tot = (dir == 0 ? total_b : total_f)[i];
-        for (uint32_t p = t0 + threadIdx.x; p < e && p < t0 + kHeavyTile; p += 256)
-            w[p] = (pre + w[p]) / tot;
+    const uint32_t* __restrict__ heavy, const uint32_t* __restrict__ tile_base,
+    const uint32_t* __restrict__ nh_dev, const uint32_t* __restrict__ cnt,
+    const double* __restrict__ tsum_f, const double* __restrict__ tsum_b,
+    const double* __restrict__ total_f, const double* __restrict__ total_b,
+    double* __restrict__ wf, double* __restrict__ wb) {
+    const uint32_t nh = *nh_dev;
+    for (uint32_t t = blockIdx.x;; t += gridDim.x) {
+        const int i = heavy_tile_node(tile_base, nh, t);
+        if (i < 0) return;
+        const uint32_t u = heavy[i];
+        const uint32_t s = cnt[u], e = cnt[u + 1];
+        const uint32_t t0 = s + (t - tile_base[i]) * kHeavyTile;
+        for (int dir = 0; dir < (wf ? 2 : 1); ++dir) {
+            double* w = dir == 0 ? wb : wf;
+            const double pre = (dir == 0 ? tsum_b : tsum_f)[t];
+            const double tot = (dir == 0 ? total_b : total_f)[i];
+            for (uint32_t p = t0 + threadIdx.x; p < e && p < t0 + kHeavyTile; p += 256)
+                w[p] = (pre + w[p]) / tot;
+        }
     }
 }
 
@@ -1336,33 +1352,39 @@ void node_weights(Engine& e, DirIndex& dir, size_t v, double bound, bool compute
     hipLaunchKernelGGL(heavy_node_flags_kernel, dim3(grid_for(v)), dim3(kB), 0, s, dir.cnt.p, v,
                        e.flags.p);
     exclusive_scan_u32(e.flags.p, e.scan.p, v, e.scan_scratch.p, s);
-    check_hip(hipMemcpyAsync(host_scratch, e.scan.p + v, 4, hipMemcpyDeviceToHost, s), "heavy n");
-    e.sync();
-    uint32_t nh;
-    std::memcpy(&nh, host_scratch, 4);
-    if (nh) {
-        // heavy ids in k32b, their tile counts then tile bases in v32b
-        e.k32b.ensure(nh);
-        e.v32b.ensure(nh + 1);
-        e.v32a.ensure(nh + 1);
+    // the heavy count stays on the device (scan[v]): the buffers are sized
+    // for the most heavy nodes the groups allow, and the kernels read it
+    (void)host_scratch;
+    const size_t nh_max = std::min<size_t>(v, dir.n_groups / (kHeavyGroups + 1));
+    if (nh_max) {
+        const uint32_t* nh_dev = e.scan.p + v;
+        // heavy ids in k32b, their tile counts (zero past the last) then tile
+        // bases in v32b
+        e.k32b.ensure(nh_max);
+        e.v32b.ensure(nh_max + 1);
+        e.v32a.ensure(nh_max + 1);
+        hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(nh_max + 1)), dim3(kB), 0, s, e.v32a.p,
+                           nh_max + 1, 0u);
         hipLaunchKernelGGL(compact_heavy_kernel, dim3(grid_for(v)), dim3(kB), 0, s, e.flags.p,
                            e.scan.p, dir.cnt.p, v, e.k32b.p, e.v32a.p);
-        e.scan_scratch.ensure(scan_scratch_elems(nh + 1));
-        exclusive_scan_u32(e.v32a.p, e.v32b.p, nh, e.scan_scratch.p, s);
-        // at most g / kHeavyTile + nh tiles: launch that many, the rest exit
-        const size_t tiles = dir.n_groups / kHeavyTile + nh + 1;
-        e.dscratch.ensure(4 * tiles + 2 * nh);
+        e.scan_scratch.ensure(scan_scratch_elems(nh_max + 1));
+        exclusive_scan_u32(e.v32a.p, e.v32b.p, nh_max, e.scan_scratch.p, s);
+        // at most g / kHeavyTile + nh tiles, taken in turn by a fixed grid
+        const size_t tiles = dir.n_groups / kHeavyTile + nh_max + 1;
+        e.dscratch.ensure(4 * tiles + 2 * nh_max);
         double* tsum_f = e.dscratch.p;
         double* tsum_b = tsum_f + tiles;
         double* total_f = tsum_b + tiles;
-        double* total_b = total_f + nh;
-        hipLaunchKernelGGL(heavy_tile_scan_kernel, dim3(tiles), dim3(256), 0, s, e.k32b.p,
-                           e.v32b.p, nh, dir.cnt.p, dir.grp.p, dir.first_ts.p, bound, wf,
+        double* total_b = total_f + nh_max;
+        const unsigned grid = static_cast<unsigned>(std::min<size_t>(tiles, kHeavyGrid));
+        hipLaunchKernelGGL(heavy_tile_scan_kernel, dim3(grid), dim3(256), 0, s, e.k32b.p,
+                           e.v32b.p, nh_dev, dir.cnt.p, dir.grp.p, dir.first_ts.p, bound, wf,
                            dir.w_bwd.p, tsum_f, tsum_b);
-        hipLaunchKernelGGL(heavy_tile_prefix_kernel, dim3(grid_for(nh)), dim3(kB), 0, s, e.v32b.p,
-                           nh, tsum_f, tsum_b, total_f, total_b, compute_forward ? 1 : 0);
-        hipLaunchKernelGGL(heavy_tile_finish_kernel, dim3(tiles), dim3(256), 0, s, e.k32b.p,
-                           e.v32b.p, nh, dir.cnt.p, tsum_f, tsum_b, total_f, total_b, wf,
+        hipLaunchKernelGGL(heavy_tile_prefix_kernel, dim3(grid_for(nh_max)), dim3(kB), 0, s,
+                           e.v32b.p, nh_dev, tsum_f, tsum_b, total_f, total_b,
+                           compute_forward ? 1 : 0);
+        hipLaunchKernelGGL(heavy_tile_finish_kernel, dim3(grid), dim3(256), 0, s, e.k32b.p,
+                           e.v32b.p, nh_dev, dir.cnt.p, tsum_f, tsum_b, total_f, total_b, wf,
                            dir.w_bwd.p);
     }
     check_hip(hipGetLastError(), "node weights launch");
