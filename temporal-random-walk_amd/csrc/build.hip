@@ -1395,17 +1395,17 @@ void node_weights(Engine& e, DirIndex& dir, size_t v, double bound, bool compute
 // key == nullptr, the whole array under the guide gg.  Each bucket is written
 // once: by its group's thread, or for a run of more than kWgRun buckets (the
 // weights jumping by orders of magnitude) by a wave of wg_long_kernel.
-void fill_weight_guides(Engine& e, const double* w, size_t ng, const uint32_t* key,
-                        const uint32_t* grp, const uint32_t* cnt, const WNodeHdr* whdr,
-                        const WGuide* gg, bool decaying, uint32_t* tab, size_t tsize) {
+void fill_weight_guides(hipStream_t s, DBuf<uint32_t>& longs, const double* w, size_t ng,
+                        const uint32_t* key, const uint32_t* grp, const uint32_t* cnt,
+                        const WNodeHdr* whdr, const WGuide* gg, bool decaying, uint32_t* tab,
+                        size_t tsize) {
     if (ng == 0) return;
-    hipStream_t s = e.stream;
-    e.wg_long.ensure(tsize / kWgRun + 2);
-    check_hip(hipMemsetAsync(e.wg_long.p, 0, 4, s), "guide long-run count");
+    longs.ensure(tsize / kWgRun + 2);
+    check_hip(hipMemsetAsync(longs.p, 0, 4, s), "guide long-run count");
     hipLaunchKernelGGL(wg_fill_kernel, dim3(grid_for(ng)), dim3(kB), 0, s, w, key, grp, cnt, whdr,
-                       gg, ng, decaying ? 1 : 0, tab, e.wg_long.p);
+                       gg, ng, decaying ? 1 : 0, tab, longs.p);
     hipLaunchKernelGGL(wg_long_kernel, dim3(kWgLongBlocks), dim3(256), 0, s, w, key, grp, cnt,
-                       whdr, gg, ng, decaying ? 1 : 0, tab, e.wg_long.p);
+                       whdr, gg, ng, decaying ? 1 : 0, tab, longs.p);
 }
 
 // The weight pickers' view of one direction's cumulative weights w (forward
@@ -1422,20 +1422,20 @@ void build_walk_weights(Engine& e, DirIndex& dir, size_t v, const DBuf<double>& 
     if (g)
         hipLaunchKernelGGL(wpan_kernel, dim3(grid_for(g)), dim3(kB), 0, s, dir.pan.p, w.p,
                            dir.rec.p, g, ww.pan.p);
-    fill_weight_guides(e, w.p, g, dir.key.p, dir.grp.p, dir.cnt.p, ww.hdr.p, nullptr, decaying,
-                       ww.tab.p, ww.tab.n);
+    fill_weight_guides(e.stream, e.wg_long, w.p, g, dir.key.p, dir.grp.p, dir.cnt.p, ww.hdr.p,
+                       nullptr, decaying, ww.tab.p, ww.tab.n);
     check_hip(hipGetLastError(), "walk weights launch");
 }
 
 // The guide of a global cumulative array (one segment of n).
-void build_global_guide(Engine& e, const DBuf<double>& w, size_t n, bool decaying,
+void build_global_guide(Engine& e, hipStream_t s, const DBuf<double>& w, size_t n, bool decaying,
                         DBuf<WGuide>& gd, DBuf<uint32_t>& tab) {
     gd.resize(1);
     tab.resize(2 * n + 1);
-    hipLaunchKernelGGL(global_guide_kernel, dim3(1), dim3(1), 0, e.stream, w.p, n,
-                       decaying ? 1 : 0, gd.p);
-    fill_weight_guides(e, w.p, n, nullptr, nullptr, nullptr, nullptr, gd.p, decaying, tab.p,
-                       tab.n);
+    hipLaunchKernelGGL(global_guide_kernel, dim3(1), dim3(1), 0, s, w.p, n, decaying ? 1 : 0,
+                       gd.p);
+    fill_weight_guides(s, e.wg_long_g, w.p, n, nullptr, nullptr, nullptr, nullptr, gd.p, decaying,
+                       tab.p, tab.n);
     check_hip(hipGetLastError(), "global guide launch");
 }
 
@@ -1914,6 +1914,40 @@ void Engine::build_accepted(const int32_t* d_src, const int32_t* d_dst, const in
                        flags.p, scan.p, tsg_off.p, uniq_ts.p, erank.p);
     update_neg1_rank(*this);
 
+    // ---- 5b. global cumulative weights (edge_data.cu:440-514) on the side
+    // stream, beside the node index: they read only the timestamp groups.
+    // Pivots are the store's min/max ts.  Their buffers are the side's own.
+    weights_ready = false;
+    const bool weights = cfg.enable_weight_computation || cfg.enable_temporal_node2vec;
+    if (weights) {
+        hipStream_t sd = side;
+        check_hip(hipEventRecord(ts_ready, s), "event");
+        check_hip(hipStreamWaitEvent(sd, ts_ready, 0), "wait timestamp groups");
+        const double bound = cfg.timescale_bound;
+        const double diff = static_cast<double>(store_tmax - store_tmin);
+        const double scale = (bound > 0 && diff > 0) ? bound / diff : 1.0;
+        fwd_cum.resize(T);
+        bwd_cum.resize(T);
+        hipLaunchKernelGGL(global_weights_kernel, dim3(grid_for(T)), dim3(kB), 0, sd, tsg_off.p,
+                           uniq_ts.p, T, store_tmin, store_tmax, bound, scale, fwd_cum.p,
+                           bwd_cum.p);
+        gsum.ensure(2 * (2 + 1024));
+        sum_f64(fwd_cum.p, T, gsum.p, sd);
+        sum_f64(bwd_cum.p, T, gsum.p + 2 + 1024, sd);
+        hipLaunchKernelGGL(divide_kernel, dim3(grid_for(T)), dim3(kB), 0, sd, fwd_cum.p,
+                           bwd_cum.p, T, gsum.p, gsum.p + 2 + 1024);
+        fscan_scratch.ensure(scan_scratch_elems(T));
+        inclusive_scan_f64(fwd_cum.p, T, fscan_scratch.p, sd);
+        inclusive_scan_f64(bwd_cum.p, T, fscan_scratch.p, sd);
+        // the weight search counts entries below its target, which is the
+        // lower_bound only on a non-decreasing array
+        running_max_f64(fwd_cum.p, T, fscan_scratch.p, sd);
+        running_max_f64(bwd_cum.p, T, fscan_scratch.p, sd);
+        build_global_guide(*this, sd, fwd_cum, T, true, gwg_fwd, gwt_fwd);
+        build_global_guide(*this, sd, bwd_cum, T, false, gwg_bwd, gwt_bwd);
+        check_hip(hipEventRecord(side_done, sd), "event");
+    }
+
     // ---- 6. node index
     const size_t v = static_cast<size_t>(max_node_id) + 1;  // active_node_ids size
     const size_t vc = v + 1;                                // node_index_capacity
@@ -2022,35 +2056,11 @@ void Engine::build_accepted(const int32_t* d_src, const int32_t* d_dst, const in
         adj_ready = true;
     }
 
-    // ---- 8. weights
-    weights_ready = false;
-    const bool weights = cfg.enable_weight_computation || cfg.enable_temporal_node2vec;
+    // ---- 8. per-node weights (node_edge_index.cu:644-684): outbound
+    // forward + backward, inbound backward (directed); the global ones run
+    // on the side stream (5b)
     if (weights) {
         const double bound = cfg.timescale_bound;
-        // global (edge_data.cu:440-514): pivots are the store's min/max ts
-        const double diff = static_cast<double>(store_tmax - store_tmin);
-        const double scale = (bound > 0 && diff > 0) ? bound / diff : 1.0;
-        fwd_cum.resize(T);
-        bwd_cum.resize(T);
-        hipLaunchKernelGGL(global_weights_kernel, dim3(grid_for(T)), dim3(kB), 0, s, tsg_off.p,
-                           uniq_ts.p, T, store_tmin, store_tmax, bound, scale, fwd_cum.p,
-                           bwd_cum.p);
-        dscratch.ensure(2 * (2 + 1024));
-        sum_f64(fwd_cum.p, T, dscratch.p, s);
-        sum_f64(bwd_cum.p, T, dscratch.p + 2 + 1024, s);
-        hipLaunchKernelGGL(divide_kernel, dim3(grid_for(T)), dim3(kB), 0, s, fwd_cum.p, bwd_cum.p,
-                           T, dscratch.p, dscratch.p + 2 + 1024);
-        fscan_scratch.ensure(scan_scratch_elems(std::max<size_t>(T, out.n_groups)));
-        inclusive_scan_f64(fwd_cum.p, T, fscan_scratch.p, s);
-        inclusive_scan_f64(bwd_cum.p, T, fscan_scratch.p, s);
-        // the weight search counts entries below its target, which is the
-        // lower_bound only on a non-decreasing array
-        running_max_f64(fwd_cum.p, T, fscan_scratch.p, s);
-        running_max_f64(bwd_cum.p, T, fscan_scratch.p, s);
-        build_global_guide(*this, fwd_cum, T, true, gwg_fwd, gwt_fwd);
-        build_global_guide(*this, bwd_cum, T, false, gwg_bwd, gwt_bwd);
-        // per node (node_edge_index.cu:644-684): outbound forward + backward,
-        // inbound backward (directed)
         out.w_fwd.resize(out.n_groups);
         out.w_bwd.resize(out.n_groups);
         node_weights(*this, out, v, bound, true, hs);

@@ -21,6 +21,7 @@ Engine::Engine(const trw_config& c) : cfg(c), device(c.device_id) {
     check_hip(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
     check_hip(hipStreamCreateWithFlags(&side, hipStreamNonBlocking), "hipStreamCreate");
     check_hip(hipEventCreateWithFlags(&side_done, hipEventDisableTiming), "hipEventCreate");
+    check_hip(hipEventCreateWithFlags(&ts_ready, hipEventDisableTiming), "hipEventCreate");
     for (auto& e : ev) check_hip(hipEventCreate(&e), "hipEventCreate");
     check_hip(hipHostMalloc(&host_scalars, 256, hipHostMallocDefault), "hipHostMalloc");
 }
@@ -33,6 +34,7 @@ Engine::~Engine() {
     for (auto& e : ev)
         if (e) (void)hipEventDestroy(e);
     if (side_done) (void)hipEventDestroy(side_done);
+    if (ts_ready) (void)hipEventDestroy(ts_ready);
     if (host_scalars) (void)hipHostFree(host_scalars);
     if (side) (void)hipStreamDestroy(side);
     if (stream) (void)hipStreamDestroy(stream);

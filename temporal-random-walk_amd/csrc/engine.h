@@ -241,10 +241,13 @@ struct Engine {
     trw_config cfg{};
     int device = 0;
     hipStream_t stream = nullptr;
-    // a second stream for copies that overlap the build (same priority), and
-    // the event the build's end waits on
+    // a second stream for work that overlaps the build (same priority): the
+    // batch's endpoint copies and the global weights; the event the build's
+    // end waits on, and the one the global weights wait on (the timestamp
+    // groups ready)
     hipStream_t side = nullptr;
     hipEvent_t side_done = nullptr;
+    hipEvent_t ts_ready = nullptr;
 
     // edge store (+ the second half of a ping-pong pair for the gather)
     DBuf<int32_t> src, dst, src2, dst2;
@@ -316,6 +319,8 @@ struct Engine {
     DBuf<uint32_t> hist, flags, scan, scan_scratch;
     DBuf<uint64_t> scan64_scratch;
     DBuf<double> dscratch, fscan_scratch;
+    DBuf<double> gsum;         // the global weights' sums (side stream)
+    DBuf<uint32_t> wg_long_g;  // their guides' long-run list (side stream)
     DBuf<int64_t> red64;    // reduction results + partials
     DBuf<int32_t> red32;
     DBuf<int32_t> stage_src, stage_dst;
