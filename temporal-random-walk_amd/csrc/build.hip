@@ -649,14 +649,43 @@ __global__ void global_guide_kernel(const double* __restrict__ w, size_t n, int 
 }
 
 // The weighted panel: every group's panel record with its end, cumulative
-// weight and first edge record.
+// weight and first edge record (with its next slice bound).
 __global__ void wpan_kernel(const PanelRec* __restrict__ pan, const double* __restrict__ w,
-                            const EdgeRec* __restrict__ rec, size_t ng,
+                            const WEdgeRec* __restrict__ wrec, size_t ng,
                             WPanelRec* __restrict__ out) {
     const size_t g = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
     if (g >= ng) return;
     const PanelRec p = pan[g];
-    out[g] = WPanelRec{p.rank, p.start, pan[g + 1].start, 0u, w[g], rec[p.start]};
+    const WEdgeRec r = wrec[p.start];
+    out[g] = WPanelRec{p.rank, p.start, pan[g + 1].start, r.nxt, w[g], EdgeRec{r.nbr, r.eid}};
+}
+
+// The weighted records of a direction (index_layout.h, WEdgeRec): entry k's
+// record, and the lower_bound of its timestamp rank among its neighbour's
+// groups -- the walk's own time search (first_ge) over the direction's
+// finished headers, bucket tables and panel -- with the flag of a group at
+// that rank.  rank: the entries' timestamp ranks.
+__global__ __launch_bounds__(kB) void entry_bounds_kernel(
+    const EdgeRec* __restrict__ rec, const uint32_t* __restrict__ rank,
+    const NodeHdr* __restrict__ hdr, const uint32_t* __restrict__ tab,
+    const PanelRec* __restrict__ pan, size_t n, size_t vc, WEdgeRec* __restrict__ out) {
+    const size_t k = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (k >= n) return;
+    const EdgeRec r = rec[k];
+    const uint32_t x = rank[k];
+    const uint32_t v = static_cast<uint32_t>(r.nbr);
+    uint32_t nxt = kNoNext;
+    if (static_cast<size_t>(v) + 1 < vc) {
+        const NodeHdr h = hdr[v];
+        uint32_t G = h.meta & kHdrGMask;
+        if (G == kHdrGMask) G = hdr[v + 1].gb - h.gb;
+        const PanelRec* f = pan + h.gb;
+        const int b = first_ge(tab, h, v, static_cast<int>(G), f, x);
+        const bool at = b < static_cast<int>(G) && f[b].rank == x;
+        const uint64_t gl = static_cast<uint64_t>(h.gb) + static_cast<uint32_t>(b);
+        if (gl <= kNextMax) nxt = static_cast<uint32_t>(gl) | (at ? 0x80000000u : 0u);
+    }
+    out[k] = WEdgeRec{r.nbr, r.eid, nxt, 0u};
 }
 
 // The buckets [from, to] of group g (local index i of a segment of G): those
@@ -1335,6 +1364,12 @@ void finish_direction(Engine& e, DirIndex& dir, size_t n, size_t vc, int64_t* ho
     if (g)
         hipLaunchKernelGGL(node_table_fill_kernel, dim3(grid_for(g)), dim3(kB), 0, s, dir.key.p,
                            dir.grp.p, dir.hdr.p, dir.pan.p, static_cast<size_t>(g), dir.tab.p);
+    // the weight pickers' records: every entry's next slice bound, searched
+    // once here instead of at every hop that takes the entry
+    dir.wrec.resize(weights ? n : 0);
+    if (weights && n)
+        hipLaunchKernelGGL(entry_bounds_kernel, dim3(grid_for(n)), dim3(kB), 0, s, dir.rec.p,
+                           e.v32a.p, dir.hdr.p, dir.tab.p, dir.pan.p, n, vc, dir.wrec.p);
     check_hip(hipGetLastError(), "direction index launch");
 }
 
@@ -1421,7 +1456,7 @@ void build_walk_weights(Engine& e, DirIndex& dir, size_t v, const DBuf<double>& 
                        vc, decaying ? 1 : 0, ww.hdr.p);
     if (g)
         hipLaunchKernelGGL(wpan_kernel, dim3(grid_for(g)), dim3(kB), 0, s, dir.pan.p, w.p,
-                           dir.rec.p, g, ww.pan.p);
+                           dir.wrec.p, g, ww.pan.p);
     fill_weight_guides(e.stream, e.wg_long, w.p, g, dir.key.p, dir.grp.p, dir.cnt.p, ww.hdr.p,
                        nullptr, decaying, ww.tab.p, ww.tab.n);
     check_hip(hipGetLastError(), "walk weights launch");

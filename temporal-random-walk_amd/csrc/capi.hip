@@ -48,7 +48,8 @@ size_t Engine::memory_used() const {
     for (const DirIndex* d : {&out, &in}) {
         b += d->off.bytes() + d->idx.bytes() + d->rec.bytes() + d->cnt.bytes() + d->grp.bytes() +
              d->first_ts.bytes() + d->pan.bytes() + d->hdr.bytes() + d->tab.bytes() +
-             d->w_fwd.bytes() + d->w_bwd.bytes() + d->wf.bytes() + d->wb.bytes();
+             d->w_fwd.bytes() + d->w_bwd.bytes() + d->wrec.bytes() + d->wf.bytes() +
+             d->wb.bytes();
     }
     // blocks of grown buffers held until the next clear() (DBuf::ensure)
     return b + retired.bytes;

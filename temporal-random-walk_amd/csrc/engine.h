@@ -197,6 +197,7 @@ struct DirIndex {
     DBuf<uint32_t> tab;      // bucket tables
     DBuf<double> w_fwd;      // g (outbound only)
     DBuf<double> w_bwd;      // g
+    DBuf<WEdgeRec> wrec;     // n entries with next slice bounds (weights only)
     // weight pickers' views: of w_fwd for forward walks (out), of w_bwd for
     // backward walks (in; out if undirected)
     WalkWeights wf, wb;
@@ -206,7 +207,7 @@ struct DirIndex {
 
     void clear() {
         off.n = idx.n = rec.n = key.n = cnt.n = grp.n = first_ts.n = pan.n = hdr.n = tab.n = w_fwd.n =
-            w_bwd.n = 0;
+            w_bwd.n = wrec.n = 0;
         wf.clear();
         wb.clear();
         n_entries = n_groups = 0;

@@ -36,12 +36,16 @@
 //                                  picked group's range usually shares the
 //                                  line of the search's last probe
 //     w_fwd, w_bwd  fp64[g]        per-node cumulative exponential weights
+//     wrec          WEdgeRec[n]    (neighbour, edge id, the walk's next slice
+//                                  bound at the neighbour) in idx order;
+//                                  built with the weights (below)
 //   per walk direction with weights (forward walks: out with w_fwd; backward
 //   walks: in with w_bwd, or out with w_bwd if undirected)
 //     whdr          WNodeHdr[V_c]  node header + guide parameters and weight
 //                                  total of the node's cumulative weights
-//     wpan          WPanelRec[g]   (ts rank, start, end, cumulative weight,
-//                                  first edge record) of every group
+//     wpan          WPanelRec[g]   (ts rank, start, end, the first entry's
+//                                  next slice bound, cumulative weight, first
+//                                  edge record) of every group
 //     wgt           uint32[2(g+V_c)] guide tables of nodes with > kWGuideMin
 //                                  groups, node u's at 2 (gb + u) (below)
 //   global weights  fwd_cum, bwd_cum fp64[T] (+ their guides: one segment)
@@ -184,18 +188,81 @@ struct alignas(32) WNodeHdr {
 static_assert(sizeof(WNodeHdr) == 32, "WNodeHdr must be 32 bytes");
 
 // One node-timestamp group in the weight pickers' panel: its panel record, its
-// end, its cumulative weight and its first edge record, so the weight search,
-// the slice's sums, the picked group's range and -- for a group of one edge
-// -- the edge itself read one aligned 32-byte record.
+// end, its cumulative weight and its first edge record (with that entry's
+// next slice bound, below), so the weight search, the slice's sums, the
+// picked group's range and -- for a group of one edge -- the edge itself read
+// one aligned 32-byte record.
 struct alignas(32) WPanelRec {
     uint32_t rank;
     uint32_t start;
-    uint32_t end;  // the next group's start
-    uint32_t pad;
+    uint32_t end;   // the next group's start
+    uint32_t nxt0;  // wrec[start].nxt
     double c;
     EdgeRec rec0;  // rec[start]
 };
 static_assert(sizeof(WPanelRec) == 32, "WPanelRec must be 32 bytes");
+
+// The records of a direction with weights: an entry (u, v, r) -- neighbour v
+// reached at timestamp rank r -- also holds where the walk's next valid slice
+// at v begins or ends.  A walk that takes the entry continues from v at time
+// r, and its time search there is the lower_bound b of r among v's group
+// ranks (backward: the slice ends at b) or of r + 1 (forward: it starts at b,
+// plus one when v has a group at r itself).  nxt holds v's first group plus b
+// (a global panel index) in bits 0-30 and that "group at r" flag in bit 31,
+// so one record serves both walk directions of an undirected index; kNoNext
+// where the index is too large for 31 bits.  The search it replaces reads a
+// node's bucket table and panel: one random line less per hop at a hub.
+struct alignas(16) WEdgeRec {
+    int32_t nbr;
+    uint32_t eid;
+    uint32_t nxt;
+    uint32_t pad;
+};
+static_assert(sizeof(WEdgeRec) == 16, "WEdgeRec must be 16 bytes");
+constexpr uint32_t kNoNext = 0xffffffffu;
+constexpr uint32_t kNextMax = 0x7ffffffeu;  // largest global bound nxt holds
+
+// The global bound a walk of direction Fwd reads from nxt (kNoNext: search).
+template <bool Fwd>
+__host__ __device__ inline uint32_t next_bound(uint32_t nxt) {
+    if (nxt == kNoNext) return kNoNext;
+    return (nxt & 0x7fffffffu) + (Fwd ? (nxt >> 31) : 0u);
+}
+
+typedef uint32_t u32x2_a4 __attribute__((ext_vector_type(2), aligned(4)));
+typedef uint32_t u32x4_a8 __attribute__((ext_vector_type(4), aligned(8)));
+
+// First local index i in [0, G) whose group rank is >= x, G if none: a
+// lower_bound over the node's sorted panel, so the answer is unique and the
+// way it is found does not change any result.  A node with more than kTabMin
+// groups that has a group at every rank of its span (dense) answers from the
+// rank itself.  Another such node looks up x's bucket b in its table: a
+// single-rank bucket holds the answer itself; a wider one gives the bracket
+// [tab[b], tab[b + 1]] (about one group).  The rest is a binary search over
+// at most kTabMin groups.
+template <class Rec>
+__device__ __forceinline__ int first_ge(const uint32_t* tab, const NodeHdr& h, uint32_t u, int G,
+                                        const Rec* f, uint32_t x) {
+    int lo = 0, hi = G;
+    if (G > static_cast<int>(kTabMin)) {
+        if (x <= h.r0) return 0;
+        if (h.meta & kHdrDense) return static_cast<int>(min(x - h.r0, static_cast<uint32_t>(G)));
+        const uint32_t shift = hdr_shift(h);
+        const uint32_t b = (x - h.r0) >> shift;
+        if (b >= h.nb) return G;  // past the last bucket
+        const uint32_t* t = tab + hdr_tab_base(h, u) + b;
+        if (shift == 0) return static_cast<int>(t[0]);
+        const u32x2_a4 br = *reinterpret_cast<const u32x2_a4*>(t);  // one 8-byte load
+        lo = static_cast<int>(br.x);
+        hi = static_cast<int>(br.y);
+    }
+    while (lo < hi) {
+        const int mid = lo + ((hi - lo) >> 1);
+        if (f[mid].rank >= x) hi = mid;
+        else lo = mid + 1;
+    }
+    return lo;
+}
 
 
 }  // namespace trw

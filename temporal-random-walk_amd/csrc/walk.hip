@@ -54,6 +54,8 @@ struct DirView {
     const PanelRec* pan;  // g + 1 group records (terminator)
     const EdgeRec* rec;   // walk-order edge records
     uint32_t idx_size;
+    // the same records with the walk's next slice bounds (weights only)
+    const WEdgeRec* wrec;
     // the weight pickers' view of the sampled direction's cumulative weights
     // (read by the weight families' kernels only; nullptr without weights)
     const WNodeHdr* whdr;   // V_c node headers with guide parameters
@@ -201,10 +203,14 @@ struct Sel {
 
 // Result of a per-node selection: the node reached, the rank of the edge's
 // time and the edge id (-1 for none).
+// A picked edge: the node it reaches, its timestamp rank, its id, and (edges
+// picked over the weighted records) the global bound of the walk's next slice
+// at that node (WEdgeRec::nxt read for the walk's direction; kNoNext: search).
 struct Hop {
     int32_t nbr;
     int32_t r;
     int32_t e;
+    uint32_t nx = kNoNext;
 };
 
 __device__ __forceinline__ Sel no_edge() { return Sel{-1, -1, -1, -1}; }
@@ -214,54 +220,33 @@ __device__ __forceinline__ Hop hop_of(const EdgeRec& rec, uint32_t rank) {
 }
 
 __device__ __forceinline__ EdgeRec load_rec(const EdgeRec* p) { return *p; }
+template <bool Fwd>
+__device__ __forceinline__ Hop whop_of(int32_t nbr, uint32_t eid, uint32_t nxt, uint32_t rank) {
+    return Hop{nbr, static_cast<int32_t>(rank), static_cast<int32_t>(eid), next_bound<Fwd>(nxt)};
+}
+// Entry `pick` of the weighted records, or the group's first entry (held in
+// the group's weighted panel record v = {rank, start, end, nxt0} and r0)
+template <bool Fwd>
+__device__ __forceinline__ Hop weighted_entry(const WalkGraph& g, const u32x4_a8& v,
+                                              const EdgeRec& r0, uint32_t pick) {
+    if (pick == v.y) return whop_of<Fwd>(r0.nbr, r0.eid, v.w, v.x);
+    const WEdgeRec wr = g.d.wrec[pick];
+    return whop_of<Fwd>(wr.nbr, wr.eid, wr.nxt, v.x);
+}
 
 // A group's panel record and the next group's start (its end), read as one
 // 16-byte load at the record's 8-byte alignment.
 struct PanelPair {
     uint32_t rank, start, next_rank, next_start;
 };
-typedef uint32_t u32x4_a8 __attribute__((ext_vector_type(4), aligned(8)));
 __device__ __forceinline__ PanelPair load_pair(const PanelRec* p) {
     const u32x4_a8 v = *reinterpret_cast<const u32x4_a8*>(p);
     return PanelPair{v.x, v.y, v.z, v.w};
 }
 
-typedef uint32_t u32x2_a4 __attribute__((ext_vector_type(2), aligned(4)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef int64_t i64x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-// First local index i in [0, G) whose group rank is >= x, G if none: a
-// lower_bound over the node's sorted panel, so the answer is unique and the
-// way it is found does not change any result.  A node with more than kTabMin
-// groups that has a group at every rank of its span (dense) answers from the
-// rank itself.  Another such node looks up x's bucket b in its table: a
-// single-rank bucket holds the answer itself; a wider one gives the bracket
-// [tab[b], tab[b + 1]] (about one group).  The rest is a binary search over
-// at most kTabMin groups.
-template <class Rec>
-__device__ __forceinline__ int first_ge(const uint32_t* tab, const NodeHdr& h, uint32_t u, int G,
-                                        const Rec* f, uint32_t x) {
-    int lo = 0, hi = G;
-    if (G > static_cast<int>(kTabMin)) {
-        if (x <= h.r0) return 0;
-        if (h.meta & kHdrDense) return static_cast<int>(min(x - h.r0, static_cast<uint32_t>(G)));
-        const uint32_t shift = hdr_shift(h);
-        const uint32_t b = (x - h.r0) >> shift;
-        if (b >= h.nb) return G;  // past the last bucket
-        const uint32_t* t = tab + hdr_tab_base(h, u) + b;
-        if (shift == 0) return static_cast<int>(t[0]);
-        const u32x2_a4 br = *reinterpret_cast<const u32x2_a4*>(t);  // one 8-byte load
-        lo = static_cast<int>(br.x);
-        hi = static_cast<int>(br.y);
-    }
-    while (lo < hi) {
-        const int mid = lo + ((hi - lo) >> 1);
-        if (f[mid].rank >= x) hi = mid;
-        else lo = mid + 1;
-    }
-    return lo;
-}
 
 __device__ __forceinline__ Sel edge_of(const WalkGraph& g, uint32_t e, long group) {
     return Sel{g.src[e], g.dst[e], static_cast<int32_t>(e), static_cast<int32_t>(group)};
@@ -394,14 +379,15 @@ __device__ __forceinline__ bool adjacent(const WalkGraph& g, int prev, int cand)
 // within the group's range, (int)(re * size) as edge_selectors.cuh:420-443
 // takes it.  The group's record holds its first edge record, so a pick of
 // entry 0 (every pick in a group of one edge) loads no record.
+template <bool Fwd>
 __device__ __forceinline__ Hop weighted_group_hop(const WalkGraph& g, const WPanelRec* f,
                                                   uint32_t x, double re) {
-    const u32x4_a8 v = *reinterpret_cast<const u32x4_a8*>(f + x);  // rank, start, end
-    const uint32_t rank = v.x, es = v.y, ee = v.z;
+    const u32x4_a8 v = *reinterpret_cast<const u32x4_a8*>(f + x);  // rank, start, end, nxt0
+    const uint32_t es = v.y, ee = v.z;
     const EdgeRec r0 = f[x].rec0;
     if (es >= ee || es >= g.d.idx_size || ee > g.d.idx_size) return no_hop();
     const uint32_t k = static_cast<uint32_t>(static_cast<int>(re * static_cast<int>(ee - es)));
-    return hop_of(k == 0 ? r0 : load_rec(g.d.rec + es + k), rank);
+    return weighted_entry<Fwd>(g, v, r0, es + k);
 }
 
 // graph/temporal_node2vec_helpers.cuh:127-199 over the slice [vb, ve) of a
@@ -429,8 +415,10 @@ __device__ Hop tn2v_pick(const WalkGraph& g, int prev, const WPanelRec* f, uint3
     // (start_sum == end_sum) picks its first group every time -- so the
     // last group's record, edge record and adjacency answer are kept and
     // reused while they still apply: the same values, no reload.
-    uint32_t gx = ~0u, g_rank = 0, g_es = 0, g_ee = 0;
-    EdgeRec g_r0{0, 0}, e_rec{0, 0};
+    uint32_t gx = ~0u;
+    u32x4_a8 gv{0u, 0u, 0u, 0u};  // the group's rank, start, end, nxt0
+    EdgeRec g_r0{0, 0};
+    Hop e_hop = no_hop();
     uint32_t e_pick = ~0u;
     int adj_cand = -1;
     bool adj_val = false, adj_known = false;
@@ -443,24 +431,22 @@ __device__ Hop tn2v_pick(const WalkGraph& g, int prev, const WPanelRec* f, uint3
         // reference (get_node_group_edge_end, walk_step_helpers.cuh:19-38)
         if (x >= G) continue;
         if (x != gx) {
-            const u32x4_a8 v = *reinterpret_cast<const u32x4_a8*>(f + x);  // rank, start, end
-            g_rank = v.x;
-            g_es = v.y;
-            g_ee = v.z;
+            gv = *reinterpret_cast<const u32x4_a8*>(f + x);
             g_r0 = f[x].rec0;
             gx = x;
         }
+        const uint32_t g_es = gv.y, g_ee = gv.z;
         if (g_es >= g_ee || g_es >= g.d.idx_size || g_ee > g.d.idx_size) continue;
         // min((size_t)(er * size), size - 1): temporal_node2vec_helpers.cuh:169-182
         const uint64_t local = static_cast<uint64_t>(er * static_cast<double>(g_ee - g_es));
         const uint32_t pick =
             g_es + static_cast<uint32_t>(local < g_ee - g_es ? local : g_ee - g_es - 1);
         if (pick != e_pick) {
-            e_rec = pick == g_es ? g_r0 : load_rec(g.d.rec + pick);
+            e_hop = weighted_entry<Fwd>(g, gv, g_r0, pick);
             e_pick = pick;
         }
-        last = hop_of(e_rec, g_rank);
-        const int cand = e_rec.nbr;
+        last = e_hop;
+        const int cand = e_hop.nbr;
         bool accept;
         if (cand == prev) {
             accept = ar < g.inv_p * inv_bmax;
@@ -522,14 +508,13 @@ __device__ __forceinline__ int tn2v_try(const WalkGraph& g, const Tn2vHop& s, in
     const uint32_t x = node_weight_pick<Fwd>(s.f, s.G, s.gt, s.gd, s.vb, s.ve, gr, s.start_sum,
                                              s.end_sum);
     if (x >= s.G) return 0;
-    const u32x4_a8 v = *reinterpret_cast<const u32x4_a8*>(s.f + x);  // rank, start, end
+    const u32x4_a8 v = *reinterpret_cast<const u32x4_a8*>(s.f + x);  // rank, start, end, nxt0
     const uint32_t es = v.y, ee = v.z;
     if (es >= ee || es >= g.d.idx_size || ee > g.d.idx_size) return 0;
     const uint64_t local = static_cast<uint64_t>(er * static_cast<double>(ee - es));
     const uint32_t pick = es + static_cast<uint32_t>(local < ee - es ? local : ee - es - 1);
-    const EdgeRec rec = pick == es ? s.f[x].rec0 : load_rec(g.d.rec + pick);
-    out = hop_of(rec, v.x);
-    const int cand = rec.nbr;
+    out = weighted_entry<Fwd>(g, v, s.f[x].rec0, pick);
+    const int cand = out.nbr;
     bool accept;
     if (cand == s.prev) accept = ar < g.inv_p * inv_bmax;
     else if (ar < acc_lo) accept = true;
@@ -564,7 +549,8 @@ __device__ __forceinline__ Tn2vHop lane_read(const Tn2vHop& s, int src) {
     return o;
 }
 __device__ __forceinline__ Hop lane_read(const Hop& h, int src) {
-    return Hop{lane_read(h.nbr, src), lane_read(h.r, src), lane_read(h.e, src)};
+    return Hop{lane_read(h.nbr, src), lane_read(h.r, src), lane_read(h.e, src),
+               lane_read(h.nx, src)};
 }
 
 // The hops of the lanes with `want` (state s) decided by the whole wave (see
@@ -662,17 +648,25 @@ __device__ __forceinline__ Hop hop_from_group(const WalkGraph& g, uint32_t gpos,
 //
 // The valid slice [vb, ve) of node u's G groups (local indexes), searched in
 // its panel f (PanelRec or WPanelRec: the ranks are the same): filter_valid_
-// groups_by_timestamp_slice (edge_selectors.cuh:66-120) and the cutoff.
+// groups_by_timestamp_slice (edge_selectors.cuh:66-120) and the cutoff.  nl:
+// the time bound carried from the edge that reached u (the same lower_bound,
+// local), searched for when it is not in [0, G].
 template <bool Fwd, class Rec>
 __device__ __forceinline__ void valid_slice(const uint32_t* tab, const NodeHdr& h, uint32_t u,
                                             int G, const Rec* f, int32_t t, int32_t cut, int& vb,
-                                            int& ve) {
+                                            int& ve, uint32_t nl = kNoNext) {
     vb = 0;
     ve = G;
     if (t != -1) {
         const uint32_t x = static_cast<uint32_t>(t);
-        if (Fwd) vb = first_ge(tab, h, u, G, f, x + 1);  // upper_bound
-        else ve = first_ge(tab, h, u, G, f, x);         // lower_bound
+        if (nl <= static_cast<uint32_t>(G)) {
+            if (Fwd) vb = static_cast<int>(nl);
+            else ve = static_cast<int>(nl);
+        } else if (Fwd) {
+            vb = first_ge(tab, h, u, G, f, x + 1);  // upper_bound
+        } else {
+            ve = first_ge(tab, h, u, G, f, x);  // lower_bound
+        }
     }
     if (cut != -1) {
         // the first group at or past the cutoff, within [vb, ve]
@@ -709,7 +703,7 @@ template <bool Fwd, int Fam>
 __device__ __forceinline__ Hop wnode_edge_from(const WalkGraph& g, int picker, uint32_t u, bool ok,
                                                const WNodeHdr& wh, int32_t t, int32_t cut,
                                                int prev, double rg, double re,
-                                               const double* em1) {
+                                               const double* em1, uint32_t nx) {
     const NodeHdr& h = wh.h;
     uint32_t Gu = ok ? (h.meta & kHdrGMask) : 0u;
     if (Gu == kHdrGMask) Gu = g.d.whdr[u + 1].h.gb - h.gb;
@@ -718,7 +712,7 @@ __device__ __forceinline__ Hop wnode_edge_from(const WalkGraph& g, int picker, u
     const int G = static_cast<int>(Gu);
     const WPanelRec* f = g.d.wpan + gb;
     int vb, ve;
-    valid_slice<Fwd>(g.d.tab, h, u, G, f, t, cut, vb, ve);
+    valid_slice<Fwd>(g.d.tab, h, u, G, f, t, cut, vb, ve, nx - gb);
     if (vb >= ve) return no_hop();
     uint32_t x;
     if (is_index_picker(picker)) {
@@ -742,7 +736,7 @@ __device__ __forceinline__ Hop wnode_edge_from(const WalkGraph& g, int picker, u
                                   static_cast<uint32_t>(ve), rg, start_sum, end_sum);
         if (x >= Gu) return no_hop();
     }
-    return weighted_group_hop(g, f, x, re);
+    return weighted_group_hop<Fwd>(g, f, x, re);
 }
 
 // wnode_edge_from in the any-picker row-writing kernel, whose node2vec
@@ -753,10 +747,11 @@ template <bool Fwd>
 __device__ __forceinline__ Hop wnode_edge_from_wave(const WalkGraph& g, int picker, uint32_t u,
                                                     bool ok, const WNodeHdr& wh, int32_t t,
                                                     int32_t cut, int prev, double rg, double re,
-                                                    const double* em1, bool& want, Tn2vHop& s) {
+                                                    const double* em1, uint32_t nx, bool& want,
+                                                    Tn2vHop& s) {
     want = false;
     if (picker != kTemporalNode2Vec || prev == -1)
-        return wnode_edge_from<Fwd, kFamAny>(g, picker, u, ok, wh, t, cut, prev, rg, re, em1);
+        return wnode_edge_from<Fwd, kFamAny>(g, picker, u, ok, wh, t, cut, prev, rg, re, em1, nx);
     const NodeHdr& h = wh.h;
     uint32_t Gu = ok ? (h.meta & kHdrGMask) : 0u;
     if (Gu == kHdrGMask) Gu = g.d.whdr[u + 1].h.gb - h.gb;
@@ -765,7 +760,7 @@ __device__ __forceinline__ Hop wnode_edge_from_wave(const WalkGraph& g, int pick
     const int G = static_cast<int>(Gu);
     const WPanelRec* f = g.d.wpan + gb;
     int vb, ve;
-    valid_slice<Fwd>(g.d.tab, h, u, G, f, t, cut, vb, ve);
+    valid_slice<Fwd>(g.d.tab, h, u, G, f, t, cut, vb, ve, nx - gb);
     if (vb >= ve) return no_hop();
     if (gb + Gu > g.d.w_size) return no_hop();
     const double start_sum = vb > 0 ? f[vb - 1].c : 0.0;
@@ -799,9 +794,10 @@ __device__ __forceinline__ HopHdr<Fam> load_hop_hdr(const WalkGraph& g, uint32_t
 template <bool Fwd, int Fam>
 __device__ __forceinline__ Hop hop_at(const WalkGraph& g, int picker, uint32_t u, bool ok,
                                       const HopHdr<Fam>& hh, int32_t t, int32_t cut, int prev,
-                                      double rg, double re, const double* em1) {
+                                      double rg, double re, const double* em1,
+                                      uint32_t nx = kNoNext) {
     if constexpr (Fam == kFamIndex) return node_edge_from<Fwd>(g, picker, u, ok, hh, t, cut, rg, re, em1);
-    else return wnode_edge_from<Fwd, Fam>(g, picker, u, ok, hh, t, cut, prev, rg, re, em1);
+    else return wnode_edge_from<Fwd, Fam>(g, picker, u, ok, hh, t, cut, prev, rg, re, em1, nx);
 }
 
 template <bool Fwd, int Fam>
@@ -944,6 +940,7 @@ __global__ __launch_bounds__(kB) __attribute__((amdgpu_waves_per_eu(Fam == kFamI
     const int first = s0.first;
     int cur = s0.cur;
     int32_t cur_r = s0.r, cur_e = s0.e;
+    uint32_t cur_nx = kNoNext;  // the next slice's bound carried by the last edge
     int len = 0;
     if (cur_e != -1) {
         int prev = -1;
@@ -971,13 +968,14 @@ __global__ __launch_bounds__(kB) __attribute__((amdgpu_waves_per_eu(Fam == kFamI
             if (a.ds.replay) r = replay_pair(a.ds, w, p);
             const Hop h = hop_at<Fwd, Fam>(g, a.walk_bias, u, ok, hd,
                                                    cur_r == neg1 ? -1 : cur_r, cut, prev, r.a,
-                                                   r.b, em1);
+                                                   r.b, em1, cur_nx);
             // the reference's failure test is ts == -1: no edge, or an edge at -1
             if (h.e == -1 || h.r == neg1) break;
             prev = cur;
             cur = h.nbr;
             cur_r = h.r;
             cur_e = h.e;
+            cur_nx = h.nx;
             ++walk_len;
         }
     }
@@ -1200,6 +1198,7 @@ __global__ __launch_bounds__(kB) __attribute__((amdgpu_waves_per_eu(4))) void wa
                                 : (a.st ? a.st[w] : walk_start<Fwd, Dir, Fam>(g, a, w, cut));
     int cur = s0.cur, prev = -1;
     int32_t cur_r = s0.r, cur_e = s0.e;
+    uint32_t cur_nx = kNoNext;  // the next slice's bound carried by the last edge
     bool alive = live && s0.e != -1;  // the walk writes its next slot
     int len = 0;
     const int nb = a.pk_nb, rb = a.pk_rb;
@@ -1235,7 +1234,7 @@ __global__ __launch_bounds__(kB) __attribute__((amdgpu_waves_per_eu(4))) void wa
                             if (a.ds.replay) r = replay_pair(a.ds, w, p);
                             h = wnode_edge_from_wave<Fwd>(g, a.walk_bias, u, ok, hd,
                                                           cur_r == neg1 ? -1 : cur_r, cut, prev,
-                                                          r.a, r.b, em1, want, ts);
+                                                          r.a, r.b, em1, cur_nx, want, ts);
                             stepping = true;
                         }
                     }
@@ -1253,6 +1252,7 @@ __global__ __launch_bounds__(kB) __attribute__((amdgpu_waves_per_eu(4))) void wa
                         cur = h.nbr;
                         cur_r = h.r;
                         cur_e = h.e;
+                        cur_nx = h.nx;
                         alive = cur != a.pad;
                     }
                 }
@@ -1286,7 +1286,7 @@ __global__ __launch_bounds__(kB) __attribute__((amdgpu_waves_per_eu(4))) void wa
                     if (a.ds.replay) r = replay_pair(a.ds, w, p);
                     const Hop h = hop_at<Fwd, Fam>(g, a.walk_bias, u, ok, hd,
                                                            cur_r == neg1 ? -1 : cur_r, cut, prev,
-                                                           r.a, r.b, em1);
+                                                           r.a, r.b, em1, cur_nx);
                     if (h.e == -1 || h.r == neg1) {
                         alive = false;
                     } else {
@@ -1294,6 +1294,7 @@ __global__ __launch_bounds__(kB) __attribute__((amdgpu_waves_per_eu(4))) void wa
                         cur = h.nbr;
                         cur_r = h.r;
                         cur_e = h.e;
+                        cur_nx = h.nx;
                         alive = cur != a.pad;
                     }
                 }
@@ -2147,7 +2148,9 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
     g.d.idx_size = static_cast<uint32_t>(d.n_entries);
     // the weight pickers' view of the sampled direction's per-node weights
     const WalkWeights& ww = forward ? out.wf : d.wb;
-    const bool wview = weights_ready && ww.hdr.n == d.hdr.n && ww.pan.n == d.n_groups;
+    const bool wview = weights_ready && ww.hdr.n == d.hdr.n && ww.pan.n == d.n_groups &&
+                       d.wrec.n == d.n_entries;
+    g.d.wrec = wview ? d.wrec.p : nullptr;
     g.d.whdr = wview ? ww.hdr.p : nullptr;
     g.d.wpan = wview ? ww.pan.p : nullptr;
     g.d.wgt = wview ? ww.tab.p : nullptr;
@@ -2190,10 +2193,10 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
     const bool no_node2vec = walk_bias != kTemporalNode2Vec;  // start_bias never is (above)
     // the index arrays the launched walk kernel reads (each counted whole):
     // headers (plain or weighted), bucket tables, panel (plain or weighted)
-    // and records of the sampled direction, the guide tables for the weight
-    // families; the adjacency pair set for node2vec
-    w_index_bytes = d.tab.bytes() + d.rec.bytes() +
-                    (index_only ? d.hdr.bytes() + d.pan.bytes() : ww.bytes());
+    // and records (plain or weighted) of the sampled direction, the guide
+    // tables for the weight families; the adjacency pair set for node2vec
+    w_index_bytes = d.tab.bytes() + (index_only ? d.rec.bytes() + d.hdr.bytes() + d.pan.bytes()
+                                                : d.wrec.bytes() + ww.bytes());
     if (walk_bias == kTemporalNode2Vec && adj_ready) w_index_bytes += adj_hash.bytes();
 #define TRW_LAUNCH_FAMILY(K, F, D, G, ...)                                                     \
     do {                                                                                       \
