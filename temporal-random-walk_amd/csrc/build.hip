@@ -680,8 +680,32 @@ __global__ __launch_bounds__(kB) void entry_bounds_kernel(
         uint32_t G = h.meta & kHdrGMask;
         if (G == kHdrGMask) G = hdr[v + 1].gb - h.gb;
         const PanelRec* f = pan + h.gb;
-        const int b = first_ge(tab, h, v, static_cast<int>(G), f, x);
-        const bool at = b < static_cast<int>(G) && f[b].rank == x;
+        // first_ge's answer b, with the flag read where it costs no line: a
+        // dense node has a group at every rank of its span, and a
+        // single-rank bucket's next entry moves past b exactly when one of
+        // the node's groups has rank x (the 8-byte load the walk's search
+        // makes anyway; the closing entry follows the last bucket)
+        int b;
+        bool at;
+        const uint32_t shift = hdr_shift(h);
+        if (G > kTabMin && x > h.r0 && !(h.meta & kHdrDense) && shift == 0) {
+            const uint32_t bk = x - h.r0;
+            if (bk >= h.nb) {
+                b = static_cast<int>(G);
+                at = false;
+            } else {
+                const u32x2_a4 br =
+                    *reinterpret_cast<const u32x2_a4*>(tab + hdr_tab_base(h, v) + bk);
+                b = static_cast<int>(br.x);
+                at = br.y > br.x;
+            }
+        } else if (G > kTabMin && x >= h.r0 && (h.meta & kHdrDense)) {
+            b = static_cast<int>(min(x - h.r0, G));
+            at = x - h.r0 < G;
+        } else {
+            b = first_ge(tab, h, v, static_cast<int>(G), f, x);
+            at = b < static_cast<int>(G) && f[b].rank == x;
+        }
         const uint64_t gl = static_cast<uint64_t>(h.gb) + static_cast<uint32_t>(b);
         if (gl <= kNextMax) nxt = static_cast<uint32_t>(gl) | (at ? 0x80000000u : 0u);
     }
