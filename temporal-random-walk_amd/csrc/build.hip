@@ -1627,34 +1627,54 @@ void Engine::sort_store(const int32_t* d_src, const int32_t* d_dst, const int64_
     hist.ensure(radix_hist_elems(2 * etot));
     uint32_t* k32s[2] = {reinterpret_cast<uint32_t*>(k64a.p), reinterpret_cast<uint32_t*>(k64b.p)};
     uint32_t* pos0 = carry_ends ? nullptr : v32a.p;
-    int which;
-    if (keys32) {
-        hipLaunchKernelGGL((make_ts_keys_kernel<uint32_t>), dim3(grid_for(etot)), dim3(kB), 0, s,
-                           ts.p, src.p, dst.p, e_old, d_ts, d_src, d_dst, n, tmin, k32s[0], pos0,
-                           ends64.p);
-        which = carry_ends
-                    ? radix_sort_u32_v64(k32s[0], ends64.p, k32s[1], ends64b.p, etot, 0, bits,
-                                         hist.p, s)
-                    : radix_sort_u32(k32s[0], v32a.p, k32s[1], v32b.p, etot, 0, bits, hist.p, s);
-    } else {
-        hipLaunchKernelGGL((make_ts_keys_kernel<uint64_t>), dim3(grid_for(etot)), dim3(kB), 0, s,
-                           ts.p, src.p, dst.p, e_old, d_ts, d_src, d_dst, n, tmin, k64a.p, pos0,
-                           ends64.p);
-        which = carry_ends
-                    ? radix_sort_u64_v64(k64a.p, ends64.p, k64b.p, ends64b.p, etot, 0, bits,
-                                         hist.p, s)
-                    : radix_sort_u64(k64a.p, v32a.p, k64b.p, v32b.p, etot, 0, bits, hist.p, s);
-    }
-    uint32_t* perm = which ? v32b.p : v32a.p;
-    const uint64_t* sorted_ends = which ? ends64b.p : ends64.p;
-
-    // ---- 3. window eviction: drop ts <= latest - capacity
+    // the window's cut (step 3), known before the sort: when it keeps every
+    // edge and the endpoints ride as values, the sort's last pass writes the
+    // new store itself (step 4 then has nothing to do)
     int64_t target = -1;
     if (cfg.max_time_capacity > 0) {
         const int64_t cutoff = latest_ts - cfg.max_time_capacity;
         if (cutoff >= tmin) target = static_cast<int64_t>(static_cast<uint64_t>(cutoff) -
                                                           static_cast<uint64_t>(tmin));
     }
+    const bool fold = carry_ends && target < 0;
+    if (fold) {
+        src2.resize(etot);
+        dst2.resize(etot);
+        ts2.resize(etot);
+    }
+    const SortedStore st{src2.p, dst2.p, ts2.p, tmin};
+    bool folded = false;
+    int which = 0;
+    if (keys32) {
+        hipLaunchKernelGGL((make_ts_keys_kernel<uint32_t>), dim3(grid_for(etot)), dim3(kB), 0, s,
+                           ts.p, src.p, dst.p, e_old, d_ts, d_src, d_dst, n, tmin, k32s[0], pos0,
+                           ends64.p);
+        if (fold)
+            folded = radix_sort_u32_v64_store(k32s[0], ends64.p, k32s[1], ends64b.p, etot, 0, bits,
+                                              hist.p, s, st);
+        else
+            which = carry_ends
+                        ? radix_sort_u32_v64(k32s[0], ends64.p, k32s[1], ends64b.p, etot, 0, bits,
+                                             hist.p, s)
+                        : radix_sort_u32(k32s[0], v32a.p, k32s[1], v32b.p, etot, 0, bits, hist.p,
+                                         s);
+    } else {
+        hipLaunchKernelGGL((make_ts_keys_kernel<uint64_t>), dim3(grid_for(etot)), dim3(kB), 0, s,
+                           ts.p, src.p, dst.p, e_old, d_ts, d_src, d_dst, n, tmin, k64a.p, pos0,
+                           ends64.p);
+        if (fold)
+            folded = radix_sort_u64_v64_store(k64a.p, ends64.p, k64b.p, ends64b.p, etot, 0, bits,
+                                              hist.p, s, st);
+        else
+            which = carry_ends
+                        ? radix_sort_u64_v64(k64a.p, ends64.p, k64b.p, ends64b.p, etot, 0, bits,
+                                             hist.p, s)
+                        : radix_sort_u64(k64a.p, v32a.p, k64b.p, v32b.p, etot, 0, bits, hist.p, s);
+    }
+    uint32_t* perm = which ? v32b.p : v32a.p;
+    const uint64_t* sorted_ends = which ? ends64b.p : ends64.p;
+
+    // ---- 3. window eviction: drop ts <= latest - capacity
     size_t del = 0;
     if (target >= 0) {
         if (keys32)
@@ -1679,7 +1699,9 @@ void Engine::sort_store(const int32_t* d_src, const int32_t* d_dst, const int64_
     src2.resize(kept);
     dst2.resize(kept);
     ts2.resize(kept);
-    if (kept && carry_ends) {
+    if (folded) {
+        // written by the sort
+    } else if (kept && carry_ends) {
         if (keys32)
             hipLaunchKernelGGL((store_from_sorted_kernel<uint32_t>), dim3(grid_for(kept)), dim3(kB),
                                0, s, k32s[which], sorted_ends, del, kept, tmin, src2.p, dst2.p,

@@ -59,6 +59,26 @@ int radix_sort_u32_v64(uint32_t* keys0, uint64_t* vals0, uint32_t* keys1, uint64
 // buffer set (passes % 2) when n > 1.
 int radix_passes(int begin_bit, int end_bit);
 
+// The edge store as the last pass of a sort of (timestamp key, packed
+// endpoints) writes it: src = low half, dst = high half of the value, ts =
+// key + tmin, each at the record's sorted position.
+struct SortedStore {
+    int32_t* src;
+    int32_t* dst;
+    int64_t* ts;
+    int64_t tmin;
+};
+// radix_sort_u32_v64 / radix_sort_u64_v64 whose last digit pass writes `out`
+// instead of the sorted keys and values (no pass of the store over them
+// afterwards).  Returns false, writing nothing, when the sort has no pass
+// (n <= 1 or no key bits): the input is then already in order.
+bool radix_sort_u32_v64_store(uint32_t* keys0, uint64_t* vals0, uint32_t* keys1, uint64_t* vals1,
+                              size_t n, int begin_bit, int end_bit, uint32_t* hist, hipStream_t s,
+                              const SortedStore& out);
+bool radix_sort_u64_v64_store(uint64_t* keys0, uint64_t* vals0, uint64_t* keys1, uint64_t* vals1,
+                              size_t n, int begin_bit, int end_bit, uint32_t* hist, hipStream_t s,
+                              const SortedStore& out);
+
 // ---- reductions ---------------------------------------------------------------
 // out[0], out[1] = min and max of v[0..n); out[2], out[3] = the smallest and
 // the largest of a[i], b[i] (INT64_MAX / INT64_MIN when n == 0); out must hold

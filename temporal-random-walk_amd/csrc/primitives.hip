@@ -2,6 +2,8 @@
 // See primitives.h for the design notes.
 #include "primitives.h"
 
+#include <type_traits>
+
 #include <stdexcept>
 #include <string>
 
@@ -379,11 +381,13 @@ __global__ __launch_bounds__(kBlock) void radix_offsets_kernel(uint32_t* __restr
 // contiguous run instead of one scattered store per key.  Dynamic LDS
 // (radix_scatter_lds): kWaves << db counters, 1 << db running positions,
 // 1 << db output bases, then the tile's staged keys and values.
-template <typename K, typename V>
+// Store: the last pass of an edge-store sort writes the store (st) instead of
+// keys_out / vals_out.
+template <typename K, typename V, bool Store = false>
 __global__ __launch_bounds__(kBlock) void radix_scatter_kernel(
     const K* __restrict__ keys_in, const V* __restrict__ vals_in, K* __restrict__ keys_out,
     V* __restrict__ vals_out, size_t n, int bit, int db, uint32_t dmask,
-    const uint32_t* __restrict__ offsets, size_t nb) {
+    const uint32_t* __restrict__ offsets, size_t nb, SortedStore st = SortedStore{}) {
     extern __shared__ __align__(16) uint32_t s_lds[];
     __shared__ uint32_t s_wave[kWaves];
     const int R = 1 << db;
@@ -464,7 +468,7 @@ __global__ __launch_bounds__(kBlock) void radix_scatter_kernel(
             if (i < n) {
                 const uint32_t lp = s_cnt[wave * R + dig[r]] + rank[r];
                 s_key[lp] = key[r];
-                if (vals_out) s_val[lp] = val[r];
+                if (vals_out || Store) s_val[lp] = val[r];  // the store pass writes no vals_out
             }
         }
         __syncthreads();
@@ -476,8 +480,16 @@ __global__ __launch_bounds__(kBlock) void radix_scatter_kernel(
                 const K k = s_key[lp];
                 const uint32_t d = static_cast<uint32_t>(k >> bit) & dmask;
                 const uint32_t pos = s_base[d] + lp;
-                keys_out[pos] = k;
-                if (vals_out) vals_out[pos] = s_val[lp];
+                if constexpr (Store) {
+                    const uint64_t v = s_val[lp];
+                    st.src[pos] = static_cast<int32_t>(static_cast<uint32_t>(v));
+                    st.dst[pos] = static_cast<int32_t>(static_cast<uint32_t>(v >> 32));
+                    st.ts[pos] = static_cast<int64_t>(static_cast<uint64_t>(k) +
+                                                      static_cast<uint64_t>(st.tmin));
+                } else {
+                    keys_out[pos] = k;
+                    if (vals_out) vals_out[pos] = s_val[lp];
+                }
             }
         }
         __syncthreads();  // s_cnt and the staging are reused by the next tile
@@ -503,7 +515,8 @@ int sort_digit_bits(int bits) {
 
 template <typename K, typename V = uint32_t>
 int radix_sort_impl(K* keys0, V* vals0, K* keys1, V* vals1, size_t n,
-                    int begin_bit, int end_bit, uint32_t* hist, hipStream_t s) {
+                    int begin_bit, int end_bit, uint32_t* hist, hipStream_t s,
+                    const SortedStore* store = nullptr) {
     if (n <= 1 || end_bit <= begin_bit) return 0;
     const size_t nb = (n + kSortSpan - 1) / kSortSpan;
     const int passes = sort_passes(end_bit - begin_bit);
@@ -525,6 +538,15 @@ int radix_sort_impl(K* keys0, V* vals0, K* keys1, V* vals1, size_t n,
                            n, bit, db, dmask, hist, nb);
         hipLaunchKernelGGL(radix_digit_totals_kernel, dim3(R), dim3(kBlock), 0, s, hist, nb, tot);
         hipLaunchKernelGGL(radix_offsets_kernel, dim3(R), dim3(kBlock), 0, s, hist, nb, tot);
+        if constexpr (std::is_same<V, uint64_t>::value) {
+            if (store && pass == passes - 1) {
+                hipLaunchKernelGGL((radix_scatter_kernel<K, V, true>), dim3(nb), dim3(kBlock),
+                                   lds_sc, s, kb[cur], vb[cur], nullptr, nullptr, n, bit, db,
+                                   dmask, hist, nb, *store);
+                check_hip(hipGetLastError(), "radix sort launch");
+                return cur ^ 1;
+            }
+        }
         hipLaunchKernelGGL((radix_scatter_kernel<K, V>), dim3(nb), dim3(kBlock), lds_sc, s,
                            kb[cur], vb[cur], kb[cur ^ 1], vb[cur ^ 1], n, bit, db, dmask, hist,
                            nb);
@@ -708,6 +730,22 @@ int radix_sort_u32_v64(uint32_t* keys0, uint64_t* vals0, uint32_t* keys1, uint64
 }
 int radix_passes(int begin_bit, int end_bit) {
     return end_bit > begin_bit ? sort_passes(end_bit - begin_bit) : 0;
+}
+bool radix_sort_u32_v64_store(uint32_t* keys0, uint64_t* vals0, uint32_t* keys1, uint64_t* vals1,
+                              size_t n, int begin_bit, int end_bit, uint32_t* hist, hipStream_t s,
+                              const SortedStore& out) {
+    if (n <= 1 || end_bit <= begin_bit) return false;
+    radix_sort_impl<uint32_t, uint64_t>(keys0, vals0, keys1, vals1, n, begin_bit, end_bit, hist, s,
+                                        &out);
+    return true;
+}
+bool radix_sort_u64_v64_store(uint64_t* keys0, uint64_t* vals0, uint64_t* keys1, uint64_t* vals1,
+                              size_t n, int begin_bit, int end_bit, uint32_t* hist, hipStream_t s,
+                              const SortedStore& out) {
+    if (n <= 1 || end_bit <= begin_bit) return false;
+    radix_sort_impl<uint64_t, uint64_t>(keys0, vals0, keys1, vals1, n, begin_bit, end_bit, hist, s,
+                                        &out);
+    return true;
 }
 
 // Scratch for the reductions lives in a small per-call static device buffer
