@@ -649,15 +649,24 @@ __global__ void global_guide_kernel(const double* __restrict__ w, size_t n, int 
 }
 
 // The weighted panel: every group's panel record with its end, cumulative
-// weight and first edge record (with its next slice bound).
+// weight and first edge record (with its next slice bound and, for the view's
+// walk direction, that slice's bounding sum).
+// wide (shift 1, forward weights): each record is followed by the start sum
+// of its first entry's next slice (index_layout.h).
 __global__ void wpan_kernel(const PanelRec* __restrict__ pan, const double* __restrict__ w,
-                            const WEdgeRec* __restrict__ wrec, size_t ng,
+                            const WEdgeRec* __restrict__ wrec, size_t ng, int wide,
                             WPanelRec* __restrict__ out) {
     const size_t g = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
     if (g >= ng) return;
     const PanelRec p = pan[g];
     const WEdgeRec r = wrec[p.start];
-    out[g] = WPanelRec{p.rank, p.start, pan[g + 1].start, r.nxt, w[g], EdgeRec{r.nbr, r.eid}};
+    out[g << wide] = WPanelRec{p.rank, p.start, pan[g + 1].start, r.nxt, w[g], EdgeRec{r.nbr, r.eid}};
+    if (wide) {
+        double bs = kNoSum;
+        if (r.nxt != kNoNext)
+            bs = next_bound_first<true>(r.nxt) ? 0.0 : w[next_bound<true>(r.nxt) - 1];
+        *reinterpret_cast<double*>(out + (g << 1) + 1) = bs;
+    }
 }
 
 // The weighted records of a direction (index_layout.h, WEdgeRec): entry k's
@@ -707,7 +716,8 @@ __global__ __launch_bounds__(kB) void entry_bounds_kernel(
             at = b < static_cast<int>(G) && f[b].rank == x;
         }
         const uint64_t gl = static_cast<uint64_t>(h.gb) + static_cast<uint32_t>(b);
-        if (gl <= kNextMax) nxt = static_cast<uint32_t>(gl) | (at ? 0x80000000u : 0u);
+        if (gl <= kNextMax)
+            nxt = static_cast<uint32_t>(gl) | (b == 0 ? kNextFirst : 0u) | (at ? kNextAt : 0u);
     }
     out[k] = WEdgeRec{r.nbr, r.eid, nxt, 0u};
 }
@@ -1474,13 +1484,16 @@ void build_walk_weights(Engine& e, DirIndex& dir, size_t v, const DBuf<double>& 
     hipStream_t s = e.stream;
     const size_t vc = v + 1, g = dir.n_groups;
     ww.hdr.resize(vc);
-    ww.pan.resize(g);
+    // a wide panel (index_layout.h) for forward walks where the ExponentialWeight
+    // weights were asked for
+    ww.shift = e.cfg.enable_weight_computation && decaying ? 1 : 0;
+    ww.pan.resize(g << ww.shift);
     ww.tab.resize(2 * (g + v));
     hipLaunchKernelGGL(whdr_kernel, dim3(grid_for(vc)), dim3(kB), 0, s, w.p, dir.cnt.p, dir.hdr.p,
                        vc, decaying ? 1 : 0, ww.hdr.p);
     if (g)
         hipLaunchKernelGGL(wpan_kernel, dim3(grid_for(g)), dim3(kB), 0, s, dir.pan.p, w.p,
-                           dir.wrec.p, g, ww.pan.p);
+                           dir.wrec.p, g, ww.shift, ww.pan.p);
     fill_weight_guides(e.stream, e.wg_long, w.p, g, dir.key.p, dir.grp.p, dir.cnt.p, ww.hdr.p,
                        nullptr, decaying, ww.tab.p, ww.tab.n);
     check_hip(hipGetLastError(), "walk weights launch");

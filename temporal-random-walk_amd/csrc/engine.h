@@ -178,8 +178,9 @@ struct SampleTarget {
 // the guide tables.
 struct WalkWeights {
     DBuf<WNodeHdr> hdr;   // V_c
-    DBuf<WPanelRec> pan;  // g
+    DBuf<WPanelRec> pan;  // g << shift (wide: every record followed by its sum slot)
     DBuf<uint32_t> tab;   // 2 (g + V_c - 1)
+    int shift = 0;
     void clear() { hdr.n = pan.n = tab.n = 0; }
     size_t bytes() const { return hdr.bytes() + pan.bytes() + tab.bytes(); }
 };

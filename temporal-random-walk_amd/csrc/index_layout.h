@@ -43,9 +43,12 @@
 //   walks: in with w_bwd, or out with w_bwd if undirected)
 //     whdr          WNodeHdr[V_c]  node header + guide parameters and weight
 //                                  total of the node's cumulative weights
-//     wpan          WPanelRec[g]   (ts rank, start, end, the first entry's
+//     wpan          WPanelRec[g << s] (ts rank, start, end, the first entry's
 //                                  next slice bound, cumulative weight, first
-//                                  edge record) of every group
+//                                  edge record) of every group; with the
+//                                  ExponentialWeight weights (s = 1) every
+//                                  record is followed by a 32-byte slot that
+//                                  holds its first entry's bounding sum
 //     wgt           uint32[2(g+V_c)] guide tables of nodes with > kWGuideMin
 //                                  groups, node u's at 2 (gb + u) (below)
 //   global weights  fwd_cum, bwd_cum fp64[T] (+ their guides: one segment)
@@ -201,6 +204,15 @@ struct alignas(32) WPanelRec {
     EdgeRec rec0;  // rec[start]
 };
 static_assert(sizeof(WPanelRec) == 32, "WPanelRec must be 32 bytes");
+// A forward view's panel whose records are followed by a 32-byte slot (wide,
+// shift 1) holds there, as its first double, the start sum of rec0's next
+// slice: c[vb - 1] in the view's cumulative weights c at rec0's neighbour v,
+// vb the bound nxt0 carries (0 when vb is 0); kNoSum where nxt0 holds no
+// bound.  A forward walk that takes rec0 then starts its next weight pick
+// without loading the record before its slice.  Panels are wide only for the
+// ExponentialWeight weights' forward walks (node2vec's retries pay for the
+// larger panel in cache; backward walks keep the build's gather per group).
+constexpr double kNoSum = -1.0;  // the sums are >= 0
 
 // The records of a direction with weights: an entry (u, v, r) -- neighbour v
 // reached at timestamp rank r -- also holds where the walk's next valid slice
@@ -210,8 +222,9 @@ static_assert(sizeof(WPanelRec) == 32, "WPanelRec must be 32 bytes");
 // plus one when v has a group at r itself).  nxt holds v's first group plus b
 // (a global panel index) in bits 0-30 and that "group at r" flag in bit 31,
 // so one record serves both walk directions of an undirected index; kNoNext
-// where the index is too large for 31 bits.  The search it replaces reads a
-// node's bucket table and panel: one random line less per hop at a hub.
+// where the index is too large for 30 bits.  Bit 30 flags b == 0.  The search
+// it replaces reads a node's bucket table and panel: one random line less per
+// hop at a hub.
 struct alignas(16) WEdgeRec {
     int32_t nbr;
     uint32_t eid;
@@ -220,13 +233,21 @@ struct alignas(16) WEdgeRec {
 };
 static_assert(sizeof(WEdgeRec) == 16, "WEdgeRec must be 16 bytes");
 constexpr uint32_t kNoNext = 0xffffffffu;
-constexpr uint32_t kNextMax = 0x7ffffffeu;  // largest global bound nxt holds
+constexpr uint32_t kNextMax = 0x3ffffffeu;  // largest global bound nxt holds
+constexpr uint32_t kNextFirst = 1u << 30;   // nxt: b is 0
+constexpr uint32_t kNextAt = 1u << 31;      // nxt: v has a group at r
 
 // The global bound a walk of direction Fwd reads from nxt (kNoNext: search).
 template <bool Fwd>
 __host__ __device__ inline uint32_t next_bound(uint32_t nxt) {
     if (nxt == kNoNext) return kNoNext;
-    return (nxt & 0x7fffffffu) + (Fwd ? (nxt >> 31) : 0u);
+    return (nxt & (kNextFirst - 1u)) + (Fwd ? (nxt >> 31) : 0u);
+}
+// Whether that bound is v's first group (local index 0): no weight bounds
+// the slice there.
+template <bool Fwd>
+__host__ __device__ inline bool next_bound_first(uint32_t nxt) {
+    return (nxt & kNextFirst) && !(Fwd && (nxt & kNextAt));
 }
 
 typedef uint32_t u32x2_a4 __attribute__((ext_vector_type(2), aligned(4)));
@@ -240,9 +261,9 @@ typedef uint32_t u32x4_a8 __attribute__((ext_vector_type(4), aligned(8)));
 // single-rank bucket holds the answer itself; a wider one gives the bracket
 // [tab[b], tab[b + 1]] (about one group).  The rest is a binary search over
 // at most kTabMin groups.
-template <class Rec>
+template <class Pan>
 __device__ __forceinline__ int first_ge(const uint32_t* tab, const NodeHdr& h, uint32_t u, int G,
-                                        const Rec* f, uint32_t x) {
+                                        const Pan& f, uint32_t x) {
     int lo = 0, hi = G;
     if (G > static_cast<int>(kTabMin)) {
         if (x <= h.r0) return 0;

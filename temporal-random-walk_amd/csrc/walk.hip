@@ -59,7 +59,8 @@ struct DirView {
     // the weight pickers' view of the sampled direction's cumulative weights
     // (read by the weight families' kernels only; nullptr without weights)
     const WNodeHdr* whdr;   // V_c node headers with guide parameters
-    const WPanelRec* wpan;  // g weighted panel records
+    const WPanelRec* wpan;  // g << wshift weighted panel records (WPan)
+    uint32_t wshift;        // 1: a wide panel (a sum slot after every record)
     const uint32_t* wgt;    // guide tables, node u's at 2 (gb + u)
     uint64_t w_size;        // groups with weights (0: none)
 };
@@ -202,15 +203,17 @@ struct Sel {
 };
 
 // Result of a per-node selection: the node reached, the rank of the edge's
-// time and the edge id (-1 for none).
-// A picked edge: the node it reaches, its timestamp rank, its id, and (edges
-// picked over the weighted records) the global bound of the walk's next slice
-// at that node (WEdgeRec::nxt read for the walk's direction; kNoNext: search).
+// time and the edge id (-1 for none), and -- for an edge picked over the
+// weighted records -- the global bound of the walk's next slice at that node
+// (WEdgeRec::nxt read for the walk's direction; kNoNext: search for it) and,
+// for a group's first entry, the weight sum that bounds that slice (kNoSum:
+// load it).
 struct Hop {
     int32_t nbr;
     int32_t r;
     int32_t e;
     uint32_t nx = kNoNext;
+    double bs = kNoSum;
 };
 
 __device__ __forceinline__ Sel no_edge() { return Sel{-1, -1, -1, -1}; }
@@ -221,17 +224,19 @@ __device__ __forceinline__ Hop hop_of(const EdgeRec& rec, uint32_t rank) {
 
 __device__ __forceinline__ EdgeRec load_rec(const EdgeRec* p) { return *p; }
 template <bool Fwd>
-__device__ __forceinline__ Hop whop_of(int32_t nbr, uint32_t eid, uint32_t nxt, uint32_t rank) {
-    return Hop{nbr, static_cast<int32_t>(rank), static_cast<int32_t>(eid), next_bound<Fwd>(nxt)};
+__device__ __forceinline__ Hop whop_of(int32_t nbr, uint32_t eid, uint32_t nxt, uint32_t rank,
+                                       double bs) {
+    return Hop{nbr, static_cast<int32_t>(rank), static_cast<int32_t>(eid), next_bound<Fwd>(nxt),
+               bs};
 }
 // Entry `pick` of the weighted records, or the group's first entry (held in
-// the group's weighted panel record v = {rank, start, end, nxt0} and r0)
+// the group's weighted panel record: v = {rank, start, end, nxt0}, r0, bs0).
 template <bool Fwd>
 __device__ __forceinline__ Hop weighted_entry(const WalkGraph& g, const u32x4_a8& v,
-                                              const EdgeRec& r0, uint32_t pick) {
-    if (pick == v.y) return whop_of<Fwd>(r0.nbr, r0.eid, v.w, v.x);
+                                              const EdgeRec& r0, double bs0, uint32_t pick) {
+    if (pick == v.y) return whop_of<Fwd>(r0.nbr, r0.eid, v.w, v.x, bs0);
     const WEdgeRec wr = g.d.wrec[pick];
-    return whop_of<Fwd>(wr.nbr, wr.eid, wr.nxt, v.x);
+    return whop_of<Fwd>(wr.nbr, wr.eid, wr.nxt, v.x, kNoSum);
 }
 
 // A group's panel record and the next group's start (its end), read as one
@@ -284,6 +289,22 @@ __device__ __forceinline__ uint32_t guided_lower_bound(CAt c, uint32_t G, const 
     return lo;
 }
 
+
+// A node's weighted panel (or the whole one): record i at p[i << sh]; in a
+// wide panel (sh = 1) the slot after each record holds its first entry's
+// bounding sum (index_layout.h).
+struct WPan {
+    const WPanelRec* p;
+    uint32_t sh;
+    __device__ __forceinline__ const WPanelRec& operator[](uint32_t i) const {
+        return p[static_cast<size_t>(i) << sh];
+    }
+    __device__ __forceinline__ double bs0(uint32_t i) const {
+        return sh ? *reinterpret_cast<const double*>(p + (static_cast<size_t>(i) << 1) + 1)
+                  : kNoSum;
+    }
+};
+
 // pick_exponential_weights (random/pickers.cuh:84-126) over the slice
 // [vb, ve) of a node's groups (local indexes; f is the node's weighted
 // panel), with the slice's sums loaded: the lower_bound over the node's whole
@@ -293,13 +314,13 @@ __device__ __forceinline__ uint32_t guided_lower_bound(CAt c, uint32_t G, const 
 // Forward weights saturate at their final sum over the late part of a node's
 // span, where start_sum == end_sum makes that the common case.
 template <bool Fwd>
-__device__ __forceinline__ uint32_t node_weight_pick(const WPanelRec* f, uint32_t G,
+__device__ __forceinline__ uint32_t node_weight_pick(const WPan& f, uint32_t G,
                                                      const uint32_t* gt, const WGuide& gd,
                                                      uint32_t vb, uint32_t ve, double r,
                                                      double start_sum, double end_sum) {
     const double target = start_sum + r * (end_sum - start_sum);
     if (target <= start_sum) return vb;
-    const uint32_t x = guided_lower_bound<Fwd>([f](uint32_t i) { return f[i].c; }, G, gt, gd, target);
+    const uint32_t x = guided_lower_bound<Fwd>([&f](uint32_t i) { return f[i].c; }, G, gt, gd, target);
     return x < vb ? vb : (x > ve ? ve : x);
 }
 
@@ -380,14 +401,15 @@ __device__ __forceinline__ bool adjacent(const WalkGraph& g, int prev, int cand)
 // takes it.  The group's record holds its first edge record, so a pick of
 // entry 0 (every pick in a group of one edge) loads no record.
 template <bool Fwd>
-__device__ __forceinline__ Hop weighted_group_hop(const WalkGraph& g, const WPanelRec* f,
-                                                  uint32_t x, double re) {
-    const u32x4_a8 v = *reinterpret_cast<const u32x4_a8*>(f + x);  // rank, start, end, nxt0
+__device__ __forceinline__ Hop weighted_group_hop(const WalkGraph& g, const WPan& f, uint32_t x,
+                                                  double re) {
+    const u32x4_a8 v = *reinterpret_cast<const u32x4_a8*>(&f[x]);  // rank, start, end, nxt0
     const uint32_t es = v.y, ee = v.z;
     const EdgeRec r0 = f[x].rec0;
+    const double bs0 = f.bs0(x);
     if (es >= ee || es >= g.d.idx_size || ee > g.d.idx_size) return no_hop();
     const uint32_t k = static_cast<uint32_t>(static_cast<int>(re * static_cast<int>(ee - es)));
-    return weighted_entry<Fwd>(g, v, r0, es + k);
+    return weighted_entry<Fwd>(g, v, r0, bs0, es + k);
 }
 
 // graph/temporal_node2vec_helpers.cuh:127-199 over the slice [vb, ve) of a
@@ -395,7 +417,7 @@ __device__ __forceinline__ Hop weighted_group_hop(const WalkGraph& g, const WPan
 // table), with the slice's sums loaded.  The candidate node of a proposal is
 // its record's neighbour (get_candidate_node, walk_step_helpers.cuh:40-54).
 template <bool Fwd>
-__device__ Hop tn2v_pick(const WalkGraph& g, int prev, const WPanelRec* f, uint32_t G,
+__device__ Hop tn2v_pick(const WalkGraph& g, int prev, const WPan& f, uint32_t G,
                          const uint32_t* gt, const WGuide& gd, uint32_t vb, uint32_t ve,
                          double start_sum, double end_sum, double rg, double re) {
     if (vb >= ve || prev == -1) return no_hop();
@@ -418,6 +440,7 @@ __device__ Hop tn2v_pick(const WalkGraph& g, int prev, const WPanelRec* f, uint3
     uint32_t gx = ~0u;
     u32x4_a8 gv{0u, 0u, 0u, 0u};  // the group's rank, start, end, nxt0
     EdgeRec g_r0{0, 0};
+    double g_bs0 = 0.0;
     Hop e_hop = no_hop();
     uint32_t e_pick = ~0u;
     int adj_cand = -1;
@@ -431,8 +454,9 @@ __device__ Hop tn2v_pick(const WalkGraph& g, int prev, const WPanelRec* f, uint3
         // reference (get_node_group_edge_end, walk_step_helpers.cuh:19-38)
         if (x >= G) continue;
         if (x != gx) {
-            gv = *reinterpret_cast<const u32x4_a8*>(f + x);
+            gv = *reinterpret_cast<const u32x4_a8*>(&f[x]);
             g_r0 = f[x].rec0;
+            g_bs0 = f.bs0(x);
             gx = x;
         }
         const uint32_t g_es = gv.y, g_ee = gv.z;
@@ -442,7 +466,7 @@ __device__ Hop tn2v_pick(const WalkGraph& g, int prev, const WPanelRec* f, uint3
         const uint32_t pick =
             g_es + static_cast<uint32_t>(local < g_ee - g_es ? local : g_ee - g_es - 1);
         if (pick != e_pick) {
-            e_hop = weighted_entry<Fwd>(g, gv, g_r0, pick);
+            e_hop = weighted_entry<Fwd>(g, gv, g_r0, g_bs0, pick);
             e_pick = pick;
         }
         last = e_hop;
@@ -481,7 +505,7 @@ __device__ Hop tn2v_pick(const WalkGraph& g, int prev, const WPanelRec* f, uint3
 
 // What any lane needs to evaluate any retry of one hop (tn2v_pick's state).
 struct Tn2vHop {
-    const WPanelRec* f;  // the node's weighted panel
+    const WPanelRec* f;  // the node's weighted panel (WPan's p)
     const uint32_t* gt;  // its guide table
     WGuide gd;
     uint32_t G, vb, ve;
@@ -505,15 +529,16 @@ __device__ __forceinline__ int tn2v_try(const WalkGraph& g, const Tn2vHop& s, in
     const double gr = derive_uniform(s.rg, s.re, retry * 3 + 0);
     const double er = derive_uniform(s.rg, s.re, retry * 3 + 1);
     const double ar = derive_uniform(s.rg, s.re, retry * 3 + 2);
-    const uint32_t x = node_weight_pick<Fwd>(s.f, s.G, s.gt, s.gd, s.vb, s.ve, gr, s.start_sum,
+    const WPan f{s.f, g.d.wshift};
+    const uint32_t x = node_weight_pick<Fwd>(f, s.G, s.gt, s.gd, s.vb, s.ve, gr, s.start_sum,
                                              s.end_sum);
     if (x >= s.G) return 0;
-    const u32x4_a8 v = *reinterpret_cast<const u32x4_a8*>(s.f + x);  // rank, start, end, nxt0
+    const u32x4_a8 v = *reinterpret_cast<const u32x4_a8*>(&f[x]);  // rank, start, end, nxt0
     const uint32_t es = v.y, ee = v.z;
     if (es >= ee || es >= g.d.idx_size || ee > g.d.idx_size) return 0;
     const uint64_t local = static_cast<uint64_t>(er * static_cast<double>(ee - es));
     const uint32_t pick = es + static_cast<uint32_t>(local < ee - es ? local : ee - es - 1);
-    out = weighted_entry<Fwd>(g, v, s.f[x].rec0, pick);
+    out = weighted_entry<Fwd>(g, v, f[x].rec0, f.bs0(x), pick);
     const int cand = out.nbr;
     bool accept;
     if (cand == s.prev) accept = ar < g.inv_p * inv_bmax;
@@ -550,7 +575,7 @@ __device__ __forceinline__ Tn2vHop lane_read(const Tn2vHop& s, int src) {
 }
 __device__ __forceinline__ Hop lane_read(const Hop& h, int src) {
     return Hop{lane_read(h.nbr, src), lane_read(h.r, src), lane_read(h.e, src),
-               lane_read(h.nx, src)};
+               lane_read(h.nx, src), lane_read(h.bs, src)};
 }
 
 // The hops of the lanes with `want` (state s) decided by the whole wave (see
@@ -651,9 +676,9 @@ __device__ __forceinline__ Hop hop_from_group(const WalkGraph& g, uint32_t gpos,
 // groups_by_timestamp_slice (edge_selectors.cuh:66-120) and the cutoff.  nl:
 // the time bound carried from the edge that reached u (the same lower_bound,
 // local), searched for when it is not in [0, G].
-template <bool Fwd, class Rec>
+template <bool Fwd, class Pan>
 __device__ __forceinline__ void valid_slice(const uint32_t* tab, const NodeHdr& h, uint32_t u,
-                                            int G, const Rec* f, int32_t t, int32_t cut, int& vb,
+                                            int G, const Pan& f, int32_t t, int32_t cut, int& vb,
                                             int& ve, uint32_t nl = kNoNext) {
     vb = 0;
     ve = G;
@@ -703,17 +728,22 @@ template <bool Fwd, int Fam>
 __device__ __forceinline__ Hop wnode_edge_from(const WalkGraph& g, int picker, uint32_t u, bool ok,
                                                const WNodeHdr& wh, int32_t t, int32_t cut,
                                                int prev, double rg, double re,
-                                               const double* em1, uint32_t nx) {
+                                               const double* em1, uint32_t nx, double bs) {
     const NodeHdr& h = wh.h;
     uint32_t Gu = ok ? (h.meta & kHdrGMask) : 0u;
     if (Gu == kHdrGMask) Gu = g.d.whdr[u + 1].h.gb - h.gb;
     if (Gu == 0) return no_hop();
     const uint32_t gb = h.gb;
     const int G = static_cast<int>(Gu);
-    const WPanelRec* f = g.d.wpan + gb;
+    const WPan f{g.d.wpan + (static_cast<size_t>(gb) << g.d.wshift), g.d.wshift};
     int vb, ve;
-    valid_slice<Fwd>(g.d.tab, h, u, G, f, t, cut, vb, ve, nx - gb);
+    const uint32_t nl = nx - gb;
+    valid_slice<Fwd>(g.d.tab, h, u, G, f, t, cut, vb, ve, nl);
     if (vb >= ve) return no_hop();
+    // the slice bound carried from the edge that reached u, and with it (in
+    // the ExponentialWeight family's forward kernels, where the build wrote
+    // one) the start sum of the slice there (bs)
+    const bool csum = Fwd && Fam == kFamWeight && t != -1 && nl <= Gu && !(bs < 0.0);
     uint32_t x;
     if (is_index_picker(picker)) {
         const int avail = ve - vb;
@@ -726,7 +756,7 @@ __device__ __forceinline__ Hop wnode_edge_from(const WalkGraph& g, int picker, u
         if (gb + Gu > g.d.w_size) return no_hop();
         const uint32_t* gt = g.d.wgt + hdr_tab_base(h, u);
         // the slice's sums: the cumulative weight before vb and at ve - 1
-        const double start_sum = vb > 0 ? f[vb - 1].c : 0.0;
+        const double start_sum = !(vb > 0) ? 0.0 : csum ? bs : f[vb - 1].c;
         const double end_sum = ve == G ? wh.g.total : f[ve - 1].c;
         if (Fam != kFamWeight && picker == kTemporalNode2Vec && prev != -1)
             return tn2v_pick<Fwd>(g, prev, f, Gu, gt, wh.g, vb, ve, start_sum, end_sum, rg, re);
@@ -751,22 +781,24 @@ __device__ __forceinline__ Hop wnode_edge_from_wave(const WalkGraph& g, int pick
                                                     Tn2vHop& s) {
     want = false;
     if (picker != kTemporalNode2Vec || prev == -1)
-        return wnode_edge_from<Fwd, kFamAny>(g, picker, u, ok, wh, t, cut, prev, rg, re, em1, nx);
+        return wnode_edge_from<Fwd, kFamAny>(g, picker, u, ok, wh, t, cut, prev, rg, re, em1, nx,
+                                             kNoSum);
     const NodeHdr& h = wh.h;
     uint32_t Gu = ok ? (h.meta & kHdrGMask) : 0u;
     if (Gu == kHdrGMask) Gu = g.d.whdr[u + 1].h.gb - h.gb;
     if (Gu == 0) return no_hop();
     const uint32_t gb = h.gb;
     const int G = static_cast<int>(Gu);
-    const WPanelRec* f = g.d.wpan + gb;
+    const WPan f{g.d.wpan + (static_cast<size_t>(gb) << g.d.wshift), g.d.wshift};
     int vb, ve;
-    valid_slice<Fwd>(g.d.tab, h, u, G, f, t, cut, vb, ve, nx - gb);
+    const uint32_t nl = nx - gb;
+    valid_slice<Fwd>(g.d.tab, h, u, G, f, t, cut, vb, ve, nl);
     if (vb >= ve) return no_hop();
     if (gb + Gu > g.d.w_size) return no_hop();
     const double start_sum = vb > 0 ? f[vb - 1].c : 0.0;
     const double end_sum = ve == G ? wh.g.total : f[ve - 1].c;
     if (end_sum < start_sum) return no_hop();
-    s = Tn2vHop{f, g.d.wgt + hdr_tab_base(h, u), wh.g, Gu, static_cast<uint32_t>(vb),
+    s = Tn2vHop{f.p, g.d.wgt + hdr_tab_base(h, u), wh.g, Gu, static_cast<uint32_t>(vb),
                 static_cast<uint32_t>(ve), prev, start_sum, end_sum, rg, re};
     want = true;
     return no_hop();
@@ -795,9 +827,9 @@ template <bool Fwd, int Fam>
 __device__ __forceinline__ Hop hop_at(const WalkGraph& g, int picker, uint32_t u, bool ok,
                                       const HopHdr<Fam>& hh, int32_t t, int32_t cut, int prev,
                                       double rg, double re, const double* em1,
-                                      uint32_t nx = kNoNext) {
+                                      uint32_t nx = kNoNext, double bs = kNoSum) {
     if constexpr (Fam == kFamIndex) return node_edge_from<Fwd>(g, picker, u, ok, hh, t, cut, rg, re, em1);
-    else return wnode_edge_from<Fwd, Fam>(g, picker, u, ok, hh, t, cut, prev, rg, re, em1, nx);
+    else return wnode_edge_from<Fwd, Fam>(g, picker, u, ok, hh, t, cut, prev, rg, re, em1, nx, bs);
 }
 
 template <bool Fwd, int Fam>
@@ -941,6 +973,7 @@ __global__ __launch_bounds__(kB) __attribute__((amdgpu_waves_per_eu(Fam == kFamI
     int cur = s0.cur;
     int32_t cur_r = s0.r, cur_e = s0.e;
     uint32_t cur_nx = kNoNext;  // the next slice's bound carried by the last edge
+    double cur_bs = kNoSum;     // and its bounding sum
     int len = 0;
     if (cur_e != -1) {
         int prev = -1;
@@ -968,7 +1001,7 @@ __global__ __launch_bounds__(kB) __attribute__((amdgpu_waves_per_eu(Fam == kFamI
             if (a.ds.replay) r = replay_pair(a.ds, w, p);
             const Hop h = hop_at<Fwd, Fam>(g, a.walk_bias, u, ok, hd,
                                                    cur_r == neg1 ? -1 : cur_r, cut, prev, r.a,
-                                                   r.b, em1, cur_nx);
+                                                   r.b, em1, cur_nx, cur_bs);
             // the reference's failure test is ts == -1: no edge, or an edge at -1
             if (h.e == -1 || h.r == neg1) break;
             prev = cur;
@@ -976,6 +1009,7 @@ __global__ __launch_bounds__(kB) __attribute__((amdgpu_waves_per_eu(Fam == kFamI
             cur_r = h.r;
             cur_e = h.e;
             cur_nx = h.nx;
+            cur_bs = h.bs;
             ++walk_len;
         }
     }
@@ -1199,6 +1233,7 @@ __global__ __launch_bounds__(kB) __attribute__((amdgpu_waves_per_eu(4))) void wa
     int cur = s0.cur, prev = -1;
     int32_t cur_r = s0.r, cur_e = s0.e;
     uint32_t cur_nx = kNoNext;  // the next slice's bound carried by the last edge
+    double cur_bs = kNoSum;     // and its bounding sum
     bool alive = live && s0.e != -1;  // the walk writes its next slot
     int len = 0;
     const int nb = a.pk_nb, rb = a.pk_rb;
@@ -1253,6 +1288,7 @@ __global__ __launch_bounds__(kB) __attribute__((amdgpu_waves_per_eu(4))) void wa
                         cur_r = h.r;
                         cur_e = h.e;
                         cur_nx = h.nx;
+                        cur_bs = h.bs;
                         alive = cur != a.pad;
                     }
                 }
@@ -1286,7 +1322,7 @@ __global__ __launch_bounds__(kB) __attribute__((amdgpu_waves_per_eu(4))) void wa
                     if (a.ds.replay) r = replay_pair(a.ds, w, p);
                     const Hop h = hop_at<Fwd, Fam>(g, a.walk_bias, u, ok, hd,
                                                            cur_r == neg1 ? -1 : cur_r, cut, prev,
-                                                           r.a, r.b, em1, cur_nx);
+                                                           r.a, r.b, em1, cur_nx, cur_bs);
                     if (h.e == -1 || h.r == neg1) {
                         alive = false;
                     } else {
@@ -1295,6 +1331,7 @@ __global__ __launch_bounds__(kB) __attribute__((amdgpu_waves_per_eu(4))) void wa
                         cur_r = h.r;
                         cur_e = h.e;
                         cur_nx = h.nx;
+                        cur_bs = h.bs;
                         alive = cur != a.pad;
                     }
                 }
@@ -2148,11 +2185,12 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
     g.d.idx_size = static_cast<uint32_t>(d.n_entries);
     // the weight pickers' view of the sampled direction's per-node weights
     const WalkWeights& ww = forward ? out.wf : d.wb;
-    const bool wview = weights_ready && ww.hdr.n == d.hdr.n && ww.pan.n == d.n_groups &&
-                       d.wrec.n == d.n_entries;
+    const bool wview = weights_ready && ww.hdr.n == d.hdr.n &&
+                       ww.pan.n == (d.n_groups << ww.shift) && d.wrec.n == d.n_entries;
     g.d.wrec = wview ? d.wrec.p : nullptr;
     g.d.whdr = wview ? ww.hdr.p : nullptr;
     g.d.wpan = wview ? ww.pan.p : nullptr;
+    g.d.wshift = wview ? static_cast<uint32_t>(ww.shift) : 0u;
     g.d.wgt = wview ? ww.tab.p : nullptr;
     g.d.w_size = wview ? d.n_groups : 0;
     g.adj_off = adj_lists_ready ? adj_off.p : nullptr;
