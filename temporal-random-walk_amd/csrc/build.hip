@@ -651,22 +651,33 @@ __global__ void global_guide_kernel(const double* __restrict__ w, size_t n, int 
 // The weighted panel: every group's panel record with its end, cumulative
 // weight and first edge record (with its next slice bound and, for the view's
 // walk direction, that slice's bounding sum).
-// wide (shift 1, forward weights): each record is followed by the start sum
-// of its first entry's next slice (index_layout.h).
+// rsh: the records' shift (1: each followed by its forward start sum).
+// wide (shift 1, forward weights, over such records): each panel record is
+// followed by the start sum of its first entry's next slice (index_layout.h),
+// copied from that entry's record.
 __global__ void wpan_kernel(const PanelRec* __restrict__ pan, const double* __restrict__ w,
-                            const WEdgeRec* __restrict__ wrec, size_t ng, int wide,
+                            const WEdgeRec* __restrict__ wrec, int rsh, size_t ng, int wide,
                             WPanelRec* __restrict__ out) {
     const size_t g = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
     if (g >= ng) return;
     const PanelRec p = pan[g];
-    const WEdgeRec r = wrec[p.start];
+    const WEdgeRec* rp = wrec + (static_cast<size_t>(p.start) << rsh);
+    const WEdgeRec r = *rp;
     out[g << wide] = WPanelRec{p.rank, p.start, pan[g + 1].start, r.nxt, w[g], EdgeRec{r.nbr, r.eid}};
-    if (wide) {
-        double bs = kNoSum;
-        if (r.nxt != kNoNext)
-            bs = next_bound_first<true>(r.nxt) ? 0.0 : w[next_bound<true>(r.nxt) - 1];
-        *reinterpret_cast<double*>(out + (g << 1) + 1) = bs;
-    }
+    if (wide)
+        *reinterpret_cast<double*>(out + (g << 1) + 1) = *reinterpret_cast<const double*>(rp + 1);
+}
+
+// The forward start sums of the out direction's wide records (index_layout.h):
+// each entry's next slice's c[vb - 1] in the forward weights w.
+__global__ void entry_sums_kernel(WEdgeRec* __restrict__ wrec, const double* __restrict__ w,
+                                  size_t n) {
+    const size_t k = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
+    if (k >= n) return;
+    const uint32_t nxt = wrec[k << 1].nxt;
+    double bs = kNoSum;
+    if (nxt != kNoNext) bs = next_bound_first<true>(nxt) ? 0.0 : w[next_bound<true>(nxt) - 1];
+    *reinterpret_cast<double*>(wrec + (k << 1) + 1) = bs;
 }
 
 // The weighted records of a direction (index_layout.h, WEdgeRec): entry k's
@@ -677,7 +688,7 @@ __global__ void wpan_kernel(const PanelRec* __restrict__ pan, const double* __re
 __global__ __launch_bounds__(kB) void entry_bounds_kernel(
     const EdgeRec* __restrict__ rec, const uint32_t* __restrict__ rank,
     const NodeHdr* __restrict__ hdr, const uint32_t* __restrict__ tab,
-    const PanelRec* __restrict__ pan, size_t n, size_t vc, WEdgeRec* __restrict__ out) {
+    const PanelRec* __restrict__ pan, size_t n, size_t vc, int sh, WEdgeRec* __restrict__ out) {
     const size_t k = blockIdx.x * static_cast<size_t>(kB) + threadIdx.x;
     if (k >= n) return;
     const EdgeRec r = rec[k];
@@ -719,7 +730,7 @@ __global__ __launch_bounds__(kB) void entry_bounds_kernel(
         if (gl <= kNextMax)
             nxt = static_cast<uint32_t>(gl) | (b == 0 ? kNextFirst : 0u) | (at ? kNextAt : 0u);
     }
-    out[k] = WEdgeRec{r.nbr, r.eid, nxt, 0u};
+    out[k << sh] = WEdgeRec{r.nbr, r.eid, nxt, 0u};
 }
 
 // The buckets [from, to] of group g (local index i of a segment of G): those
@@ -1400,10 +1411,13 @@ void finish_direction(Engine& e, DirIndex& dir, size_t n, size_t vc, int64_t* ho
                            dir.grp.p, dir.hdr.p, dir.pan.p, static_cast<size_t>(g), dir.tab.p);
     // the weight pickers' records: every entry's next slice bound, searched
     // once here instead of at every hop that takes the entry
-    dir.wrec.resize(weights ? n : 0);
+    // wide in the out direction when the ExponentialWeight weights were asked for
+    dir.wrec_shift = weights && e.cfg.enable_weight_computation && &dir == &e.out ? 1 : 0;
+    dir.wrec.resize(weights ? n << dir.wrec_shift : 0);
     if (weights && n)
         hipLaunchKernelGGL(entry_bounds_kernel, dim3(grid_for(n)), dim3(kB), 0, s, dir.rec.p,
-                           e.v32a.p, dir.hdr.p, dir.tab.p, dir.pan.p, n, vc, dir.wrec.p);
+                           e.v32a.p, dir.hdr.p, dir.tab.p, dir.pan.p, n, vc, dir.wrec_shift,
+                           dir.wrec.p);
     check_hip(hipGetLastError(), "direction index launch");
 }
 
@@ -1485,15 +1499,19 @@ void build_walk_weights(Engine& e, DirIndex& dir, size_t v, const DBuf<double>& 
     const size_t vc = v + 1, g = dir.n_groups;
     ww.hdr.resize(vc);
     // a wide panel (index_layout.h) for forward walks where the ExponentialWeight
-    // weights were asked for
-    ww.shift = e.cfg.enable_weight_computation && decaying ? 1 : 0;
+    // weights were asked for, over the out direction's wide records
+    ww.shift = dir.wrec_shift && decaying ? 1 : 0;
     ww.pan.resize(g << ww.shift);
     ww.tab.resize(2 * (g + v));
     hipLaunchKernelGGL(whdr_kernel, dim3(grid_for(vc)), dim3(kB), 0, s, w.p, dir.cnt.p, dir.hdr.p,
                        vc, decaying ? 1 : 0, ww.hdr.p);
+    // the records' start sums first: the wide panel copies its first entries'
+    const size_t n = dir.wrec.n >> dir.wrec_shift;
+    if (ww.shift && n)
+        hipLaunchKernelGGL(entry_sums_kernel, dim3(grid_for(n)), dim3(kB), 0, s, dir.wrec.p, w.p, n);
     if (g)
         hipLaunchKernelGGL(wpan_kernel, dim3(grid_for(g)), dim3(kB), 0, s, dir.pan.p, w.p,
-                           dir.wrec.p, g, ww.shift, ww.pan.p);
+                           dir.wrec.p, dir.wrec_shift, g, ww.shift, ww.pan.p);
     fill_weight_guides(e.stream, e.wg_long, w.p, g, dir.key.p, dir.grp.p, dir.cnt.p, ww.hdr.p,
                        nullptr, decaying, ww.tab.p, ww.tab.n);
     check_hip(hipGetLastError(), "walk weights launch");

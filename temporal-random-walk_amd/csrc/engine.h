@@ -198,7 +198,8 @@ struct DirIndex {
     DBuf<uint32_t> tab;      // bucket tables
     DBuf<double> w_fwd;      // g (outbound only)
     DBuf<double> w_bwd;      // g
-    DBuf<WEdgeRec> wrec;     // n entries with next slice bounds (weights only)
+    DBuf<WEdgeRec> wrec;     // n << wrec_shift: entries with next slice bounds (weights only)
+    int wrec_shift = 0;      // 1: each record followed by its forward start sum
     // weight pickers' views: of w_fwd for forward walks (out), of w_bwd for
     // backward walks (in; out if undirected)
     WalkWeights wf, wb;

@@ -36,9 +36,13 @@
 //                                  picked group's range usually shares the
 //                                  line of the search's last probe
 //     w_fwd, w_bwd  fp64[g]        per-node cumulative exponential weights
-//     wrec          WEdgeRec[n]    (neighbour, edge id, the walk's next slice
-//                                  bound at the neighbour) in idx order;
-//                                  built with the weights (below)
+//     wrec          WEdgeRec[n << s] (neighbour, edge id, the walk's next
+//                                  slice bound at the neighbour) in idx
+//                                  order, built with the weights (below); in
+//                                  the out direction with the ExponentialWeight
+//                                  weights (s = 1) every record is followed by
+//                                  a 16-byte slot: the forward start sum of
+//                                  its next slice
 //   per walk direction with weights (forward walks: out with w_fwd; backward
 //   walks: in with w_bwd, or out with w_bwd if undirected)
 //     whdr          WNodeHdr[V_c]  node header + guide parameters and weight
@@ -209,9 +213,12 @@ static_assert(sizeof(WPanelRec) == 32, "WPanelRec must be 32 bytes");
 // slice: c[vb - 1] in the view's cumulative weights c at rec0's neighbour v,
 // vb the bound nxt0 carries (0 when vb is 0); kNoSum where nxt0 holds no
 // bound.  A forward walk that takes rec0 then starts its next weight pick
-// without loading the record before its slice.  Panels are wide only for the
-// ExponentialWeight weights' forward walks (node2vec's retries pay for the
-// larger panel in cache; backward walks keep the build's gather per group).
+// without loading the record before its slice.  The forward view's edge
+// records (WEdgeRec, the out direction's) are wide alike, a 16-byte slot after
+// each holding the same start sum for that entry.  Panels and records are
+// wide only for the ExponentialWeight weights' forward walks (node2vec's
+// retries pay for the larger arrays in cache; backward walks keep the build's
+// gathers).
 constexpr double kNoSum = -1.0;  // the sums are >= 0
 
 // The records of a direction with weights: an entry (u, v, r) -- neighbour v

@@ -54,8 +54,10 @@ struct DirView {
     const PanelRec* pan;  // g + 1 group records (terminator)
     const EdgeRec* rec;   // walk-order edge records
     uint32_t idx_size;
-    // the same records with the walk's next slice bounds (weights only)
+    // the same records with the walk's next slice bounds (weights only);
+    // wrshift 1: each followed by its forward start sum
     const WEdgeRec* wrec;
+    uint32_t wrshift;
     // the weight pickers' view of the sampled direction's cumulative weights
     // (read by the weight families' kernels only; nullptr without weights)
     const WNodeHdr* whdr;   // V_c node headers with guide parameters
@@ -235,8 +237,10 @@ template <bool Fwd>
 __device__ __forceinline__ Hop weighted_entry(const WalkGraph& g, const u32x4_a8& v,
                                               const EdgeRec& r0, double bs0, uint32_t pick) {
     if (pick == v.y) return whop_of<Fwd>(r0.nbr, r0.eid, v.w, v.x, bs0);
-    const WEdgeRec wr = g.d.wrec[pick];
-    return whop_of<Fwd>(wr.nbr, wr.eid, wr.nxt, v.x, kNoSum);
+    const WEdgeRec* p = g.d.wrec + (static_cast<size_t>(pick) << g.d.wrshift);
+    const WEdgeRec wr = *p;
+    const double bs = g.d.wrshift ? *reinterpret_cast<const double*>(p + 1) : kNoSum;
+    return whop_of<Fwd>(wr.nbr, wr.eid, wr.nxt, v.x, bs);
 }
 
 // A group's panel record and the next group's start (its end), read as one
@@ -2186,8 +2190,10 @@ void Engine::sample(const trw_sample_params& p, const SampleTarget* into) {
     // the weight pickers' view of the sampled direction's per-node weights
     const WalkWeights& ww = forward ? out.wf : d.wb;
     const bool wview = weights_ready && ww.hdr.n == d.hdr.n &&
-                       ww.pan.n == (d.n_groups << ww.shift) && d.wrec.n == d.n_entries;
+                       ww.pan.n == (d.n_groups << ww.shift) &&
+                       d.wrec.n == (d.n_entries << d.wrec_shift);
     g.d.wrec = wview ? d.wrec.p : nullptr;
+    g.d.wrshift = wview ? static_cast<uint32_t>(d.wrec_shift) : 0u;
     g.d.whdr = wview ? ww.hdr.p : nullptr;
     g.d.wpan = wview ? ww.pan.p : nullptr;
     g.d.wshift = wview ? static_cast<uint32_t>(ww.shift) : 0u;
