@@ -653,8 +653,9 @@ __global__ void global_guide_kernel(const double* __restrict__ w, size_t n, int 
 // walk direction, that slice's bounding sum).
 // rsh: the records' shift (1: each followed by its forward start sum).
 // wide (shift 1, forward weights, over such records): each panel record is
-// followed by the start sum of its first entry's next slice (index_layout.h),
-// copied from that entry's record.
+// followed by its slot (index_layout.h, WPanelSlot): the start sum of its first
+// entry's next slice, copied from that entry's record, and the group's second
+// entry.
 __global__ void wpan_kernel(const PanelRec* __restrict__ pan, const double* __restrict__ w,
                             const WEdgeRec* __restrict__ wrec, int rsh, size_t ng, int wide,
                             WPanelRec* __restrict__ out) {
@@ -663,9 +664,18 @@ __global__ void wpan_kernel(const PanelRec* __restrict__ pan, const double* __re
     const PanelRec p = pan[g];
     const WEdgeRec* rp = wrec + (static_cast<size_t>(p.start) << rsh);
     const WEdgeRec r = *rp;
-    out[g << wide] = WPanelRec{p.rank, p.start, pan[g + 1].start, r.nxt, w[g], EdgeRec{r.nbr, r.eid}};
-    if (wide)
-        *reinterpret_cast<double*>(out + (g << 1) + 1) = *reinterpret_cast<const double*>(rp + 1);
+    const uint32_t end = pan[g + 1].start;
+    out[g << wide] = WPanelRec{p.rank, p.start, end, r.nxt, w[g], EdgeRec{r.nbr, r.eid}};
+    if (wide) {
+        WPanelSlot sl{*reinterpret_cast<const double*>(rp + 1), EdgeRec{0, 0}, kNoNext, 0u, kNoSum};
+        if (end - p.start >= 2) {
+            const WEdgeRec r1 = rp[2];  // entry start + 1 and its sum
+            sl.rec1 = EdgeRec{r1.nbr, r1.eid};
+            sl.nxt1 = r1.nxt;
+            sl.bs1 = *reinterpret_cast<const double*>(rp + 3);
+        }
+        *reinterpret_cast<WPanelSlot*>(out + (g << 1) + 1) = sl;
+    }
 }
 
 // The forward start sums of the out direction's wide records (index_layout.h):

@@ -213,12 +213,23 @@ static_assert(sizeof(WPanelRec) == 32, "WPanelRec must be 32 bytes");
 // slice: c[vb - 1] in the view's cumulative weights c at rec0's neighbour v,
 // vb the bound nxt0 carries (0 when vb is 0); kNoSum where nxt0 holds no
 // bound.  A forward walk that takes rec0 then starts its next weight pick
-// without loading the record before its slice.  The forward view's edge
+// without loading the record before its slice.  The rest of the slot holds the
+// group's second entry (its record, next slice bound and start sum; rec1 =
+// {0, 0}, bs1 = kNoSum for a group of one entry), so a pick of either of a
+// group's first two entries reads no edge record.  The forward view's edge
 // records (WEdgeRec, the out direction's) are wide alike, a 16-byte slot after
 // each holding the same start sum for that entry.  Panels and records are
 // wide only for the ExponentialWeight weights' forward walks (node2vec's
 // retries pay for the larger arrays in cache; backward walks keep the build's
 // gathers).
+struct alignas(32) WPanelSlot {
+    double bs0;
+    EdgeRec rec1;  // rec[start + 1]
+    uint32_t nxt1;
+    uint32_t pad;
+    double bs1;
+};
+static_assert(sizeof(WPanelSlot) == 32, "WPanelSlot must be 32 bytes");
 constexpr double kNoSum = -1.0;  // the sums are >= 0
 
 // The records of a direction with weights: an entry (u, v, r) -- neighbour v

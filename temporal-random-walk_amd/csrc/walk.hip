@@ -232,11 +232,14 @@ __device__ __forceinline__ Hop whop_of(int32_t nbr, uint32_t eid, uint32_t nxt, 
                bs};
 }
 // Entry `pick` of the weighted records, or the group's first entry (held in
-// the group's weighted panel record: v = {rank, start, end, nxt0}, r0, bs0).
+// the group's weighted panel record: v = {rank, start, end, nxt0}, r0, bs0) or
+// second (in a wide panel's slot sl; nullptr for a narrow panel).
 template <bool Fwd>
 __device__ __forceinline__ Hop weighted_entry(const WalkGraph& g, const u32x4_a8& v,
-                                              const EdgeRec& r0, double bs0, uint32_t pick) {
+                                              const EdgeRec& r0, double bs0,
+                                              const WPanelSlot* sl, uint32_t pick) {
     if (pick == v.y) return whop_of<Fwd>(r0.nbr, r0.eid, v.w, v.x, bs0);
+    if (sl && pick == v.y + 1) return whop_of<Fwd>(sl->rec1.nbr, sl->rec1.eid, sl->nxt1, v.x, sl->bs1);
     const WEdgeRec* p = g.d.wrec + (static_cast<size_t>(pick) << g.d.wrshift);
     const WEdgeRec wr = *p;
     const double bs = g.d.wrshift ? *reinterpret_cast<const double*>(p + 1) : kNoSum;
@@ -296,17 +299,18 @@ __device__ __forceinline__ uint32_t guided_lower_bound(CAt c, uint32_t G, const 
 
 // A node's weighted panel (or the whole one): record i at p[i << sh]; in a
 // wide panel (sh = 1) the slot after each record holds its first entry's
-// bounding sum (index_layout.h).
+// start sum and its second entry (index_layout.h, WPanelSlot).
 struct WPan {
     const WPanelRec* p;
     uint32_t sh;
     __device__ __forceinline__ const WPanelRec& operator[](uint32_t i) const {
         return p[static_cast<size_t>(i) << sh];
     }
-    __device__ __forceinline__ double bs0(uint32_t i) const {
-        return sh ? *reinterpret_cast<const double*>(p + (static_cast<size_t>(i) << 1) + 1)
-                  : kNoSum;
+    __device__ __forceinline__ const WPanelSlot* slot(uint32_t i) const {
+        return sh ? reinterpret_cast<const WPanelSlot*>(p + (static_cast<size_t>(i) << 1) + 1)
+                  : nullptr;
     }
+    __device__ __forceinline__ double bs0(uint32_t i) const { return sh ? slot(i)->bs0 : kNoSum; }
 };
 
 // pick_exponential_weights (random/pickers.cuh:84-126) over the slice
@@ -413,7 +417,7 @@ __device__ __forceinline__ Hop weighted_group_hop(const WalkGraph& g, const WPan
     const double bs0 = f.bs0(x);
     if (es >= ee || es >= g.d.idx_size || ee > g.d.idx_size) return no_hop();
     const uint32_t k = static_cast<uint32_t>(static_cast<int>(re * static_cast<int>(ee - es)));
-    return weighted_entry<Fwd>(g, v, r0, bs0, es + k);
+    return weighted_entry<Fwd>(g, v, r0, bs0, f.slot(x), es + k);
 }
 
 // graph/temporal_node2vec_helpers.cuh:127-199 over the slice [vb, ve) of a
@@ -445,6 +449,7 @@ __device__ Hop tn2v_pick(const WalkGraph& g, int prev, const WPan& f, uint32_t G
     u32x4_a8 gv{0u, 0u, 0u, 0u};  // the group's rank, start, end, nxt0
     EdgeRec g_r0{0, 0};
     double g_bs0 = 0.0;
+    const WPanelSlot* g_sl = nullptr;
     Hop e_hop = no_hop();
     uint32_t e_pick = ~0u;
     int adj_cand = -1;
@@ -461,6 +466,7 @@ __device__ Hop tn2v_pick(const WalkGraph& g, int prev, const WPan& f, uint32_t G
             gv = *reinterpret_cast<const u32x4_a8*>(&f[x]);
             g_r0 = f[x].rec0;
             g_bs0 = f.bs0(x);
+            g_sl = f.slot(x);
             gx = x;
         }
         const uint32_t g_es = gv.y, g_ee = gv.z;
@@ -470,7 +476,7 @@ __device__ Hop tn2v_pick(const WalkGraph& g, int prev, const WPan& f, uint32_t G
         const uint32_t pick =
             g_es + static_cast<uint32_t>(local < g_ee - g_es ? local : g_ee - g_es - 1);
         if (pick != e_pick) {
-            e_hop = weighted_entry<Fwd>(g, gv, g_r0, g_bs0, pick);
+            e_hop = weighted_entry<Fwd>(g, gv, g_r0, g_bs0, g_sl, pick);
             e_pick = pick;
         }
         last = e_hop;
@@ -542,7 +548,7 @@ __device__ __forceinline__ int tn2v_try(const WalkGraph& g, const Tn2vHop& s, in
     if (es >= ee || es >= g.d.idx_size || ee > g.d.idx_size) return 0;
     const uint64_t local = static_cast<uint64_t>(er * static_cast<double>(ee - es));
     const uint32_t pick = es + static_cast<uint32_t>(local < ee - es ? local : ee - es - 1);
-    out = weighted_entry<Fwd>(g, v, f[x].rec0, f.bs0(x), pick);
+    out = weighted_entry<Fwd>(g, v, f[x].rec0, f.bs0(x), f.slot(x), pick);
     const int cand = out.nbr;
     bool accept;
     if (cand == s.prev) accept = ar < g.inv_p * inv_bmax;
