@@ -492,6 +492,32 @@ def test_replay_walks_weight_pickers(directed, forward, picker):
                seed=6)
 
 
+@pytest.mark.parametrize("directed", [True, False])
+@pytest.mark.parametrize("forward", [True, False])
+@pytest.mark.parametrize("picker", ["ExponentialWeight", "TemporalNode2Vec"])
+def test_replay_walks_weight_pickers_multi_entry_groups(directed, forward, picker):
+    """The weight pickers on a graph whose node-timestamp groups hold many
+    entries (60k edges over 400 timestamps): picks of a group's first, second
+    and later entries read the group's panel record, its wide slot and the
+    weighted edge records, each with the next slice's bound and start sum
+    they carry (forward walks over the ExponentialWeight weights' wide
+    panel), so every one of those sources feeds the next hop."""
+    s, d, t = graphs.powerlaw(2_000, 60_000, s=1.6, seed=19, ts_hi=400)
+    og, eng = _pair(directed, [(s, d, t)], weights=True, tn2v=picker == "TemporalNode2Vec",
+                    timescale_bound=20.0, p=0.5, q=2.0)
+    _assert_index_equal(og, eng, weights=True)
+    for name in WEIGHT_ARRAYS:
+        w = eng.array(name)
+        if w.size:
+            og.set_weights(name, w)
+    # groups of several entries: the test means what it says only if they occur
+    # (and a walk picks past their first entry)
+    counts = np.diff(eng.array("node_ts_group_outbound_offsets"))
+    assert counts.size and (counts >= 3).mean() > 0.15, np.bincount(counts)[:8]
+    _walk_case(og, eng, picker, picker, forward, "total", 24, 4_000, seed=21)
+    _walk_case(og, eng, picker, "Uniform", forward, "total", 16, 2_000, seed=22)
+
+
 @pytest.mark.parametrize("directed,g", [(True, 300_000), (False, 300_000), (True, 1_200_000)])
 def test_replay_walks_exponential_weight_deep_search_index(directed, g):
     """ExponentialWeight walks through a hub of 300k (1.2M) timestamp groups,
