@@ -649,10 +649,9 @@ __global__ void global_guide_kernel(const double* __restrict__ w, size_t n, int 
 }
 
 // The weighted panel: every group's panel record with its end, cumulative
-// weight and first edge record (with its next slice bound and, for the view's
-// walk direction, that slice's bounding sum).
-// rsh: the records' shift (1: each followed by its forward start sum).
-// wide (shift 1, forward weights, over such records): each panel record is
+// weight and first edge record (with that entry's next slice bound).  rsh:
+// the weighted records' shift (1: each followed by its forward start sum).
+// wide (shift 1; forward weights, over such records): each panel record is
 // followed by its slot (index_layout.h, WPanelSlot): the start sum of its first
 // entry's next slice, copied from that entry's record, and the group's second
 // entry.

@@ -49,10 +49,11 @@
 //                                  total of the node's cumulative weights
 //     wpan          WPanelRec[g << s] (ts rank, start, end, the first entry's
 //                                  next slice bound, cumulative weight, first
-//                                  edge record) of every group; with the
-//                                  ExponentialWeight weights (s = 1) every
-//                                  record is followed by a 32-byte slot that
-//                                  holds its first entry's bounding sum
+//                                  edge record) of every group; forward views
+//                                  with the ExponentialWeight weights (s = 1)
+//                                  follow every record with a 32-byte slot:
+//                                  its first entry's next slice's start sum
+//                                  and its second entry (WPanelSlot)
 //     wgt           uint32[2(g+V_c)] guide tables of nodes with > kWGuideMin
 //                                  groups, node u's at 2 (gb + u) (below)
 //   global weights  fwd_cum, bwd_cum fp64[T] (+ their guides: one segment)

@@ -406,8 +406,9 @@ __device__ __forceinline__ bool adjacent(const WalkGraph& g, int prev, int cand)
 
 // The edge of group x of a node's weighted panel f (x < G): a uniform pick re
 // within the group's range, (int)(re * size) as edge_selectors.cuh:420-443
-// takes it.  The group's record holds its first edge record, so a pick of
-// entry 0 (every pick in a group of one edge) loads no record.
+// takes it.  The group's record holds its first edge record (and a wide
+// panel's slot its second), so a pick of entry 0 (every pick in a group of one
+// edge) -- or 1 -- loads no weighted edge record.
 template <bool Fwd>
 __device__ __forceinline__ Hop weighted_group_hop(const WalkGraph& g, const WPan& f, uint32_t x,
                                                   double re) {
